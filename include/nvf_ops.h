@@ -1,0 +1,144 @@
+/*
+ * nvf_ops.h -- C ABI of the MI355X (gfx950) fused per-layer ops library
+ * (libnvf_ops.so).  Plain pointers and sizes only.
+ *
+ * Two families of entry points:
+ *
+ *  1. Drop-in replacements with the exact names and parameter lists of the
+ *     Nano_vLLM_cpp op interface (include/nanovllm/hip_ops.hpp), given C
+ *     linkage.  Semantics kept: fp32 activations, device pointers owned by the
+ *     caller, launches on the legacy null stream, early return for a zero or
+ *     negative size, and on a launch failure a message on stderr followed by
+ *     exit(1) (the reference's HIP_CHECK, include/nanovllm/common.hpp:14-23).
+ *
+ *  2. Typed entry points (nvf_*): fp32 / fp16 / bf16 storage (NVF_F32 /
+ *     NVF_F16 / NVF_BF16), an explicit stream (a hipStream_t passed as void*;
+ *     NULL = null stream) and an int status (NVF_OK or a negative code;
+ *     nvf_last_error() describes the last failure of the calling thread).
+ *     Math is fp32 on upcast inputs, rounded once to the storage type.
+ *
+ * No entry point allocates device memory or synchronises the stream.
+ * Calls are asynchronous; concurrent calls on different streams are safe.
+ */
+#ifndef NVF_OPS_H
+#define NVF_OPS_H
+
+#include <stdbool.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum nvf_dtype { NVF_F32 = 0, NVF_F16 = 1, NVF_BF16 = 2 };
+
+/* Nibble order inside a Q4_K superblock.  GGML is the GGUF on-disk order
+ * (src/gguf.cpp:477-496, tools/ref_top5.cpp:140-165,
+ * shaders/vulkan/embedding_qk.comp:54-55).  HIP_LEGACY reproduces the
+ * reference's device decoder qk_w_q4 (src/hip_ops.hip:130-140). */
+enum nvf_qk_layout { NVF_QK_LAYOUT_GGML = 0, NVF_QK_LAYOUT_HIP_LEGACY = 1 };
+
+/* K-quant kinds, the GGML type ids the reference passes (src/model.cpp:163). */
+enum nvf_qk_kind { NVF_Q4_K = 12, NVF_Q5_K = 13, NVF_Q6_K = 14 };
+
+enum nvf_status {
+  NVF_OK = 0,
+  NVF_ERR_INVALID = -1, /* bad size, dtype, kind, layout or NULL pointer */
+  NVF_ERR_LAUNCH = -2   /* the HIP launch failed */
+};
+
+/* ---- 1. drop-in replacements (include/nanovllm/hip_ops.hpp) ------------- */
+
+/* hip_ops.hpp:14 -- out = x * rsqrt(mean(x^2) + eps) * weight per row.
+ * out == x allowed (Qwen3 QK-norm in place, src/model.cpp:774-775). */
+void hip_rms_norm(const float* x, const float* weight, float* out, int rows, int hidden, float eps);
+
+/* hip_ops.hpp:15 -- residual <- x + residual; out = RMSNorm(residual) * weight. */
+void hip_rms_norm_add(const float* x, float* residual, const float* weight, float* out, int rows, int hidden,
+                      float eps);
+
+/* hip_ops.hpp:17 -- out[r,c] = silu(gate_up[r,c]) * gate_up[r,I+c]. */
+void hip_silu_and_mul(const float* gate_up, float* out, int rows, int intermediate);
+
+/* hip_ops.hpp:19-20 -- NeoX RoPE in place on data[t*stride + h*head_dim + d]. */
+void hip_rope_inplace(float* data, const int64_t* positions, int tokens, int heads, int head_dim, int64_t stride,
+                      const float* inv_freq);
+
+/* hip_ops.hpp:30 -- fp32 table gather. */
+void hip_embedding(const int64_t* ids, const float* table, int tokens, int hidden, float* out);
+
+/* hip_ops.hpp:31 -- F16 / BF16 table gather to fp32. */
+void hip_embedding_u16(const int64_t* ids, const uint16_t* table, int tokens, int hidden, float* out,
+                       bool table_bf16);
+
+/* hip_ops.hpp:32 -- Q8_0 gather from split planes (int8 w8 + fp16 scale plane ws,
+ * src/model.cpp:394-404) to fp32; bit-exact. */
+void hip_embedding_q8(const int64_t* ids, const uint8_t* w8, const uint16_t* ws, int tokens, int hidden,
+                      float* out);
+
+/* hip_ops.hpp:33 -- K-quant gather (kind 12/13/14) to fp32; Q4_K in GGML order. */
+void hip_embedding_qk(const int64_t* ids, const uint8_t* wq, int tokens, int hidden, float* out, int kind);
+
+/* ---- 2. typed entry points ---------------------------------------------- */
+
+/* Residual-add + RMSNorm (replaces hip_rms_norm_add, hip_ops.hpp:15).  All four
+ * tensors in `dtype`; residual is read and written back rounded to `dtype`,
+ * and the norm is taken over that stored row. */
+int nvf_rms_norm_add(const void* x, void* residual, const void* weight, void* out, int64_t rows, int64_t hidden,
+                     float eps, int dtype, void* stream);
+
+/* RMSNorm (replaces hip_rms_norm, hip_ops.hpp:14); out == x allowed. */
+int nvf_rms_norm(const void* x, const void* weight, void* out, int64_t rows, int64_t hidden, float eps, int dtype,
+                 void* stream);
+
+/* SiLU(gate) * up over gate_up [rows, 2*inter] -> out [rows, inter]
+ * (replaces hip_silu_and_mul, hip_ops.hpp:17). */
+int nvf_silu_and_mul(const void* gate_up, void* out, int64_t rows, int64_t inter, int dtype, void* stream);
+
+/* Fused Qwen3 QK-norm + NeoX RoPE on q and k in one launch (composition of
+ * hip_rms_norm at src/model.cpp:774-775 and hip_rope_inplace at :777-778).
+ * q: [tokens, q_stride], heads at h*head_dim; k: [tokens, k_stride].  q_w / k_w
+ * are [head_dim] gammas in `dtype`; pass both NULL for plain RoPE.  k may be NULL
+ * when kv_heads == 0.  inv_freq: device fp32 [head_dim/2].  The normalised head
+ * stays fp32 until the rotated value is stored. */
+int nvf_qk_norm_rope(void* q, void* k, const int64_t* positions, const void* q_w, const void* k_w,
+                     const float* inv_freq, int64_t tokens, int q_heads, int kv_heads, int head_dim,
+                     int64_t q_stride, int64_t k_stride, float eps, int dtype, void* stream);
+
+/* Q8_0 gather, split planes (as hip_embedding_q8) -> out in out_dtype.
+ * vocab > 0: ids outside [0, vocab) produce a NaN row instead of a read;
+ * vocab <= 0: ids are trusted (the reference validates them on the host,
+ * src/model.cpp:712-716). */
+int nvf_embedding_q8_0(const int64_t* ids, const uint8_t* w8, const uint16_t* ws, int64_t tokens, int64_t hidden,
+                       int64_t vocab, void* out, int out_dtype, void* stream);
+
+/* Q8_0 gather straight from interleaved 34-byte GGUF blocks
+ * ([fp16 d][32 x int8], src/gguf.cpp:353-362) -> out in out_dtype. */
+int nvf_embedding_q8_0_blocks(const int64_t* ids, const uint8_t* blocks, int64_t tokens, int64_t hidden,
+                              int64_t vocab, void* out, int out_dtype, void* stream);
+
+/* K-quant gather (replaces hip_embedding_qk, hip_ops.hpp:33): kind NVF_Q4_K /
+ * NVF_Q5_K / NVF_Q6_K, layout applies to Q4_K only. */
+int nvf_embedding_qk(const int64_t* ids, const uint8_t* wq, int64_t tokens, int64_t hidden, int64_t vocab,
+                     int kind, int layout, void* out, int out_dtype, void* stream);
+
+/* Plain table gather: table in table_dtype, out in out_dtype
+ * (replaces hip_embedding / hip_embedding_u16, hip_ops.hpp:30-31). */
+int nvf_embedding(const int64_t* ids, const void* table, int64_t tokens, int64_t hidden, int64_t vocab,
+                  int table_dtype, void* out, int out_dtype, void* stream);
+
+/* Host helper: inv_freq[i] = (float)(1 / theta^(2i/head_dim)) in double, the
+ * table Qwen3Model builds in its constructor (src/model.cpp:416-420).
+ * out is HOST memory of head_dim/2 floats. */
+int nvf_rope_inv_freq(double theta, int head_dim, float* out);
+
+/* Text of the calling thread's last failure ("" if none). */
+const char* nvf_last_error(void);
+
+/* ABI version, bumped on any signature change. */
+int nvf_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* NVF_OPS_H */

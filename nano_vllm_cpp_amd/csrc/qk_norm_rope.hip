@@ -1,0 +1,213 @@
+// Qwen3 per-head QK-norm fused with NeoX RoPE, on q and k in one launch.
+//
+// Reference semantics:
+//   QK-norm: src/model.cpp:774-775 -> hip_rms_norm with rows = T*heads,
+//            hidden = head_dim (src/hip_ops.hip:373-393), before RoPE;
+//   RoPE:    src/model.cpp:777-778 -> rope_kernel (src/hip_ops.hip:431-450):
+//            a = float(pos[t]) * inv_freq[d]; (x1, x2) -> (x1 c - x2 s, x2 c + x1 s)
+//            for the pair (d, d + head_dim/2).
+//
+// Design: one 256-thread workgroup per token.  The head_dim/2 (cos, sin) pairs
+// of the token are computed once (precise cosf/sinf, the reference's own
+// functions) into LDS and reused by every q and k head -- the reference
+// recomputes them per head.  A head is LPH = (head_dim/2)/N lanes; lane l
+// holds the 16-byte vectors at d0 = l*N and d0 + head_dim/2, so every rotation
+// pair is lane-local.  QK-norm reduces the head's sum of squares over those LPH
+// lanes with DPP (group_sum) and keeps the normalised values in registers, so q
+// and k are read once and written once: 2 passes instead of the reference's 8
+// (norm q, norm k, rope q, rope k, each read + write).
+#include "nvf_device.hpp"
+#include "nvf_host.hpp"
+
+namespace nvf {
+
+constexpr int kRopeThreads = 256;
+
+template <typename T, int HD, bool NORM>
+__global__ __launch_bounds__(kRopeThreads) void qk_norm_rope_kernel(T* q, T* k, const int64_t* __restrict__ positions,
+                                                                    const T* __restrict__ qw, const T* __restrict__ kw,
+                                                                    const float* __restrict__ inv_freq, int q_heads,
+                                                                    int kv_heads, int64_t q_stride, int64_t k_stride,
+                                                                    float eps) {
+  constexpr int N = Pack<T>::N;
+  constexpr int HALF = HD / 2;
+  constexpr int LPH = HALF / N;                   // lanes per head
+  constexpr int HPP = kRopeThreads / LPH;         // heads per pass of the workgroup
+  static_assert(LPH >= 1 && LPH <= 32 && (LPH & (LPH - 1)) == 0, "lanes per head");
+
+  __shared__ float cs_lds[HALF];
+  __shared__ float sn_lds[HALF];
+  const int64_t t = blockIdx.x;
+  if (threadIdx.x < HALF) {
+    const float a = (float)positions[t] * inv_freq[threadIdx.x];
+    cs_lds[threadIdx.x] = cosf(a);
+    sn_lds[threadIdx.x] = sinf(a);
+  }
+
+  const int sub = threadIdx.x % LPH;
+  const int d0 = sub * N;
+  float qg1[N], qg2[N], kg1[N], kg2[N];
+  if constexpr (NORM) {
+    Pack<T>::unpack(ld16(qw + d0), qg1);
+    Pack<T>::unpack(ld16(qw + HALF + d0), qg2);
+    Pack<T>::unpack(ld16(kw + d0), kg1);
+    Pack<T>::unpack(ld16(kw + HALF + d0), kg2);
+  }
+  __syncthreads();
+  float c[N], s[N];
+#pragma unroll
+  for (int j = 0; j < N; ++j) {
+    c[j] = cs_lds[d0 + j];
+    s[j] = sn_lds[d0 + j];
+  }
+
+  const int total_heads = q_heads + kv_heads;
+  for (int h = threadIdx.x / LPH; h < total_heads; h += HPP) {
+    const bool is_q = h < q_heads;
+    T* base = is_q ? q + t * q_stride + (int64_t)h * HD : k + t * k_stride + (int64_t)(h - q_heads) * HD;
+    float x1[N], x2[N];
+    Pack<T>::unpack(ld16(base + d0), x1);
+    Pack<T>::unpack(ld16(base + HALF + d0), x2);
+    if constexpr (NORM) {
+      float ss = 0.f;
+#pragma unroll
+      for (int j = 0; j < N; ++j) ss += x1[j] * x1[j] + x2[j] * x2[j];
+      ss = group_sum<LPH>(ss);
+      const float inv = rsqrtf(ss / (float)HD + eps);
+#pragma unroll
+      for (int j = 0; j < N; ++j) {
+        x1[j] = x1[j] * inv * (is_q ? qg1[j] : kg1[j]);
+        x2[j] = x2[j] * inv * (is_q ? qg2[j] : kg2[j]);
+      }
+    }
+    float y1[N], y2[N];
+#pragma unroll
+    for (int j = 0; j < N; ++j) {
+      y1[j] = x1[j] * c[j] - x2[j] * s[j];
+      y2[j] = x2[j] * c[j] + x1[j] * s[j];
+    }
+    st16(base + d0, Pack<T>::pack(y1));
+    st16(base + HALF + d0, Pack<T>::pack(y2));
+  }
+}
+
+// Any head_dim / stride / alignment: one wave per (token, head); lanes walk the
+// rotation pairs.  Norm uses a wave-wide sum.
+template <typename T, bool NORM>
+__global__ __launch_bounds__(kRopeThreads) void qk_norm_rope_generic_kernel(
+    T* q, T* k, const int64_t* __restrict__ positions, const T* __restrict__ qw, const T* __restrict__ kw,
+    const float* __restrict__ inv_freq, int64_t tokens, int q_heads, int kv_heads, int head_dim, int64_t q_stride,
+    int64_t k_stride, float eps) {
+  const int total_heads = q_heads + kv_heads;
+  const int64_t item = (int64_t)blockIdx.x * (kRopeThreads / kWave) + threadIdx.x / kWave;
+  if (item >= tokens * total_heads) return;  // wave-uniform
+  const int lane = threadIdx.x % kWave;
+  const int64_t t = item / total_heads;
+  const int h = (int)(item - t * total_heads);
+  const bool is_q = h < q_heads;
+  T* base = is_q ? q + t * q_stride + (int64_t)h * head_dim : k + t * k_stride + (int64_t)(h - q_heads) * head_dim;
+  const T* gw = is_q ? qw : kw;
+  const int half = head_dim / 2;
+  float inv = 1.f;
+  if constexpr (NORM) {
+    float ss = 0.f;
+    for (int d = lane; d < head_dim; d += kWave) {
+      const float v = to_f32(base[d]);
+      ss += v * v;
+    }
+    ss = wave_sum(ss);
+    inv = rsqrtf(ss / (float)head_dim + eps);
+  }
+  const float pos = (float)positions[t];
+  for (int d = lane; d < half; d += kWave) {
+    float x1 = to_f32(base[d]), x2 = to_f32(base[d + half]);
+    if constexpr (NORM) {
+      x1 = x1 * inv * to_f32(gw[d]);
+      x2 = x2 * inv * to_f32(gw[d + half]);
+    }
+    const float a = pos * inv_freq[d];
+    const float c = cosf(a), s = sinf(a);
+    base[d] = from_f32<T>(x1 * c - x2 * s);
+    base[d + half] = from_f32<T>(x2 * c + x1 * s);
+  }
+}
+
+template <typename T, bool NORM>
+static int launch_rope(void* q, void* k, const int64_t* pos, const void* qw, const void* kw, const float* inv_freq,
+                       int64_t tokens, int q_heads, int kv_heads, int head_dim, int64_t q_stride, int64_t k_stride,
+                       float eps, hipStream_t st) {
+  constexpr int N = Pack<T>::N;
+  T* qp = static_cast<T*>(q);
+  T* kp = static_cast<T*>(k);
+  const T* qwp = static_cast<const T*>(qw);
+  const T* kwp = static_cast<const T*>(kw);
+  bool vec_ok = (q_heads == 0 || (aligned16(q) && q_stride % N == 0)) &&
+                (kv_heads == 0 || (aligned16(k) && k_stride % N == 0)) &&
+                (!NORM || (aligned16(qw) && aligned16(kw)));
+  if (vec_ok) {
+    const dim3 grid((unsigned)tokens);
+    // NORM needs both gamma pointers readable even when one side has no heads.
+    if (NORM && !qwp) qwp = kwp;
+    if (NORM && !kwp) kwp = qwp;
+#define NVF_ROPE_LAUNCH(HDV)                                                                                 \
+  qk_norm_rope_kernel<T, HDV, NORM><<<grid, kRopeThreads, 0, st>>>(qp, kp, pos, qwp, kwp, inv_freq, q_heads, \
+                                                                   kv_heads, q_stride, k_stride, eps)
+    if (head_dim == 64) {
+      NVF_ROPE_LAUNCH(64);
+      return launch_status("qk_norm_rope");
+    }
+    if (head_dim == 128) {
+      NVF_ROPE_LAUNCH(128);
+      return launch_status("qk_norm_rope");
+    }
+    if (head_dim == 256) {
+      NVF_ROPE_LAUNCH(256);
+      return launch_status("qk_norm_rope");
+    }
+#undef NVF_ROPE_LAUNCH
+  }
+  const int64_t items = tokens * (q_heads + kv_heads);
+  const int per_block = kRopeThreads / kWave;
+  const dim3 grid((unsigned)((items + per_block - 1) / per_block));
+  qk_norm_rope_generic_kernel<T, NORM><<<grid, kRopeThreads, 0, st>>>(qp, kp, pos, qwp, kwp, inv_freq, tokens, q_heads,
+                                                                      kv_heads, head_dim, q_stride, k_stride, eps);
+  return launch_status("qk_norm_rope(generic)");
+}
+
+}  // namespace nvf
+
+extern "C" int nvf_qk_norm_rope(void* q, void* k, const int64_t* positions, const void* q_w, const void* k_w,
+                                const float* inv_freq, int64_t tokens, int q_heads, int kv_heads, int head_dim,
+                                int64_t q_stride, int64_t k_stride, float eps, int dtype, void* stream) {
+  using namespace nvf;
+  if (!dtype_ok(dtype)) return fail(NVF_ERR_INVALID, "nvf_qk_norm_rope: bad dtype %d", dtype);
+  if (tokens < 0 || q_heads < 0 || kv_heads < 0 || head_dim < 2 || tokens > INT32_MAX)
+    return fail(NVF_ERR_INVALID, "nvf_qk_norm_rope: bad shape tokens=%lld q_heads=%d kv_heads=%d head_dim=%d",
+                (long long)tokens, q_heads, kv_heads, head_dim);
+  if (tokens == 0 || q_heads + kv_heads == 0) return NVF_OK;
+  if ((q_heads > 0 && (!q || q_stride < (int64_t)q_heads * head_dim)) ||
+      (kv_heads > 0 && (!k || k_stride < (int64_t)kv_heads * head_dim)))
+    return fail(NVF_ERR_INVALID, "nvf_qk_norm_rope: NULL tensor or stride smaller than heads*head_dim");
+  if (!positions || !inv_freq) return fail(NVF_ERR_INVALID, "nvf_qk_norm_rope: NULL positions or inv_freq");
+  const bool norm = q_w || k_w;
+  if (norm && ((q_heads > 0 && !q_w) || (kv_heads > 0 && !k_w)))
+    return fail(NVF_ERR_INVALID, "nvf_qk_norm_rope: q_w and k_w must both be given (or both NULL)");
+  int s = NVF_OK;
+  hipStream_t st = as_stream(stream);
+  if (norm)
+    NVF_DISPATCH_DTYPE(dtype, T, s = (launch_rope<T, true>(q, k, positions, q_w, k_w, inv_freq, tokens, q_heads,
+                                                           kv_heads, head_dim, q_stride, k_stride, eps, st)));
+  else
+    NVF_DISPATCH_DTYPE(dtype, T, s = (launch_rope<T, false>(q, k, positions, nullptr, nullptr, inv_freq, tokens,
+                                                            q_heads, kv_heads, head_dim, q_stride, k_stride, eps, st)));
+  return s;
+}
+
+// Drop-in: include/nanovllm/hip_ops.hpp:19-20 / src/hip_ops.hip:715-722.
+extern "C" void hip_rope_inplace(float* data, const int64_t* positions, int tokens, int heads, int head_dim,
+                                 int64_t stride, const float* inv_freq) {
+  if (tokens <= 0 || heads <= 0 || head_dim / 2 <= 0) return;
+  nvf::dropin_check(nvf_qk_norm_rope(data, nullptr, positions, nullptr, nullptr, inv_freq, tokens, heads, 0, head_dim,
+                                     stride, 0, 0.f, NVF_F32, nullptr),
+                    "hip_rope_inplace");
+}

@@ -1,0 +1,186 @@
+// Fused residual-add + RMSNorm and plain RMSNorm for gfx950.
+//
+// Reference semantics: src/hip_ops.hip:373-417 (rms_norm_kernel,
+// rms_norm_add_kernel) -- residual <- x + residual is written back, then
+// out = residual * rsqrt(sum(residual^2)/hidden + eps) * weight.
+//
+// Design: one wave64 per row, four rows per 256-thread workgroup.  The row is
+// read once with 16-byte loads and held in VGPRs (VPL vectors per lane), so x
+// and residual cross HBM once and residual/out are written once: 4 row passes
+// instead of the reference's 5, and no LDS or barrier -- the sum of squares is
+// reduced with DPP row ops and one ds_swizzle (wave_sum).
+#include "nvf_device.hpp"
+#include "nvf_host.hpp"
+
+namespace nvf {
+
+constexpr int kNormThreads = 256;
+constexpr int kNormRowsPerBlock = kNormThreads / kWave;
+constexpr int kNormMaxVpl = 16;  // 16 x 64 lanes x 16 B = a 16 KiB row in registers
+
+template <typename T, int VPL, bool ADD>
+__global__ __launch_bounds__(kNormThreads) void rms_norm_vec_kernel(const T* x, T* residual, const T* __restrict__ w,
+                                                                    T* out, int64_t rows, int hidden, float eps) {
+  constexpr int N = Pack<T>::N;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t row = (int64_t)blockIdx.x * kNormRowsPerBlock + (threadIdx.x / kWave);
+  if (row >= rows) return;  // wave-uniform
+  const int nvec = hidden / N;
+  const int64_t off = row * (int64_t)hidden;
+  const u32x4* xv = reinterpret_cast<const u32x4*>(x + off);
+  u32x4* rv = reinterpret_cast<u32x4*>(residual + off);
+  const u32x4* wv = reinterpret_cast<const u32x4*>(w);
+  u32x4* ov = reinterpret_cast<u32x4*>(out + off);
+
+  u32x4 xa[VPL], ra[VPL], wa[VPL];
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) {
+    const int c = i * kWave + lane;
+    if (c < nvec) {
+      xa[i] = xv[c];
+      if constexpr (ADD) ra[i] = rv[c];
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) {
+    const int c = i * kWave + lane;
+    if (c < nvec) wa[i] = wv[c];
+  }
+
+  float v[VPL][N];
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) {
+    const int c = i * kWave + lane;
+    if (c < nvec) {
+      Pack<T>::unpack(xa[i], v[i]);
+      if constexpr (ADD) {
+        float r[N];
+        Pack<T>::unpack(ra[i], r);
+#pragma unroll
+        for (int j = 0; j < N; ++j) v[i][j] += r[j];
+        const u32x4 stored = Pack<T>::pack(v[i]);
+        rv[c] = stored;
+        Pack<T>::unpack(stored, v[i]);  // the norm sees the stored (rounded) row
+      }
+#pragma unroll
+      for (int j = 0; j < N; ++j) ss += v[i][j] * v[i][j];
+    }
+  }
+  ss = wave_sum(ss);
+  const float inv = rsqrtf(ss / (float)hidden + eps);
+
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) {
+    const int c = i * kWave + lane;
+    if (c < nvec) {
+      float g[N], o[N];
+      Pack<T>::unpack(wa[i], g);
+#pragma unroll
+      for (int j = 0; j < N; ++j) o[j] = v[i][j] * inv * g[j];
+      ov[c] = Pack<T>::pack(o);
+    }
+  }
+}
+
+// Any hidden / alignment: one wave per row, scalar two-pass (the second pass
+// re-reads the row this lane wrote, an L2 hit).
+template <typename T, bool ADD>
+__global__ __launch_bounds__(kNormThreads) void rms_norm_generic_kernel(const T* x, T* residual, const T* w, T* out,
+                                                                        int64_t rows, int hidden, float eps) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t row = (int64_t)blockIdx.x * kNormRowsPerBlock + (threadIdx.x / kWave);
+  if (row >= rows) return;
+  const int64_t off = row * (int64_t)hidden;
+  float ss = 0.f;
+  for (int c = lane; c < hidden; c += kWave) {
+    float v = to_f32(x[off + c]);
+    if constexpr (ADD) {
+      const T s = from_f32<T>(v + to_f32(residual[off + c]));
+      residual[off + c] = s;
+      v = to_f32(s);
+    }
+    ss += v * v;
+  }
+  ss = wave_sum(ss);
+  const float inv = rsqrtf(ss / (float)hidden + eps);
+  for (int c = lane; c < hidden; c += kWave) {
+    const float v = ADD ? to_f32(residual[off + c]) : to_f32(x[off + c]);
+    out[off + c] = from_f32<T>(v * inv * to_f32(w[c]));
+  }
+}
+
+template <typename T, bool ADD>
+static int launch_rms(const void* x, void* residual, const void* w, void* out, int64_t rows, int64_t hidden,
+                      float eps, hipStream_t st) {
+  constexpr int N = Pack<T>::N;
+  const int64_t nvec = hidden / N;
+  const int vpl = (int)((nvec + kWave - 1) / kWave);
+  const bool vec_ok = hidden % N == 0 && vpl >= 1 && vpl <= kNormMaxVpl && aligned16(x) && aligned16(w) &&
+                      aligned16(out) && (!ADD || aligned16(residual));
+  const dim3 grid((unsigned)((rows + kNormRowsPerBlock - 1) / kNormRowsPerBlock));
+  const dim3 block(kNormThreads);
+  const T* xp = static_cast<const T*>(x);
+  T* rp = static_cast<T*>(residual);
+  const T* wp = static_cast<const T*>(w);
+  T* op = static_cast<T*>(out);
+  const int h = (int)hidden;
+  if (!vec_ok) {
+    rms_norm_generic_kernel<T, ADD><<<grid, block, 0, st>>>(xp, rp, wp, op, rows, h, eps);
+    return launch_status("rms_norm(generic)");
+  }
+  switch (vpl) {
+#define NVF_RMS_CASE(V)                                                                   \
+  case V:                                                                                 \
+    rms_norm_vec_kernel<T, V, ADD><<<grid, block, 0, st>>>(xp, rp, wp, op, rows, h, eps); \
+    break;
+    NVF_RMS_CASE(1) NVF_RMS_CASE(2) NVF_RMS_CASE(3) NVF_RMS_CASE(4) NVF_RMS_CASE(5) NVF_RMS_CASE(6)
+    NVF_RMS_CASE(7) NVF_RMS_CASE(8) NVF_RMS_CASE(9) NVF_RMS_CASE(10) NVF_RMS_CASE(11) NVF_RMS_CASE(12)
+    NVF_RMS_CASE(13) NVF_RMS_CASE(14) NVF_RMS_CASE(15) NVF_RMS_CASE(16)
+#undef NVF_RMS_CASE
+  }
+  return launch_status("rms_norm");
+}
+
+static int rms_entry(const void* x, void* residual, const void* w, void* out, int64_t rows, int64_t hidden,
+                     float eps, int dtype, void* stream, bool add) {
+  const char* name = add ? "nvf_rms_norm_add" : "nvf_rms_norm";
+  if (!dtype_ok(dtype)) return fail(NVF_ERR_INVALID, "%s: bad dtype %d", name, dtype);
+  if (rows < 0 || hidden < 0 || hidden > INT32_MAX)
+    return fail(NVF_ERR_INVALID, "%s: bad shape rows=%lld hidden=%lld", name, (long long)rows, (long long)hidden);
+  if (rows == 0 || hidden == 0) return NVF_OK;
+  if (!x || !w || !out || (add && !residual)) return fail(NVF_ERR_INVALID, "%s: NULL pointer", name);
+  int st = NVF_OK;
+  if (add)
+    NVF_DISPATCH_DTYPE(dtype, T, st = (launch_rms<T, true>(x, residual, w, out, rows, hidden, eps, as_stream(stream))));
+  else
+    NVF_DISPATCH_DTYPE(dtype, T, st = (launch_rms<T, false>(x, nullptr, w, out, rows, hidden, eps, as_stream(stream))));
+  return st;
+}
+
+}  // namespace nvf
+
+extern "C" int nvf_rms_norm_add(const void* x, void* residual, const void* weight, void* out, int64_t rows,
+                                int64_t hidden, float eps, int dtype, void* stream) {
+  return nvf::rms_entry(x, residual, weight, out, rows, hidden, eps, dtype, stream, true);
+}
+
+extern "C" int nvf_rms_norm(const void* x, const void* weight, void* out, int64_t rows, int64_t hidden, float eps,
+                            int dtype, void* stream) {
+  return nvf::rms_entry(x, nullptr, weight, out, rows, hidden, eps, dtype, stream, false);
+}
+
+// Drop-in: include/nanovllm/hip_ops.hpp:14 / src/hip_ops.hip:694-698.
+extern "C" void hip_rms_norm(const float* x, const float* weight, float* out, int rows, int hidden, float eps) {
+  if (rows <= 0 || hidden <= 0) return;
+  nvf::dropin_check(nvf::rms_entry(x, nullptr, weight, out, rows, hidden, eps, NVF_F32, nullptr, false),
+                    "hip_rms_norm");
+}
+
+// Drop-in: include/nanovllm/hip_ops.hpp:15 / src/hip_ops.hip:700-705.
+extern "C" void hip_rms_norm_add(const float* x, float* residual, const float* weight, float* out, int rows,
+                                 int hidden, float eps) {
+  if (rows <= 0 || hidden <= 0) return;
+  nvf::dropin_check(nvf::rms_entry(x, residual, weight, out, rows, hidden, eps, NVF_F32, nullptr, true),
+                    "hip_rms_norm_add");
+}

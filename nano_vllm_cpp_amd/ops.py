@@ -1,0 +1,217 @@
+"""Python front end of libnvf_ops.so (the gfx950 fused per-layer ops).
+
+`lib()` returns the ctypes handle with every C-ABI symbol of include/nvf_ops.h
+typed.  The torch-facing wrappers below only validate shapes, pick the stream
+(torch's current stream) and call the C ABI; all compute is in the HIP
+library.  There is no fallback: a missing library raises immediately.
+
+Names and argument meaning follow the reference op interface
+(include/nanovllm/hip_ops.hpp:14-33 in Nano_vLLM_cpp).
+"""
+from __future__ import annotations
+
+import ctypes as C
+import threading
+from pathlib import Path
+
+import torch
+
+LIB_PATH = Path(__file__).resolve().parent / "lib" / "libnvf_ops.so"
+
+F32, F16, BF16 = 0, 1, 2
+QK_LAYOUT_GGML, QK_LAYOUT_HIP_LEGACY = 0, 1
+Q4_K, Q5_K, Q6_K = 12, 13, 14
+
+_DT = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16}
+
+_vp, _i64, _i32, _f32, _f64 = C.c_void_p, C.c_int64, C.c_int, C.c_float, C.c_double
+
+# symbol -> (restype, argtypes); mirrors include/nvf_ops.h
+SIGNATURES: dict[str, tuple] = {
+    "hip_rms_norm": (None, [_vp, _vp, _vp, _i32, _i32, _f32]),
+    "hip_rms_norm_add": (None, [_vp, _vp, _vp, _vp, _i32, _i32, _f32]),
+    "hip_silu_and_mul": (None, [_vp, _vp, _i32, _i32]),
+    "hip_rope_inplace": (None, [_vp, _vp, _i32, _i32, _i32, _i64, _vp]),
+    "hip_embedding": (None, [_vp, _vp, _i32, _i32, _vp]),
+    "hip_embedding_u16": (None, [_vp, _vp, _i32, _i32, _vp, C.c_bool]),
+    "hip_embedding_q8": (None, [_vp, _vp, _vp, _i32, _i32, _vp]),
+    "hip_embedding_qk": (None, [_vp, _vp, _i32, _i32, _vp, _i32]),
+    "nvf_rms_norm_add": (_i32, [_vp, _vp, _vp, _vp, _i64, _i64, _f32, _i32, _vp]),
+    "nvf_rms_norm": (_i32, [_vp, _vp, _vp, _i64, _i64, _f32, _i32, _vp]),
+    "nvf_silu_and_mul": (_i32, [_vp, _vp, _i64, _i64, _i32, _vp]),
+    "nvf_qk_norm_rope": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i32, _i32, _i32, _i64, _i64, _f32, _i32, _vp]),
+    "nvf_embedding_q8_0": (_i32, [_vp, _vp, _vp, _i64, _i64, _i64, _vp, _i32, _vp]),
+    "nvf_embedding_q8_0_blocks": (_i32, [_vp, _vp, _i64, _i64, _i64, _vp, _i32, _vp]),
+    "nvf_embedding_qk": (_i32, [_vp, _vp, _i64, _i64, _i64, _i32, _i32, _vp, _i32, _vp]),
+    "nvf_embedding": (_i32, [_vp, _vp, _i64, _i64, _i64, _i32, _vp, _i32, _vp]),
+    "nvf_rope_inv_freq": (_i32, [_f64, _i32, _vp]),
+    "nvf_last_error": (C.c_char_p, []),
+    "nvf_abi_version": (_i32, []),
+}
+
+_lock = threading.Lock()
+_lib: C.CDLL | None = None
+
+
+class NvfError(RuntimeError):
+    """A nonzero status from the C ABI."""
+
+
+def lib() -> C.CDLL:
+    """Loads libnvf_ops.so once; raises if it has not been built."""
+    global _lib
+    with _lock:
+        if _lib is None:
+            if not LIB_PATH.exists():
+                raise RuntimeError(
+                    f"{LIB_PATH} is missing: build it with `python -m nano_vllm_cpp_amd.build` "
+                    "(there is no CPU fallback)")
+            h = C.CDLL(str(LIB_PATH))
+            for name, (res, args) in SIGNATURES.items():
+                fn = getattr(h, name)
+                fn.restype = res
+                fn.argtypes = args
+            _lib = h
+        return _lib
+
+
+def _check(status: int, what: str) -> None:
+    if status != 0:
+        msg = lib().nvf_last_error().decode(errors="replace")
+        raise NvfError(f"{what} failed ({status}): {msg}")
+
+
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _dev(t: torch.Tensor, name: str) -> int:
+    if not t.is_cuda:
+        raise ValueError(f"{name} must be a GPU tensor")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+    return t.data_ptr()
+
+
+def _dt(t: torch.Tensor) -> int:
+    try:
+        return _DT[t.dtype]
+    except KeyError:
+        raise ValueError(f"unsupported dtype {t.dtype}") from None
+
+
+# ---------------------------------------------------------------------------
+# norms
+# ---------------------------------------------------------------------------
+def rms_norm_add(x: torch.Tensor, residual: torch.Tensor, weight: torch.Tensor, eps: float,
+                 out: torch.Tensor | None = None) -> torch.Tensor:
+    """residual <- x + residual (in place); returns RMSNorm(residual) * weight."""
+    rows, hidden = x.shape
+    if residual.shape != x.shape or weight.shape != (hidden,):
+        raise ValueError("shape mismatch")
+    if not (x.dtype == residual.dtype == weight.dtype):
+        raise ValueError("x, residual and weight must share a dtype")
+    out = torch.empty_like(x) if out is None else out
+    _check(lib().nvf_rms_norm_add(_dev(x, "x"), _dev(residual, "residual"), _dev(weight, "weight"),
+                                  _dev(out, "out"), rows, hidden, eps, _dt(x), _stream()), "rms_norm_add")
+    return out
+
+
+def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float, out: torch.Tensor | None = None) -> torch.Tensor:
+    rows, hidden = x.shape
+    if weight.shape != (hidden,) or weight.dtype != x.dtype:
+        raise ValueError("weight must be [hidden] in x's dtype")
+    out = torch.empty_like(x) if out is None else out
+    _check(lib().nvf_rms_norm(_dev(x, "x"), _dev(weight, "weight"), _dev(out, "out"), rows, hidden, eps, _dt(x),
+                              _stream()), "rms_norm")
+    return out
+
+
+# ---------------------------------------------------------------------------
+# SwiGLU
+# ---------------------------------------------------------------------------
+def silu_and_mul(gate_up: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    rows, two_i = gate_up.shape
+    if two_i % 2:
+        raise ValueError("gate_up width must be even")
+    inter = two_i // 2
+    out = torch.empty((rows, inter), dtype=gate_up.dtype, device=gate_up.device) if out is None else out
+    _check(lib().nvf_silu_and_mul(_dev(gate_up, "gate_up"), _dev(out, "out"), rows, inter, _dt(gate_up), _stream()),
+           "silu_and_mul")
+    return out
+
+
+# ---------------------------------------------------------------------------
+# QK-norm + RoPE
+# ---------------------------------------------------------------------------
+def rope_inv_freq(theta: float, head_dim: int, device: str | torch.device = "cpu") -> torch.Tensor:
+    """inv_freq[i] = float(1 / theta^(2i/head_dim)) computed in double (model.cpp:416-420)."""
+    out = torch.empty(head_dim // 2, dtype=torch.float32)
+    _check(lib().nvf_rope_inv_freq(theta, head_dim, out.data_ptr()), "rope_inv_freq")
+    return out.to(device)
+
+
+def qk_norm_rope(q: torch.Tensor, k: torch.Tensor | None, positions: torch.Tensor, q_w: torch.Tensor | None,
+                 k_w: torch.Tensor | None, inv_freq: torch.Tensor, q_heads: int, kv_heads: int, head_dim: int,
+                 eps: float = 1e-6) -> None:
+    """In place on q [T, q_stride] and k [T, k_stride] (row strides = the tensors' widths).
+
+    q_w / k_w None -> plain NeoX RoPE.  positions: int64 [T] on the GPU."""
+    tokens = q.shape[0]
+    if positions.dtype != torch.int64 or positions.shape != (tokens,):
+        raise ValueError("positions must be int64 [tokens]")
+    if inv_freq.dtype != torch.float32 or inv_freq.numel() != head_dim // 2:
+        raise ValueError("inv_freq must be float32 [head_dim/2]")
+    q2 = q.reshape(tokens, -1)
+    k2 = k.reshape(tokens, -1) if k is not None else None
+    _check(lib().nvf_qk_norm_rope(
+        _dev(q, "q"), _dev(k, "k") if k is not None else None, _dev(positions, "positions"),
+        _dev(q_w, "q_w") if q_w is not None else None, _dev(k_w, "k_w") if k_w is not None else None,
+        _dev(inv_freq, "inv_freq"), tokens, q_heads, kv_heads, head_dim, q2.shape[1],
+        k2.shape[1] if k2 is not None else 0, eps, _dt(q), _stream()), "qk_norm_rope")
+
+
+# ---------------------------------------------------------------------------
+# embeddings
+# ---------------------------------------------------------------------------
+def _out(tokens: int, hidden: int, dtype: torch.dtype, device) -> torch.Tensor:
+    return torch.empty((tokens, hidden), dtype=dtype, device=device)
+
+
+def embedding_q8_0(ids: torch.Tensor, w8: torch.Tensor, ws: torch.Tensor, hidden: int, vocab: int = 0,
+                   out_dtype: torch.dtype = torch.float16, out: torch.Tensor | None = None) -> torch.Tensor:
+    """Q8_0 gather from split planes: w8 int8/uint8 [V*H], ws fp16-bits [V*H/32]."""
+    tokens = ids.numel()
+    out = _out(tokens, hidden, out_dtype, ids.device) if out is None else out
+    _check(lib().nvf_embedding_q8_0(_dev(ids, "ids"), _dev(w8, "w8"), _dev(ws, "ws"), tokens, hidden, vocab,
+                                    _dev(out, "out"), _dt(out), _stream()), "embedding_q8_0")
+    return out
+
+
+def embedding_q8_0_blocks(ids: torch.Tensor, blocks: torch.Tensor, hidden: int, vocab: int = 0,
+                          out_dtype: torch.dtype = torch.float16, out: torch.Tensor | None = None) -> torch.Tensor:
+    """Q8_0 gather from interleaved 34-byte GGUF blocks (uint8 [V*H/32*34])."""
+    tokens = ids.numel()
+    out = _out(tokens, hidden, out_dtype, ids.device) if out is None else out
+    _check(lib().nvf_embedding_q8_0_blocks(_dev(ids, "ids"), _dev(blocks, "blocks"), tokens, hidden, vocab,
+                                           _dev(out, "out"), _dt(out), _stream()), "embedding_q8_0_blocks")
+    return out
+
+
+def embedding_qk(ids: torch.Tensor, wq: torch.Tensor, hidden: int, kind: int = Q4_K, vocab: int = 0,
+                 layout: int = QK_LAYOUT_GGML, out_dtype: torch.dtype = torch.float16,
+                 out: torch.Tensor | None = None) -> torch.Tensor:
+    tokens = ids.numel()
+    out = _out(tokens, hidden, out_dtype, ids.device) if out is None else out
+    _check(lib().nvf_embedding_qk(_dev(ids, "ids"), _dev(wq, "wq"), tokens, hidden, vocab, kind, layout,
+                                  _dev(out, "out"), _dt(out), _stream()), "embedding_qk")
+    return out
+
+
+def embedding(ids: torch.Tensor, table: torch.Tensor, vocab: int = 0, out_dtype: torch.dtype | None = None,
+              out: torch.Tensor | None = None) -> torch.Tensor:
+    tokens, hidden = ids.numel(), table.shape[-1]
+    out = _out(tokens, hidden, out_dtype or table.dtype, ids.device) if out is None else out
+    _check(lib().nvf_embedding(_dev(ids, "ids"), _dev(table, "table"), tokens, hidden, vocab, _dt(table),
+                               _dev(out, "out"), _dt(out), _stream()), "embedding")
+    return out

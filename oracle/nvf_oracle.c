@@ -1,0 +1,365 @@
+/*
+ * nvf_oracle.c -- scalar C restatement of Nano_vLLM_cpp's fused per-layer ops.
+ *
+ * TEST INFRASTRUCTURE ONLY (the checker, never the product).  See nvf_oracle.h
+ * for the pin of every function.  Citations are Nano_vLLM_cpp source paths.
+ */
+#include "nvf_oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* ---- storage codecs ----------------------------------------------------- */
+
+/* include/nanovllm/common.hpp:28-54: exact fp16 decode, subnormals included. */
+float orc_fp16_to_f32(uint16_t h) {
+  uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+  uint32_t ex = (h >> 10) & 0x1fu;
+  uint32_t man = h & 0x3ffu;
+  uint32_t bits;
+  if (ex == 0) {
+    if (man == 0) {
+      bits = sign;
+    } else {
+      /* value = man * 2^-24; normalise the mantissa */
+      int e = 127 - 14;
+      while (!(man & 0x400u)) {
+        man <<= 1;
+        --e;
+      }
+      bits = sign | ((uint32_t)e << 23) | ((man & 0x3ffu) << 13);
+    }
+  } else if (ex == 0x1fu) {
+    bits = sign | 0x7f800000u | (man << 13);
+  } else {
+    bits = sign | ((ex + 112u) << 23) | (man << 13);
+  }
+  float f;
+  memcpy(&f, &bits, 4);
+  return f;
+}
+
+/* include/nanovllm/common.hpp:65-91: round-to-nearest-even, overflow -> Inf.
+ * NaN keeps a quiet NaN (the reference maps NaN to Inf; no path here makes one). */
+uint16_t orc_f32_to_fp16(float f) {
+  uint32_t b;
+  memcpy(&b, &f, 4);
+  uint32_t sign = (b >> 16) & 0x8000u;
+  uint32_t absb = b & 0x7fffffffu;
+  if (absb > 0x7f800000u) return (uint16_t)(sign | 0x7e00u);
+  int32_t ex = (int32_t)(absb >> 23) - 127 + 15;
+  uint32_t man = absb & 0x7fffffu;
+  if (ex >= 31) return (uint16_t)(sign | 0x7c00u);
+  if (ex <= 0) {
+    if (ex < -10) return (uint16_t)sign;
+    man |= 0x800000u;
+    uint32_t sh = (uint32_t)(14 - ex);
+    uint32_t m = man >> sh;
+    uint32_t rem = man & ((1u << sh) - 1u);
+    uint32_t halfway = 1u << (sh - 1);
+    if (rem > halfway || (rem == halfway && (m & 1u))) ++m;
+    return (uint16_t)(sign | m); /* m may carry into the exponent field: correct */
+  }
+  uint32_t m = man >> 13;
+  uint32_t rem = man & 0x1fffu;
+  uint32_t out = ((uint32_t)ex << 10) | m;
+  if (rem > 0x1000u || (rem == 0x1000u && (m & 1u))) ++out; /* carry is correct */
+  if (out >= 0x7c00u) out = 0x7c00u;
+  return (uint16_t)(sign | out);
+}
+
+/* include/nanovllm/common.hpp:56-61 */
+float orc_bf16_to_f32(uint16_t h) {
+  uint32_t b = (uint32_t)h << 16;
+  float f;
+  memcpy(&f, &b, 4);
+  return f;
+}
+
+/* round-to-nearest-even fp32 -> bf16, quiet NaN preserved */
+uint16_t orc_f32_to_bf16(float f) {
+  uint32_t b;
+  memcpy(&b, &f, 4);
+  if ((b & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((b >> 16) | 0x40u);
+  uint32_t lsb = (b >> 16) & 1u;
+  b += 0x7fffu + lsb;
+  return (uint16_t)(b >> 16);
+}
+
+float orc_load(const void* p, int64_t i, int dtype) {
+  if (dtype == ORC_F32) return ((const float*)p)[i];
+  uint16_t h = ((const uint16_t*)p)[i];
+  return dtype == ORC_F16 ? orc_fp16_to_f32(h) : orc_bf16_to_f32(h);
+}
+
+void orc_store(void* p, int64_t i, float v, int dtype) {
+  if (dtype == ORC_F32)
+    ((float*)p)[i] = v;
+  else
+    ((uint16_t*)p)[i] = dtype == ORC_F16 ? orc_f32_to_fp16(v) : orc_f32_to_bf16(v);
+}
+
+/* src/model.cpp:416-420: inv_freq in double, rounded to float. */
+void orc_inv_freq(double theta, int head_dim, float* out) {
+  for (int i = 0; i < head_dim / 2; ++i) out[i] = (float)(1.0 / pow(theta, (2.0 * i) / head_dim));
+}
+
+/* ---- K-quant superblocks ----------------------------------------------- */
+
+/* 6-bit (scale, min) of group j from the 12-byte table:
+ * src/gguf.cpp:482-489 == src/hip_ops.hip:116-128 */
+static void q4k_scale_min(const uint8_t* s12, int j, uint32_t* sc, uint32_t* mn) {
+  if (j < 4) {
+    *sc = s12[j] & 63;
+    *mn = s12[j + 4] & 63;
+  } else {
+    *sc = (s12[j + 4] & 0xF) | ((s12[j - 4] >> 6) << 4);
+    *mn = (s12[j + 4] >> 4) | ((s12[j] >> 6) << 4);
+  }
+}
+
+/* Q4_K, 144 B: [fp16 d][fp16 dmin][12 B scales][128 B qs].
+ * GGML layout: src/gguf.cpp:477-496 (also tools/ref_top5.cpp:140-165):
+ *   group j reads bytes qs[(j>>1)*32 + kk], nibble (j&1)*4.
+ * HIP_LEGACY layout: src/hip_ops.hip:130-140 (qk_w_q4):
+ *   group j reads bytes qs[j*16 + (e&15)], low nibble when e < 16. */
+void orc_dequant_q4k_block(const uint8_t* blk, float* y, int layout) {
+  float d = orc_fp16_to_f32((uint16_t)(blk[0] | (blk[1] << 8)));
+  float dmin = orc_fp16_to_f32((uint16_t)(blk[2] | (blk[3] << 8)));
+  for (int j = 0; j < 8; ++j) {
+    uint32_t sc, mn;
+    q4k_scale_min(blk + 4, j, &sc, &mn);
+    float d1 = d * (float)sc, m1 = dmin * (float)mn;
+    for (int e = 0; e < 32; ++e) {
+      int q;
+      if (layout == ORC_QK_LAYOUT_GGML) {
+        q = (blk[16 + (j >> 1) * 32 + e] >> ((j & 1) * 4)) & 0xF;
+      } else {
+        uint8_t qb = blk[16 + j * 16 + (e & 15)];
+        q = e < 16 ? (qb & 0xF) : (qb >> 4);
+      }
+      y[j * 32 + e] = d1 * (float)q - m1;
+    }
+  }
+}
+
+/* Q5_K, 176 B: [fp16 d][fp16 dmin][12 B scales][32 B qh][128 B ql].
+ * tools/ref_top5.cpp:166-186 == src/hip_ops.hip:142-155 (qk_w_q5). */
+void orc_dequant_q5k_block(const uint8_t* blk, float* y) {
+  float d = orc_fp16_to_f32((uint16_t)(blk[0] | (blk[1] << 8)));
+  float dmin = orc_fp16_to_f32((uint16_t)(blk[2] | (blk[3] << 8)));
+  const uint8_t* qh = blk + 16;
+  const uint8_t* ql = blk + 48;
+  for (int group = 0; group < 4; ++group) {
+    for (int slot = 0; slot < 2; ++slot) {
+      int j = group * 2 + slot;
+      uint32_t sc, mn;
+      q4k_scale_min(blk + 4, j, &sc, &mn);
+      float d1 = d * (float)sc, m1 = dmin * (float)mn;
+      uint32_t hmask = (slot == 0 ? 1u : 2u) << (group * 2);
+      for (int l = 0; l < 32; ++l) {
+        int q = slot == 0 ? (ql[group * 32 + l] & 0xF) : (ql[group * 32 + l] >> 4);
+        if (qh[l] & hmask) q += 16;
+        y[group * 64 + slot * 32 + l] = d1 * (float)q - m1;
+      }
+    }
+  }
+}
+
+/* Q6_K, 210 B: [128 B ql][64 B qh][16 x int8 scales][fp16 d].
+ * src/gguf.cpp:500-518 == src/hip_ops.hip:157-182 (qk_w_q6); (d*sc)*(q-32). */
+void orc_dequant_q6k_block(const uint8_t* blk, float* y) {
+  float d = orc_fp16_to_f32((uint16_t)(blk[208] | (blk[209] << 8)));
+  for (int half = 0; half < 2; ++half) {
+    const uint8_t* ql = blk + half * 64;
+    const uint8_t* qh = blk + 128 + half * 32;
+    const int8_t* sc = (const int8_t*)(blk + 192 + half * 8);
+    for (int l = 0; l < 32; ++l) {
+      int is = l >> 4;
+      int q1 = (ql[l] & 0xF) | (((qh[l] >> 0) & 3) << 4);
+      int q2 = (ql[l + 32] & 0xF) | (((qh[l] >> 2) & 3) << 4);
+      int q3 = (ql[l] >> 4) | (((qh[l] >> 4) & 3) << 4);
+      int q4 = (ql[l + 32] >> 4) | (((qh[l] >> 6) & 3) << 4);
+      y[half * 128 + l] = d * (float)sc[is + 0] * (float)(q1 - 32);
+      y[half * 128 + l + 32] = d * (float)sc[is + 2] * (float)(q2 - 32);
+      y[half * 128 + l + 64] = d * (float)sc[is + 4] * (float)(q3 - 32);
+      y[half * 128 + l + 96] = d * (float)sc[is + 6] * (float)(q4 - 32);
+    }
+  }
+}
+
+/* ---- embedding gathers -------------------------------------------------- */
+
+/* src/hip_ops.hip:565-574 over the split planes of src/model.cpp:394-404:
+ * out[t,c] = fp16(ws[e>>5]) * int8(w8[e]), e = ids[t]*H + c.  Exact in fp32. */
+void orc_embedding_q8_split(const int64_t* ids, const uint8_t* w8, const uint16_t* ws, int64_t tokens,
+                            int64_t hidden, void* out, int out_dtype) {
+  for (int64_t t = 0; t < tokens; ++t)
+    for (int64_t c = 0; c < hidden; ++c) {
+      int64_t e = ids[t] * hidden + c;
+      float v = orc_fp16_to_f32(ws[e >> 5]) * (float)(int8_t)w8[e];
+      orc_store(out, t * hidden + c, v, out_dtype);
+    }
+}
+
+/* The same gather over interleaved 34-byte GGUF Q8_0 blocks
+ * (src/gguf.cpp:353-362; decode as tools/ref_top5.cpp:121-136). */
+void orc_embedding_q8_blocks(const int64_t* ids, const uint8_t* blocks, int64_t tokens, int64_t hidden,
+                             void* out, int out_dtype) {
+  for (int64_t t = 0; t < tokens; ++t)
+    for (int64_t c = 0; c < hidden; ++c) {
+      int64_t e = ids[t] * hidden + c;
+      const uint8_t* b = blocks + (e >> 5) * 34;
+      float s = orc_fp16_to_f32((uint16_t)(b[0] | (b[1] << 8)));
+      float v = s * (float)(int8_t)b[2 + (e & 31)];
+      orc_store(out, t * hidden + c, v, out_dtype);
+    }
+}
+
+/* src/hip_ops.hip:600-609 (+ qk_w :184-193): element e = ids[t]*H + c lives in
+ * superblock e>>8 at offset e&255; kinds 12/13/14 = Q4_K/Q5_K/Q6_K. */
+void orc_embedding_qk(const int64_t* ids, const uint8_t* wq, int64_t tokens, int64_t hidden, int kind,
+                      int layout, void* out, int out_dtype) {
+  int64_t bb = kind == 12 ? 144 : (kind == 13 ? 176 : 210);
+  float y[256];
+  int64_t cached = -1;
+  for (int64_t t = 0; t < tokens; ++t)
+    for (int64_t c = 0; c < hidden; ++c) {
+      int64_t e = ids[t] * hidden + c;
+      int64_t b = e >> 8;
+      if (b != cached) {
+        const uint8_t* blk = wq + b * bb;
+        if (kind == 12)
+          orc_dequant_q4k_block(blk, y, layout);
+        else if (kind == 13)
+          orc_dequant_q5k_block(blk, y);
+        else
+          orc_dequant_q6k_block(blk, y);
+        cached = b;
+      }
+      orc_store(out, t * hidden + c, y[e & 255], out_dtype);
+    }
+}
+
+/* src/hip_ops.hip:553-563 (embedding_kernel<uint16_t>) */
+void orc_embedding_u16(const int64_t* ids, const uint16_t* table, int64_t tokens, int64_t hidden,
+                       int table_bf16, void* out, int out_dtype) {
+  for (int64_t t = 0; t < tokens; ++t)
+    for (int64_t c = 0; c < hidden; ++c) {
+      uint16_t h = table[ids[t] * hidden + c];
+      float v = table_bf16 ? orc_bf16_to_f32(h) : orc_fp16_to_f32(h);
+      orc_store(out, t * hidden + c, v, out_dtype);
+    }
+}
+
+/* ---- norms -------------------------------------------------------------- */
+
+/* tools/ref_top5.cpp:243-252 (double accumulation; inv rounded to float);
+ * operation order of src/hip_ops.hip:373-393: out = (x * inv) * w. */
+static void rms_row(const float* xr, const void* w, float* o, int64_t hidden, float eps, int dtype) {
+  double s = 0.0;
+  for (int64_t i = 0; i < hidden; ++i) s += (double)xr[i] * xr[i];
+  float inv = (float)(1.0 / sqrt(s / (double)hidden + (double)eps));
+  for (int64_t i = 0; i < hidden; ++i) o[i] = xr[i] * inv * orc_load(w, i, dtype);
+}
+
+void orc_rms_norm(const void* x, const void* w, void* out, int64_t rows, int64_t hidden, float eps,
+                  int dtype) {
+  float* xr = (float*)malloc(sizeof(float) * (size_t)hidden * 2);
+  float* o = xr + hidden;
+  for (int64_t r = 0; r < rows; ++r) {
+    for (int64_t i = 0; i < hidden; ++i) xr[i] = orc_load(x, r * hidden + i, dtype);
+    rms_row(xr, w, o, hidden, eps, dtype);
+    for (int64_t i = 0; i < hidden; ++i) orc_store(out, r * hidden + i, o[i], dtype);
+  }
+  free(xr);
+}
+
+/* src/hip_ops.hip:395-417 + tools/ref_top5.cpp:346-348: residual <- x + residual
+ * (stored, i.e. rounded to the storage dtype), then RMSNorm of the stored row. */
+void orc_rms_norm_add(const void* x, void* residual, const void* w, void* out, int64_t rows,
+                      int64_t hidden, float eps, int dtype) {
+  float* rr = (float*)malloc(sizeof(float) * (size_t)hidden * 2);
+  float* o = rr + hidden;
+  for (int64_t r = 0; r < rows; ++r) {
+    for (int64_t i = 0; i < hidden; ++i) {
+      float v = orc_load(x, r * hidden + i, dtype) + orc_load(residual, r * hidden + i, dtype);
+      orc_store(residual, r * hidden + i, v, dtype);
+      rr[i] = orc_load(residual, r * hidden + i, dtype);
+    }
+    rms_row(rr, w, o, hidden, eps, dtype);
+    for (int64_t i = 0; i < hidden; ++i) orc_store(out, r * hidden + i, o[i], dtype);
+  }
+  free(rr);
+}
+
+/* ---- SwiGLU ------------------------------------------------------------- */
+
+/* src/hip_ops.hip:419-429 and tools/ref_top5.cpp:576:
+ * out[r,c] = g / (1 + expf(-g)) * u, g = gu[r, c], u = gu[r, I + c]. */
+void orc_silu_and_mul(const void* gate_up, void* out, int64_t rows, int64_t inter, int dtype) {
+  for (int64_t r = 0; r < rows; ++r)
+    for (int64_t c = 0; c < inter; ++c) {
+      float g = orc_load(gate_up, r * 2 * inter + c, dtype);
+      float u = orc_load(gate_up, r * 2 * inter + inter + c, dtype);
+      orc_store(out, r * inter + c, g / (1.0f + expf(-g)) * u, dtype);
+    }
+}
+
+/* ---- RoPE --------------------------------------------------------------- */
+
+/* NeoX rotate-half on one head held in fp32, src/hip_ops.hip:431-450 and
+ * tools/ref_top5.cpp:409-426: angle = float(pos) * inv_freq[d]. */
+static void rope_head(float* hv, float pos, const float* inv_freq, int head_dim) {
+  int half = head_dim / 2;
+  for (int d = 0; d < half; ++d) {
+    float fr = pos * inv_freq[d];
+    float c = cosf(fr), s = sinf(fr);
+    float x1 = hv[d], x2 = hv[d + half];
+    hv[d] = x1 * c - x2 * s;
+    hv[d + half] = x2 * c + x1 * s;
+  }
+}
+
+void orc_rope(void* data, const int64_t* positions, int64_t tokens, int heads, int head_dim,
+              int64_t stride, const float* inv_freq, int dtype) {
+  float* hv = (float*)malloc(sizeof(float) * (size_t)head_dim);
+  for (int64_t t = 0; t < tokens; ++t)
+    for (int h = 0; h < heads; ++h) {
+      int64_t base = t * stride + (int64_t)h * head_dim;
+      for (int d = 0; d < head_dim; ++d) hv[d] = orc_load(data, base + d, dtype);
+      rope_head(hv, (float)positions[t], inv_freq, head_dim);
+      for (int d = 0; d < head_dim; ++d) orc_store(data, base + d, hv[d], dtype);
+    }
+  free(hv);
+}
+
+/* Qwen3 QK-norm then RoPE, src/model.cpp:774-778 (rms_norm rows = T*heads,
+ * hidden = head_dim, tools/ref_top5.cpp:398-407), then rope as above.  The
+ * normalised head stays fp32 between the two steps; one rounding at the end.
+ * A NULL gamma skips the norm for that tensor. */
+static void qk_one(void* buf, const int64_t* positions, const void* gw, const float* inv_freq,
+                   int64_t tokens, int heads, int head_dim, int64_t stride, float eps, int dtype) {
+  float* hv = (float*)malloc(sizeof(float) * (size_t)head_dim * 2);
+  float* nv = hv + head_dim;
+  for (int64_t t = 0; t < tokens; ++t)
+    for (int h = 0; h < heads; ++h) {
+      int64_t base = t * stride + (int64_t)h * head_dim;
+      for (int d = 0; d < head_dim; ++d) hv[d] = orc_load(buf, base + d, dtype);
+      if (gw) {
+        rms_row(hv, gw, nv, head_dim, eps, dtype);
+        memcpy(hv, nv, sizeof(float) * (size_t)head_dim);
+      }
+      rope_head(hv, (float)positions[t], inv_freq, head_dim);
+      for (int d = 0; d < head_dim; ++d) orc_store(buf, base + d, hv[d], dtype);
+    }
+  free(hv);
+}
+
+void orc_qk_norm_rope(void* q, void* k, const int64_t* positions, const void* q_w, const void* k_w,
+                      const float* inv_freq, int64_t tokens, int q_heads, int kv_heads, int head_dim,
+                      int64_t q_stride, int64_t k_stride, float eps, int dtype) {
+  if (q && q_heads > 0) qk_one(q, positions, q_w, inv_freq, tokens, q_heads, head_dim, q_stride, eps, dtype);
+  if (k && kv_heads > 0) qk_one(k, positions, k_w, inv_freq, tokens, kv_heads, head_dim, k_stride, eps, dtype);
+}

@@ -1,0 +1,83 @@
+/*
+ * nvf_oracle.h -- CPU restatement of Nano_vLLM_cpp's fused per-layer ops.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This library is the checker for the HIP kernels in
+ * nano_vllm_cpp_amd/csrc.  Only tests/, __graft_entry__.smoke() and the
+ * cpu_baseline leg of bench.py may load it.  The product library never links it
+ * and has no CPU fallback.
+ *
+ * Every function states the reference file:line whose loop it restates
+ * (paths relative to the Nano_vLLM_cpp source tree).  All arithmetic is scalar,
+ * single-threaded C compiled -O2 (the reference's own -O2, CMakeLists.txt:33),
+ * with fp32 math on upcast inputs and one rounding to the storage dtype.
+ *
+ * Parity pins (each checked in tests/test_oracle.py):
+ *   fp16/bf16 codecs ......... exhaustive 65536-code round trip vs numpy + RNE
+ *                              midpoint cases
+ *   Q8_0 ..................... hand vector vulkanised/test_gguf2vk.py:77-83;
+ *                              split-plane == 34 B-block equivalence
+ *   Q4_K / Q6_K .............. bytes produced by the reference's own
+ *                              gguf.cpp dequant (oracle/_ref, tests/golden)
+ *   Q5_K ..................... closed forms on hand-built blocks (the
+ *                              reference's host Q5_K decoder lives inside
+ *                              tools/ref_top5.cpp's main program and cannot
+ *                              be linked); on the GPU box also compared with
+ *                              the reference's own hip_embedding_qk kind 13
+ *   RMSNorm (+add) ........... closed form test/test_basic.cpp:23-31,
+ *                              homogeneity and gamma-linearity invariants
+ *   RoPE / QK-norm ........... pos=0 identity, pair-norm preservation,
+ *                              rotate(p) then rotate(-p) identity, composition
+ *   SiLU*up .................. silu(0)=0, silu(g)-silu(-g)=g, double-exp
+ *                              brute force
+ */
+#ifndef NVF_ORACLE_H
+#define NVF_ORACLE_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum { ORC_F32 = 0, ORC_F16 = 1, ORC_BF16 = 2 };
+enum { ORC_QK_LAYOUT_GGML = 0, ORC_QK_LAYOUT_HIP_LEGACY = 1 };
+
+float orc_fp16_to_f32(uint16_t h);
+uint16_t orc_f32_to_fp16(float f);
+float orc_bf16_to_f32(uint16_t h);
+uint16_t orc_f32_to_bf16(float f);
+
+/* element loads/stores through a dtype tag (storage -> fp32 -> storage) */
+float orc_load(const void* p, int64_t i, int dtype);
+void orc_store(void* p, int64_t i, float v, int dtype);
+
+void orc_inv_freq(double theta, int head_dim, float* out);
+
+void orc_dequant_q4k_block(const uint8_t* blk, float* y, int layout);
+void orc_dequant_q5k_block(const uint8_t* blk, float* y);
+void orc_dequant_q6k_block(const uint8_t* blk, float* y);
+
+void orc_embedding_q8_split(const int64_t* ids, const uint8_t* w8, const uint16_t* ws, int64_t tokens,
+                            int64_t hidden, void* out, int out_dtype);
+void orc_embedding_q8_blocks(const int64_t* ids, const uint8_t* blocks, int64_t tokens, int64_t hidden,
+                             void* out, int out_dtype);
+void orc_embedding_qk(const int64_t* ids, const uint8_t* wq, int64_t tokens, int64_t hidden, int kind,
+                      int layout, void* out, int out_dtype);
+void orc_embedding_u16(const int64_t* ids, const uint16_t* table, int64_t tokens, int64_t hidden,
+                       int table_bf16, void* out, int out_dtype);
+
+void orc_rms_norm(const void* x, const void* w, void* out, int64_t rows, int64_t hidden, float eps,
+                  int dtype);
+void orc_rms_norm_add(const void* x, void* residual, const void* w, void* out, int64_t rows,
+                      int64_t hidden, float eps, int dtype);
+void orc_silu_and_mul(const void* gate_up, void* out, int64_t rows, int64_t inter, int dtype);
+void orc_rope(void* data, const int64_t* positions, int64_t tokens, int heads, int head_dim,
+              int64_t stride, const float* inv_freq, int dtype);
+void orc_qk_norm_rope(void* q, void* k, const int64_t* positions, const void* q_w, const void* k_w,
+                      const float* inv_freq, int64_t tokens, int q_heads, int kv_heads, int head_dim,
+                      int64_t q_stride, int64_t k_stride, float eps, int dtype);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

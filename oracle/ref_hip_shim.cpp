@@ -1,0 +1,44 @@
+// C-ABI shim over the reference's own HIP launchers (src/hip_ops.hip, C++
+// linkage, include/nanovllm/hip_ops.hpp:14-34), compiled for gfx950 from the
+// reference sources where they lie (see Makefile) into oracle/_ref/.
+// TEST INFRASTRUCTURE ONLY: GPU parity tests use it as a second checker beside
+// the C oracle.  Each wrapper launches on the null stream like the reference
+// and synchronises so the caller can read the result.
+#include <cstdint>
+
+#include "nanovllm/hip_ops.hpp"
+
+extern "C" {
+void ref_hip_rms_norm(const float* x, const float* w, float* out, int rows, int hidden, float eps) {
+  hip_rms_norm(x, w, out, rows, hidden, eps);
+  HIP_CHECK(hipDeviceSynchronize());
+}
+void ref_hip_rms_norm_add(const float* x, float* residual, const float* w, float* out, int rows, int hidden,
+                          float eps) {
+  hip_rms_norm_add(x, residual, w, out, rows, hidden, eps);
+  HIP_CHECK(hipDeviceSynchronize());
+}
+void ref_hip_silu_and_mul(const float* gate_up, float* out, int rows, int inter) {
+  hip_silu_and_mul(gate_up, out, rows, inter);
+  HIP_CHECK(hipDeviceSynchronize());
+}
+void ref_hip_rope_inplace(float* data, const int64_t* positions, int tokens, int heads, int head_dim,
+                          int64_t stride, const float* inv_freq) {
+  hip_rope_inplace(data, positions, tokens, heads, head_dim, stride, inv_freq);
+  HIP_CHECK(hipDeviceSynchronize());
+}
+void ref_hip_embedding_q8(const int64_t* ids, const uint8_t* w8, const uint16_t* ws, int tokens, int hidden,
+                          float* out) {
+  hip_embedding_q8(ids, w8, ws, tokens, hidden, out);
+  HIP_CHECK(hipDeviceSynchronize());
+}
+void ref_hip_embedding_qk(const int64_t* ids, const uint8_t* wq, int tokens, int hidden, float* out, int kind) {
+  hip_embedding_qk(ids, wq, tokens, hidden, out, kind);
+  HIP_CHECK(hipDeviceSynchronize());
+}
+void ref_hip_embedding_u16(const int64_t* ids, const uint16_t* table, int tokens, int hidden, float* out,
+                           int table_bf16) {
+  hip_embedding_u16(ids, table, tokens, hidden, out, table_bf16 != 0);
+  HIP_CHECK(hipDeviceSynchronize());
+}
+}

@@ -1,0 +1,89 @@
+"""The C-ABI library: loads, exports every symbol include/nvf_ops.h declares, and
+rejects bad arguments on the host (no GPU work is issued by these tests)."""
+from __future__ import annotations
+
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from nano_vllm_cpp_amd import ops
+from tests import harness as H
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "nvf_ops.h"
+
+
+def declared_functions() -> list[str]:
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return re.findall(r"^\s*(?:const\s+)?[a-z_0-9]+\s*\*?\s*([a-z_0-9]+)\s*\(", text, flags=re.M)
+
+
+def test_header_declares_expected_surface():
+    names = set(declared_functions())
+    dropins = {"hip_rms_norm", "hip_rms_norm_add", "hip_silu_and_mul", "hip_rope_inplace", "hip_embedding",
+               "hip_embedding_u16", "hip_embedding_q8", "hip_embedding_qk"}
+    assert dropins <= names
+    assert {"nvf_rms_norm_add", "nvf_qk_norm_rope", "nvf_silu_and_mul", "nvf_embedding_q8_0",
+            "nvf_embedding_q8_0_blocks", "nvf_embedding_qk"} <= names
+
+
+def test_library_exports_every_declared_symbol():
+    lib = ops.lib()
+    names = declared_functions()
+    assert names
+    for n in names:
+        assert hasattr(lib, n), f"{n} declared in nvf_ops.h but not exported"
+        assert n in ops.SIGNATURES, f"{n} has no ctypes signature in ops.py"
+    assert set(ops.SIGNATURES) == set(names)
+    assert lib.nvf_abi_version() == 1
+
+
+def _status(rc: int) -> tuple[int, str]:
+    return rc, ops.lib().nvf_last_error().decode()
+
+
+def test_host_argument_checks():
+    lib = ops.lib()
+    p = 0x1000  # never dereferenced: every call below fails or returns before a launch
+    rc, msg = _status(lib.nvf_rms_norm_add(p, p, p, p, 4, 64, 1e-6, 7, None))
+    assert rc == -1 and "dtype" in msg
+    rc, msg = _status(lib.nvf_rms_norm_add(p, p, p, p, -1, 64, 1e-6, 1, None))
+    assert rc == -1 and "shape" in msg
+    assert lib.nvf_rms_norm_add(p, p, p, p, 0, 64, 1e-6, 1, None) == 0       # empty: no launch
+    rc, msg = _status(lib.nvf_rms_norm_add(None, p, p, p, 4, 64, 1e-6, 1, None))
+    assert rc == -1 and "NULL" in msg
+    rc, msg = _status(lib.nvf_silu_and_mul(p, p, 3, -2, 1, None))
+    assert rc == -1
+    assert lib.nvf_silu_and_mul(p, p, 0, 10, 1, None) == 0
+    rc, msg = _status(lib.nvf_embedding_qk(p, p, 4, 256, 0, 11, 0, p, 1, None))
+    assert rc == -1 and "kind" in msg
+    rc, msg = _status(lib.nvf_embedding_qk(p, p, 4, 256, 0, 12, 5, p, 1, None))
+    assert rc == -1 and "layout" in msg
+    rc, msg = _status(lib.nvf_embedding_q8_0_blocks(p, p, 4, 48, 0, p, 1, None))
+    assert rc == -1 and "multiple of 32" in msg
+    rc, msg = _status(lib.nvf_embedding_q8_0(p, p, None, 4, 64, 0, p, 1, None))
+    assert rc == -1 and "scale" in msg
+    assert lib.nvf_embedding_q8_0(p, p, p, 0, 64, 0, p, 1, None) == 0
+    rc, msg = _status(lib.nvf_qk_norm_rope(p, p, p, p, None, p, 4, 2, 1, 128, 256, 128, 1e-6, 1, None))
+    assert rc == -1 and "q_w and k_w" in msg
+    rc, msg = _status(lib.nvf_qk_norm_rope(p, p, p, None, None, p, 4, 2, 1, 128, 200, 128, 1e-6, 1, None))
+    assert rc == -1 and "stride" in msg
+    assert lib.nvf_qk_norm_rope(p, p, p, None, None, p, 0, 2, 1, 128, 256, 128, 1e-6, 1, None) == 0
+
+
+def test_inv_freq_host_helper_matches_oracle():
+    for theta, hd in ((1e6, 128), (1e6, 64), (10000.0, 256), (5e5, 80)):
+        mine = ops.rope_inv_freq(theta, hd).numpy()
+        ref = np.empty(hd // 2, np.float32)
+        H.oracle().orc_inv_freq(theta, hd, H.ptr(ref))
+        assert np.array_equal(mine, ref)
+    with pytest.raises(ops.NvfError):
+        ops.rope_inv_freq(1e6, 0)
+
+
+def test_missing_library_fails_loudly(monkeypatch, tmp_path):
+    monkeypatch.setattr(ops, "LIB_PATH", tmp_path / "nope.so")
+    monkeypatch.setattr(ops, "_lib", None)
+    with pytest.raises(RuntimeError, match="no CPU fallback"):
+        ops.lib()

@@ -1,0 +1,393 @@
+"""Pins the C oracle (oracle/nvf_oracle.c) before it is trusted as the checker.
+
+Each function is checked against the reference's own outputs (golden vectors
+written by the reference's gguf.cpp / common.hpp, and the live reference build
+in oracle/_ref when present), hand vectors from the reference's tests, or what
+the mathematics fixes (closed forms, invariants, exhaustive codec checks).
+"""
+from __future__ import annotations
+
+import math
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from tests import harness as H
+
+GOLD = np.load(Path(__file__).resolve().parent / "golden" / "reference_vectors.npz")
+
+
+@pytest.fixture(scope="module")
+def o():
+    return H.oracle()
+
+
+# ---------------------------------------------------------------------------
+# storage codecs
+# ---------------------------------------------------------------------------
+def test_fp16_decode_exhaustive(o):
+    codes = np.arange(65536, dtype=np.uint16)
+    got = np.array([o.orc_fp16_to_f32(int(c)) for c in codes], np.float32)
+    ref = codes.view(np.float16).astype(np.float32)
+    nan = np.isnan(ref)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), ref[~nan].view(np.uint32))
+
+
+def test_fp16_codecs_match_reference_vectors(o):
+    got = np.array([o.orc_fp16_to_f32(int(c)) for c in GOLD["fp16_codes"]], np.float32)
+    ref = GOLD["fp16_decoded"]
+    nan = np.isnan(ref)
+    assert np.array_equal(got[~nan].view(np.uint32), ref[~nan].view(np.uint32))
+    enc = np.array([o.orc_f32_to_fp16(float(v)) for v in GOLD["f32_values"]], np.uint16)
+    assert np.array_equal(enc, GOLD["fp16_encoded"])
+
+
+def test_fp16_encode_matches_numpy_rne(o):
+    r = np.random.default_rng(1)
+    f = np.concatenate([r.normal(0, 1, 4000), r.normal(0, 1e-6, 2000), r.uniform(-7e4, 7e4, 2000),
+                        (np.arange(1, 3000) + 0.5) * 2.0 ** -24, [0.0, -0.0, np.inf, -np.inf]]).astype(np.float32)
+    got = np.array([o.orc_f32_to_fp16(float(v)) for v in f], np.uint16)
+    with np.errstate(over="ignore"):
+        assert np.array_equal(got, f.astype(np.float16).view(np.uint16))
+
+
+def test_bf16_codecs_match_torch(o):
+    r = np.random.default_rng(2)
+    f = np.concatenate([r.normal(0, 1, 4000), r.normal(0, 1e30, 500), r.normal(0, 1e-30, 500),
+                        [0.0, -0.0, np.inf, -np.inf]]).astype(np.float32)
+    # exact ties: low 16 bits == 0x8000 with even and odd kept mantissa
+    ties = (r.integers(0x3F000000 >> 16, 0x43000000 >> 16, 200).astype(np.uint32) << 16) | 0x8000
+    f = np.concatenate([f, ties.view(np.float32)])
+    got = np.array([o.orc_f32_to_bf16(float(v)) for v in f], np.uint16)
+    ref = torch.from_numpy(f).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(got, ref)
+    back = np.array([o.orc_bf16_to_f32(int(c)) for c in got], np.float32)
+    assert np.array_equal(back.view(np.uint32), got.astype(np.uint32) << 16)
+    assert np.array_equal(H.to_storage(f, H.BF16), ref)
+
+
+# ---------------------------------------------------------------------------
+# Q8_0
+# ---------------------------------------------------------------------------
+def test_q8_0_hand_vector(o):
+    """vulkanised/test_gguf2vk.py:77-83: scale 2.0 x [0,1,-1,127,-127] -> [0,2,-2,254,-254]."""
+    q = np.array([0, 1, -1, 127, -127] + [0] * 27, np.int8)
+    ws = np.array([np.float16(2.0)], np.float16).view(np.uint16)
+    blocks = H.q8_split_to_blocks(q, ws)
+    ids = np.zeros(1, np.int64)
+    for dt in (H.F32, H.F16, H.BF16):
+        a = np.empty(32, H.NP_STORAGE[dt])
+        b = np.empty(32, H.NP_STORAGE[dt])
+        o.orc_embedding_q8_split(H.ptr(ids), H.ptr(q), H.ptr(ws), 1, 32, H.ptr(a), dt)
+        o.orc_embedding_q8_blocks(H.ptr(ids), H.ptr(blocks), 1, 32, H.ptr(b), dt)
+        assert list(H.from_storage(a, dt)[:5]) == [0, 2, -2, 254, -254]
+        assert np.array_equal(a, b)
+
+
+def test_q8_0_gather_exact_product(o):
+    """Split planes == 34 B blocks == fp16(scale) * int8 computed in float64 (exact)."""
+    r = H.rng(3)
+    V, Hd, T = 37, 96, 50
+    w8, ws = H.gen_q8_0(r, V, Hd)
+    ws[0] = 0x0001  # a subnormal scale: exact decode required
+    blocks = H.q8_split_to_blocks(w8, ws)
+    ids = r.integers(0, V, T).astype(np.int64)
+    ids[0] = 0
+    a = np.empty((T, Hd), np.float32)
+    b = np.empty((T, Hd), np.float32)
+    o.orc_embedding_q8_split(H.ptr(ids), H.ptr(w8), H.ptr(ws), T, Hd, H.ptr(a), H.F32)
+    o.orc_embedding_q8_blocks(H.ptr(ids), H.ptr(blocks), T, Hd, H.ptr(b), H.F32)
+    scale = ws.view(np.float16).astype(np.float64).reshape(V, Hd // 32).repeat(32, axis=1)
+    exact = (scale * w8.reshape(V, Hd).astype(np.float64))[ids]
+    assert np.array_equal(a.astype(np.float64), exact)
+    assert np.array_equal(a, b)
+
+
+# ---------------------------------------------------------------------------
+# K-quants
+# ---------------------------------------------------------------------------
+def _deq(o, fn, blocks, bb, *extra):
+    n = blocks.size // bb
+    y = np.empty(n * 256, np.float32)
+    for i in range(n):
+        blk = np.ascontiguousarray(blocks[i * bb:(i + 1) * bb])
+        fn(H.ptr(blk), y[i * 256:].ctypes.data, *extra)
+    return y
+
+
+def test_q4k_matches_reference_gguf_cpp(o):
+    y = _deq(o, o.orc_dequant_q4k_block, GOLD["q4k_blocks"], 144, H.GGML)
+    assert np.array_equal(y.view(np.uint32), GOLD["q4k_expected"].view(np.uint32))
+
+
+def test_q6k_matches_reference_gguf_cpp(o):
+    y = _deq(o, o.orc_dequant_q6k_block, GOLD["q6k_blocks"], 210)
+    assert np.array_equal(y.view(np.uint32), GOLD["q6k_expected"].view(np.uint32))
+
+
+def test_kquant_vs_live_reference_build(o):
+    ref = H.ref_host()
+    if ref is None:
+        pytest.skip("oracle/_ref not built here")
+    r = H.rng(4)
+    for kind, bb, fn, extra in (("Q4_K", 144, o.orc_dequant_q4k_block, (H.GGML,)),
+                                ("Q6_K", 210, o.orc_dequant_q6k_block, ())):
+        blocks = H.gen_raw_blocks(r, 64, bb, (0, 2) if kind == "Q4_K" else (208,))
+        mine = _deq(o, fn, blocks, bb, *extra)
+        theirs = np.empty_like(mine)
+        for i in range(64):
+            blk = np.ascontiguousarray(blocks[i * bb:(i + 1) * bb])
+            assert ref.ref_dequant_block_f32(kind.encode(), H.ptr(blk), theirs[i * 256:].ctypes.data)
+        assert np.array_equal(mine.view(np.uint32), theirs.view(np.uint32)), kind
+
+
+def _unit_block_q4k(sc, mn):
+    b = np.zeros(144, np.uint8)
+    b[0:4] = np.array([1.0, 1.0], np.float16).view(np.uint8)
+    b[4:16] = H.pack_q4k_scales(np.array(sc), np.array(mn))
+    return b
+
+
+def test_q4k_legacy_layout_closed_form(o):
+    """src/hip_ops.hip:130-140: element 32j+e reads byte 16 + 16j + (e & 15), low nibble for e < 16."""
+    b = _unit_block_q4k([1] * 8, [0] * 8)
+    b[16:] = (np.arange(128) * 37 % 256).astype(np.uint8)
+    y = np.empty(256, np.float32)
+    o.orc_dequant_q4k_block(H.ptr(b), y.ctypes.data, H.HIP_LEGACY)
+    qs = b[16:].astype(int)
+    for i in range(256):
+        j, e = divmod(i, 32)
+        byte = qs[16 * j + (e & 15)]
+        assert y[i] == (byte & 15 if e < 16 else byte >> 4), i
+    # and the GGML layout differs on the same bytes
+    g = np.empty(256, np.float32)
+    o.orc_dequant_q4k_block(H.ptr(b), g.ctypes.data, H.GGML)
+    assert not np.array_equal(g, y)
+
+
+def test_q5k_closed_form(o):
+    """Q5_K (src/hip_ops.hip:142-155): with d = 1, dmin = 0, unit scales the
+    element equals its 5-bit code: low nibble from ql, bit 4 from qh."""
+    r = H.rng(5)
+    codes = r.integers(0, 32, 256)
+    b = np.zeros(176, np.uint8)
+    b[0:4] = np.array([1.0, 0.0], np.float16).view(np.uint8)
+    b[4:16] = H.pack_q4k_scales(np.ones(8, int), np.zeros(8, int))
+    qh = np.zeros(32, np.uint8)
+    ql = np.zeros(128, np.uint8)
+    for i, v in enumerate(codes):
+        group, slot, l = i // 64, (i % 64) // 32, i % 32
+        ql[group * 32 + l] |= (v & 15) << (4 * slot)
+        qh[l] |= (v >> 4) << (2 * group + slot)
+    b[16:48] = qh
+    b[48:] = ql
+    y = np.empty(256, np.float32)
+    o.orc_dequant_q5k_block(H.ptr(b), y.ctypes.data)
+    assert np.array_equal(y, codes.astype(np.float32))
+    # scale/min path: group j scaled by (j+1), offset by -j*dmin
+    b[0:4] = np.array([1.0, 0.5], np.float16).view(np.uint8)
+    b[4:16] = H.pack_q4k_scales(np.arange(1, 9), np.arange(8))
+    o.orc_dequant_q5k_block(H.ptr(b), y.ctypes.data)
+    j = np.arange(256) // 32
+    assert np.array_equal(y, ((j + 1) * codes - 0.5 * j).astype(np.float32))
+
+
+def test_q4k_scale_min_unpack_closed_form(o):
+    """All 64 x 64 (scale, min) values survive the 12-byte packing for every group."""
+    for s in range(0, 64, 7):
+        for m in range(0, 64, 5):
+            sc = (np.arange(8) * 9 + s) % 64
+            mn = (np.arange(8) * 13 + m) % 64
+            b = _unit_block_q4k(sc, mn)
+            b[16:] = 0x11  # every nibble = 1
+            y = np.empty(256, np.float32)
+            o.orc_dequant_q4k_block(H.ptr(b), y.ctypes.data, H.GGML)
+            assert np.array_equal(y, np.repeat(sc - mn, 32).astype(np.float32))
+
+
+def test_embedding_qk_matches_block_decode(o):
+    """Gather = block decode at element id*H + c, including rows that straddle superblocks."""
+    r = H.rng(6)
+    V, Hd, T = 24, 320, 20  # 320 is not a multiple of 256: rows straddle superblocks
+    for kind, bb in ((12, 144), (13, 176), (14, 210)):
+        nb = V * Hd // 256
+        blocks = H.gen_raw_blocks(r, nb, bb, (0, 2) if kind != 14 else (208,))
+        full = np.empty(nb * 256, np.float32)
+        for i in range(nb):
+            blk = np.ascontiguousarray(blocks[i * bb:(i + 1) * bb])
+            if kind == 12:
+                o.orc_dequant_q4k_block(H.ptr(blk), full[i * 256:].ctypes.data, H.GGML)
+            elif kind == 13:
+                o.orc_dequant_q5k_block(H.ptr(blk), full[i * 256:].ctypes.data)
+            else:
+                o.orc_dequant_q6k_block(H.ptr(blk), full[i * 256:].ctypes.data)
+        ids = r.integers(0, V, T).astype(np.int64)
+        out = np.empty((T, Hd), np.float32)
+        o.orc_embedding_qk(H.ptr(ids), H.ptr(blocks), T, Hd, kind, H.GGML, H.ptr(out), H.F32)
+        assert np.array_equal(out, full.reshape(V, Hd)[ids])
+
+
+# ---------------------------------------------------------------------------
+# RMSNorm
+# ---------------------------------------------------------------------------
+def test_rms_norm_closed_form(o):
+    """test/test_basic.cpp:23-31: [1,2,3,4], w = 1, eps = 1e-6."""
+    x = np.array([1, 2, 3, 4], np.float32)
+    w = np.ones(4, np.float32)
+    out = np.empty(4, np.float32)
+    o.orc_rms_norm(H.ptr(x), H.ptr(w), H.ptr(out), 1, 4, 1e-6, H.F32)
+    expected0 = 1.0 / math.sqrt(30.0 / 4.0 + 1e-6)
+    assert abs(out[0] - expected0) < 1e-4 and out[3] > out[0]
+    assert np.allclose(out, x / math.sqrt(7.5 + 1e-6), rtol=1e-6, atol=0)
+
+
+def test_rms_norm_invariants(o):
+    r = H.rng(7)
+    x = r.normal(0, 1, (8, 96)).astype(np.float32)
+    w = r.normal(1, 0.1, 96).astype(np.float32)
+    a = np.empty_like(x)
+    b = np.empty_like(x)
+    o.orc_rms_norm(H.ptr(x), H.ptr(w), H.ptr(a), 8, 96, 0.0, H.F32)
+    x2 = (x * 4.0).astype(np.float32)  # power-of-two scaling is exact
+    o.orc_rms_norm(H.ptr(x2), H.ptr(w), H.ptr(b), 8, 96, 0.0, H.F32)
+    assert np.allclose(a, b, rtol=2e-6, atol=0)
+    w2 = (w * 2.0).astype(np.float32)  # linear in the gamma
+    o.orc_rms_norm(H.ptr(x), H.ptr(w2), H.ptr(b), 8, 96, 0.0, H.F32)
+    assert np.array_equal(b, a * 2)
+    # mean of the squares of the normalised row (w = 1) is 1
+    ones = np.ones(96, np.float32)
+    o.orc_rms_norm(H.ptr(x), H.ptr(ones), H.ptr(b), 8, 96, 0.0, H.F32)
+    assert np.allclose((b.astype(np.float64) ** 2).mean(axis=1), 1.0, rtol=1e-6)
+
+
+def test_rms_norm_add_residual_and_norm(o):
+    r = H.rng(8)
+    for dt in (H.F32, H.F16, H.BF16):
+        x, res = H.gen_act(r, (5, 64), dt), H.gen_act(r, (5, 64), dt)
+        w = H.gen_act(r, (64,), dt, 1.0, 0.1)
+        res_out = res.copy()
+        out = np.empty_like(x)
+        o.orc_rms_norm_add(H.ptr(x), H.ptr(res_out), H.ptr(w), H.ptr(out), 5, 64, 1e-6, dt)
+        # residual = one RNE rounding of the fp32 sum
+        s = (H.from_storage(x, dt).astype(np.float32) + H.from_storage(res, dt).astype(np.float32))
+        assert np.array_equal(res_out, H.to_storage(s, dt))
+        # out = rms_norm of the stored residual
+        out2 = np.empty_like(x)
+        o.orc_rms_norm(H.ptr(res_out), H.ptr(w), H.ptr(out2), 5, 64, 1e-6, dt)
+        assert np.array_equal(out, out2)
+
+
+# ---------------------------------------------------------------------------
+# SiLU * up
+# ---------------------------------------------------------------------------
+def test_silu_closed_forms(o):
+    g = np.array([0.0, 1.0, -1.0, 20.0, -20.0, 100.0, -100.0, 3.5, -3.5], np.float32)
+    gu = np.concatenate([g, np.ones_like(g)]).reshape(1, -1).astype(np.float32)
+    out = np.empty((1, g.size), np.float32)
+    o.orc_silu_and_mul(H.ptr(gu), H.ptr(out), 1, g.size, H.F32)
+    s = out[0].astype(np.float64)
+    assert s[0] == 0.0
+    assert s[5] == 100.0 and s[6] == 0.0 or abs(s[6]) < 1e-40
+    for i, j in ((1, 2), (3, 4), (7, 8)):  # silu(g) - silu(-g) = g
+        assert abs((s[i] - s[j]) - g[i]) <= 2e-7 * abs(g[i])
+    exact = g.astype(np.float64) / (1 + np.exp(-g.astype(np.float64)))
+    assert np.allclose(s, exact, rtol=1e-6, atol=1e-30)
+
+
+def test_silu_brute_force(o):
+    r = H.rng(9)
+    R, I = 4, 1000
+    gu = r.normal(0, 3, (R, 2 * I)).astype(np.float32)
+    out = np.empty((R, I), np.float32)
+    o.orc_silu_and_mul(H.ptr(gu), H.ptr(out), R, I, H.F32)
+    g, u = gu[:, :I].astype(np.float64), gu[:, I:].astype(np.float64)
+    assert np.allclose(out, g / (1 + np.exp(-g)) * u, rtol=1e-6, atol=1e-12)
+
+
+# ---------------------------------------------------------------------------
+# RoPE / QK-norm
+# ---------------------------------------------------------------------------
+def _inv(o, theta, hd):
+    inv = np.empty(hd // 2, np.float32)
+    o.orc_inv_freq(theta, hd, H.ptr(inv))
+    return inv
+
+
+def test_inv_freq_closed_form(o):
+    inv = _inv(o, 1e6, 128)
+    assert inv[0] == 1.0
+    assert inv[32] == np.float32(1e-3)  # theta^(-64/128) = 1e-3
+    assert inv[16] == np.float32(10 ** -1.5)
+
+
+def test_rope_identity_at_zero_and_unit_vector(o):
+    r = H.rng(10)
+    T, heads, hd = 6, 3, 64
+    inv = _inv(o, 1e6, hd)
+    x = r.normal(0, 1, (T, heads * hd)).astype(np.float32)
+    y = x.copy()
+    pos = np.zeros(T, np.int64)
+    o.orc_rope(H.ptr(y), H.ptr(pos), T, heads, hd, heads * hd, H.ptr(inv), H.F32)
+    assert np.array_equal(x, y)  # cos 0 = 1, sin 0 = 0 exactly
+    # e_0 rotates to (cos p, sin p) with angle p * inv_freq[0] = p
+    e = np.zeros((T, hd), np.float32)
+    e[:, 0] = 1.0
+    pos = np.array([1, 2, 100, 4095, 8191, 3], np.int64)
+    o.orc_rope(H.ptr(e), H.ptr(pos), T, 1, hd, hd, H.ptr(inv), H.F32)
+    assert np.allclose(e[:, 0], np.cos(pos.astype(np.float64)), rtol=0, atol=2e-7)
+    assert np.allclose(e[:, hd // 2], np.sin(pos.astype(np.float64)), rtol=0, atol=2e-7)
+
+
+def test_rope_norm_preserving_and_inverse(o):
+    r = H.rng(11)
+    T, heads, hd = 16, 4, 128
+    inv = _inv(o, 1e6, hd)
+    x = r.normal(0, 1, (T, heads, hd)).astype(np.float32)
+    y = x.copy()
+    pos = r.integers(0, 4096, T).astype(np.int64)
+    o.orc_rope(H.ptr(y), H.ptr(pos), T, heads, hd, heads * hd, H.ptr(inv), H.F32)
+    n0 = x[..., :64].astype(np.float64) ** 2 + x[..., 64:].astype(np.float64) ** 2
+    n1 = y[..., :64].astype(np.float64) ** 2 + y[..., 64:].astype(np.float64) ** 2
+    assert np.allclose(n0, n1, rtol=1e-5, atol=1e-6)
+    neg = -pos
+    o.orc_rope(H.ptr(y), H.ptr(neg), T, heads, hd, heads * hd, H.ptr(inv), H.F32)
+    assert np.allclose(y, x, rtol=0, atol=5e-5)
+
+
+def test_qk_norm_rope_is_the_composition(o):
+    """fp32: fused oracle == rms_norm (rows = T*heads, hidden = hd) then rope, bit for bit."""
+    r = H.rng(12)
+    T, hq, hk, hd = 9, 4, 2, 128
+    inv = _inv(o, 1e6, hd)
+    q = r.normal(0, 1, (T, hq * hd)).astype(np.float32)
+    k = r.normal(0, 1, (T, hk * hd)).astype(np.float32)
+    qw = r.normal(1, 0.1, hd).astype(np.float32)
+    kw = r.normal(1, 0.1, hd).astype(np.float32)
+    pos = r.integers(0, 4096, T).astype(np.int64)
+    fq, fk = q.copy(), k.copy()
+    o.orc_qk_norm_rope(H.ptr(fq), H.ptr(fk), H.ptr(pos), H.ptr(qw), H.ptr(kw), H.ptr(inv), T, hq, hk, hd,
+                       hq * hd, hk * hd, 1e-6, H.F32)
+    uq, uk = np.empty_like(q), np.empty_like(k)
+    o.orc_rms_norm(H.ptr(q), H.ptr(qw), H.ptr(uq), T * hq, hd, 1e-6, H.F32)
+    o.orc_rms_norm(H.ptr(k), H.ptr(kw), H.ptr(uk), T * hk, hd, 1e-6, H.F32)
+    o.orc_rope(H.ptr(uq), H.ptr(pos), T, hq, hd, hq * hd, H.ptr(inv), H.F32)
+    o.orc_rope(H.ptr(uk), H.ptr(pos), T, hk, hd, hk * hd, H.ptr(inv), H.F32)
+    assert np.array_equal(fq, uq) and np.array_equal(fk, uk)
+
+
+# ---------------------------------------------------------------------------
+# tolerance helpers themselves
+# ---------------------------------------------------------------------------
+def test_tolerance_rule_rejects_two_ulp():
+    ref = H.to_storage(np.array([1.0, 3.0, -0.125], np.float32), H.F16)
+    one = ref + np.uint16(1)
+    H.assert_close(one, ref, H.F16)
+    with pytest.raises(AssertionError):
+        H.assert_close(ref + np.uint16(2), ref, H.F16)
+    refb = H.to_storage(np.array([1.0, 3.0], np.float32), H.BF16)
+    H.assert_close(refb + np.uint16(1), refb, H.BF16)
+    with pytest.raises(AssertionError):
+        H.assert_close(refb + np.uint16(2), refb, H.BF16)
