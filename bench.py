@@ -1,0 +1,296 @@
+"""Layer-op benchmark of the MI355X fused per-layer ops (one GPU).
+
+One step = one pass of the hot path over one batch of the workload (BASELINE
+config 2 by default: Qwen2.5-7B chunked prefill, 4 x 4096 = 16384 packed
+tokens, fp16 activations):
+
+  Q8_0 embedding gather (152064 x 3584 table, split planes) -> fp16 [T, 3584]
+  residual-add + RMSNorm [T, 3584]
+  NeoX RoPE on q [T, 28, 128] and k [T, 4, 128] (one fused launch)
+  SiLU(gate) * up [T, 18944]
+
+Every op reads synthetic inputs already resident in HBM.  Each op rotates over
+enough independent buffer sets (>= 1 GiB per op) that its inputs were last
+touched long before the launch, so the 256 MB MALL cannot serve them: the
+figures are HBM figures.  Per-op times come from HIP events on the stream the
+kernels run on; the dominant kernel (SwiGLU) gives the roofline object.
+
+The CPU baseline is the C oracle (single thread, -O2) timed on a bounded
+sample of the same workload on this host.
+
+Prints ONE JSON line.  `python bench.py --gpus N` with N > 1 exits: this build
+measures one GPU only.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "fused-op HBM GB/s (% of peak) + layer-op tokens/s at Qwen2.5-7B shapes"
+POOL_BYTES = 1 << 30
+
+
+def parse() -> argparse.Namespace:
+    p = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=50)
+    p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--config", type=int, default=2, help="BASELINE config index (1-4)")
+    p.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU-baseline budget (0 = skip)")
+    p.add_argument("--only", default="", help="comma list of ops to run (profiling): emb,rms,rope,silu,copy")
+    return p.parse_args()
+
+
+def op_bytes(cfg, e: int) -> dict[str, int]:
+    """Algorithmic HBM bytes per launch (each input read once, each output written once)."""
+    T, Hd, I = cfg.tokens, cfg.hidden, cfg.inter
+    heads = cfg.q_heads + cfg.kv_heads
+    emb = (T * Hd * 144 // 256 if cfg.emb == "q4_k" else T * Hd * 34 // 32) + 8 * T + T * Hd * e
+    rope = 2 * T * heads * cfg.head_dim * e + 8 * T + (2 * cfg.head_dim * e if cfg.qk_norm else 0)
+    return {"emb": emb, "rms": 4 * T * Hd * e + Hd * e, "rope": rope, "silu": 3 * T * I * e}
+
+
+def main() -> int:
+    args = parse()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print(json.dumps({"error": "this build measures one GPU only; run with --gpus 1",
+                          "n_gpus_requested": args.gpus}))
+        return 2
+
+    import torch
+
+    from nano_vllm_cpp_amd import ops
+    from tests import harness as H
+
+    cfg = H.CONFIGS[args.config]
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    dt = cfg.dtype
+    tdt = H.torch_dtype(dt)
+    e = 2 if dt != H.F32 else 4
+    T, Hd, I, V = cfg.tokens, cfg.hidden, cfg.inter, cfg.vocab
+    qs, ks = cfg.q_heads * cfg.head_dim, cfg.kv_heads * cfg.head_dim
+    g = torch.Generator(device=dev).manual_seed(cfg.seed)
+    nbytes = op_bytes(cfg, e)
+    only = set(filter(None, args.only.split(","))) or {"emb", "rms", "rope", "silu"}
+
+    def nsets(b: int) -> int:
+        return max(2, -(-POOL_BYTES // b))
+
+    def randn(shape, mean=0.0, std=1.0):
+        return (torch.randn(shape, generator=g, device=dev) * std + mean).to(tdt)
+
+    # ---- inputs (resident in HBM before timing) ------------------------------
+    if cfg.emb == "q8_0":
+        w8 = torch.randint(-127, 128, (V * Hd,), generator=g, device=dev, dtype=torch.int8)
+        ws = torch.empty(V * Hd // 32, device=dev).uniform_(1e-3, 1e-2, generator=g).half().view(torch.int16)
+    else:
+        blocks = torch.from_numpy(H.gen_q4_k(np.random.default_rng(cfg.seed), V * Hd // 256)).to(dev)
+    n_emb = nsets(nbytes["emb"])
+    emb_sets = [(torch.randint(0, V, (T,), generator=g, device=dev), torch.empty(T, Hd, dtype=tdt, device=dev))
+                for _ in range(n_emb)] if "emb" in only else []
+    rms_sets = [(randn((T, Hd)), randn((T, Hd)), torch.empty(T, Hd, dtype=tdt, device=dev))
+                for _ in range(nsets(nbytes["rms"]))] if "rms" in only else []
+    gamma = randn((Hd,), 1.0, 0.1)
+    rope_sets = [(randn((T, qs)), randn((T, ks))) for _ in range(nsets(nbytes["rope"]))] if "rope" in only else []
+    pos = torch.from_numpy(cfg.positions()).to(dev)
+    inv = ops.rope_inv_freq(cfg.theta, cfg.head_dim, dev)
+    qw = randn((cfg.head_dim,), 1.0, 0.1) if cfg.qk_norm else None
+    kw = randn((cfg.head_dim,), 1.0, 0.1) if cfg.qk_norm else None
+    silu_sets = [(randn((T, 2 * I)), torch.empty(T, I, dtype=tdt, device=dev))
+                 for _ in range(nsets(nbytes["silu"]))] if "silu" in only else []
+    copy_pair = None
+    if "copy" in only:  # plain-copy reference kernel for the traffic-counter calibration
+        copy_pair = (torch.empty(1 << 28, dtype=torch.int32, device=dev), torch.empty(1 << 28, dtype=torch.int32, device=dev))
+    torch.cuda.synchronize()
+
+    def run_emb(i):
+        ids, out = emb_sets[i % len(emb_sets)]
+        if cfg.emb == "q8_0":
+            ops.embedding_q8_0(ids, w8, ws, Hd, V, out=out)
+        else:
+            ops.embedding_qk(ids, blocks, Hd, ops.Q4_K, V, out=out)
+
+    def run_rms(i):
+        x, r, out = rms_sets[i % len(rms_sets)]
+        ops.rms_norm_add(x, r, gamma, cfg.eps, out=out)
+
+    def run_rope(i):
+        q, k = rope_sets[i % len(rope_sets)]
+        ops.qk_norm_rope(q, k, pos, qw, kw, inv, cfg.q_heads, cfg.kv_heads, cfg.head_dim, cfg.eps)
+
+    def run_silu(i):
+        gu, out = silu_sets[i % len(silu_sets)]
+        ops.silu_and_mul(gu, out=out)
+
+    def run_copy(i):
+        copy_pair[1].copy_(copy_pair[0])
+
+    table = [("emb", run_emb), ("rms", run_rms), ("rope", run_rope), ("silu", run_silu), ("copy", run_copy)]
+    active = [(n, f) for n, f in table if n in only]
+
+    for i in range(args.warmup):
+        for _, f in active:
+            f(i)
+    torch.cuda.synchronize()
+
+    stream = torch.cuda.current_stream()
+    ev = {n: [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+              for _ in range(args.steps)] for n, _ in active}
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        for n, f in active:
+            a, b = ev[n][i]
+            a.record(stream)
+            f(args.warmup + i)
+            b.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+
+    res_ops = {}
+    for n, _ in active:
+        times = np.array([a.elapsed_time(b) for a, b in ev[n]]) * 1e3  # us
+        t_us = float(np.mean(times))
+        entry = {"us_mean": round(t_us, 2), "us_median": round(float(np.median(times)), 2),
+                 "us_p10": round(float(np.percentile(times, 10)), 2),
+                 "us_p90": round(float(np.percentile(times, 90)), 2)}
+        if n in nbytes:
+            gbs = nbytes[n] / (t_us * 1e-6) / 1e9
+            entry.update({"bytes": nbytes[n], "GB_s": round(gbs, 1), "frac_of_peak": round(gbs / HBM_PEAK_GBS, 4),
+                          "tokens_per_s": round(T / (t_us * 1e-6), 1)})
+        elif n == "copy":
+            entry.update({"bytes": 2 * copy_pair[0].numel() * 4,
+                          "GB_s": round(2 * copy_pair[0].numel() * 4 / (t_us * 1e-6) / 1e9, 1)})
+        res_ops[n] = entry
+
+    chain_ops = [n for n in ("emb", "rms", "rope", "silu") if n in res_ops]
+    chain_us = sum(res_ops[n]["us_mean"] for n in chain_ops)
+    ms_per_step = wall / args.steps * 1e3
+    dom = max(chain_ops, key=lambda n: nbytes[n]) if chain_ops else None
+    roofline = None
+    if dom:
+        roofline = {"kernel": {"emb": "embedding", "rms": "rms_norm_add", "rope": "qk_norm_rope",
+                               "silu": "silu_and_mul"}[dom],
+                    "bound": "hbm", "achieved": res_ops[dom]["GB_s"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                    "frac": res_ops[dom]["frac_of_peak"], "traffic": traffic_from_profiles(dom, args.config)}
+
+    cpu = cpu_baseline(cfg, args.cpu_seconds, H) if args.cpu_seconds > 0 and chain_ops == ["emb", "rms", "rope", "silu"] else None
+
+    line = {
+        "metric": METRIC,
+        "value": round(T / (chain_us * 1e-6), 1) if chain_ops else None,
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": {H.F16: "f16", H.BF16: "bf16", H.F32: "f32"}[dt],
+        "data": "synthetic (seeded; BASELINE value distributions)",
+        "config": {"workload": f"BASELINE config {args.config}: {cfg.name}; one step = "
+                               f"{cfg.emb} embedding gather + residual-add RMSNorm + "
+                               f"{'QK-norm + ' if cfg.qk_norm else ''}NeoX RoPE q/k + SwiGLU",
+                   "tokens": T, "hidden": Hd, "intermediate": I, "vocab": V, "q_heads": cfg.q_heads,
+                   "kv_heads": cfg.kv_heads, "head_dim": cfg.head_dim, "value_is": "tokens / sum of per-op HIP-event times"},
+        "ops": res_ops,
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+def traffic_from_profiles(op: str, config: int):
+    """HBM bytes per launch from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary, if present."""
+    f = ROOT / "profiles" / "traffic.json"
+    if not f.exists():
+        return None
+    try:
+        d = json.loads(f.read_text())
+        return d.get(f"c{config}", {}).get(op, {}).get("hbm_bytes_per_launch")
+    except (ValueError, AttributeError):
+        return None
+
+
+def cpu_baseline(cfg, budget_s: float, H) -> dict:
+    """The C oracle (scalar, 1 thread, -O2) on a bounded sample of the same chain."""
+    o = H.oracle()
+    r = np.random.default_rng(cfg.seed)
+    S = 256  # sample tokens per chain call
+    T, Hd, I, dt = S, cfg.hidden, cfg.inter, cfg.dtype
+    Vs = 4096  # gathered rows come from a 4096-row slice of the table: same per-row work
+    ids = r.integers(0, Vs, S).astype(np.int64)
+    if cfg.emb == "q8_0":
+        w8, ws = H.gen_q8_0(r, Vs, Hd)
+    else:
+        blocks = H.gen_q4_k(r, Vs * Hd // 256)
+    emb = np.empty((S, Hd), H.NP_STORAGE[dt])
+    x, res = H.gen_act(r, (S, Hd), dt), H.gen_act(r, (S, Hd), dt)
+    w = H.gen_act(r, (Hd,), dt, 1.0, 0.1)
+    out = np.empty_like(x)
+    qs, ks = cfg.q_heads * cfg.head_dim, cfg.kv_heads * cfg.head_dim
+    q, k = H.gen_act(r, (S, qs), dt), H.gen_act(r, (S, ks), dt)
+    pos = np.ascontiguousarray(cfg.positions()[:S])
+    inv = np.empty(cfg.head_dim // 2, np.float32)
+    o.orc_inv_freq(cfg.theta, cfg.head_dim, H.ptr(inv))
+    qw = H.gen_act(r, (cfg.head_dim,), dt, 1.0, 0.1) if cfg.qk_norm else None
+    kw = H.gen_act(r, (cfg.head_dim,), dt, 1.0, 0.1) if cfg.qk_norm else None
+    gu = H.gen_act(r, (S, 2 * I), dt)
+    so = np.empty((S, I), H.NP_STORAGE[dt])
+    per = {"emb": 0.0, "rms": 0.0, "rope": 0.0, "silu": 0.0}
+    calls = 0
+    t_start = time.perf_counter()
+    while True:
+        t = time.perf_counter()
+        if cfg.emb == "q8_0":
+            o.orc_embedding_q8_split(H.ptr(ids), H.ptr(w8), H.ptr(ws), S, Hd, H.ptr(emb), dt)
+        else:
+            o.orc_embedding_qk(H.ptr(ids), H.ptr(blocks), S, Hd, 12, H.GGML, H.ptr(emb), dt)
+        t1 = time.perf_counter()
+        o.orc_rms_norm_add(H.ptr(x), H.ptr(res), H.ptr(w), H.ptr(out), S, Hd, cfg.eps, dt)
+        t2 = time.perf_counter()
+        o.orc_qk_norm_rope(H.ptr(q), H.ptr(k), H.ptr(pos), H.ptr(qw), H.ptr(kw), H.ptr(inv), S, cfg.q_heads,
+                           cfg.kv_heads, cfg.head_dim, qs, ks, cfg.eps, dt)
+        t3 = time.perf_counter()
+        o.orc_silu_and_mul(H.ptr(gu), H.ptr(so), S, I, dt)
+        t4 = time.perf_counter()
+        per["emb"] += t1 - t
+        per["rms"] += t2 - t1
+        per["rope"] += t3 - t2
+        per["silu"] += t4 - t3
+        calls += 1
+        if t4 - t_start >= budget_s:
+            break
+    total = sum(per.values())
+    e = 2 if dt != H.F32 else 4
+    scale = {k_: v * S / cfg.tokens for k_, v in op_bytes(cfg, e).items()}  # bytes of one S-token call
+    cpu_model = ""
+    try:
+        for ln in Path("/proc/cpuinfo").read_text().splitlines():
+            if ln.startswith("model name"):
+                cpu_model = ln.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"value": round(calls * S / total, 1), "unit": "tokens/s", "cores": 1, "kind": "port",
+            "sample": f"{calls} x the {S}-token chain of the same config (table rows from a {Vs}-row slice), "
+                      f"{total:.1f} s of single-thread C oracle (-O2) on {cpu_model or 'this host'}, "
+                      f"nproc={os.cpu_count()}",
+            "ops_GB_s": {k_: round(scale[k_] * calls / per[k_] / 1e9, 3) for k_ in per}}
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -30,12 +30,18 @@ struct Pack<float> {
   static constexpr int N = 4;
   static __device__ __forceinline__ void unpack(const u32x4 v, float* f) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) f[i] = __builtin_bit_cast(float, v[i]);
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t w = v[i];  // bit_cast of a vector-element lvalue reads element 0: copy first
+      f[i] = __builtin_bit_cast(float, w);
+    }
   }
   static __device__ __forceinline__ u32x4 pack(const float* f) {
     u32x4 v;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) v[i] = __builtin_bit_cast(uint32_t, f[i]);
+    for (int i = 0; i < 4; ++i) {
+      const float x = f[i];
+      v[i] = __builtin_bit_cast(uint32_t, x);
+    }
     return v;
   }
 };
@@ -46,7 +52,8 @@ struct Pack<_Float16> {
   static __device__ __forceinline__ void unpack(const u32x4 v, float* f) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      f16x2 h = __builtin_bit_cast(f16x2, v[i]);
+      const uint32_t w = v[i];
+      const f16x2 h = __builtin_bit_cast(f16x2, w);
       f[2 * i] = (float)h[0];
       f[2 * i + 1] = (float)h[1];
     }

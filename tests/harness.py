@@ -148,8 +148,9 @@ def assert_close(got: np.ndarray, ref: np.ndarray, dt: int, *, rel: float = 1e-5
     g = from_storage(np.asarray(got), dt)
     r = from_storage(np.asarray(ref), dt)
     both_nan = np.isnan(g) & np.isnan(r)
-    tol = np.maximum(np.maximum(rel * np.abs(r), ulp(r, dt)), floor)
-    bad = ~both_nan & ~(np.abs(g - r) <= tol)
+    with np.errstate(invalid="ignore", over="ignore"):
+        tol = np.maximum(np.maximum(rel * np.abs(r), ulp(r, dt)), floor)
+        bad = ~both_nan & (g != r) & ~(np.abs(g - r) <= tol)
     if bad.any():
         idx = np.argwhere(bad)[:5]
         rows = ", ".join(f"{tuple(i)}: got {g[tuple(i)]!r} ref {r[tuple(i)]!r}" for i in idx)

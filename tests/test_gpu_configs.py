@@ -82,8 +82,8 @@ def test_config_full_size(gpu, ci):
     assert torch.isfinite(out).all()
     sr = np.ascontiguousarray(res_h[rows])
     ref = np.empty_like(sr)
-    o.orc_rms_norm_add(H.ptr(np.ascontiguousarray(x_h[rows])), H.ptr(sr), H.ptr(w_h), H.ptr(ref), rows.size, Hd,
-                       cfg.eps, dt)
+    sx = np.ascontiguousarray(x_h[rows])  # keep every array the oracle reads alive across the call
+    o.orc_rms_norm_add(H.ptr(sx), H.ptr(sr), H.ptr(w_h), H.ptr(ref), rows.size, Hd, cfg.eps, dt)
     H.assert_close(H.to_host(out)[rows], ref, dt, what=f"c{ci} rms_norm_add")
     del x, res, out, expect_res
 
@@ -100,8 +100,10 @@ def test_config_full_size(gpu, ci):
                      cfg.head_dim, cfg.eps)
     rq, rk = np.ascontiguousarray(q_h[rows]), np.ascontiguousarray(k_h[rows])
     rpos = np.ascontiguousarray(pos[rows])
-    o.orc_qk_norm_rope(H.ptr(rq), H.ptr(rk), H.ptr(rpos), H.ptr(H.to_host(qw)) if qw is not None else None,
-                       H.ptr(H.to_host(kw)) if kw is not None else None, H.ptr(inv.numpy()), rows.size,
+    qw_h = H.to_host(qw) if qw is not None else None
+    kw_h = H.to_host(kw) if kw is not None else None
+    inv_h = inv.numpy()
+    o.orc_qk_norm_rope(H.ptr(rq), H.ptr(rk), H.ptr(rpos), H.ptr(qw_h), H.ptr(kw_h), H.ptr(inv_h), rows.size,
                        cfg.q_heads, cfg.kv_heads, cfg.head_dim, qs, ks, cfg.eps, dt)
     H.assert_close(H.to_host(q)[rows], rq, dt, floor=1e-6, what=f"c{ci} rope q")
     H.assert_close(H.to_host(k)[rows], rk, dt, floor=1e-6, what=f"c{ci} rope k")

@@ -59,7 +59,8 @@ def test_dropin_rms_norm_add_and_rms_norm(gpu):
     H.oracle().orc_rms_norm_add(H.ptr(x), H.ptr(ref_res), H.ptr(w), H.ptr(ref_out), rows, hidden, 1e-6, H.F32)
     dres, out = f32(gpu, res), torch.empty(rows, hidden, device=gpu)
     case("hip_rms_norm_add")
-    ops.lib().hip_rms_norm_add(dptr(f32(gpu, x)), dptr(dres), dptr(f32(gpu, w)), dptr(out), rows, hidden, 1e-6)
+    dx, dw = f32(gpu, x), f32(gpu, w)  # named: a temporary's memory could be reused before the launch
+    ops.lib().hip_rms_norm_add(dptr(dx), dptr(dres), dptr(dw), dptr(out), rows, hidden, 1e-6)
     torch.cuda.synchronize()
     H.assert_bitexact(dres.cpu().numpy(), ref_res, "residual")
     H.assert_close(out.cpu().numpy(), ref_out, H.F32, what="hip_rms_norm_add")
@@ -70,7 +71,8 @@ def test_dropin_rms_norm_add_and_rms_norm(gpu):
     H.oracle().orc_rms_norm(H.ptr(q), H.ptr(qw), H.ptr(refq), q.shape[0], 128, 1e-6, H.F32)
     dq = f32(gpu, q)
     case("hip_rms_norm in place, head_dim rows")
-    ops.lib().hip_rms_norm(dptr(dq), dptr(f32(gpu, qw)), dptr(dq), q.shape[0], 128, 1e-6)
+    dqw = f32(gpu, qw)
+    ops.lib().hip_rms_norm(dptr(dq), dptr(dqw), dptr(dq), q.shape[0], 128, 1e-6)
     torch.cuda.synchronize()
     H.assert_close(dq.cpu().numpy(), refq, H.F32, what="hip_rms_norm")
 

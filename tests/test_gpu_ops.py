@@ -217,10 +217,13 @@ def _rope_case(gpu, dt, T, hq, hk, hd, norm, packed, seed, positions=None):
         d = H.to_dev(qkv, gpu, dt)
         flat = d.view(-1)
         case(f"qk_norm_rope packed T={T} hq={hq} hk={hk} hd={hd} norm={norm} dt={dt}")
-        rc = ops.lib().nvf_qk_norm_rope(flat.data_ptr(), flat[qs:].data_ptr(), H.to_dev(pos, gpu).data_ptr(),
-                                        H.to_dev(qw, gpu, dt).data_ptr() if norm else None,
-                                        H.to_dev(kw, gpu, dt).data_ptr() if norm else None,
-                                        H.to_dev(inv, gpu).data_ptr(), T, hq, hk, hd, stride, stride, 1e-6, dt,
+        # hold every device tensor in a name: a temporary's memory can be reused before the kernel runs
+        d_pos, d_inv = H.to_dev(pos, gpu), H.to_dev(inv, gpu)
+        d_qw = H.to_dev(qw, gpu, dt) if norm else None
+        d_kw = H.to_dev(kw, gpu, dt) if norm else None
+        rc = ops.lib().nvf_qk_norm_rope(flat.data_ptr(), flat[qs:].data_ptr(), d_pos.data_ptr(),
+                                        d_qw.data_ptr() if norm else None, d_kw.data_ptr() if norm else None,
+                                        d_inv.data_ptr(), T, hq, hk, hd, stride, stride, 1e-6, dt,
                                         torch.cuda.current_stream().cuda_stream)
         assert rc == 0, ops.lib().nvf_last_error()
         got = H.to_host(d)
