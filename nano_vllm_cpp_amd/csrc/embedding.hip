@@ -9,14 +9,17 @@
 //                      order GGML (src/gguf.cpp:477-496) or HIP_LEGACY (:130-140)
 //   F16/BF16/F32       src/hip_ops.hip:553-563
 //
-// Design: flat grids of independent threads, each owning a 16- or 32-element
-// run of one output row, so table bytes are read with 16-byte (or aligned
-// dword) loads and every output element is written once with 16-byte stores.
-// The fp16 scale is decoded by v_cvt_f32_f16 (exact, subnormals included).
-// Q4_K: eight lanes share a 144 B superblock; each lane loads the 16 B header
-// (d, dmin, 12 B of 6-bit scales/mins -- one cache line serves the eight lanes)
-// plus its own 16 B of nibbles, unpacks its two (scale, min) pairs in VGPRs and
-// writes 32 outputs.
+// Design: one wave64 per token row (the id is read once per wave); lane l owns
+// the 16-byte output chunks l, l + 64, ..., so every store instruction writes
+// 1 KiB of contiguous output -- the output is the larger side of every gather
+// (2 bytes out per 1.06 (Q8_0) or 0.56 (Q4_K) bytes in).  Each lane issues the
+// loads of up to 8 chunks before decoding any, and the output streams out with
+// non-temporal stores.  The fp16 scales are decoded by v_cvt_f32_f16 (exact,
+// subnormals included).  Q4_K: the 8 outputs of a chunk share one 6-bit
+// (scale, min) pair and 8 consecutive nibble bytes; each lane reads the 16 B
+// superblock header (the 32 lanes of a superblock hit the same cache line)
+// and unpacks its pair in VGPRs.  Q5_K / Q6_K use a per-element kernel
+// (correct, not tuned).
 #include "nvf_device.hpp"
 #include "nvf_host.hpp"
 
@@ -28,110 +31,86 @@ __device__ __forceinline__ float half_bits_to_f32(uint32_t h16) {
   return (float)__builtin_bit_cast(_Float16, (uint16_t)h16);
 }
 
-__device__ __forceinline__ bool bad_id(int64_t id, int64_t vocab) { return vocab > 0 && (id < 0 || id >= vocab); }
-
-// Stores `n` (multiple of 8, or 4 for fp32) floats as TO with 16-byte stores.
-template <typename TO, int NV>
-__device__ __forceinline__ void store_run(TO* dst, const float* v) {
-  constexpr int N = Pack<TO>::N;
-  static_assert(NV % N == 0, "run length");
-#pragma unroll
-  for (int i = 0; i < NV / N; ++i) st16(dst + i * N, Pack<TO>::pack(v + i * N));
-}
-
-template <typename TO, int NV>
-__device__ __forceinline__ void store_nan_run(TO* dst) {
-  float v[NV];
-#pragma unroll
-  for (int i = 0; i < NV; ++i) v[i] = __builtin_nanf("");
-  store_run<TO, NV>(dst, v);
-}
-
 __device__ __forceinline__ float sbyte(uint32_t w, int k) { return (float)(int8_t)((w >> (8 * k)) & 0xffu); }
 
-// ---------------------------------------------------------------------------
-// Q8_0, split planes: one thread per 16 outputs (one 16 B load of w8).
-// ---------------------------------------------------------------------------
-template <typename TO>
-__global__ __launch_bounds__(kEmbThreads) void embed_q8_split_kernel(const int64_t* __restrict__ ids,
-                                                                     const uint8_t* __restrict__ w8,
-                                                                     const uint16_t* __restrict__ ws,
-                                                                     TO* __restrict__ out, uint32_t total,
-                                                                     FastDiv chunks_per_row, int64_t hidden,
-                                                                     int64_t vocab) {
-  const uint32_t g = blockIdx.x * kEmbThreads + threadIdx.x;
-  if (g >= total) return;
-  const uint32_t t = chunks_per_row.div(g);
-  const int64_t c0 = (int64_t)(g - t * chunks_per_row.d) * 16;
-  const int64_t id = ids[t];
-  TO* dst = out + (int64_t)t * hidden + c0;
-  if (bad_id(id, vocab)) {
-    store_nan_run<TO, 16>(dst);
-    return;
-  }
-  const int64_t e0 = id * hidden + c0;
-  const u32x4 q = ld16(w8 + e0);
-  const float s = half_bits_to_f32(ws[e0 >> 5]);
-  float v[16];
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int k = 0; k < 4; ++k) v[4 * i + k] = s * sbyte(q[i], k);
-  store_run<TO, 16>(dst, v);
-}
+__device__ __forceinline__ bool bad_id(int64_t id, int64_t vocab) { return vocab > 0 && (id < 0 || id >= vocab); }
 
 // ---------------------------------------------------------------------------
-// Q8_0, interleaved 34 B blocks: one thread per block (32 outputs).  Block
-// starts are 2 B aligned; the thread reads the aligned dwords covering its 34
-// bytes (never a byte outside the block's dwords) and realigns with
-// v_alignbyte.
+// Row-gather kernel.  One wave per token row; lane l owns the 16-byte output
+// chunks l, l + 64, ... (N = 8 outputs for fp16/bf16, 4 for fp32), so each
+// store instruction writes 1 KiB of contiguous row.  Up to U chunks per lane
+// have their loads in flight before any decode.  The table row is located
+// once per wave (the id is wave-uniform).  A Source supplies
+//   Raw  load(row_elem0, c0)   -- issue the loads for outputs c0 .. c0+N-1
+//   void decode(Raw, float*)   -- produce the N fp32 values (exact)
 // ---------------------------------------------------------------------------
-template <typename TO>
-__global__ __launch_bounds__(kEmbThreads) void embed_q8_blocks_kernel(const int64_t* __restrict__ ids,
-                                                                      const uint8_t* __restrict__ blocks,
-                                                                      TO* __restrict__ out, uint32_t total,
-                                                                      FastDiv blocks_per_row, int64_t hidden,
-                                                                      int64_t vocab) {
-  const uint32_t g = blockIdx.x * kEmbThreads + threadIdx.x;
-  if (g >= total) return;
-  const uint32_t t = blocks_per_row.div(g);
-  const uint32_t b = g - t * blocks_per_row.d;
-  const int64_t id = ids[t];
-  TO* dst = out + (int64_t)t * hidden + (int64_t)b * 32;
-  if (bad_id(id, vocab)) {
-    store_nan_run<TO, 32>(dst);
-    return;
+template <int N>
+struct Q8Split {  // int8 plane + fp16 scale plane (src/model.cpp:394-404)
+  const uint8_t* w8;
+  const uint16_t* ws;
+  struct Raw {
+    uint32_t q[N / 4];
+    uint32_t s;
+  };
+  __device__ __forceinline__ Raw load(int64_t e0) const {
+    Raw r;
+    if constexpr (N == 8) {
+      const uint2 v = *reinterpret_cast<const uint2*>(w8 + e0);
+      r.q[0] = v.x;
+      r.q[1] = v.y;
+    } else {
+      r.q[0] = *reinterpret_cast<const uint32_t*>(w8 + e0);
+    }
+    r.s = ws[e0 >> 5];
+    return r;
   }
-  const uint8_t* blk = blocks + (id * blocks_per_row.d + b) * 34;
-  const bool odd = (reinterpret_cast<uintptr_t>(blk) & 2u) != 0;  // block starts 2 B into a dword
-  const uint32_t* w = reinterpret_cast<const uint32_t*>(reinterpret_cast<uintptr_t>(blk) & ~uintptr_t(3));
-  uint32_t wd[9];
+  __device__ __forceinline__ void decode(const Raw& r, float* v) const {
+    const float s = half_bits_to_f32(r.s);
 #pragma unroll
-  for (int i = 0; i < 8; ++i) wd[i] = w[i];
-  // dword 8: the whole dword when the block starts mid-dword (bytes 30..33),
-  // else only the block's last two bytes (32, 33).
-  if (odd)
-    wd[8] = w[8];
-  else
-    wd[8] = reinterpret_cast<const uint16_t*>(w + 8)[0];
-  const float s = half_bits_to_f32(odd ? (wd[0] >> 16) : (wd[0] & 0xffffu));
-  float v[32];
+    for (int i = 0; i < N / 4; ++i)
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const uint32_t qd = odd ? wd[i + 1] : __builtin_amdgcn_alignbyte(wd[i + 1], wd[i], 2);
-#pragma unroll
-    for (int k = 0; k < 4; ++k) v[4 * i + k] = s * sbyte(qd, k);
+      for (int k = 0; k < 4; ++k) v[4 * i + k] = s * sbyte(r.q[i], k);
   }
-  store_run<TO, 32>(dst, v);
-}
+};
 
-// ---------------------------------------------------------------------------
-// Q4_K: one thread per 16 B of nibbles (32 outputs); needs hidden % 256 == 0.
-// ---------------------------------------------------------------------------
+template <int N>
+struct Q8Blocks {  // interleaved 34-byte blocks [fp16 d][32 x int8]
+  const uint8_t* blocks;
+  struct Raw {
+    uint32_t q[N / 4];
+    uint32_t s;
+  };
+  // The N quant bytes start 2 bytes into a dword when the block index is even.
+  // Only dwords that hold chunk bytes are read; the last two bytes come from a
+  // 16-bit load, so nothing past the block (or the table) is touched.
+  __device__ __forceinline__ Raw load(int64_t e0) const {
+    const uint8_t* blk = blocks + (e0 >> 5) * 34;
+    const uint8_t* p = blk + 2 + (e0 & 31);
+    const bool mid = (reinterpret_cast<uintptr_t>(p) & 2u) != 0;
+    const uint32_t* w = reinterpret_cast<const uint32_t*>(reinterpret_cast<uintptr_t>(p) & ~uintptr_t(3));
+    Raw r;
+    uint32_t d[N / 4 + 1];
+#pragma unroll
+    for (int i = 0; i < N / 4; ++i) d[i] = w[i];
+    d[N / 4] = mid ? (uint32_t)reinterpret_cast<const uint16_t*>(w + N / 4)[0] : 0u;
+#pragma unroll
+    for (int i = 0; i < N / 4; ++i) r.q[i] = mid ? __builtin_amdgcn_alignbyte(d[i + 1], d[i], 2) : d[i];
+    r.s = *reinterpret_cast<const uint16_t*>(blk);
+    return r;
+  }
+  __device__ __forceinline__ void decode(const Raw& r, float* v) const {
+    const float s = half_bits_to_f32(r.s);
+#pragma unroll
+    for (int i = 0; i < N / 4; ++i)
+#pragma unroll
+      for (int k = 0; k < 4; ++k) v[4 * i + k] = s * sbyte(r.q[i], k);
+  }
+};
+
 __device__ __forceinline__ uint32_t byte_of(uint32_t w, int k) { return (w >> (8 * k)) & 0xffu; }
 
 // (scale, min) of group j from the header dwords h1 = bytes 4..7, h2 = 8..11,
-// h3 = 12..15 of the superblock (src/gguf.cpp:482-489).
+// h3 = 12..15 of a K-quant superblock (src/gguf.cpp:482-489).
 __device__ __forceinline__ void q4k_sm(uint32_t h1, uint32_t h2, uint32_t h3, int j, uint32_t& sc, uint32_t& mn) {
   if (j < 4) {
     sc = byte_of(h1, j) & 63u;
@@ -143,57 +122,151 @@ __device__ __forceinline__ void q4k_sm(uint32_t h1, uint32_t h2, uint32_t h3, in
   }
 }
 
-template <typename TO, int LAYOUT>
-__global__ __launch_bounds__(kEmbThreads) void embed_q4k_kernel(const int64_t* __restrict__ ids,
-                                                                const uint8_t* __restrict__ wq, TO* __restrict__ out,
-                                                                uint32_t total, FastDiv chunks_per_row, int64_t hidden,
-                                                                int64_t vocab) {
-  const uint32_t g = blockIdx.x * kEmbThreads + threadIdx.x;
-  if (g >= total) return;
-  const uint32_t t = chunks_per_row.div(g);
-  const uint32_t rem = g - t * chunks_per_row.d;
-  const uint32_t sb = rem >> 3, ch = rem & 7u;
-  const int64_t id = ids[t];
-  TO* row = out + (int64_t)t * hidden + (int64_t)sb * 256;
-  int lo_off, j_lo, j_hi;
-  if (LAYOUT == NVF_QK_LAYOUT_GGML) {
-    // byte qs[32p + 16hh + k]: low nibble -> element 64p + 16hh + k (group 2p),
-    // high nibble -> element 64p + 32 + 16hh + k (group 2p + 1)
-    j_lo = 2 * (int)(ch >> 1);
-    j_hi = j_lo + 1;
-    lo_off = 64 * (int)(ch >> 1) + 16 * (int)(ch & 1u);
-  } else {
-    // byte qs[16j + k]: low nibble -> element 32j + k, high -> 32j + 16 + k
-    j_lo = j_hi = (int)ch;
-    lo_off = 32 * (int)ch;
+template <int N, int LAYOUT>
+struct Q4K {  // 144-byte superblocks; N consecutive outputs share one group j = i >> 5
+  const uint8_t* wq;
+  struct Raw {
+    u32x4 hdr;
+    uint32_t q[N / 4];
+    int i;  // element index inside the superblock
+  };
+  __device__ __forceinline__ Raw load(int64_t e0) const {
+    const uint8_t* blk = wq + (e0 >> 8) * 144;
+    Raw r;
+    r.i = (int)(e0 & 255);
+    // GGML: element 64p + 32h + k is byte 32p + k, nibble h; HIP_LEGACY:
+    // element 32j + 16h + k is byte 16j + k, nibble h.  N-aligned runs of
+    // elements map to N consecutive bytes with one nibble.
+    const int off = LAYOUT == NVF_QK_LAYOUT_GGML ? 32 * (r.i >> 6) + (r.i & 31) : 16 * (r.i >> 5) + (r.i & 15);
+    r.hdr = ld16(blk);  // d, dmin, 12 B of scales: shared by the row's lanes (cache hits)
+    if constexpr (N == 8) {
+      const uint2 v = *reinterpret_cast<const uint2*>(blk + 16 + off);
+      r.q[0] = v.x;
+      r.q[1] = v.y;
+    } else {
+      r.q[0] = *reinterpret_cast<const uint32_t*>(blk + 16 + off);
+    }
+    return r;
   }
-  const int hi_off = LAYOUT == NVF_QK_LAYOUT_GGML ? lo_off + 32 : lo_off + 16;
+  __device__ __forceinline__ void decode(const Raw& r, float* v) const {
+    const int j = r.i >> 5;
+    const int sh = LAYOUT == NVF_QK_LAYOUT_GGML ? ((r.i >> 5) & 1) * 4 : ((r.i >> 4) & 1) * 4;
+    uint32_t sc, mn;
+    q4k_sm(r.hdr[1], r.hdr[2], r.hdr[3], j, sc, mn);
+    const float s = half_bits_to_f32(r.hdr[0] & 0xffffu) * (float)sc;
+    const float m = half_bits_to_f32(r.hdr[0] >> 16) * (float)mn;
+#pragma unroll
+    for (int i = 0; i < N / 4; ++i)
+#pragma unroll
+      for (int k = 0; k < 4; ++k) v[4 * i + k] = s * (float)((byte_of(r.q[i], k) >> sh) & 0xfu) - m;
+  }
+};
+
+template <int N, typename TI>
+struct Table {  // plain fp32 / fp16 / bf16 rows
+  const TI* table;
+  static constexpr int kWords = N * (int)sizeof(TI) / 4;
+  struct Raw {
+    uint32_t w[kWords];
+  };
+  __device__ __forceinline__ Raw load(int64_t e0) const {
+    Raw r;
+    const TI* p = table + e0;
+    if constexpr (kWords == 8) {
+      const u32x4 a = ld16(p), b = ld16(p + 16 / sizeof(TI));
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        r.w[i] = a[i];
+        r.w[4 + i] = b[i];
+      }
+    } else if constexpr (kWords == 4) {
+      const u32x4 a = ld16(p);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) r.w[i] = a[i];
+    } else {
+      const uint2 a = *reinterpret_cast<const uint2*>(p);
+      r.w[0] = a.x;
+      r.w[1] = a.y;
+    }
+    return r;
+  }
+  __device__ __forceinline__ void decode(const Raw& r, float* v) const {
+    if constexpr (sizeof(TI) == 4) {
+#pragma unroll
+      for (int i = 0; i < N; ++i) v[i] = __builtin_bit_cast(float, r.w[i]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < N / 2; ++i) {
+        const uint32_t w = r.w[i];
+        if constexpr (sizeof(TI) == 2 && __is_same(TI, __bf16)) {
+          v[2 * i] = __builtin_bit_cast(float, w << 16);
+          v[2 * i + 1] = __builtin_bit_cast(float, w & 0xffff0000u);
+        } else {
+          v[2 * i] = half_bits_to_f32(w & 0xffffu);
+          v[2 * i + 1] = half_bits_to_f32(w >> 16);
+        }
+      }
+    }
+  }
+};
+
+constexpr int kEmbRowsPerBlock = kEmbThreads / kWave;
+
+template <typename TO, typename Src, int U>
+__global__ __launch_bounds__(kEmbThreads) void embed_rows_kernel(const int64_t* __restrict__ ids, Src src,
+                                                                 TO* __restrict__ out, int64_t tokens, int hidden,
+                                                                 int64_t vocab) {
+  constexpr int N = Pack<TO>::N;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t t = (int64_t)blockIdx.x * kEmbRowsPerBlock +
+                    __builtin_amdgcn_readfirstlane((int)(threadIdx.x / kWave));
+  if (t >= tokens) return;  // wave-uniform
+  const int64_t id = ids[t];
+  const int nch = hidden / N;
+  TO* dst = out + t * hidden;
   if (bad_id(id, vocab)) {
-    store_nan_run<TO, 16>(row + lo_off);
-    store_nan_run<TO, 16>(row + hi_off);
+    float nan[N];
+#pragma unroll
+    for (int i = 0; i < N; ++i) nan[i] = __builtin_nanf("");
+    for (int c = lane; c < nch; c += kWave) st16(dst + c * N, Pack<TO>::pack(nan));
     return;
   }
-  const uint8_t* blk = wq + (id * (hidden >> 8) + sb) * 144;
-  const u32x4 hdr = ld16(blk);
-  const u32x4 qs = ld16(blk + 16 + ch * 16);
-  const float d = half_bits_to_f32(hdr[0] & 0xffffu);
-  const float dmin = half_bits_to_f32(hdr[0] >> 16);
-  uint32_t sc, mn;
-  q4k_sm(hdr[1], hdr[2], hdr[3], j_lo, sc, mn);
-  const float s_lo = d * (float)sc, m_lo = dmin * (float)mn;
-  q4k_sm(hdr[1], hdr[2], hdr[3], j_hi, sc, mn);
-  const float s_hi = d * (float)sc, m_hi = dmin * (float)mn;
-  float lo[16], hi[16];
+  const int64_t row0 = id * hidden;
+  for (int base = 0; base < nch; base += U * kWave) {
+    typename Src::Raw raw[U];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const uint32_t by = byte_of(qs[i], k);
-      lo[4 * i + k] = s_lo * (float)(by & 0xfu) - m_lo;
-      hi[4 * i + k] = s_hi * (float)(by >> 4) - m_hi;
+    for (int u = 0; u < U; ++u) {
+      const int c = base + u * kWave + lane;
+      if (c < nch) raw[u] = src.load(row0 + c * N);
     }
-  store_run<TO, 16>(row + lo_off, lo);
-  store_run<TO, 16>(row + hi_off, hi);
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int c = base + u * kWave + lane;
+      if (c < nch) {
+        float v[N];
+        src.decode(raw[u], v);
+        st16_nt(dst + c * N, Pack<TO>::pack(v));
+      }
+    }
+  }
+}
+
+template <typename TO, typename Src>
+static int launch_rows(const int64_t* ids, const Src& src, TO* out, int64_t tokens, int64_t hidden, int64_t vocab,
+                       hipStream_t st, const char* what) {
+  constexpr int N = Pack<TO>::N;
+  const int64_t nch = hidden / N;
+  const dim3 grid((unsigned)((tokens + kEmbRowsPerBlock - 1) / kEmbRowsPerBlock));
+  const int h = (int)hidden;
+  if (nch <= kWave)
+    embed_rows_kernel<TO, Src, 1><<<grid, kEmbThreads, 0, st>>>(ids, src, out, tokens, h, vocab);
+  else if (nch <= 2 * kWave)
+    embed_rows_kernel<TO, Src, 2><<<grid, kEmbThreads, 0, st>>>(ids, src, out, tokens, h, vocab);
+  else if (nch <= 4 * kWave)
+    embed_rows_kernel<TO, Src, 4><<<grid, kEmbThreads, 0, st>>>(ids, src, out, tokens, h, vocab);
+  else
+    embed_rows_kernel<TO, Src, 8><<<grid, kEmbThreads, 0, st>>>(ids, src, out, tokens, h, vocab);
+  return launch_status(what);
 }
 
 // ---------------------------------------------------------------------------
@@ -304,28 +377,6 @@ __global__ __launch_bounds__(kEmbThreads) void embed_q8_generic_kernel(const int
 // ---------------------------------------------------------------------------
 // Plain table gather: one thread per 8 elements.
 // ---------------------------------------------------------------------------
-template <typename TI, typename TO>
-__global__ __launch_bounds__(kEmbThreads) void embed_table_kernel(const int64_t* __restrict__ ids,
-                                                                  const TI* __restrict__ table, TO* __restrict__ out,
-                                                                  uint32_t total, FastDiv chunks_per_row,
-                                                                  int64_t hidden, int64_t vocab) {
-  const uint32_t g = blockIdx.x * kEmbThreads + threadIdx.x;
-  if (g >= total) return;
-  const uint32_t t = chunks_per_row.div(g);
-  const int64_t c0 = (int64_t)(g - t * chunks_per_row.d) * 8;
-  const int64_t id = ids[t];
-  TO* dst = out + (int64_t)t * hidden + c0;
-  if (bad_id(id, vocab)) {
-    store_nan_run<TO, 8>(dst);
-    return;
-  }
-  const TI* src = table + id * hidden + c0;
-  float v[8];
-  constexpr int NI = Pack<TI>::N;
-#pragma unroll
-  for (int i = 0; i < 8 / NI; ++i) Pack<TI>::unpack(ld16(src + i * NI), v + i * NI);
-  store_run<TO, 8>(dst, v);
-}
 
 template <typename TI, typename TO>
 __global__ __launch_bounds__(kEmbThreads) void embed_table_generic_kernel(const int64_t* __restrict__ ids,
@@ -358,22 +409,14 @@ static int check_common(const char* name, const int64_t* ids, const void* table,
 template <typename TO>
 static int launch_q8(const int64_t* ids, const uint8_t* w8, const uint16_t* ws, const uint8_t* blocks, int64_t tokens,
                      int64_t hidden, int64_t vocab, void* out, hipStream_t st) {
+  constexpr int N = Pack<TO>::N;
   TO* o = static_cast<TO*>(out);
+  const bool row_ok = hidden % 32 == 0 && hidden <= INT32_MAX && aligned16(out);
   if (blocks) {
-    const int64_t total = tokens * (hidden / 32);
-    if (hidden % 32 == 0 && aligned16(out) && (reinterpret_cast<uintptr_t>(blocks) & 3u) == 0 && total < UINT32_MAX) {
-      embed_q8_blocks_kernel<TO><<<grid_for(total), kEmbThreads, 0, st>>>(ids, blocks, o, (uint32_t)total,
-                                                                          FastDiv((uint32_t)(hidden / 32)), hidden, vocab);
-      return launch_status("embedding_q8_0_blocks");
-    }
-  } else {
-    const int64_t total = tokens * (hidden / 16);
-    if (hidden % 32 == 0 && aligned16(out) && aligned16(w8) && (reinterpret_cast<uintptr_t>(ws) & 1u) == 0 &&
-        total < UINT32_MAX) {
-      embed_q8_split_kernel<TO><<<grid_for(total), kEmbThreads, 0, st>>>(ids, w8, ws, o, (uint32_t)total,
-                                                                         FastDiv((uint32_t)(hidden / 16)), hidden, vocab);
-      return launch_status("embedding_q8_0");
-    }
+    if (row_ok && (reinterpret_cast<uintptr_t>(blocks) & 3u) == 0)
+      return launch_rows(ids, Q8Blocks<N>{blocks}, o, tokens, hidden, vocab, st, "embedding_q8_0_blocks");
+  } else if (row_ok && (reinterpret_cast<uintptr_t>(w8) & 7u) == 0 && (reinterpret_cast<uintptr_t>(ws) & 1u) == 0) {
+    return launch_rows(ids, Q8Split<N>{w8, ws}, o, tokens, hidden, vocab, st, "embedding_q8_0");
   }
   const int64_t total = tokens * hidden;
   embed_q8_generic_kernel<TO><<<grid_for(total), kEmbThreads, 0, st>>>(ids, w8, ws, blocks, o, total, hidden, vocab);
@@ -383,17 +426,12 @@ static int launch_q8(const int64_t* ids, const uint8_t* w8, const uint16_t* ws, 
 template <typename TO>
 static int launch_qk(const int64_t* ids, const uint8_t* wq, int64_t tokens, int64_t hidden, int64_t vocab, int kind,
                      int layout, void* out, hipStream_t st) {
+  constexpr int N = Pack<TO>::N;
   TO* o = static_cast<TO*>(out);
-  const int64_t chunks = tokens * (hidden / 256) * 8;
-  if (kind == NVF_Q4_K && hidden % 256 == 0 && aligned16(wq) && aligned16(out) && chunks < UINT32_MAX) {
-    const FastDiv cpr((uint32_t)(hidden / 256 * 8));
+  if (kind == NVF_Q4_K && hidden % 256 == 0 && hidden <= INT32_MAX && aligned16(wq) && aligned16(out)) {
     if (layout == NVF_QK_LAYOUT_GGML)
-      embed_q4k_kernel<TO, NVF_QK_LAYOUT_GGML>
-          <<<grid_for(chunks), kEmbThreads, 0, st>>>(ids, wq, o, (uint32_t)chunks, cpr, hidden, vocab);
-    else
-      embed_q4k_kernel<TO, NVF_QK_LAYOUT_HIP_LEGACY>
-          <<<grid_for(chunks), kEmbThreads, 0, st>>>(ids, wq, o, (uint32_t)chunks, cpr, hidden, vocab);
-    return launch_status("embedding_q4_k");
+      return launch_rows(ids, Q4K<N, NVF_QK_LAYOUT_GGML>{wq}, o, tokens, hidden, vocab, st, "embedding_q4_k");
+    return launch_rows(ids, Q4K<N, NVF_QK_LAYOUT_HIP_LEGACY>{wq}, o, tokens, hidden, vocab, st, "embedding_q4_k");
   }
   const int bb = kind == NVF_Q4_K ? 144 : (kind == NVF_Q5_K ? 176 : 210);
   const int64_t total = tokens * hidden;
@@ -405,14 +443,11 @@ static int launch_qk(const int64_t* ids, const uint8_t* wq, int64_t tokens, int6
 template <typename TI, typename TO>
 static int launch_table(const int64_t* ids, const void* table, int64_t tokens, int64_t hidden, int64_t vocab, void* out,
                         hipStream_t st) {
+  constexpr int N = Pack<TO>::N;
   const TI* tb = static_cast<const TI*>(table);
   TO* o = static_cast<TO*>(out);
-  const int64_t total = tokens * (hidden / 8);
-  if (hidden % 8 == 0 && aligned16(table) && aligned16(out) && total < UINT32_MAX) {
-    embed_table_kernel<TI, TO><<<grid_for(total), kEmbThreads, 0, st>>>(ids, tb, o, (uint32_t)total,
-                                                                        FastDiv((uint32_t)(hidden / 8)), hidden, vocab);
-    return launch_status("embedding");
-  }
+  if (hidden % 8 == 0 && hidden <= INT32_MAX && aligned16(table) && aligned16(out))
+    return launch_rows(ids, Table<N, TI>{tb}, o, tokens, hidden, vocab, st, "embedding");
   embed_table_generic_kernel<TI, TO>
       <<<grid_for(tokens * hidden), kEmbThreads, 0, st>>>(ids, tb, o, tokens * hidden, hidden, vocab);
   return launch_status("embedding(generic)");

@@ -10,7 +10,8 @@
 // Design: one 256-thread workgroup per token.  The head_dim/2 (cos, sin) pairs
 // of the token are computed once (precise cosf/sinf, the reference's own
 // functions) into LDS and reused by every q and k head -- the reference
-// recomputes them per head.  A head is LPH = (head_dim/2)/N lanes; lane l
+// recomputes them per head.  The data loads of the first pass are issued before
+// that table is built, and q/k are streamed with non-temporal loads/stores.  A head is LPH = (head_dim/2)/N lanes; lane l
 // holds the 16-byte vectors at d0 = l*N and d0 + head_dim/2, so every rotation
 // pair is lane-local.  QK-norm reduces the head's sum of squares over those LPH
 // lanes with DPP (group_sum) and keeps the normalised values in registers, so q
@@ -38,14 +39,27 @@ __global__ __launch_bounds__(kRopeThreads) void qk_norm_rope_kernel(T* q, T* k, 
   __shared__ float cs_lds[HALF];
   __shared__ float sn_lds[HALF];
   const int64_t t = blockIdx.x;
-  if (threadIdx.x < HALF) {
-    const float a = (float)positions[t] * inv_freq[threadIdx.x];
-    cs_lds[threadIdx.x] = cosf(a);
-    sn_lds[threadIdx.x] = sinf(a);
-  }
-
   const int sub = threadIdx.x % LPH;
   const int d0 = sub * N;
+  const int total_heads = q_heads + kv_heads;
+  auto head_base = [&](int h) -> T* {
+    return h < q_heads ? q + t * q_stride + (int64_t)h * HD : k + t * k_stride + (int64_t)(h - q_heads) * HD;
+  };
+
+  // The first pass's loads go out before the (cos, sin) table is built, so
+  // the HBM latency overlaps the sincos work and the barrier.
+  int h = threadIdx.x / LPH;
+  u32x4 a, b;
+  if (h < total_heads) {
+    T* base = head_base(h);
+    a = ld16_nt(base + d0);
+    b = ld16_nt(base + HALF + d0);
+  }
+  if (threadIdx.x < HALF) {
+    const float ang = (float)positions[t] * inv_freq[threadIdx.x];
+    cs_lds[threadIdx.x] = cosf(ang);
+    sn_lds[threadIdx.x] = sinf(ang);
+  }
   float qg1[N], qg2[N], kg1[N], kg2[N];
   if constexpr (NORM) {
     Pack<T>::unpack(ld16(qw + d0), qg1);
@@ -61,13 +75,16 @@ __global__ __launch_bounds__(kRopeThreads) void qk_norm_rope_kernel(T* q, T* k, 
     s[j] = sn_lds[d0 + j];
   }
 
-  const int total_heads = q_heads + kv_heads;
-  for (int h = threadIdx.x / LPH; h < total_heads; h += HPP) {
+  for (; h < total_heads; h += HPP) {
+    T* base = head_base(h);
     const bool is_q = h < q_heads;
-    T* base = is_q ? q + t * q_stride + (int64_t)h * HD : k + t * k_stride + (int64_t)(h - q_heads) * HD;
+    if (h >= HPP) {  // later passes (more heads than one pass covers)
+      a = ld16_nt(base + d0);
+      b = ld16_nt(base + HALF + d0);
+    }
     float x1[N], x2[N];
-    Pack<T>::unpack(ld16(base + d0), x1);
-    Pack<T>::unpack(ld16(base + HALF + d0), x2);
+    Pack<T>::unpack(a, x1);
+    Pack<T>::unpack(b, x2);
     if constexpr (NORM) {
       float ss = 0.f;
 #pragma unroll
@@ -86,8 +103,8 @@ __global__ __launch_bounds__(kRopeThreads) void qk_norm_rope_kernel(T* q, T* k, 
       y1[j] = x1[j] * c[j] - x2[j] * s[j];
       y2[j] = x2[j] * c[j] + x1[j] * s[j];
     }
-    st16(base + d0, Pack<T>::pack(y1));
-    st16(base + HALF + d0, Pack<T>::pack(y2));
+    st16_nt(base + d0, Pack<T>::pack(y1));
+    st16_nt(base + HALF + d0, Pack<T>::pack(y2));
   }
 }
 
