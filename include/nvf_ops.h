@@ -132,6 +132,12 @@ int nvf_embedding(const int64_t* ids, const void* table, int64_t tokens, int64_t
  * out is HOST memory of head_dim/2 floats. */
 int nvf_rope_inv_freq(double theta, int head_dim, float* out);
 
+/* Copies `bytes` (a multiple of 16; 16-byte aligned pointers) with the same
+ * 16-byte non-temporal loads/stores the op kernels use.  No counterpart in the
+ * reference: it is the attainable-bandwidth and traffic-counter reference that
+ * the op kernels' HBM figures are calibrated against. */
+int nvf_stream_copy(void* dst, const void* src, int64_t bytes, void* stream);
+
 /* Text of the calling thread's last failure ("" if none). */
 const char* nvf_last_error(void);
 

@@ -9,17 +9,17 @@
 //                      order GGML (src/gguf.cpp:477-496) or HIP_LEGACY (:130-140)
 //   F16/BF16/F32       src/hip_ops.hip:553-563
 //
-// Design: one wave64 per token row (the id is read once per wave); lane l owns
-// the 16-byte output chunks l, l + 64, ..., so every store instruction writes
-// 1 KiB of contiguous output -- the output is the larger side of every gather
-// (2 bytes out per 1.06 (Q8_0) or 0.56 (Q4_K) bytes in).  Each lane issues the
-// loads of up to 8 chunks before decoding any, and the output streams out with
-// non-temporal stores.  The fp16 scales are decoded by v_cvt_f32_f16 (exact,
-// subnormals included).  Q4_K: the 8 outputs of a chunk share one 6-bit
-// (scale, min) pair and 8 consecutive nibble bytes; each lane reads the 16 B
-// superblock header (the 32 lanes of a superblock hit the same cache line)
-// and unpacks its pair in VGPRs.  Q5_K / Q6_K use a per-element kernel
-// (correct, not tuned).
+// Design: wave64s own token rows (the id is read once per wave; Q4_K splits a
+// row over 4 waves).  Lane l owns the 16-byte output chunks l, l + 64, ... of
+// its wave, so every store instruction writes 1 KiB of contiguous output --
+// the output is the larger side of every gather (2 bytes out per 1.06 (Q8_0)
+// or 0.56 (Q4_K) bytes in).  Each lane issues the loads of all its chunks (up
+// to 8) before decoding any, and the output streams out with non-temporal
+// stores.  The fp16 scales are decoded by v_cvt_f32_f16 (exact, subnormals
+// included).  Q4_K: the 8 outputs of a chunk share one 6-bit (scale, min) pair
+// and 8 consecutive nibble bytes; each lane reads the 16 B superblock header
+// (the 32 lanes of a superblock hit the same cache line) and unpacks its pair
+// in VGPRs.  Q5_K / Q6_K use a per-element kernel (correct, not tuned).
 #include "nvf_device.hpp"
 #include "nvf_host.hpp"
 
@@ -210,62 +210,70 @@ struct Table {  // plain fp32 / fp16 / bf16 rows
   }
 };
 
-constexpr int kEmbRowsPerBlock = kEmbThreads / kWave;
+constexpr int kEmbWaves = kEmbThreads / kWave;
 
-template <typename TO, typename Src, int U>
+// WPR waves per row: wave w of a row covers its chunk groups w, w + WPR, ...
+// Measured at Qwen2.5-7B prefill shapes: Q8_0 and tables gather best with one
+// wave per row and exactly ceil(chunks / 64) chunks per lane in flight; Q4_K
+// (smaller loads per output) with four waves per row.  Packing two rows into
+// one wave was slower in this form.
+template <typename TO, typename Src, int U, int WPR>
 __global__ __launch_bounds__(kEmbThreads) void embed_rows_kernel(const int64_t* __restrict__ ids, Src src,
                                                                  TO* __restrict__ out, int64_t tokens, int hidden,
                                                                  int64_t vocab) {
   constexpr int N = Pack<TO>::N;
   const int lane = threadIdx.x & (kWave - 1);
-  const int64_t t = (int64_t)blockIdx.x * kEmbRowsPerBlock +
-                    __builtin_amdgcn_readfirstlane((int)(threadIdx.x / kWave));
+  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x / kWave));
+  const int64_t t = (int64_t)blockIdx.x * (kEmbWaves / WPR) + wave / WPR;
+  const int part = wave % WPR;
   if (t >= tokens) return;  // wave-uniform
-  const int64_t id = ids[t];
   const int nch = hidden / N;
+  const int64_t id = ids[t];  // wave-uniform
   TO* dst = out + t * hidden;
-  if (bad_id(id, vocab)) {
+  if (bad_id(id, vocab)) {  // out-of-range id: a NaN row instead of a read
     float nan[N];
 #pragma unroll
     for (int i = 0; i < N; ++i) nan[i] = __builtin_nanf("");
-    for (int c = lane; c < nch; c += kWave) st16(dst + c * N, Pack<TO>::pack(nan));
+    for (int c = part * kWave + lane; c < nch; c += WPR * kWave) st16(dst + c * N, Pack<TO>::pack(nan));
     return;
   }
   const int64_t row0 = id * hidden;
-  for (int base = 0; base < nch; base += U * kWave) {
+  for (int base = 0; base < nch; base += U * WPR * kWave) {
     typename Src::Raw raw[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int c = base + u * kWave + lane;
-      if (c < nch) raw[u] = src.load(row0 + c * N);
+      const int c = base + (u * WPR + part) * kWave + lane;
+      if (c < nch) raw[u] = src.load(row0 + (int64_t)c * N);
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int c = base + u * kWave + lane;
+      const int c = base + (u * WPR + part) * kWave + lane;
       if (c < nch) {
         float v[N];
         src.decode(raw[u], v);
-        st16_nt(dst + c * N, Pack<TO>::pack(v));
+        st16_nt(dst + (int64_t)c * N, Pack<TO>::pack(v));
       }
     }
   }
 }
 
-template <typename TO, typename Src>
+template <typename TO, typename Src, int WPR>
 static int launch_rows(const int64_t* ids, const Src& src, TO* out, int64_t tokens, int64_t hidden, int64_t vocab,
                        hipStream_t st, const char* what) {
   constexpr int N = Pack<TO>::N;
-  const int64_t nch = hidden / N;
-  const dim3 grid((unsigned)((tokens + kEmbRowsPerBlock - 1) / kEmbRowsPerBlock));
+  const int64_t per_lane = (hidden / N + WPR * kWave - 1) / (WPR * kWave);  // chunks per lane
+  const int64_t rows_per_block = kEmbWaves / WPR;
+  const dim3 grid((unsigned)((tokens + rows_per_block - 1) / rows_per_block));
   const int h = (int)hidden;
-  if (nch <= kWave)
-    embed_rows_kernel<TO, Src, 1><<<grid, kEmbThreads, 0, st>>>(ids, src, out, tokens, h, vocab);
-  else if (nch <= 2 * kWave)
-    embed_rows_kernel<TO, Src, 2><<<grid, kEmbThreads, 0, st>>>(ids, src, out, tokens, h, vocab);
-  else if (nch <= 4 * kWave)
-    embed_rows_kernel<TO, Src, 4><<<grid, kEmbThreads, 0, st>>>(ids, src, out, tokens, h, vocab);
-  else
-    embed_rows_kernel<TO, Src, 8><<<grid, kEmbThreads, 0, st>>>(ids, src, out, tokens, h, vocab);
+  switch (per_lane < 8 ? per_lane : 8) {  // exact up to 8 chunks per lane, then the row loops
+#define NVF_EMB_CASE(UU)                                                                                          \
+  case UU:                                                                                                        \
+    embed_rows_kernel<TO, Src, UU, WPR><<<grid, kEmbThreads, 0, st>>>(ids, src, out, tokens, h, vocab); \
+    break;
+    NVF_EMB_CASE(1) NVF_EMB_CASE(2) NVF_EMB_CASE(3) NVF_EMB_CASE(4)
+    NVF_EMB_CASE(5) NVF_EMB_CASE(6) NVF_EMB_CASE(7) NVF_EMB_CASE(8)
+#undef NVF_EMB_CASE
+  }
   return launch_status(what);
 }
 
@@ -414,9 +422,10 @@ static int launch_q8(const int64_t* ids, const uint8_t* w8, const uint16_t* ws, 
   const bool row_ok = hidden % 32 == 0 && hidden <= INT32_MAX && aligned16(out);
   if (blocks) {
     if (row_ok && (reinterpret_cast<uintptr_t>(blocks) & 3u) == 0)
-      return launch_rows(ids, Q8Blocks<N>{blocks}, o, tokens, hidden, vocab, st, "embedding_q8_0_blocks");
+      return launch_rows<TO, Q8Blocks<N>, 1>(ids, Q8Blocks<N>{blocks}, o, tokens, hidden, vocab, st,
+                                                 "embedding_q8_0_blocks");
   } else if (row_ok && (reinterpret_cast<uintptr_t>(w8) & 7u) == 0 && (reinterpret_cast<uintptr_t>(ws) & 1u) == 0) {
-    return launch_rows(ids, Q8Split<N>{w8, ws}, o, tokens, hidden, vocab, st, "embedding_q8_0");
+    return launch_rows<TO, Q8Split<N>, 1>(ids, Q8Split<N>{w8, ws}, o, tokens, hidden, vocab, st, "embedding_q8_0");
   }
   const int64_t total = tokens * hidden;
   embed_q8_generic_kernel<TO><<<grid_for(total), kEmbThreads, 0, st>>>(ids, w8, ws, blocks, o, total, hidden, vocab);
@@ -430,8 +439,9 @@ static int launch_qk(const int64_t* ids, const uint8_t* wq, int64_t tokens, int6
   TO* o = static_cast<TO*>(out);
   if (kind == NVF_Q4_K && hidden % 256 == 0 && hidden <= INT32_MAX && aligned16(wq) && aligned16(out)) {
     if (layout == NVF_QK_LAYOUT_GGML)
-      return launch_rows(ids, Q4K<N, NVF_QK_LAYOUT_GGML>{wq}, o, tokens, hidden, vocab, st, "embedding_q4_k");
-    return launch_rows(ids, Q4K<N, NVF_QK_LAYOUT_HIP_LEGACY>{wq}, o, tokens, hidden, vocab, st, "embedding_q4_k");
+      return launch_rows<TO, Q4K<N, NVF_QK_LAYOUT_GGML>, 4>(ids, {wq}, o, tokens, hidden, vocab, st, "embedding_q4_k");
+    return launch_rows<TO, Q4K<N, NVF_QK_LAYOUT_HIP_LEGACY>, 4>(ids, {wq}, o, tokens, hidden, vocab, st,
+                                                                "embedding_q4_k");
   }
   const int bb = kind == NVF_Q4_K ? 144 : (kind == NVF_Q5_K ? 176 : 210);
   const int64_t total = tokens * hidden;
@@ -447,7 +457,7 @@ static int launch_table(const int64_t* ids, const void* table, int64_t tokens, i
   const TI* tb = static_cast<const TI*>(table);
   TO* o = static_cast<TO*>(out);
   if (hidden % 8 == 0 && hidden <= INT32_MAX && aligned16(table) && aligned16(out))
-    return launch_rows(ids, Table<N, TI>{tb}, o, tokens, hidden, vocab, st, "embedding");
+    return launch_rows<TO, Table<N, TI>, 1>(ids, Table<N, TI>{tb}, o, tokens, hidden, vocab, st, "embedding");
   embed_table_generic_kernel<TI, TO>
       <<<grid_for(tokens * hidden), kEmbThreads, 0, st>>>(ids, tb, o, tokens * hidden, hidden, vocab);
   return launch_status("embedding(generic)");

@@ -7,7 +7,10 @@
 //            a = float(pos[t]) * inv_freq[d]; (x1, x2) -> (x1 c - x2 s, x2 c + x1 s)
 //            for the pair (d, d + head_dim/2).
 //
-// Design: one 256-thread workgroup per token.  The head_dim/2 (cos, sin) pairs
+// Design: one 256-thread workgroup per token, walking the token's q and k heads
+// in passes of 256 / LPH heads with the next pass's loads issued before the
+// current pass's math (a 256-thread two-pass workgroup measured faster than
+// one sized for all 40 heads of Qwen3-8B).  The head_dim/2 (cos, sin) pairs
 // of the token are computed once (precise cosf/sinf, the reference's own
 // functions) into LDS and reused by every q and k head -- the reference
 // recomputes them per head.  The data loads of the first pass are issued before
@@ -22,10 +25,11 @@
 
 namespace nvf {
 
-constexpr int kRopeThreads = 256;
+constexpr int kRopeThreads = 256;     // generic kernel
+constexpr int kRopeVecThreads = 256;   // vector kernel: a token's heads in passes of 256 / LPH
 
 template <typename T, int HD, bool NORM>
-__global__ __launch_bounds__(kRopeThreads) void qk_norm_rope_kernel(T* q, T* k, const int64_t* __restrict__ positions,
+__global__ __launch_bounds__(kRopeVecThreads) void qk_norm_rope_kernel(T* q, T* k, const int64_t* __restrict__ positions,
                                                                     const T* __restrict__ qw, const T* __restrict__ kw,
                                                                     const float* __restrict__ inv_freq, int q_heads,
                                                                     int kv_heads, int64_t q_stride, int64_t k_stride,
@@ -33,7 +37,6 @@ __global__ __launch_bounds__(kRopeThreads) void qk_norm_rope_kernel(T* q, T* k, 
   constexpr int N = Pack<T>::N;
   constexpr int HALF = HD / 2;
   constexpr int LPH = HALF / N;                   // lanes per head
-  constexpr int HPP = kRopeThreads / LPH;         // heads per pass of the workgroup
   static_assert(LPH >= 1 && LPH <= 32 && (LPH & (LPH - 1)) == 0, "lanes per head");
 
   __shared__ float cs_lds[HALF];
@@ -42,6 +45,7 @@ __global__ __launch_bounds__(kRopeThreads) void qk_norm_rope_kernel(T* q, T* k, 
   const int sub = threadIdx.x % LPH;
   const int d0 = sub * N;
   const int total_heads = q_heads + kv_heads;
+  constexpr int hpp = kRopeVecThreads / LPH;  // heads per pass
   auto head_base = [&](int h) -> T* {
     return h < q_heads ? q + t * q_stride + (int64_t)h * HD : k + t * k_stride + (int64_t)(h - q_heads) * HD;
   };
@@ -75,12 +79,16 @@ __global__ __launch_bounds__(kRopeThreads) void qk_norm_rope_kernel(T* q, T* k, 
     s[j] = sn_lds[d0 + j];
   }
 
-  for (; h < total_heads; h += HPP) {
+  for (; h < total_heads; h += hpp) {
     T* base = head_base(h);
     const bool is_q = h < q_heads;
-    if (h >= HPP) {  // later passes (more heads than one pass covers)
-      a = ld16_nt(base + d0);
-      b = ld16_nt(base + HALF + d0);
+    // software pipeline: the next pass's loads go out before this pass's math
+    const int hn = h + hpp;
+    u32x4 an, bn;
+    if (hn < total_heads) {
+      T* nb = head_base(hn);
+      an = ld16_nt(nb + d0);
+      bn = ld16_nt(nb + HALF + d0);
     }
     float x1[N], x2[N];
     Pack<T>::unpack(a, x1);
@@ -105,6 +113,8 @@ __global__ __launch_bounds__(kRopeThreads) void qk_norm_rope_kernel(T* q, T* k, 
     }
     st16_nt(base + d0, Pack<T>::pack(y1));
     st16_nt(base + HALF + d0, Pack<T>::pack(y2));
+    a = an;
+    b = bn;
   }
 }
 
@@ -161,13 +171,11 @@ static int launch_rope(void* q, void* k, const int64_t* pos, const void* qw, con
   bool vec_ok = (q_heads == 0 || (aligned16(q) && q_stride % N == 0)) &&
                 (kv_heads == 0 || (aligned16(k) && k_stride % N == 0)) &&
                 (!NORM || (aligned16(qw) && aligned16(kw)));
-  if (vec_ok) {
+  if (vec_ok && (head_dim == 64 || head_dim == 128 || head_dim == 256)) {
     const dim3 grid((unsigned)tokens);
-    // NORM needs both gamma pointers readable even when one side has no heads.
-    if (NORM && !qwp) qwp = kwp;
-    if (NORM && !kwp) kwp = qwp;
+    const unsigned block = kRopeVecThreads;
 #define NVF_ROPE_LAUNCH(HDV)                                                                                 \
-  qk_norm_rope_kernel<T, HDV, NORM><<<grid, kRopeThreads, 0, st>>>(qp, kp, pos, qwp, kwp, inv_freq, q_heads, \
+  qk_norm_rope_kernel<T, HDV, NORM><<<grid, block, 0, st>>>(qp, kp, pos, qwp, kwp, inv_freq, q_heads, \
                                                                    kv_heads, q_stride, k_stride, eps)
     if (head_dim == 64) {
       NVF_ROPE_LAUNCH(64);

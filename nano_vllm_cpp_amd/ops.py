@@ -45,6 +45,7 @@ SIGNATURES: dict[str, tuple] = {
     "nvf_embedding_qk": (_i32, [_vp, _vp, _i64, _i64, _i64, _i32, _i32, _vp, _i32, _vp]),
     "nvf_embedding": (_i32, [_vp, _vp, _i64, _i64, _i64, _i32, _vp, _i32, _vp]),
     "nvf_rope_inv_freq": (_i32, [_f64, _i32, _vp]),
+    "nvf_stream_copy": (_i32, [_vp, _vp, _i64, _vp]),
     "nvf_last_error": (C.c_char_p, []),
     "nvf_abi_version": (_i32, []),
 }
@@ -215,3 +216,11 @@ def embedding(ids: torch.Tensor, table: torch.Tensor, vocab: int = 0, out_dtype:
     _check(lib().nvf_embedding(_dev(ids, "ids"), _dev(table, "table"), tokens, hidden, vocab, _dt(table),
                                _dev(out, "out"), _dt(out), _stream()), "embedding")
     return out
+
+
+def stream_copy(dst: torch.Tensor, src: torch.Tensor) -> None:
+    """Bandwidth reference copy (16-byte non-temporal loads/stores)."""
+    n = src.numel() * src.element_size()
+    if dst.numel() * dst.element_size() != n:
+        raise ValueError("size mismatch")
+    _check(lib().nvf_stream_copy(_dev(dst, "dst"), _dev(src, "src"), n, _stream()), "stream_copy")

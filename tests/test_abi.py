@@ -70,6 +70,11 @@ def test_host_argument_checks():
     rc, msg = _status(lib.nvf_qk_norm_rope(p, p, p, None, None, p, 4, 2, 1, 128, 200, 128, 1e-6, 1, None))
     assert rc == -1 and "stride" in msg
     assert lib.nvf_qk_norm_rope(p, p, p, None, None, p, 0, 2, 1, 128, 256, 128, 1e-6, 1, None) == 0
+    rc, msg = _status(lib.nvf_stream_copy(p, p, 24, None))
+    assert rc == -1 and "multiple of 16" in msg
+    rc, msg = _status(lib.nvf_stream_copy(p + 8, p, 32, None))
+    assert rc == -1 and "unaligned" in msg
+    assert lib.nvf_stream_copy(p, p, 0, None) == 0
 
 
 def test_inv_freq_host_helper_matches_oracle():

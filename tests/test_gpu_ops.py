@@ -276,3 +276,11 @@ def test_ops_follow_the_current_stream(gpu):
         out = ops.silu_and_mul(d)
     s.synchronize()
     H.assert_close(H.to_host(out), ref, H.F16, what="side stream")
+
+
+def test_stream_copy(gpu):
+    src = torch.arange(1 << 20, dtype=torch.int32, device=gpu)
+    dst = torch.zeros_like(src)
+    case("stream_copy 4 MiB")
+    ops.stream_copy(dst, src)
+    assert torch.equal(dst, src)
