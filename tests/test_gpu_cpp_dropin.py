@@ -1,0 +1,23 @@
+"""Runs tests/cpp/dropin_chain: a C++ program that calls the drop-in C ABI in
+the order src/model.cpp:756-835 does and checks every stage against the C
+oracle (bit-exact gathers and residuals, tolerance elsewhere)."""
+from __future__ import annotations
+
+import subprocess
+from pathlib import Path
+
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+BIN = Path(__file__).resolve().parent / "cpp" / "_build" / "dropin_chain"
+
+
+def test_cpp_model_call_sequence(gpu):
+    if not BIN.exists():
+        pytest.fail(f"{BIN} not built (run __graft_entry__.build())")
+    print("[case] C++ drop-in chain", flush=True)
+    r = subprocess.run([str(BIN)], capture_output=True, text=True, timeout=120)
+    print(r.stdout)
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert "DROPIN CHAIN OK" in r.stdout
