@@ -47,15 +47,21 @@ def parse() -> argparse.Namespace:
     p.add_argument("--warmup", type=int, default=5)
     p.add_argument("--config", type=int, default=2, help="BASELINE config index (1-4)")
     p.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU-baseline budget (0 = skip)")
+    p.add_argument("--emb", default="", choices=["", "q8_0", "q8_0_blocks", "q4_k", "q5_k", "q6_k", "f16"],
+                   help="embedding table format (default: the config's)")
     p.add_argument("--only", default="", help="comma list of ops to run (default all): emb,rms,rope,silu,copy")
     return p.parse_args()
 
 
-def op_bytes(cfg, e: int) -> dict[str, int]:
+TABLE_BYTES_PER_ELEM = {"q8_0": 34 / 32, "q8_0_blocks": 34 / 32, "q4_k": 144 / 256, "q5_k": 176 / 256,
+                        "q6_k": 210 / 256, "f16": 2.0}
+
+
+def op_bytes(cfg, e: int, emb_fmt: str) -> dict[str, int]:
     """Algorithmic HBM bytes per launch (each input read once, each output written once)."""
     T, Hd, I = cfg.tokens, cfg.hidden, cfg.inter
     heads = cfg.q_heads + cfg.kv_heads
-    emb = (T * Hd * 144 // 256 if cfg.emb == "q4_k" else T * Hd * 34 // 32) + 8 * T + T * Hd * e
+    emb = int(T * Hd * TABLE_BYTES_PER_ELEM[emb_fmt]) + 8 * T + T * Hd * e
     rope = 2 * T * heads * cfg.head_dim * e + 8 * T + (2 * cfg.head_dim * e if cfg.qk_norm else 0)
     return {"emb": emb, "rms": 4 * T * Hd * e + Hd * e, "rope": rope, "silu": 3 * T * I * e}
 
@@ -81,7 +87,8 @@ def main() -> int:
     T, Hd, I, V = cfg.tokens, cfg.hidden, cfg.inter, cfg.vocab
     qs, ks = cfg.q_heads * cfg.head_dim, cfg.kv_heads * cfg.head_dim
     g = torch.Generator(device=dev).manual_seed(cfg.seed)
-    nbytes = op_bytes(cfg, e)
+    emb_fmt = args.emb or cfg.emb
+    nbytes = op_bytes(cfg, e, emb_fmt)
     only = set(filter(None, args.only.split(","))) or {"emb", "rms", "rope", "silu", "copy"}
 
     def nsets(b: int) -> int:
@@ -91,11 +98,19 @@ def main() -> int:
         return (torch.randn(shape, generator=g, device=dev) * std + mean).to(tdt)
 
     # ---- inputs (resident in HBM before timing) ------------------------------
-    if cfg.emb == "q8_0":
+    if emb_fmt in ("q8_0", "q8_0_blocks"):
         w8 = torch.randint(-127, 128, (V * Hd,), generator=g, device=dev, dtype=torch.int8)
         ws = torch.empty(V * Hd // 32, device=dev).uniform_(1e-3, 1e-2, generator=g).half().view(torch.int16)
-    else:
+        if emb_fmt == "q8_0_blocks":
+            blocks = torch.cat([ws.view(torch.uint8).view(-1, 2), w8.view(torch.uint8).view(-1, 32)], 1).reshape(-1)
+            del w8, ws
+    elif emb_fmt == "q4_k":
         blocks = torch.from_numpy(H.gen_q4_k(np.random.default_rng(cfg.seed), V * Hd // 256)).to(dev)
+    elif emb_fmt in ("q5_k", "q6_k"):
+        bb, offs = (176, (0, 2)) if emb_fmt == "q5_k" else (210, (208,))
+        blocks = torch.from_numpy(H.gen_raw_blocks(np.random.default_rng(cfg.seed), V * Hd // 256, bb, offs)).to(dev)
+    else:
+        f16_table = randn((V, Hd)).half()
     n_emb = nsets(nbytes["emb"])
     emb_sets = [(torch.randint(0, V, (T,), generator=g, device=dev), torch.empty(T, Hd, dtype=tdt, device=dev))
                 for _ in range(n_emb)] if "emb" in only else []
@@ -117,10 +132,15 @@ def main() -> int:
 
     def run_emb(i):
         ids, out = emb_sets[i % len(emb_sets)]
-        if cfg.emb == "q8_0":
+        if emb_fmt == "q8_0":
             ops.embedding_q8_0(ids, w8, ws, Hd, V, out=out)
+        elif emb_fmt == "q8_0_blocks":
+            ops.embedding_q8_0_blocks(ids, blocks, Hd, V, out=out)
+        elif emb_fmt == "f16":
+            ops.embedding(ids, f16_table, V, out=out)
         else:
-            ops.embedding_qk(ids, blocks, Hd, ops.Q4_K, V, out=out)
+            kind = {"q4_k": ops.Q4_K, "q5_k": ops.Q5_K, "q6_k": ops.Q6_K}[emb_fmt]
+            ops.embedding_qk(ids, blocks, Hd, kind, V, out=out)
 
     def run_rms(i):
         x, r, out = rms_sets[i % len(rms_sets)]
@@ -192,7 +212,8 @@ def main() -> int:
                     "bound": "hbm", "achieved": res_ops[dom]["GB_s"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                     "frac": res_ops[dom]["frac_of_peak"], "traffic": traffic_from_profiles(dom, args.config)}
 
-    cpu = cpu_baseline(cfg, args.cpu_seconds, H) if args.cpu_seconds > 0 and chain_ops == ["emb", "rms", "rope", "silu"] else None
+    cpu = (cpu_baseline(cfg, args.cpu_seconds, H)
+           if args.cpu_seconds > 0 and chain_ops == ["emb", "rms", "rope", "silu"] and emb_fmt == cfg.emb else None)
 
     line = {
         "metric": METRIC,
@@ -208,7 +229,7 @@ def main() -> int:
         "dtype": {H.F16: "f16", H.BF16: "bf16", H.F32: "f32"}[dt],
         "data": "synthetic (seeded; BASELINE value distributions)",
         "config": {"workload": f"BASELINE config {args.config}: {cfg.name}; one step = "
-                               f"{cfg.emb} embedding gather + residual-add RMSNorm + "
+                               f"{emb_fmt} embedding gather + residual-add RMSNorm + "
                                f"{'QK-norm + ' if cfg.qk_norm else ''}NeoX RoPE q/k + SwiGLU",
                    "tokens": T, "hidden": Hd, "intermediate": I, "vocab": V, "q_heads": cfg.q_heads,
                    "kv_heads": cfg.kv_heads, "head_dim": cfg.head_dim, "value_is": "tokens / GPU time of one step (HIP events around all timed steps)",

@@ -9,17 +9,22 @@
 //                      order GGML (src/gguf.cpp:477-496) or HIP_LEGACY (:130-140)
 //   F16/BF16/F32       src/hip_ops.hip:553-563
 //
-// Design: wave64s own token rows (the id is read once per wave; Q4_K splits a
-// row over 4 waves).  Lane l owns the 16-byte output chunks l, l + 64, ... of
-// its wave, so every store instruction writes 1 KiB of contiguous output --
-// the output is the larger side of every gather (2 bytes out per 1.06 (Q8_0)
-// or 0.56 (Q4_K) bytes in).  Each lane issues the loads of all its chunks (up
-// to 8) before decoding any, and the output streams out with non-temporal
-// stores.  The fp16 scales are decoded by v_cvt_f32_f16 (exact, subnormals
-// included).  Q4_K: the 8 outputs of a chunk share one 6-bit (scale, min) pair
-// and 8 consecutive nibble bytes; each lane reads the 16 B superblock header
-// (the 32 lanes of a superblock hit the same cache line) and unpacks its pair
-// in VGPRs.  Q5_K / Q6_K use a per-element kernel (correct, not tuned).
+// Design: wave64s own token rows (the id is read once per wave).  Lane l owns
+// the 16-byte output chunks l, l + 64, ... of its wave, so every store
+// instruction writes 1 KiB of contiguous output -- the output is the larger
+// side of every gather (2 bytes out per 1.06 (Q8_0) or 0.56 (Q4_K) bytes in)
+// -- and the output streams out with non-temporal stores.  The fp16 scales are
+// decoded by v_cvt_f32_f16 (exact, subnormals included).
+//   * Q8_0 split planes and plain tables: each lane issues the loads of all its
+//     chunks (up to 8) straight from HBM before decoding any.
+//   * Block formats (Q8_0 34 B blocks, Q4_K, Q5_K, Q6_K): the wave stages its
+//     row's blocks in LDS with coalesced 16-byte loads, then each lane decodes
+//     its chunks from LDS.  The 8 outputs of a chunk share one scale (and for
+//     the K-quants one 6-bit (scale, min) pair, unpacked in VGPRs from the
+//     staged 12-byte table).  Rows longer than the 16 KiB stage fall back to
+//     direct per-chunk loads (Q4_K/Q5_K/Q6_K split a row over 4 waves there).
+//   * A hidden that is not a multiple of the block takes a per-element kernel
+//     (correct, not tuned).
 #include "nvf_device.hpp"
 #include "nvf_host.hpp"
 
@@ -73,6 +78,22 @@ struct Q8Split {  // int8 plane + fp16 scale plane (src/model.cpp:394-404)
   }
 };
 
+// Reads NB (4 or 8) bytes at a 2-byte-aligned address: only the dwords that
+// hold those bytes are loaded (plus a 16-bit tail load when the run starts 2
+// bytes into a dword), realigned with v_alignbyte.  Nothing outside the run's
+// dwords is touched, so a run at the very end of a table stays in bounds.
+template <int NB>
+__device__ __forceinline__ void load_a2(const uint8_t* p, uint32_t* out) {
+  const bool mid = (reinterpret_cast<uintptr_t>(p) & 2u) != 0;
+  const uint32_t* w = reinterpret_cast<const uint32_t*>(reinterpret_cast<uintptr_t>(p) & ~uintptr_t(3));
+  uint32_t d[NB / 4 + 1];
+#pragma unroll
+  for (int i = 0; i < NB / 4; ++i) d[i] = w[i];
+  d[NB / 4] = mid ? (uint32_t)reinterpret_cast<const uint16_t*>(w + NB / 4)[0] : 0u;
+#pragma unroll
+  for (int i = 0; i < NB / 4; ++i) out[i] = mid ? __builtin_amdgcn_alignbyte(d[i + 1], d[i], 2) : d[i];
+}
+
 template <int N>
 struct Q8Blocks {  // interleaved 34-byte blocks [fp16 d][32 x int8]
   const uint8_t* blocks;
@@ -80,21 +101,10 @@ struct Q8Blocks {  // interleaved 34-byte blocks [fp16 d][32 x int8]
     uint32_t q[N / 4];
     uint32_t s;
   };
-  // The N quant bytes start 2 bytes into a dword when the block index is even.
-  // Only dwords that hold chunk bytes are read; the last two bytes come from a
-  // 16-bit load, so nothing past the block (or the table) is touched.
   __device__ __forceinline__ Raw load(int64_t e0) const {
     const uint8_t* blk = blocks + (e0 >> 5) * 34;
-    const uint8_t* p = blk + 2 + (e0 & 31);
-    const bool mid = (reinterpret_cast<uintptr_t>(p) & 2u) != 0;
-    const uint32_t* w = reinterpret_cast<const uint32_t*>(reinterpret_cast<uintptr_t>(p) & ~uintptr_t(3));
     Raw r;
-    uint32_t d[N / 4 + 1];
-#pragma unroll
-    for (int i = 0; i < N / 4; ++i) d[i] = w[i];
-    d[N / 4] = mid ? (uint32_t)reinterpret_cast<const uint16_t*>(w + N / 4)[0] : 0u;
-#pragma unroll
-    for (int i = 0; i < N / 4; ++i) r.q[i] = mid ? __builtin_amdgcn_alignbyte(d[i + 1], d[i], 2) : d[i];
+    load_a2<N>(blk + 2 + (e0 & 31), r.q);  // the quants start 2 bytes into a dword for even blocks
     r.s = *reinterpret_cast<const uint16_t*>(blk);
     return r;
   }
@@ -159,6 +169,88 @@ struct Q4K {  // 144-byte superblocks; N consecutive outputs share one group j =
     for (int i = 0; i < N / 4; ++i)
 #pragma unroll
       for (int k = 0; k < 4; ++k) v[4 * i + k] = s * (float)((byte_of(r.q[i], k) >> sh) & 0xfu) - m;
+  }
+};
+
+template <int N>
+__device__ __forceinline__ void load_n(const uint8_t* p, uint32_t* out) {  // N-byte aligned run
+  if constexpr (N == 8) {
+    const uint2 v = *reinterpret_cast<const uint2*>(p);
+    out[0] = v.x;
+    out[1] = v.y;
+  } else {
+    out[0] = *reinterpret_cast<const uint32_t*>(p);
+  }
+}
+
+template <int N>
+struct Q5K {  // 176-byte superblocks [d][dmin][12 B scales][32 B qh][128 B ql] (src/hip_ops.hip:142-155)
+  const uint8_t* wq;
+  struct Raw {
+    u32x4 hdr;
+    uint32_t ql[N / 4];
+    uint32_t qh[N / 4];
+    int i;
+  };
+  // element 64g + 32s + l: low bits = nibble s of ql[32g + l], bit 4 = bit (2g + s) of qh[l]
+  __device__ __forceinline__ Raw load(int64_t e0) const {
+    const uint8_t* blk = wq + (e0 >> 8) * 176;
+    Raw r;
+    r.i = (int)(e0 & 255);
+    r.hdr = ld16(blk);
+    load_n<N>(blk + 48 + 32 * (r.i >> 6) + (r.i & 31), r.ql);
+    load_n<N>(blk + 16 + (r.i & 31), r.qh);
+    return r;
+  }
+  __device__ __forceinline__ void decode(const Raw& r, float* v) const {
+    const int j = r.i >> 5, sh = (j & 1) * 4, hb = j;  // j = 2g + s
+    uint32_t sc, mn;
+    q4k_sm(r.hdr[1], r.hdr[2], r.hdr[3], j, sc, mn);
+    const float s = half_bits_to_f32(r.hdr[0] & 0xffffu) * (float)sc;
+    const float m = half_bits_to_f32(r.hdr[0] >> 16) * (float)mn;
+#pragma unroll
+    for (int w = 0; w < N / 4; ++w)
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const uint32_t q = ((byte_of(r.ql[w], k) >> sh) & 0xfu) | (((byte_of(r.qh[w], k) >> hb) & 1u) << 4);
+        v[4 * w + k] = s * (float)q - m;
+      }
+  }
+};
+
+template <int N>
+struct Q6K {  // 210-byte superblocks [128 B ql][64 B qh][16 x int8 scales][fp16 d] (src/gguf.cpp:500-518)
+  const uint8_t* wq;
+  struct Raw {
+    uint32_t ql[N / 4];
+    uint32_t qh[N / 4];
+    uint32_t sd;  // int8 scale (low byte) | fp16 d << 16
+    int i;
+  };
+  // element 128h + 32s + l: low 4 bits = nibble (s >> 1) of ql[64h + 32(s & 1) + l],
+  // high 2 bits = bits 2s..2s+1 of qh[32h + l], scale sc[8h + l/16 + 2s]
+  __device__ __forceinline__ Raw load(int64_t e0) const {
+    const uint8_t* blk = wq + (e0 >> 8) * 210;  // 2-byte aligned
+    Raw r;
+    r.i = (int)(e0 & 255);
+    const int h = r.i >> 7, t = r.i & 127, l0 = t & 31, slot = t >> 5;
+    load_a2<N>(blk + 64 * h + 32 * (slot & 1) + l0, r.ql);
+    load_a2<N>(blk + 128 + 32 * h + l0, r.qh);
+    const uint32_t sc = blk[192 + 8 * h + (l0 >> 4) + 2 * slot];
+    r.sd = sc | ((uint32_t)*reinterpret_cast<const uint16_t*>(blk + 208) << 16);
+    return r;
+  }
+  __device__ __forceinline__ void decode(const Raw& r, float* v) const {
+    const int slot = (r.i & 127) >> 5;
+    const int lsh = (slot >> 1) * 4, hsh = 2 * slot;
+    const float ds = half_bits_to_f32(r.sd >> 16) * (float)(int8_t)(r.sd & 0xffu);  // (d * sc) first, as the reference
+#pragma unroll
+    for (int w = 0; w < N / 4; ++w)
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int q = (int)(((byte_of(r.ql[w], k) >> lsh) & 0xfu) | (((byte_of(r.qh[w], k) >> hsh) & 3u) << 4));
+        v[4 * w + k] = ds * (float)(q - 32);
+      }
   }
 };
 
@@ -278,7 +370,189 @@ static int launch_rows(const int64_t* ids, const Src& src, TO* out, int64_t toke
 }
 
 // ---------------------------------------------------------------------------
-// Generic K-quant element decode (any hidden; Q5_K and Q6_K always).
+// LDS-staged row gather for block formats.  A wave copies its row's blocks
+// into LDS with coalesced 16-byte loads (from the 16-byte-aligned address at
+// or below the row's first block), then every lane decodes its own chunks of
+// N outputs out of LDS and stores them as before.  This turns the many small
+// per-chunk loads of the K-quant formats (header, nibbles, high bits, scales)
+// into a few full-width loads per lane (measured at Qwen2.5-7B shape: Q5_K
+// 57% -> 69%, Q6_K 50% -> 60%, Q8_0 blocks 65% -> 68%, Q4_K 74% -> 75% of the
+// 8 TB/s peak).  The stage starts at the 16-byte-aligned address at or below
+// the row and ends with the 16-byte granule holding the row's last byte, so
+// the few extra bytes read never leave those granules (no fault is possible).
+// A format supplies
+//   kBlockBytes, kBlockElems, decode(const uint8_t* blk, int i, float* v)
+// reading the block from LDS (elements i .. i+N-1 of the block).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ uint32_t lds_u32_a2(const uint8_t* p) {  // 4 bytes at a 2-byte-aligned LDS address
+  const uint16_t* h = reinterpret_cast<const uint16_t*>(p);
+  return (uint32_t)h[0] | ((uint32_t)h[1] << 16);
+}
+
+template <int N>
+struct StagedQ6K {
+  static constexpr int kBlockBytes = 210, kBlockElems = 256;
+  __device__ __forceinline__ static void decode(const uint8_t* blk, int i, float* v) {
+    const int h = i >> 7, t = i & 127, l0 = t & 31, slot = t >> 5;
+    const int lsh = (slot >> 1) * 4, hsh = 2 * slot;
+    const float ds = half_bits_to_f32(*reinterpret_cast<const uint16_t*>(blk + 208)) *
+                     (float)(int8_t)blk[192 + 8 * h + (l0 >> 4) + 2 * slot];
+    const uint8_t* ql = blk + 64 * h + 32 * (slot & 1) + l0;
+    const uint8_t* qh = blk + 128 + 32 * h + l0;
+#pragma unroll
+    for (int w = 0; w < N / 4; ++w) {
+      const uint32_t a = lds_u32_a2(ql + 4 * w), b = lds_u32_a2(qh + 4 * w);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int q = (int)(((byte_of(a, k) >> lsh) & 0xfu) | (((byte_of(b, k) >> hsh) & 3u) << 4));
+        v[4 * w + k] = ds * (float)(q - 32);
+      }
+    }
+  }
+};
+
+template <int N>
+struct StagedQ5K {
+  static constexpr int kBlockBytes = 176, kBlockElems = 256;
+  __device__ __forceinline__ static void decode(const uint8_t* blk, int i, float* v) {
+    const int j = i >> 5, sh = (j & 1) * 4, l0 = i & 31;
+    const uint32_t* hd = reinterpret_cast<const uint32_t*>(blk);  // 176 B blocks stay 16-byte aligned
+    uint32_t sc, mn;
+    q4k_sm(hd[1], hd[2], hd[3], j, sc, mn);
+    const float s = half_bits_to_f32(hd[0] & 0xffffu) * (float)sc;
+    const float m = half_bits_to_f32(hd[0] >> 16) * (float)mn;
+    const uint32_t* ql = reinterpret_cast<const uint32_t*>(blk + 48 + 32 * (i >> 6) + l0);
+    const uint32_t* qh = reinterpret_cast<const uint32_t*>(blk + 16 + l0);
+#pragma unroll
+    for (int w = 0; w < N / 4; ++w) {
+      const uint32_t a = ql[w], b = qh[w];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const uint32_t q = ((byte_of(a, k) >> sh) & 0xfu) | (((byte_of(b, k) >> j) & 1u) << 4);
+        v[4 * w + k] = s * (float)q - m;
+      }
+    }
+  }
+};
+
+template <int N, int LAYOUT>
+struct StagedQ4K {
+  static constexpr int kBlockBytes = 144, kBlockElems = 256;
+  __device__ __forceinline__ static void decode(const uint8_t* blk, int i, float* v) {
+    const int j = i >> 5;
+    const int off = LAYOUT == NVF_QK_LAYOUT_GGML ? 32 * (i >> 6) + (i & 31) : 16 * (i >> 5) + (i & 15);
+    const int sh = LAYOUT == NVF_QK_LAYOUT_GGML ? ((i >> 5) & 1) * 4 : ((i >> 4) & 1) * 4;
+    const uint32_t* hd = reinterpret_cast<const uint32_t*>(blk);
+    uint32_t sc, mn;
+    q4k_sm(hd[1], hd[2], hd[3], j, sc, mn);
+    const float s = half_bits_to_f32(hd[0] & 0xffffu) * (float)sc;
+    const float m = half_bits_to_f32(hd[0] >> 16) * (float)mn;
+    const uint32_t* q = reinterpret_cast<const uint32_t*>(blk + 16 + off);
+#pragma unroll
+    for (int w = 0; w < N / 4; ++w) {
+      const uint32_t a = q[w];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) v[4 * w + k] = s * (float)((byte_of(a, k) >> sh) & 0xfu) - m;
+    }
+  }
+};
+
+template <int N>
+struct StagedQ8Blocks {
+  static constexpr int kBlockBytes = 34, kBlockElems = 32;
+  __device__ __forceinline__ static void decode(const uint8_t* blk, int i, float* v) {
+    const float s = half_bits_to_f32(*reinterpret_cast<const uint16_t*>(blk));
+#pragma unroll
+    for (int w = 0; w < N / 4; ++w) {
+      const uint32_t a = lds_u32_a2(blk + 2 + i + 4 * w);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) v[4 * w + k] = s * sbyte(a, k);
+    }
+  }
+};
+
+constexpr int kStageMaxBytesPerWave = 16384;  // LDS per wave: rows up to 16 KiB of blocks
+
+template <typename TO, typename Fmt, int L16>  // L16: 16-byte loads per lane to stage a row
+__global__ __launch_bounds__(kEmbThreads) void embed_rows_staged_kernel(const int64_t* __restrict__ ids,
+                                                                        const uint8_t* __restrict__ table,
+                                                                        TO* __restrict__ out, int64_t tokens,
+                                                                        int hidden, int64_t vocab, int stage_bytes) {
+  constexpr int N = Pack<TO>::N;
+  extern __shared__ __attribute__((aligned(16))) uint8_t stage[];  // kEmbWaves slices of stage_bytes
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x / kWave));
+  const int64_t t = (int64_t)blockIdx.x * kEmbWaves + wave;
+  if (t >= tokens) return;  // wave-uniform; the wave's LDS slice is its own (no workgroup barrier)
+  const int64_t id = ids[t];
+  const int nch = hidden / N;
+  TO* dst = out + t * hidden;
+  if (bad_id(id, vocab)) {
+    float nan[N];
+#pragma unroll
+    for (int i = 0; i < N; ++i) nan[i] = __builtin_nanf("");
+    for (int c = lane; c < nch; c += kWave) st16(dst + c * N, Pack<TO>::pack(nan));
+    return;
+  }
+  const int nblk = hidden / Fmt::kBlockElems;
+  const uint8_t* row = table + id * (int64_t)nblk * Fmt::kBlockBytes;
+  const uintptr_t a16 = reinterpret_cast<uintptr_t>(row) & ~uintptr_t(15);
+  const int delta = (int)(reinterpret_cast<uintptr_t>(row) - a16);
+  const int n16 = (delta + nblk * Fmt::kBlockBytes + 15) >> 4;
+  uint8_t* my = stage + wave * stage_bytes;
+  u32x4 r[L16];
+#pragma unroll
+  for (int u = 0; u < L16; ++u) {
+    const int c = u * kWave + lane;
+    if (c < n16) r[u] = ld16(reinterpret_cast<const uint8_t*>(a16) + c * 16);
+  }
+#pragma unroll
+  for (int u = 0; u < L16; ++u) {
+    const int c = u * kWave + lane;
+    if (c < n16) *reinterpret_cast<u32x4*>(my + c * 16) = r[u];
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  const uint8_t* rowl = my + delta;
+  for (int c = lane; c < nch; c += kWave) {
+    const int e = c * N;
+    float v[N];
+    Fmt::decode(rowl + (e / Fmt::kBlockElems) * Fmt::kBlockBytes, e % Fmt::kBlockElems, v);
+    st16_nt(dst + (int64_t)c * N, Pack<TO>::pack(v));
+  }
+}
+
+template <typename TO, typename Fmt>
+static bool launch_staged(const int64_t* ids, const uint8_t* table, TO* out, int64_t tokens, int64_t hidden,
+                          int64_t vocab, hipStream_t st) {
+  const int64_t row_bytes = hidden / Fmt::kBlockElems * Fmt::kBlockBytes;
+  const int64_t n16 = (15 + row_bytes + 15) / 16;
+  if (hidden % Fmt::kBlockElems != 0 || n16 * 16 > kStageMaxBytesPerWave || hidden > INT32_MAX) return false;
+  const int stage_bytes = (int)(n16 * 16);
+  const size_t lds = (size_t)stage_bytes * kEmbWaves;
+  const dim3 grid((unsigned)((tokens + kEmbWaves - 1) / kEmbWaves));
+  const int h = (int)hidden;
+  const int l16 = (int)((n16 + kWave - 1) / kWave);
+  switch (l16) {
+#define NVF_STAGE_CASE(L)                                                                                   \
+  case L:                                                                                                   \
+    embed_rows_staged_kernel<TO, Fmt, L><<<grid, kEmbThreads, lds, st>>>(ids, table, out, tokens, h, vocab, \
+                                                                          stage_bytes);                      \
+    break;
+    NVF_STAGE_CASE(1) NVF_STAGE_CASE(2) NVF_STAGE_CASE(3) NVF_STAGE_CASE(4)
+    NVF_STAGE_CASE(5) NVF_STAGE_CASE(6) NVF_STAGE_CASE(7) NVF_STAGE_CASE(8)
+    NVF_STAGE_CASE(9) NVF_STAGE_CASE(10) NVF_STAGE_CASE(11) NVF_STAGE_CASE(12)
+    NVF_STAGE_CASE(13) NVF_STAGE_CASE(14) NVF_STAGE_CASE(15) NVF_STAGE_CASE(16)
+#undef NVF_STAGE_CASE
+    default:
+      return false;
+  }
+  return true;
+}
+
+// ---------------------------------------------------------------------------
+// Generic K-quant element decode (hidden not a multiple of 256).
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ float fp16_at(const uint8_t* p) {
   return half_bits_to_f32((uint32_t)p[0] | ((uint32_t)p[1] << 8));
@@ -421,6 +695,8 @@ static int launch_q8(const int64_t* ids, const uint8_t* w8, const uint16_t* ws, 
   TO* o = static_cast<TO*>(out);
   const bool row_ok = hidden % 32 == 0 && hidden <= INT32_MAX && aligned16(out);
   if (blocks) {
+    if (row_ok && launch_staged<TO, StagedQ8Blocks<N>>(ids, blocks, o, tokens, hidden, vocab, st))
+      return launch_status("embedding_q8_0_blocks(staged)");
     if (row_ok && (reinterpret_cast<uintptr_t>(blocks) & 3u) == 0)
       return launch_rows<TO, Q8Blocks<N>, 1>(ids, Q8Blocks<N>{blocks}, o, tokens, hidden, vocab, st,
                                                  "embedding_q8_0_blocks");
@@ -437,7 +713,23 @@ static int launch_qk(const int64_t* ids, const uint8_t* wq, int64_t tokens, int6
                      int layout, void* out, hipStream_t st) {
   constexpr int N = Pack<TO>::N;
   TO* o = static_cast<TO*>(out);
-  if (kind == NVF_Q4_K && hidden % 256 == 0 && hidden <= INT32_MAX && aligned16(wq) && aligned16(out)) {
+  if (hidden % 256 == 0 && hidden <= INT32_MAX && aligned16(wq) && aligned16(out)) {
+    // rows up to the 16 KiB stage: LDS-staged (measured faster for every
+    // K-quant); longer rows: the direct per-chunk loads below
+    bool staged = false;
+    if (kind == NVF_Q5_K)
+      staged = launch_staged<TO, StagedQ5K<N>>(ids, wq, o, tokens, hidden, vocab, st);
+    else if (kind == NVF_Q6_K)
+      staged = launch_staged<TO, StagedQ6K<N>>(ids, wq, o, tokens, hidden, vocab, st);
+    else if (layout == NVF_QK_LAYOUT_GGML)
+      staged = launch_staged<TO, StagedQ4K<N, NVF_QK_LAYOUT_GGML>>(ids, wq, o, tokens, hidden, vocab, st);
+    else
+      staged = launch_staged<TO, StagedQ4K<N, NVF_QK_LAYOUT_HIP_LEGACY>>(ids, wq, o, tokens, hidden, vocab, st);
+    if (staged) return launch_status("embedding_qk(staged)");
+    if (kind == NVF_Q5_K)
+      return launch_rows<TO, Q5K<N>, 4>(ids, {wq}, o, tokens, hidden, vocab, st, "embedding_q5_k");
+    if (kind == NVF_Q6_K)
+      return launch_rows<TO, Q6K<N>, 4>(ids, {wq}, o, tokens, hidden, vocab, st, "embedding_q6_k");
     if (layout == NVF_QK_LAYOUT_GGML)
       return launch_rows<TO, Q4K<N, NVF_QK_LAYOUT_GGML>, 4>(ids, {wq}, o, tokens, hidden, vocab, st, "embedding_q4_k");
     return launch_rows<TO, Q4K<N, NVF_QK_LAYOUT_HIP_LEGACY>, 4>(ids, {wq}, o, tokens, hidden, vocab, st,

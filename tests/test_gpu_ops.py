@@ -89,12 +89,13 @@ def test_embedding_q4_k(gpu, layout, dt, hidden):
 
 
 @pytest.mark.parametrize("kind,bb,fp16_off", [(13, 176, (0, 2)), (14, 210, (208,))], ids=["q5_k", "q6_k"])
-@pytest.mark.parametrize("hidden", [512, 896])
+@pytest.mark.parametrize("hidden", [512, 896, 3584])
 def test_embedding_q5_q6_k(gpu, kind, bb, fp16_off, hidden):
     r = H.rng(kind * 7 + hidden)
     V, T = 64, 33
     blocks = H.gen_raw_blocks(r, V * hidden // 256, bb, fp16_off)
     ids = r.integers(0, V, T).astype(np.int64)
+    ids[:2] = [V - 1, 0]  # the table's last superblock (Q6_K: 2-byte aligned end) and its first
     for dt in DTYPES:
         ref = np.empty((T, hidden), H.NP_STORAGE[dt])
         o().orc_embedding_qk(H.ptr(ids), H.ptr(blocks), T, hidden, kind, H.GGML, H.ptr(ref), dt)
@@ -102,6 +103,31 @@ def test_embedding_q5_q6_k(gpu, kind, bb, fp16_off, hidden):
         got = ops.embedding_qk(H.to_dev(ids, gpu), H.to_dev(blocks, gpu), hidden, kind, V,
                                out_dtype=H.torch_dtype(dt))
         H.assert_bitexact(H.to_host(got), ref, f"kind {kind}")
+
+
+@pytest.mark.parametrize("fmt,hidden", [("q8_0_blocks", 15424), ("q4_k", 29440), ("q5_k", 24064),
+                                        ("q6_k", 20480)])
+def test_embedding_rows_beyond_the_lds_stage(gpu, fmt, hidden):
+    """Rows longer than the 16 KiB per-wave LDS stage take the direct-load path."""
+    r = H.rng(hidden)
+    V, T = 8, 12
+    ids = r.integers(0, V, T).astype(np.int64)
+    ids[0] = V - 1
+    if fmt == "q8_0_blocks":
+        w8, ws = H.gen_q8_0(r, V, hidden)
+        blocks = H.q8_split_to_blocks(w8, ws)
+        ref = np.empty((T, hidden), np.uint16)
+        o().orc_embedding_q8_split(H.ptr(ids), H.ptr(w8), H.ptr(ws), T, hidden, H.ptr(ref), H.F16)
+        case(f"q8_0 blocks direct path hidden={hidden}")
+        got = ops.embedding_q8_0_blocks(H.to_dev(ids, gpu), H.to_dev(blocks, gpu), hidden, V, out_dtype=torch.float16)
+    else:
+        kind, bb, offs = {"q4_k": (12, 144, (0, 2)), "q5_k": (13, 176, (0, 2)), "q6_k": (14, 210, (208,))}[fmt]
+        blocks = H.gen_raw_blocks(r, V * hidden // 256, bb, offs)
+        ref = np.empty((T, hidden), np.uint16)
+        o().orc_embedding_qk(H.ptr(ids), H.ptr(blocks), T, hidden, kind, H.GGML, H.ptr(ref), H.F16)
+        case(f"{fmt} direct path hidden={hidden}")
+        got = ops.embedding_qk(H.to_dev(ids, gpu), H.to_dev(blocks, gpu), hidden, kind, V, out_dtype=torch.float16)
+    H.assert_bitexact(H.to_host(got), ref, f"{fmt} direct path")
 
 
 @pytest.mark.parametrize("tdt", DTYPES, ids=DT_IDS)
