@@ -157,8 +157,11 @@ struct FastDiv {
     while ((1ull << s) < div) ++s;
     m = (uint32_t)(((1ull << 32) * ((1ull << s) - div)) / div + 1);
   }
-  __device__ __forceinline__ uint32_t div(uint32_t n) const {
-    return (uint32_t)(((uint64_t)__umulhi(n, m) + n) >> s);
+  // (n * m) >> 32 is v_mul_hi_u32 on the device; the same code runs on the host
+  // for the unit test.
+  __host__ __device__ __forceinline__ uint32_t div(uint32_t n) const {
+    const uint32_t hi = (uint32_t)(((uint64_t)n * m) >> 32);
+    return (uint32_t)(((uint64_t)hi + n) >> s);
   }
 };
 
