@@ -49,7 +49,8 @@ def parse() -> argparse.Namespace:
     p.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU-baseline budget (0 = skip)")
     p.add_argument("--emb", default="", choices=["", "q8_0", "q8_0_blocks", "q4_k", "q5_k", "q6_k", "f16"],
                    help="embedding table format (default: the config's)")
-    p.add_argument("--only", default="", help="comma list of ops to run (default all): emb,rms,rope,silu,copy")
+    p.add_argument("--only", default="",
+                   help="comma list of ops (default emb,rms,rope,silu,copy); also emb_rms, rms_q8 (fusions)")
     return p.parse_args()
 
 
@@ -63,7 +64,12 @@ def op_bytes(cfg, e: int, emb_fmt: str) -> dict[str, int]:
     heads = cfg.q_heads + cfg.kv_heads
     emb = int(T * Hd * TABLE_BYTES_PER_ELEM[emb_fmt]) + 8 * T + T * Hd * e
     rope = 2 * T * heads * cfg.head_dim * e + 8 * T + (2 * cfg.head_dim * e if cfg.qk_norm else 0)
-    return {"emb": emb, "rms": 4 * T * Hd * e + Hd * e, "rope": rope, "silu": 3 * T * I * e}
+    return {"emb": emb, "rms": 4 * T * Hd * e + Hd * e, "rope": rope, "silu": 3 * T * I * e,
+            # fusions with the neighbours (not in the default chain):
+            # layer-0 gather + norm: table rows + ids + residual and out writes
+            "emb_rms": int(T * Hd * TABLE_BYTES_PER_ELEM[emb_fmt]) + 8 * T + 2 * T * Hd * e + Hd * e,
+            # residual-add + RMSNorm + Q8 row scale + int8 row
+            "rms_q8": 4 * T * Hd * e + Hd * e + T * Hd + 4 * T}
 
 
 def main() -> int:
@@ -124,6 +130,12 @@ def main() -> int:
     kw = randn((cfg.head_dim,), 1.0, 0.1) if cfg.qk_norm else None
     silu_sets = [(randn((T, 2 * I)), torch.empty(T, I, dtype=tdt, device=dev))
                  for _ in range(nsets(nbytes["silu"]))] if "silu" in only else []
+    q8_sets = [(randn((T, Hd)), randn((T, Hd)), torch.empty(T, Hd, dtype=tdt, device=dev),
+                torch.empty(T, dtype=torch.float32, device=dev), torch.empty(T, Hd, dtype=torch.int8, device=dev))
+               for _ in range(nsets(nbytes["rms_q8"]))] if "rms_q8" in only else []
+    er_sets = [(torch.randint(0, V, (T,), generator=g, device=dev), torch.empty(T, Hd, dtype=tdt, device=dev),
+                torch.empty(T, Hd, dtype=tdt, device=dev)) for _ in range(nsets(nbytes["emb_rms"]))] \
+        if "emb_rms" in only else []
     copy_pair = None
     if "copy" in only:  # 1 GiB plain copy: the attainable-bandwidth and traffic-counter reference
         copy_pair = (torch.ones(1 << 28, dtype=torch.int32, device=dev),
@@ -154,10 +166,28 @@ def main() -> int:
         gu, out = silu_sets[i % len(silu_sets)]
         ops.silu_and_mul(gu, out=out)
 
+    def run_rms_q8(i):
+        x, r, out, sc, q = q8_sets[i % len(q8_sets)]
+        ops._check(ops.lib().nvf_rms_norm_q8(x.data_ptr(), r.data_ptr(), gamma.data_ptr(), out.data_ptr(),
+                                             sc.data_ptr(), q.data_ptr(), T, Hd, cfg.eps, ops._dt(x), ops._stream()),
+                   "rms_norm_q8")
+
+    def run_emb_rms(i):
+        ids, res, out = er_sets[i % len(er_sets)]
+        fmt = {"q8_0": ops.EMB_Q8_0, "q8_0_blocks": ops.EMB_Q8_0_BLOCKS, "q4_k": ops.EMB_Q4_K,
+               "q5_k": ops.EMB_Q5_K, "q6_k": ops.EMB_Q6_K}[emb_fmt]
+        tab = w8 if emb_fmt == "q8_0" else blocks
+        sc = ws if emb_fmt == "q8_0" else None
+        ops._check(ops.lib().nvf_embedding_rms_norm(ids.data_ptr(), fmt, tab.data_ptr(),
+                                                    sc.data_ptr() if sc is not None else None, T, Hd, V,
+                                                    gamma.data_ptr(), res.data_ptr(), out.data_ptr(), cfg.eps,
+                                                    ops._dt(out), ops._stream()), "embedding_rms_norm")
+
     def run_copy(i):
         ops.stream_copy(copy_pair[1], copy_pair[0])
 
-    table = [("emb", run_emb), ("rms", run_rms), ("rope", run_rope), ("silu", run_silu), ("copy", run_copy)]
+    table = [("emb", run_emb), ("rms", run_rms), ("rope", run_rope), ("silu", run_silu), ("emb_rms", run_emb_rms),
+             ("rms_q8", run_rms_q8), ("copy", run_copy)]
     active = [(n, f) for n, f in table if n in only]
 
     for i in range(args.warmup):
@@ -195,7 +225,7 @@ def main() -> int:
     a.record(stream)
     for i in range(args.steps):
         for n, f in active:
-            if n != "copy":
+            if n in ("emb", "rms", "rope", "silu"):
                 f(args.warmup + i)
     b.record(stream)
     torch.cuda.synchronize()
@@ -234,7 +264,8 @@ def main() -> int:
                    "tokens": T, "hidden": Hd, "intermediate": I, "vocab": V, "q_heads": cfg.q_heads,
                    "kv_heads": cfg.kv_heads, "head_dim": cfg.head_dim, "value_is": "tokens / GPU time of one step (HIP events around all timed steps)",
                    "step_us": round(step_us, 2)},
-        "ops": {k: v for k, v in res_ops.items() if k != "copy"},
+        "ops": {k: v for k, v in res_ops.items() if k in ("emb", "rms", "rope", "silu")},
+        "fused_ops": {k: v for k, v in res_ops.items() if k in ("emb_rms", "rms_q8")} or None,
         "attainable": ({"kernel": "nvf_stream_copy (1 GiB, 16 B non-temporal loads/stores)",
                         "GB_s": res_ops["copy"]["GB_s"],
                         "frac_of_peak": round(res_ops["copy"]["GB_s"] / HBM_PEAK_GBS, 4)} if "copy" in res_ops else None),

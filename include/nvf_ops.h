@@ -41,6 +41,15 @@ enum nvf_qk_layout { NVF_QK_LAYOUT_GGML = 0, NVF_QK_LAYOUT_HIP_LEGACY = 1 };
 /* K-quant kinds, the GGML type ids the reference passes (src/model.cpp:163). */
 enum nvf_qk_kind { NVF_Q4_K = 12, NVF_Q5_K = 13, NVF_Q6_K = 14 };
 
+/* Table formats of the fused embedding entry point. */
+enum nvf_emb_format {
+  NVF_EMB_Q8_0 = 0,        /* split planes: table = int8 [V*H], scales = fp16 [V*H/32] */
+  NVF_EMB_Q8_0_BLOCKS = 1, /* 34-byte GGUF blocks */
+  NVF_EMB_Q4_K = 12,       /* GGML nibble order */
+  NVF_EMB_Q5_K = 13,
+  NVF_EMB_Q6_K = 14
+};
+
 enum nvf_status {
   NVF_OK = 0,
   NVF_ERR_INVALID = -1, /* bad size, dtype, kind, layout or NULL pointer */
@@ -91,6 +100,16 @@ int nvf_rms_norm_add(const void* x, void* residual, const void* weight, void* ou
 int nvf_rms_norm(const void* x, const void* weight, void* out, int64_t rows, int64_t hidden, float eps, int dtype,
                  void* stream);
 
+/* RMSNorm (residual NULL) or residual-add + RMSNorm (residual given) that also
+ * writes the Q8_0 GEMM's activation quantizer outputs, fused: row_scale[r] =
+ * 127 / max|out[r,:]| (0 when that max <= 1e-8) -- the reference computes it
+ * in a separate pass, q8_row_scale_kernel (src/hip_ops.hip:205-217, called by
+ * hip_matmul_q8 :639-686) -- and, when q_out is given, the int8 row
+ * q = (int8)clamp(out * row_scale, +-127) (truncation, :244-245).  out may be
+ * NULL when q_out is given.  row_scale: fp32 [rows]; q_out: int8 [rows, hidden]. */
+int nvf_rms_norm_q8(const void* x, void* residual, const void* weight, void* out, float* row_scale, int8_t* q_out,
+                    int64_t rows, int64_t hidden, float eps, int dtype, void* stream);
+
 /* SiLU(gate) * up over gate_up [rows, 2*inter] -> out [rows, inter]
  * (replaces hip_silu_and_mul, hip_ops.hpp:17). */
 int nvf_silu_and_mul(const void* gate_up, void* out, int64_t rows, int64_t inter, int dtype, void* stream);
@@ -126,6 +145,16 @@ int nvf_embedding_qk(const int64_t* ids, const uint8_t* wq, int64_t tokens, int6
  * (replaces hip_embedding / hip_embedding_u16, hip_ops.hpp:30-31). */
 int nvf_embedding(const int64_t* ids, const void* table, int64_t tokens, int64_t hidden, int64_t vocab,
                   int table_dtype, void* out, int out_dtype, void* stream);
+
+/* Layer-0 embedding gather fused with residual-add + RMSNorm: the reference
+ * gathers into `hidden` (src/model.cpp:756) and then calls
+ * hip_rms_norm_add(hidden, residual, input_layernorm, norm) on its zero-filled
+ * residual (:762).  Here residual <- emb + 0 and out <- RMSNorm(residual) * weight
+ * are written directly; the gathered row never goes to memory.  residual, out
+ * and weight in `dtype`; hidden <= 16 * 64 * (16 / element size). */
+int nvf_embedding_rms_norm(const int64_t* ids, int format, const void* table, const void* scales, int64_t tokens,
+                           int64_t hidden, int64_t vocab, const void* weight, void* residual, void* out, float eps,
+                           int dtype, void* stream);
 
 /* Host helper: inv_freq[i] = (float)(1 / theta^(2i/head_dim)) in double, the
  * table Qwen3Model builds in its constructor (src/model.cpp:416-420).

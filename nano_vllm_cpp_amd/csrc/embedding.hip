@@ -552,6 +552,117 @@ static bool launch_staged(const int64_t* ids, const uint8_t* table, TO* out, int
 }
 
 // ---------------------------------------------------------------------------
+// Layer-0 embedding + residual-add + RMSNorm in one pass (src/model.cpp:756
+// then :762: the residual buffer is zero-filled, so residual = emb + 0 and
+// out = RMSNorm(residual) * w).  The embedding row never exists in HBM: the
+// wave gathers it into VGPRs, stores the residual, reduces the sum of squares
+// with DPP and stores the normalised row -- table rows + 2 row writes instead
+// of table rows + 5 row passes.  U chunks of N per lane; long rows are split
+// over 4 waves.
+// ---------------------------------------------------------------------------
+template <typename T, typename Src, int U, int WPR>
+__global__ __launch_bounds__(kEmbThreads) void embed_rms_kernel(const int64_t* __restrict__ ids, Src src,
+                                                                const T* __restrict__ w, T* __restrict__ residual,
+                                                                T* __restrict__ out, int64_t tokens, int hidden,
+                                                                int64_t vocab, float eps) {
+  constexpr int N = Pack<T>::N;
+  __shared__ float partial[kEmbWaves];
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x / kWave));
+  const int part = wave % WPR;
+  const int64_t t = (int64_t)blockIdx.x * (kEmbWaves / WPR) + wave / WPR;
+  const bool live = t < tokens;  // no early return: the row's waves meet at a barrier
+  const int nch = hidden / N;
+  const int64_t id = live ? ids[t] : 0;
+  const bool bad = bad_id(id, vocab);
+  const int64_t row0 = (bad ? 0 : id) * hidden;  // a bad id reads row 0, stores NaN
+  typename Src::Raw raw[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int c = (u * WPR + part) * kWave + lane;
+    if (live && c < nch) raw[u] = src.load(row0 + (int64_t)c * N);
+  }
+  u32x4 wa[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int c = (u * WPR + part) * kWave + lane;
+    if (live && c < nch) wa[u] = ld16(w + (int64_t)c * N);
+  }
+  float v[U][N];
+  float ss = 0.f;
+  T* rrow = residual + (live ? t : 0) * hidden;
+  T* orow = out + (live ? t : 0) * hidden;
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int c = (u * WPR + part) * kWave + lane;
+    if (live && c < nch) {
+      src.decode(raw[u], v[u]);
+#pragma unroll
+      for (int j = 0; j < N; ++j) v[u][j] = (bad ? __builtin_nanf("") : v[u][j]) + 0.0f;  // x + the zero residual
+      const u32x4 stored = Pack<T>::pack(v[u]);
+      st16_nt(rrow + (int64_t)c * N, stored);
+      Pack<T>::unpack(stored, v[u]);  // the norm sees the stored residual
+#pragma unroll
+      for (int j = 0; j < N; ++j) ss += v[u][j] * v[u][j];
+    }
+  }
+  ss = wave_sum(ss);
+  if constexpr (WPR > 1) {
+    if (lane == 0) partial[wave] = ss;
+    __syncthreads();
+    ss = 0.f;
+#pragma unroll
+    for (int k = 0; k < WPR; ++k) ss += partial[(wave / WPR) * WPR + k];
+  }
+  const float inv = rsqrtf(ss / (float)hidden + eps);
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int c = (u * WPR + part) * kWave + lane;
+    if (live && c < nch) {
+      float g[N], o[N];
+      Pack<T>::unpack(wa[u], g);
+#pragma unroll
+      for (int j = 0; j < N; ++j) o[j] = v[u][j] * inv * g[j];
+      st16_nt(orow + (int64_t)c * N, Pack<T>::pack(o));
+    }
+  }
+}
+
+// Rows of >= 256 chunks are split over 4 waves (LDS combine of the partial
+// sums), as in the RMSNorm kernel; shorter rows keep one wave.
+template <typename T, typename Src>
+static bool launch_embed_rms(const int64_t* ids, const Src& src, const T* w, T* residual, T* out, int64_t tokens,
+                             int64_t hidden, int64_t vocab, float eps, hipStream_t st) {
+  constexpr int N = Pack<T>::N;
+  const int64_t nch = hidden / N;
+  const int wpr = nch >= 4 * kWave ? 4 : 1;
+  const int64_t per_lane = (nch + wpr * kWave - 1) / (wpr * kWave);
+  if (per_lane < 1 || per_lane > 16) return false;
+  const dim3 grid((unsigned)((tokens + kEmbWaves / wpr - 1) / (kEmbWaves / wpr)));
+  const int h = (int)hidden;
+#define NVF_ER_LAUNCH(UU, W) \
+  embed_rms_kernel<T, Src, UU, W><<<grid, kEmbThreads, 0, st>>>(ids, src, w, residual, out, tokens, h, vocab, eps)
+  if (wpr == 1) {
+    switch (per_lane) {
+#define NVF_ER_CASE(UU) case UU: NVF_ER_LAUNCH(UU, 1); break;
+      NVF_ER_CASE(1) NVF_ER_CASE(2) NVF_ER_CASE(3) NVF_ER_CASE(4)
+#undef NVF_ER_CASE
+      default: return false;
+    }
+  } else {
+    switch (per_lane) {
+#define NVF_ER_CASE(UU) case UU: NVF_ER_LAUNCH(UU, 4); break;
+      NVF_ER_CASE(1) NVF_ER_CASE(2) NVF_ER_CASE(3) NVF_ER_CASE(4) NVF_ER_CASE(5) NVF_ER_CASE(6) NVF_ER_CASE(7)
+      NVF_ER_CASE(8) NVF_ER_CASE(9) NVF_ER_CASE(10) NVF_ER_CASE(11) NVF_ER_CASE(12) NVF_ER_CASE(13) NVF_ER_CASE(14)
+      NVF_ER_CASE(15) NVF_ER_CASE(16)
+#undef NVF_ER_CASE
+    }
+  }
+#undef NVF_ER_LAUNCH
+  return true;
+}
+
+// ---------------------------------------------------------------------------
 // Generic K-quant element decode (hidden not a multiple of 256).
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ float fp16_at(const uint8_t* p) {
@@ -807,6 +918,52 @@ extern "C" int nvf_embedding(const int64_t* ids, const void* table, int64_t toke
                      NVF_DISPATCH_DTYPE(out_dtype, TO,
                                         s = (launch_table<TI, TO>(ids, table, tokens, hidden, vocab, out, st))));
   return s;
+}
+
+extern "C" int nvf_embedding_rms_norm(const int64_t* ids, int format, const void* table, const void* scales,
+                                      int64_t tokens, int64_t hidden, int64_t vocab, const void* weight,
+                                      void* residual, void* out, float eps, int dtype, void* stream) {
+  const int c = check_common("nvf_embedding_rms_norm", ids, table, out, tokens, hidden, dtype);
+  if (c) return c < 0 ? c : NVF_OK;
+  if (!weight || !residual) return fail(NVF_ERR_INVALID, "nvf_embedding_rms_norm: NULL weight or residual");
+  if (format == NVF_EMB_Q8_0 && !scales) return fail(NVF_ERR_INVALID, "nvf_embedding_rms_norm: NULL scale plane");
+  const int64_t blk = format == NVF_EMB_Q8_0 || format == NVF_EMB_Q8_0_BLOCKS ? 32 : 256;
+  if ((format != NVF_EMB_Q8_0 && format != NVF_EMB_Q8_0_BLOCKS && format != NVF_EMB_Q4_K &&
+       format != NVF_EMB_Q5_K && format != NVF_EMB_Q6_K) ||
+      hidden % blk != 0 || hidden > INT32_MAX)
+    return fail(NVF_ERR_INVALID, "nvf_embedding_rms_norm: format %d needs hidden %% %lld == 0 (got %lld)", format,
+                (long long)blk, (long long)hidden);
+  const uint8_t* tb = static_cast<const uint8_t*>(table);
+  const bool aligned = aligned16(weight) && aligned16(residual) && aligned16(out) &&
+                       (format == NVF_EMB_Q8_0 ? ((reinterpret_cast<uintptr_t>(tb) & 7u) == 0 &&
+                                                 (reinterpret_cast<uintptr_t>(scales) & 1u) == 0)
+                        : format == NVF_EMB_Q8_0_BLOCKS || format == NVF_EMB_Q6_K
+                            ? (reinterpret_cast<uintptr_t>(tb) & 3u) == 0
+                            : aligned16(tb));
+  if (!aligned) return fail(NVF_ERR_INVALID, "nvf_embedding_rms_norm: misaligned pointer");
+  bool ok = false;
+  hipStream_t st = as_stream(stream);
+  NVF_DISPATCH_DTYPE(dtype, T, {
+    constexpr int N = Pack<T>::N;
+    const T* wp = static_cast<const T*>(weight);
+    T* rp = static_cast<T*>(residual);
+    T* op = static_cast<T*>(out);
+    if (format == NVF_EMB_Q8_0)
+      ok = launch_embed_rms(ids, Q8Split<N>{tb, static_cast<const uint16_t*>(scales)}, wp, rp, op, tokens, hidden,
+                            vocab, eps, st);
+    else if (format == NVF_EMB_Q8_0_BLOCKS)
+      ok = launch_embed_rms(ids, Q8Blocks<N>{tb}, wp, rp, op, tokens, hidden, vocab, eps, st);
+    else if (format == NVF_EMB_Q4_K)
+      ok = launch_embed_rms(ids, Q4K<N, NVF_QK_LAYOUT_GGML>{tb}, wp, rp, op, tokens, hidden, vocab, eps, st);
+    else if (format == NVF_EMB_Q5_K)
+      ok = launch_embed_rms(ids, Q5K<N>{tb}, wp, rp, op, tokens, hidden, vocab, eps, st);
+    else
+      ok = launch_embed_rms(ids, Q6K<N>{tb}, wp, rp, op, tokens, hidden, vocab, eps, st);
+  });
+  if (!ok)
+    return fail(NVF_ERR_INVALID, "nvf_embedding_rms_norm: hidden %lld exceeds the fused row (4 x 16 x 64 chunks)",
+                (long long)hidden);
+  return launch_status("embedding_rms_norm");
 }
 
 // Drop-ins: include/nanovllm/hip_ops.hpp:30-33 / src/hip_ops.hip:746-786.

@@ -139,11 +139,38 @@ __device__ __forceinline__ float group_sum(float v) {
   return v;
 }
 
+// Max over aligned groups of G lanes, same lane pattern as group_sum.
+template <int G>
+__device__ __forceinline__ float group_max(float v) {
+  static_assert(G == 1 || G == 2 || G == 4 || G == 8 || G == 16 || G == 32, "group size");
+  if constexpr (G >= 2) v = fmaxf(v, dpp_mov<0xb1>(v));
+  if constexpr (G >= 4) v = fmaxf(v, dpp_mov<0x4e>(v));
+  if constexpr (G >= 8) v = fmaxf(v, dpp_mov<0x141>(v));
+  if constexpr (G >= 16) v = fmaxf(v, dpp_mov<0x140>(v));
+  if constexpr (G >= 32)
+    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401f)));
+  return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+  v = group_max<32>(v);
+  return fmaxf(__builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0)),
+               __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32)));
+}
+
 // Sum over the full wave; wave-uniform result.  EXEC must be full.
 __device__ __forceinline__ float wave_sum(float v) {
   v = group_sum<32>(v);
   return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0)) +
          __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32));
+}
+
+// Q8 activation quantizer of the reference's INT8 GEMM path: per-row scale
+// 127 / max|x| (0 for an all-~zero row) and q = (int8)clamp(x * scale, +-127)
+// with C truncation (src/hip_ops.hip:205-217, :244-245).
+__device__ __forceinline__ float q8_row_scale(float max_abs) { return max_abs > 1e-8f ? 127.0f / max_abs : 0.0f; }
+__device__ __forceinline__ int q8_quantize(float v, float scale) {
+  return (int)(int8_t)fminf(127.0f, fmaxf(-127.0f, v * scale));
 }
 
 // ---------------------------------------------------------------------------

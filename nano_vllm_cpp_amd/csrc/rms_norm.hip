@@ -15,6 +15,12 @@
 // (i * WPR + w) * 64 + l: each load/store instruction of a wave covers 1 KiB of
 // contiguous row.  At Qwen2.5-7B prefill shape 4 waves per row measured ~77%
 // of the 8 TB/s HBM peak against ~63% for one wave per row.
+//
+// nvf_rms_norm_q8 also emits what the reference's INT8 GEMM path computes in a
+// separate pass over the normalised row (q8_row_scale_kernel,
+// src/hip_ops.hip:205-217): the per-row scale 127 / max|out| from a DPP + LDS
+// max reduction of the row already in registers, and optionally the int8 row
+// its GEMM forms on the fly (:244-245).
 #include "nvf_device.hpp"
 #include "nvf_host.hpp"
 
@@ -24,12 +30,14 @@ constexpr int kNormThreads = 256;
 constexpr int kNormWaves = kNormThreads / kWave;
 constexpr int kNormMaxVpl = 16;  // 16 x 4 waves x 64 lanes x 16 B = a 64 KiB row in registers
 
-template <typename T, int VPL, int WPR, bool ADD>
+template <typename T, int VPL, int WPR, bool ADD, bool Q8>
 __global__ __launch_bounds__(kNormThreads) void rms_norm_vec_kernel(const T* x, T* residual, const T* __restrict__ w,
-                                                                    T* out, int64_t rows, int hidden, float eps) {
+                                                                    T* out, int64_t rows, int hidden, float eps,
+                                                                    float* row_scale, int8_t* q_out) {
   constexpr int N = Pack<T>::N;
   constexpr int RPB = kNormWaves / WPR;  // rows per workgroup
   __shared__ float partial[kNormWaves];
+  __shared__ float partial_max[kNormWaves];
   const int wave = threadIdx.x / kWave, lane = threadIdx.x & (kWave - 1);
   const int sub = wave % WPR;
   const int64_t row = (int64_t)blockIdx.x * RPB + wave / WPR;
@@ -81,6 +89,7 @@ __global__ __launch_bounds__(kNormThreads) void rms_norm_vec_kernel(const T* x, 
   }
   const float inv = rsqrtf(ss / (float)hidden + eps);
 
+  float mx = 0.f;  // max |out| as stored, for the Q8 row scale
 #pragma unroll
   for (int i = 0; i < VPL; ++i) {
     const int c = (i * WPR + sub) * kWave + lane;
@@ -89,16 +98,58 @@ __global__ __launch_bounds__(kNormThreads) void rms_norm_vec_kernel(const T* x, 
       Pack<T>::unpack(wa[i], g);
 #pragma unroll
       for (int j = 0; j < N; ++j) o[j] = v[i][j] * inv * g[j];
-      st16_nt(orow + c * N, Pack<T>::pack(o));
+      const u32x4 stored = Pack<T>::pack(o);
+      if (out) st16_nt(orow + c * N, stored);
+      if constexpr (Q8) {
+        Pack<T>::unpack(stored, v[i]);  // keep the stored values for the quantizer
+#pragma unroll
+        for (int j = 0; j < N; ++j) mx = fmaxf(mx, fabsf(v[i][j]));
+      }
+    }
+  }
+  if constexpr (Q8) {
+    mx = wave_max(mx);
+    if constexpr (WPR > 1) {
+      if (lane == 0) partial_max[wave] = mx;
+      __syncthreads();
+      mx = 0.f;
+#pragma unroll
+      for (int k = 0; k < WPR; ++k) mx = fmaxf(mx, partial_max[(wave / WPR) * WPR + k]);
+    }
+    const float scale = q8_row_scale(mx);
+    if (active && sub == 0 && lane == 0) row_scale[row] = scale;
+    if (q_out) {
+      int8_t* qrow = q_out + off;
+#pragma unroll
+      for (int i = 0; i < VPL; ++i) {
+        const int c = (i * WPR + sub) * kWave + lane;
+        if (active && c < nvec) {
+          uint32_t pk[N / 4];
+#pragma unroll
+          for (int w4 = 0; w4 < N / 4; ++w4) {
+            uint32_t b = 0;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) b |= ((uint32_t)q8_quantize(v[i][4 * w4 + k], scale) & 0xffu) << (8 * k);
+            pk[w4] = b;
+          }
+          if constexpr (N == 8) {
+            *reinterpret_cast<uint2*>(qrow + c * N) = make_uint2(pk[0], pk[1]);
+          } else {
+            *reinterpret_cast<uint32_t*>(qrow + c * N) = pk[0];
+          }
+        }
+      }
     }
   }
 }
 
 // Any hidden / alignment: one wave per row, scalar two-pass (the second pass
-// re-reads the row this lane wrote, an L2 hit).
-template <typename T, bool ADD>
+// re-reads the row this lane wrote, an L2 hit); Q8 adds a third pass over the
+// stored output for the int8 row.
+template <typename T, bool ADD, bool Q8>
 __global__ __launch_bounds__(kNormThreads) void rms_norm_generic_kernel(const T* x, T* residual, const T* w, T* out,
-                                                                        int64_t rows, int hidden, float eps) {
+                                                                        int64_t rows, int hidden, float eps,
+                                                                        float* row_scale, int8_t* q_out) {
   const int lane = threadIdx.x & (kWave - 1);
   const int64_t row = (int64_t)blockIdx.x * kNormWaves + (threadIdx.x / kWave);
   if (row >= rows) return;
@@ -115,22 +166,37 @@ __global__ __launch_bounds__(kNormThreads) void rms_norm_generic_kernel(const T*
   }
   ss = wave_sum(ss);
   const float inv = rsqrtf(ss / (float)hidden + eps);
+  float mx = 0.f;
   for (int c = lane; c < hidden; c += kWave) {
     const float v = ADD ? to_f32(residual[off + c]) : to_f32(x[off + c]);
-    out[off + c] = from_f32<T>(v * inv * to_f32(w[c]));
+    const T o = from_f32<T>(v * inv * to_f32(w[c]));
+    if (out) out[off + c] = o;
+    mx = fmaxf(mx, fabsf(to_f32(o)));
+  }
+  if constexpr (Q8) {
+    const float scale = q8_row_scale(wave_max(mx));
+    if (lane == 0) row_scale[row] = scale;
+    if (q_out) {
+      for (int c = lane; c < hidden; c += kWave) {  // recompute: out may be absent
+        const float v = ADD ? to_f32(residual[off + c]) : to_f32(x[off + c]);
+        const T o = from_f32<T>(v * inv * to_f32(w[c]));
+        q_out[off + c] = (int8_t)q8_quantize(to_f32(o), scale);
+      }
+    }
   }
 }
 
-template <typename T, bool ADD>
+template <typename T, bool ADD, bool Q8>
 static int launch_rms(const void* x, void* residual, const void* w, void* out, int64_t rows, int64_t hidden,
-                      float eps, hipStream_t st) {
+                      float eps, float* row_scale, int8_t* q_out, hipStream_t st) {
   constexpr int N = Pack<T>::N;
   const int64_t nvec = hidden / N;
   // waves per row: 4 once a row has >= 256 vectors, else fewer, so lanes stay busy
   const int wpr = nvec >= 4 * kWave ? 4 : (nvec >= 2 * kWave ? 2 : 1);
   const int vpl = (int)((nvec + (int64_t)wpr * kWave - 1) / ((int64_t)wpr * kWave));
   const bool vec_ok = hidden % N == 0 && vpl >= 1 && vpl <= (wpr == 4 ? kNormMaxVpl : 2) && aligned16(x) &&
-                      aligned16(w) && aligned16(out) && (!ADD || aligned16(residual));
+                      aligned16(w) && (!out || aligned16(out)) && (!ADD || aligned16(residual)) &&
+                      (!q_out || (reinterpret_cast<uintptr_t>(q_out) & (N - 1)) == 0);
   const dim3 block(kNormThreads);
   const T* xp = static_cast<const T*>(x);
   T* rp = static_cast<T*>(residual);
@@ -139,12 +205,13 @@ static int launch_rms(const void* x, void* residual, const void* w, void* out, i
   const int h = (int)hidden;
   if (!vec_ok) {
     const dim3 grid((unsigned)((rows + kNormWaves - 1) / kNormWaves));
-    rms_norm_generic_kernel<T, ADD><<<grid, block, 0, st>>>(xp, rp, wp, op, rows, h, eps);
+    rms_norm_generic_kernel<T, ADD, Q8><<<grid, block, 0, st>>>(xp, rp, wp, op, rows, h, eps, row_scale, q_out);
     return launch_status("rms_norm(generic)");
   }
   const int rpb = kNormWaves / wpr;
   const dim3 grid((unsigned)((rows + rpb - 1) / rpb));
-#define NVF_RMS_LAUNCH(V, W) rms_norm_vec_kernel<T, V, W, ADD><<<grid, block, 0, st>>>(xp, rp, wp, op, rows, h, eps)
+#define NVF_RMS_LAUNCH(V, W) \
+  rms_norm_vec_kernel<T, V, W, ADD, Q8><<<grid, block, 0, st>>>(xp, rp, wp, op, rows, h, eps, row_scale, q_out)
   if (wpr == 1) {
     if (vpl == 1) NVF_RMS_LAUNCH(1, 1); else NVF_RMS_LAUNCH(2, 1);
   } else if (wpr == 2) {
@@ -163,18 +230,26 @@ static int launch_rms(const void* x, void* residual, const void* w, void* out, i
 }
 
 static int rms_entry(const void* x, void* residual, const void* w, void* out, int64_t rows, int64_t hidden,
-                     float eps, int dtype, void* stream, bool add) {
-  const char* name = add ? "nvf_rms_norm_add" : "nvf_rms_norm";
+                     float eps, int dtype, void* stream, bool add, float* row_scale = nullptr,
+                     int8_t* q_out = nullptr) {
+  const bool q8 = row_scale != nullptr;
+  const char* name = q8 ? "nvf_rms_norm_q8" : (add ? "nvf_rms_norm_add" : "nvf_rms_norm");
   if (!dtype_ok(dtype)) return fail(NVF_ERR_INVALID, "%s: bad dtype %d", name, dtype);
   if (rows < 0 || hidden < 0 || hidden > INT32_MAX)
     return fail(NVF_ERR_INVALID, "%s: bad shape rows=%lld hidden=%lld", name, (long long)rows, (long long)hidden);
   if (rows == 0 || hidden == 0) return NVF_OK;
-  if (!x || !w || !out || (add && !residual)) return fail(NVF_ERR_INVALID, "%s: NULL pointer", name);
+  if (!x || !w || (!out && !q8) || (add && !residual)) return fail(NVF_ERR_INVALID, "%s: NULL pointer", name);
+  if (q8 && !out && !q_out) return fail(NVF_ERR_INVALID, "%s: neither out nor q_out given", name);
+  if ((int64_t)((rows + kNormWaves - 1) / kNormWaves) > INT32_MAX)
+    return fail(NVF_ERR_INVALID, "%s: %lld rows exceed one launch", name, (long long)rows);
   int st = NVF_OK;
-  if (add)
-    NVF_DISPATCH_DTYPE(dtype, T, st = (launch_rms<T, true>(x, residual, w, out, rows, hidden, eps, as_stream(stream))));
-  else
-    NVF_DISPATCH_DTYPE(dtype, T, st = (launch_rms<T, false>(x, nullptr, w, out, rows, hidden, eps, as_stream(stream))));
+  const hipStream_t s = as_stream(stream);
+#define NVF_RMS_GO(A, Q) NVF_DISPATCH_DTYPE(dtype, T, st = (launch_rms<T, A, Q>(x, residual, w, out, rows, hidden, eps, row_scale, q_out, s)))
+  if (add && q8) NVF_RMS_GO(true, true);
+  else if (add) NVF_RMS_GO(true, false);
+  else if (q8) NVF_RMS_GO(false, true);
+  else NVF_RMS_GO(false, false);
+#undef NVF_RMS_GO
   return st;
 }
 
@@ -188,6 +263,13 @@ extern "C" int nvf_rms_norm_add(const void* x, void* residual, const void* weigh
 extern "C" int nvf_rms_norm(const void* x, const void* weight, void* out, int64_t rows, int64_t hidden, float eps,
                             int dtype, void* stream) {
   return nvf::rms_entry(x, nullptr, weight, out, rows, hidden, eps, dtype, stream, false);
+}
+
+extern "C" int nvf_rms_norm_q8(const void* x, void* residual, const void* weight, void* out, float* row_scale,
+                               int8_t* q_out, int64_t rows, int64_t hidden, float eps, int dtype, void* stream) {
+  if (!row_scale) return nvf::fail(NVF_ERR_INVALID, "nvf_rms_norm_q8: NULL row_scale");
+  return nvf::rms_entry(x, residual, weight, out, rows, hidden, eps, dtype, stream, residual != nullptr, row_scale,
+                        q_out);
 }
 
 // Drop-in: include/nanovllm/hip_ops.hpp:14 / src/hip_ops.hip:694-698.

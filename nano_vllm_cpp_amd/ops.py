@@ -19,6 +19,7 @@ import torch
 LIB_PATH = Path(__file__).resolve().parent / "lib" / "libnvf_ops.so"
 
 F32, F16, BF16 = 0, 1, 2
+EMB_Q8_0, EMB_Q8_0_BLOCKS, EMB_Q4_K, EMB_Q5_K, EMB_Q6_K = 0, 1, 12, 13, 14
 QK_LAYOUT_GGML, QK_LAYOUT_HIP_LEGACY = 0, 1
 Q4_K, Q5_K, Q6_K = 12, 13, 14
 
@@ -38,12 +39,14 @@ SIGNATURES: dict[str, tuple] = {
     "hip_embedding_qk": (None, [_vp, _vp, _i32, _i32, _vp, _i32]),
     "nvf_rms_norm_add": (_i32, [_vp, _vp, _vp, _vp, _i64, _i64, _f32, _i32, _vp]),
     "nvf_rms_norm": (_i32, [_vp, _vp, _vp, _i64, _i64, _f32, _i32, _vp]),
+    "nvf_rms_norm_q8": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _f32, _i32, _vp]),
     "nvf_silu_and_mul": (_i32, [_vp, _vp, _i64, _i64, _i32, _vp]),
     "nvf_qk_norm_rope": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i32, _i32, _i32, _i64, _i64, _f32, _i32, _vp]),
     "nvf_embedding_q8_0": (_i32, [_vp, _vp, _vp, _i64, _i64, _i64, _vp, _i32, _vp]),
     "nvf_embedding_q8_0_blocks": (_i32, [_vp, _vp, _i64, _i64, _i64, _vp, _i32, _vp]),
     "nvf_embedding_qk": (_i32, [_vp, _vp, _i64, _i64, _i64, _i32, _i32, _vp, _i32, _vp]),
     "nvf_embedding": (_i32, [_vp, _vp, _i64, _i64, _i64, _i32, _vp, _i32, _vp]),
+    "nvf_embedding_rms_norm": (_i32, [_vp, _i32, _vp, _vp, _i64, _i64, _i64, _vp, _vp, _vp, _f32, _i32, _vp]),
     "nvf_rope_inv_freq": (_i32, [_f64, _i32, _vp]),
     "nvf_stream_copy": (_i32, [_vp, _vp, _i64, _vp]),
     "nvf_last_error": (C.c_char_p, []),
@@ -128,6 +131,21 @@ def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float, out: torch.Tenso
     return out
 
 
+def rms_norm_q8(x: torch.Tensor, weight: torch.Tensor, eps: float, residual: torch.Tensor | None = None,
+                want_out: bool = True, want_q: bool = True):
+    """(Residual-add +) RMSNorm that also emits the Q8_0 GEMM's per-row scale
+    127/max|out| and, optionally, the int8 row.  Returns (out | None, row_scale, q | None)."""
+    rows, hidden = x.shape
+    out = torch.empty_like(x) if want_out else None
+    scale = torch.empty(rows, dtype=torch.float32, device=x.device)
+    q = torch.empty((rows, hidden), dtype=torch.int8, device=x.device) if want_q else None
+    _check(lib().nvf_rms_norm_q8(_dev(x, "x"), _dev(residual, "residual") if residual is not None else None,
+                                 _dev(weight, "weight"), _dev(out, "out") if out is not None else None,
+                                 _dev(scale, "row_scale"), _dev(q, "q_out") if q is not None else None, rows, hidden,
+                                 eps, _dt(x), _stream()), "rms_norm_q8")
+    return out, scale, q
+
+
 # ---------------------------------------------------------------------------
 # SwiGLU
 # ---------------------------------------------------------------------------
@@ -207,6 +225,19 @@ def embedding_qk(ids: torch.Tensor, wq: torch.Tensor, hidden: int, kind: int = Q
     _check(lib().nvf_embedding_qk(_dev(ids, "ids"), _dev(wq, "wq"), tokens, hidden, vocab, kind, layout,
                                   _dev(out, "out"), _dt(out), _stream()), "embedding_qk")
     return out
+
+
+def embedding_rms_norm(ids: torch.Tensor, fmt: int, table: torch.Tensor, scales: torch.Tensor | None, hidden: int,
+                       weight: torch.Tensor, eps: float, vocab: int = 0):
+    """Layer-0 embedding + residual-add (onto zeros) + RMSNorm; returns (residual, out) in weight's dtype."""
+    tokens = ids.numel()
+    residual = _out(tokens, hidden, weight.dtype, ids.device)
+    out = torch.empty_like(residual)
+    _check(lib().nvf_embedding_rms_norm(_dev(ids, "ids"), fmt, _dev(table, "table"),
+                                        _dev(scales, "scales") if scales is not None else None, tokens, hidden, vocab,
+                                        _dev(weight, "weight"), _dev(residual, "residual"), _dev(out, "out"), eps,
+                                        _dt(weight), _stream()), "embedding_rms_norm")
+    return residual, out
 
 
 def embedding(ids: torch.Tensor, table: torch.Tensor, vocab: int = 0, out_dtype: torch.dtype | None = None,

@@ -363,3 +363,44 @@ void orc_qk_norm_rope(void* q, void* k, const int64_t* positions, const void* q_
   if (q && q_heads > 0) qk_one(q, positions, q_w, inv_freq, tokens, q_heads, head_dim, q_stride, eps, dtype);
   if (k && kv_heads > 0) qk_one(k, positions, k_w, inv_freq, tokens, kv_heads, head_dim, k_stride, eps, dtype);
 }
+
+/* ---- Q8 activation row scale (for the Q8_0 GEMM) ------------------------ */
+
+/* src/hip_ops.hip:205-217: max |x| over the row, scale = 127 / max or 0. */
+void orc_q8_row_scale(const void* x, float* scale, int64_t rows, int64_t hidden, int dtype) {
+  for (int64_t r = 0; r < rows; ++r) {
+    float mx = 0.0f;
+    for (int64_t i = 0; i < hidden; ++i) mx = fmaxf(mx, fabsf(orc_load(x, r * hidden + i, dtype)));
+    scale[r] = mx > 1e-8f ? 127.0f / mx : 0.0f;
+  }
+}
+
+/* src/hip_ops.hip:244-245: (int8_t)fminf(127, fmaxf(-127, v * as)), a C cast
+ * (truncation toward zero). */
+void orc_q8_quantize(const void* x, const float* scale, int8_t* q, int64_t rows, int64_t hidden, int dtype) {
+  for (int64_t r = 0; r < rows; ++r)
+    for (int64_t i = 0; i < hidden; ++i) {
+      const float v = orc_load(x, r * hidden + i, dtype) * scale[r];
+      q[r * hidden + i] = (int8_t)fminf(127.0f, fmaxf(-127.0f, v));
+    }
+}
+
+/* ---- layer-0 embedding + residual-add + RMSNorm -------------------------- */
+
+void orc_embedding_rms_norm(const int64_t* ids, int format, const void* table, const void* scales, int64_t tokens,
+                            int64_t hidden, const void* w, void* residual, void* out, float eps, int dtype) {
+  float* emb = (float*)malloc(sizeof(float) * (size_t)(tokens * hidden));
+  if (format == 0)
+    orc_embedding_q8_split(ids, (const uint8_t*)table, (const uint16_t*)scales, tokens, hidden, emb, ORC_F32);
+  else
+    orc_embedding_q8_blocks(ids, (const uint8_t*)table, tokens, hidden, emb, ORC_F32);
+  /* the gather's value in the storage dtype, then the layer-0 add onto zeros */
+  void* x = malloc((size_t)(tokens * hidden) * (dtype == ORC_F32 ? 4 : 2));
+  for (int64_t i = 0; i < tokens * hidden; ++i) {
+    orc_store(x, i, emb[i], dtype);
+    orc_store(residual, i, 0.0f, dtype);
+  }
+  orc_rms_norm_add(x, residual, w, out, tokens, hidden, eps, dtype);
+  free(x);
+  free(emb);
+}

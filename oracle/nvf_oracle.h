@@ -29,6 +29,10 @@
  *                              rotate(p) then rotate(-p) identity, composition
  *   SiLU*up .................. silu(0)=0, silu(g)-silu(-g)=g, double-exp
  *                              brute force
+ *   Q8 row scale / quantize .. closed forms (the row maximum maps to +-127,
+ *                              zero rows give scale 0), truncation toward zero
+ *   embedding + layer-0 norm . equal to the composition gather ->
+ *                              rms_norm_add with a zero residual
  */
 #ifndef NVF_ORACLE_H
 #define NVF_ORACLE_H
@@ -76,6 +80,18 @@ void orc_rope(void* data, const int64_t* positions, int64_t tokens, int heads, i
 void orc_qk_norm_rope(void* q, void* k, const int64_t* positions, const void* q_w, const void* k_w,
                       const float* inv_freq, int64_t tokens, int q_heads, int kv_heads, int head_dim,
                       int64_t q_stride, int64_t k_stride, float eps, int dtype);
+
+/* src/hip_ops.hip:205-217 (q8_row_scale_kernel): scale[r] = 127 / max|x[r,:]|,
+ * 0 when the maximum is <= 1e-8; and the int8 values its GEMM forms from them,
+ * src/hip_ops.hip:244-245: q = (int8)min(127, max(-127, x * scale)) (truncation). */
+void orc_q8_row_scale(const void* x, float* scale, int64_t rows, int64_t hidden, int dtype);
+void orc_q8_quantize(const void* x, const float* scale, int8_t* q, int64_t rows, int64_t hidden, int dtype);
+
+/* Layer-0 embedding + residual-add + RMSNorm (src/model.cpp:756 then :762 with
+ * the zero-filled residual): residual = emb + 0, out = RMSNorm(residual) * w.
+ * format: 0 = Q8_0 split planes (table = w8, scales = ws), 1 = Q8_0 blocks. */
+void orc_embedding_rms_norm(const int64_t* ids, int format, const void* table, const void* scales, int64_t tokens,
+                            int64_t hidden, const void* w, void* residual, void* out, float eps, int dtype);
 
 #ifdef __cplusplus
 }

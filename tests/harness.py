@@ -41,6 +41,9 @@ _ORACLE_SIGS = {
     "orc_silu_and_mul": (None, [_vp, _vp, _i64, _i64, _i32]),
     "orc_rope": (None, [_vp, _vp, _i64, _i32, _i32, _i64, _vp, _i32]),
     "orc_qk_norm_rope": (None, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i32, _i32, _i32, _i64, _i64, _f32, _i32]),
+    "orc_q8_row_scale": (None, [_vp, _vp, _i64, _i64, _i32]),
+    "orc_q8_quantize": (None, [_vp, _vp, _vp, _i64, _i64, _i32]),
+    "orc_embedding_rms_norm": (None, [_vp, _i32, _vp, _vp, _i64, _i64, _vp, _vp, _vp, _f32, _i32]),
 }
 
 _cache: dict[str, C.CDLL] = {}

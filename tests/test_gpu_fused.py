@@ -1,0 +1,126 @@
+"""GPU parity for the fusions with the path's neighbours:
+
+* nvf_rms_norm_q8 -- RMSNorm (+ residual add) that also emits the Q8_0 GEMM's
+  activation row scale and int8 row (the reference's q8_row_scale_kernel pass,
+  src/hip_ops.hip:205-217, and its GEMM's quantizer, :244-245);
+* nvf_embedding_rms_norm -- layer-0 gather + residual-add onto zeros + RMSNorm
+  (src/model.cpp:756 then :762).
+
+Bars: the row scale and int8 row bit-exact against the oracle's quantizer
+applied to the kernel's own stored output (the quantizer is exact arithmetic on
+that row); the stored output within the RMSNorm tolerance of the oracle; the
+fused residual bit-exact (emb + 0).
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from nano_vllm_cpp_amd import ops
+from tests import harness as H
+
+pytestmark = pytest.mark.gpu
+
+DTYPES = [H.F32, H.F16, H.BF16]
+DT_IDS = ["f32", "f16", "bf16"]
+
+
+def case(msg: str) -> None:
+    print(f"[case] {msg}", flush=True)
+
+
+@pytest.mark.parametrize("dt", DTYPES, ids=DT_IDS)
+@pytest.mark.parametrize("add", [True, False], ids=["add", "plain"])
+@pytest.mark.parametrize("rows,hidden", [(64, 3584), (33, 896), (5, 999), (7, 4096)])
+def test_rms_norm_q8(gpu, dt, add, rows, hidden):
+    o = H.oracle()
+    r = H.rng(rows * hidden + dt + 7 * add)
+    x, res = H.gen_act(r, (rows, hidden), dt), H.gen_act(r, (rows, hidden), dt)
+    x[1] = H.to_storage(np.zeros(hidden, np.float32), dt)  # an all-zero input row (scale 0 when plain)
+    w = H.gen_act(r, (hidden,), dt, 1.0, 0.1)
+    ref_res, ref_out = res.copy(), np.empty_like(x)
+    if add:
+        o.orc_rms_norm_add(H.ptr(x), H.ptr(ref_res), H.ptr(w), H.ptr(ref_out), rows, hidden, 1e-6, dt)
+    else:
+        o.orc_rms_norm(H.ptr(x), H.ptr(w), H.ptr(ref_out), rows, hidden, 1e-6, dt)
+    d_res = H.to_dev(res, gpu, dt)
+    case(f"rms_norm_q8 add={add} rows={rows} hidden={hidden} dt={dt}")
+    out, scale, q = ops.rms_norm_q8(H.to_dev(x, gpu, dt), H.to_dev(w, gpu, dt), 1e-6, d_res if add else None)
+    got_out, got_scale, got_q = H.to_host(out), scale.cpu().numpy(), q.cpu().numpy()
+    if add:
+        H.assert_bitexact(H.to_host(d_res), ref_res, "residual")
+    H.assert_close(got_out, ref_out, dt, what="out")
+    exp_scale = np.empty(rows, np.float32)
+    o.orc_q8_row_scale(H.ptr(got_out), H.ptr(exp_scale), rows, hidden, dt)
+    H.assert_bitexact(got_scale, exp_scale, "row scale")
+    exp_q = np.empty((rows, hidden), np.int8)
+    o.orc_q8_quantize(H.ptr(got_out), H.ptr(exp_scale), exp_q.ctypes.data, rows, hidden, dt)
+    H.assert_bitexact(got_q, exp_q, "int8 row")
+    if not add:
+        assert got_scale[1] == 0.0 and not got_q[1].any()
+    # the same call without the fp output: identical scale and int8 row
+    d_res2 = H.to_dev(res, gpu, dt)
+    case("rms_norm_q8 without out")
+    none, scale2, q2 = ops.rms_norm_q8(H.to_dev(x, gpu, dt), H.to_dev(w, gpu, dt), 1e-6, d_res2 if add else None,
+                                       want_out=False)
+    assert none is None
+    H.assert_bitexact(scale2.cpu().numpy(), got_scale, "row scale (no out)")
+    H.assert_bitexact(q2.cpu().numpy(), got_q, "int8 row (no out)")
+
+
+def _emb_reference(o, fmt, ids, table, scales, T, Hd, dt):
+    """The gathered rows in the storage dtype (oracle)."""
+    emb = np.empty((T, Hd), H.NP_STORAGE[dt])
+    if fmt == ops.EMB_Q8_0:
+        o.orc_embedding_q8_split(H.ptr(ids), H.ptr(table), H.ptr(scales), T, Hd, H.ptr(emb), dt)
+    elif fmt == ops.EMB_Q8_0_BLOCKS:
+        o.orc_embedding_q8_blocks(H.ptr(ids), H.ptr(table), T, Hd, H.ptr(emb), dt)
+    else:
+        o.orc_embedding_qk(H.ptr(ids), H.ptr(table), T, Hd, fmt, H.GGML, H.ptr(emb), dt)
+    return emb
+
+
+@pytest.mark.parametrize("dt", DTYPES, ids=DT_IDS)
+@pytest.mark.parametrize("fmt", [ops.EMB_Q8_0, ops.EMB_Q8_0_BLOCKS, ops.EMB_Q4_K, ops.EMB_Q5_K, ops.EMB_Q6_K],
+                         ids=["q8_0", "q8_0_blocks", "q4_k", "q5_k", "q6_k"])
+@pytest.mark.parametrize("hidden", [3584, 1024])
+def test_embedding_rms_norm(gpu, dt, fmt, hidden):
+    o = H.oracle()
+    r = H.rng(hidden + fmt * 3 + dt)
+    V, T = 300, 70
+    scales = None
+    if fmt in (ops.EMB_Q8_0, ops.EMB_Q8_0_BLOCKS):
+        w8, ws = H.gen_q8_0(r, V, hidden)
+        table, scales = (w8, ws) if fmt == ops.EMB_Q8_0 else (H.q8_split_to_blocks(w8, ws), None)
+    else:
+        bb, offs = {ops.EMB_Q4_K: (144, (0, 2)), ops.EMB_Q5_K: (176, (0, 2)), ops.EMB_Q6_K: (210, (208,))}[fmt]
+        table = H.gen_raw_blocks(r, V * hidden // 256, bb, offs)
+    ids = r.integers(0, V, T).astype(np.int64)
+    ids[:2] = [V - 1, 0]
+    w = H.gen_act(r, (hidden,), dt, 1.0, 0.1)
+    emb = _emb_reference(o, fmt, ids, table, scales, T, hidden, dt)
+    ref_res = H.to_storage(np.zeros((T, hidden), np.float32), dt)
+    ref_out = np.empty_like(emb)
+    o.orc_rms_norm_add(H.ptr(emb), H.ptr(ref_res), H.ptr(w), H.ptr(ref_out), T, hidden, 1e-6, dt)
+    case(f"embedding_rms_norm fmt={fmt} hidden={hidden} dt={dt}")
+    res, out = ops.embedding_rms_norm(H.to_dev(ids, gpu), fmt, H.to_dev(table, gpu),
+                                      H.to_dev(scales, gpu) if scales is not None else None, hidden,
+                                      H.to_dev(w, gpu, dt), 1e-6, V)
+    H.assert_bitexact(H.to_host(res), ref_res, "fused residual")
+    H.assert_close(H.to_host(out), ref_out, dt, what="fused norm")
+
+
+def test_embedding_rms_norm_bad_ids_and_args(gpu):
+    r = H.rng(5)
+    V, hidden = 40, 512
+    w8, ws = H.gen_q8_0(r, V, hidden)
+    ids = np.array([3, V, -2], np.int64)
+    w = torch.ones(hidden, dtype=torch.float16, device=gpu)
+    case("embedding_rms_norm out-of-range ids")
+    res, out = ops.embedding_rms_norm(H.to_dev(ids, gpu), ops.EMB_Q8_0, H.to_dev(w8, gpu), H.to_dev(ws, gpu), hidden,
+                                      w, 1e-6, V)
+    o = out.float().cpu().numpy()
+    assert np.isfinite(o[0]).all() and np.isnan(o[1:]).all()
+    with pytest.raises(ops.NvfError, match="hidden"):
+        ops.embedding_rms_norm(H.to_dev(ids, gpu), ops.EMB_Q4_K, H.to_dev(w8, gpu), None, 500, w[:500], 1e-6, V)

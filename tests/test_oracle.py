@@ -379,6 +379,54 @@ def test_qk_norm_rope_is_the_composition(o):
 
 
 # ---------------------------------------------------------------------------
+# Q8 activation row scale / quantize, fused layer-0 embedding + norm
+# ---------------------------------------------------------------------------
+def test_q8_row_scale_closed_form(o):
+    x = np.array([[1.0, -4.0, 2.0, 0.5], [0, 0, 0, 0], [1e-9, -1e-9, 0, 0], [3.0, 3.0, -3.0, 1.5]], np.float32)
+    sc = np.empty(4, np.float32)
+    o.orc_q8_row_scale(H.ptr(x), H.ptr(sc), 4, 4, H.F32)
+    assert sc[0] == np.float32(127.0) / np.float32(4.0) and sc[1] == 0 and sc[2] == 0
+    assert sc[3] == np.float32(127.0) / np.float32(3.0)
+    q = np.empty((4, 4), np.int8)
+    o.orc_q8_quantize(H.ptr(x), H.ptr(sc), q.ctypes.data, 4, 4, H.F32)
+    assert list(q[0]) == [31, -127, 63, 15]          # 31.75 -> 31, 63.5 -> 63, 15.875 -> 15 (truncation)
+    assert list(q[1]) == [0, 0, 0, 0]
+    assert abs(int(q[3, 0])) == 127 and q[3, 2] == -127  # the row maximum maps to +-127
+
+
+def test_q8_quantize_bounds_and_truncation(o):
+    r = H.rng(20)
+    x = r.normal(0, 1, (16, 256)).astype(np.float32)
+    sc = np.empty(16, np.float32)
+    q = np.empty((16, 256), np.int8)
+    o.orc_q8_row_scale(H.ptr(x), H.ptr(sc), 16, 256, H.F32)
+    o.orc_q8_quantize(H.ptr(x), H.ptr(sc), q.ctypes.data, 16, 256, H.F32)
+    v = x.astype(np.float32) * sc[:, None]
+    assert np.array_equal(q, np.trunc(np.clip(v, -127, 127)).astype(np.int8))
+    # the row maximum lands on 127, or on 126 when max * (127 / max) rounds just below 127
+    assert np.isin(np.abs(q.astype(np.int32)).max(axis=1), (126, 127)).all()
+
+
+def test_embedding_rms_norm_is_the_composition(o):
+    r = H.rng(21)
+    V, Hd, T = 50, 256, 9
+    w8, ws = H.gen_q8_0(r, V, Hd)
+    ids = r.integers(0, V, T).astype(np.int64)
+    for dt in (H.F32, H.F16, H.BF16):
+        w = H.gen_act(r, (Hd,), dt, 1.0, 0.1)
+        res, out = np.empty((T, Hd), H.NP_STORAGE[dt]), np.empty((T, Hd), H.NP_STORAGE[dt])
+        o.orc_embedding_rms_norm(H.ptr(ids), 0, H.ptr(w8), H.ptr(ws), T, Hd, H.ptr(w), H.ptr(res), H.ptr(out), 1e-6, dt)
+        emb = np.empty((T, Hd), H.NP_STORAGE[dt])
+        o.orc_embedding_q8_split(H.ptr(ids), H.ptr(w8), H.ptr(ws), T, Hd, H.ptr(emb), dt)
+        zero = H.to_storage(np.zeros((T, Hd), np.float32), dt)
+        out2 = np.empty_like(out)
+        o.orc_rms_norm_add(H.ptr(emb), H.ptr(zero), H.ptr(w), H.ptr(out2), T, Hd, 1e-6, dt)
+        assert np.array_equal(res, zero) and np.array_equal(out, out2)
+        # residual = emb + 0: identical to the gather except -0 becomes +0
+        assert np.array_equal(H.from_storage(res, dt), H.from_storage(emb, dt) + 0.0)
+
+
+# ---------------------------------------------------------------------------
 # tolerance helpers themselves
 # ---------------------------------------------------------------------------
 def test_tolerance_rule_rejects_two_ulp():
