@@ -339,7 +339,7 @@ def cpu_baseline(cfg, budget_s: float, H) -> dict:
             break
     total = sum(per.values())
     e = 2 if dt != H.F32 else 4
-    scale = {k_: v * S / cfg.tokens for k_, v in op_bytes(cfg, e).items()}  # bytes of one S-token call
+    scale = {k_: v * S / cfg.tokens for k_, v in op_bytes(cfg, e, "q8_0").items()}  # bytes of one S-token call
     cpu_model = ""
     try:
         for ln in Path("/proc/cpuinfo").read_text().splitlines():

@@ -1,0 +1,33 @@
+"""Host-side legs of bench.py that run without a GPU: the algorithmic byte
+model and the CPU baseline (the oracle timed on a bounded sample)."""
+from __future__ import annotations
+
+import subprocess
+import sys
+
+import pytest
+
+import bench
+from tests import harness as H
+
+
+@pytest.mark.parametrize("fmt", sorted(bench.TABLE_BYTES_PER_ELEM))
+def test_op_bytes_all_formats(fmt):
+    cfg = H.CONFIGS[2]
+    b = bench.op_bytes(cfg, 2, fmt)
+    assert set(b) == {"emb", "rms", "rope", "silu", "emb_rms", "rms_q8"}
+    # the residual-add + RMSNorm moves x, residual in/out and out: 4 rows of fp16
+    assert b["rms"] == 4 * cfg.tokens * cfg.hidden * 2 + cfg.hidden * 2
+    # the fused layer-0 op writes one more row than the bare gather
+    assert b["emb_rms"] - b["emb"] == cfg.tokens * cfg.hidden * 2 + cfg.hidden * 2
+
+
+def test_cpu_baseline_leg():
+    cb = bench.cpu_baseline(H.CONFIGS[2], 0.05, H)
+    assert cb["kind"] == "port" and cb["cores"] == 1 and cb["unit"] == "tokens/s"
+    assert cb["value"] > 0 and set(cb["ops_GB_s"]) == {"emb", "rms", "rope", "silu"}
+
+
+def test_multi_gpu_request_exits_with_message():
+    p = subprocess.run([sys.executable, "bench.py", "--gpus", "2"], capture_output=True, text=True, timeout=120)
+    assert p.returncode == 2 and "one GPU" in p.stdout
