@@ -15,6 +15,10 @@ touched long before the launch, so the 256 MB MALL cannot serve them: the
 figures are HBM figures.  Per-op times come from HIP events on the stream the
 kernels run on; the dominant kernel (SwiGLU) gives the roofline object.
 
+Beside the chain, `q8_gemm` times the Q8_0 GEMM (the reference's hip_matmul_q8) at
+the gate_up projection shape [T, H] x [2I, H]^T on pre-quantized activations, in
+TOP/s against the dense int8 MFMA peak; it does not enter `value`.
+
 The CPU baseline is the C oracle (single thread, -O2) timed on a bounded
 sample of the same workload on this host.
 
@@ -36,6 +40,7 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0
+INT8_PEAK_OPS = 5.0e15  # MI355X dense int8 MFMA
 METRIC = "fused-op HBM GB/s (% of peak) + layer-op tokens/s at Qwen2.5-7B shapes"
 POOL_BYTES = 1 << 30
 
@@ -50,7 +55,7 @@ def parse() -> argparse.Namespace:
     p.add_argument("--emb", default="", choices=["", "q8_0", "q8_0_blocks", "q4_k", "q5_k", "q6_k", "f16"],
                    help="embedding table format (default: the config's)")
     p.add_argument("--only", default="",
-                   help="comma list of ops (default emb,rms,rope,silu,copy); also emb_rms, rms_q8 (fusions)")
+                   help="comma list of ops (default emb,rms,rope,silu,copy,gemm); also emb_rms, rms_q8 (fusions)")
     return p.parse_args()
 
 
@@ -95,7 +100,7 @@ def main() -> int:
     g = torch.Generator(device=dev).manual_seed(cfg.seed)
     emb_fmt = args.emb or cfg.emb
     nbytes = op_bytes(cfg, e, emb_fmt)
-    only = set(filter(None, args.only.split(","))) or {"emb", "rms", "rope", "silu", "copy"}
+    only = set(filter(None, args.only.split(","))) or {"emb", "rms", "rope", "silu", "copy", "gemm"}
 
     def nsets(b: int) -> int:
         return max(2, -(-POOL_BYTES // b))
@@ -136,6 +141,12 @@ def main() -> int:
     er_sets = [(torch.randint(0, V, (T,), generator=g, device=dev), torch.empty(T, Hd, dtype=tdt, device=dev),
                 torch.empty(T, Hd, dtype=tdt, device=dev)) for _ in range(nsets(nbytes["emb_rms"]))] \
         if "emb_rms" in only else []
+    gemm_in = None
+    if "gemm" in only:  # Q8_0 GEMM at the gate_up projection shape: [T, H] x [2I, H]^T
+        gw8 = torch.randint(-127, 128, (2 * I * Hd,), generator=g, device=dev, dtype=torch.int8)
+        gws = torch.empty(2 * I * Hd // 32, device=dev).uniform_(1e-3, 1e-2, generator=g).half().view(torch.int16)
+        gsc, gxq = ops.q8_quantize_rows(randn((T, Hd)))
+        gemm_in = (gxq, gsc, gw8, gws, torch.empty(T, 2 * I, dtype=tdt, device=dev))
     copy_pair = None
     if "copy" in only:  # 1 GiB plain copy: the attainable-bandwidth and traffic-counter reference
         copy_pair = (torch.ones(1 << 28, dtype=torch.int32, device=dev),
@@ -183,11 +194,15 @@ def main() -> int:
                                                     gamma.data_ptr(), res.data_ptr(), out.data_ptr(), cfg.eps,
                                                     ops._dt(out), ops._stream()), "embedding_rms_norm")
 
+    def run_gemm(i):
+        xq_, sc_, w8_, ws_, out_ = gemm_in
+        ops.matmul_q8_0(xq_, sc_, w8_, ws_, 2 * I, out=out_)
+
     def run_copy(i):
         ops.stream_copy(copy_pair[1], copy_pair[0])
 
     table = [("emb", run_emb), ("rms", run_rms), ("rope", run_rope), ("silu", run_silu), ("emb_rms", run_emb_rms),
-             ("rms_q8", run_rms_q8), ("copy", run_copy)]
+             ("rms_q8", run_rms_q8), ("copy", run_copy), ("gemm", run_gemm)]
     active = [(n, f) for n, f in table if n in only]
 
     for i in range(args.warmup):
@@ -208,11 +223,26 @@ def main() -> int:
         b.record(stream)
         b.synchronize()
         t_us = a.elapsed_time(b) * 1e3 / args.steps
-        entry = {"us": round(t_us, 2)}
+        # distribution: an event pair around each launch (a second pass, same rotation)
+        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+               for _ in range(args.steps)]
+        for i, (ea, eb) in enumerate(evs):
+            ea.record(stream)
+            f(args.warmup + i)
+            eb.record(stream)
+        torch.cuda.synchronize()
+        per = np.array([ea.elapsed_time(eb) * 1e3 for ea, eb in evs])
+        entry = {"us": round(t_us, 2), "p10_us": round(float(np.percentile(per, 10)), 2),
+                 "p50_us": round(float(np.percentile(per, 50)), 2),
+                 "p90_us": round(float(np.percentile(per, 90)), 2)}
         if n in nbytes:
             gbs = nbytes[n] / (t_us * 1e-6) / 1e9
             entry.update({"bytes": nbytes[n], "GB_s": round(gbs, 1), "frac_of_peak": round(gbs / HBM_PEAK_GBS, 4),
                           "tokens_per_s": round(T / (t_us * 1e-6), 1)})
+        elif n == "gemm":
+            ops_n = 2.0 * T * (2 * I) * Hd
+            entry.update({"shape": f"m={T} n={2 * I} k={Hd} (gate_up)", "TOP_s": round(ops_n / (t_us * 1e-6) / 1e12, 1),
+                          "frac_of_int8_peak": round(ops_n / (t_us * 1e-6) / INT8_PEAK_OPS, 4)})
         elif n == "copy":
             entry.update({"bytes": 2 * copy_pair[0].numel() * 4,
                           "GB_s": round(2 * copy_pair[0].numel() * 4 / (t_us * 1e-6) / 1e9, 1)})
@@ -270,6 +300,7 @@ def main() -> int:
                         "GB_s": res_ops["copy"]["GB_s"],
                         "frac_of_peak": round(res_ops["copy"]["GB_s"] / HBM_PEAK_GBS, 4)} if "copy" in res_ops else None),
         "roofline": roofline,
+        "q8_gemm": res_ops.get("gemm"),
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

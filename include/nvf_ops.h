@@ -88,6 +88,12 @@ void hip_embedding_q8(const int64_t* ids, const uint8_t* w8, const uint16_t* ws,
 /* hip_ops.hpp:33 -- K-quant gather (kind 12/13/14) to fp32; Q4_K in GGML order. */
 void hip_embedding_qk(const int64_t* ids, const uint8_t* wq, int tokens, int hidden, float* out, int kind);
 
+/* hip_ops.hpp:10 -- Q8_0 GEMM, out[m,n] = x[m,k] * dequant(w8, ws)^T in fp32, with
+ * the reference's per-row int8 activation quantization (hip_ops.hip:639-686).
+ * k must be a multiple of 32; the quantized rows go to a grow-only device scratch
+ * (the reference's own policy, hip_ops.hip:642-648). */
+void hip_matmul_q8(const float* x, const uint8_t* w8, const uint16_t* ws, int m, int n, int k, float* out);
+
 /* ---- 2. typed entry points ---------------------------------------------- */
 
 /* Residual-add + RMSNorm (replaces hip_rms_norm_add, hip_ops.hpp:15).  All four
@@ -155,6 +161,21 @@ int nvf_embedding(const int64_t* ids, const void* table, int64_t tokens, int64_t
 int nvf_embedding_rms_norm(const int64_t* ids, int format, const void* table, const void* scales, int64_t tokens,
                            int64_t hidden, int64_t vocab, const void* weight, void* residual, void* out, float eps,
                            int dtype, void* stream);
+
+/* Per-row int8 quantization of activations for the Q8_0 GEMM: row_scale[r] =
+ * 127 / max|x[r,:]| (0 when the maximum is <= 1e-8) and xq[r,i] = (int8)
+ * min(127, max(-127, x[r,i] * row_scale[r])), truncating -- q8_row_scale_kernel
+ * (hip_ops.hip:205-217) and its GEMMs' quantizer (hip_ops.hip:244-245). */
+int nvf_q8_quantize_rows(const void* x, float* row_scale, int8_t* xq, int64_t rows, int64_t k, int dtype,
+                         void* stream);
+
+/* Q8_0 GEMM on pre-quantized activations (replaces hip_matmul_q8, hip_ops.hpp:10,
+ * after nvf_q8_quantize_rows or nvf_rms_norm_q8): out[r,c] = (sum_b ws[c,b] *
+ * sum_{i in b} xq[r,i] * w8[c,i]) / row_scale[r] (0 where row_scale is 0), written
+ * as out_dtype.  w8 [n,k] int8 and xq [m,k] 16-byte aligned; ws [n,k/32] fp16;
+ * k a multiple of 32. */
+int nvf_matmul_q8_0(const int8_t* xq, const float* row_scale, const uint8_t* w8, const uint16_t* ws, int64_t m,
+                    int64_t n, int64_t k, void* out, int out_dtype, void* stream);
 
 /* Host helper: inv_freq[i] = (float)(1 / theta^(2i/head_dim)) in double, the
  * table Qwen3Model builds in its constructor (src/model.cpp:416-420).

@@ -37,6 +37,9 @@ SIGNATURES: dict[str, tuple] = {
     "hip_embedding_u16": (None, [_vp, _vp, _i32, _i32, _vp, C.c_bool]),
     "hip_embedding_q8": (None, [_vp, _vp, _vp, _i32, _i32, _vp]),
     "hip_embedding_qk": (None, [_vp, _vp, _i32, _i32, _vp, _i32]),
+    "hip_matmul_q8": (None, [_vp, _vp, _vp, _i32, _i32, _i32, _vp]),
+    "nvf_q8_quantize_rows": (_i32, [_vp, _vp, _vp, _i64, _i64, _i32, _vp]),
+    "nvf_matmul_q8_0": (_i32, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _i32, _vp]),
     "nvf_rms_norm_add": (_i32, [_vp, _vp, _vp, _vp, _i64, _i64, _f32, _i32, _vp]),
     "nvf_rms_norm": (_i32, [_vp, _vp, _vp, _i64, _i64, _f32, _i32, _vp]),
     "nvf_rms_norm_q8": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _f32, _i32, _vp]),
@@ -144,6 +147,38 @@ def rms_norm_q8(x: torch.Tensor, weight: torch.Tensor, eps: float, residual: tor
                                  _dev(scale, "row_scale"), _dev(q, "q_out") if q is not None else None, rows, hidden,
                                  eps, _dt(x), _stream()), "rms_norm_q8")
     return out, scale, q
+
+
+# ---------------------------------------------------------------------------
+# Q8_0 GEMM
+# ---------------------------------------------------------------------------
+def q8_quantize_rows(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """Per-row int8 quantization for the Q8_0 GEMM: (row_scale [rows] fp32, xq [rows, k] int8)."""
+    rows, k = x.shape
+    scale = torch.empty(rows, dtype=torch.float32, device=x.device)
+    xq = torch.empty((rows, k), dtype=torch.int8, device=x.device)
+    _check(lib().nvf_q8_quantize_rows(_dev(x, "x"), _dev(scale, "row_scale"), _dev(xq, "xq"), rows, k, _dt(x),
+                                      _stream()), "q8_quantize_rows")
+    return scale, xq
+
+
+def matmul_q8_0(xq: torch.Tensor, row_scale: torch.Tensor, w8: torch.Tensor, ws: torch.Tensor, n: int,
+                out_dtype: torch.dtype = torch.float32, out: torch.Tensor | None = None) -> torch.Tensor:
+    """out [m, n] = dequantized Q8_0 product of pre-quantized activations xq [m, k]
+    (int8, with row_scale) and split-plane weights w8 [n*k] int8, ws [n*k/32] fp16 bits."""
+    m, k = xq.shape
+    out = torch.empty((m, n), dtype=out_dtype, device=xq.device) if out is None else out
+    _check(lib().nvf_matmul_q8_0(_dev(xq, "xq"), _dev(row_scale, "row_scale"), _dev(w8, "w8"), _dev(ws, "ws"), m, n,
+                                 k, _dev(out, "out"), _dt(out), _stream()), "matmul_q8_0")
+    return out
+
+
+def matmul_q8(x: torch.Tensor, w8: torch.Tensor, ws: torch.Tensor, n: int,
+              out_dtype: torch.dtype | None = None) -> torch.Tensor:
+    """The reference's hip_matmul_q8 on activations x [m, k] (fp32/fp16/bf16):
+    quantize the rows, then the int8 GEMM.  Output in out_dtype (default x's)."""
+    scale, xq = q8_quantize_rows(x)
+    return matmul_q8_0(xq, scale, w8, ws, n, out_dtype or x.dtype)
 
 
 # ---------------------------------------------------------------------------

@@ -385,6 +385,55 @@ void orc_q8_quantize(const void* x, const float* scale, int8_t* q, int64_t rows,
     }
 }
 
+/* ---- Q8_0 GEMM ------------------------------------------------------------ */
+
+/* src/hip_ops.hip:639-686 (hip_matmul_q8).  With I[r,c,b] the exact integer dot
+ * of block b, I = sum_{i in b} xq[r,i] * w8[c,i], and adq[r] = 1.0f / scale[r]
+ * (0 when scale[r] is 0, :309 and :358), the reference's tile kernel (:221-312)
+ * and GEMV (:317-364) both compute
+ *     out[r,c] = (sum_b ws[c,b] * I[r,c,b]) * adq[r]
+ * in fp32, summing the block terms in different orders (16-element halves in the
+ * tile kernel, 4-element lane chunks then 32 lanes in the GEMV).  This function
+ * returns that value in double, where each term ws*I is exact (11 x 20 bits) and
+ * the sum carries at most a 2^-53 relative error, together with
+ *     err[r,c] = (k/32 + 4) * 2^-24 * sum_b |ws[c,b] * I[r,c,b]| * adq[r],
+ * a bound on the error of any fp32 recursive summation of the 2*k/32 half-block
+ * terms followed by the adq product: the tolerance for a fp32 implementation. */
+void orc_matmul_q8_i8(const int8_t* xq, const float* scale, const uint8_t* w8, const uint16_t* ws, int64_t m,
+                      int64_t n, int64_t k, double* out, double* err) {
+  const int64_t nblk = k / 32;
+  for (int64_t r = 0; r < m; ++r) {
+    const float adq = scale[r] > 0.0f ? 1.0f / scale[r] : 0.0f;
+    for (int64_t c = 0; c < n; ++c) {
+      double sum = 0.0, mag = 0.0;
+      for (int64_t b = 0; b < nblk; ++b) {
+        int32_t dot = 0;
+        for (int i = 0; i < 32; ++i)
+          dot += (int32_t)xq[r * k + b * 32 + i] * (int32_t)(int8_t)w8[c * k + b * 32 + i];
+        const double t = (double)orc_fp16_to_f32(ws[c * nblk + b]) * (double)dot;
+        sum += t;
+        mag += fabs(t);
+      }
+      out[r * n + c] = sum * (double)adq;
+      err[r * n + c] = (double)(nblk + 4) * ldexp(1.0, -24) * mag * (double)adq;
+    }
+  }
+}
+
+/* The reference's whole hip_matmul_q8 on activations x [m,k] in `dtype`: row
+ * scales (:205-217), quantization (:244-245), then orc_matmul_q8_i8.  scale_out
+ * [m] and xq_out [m,k] receive the intermediate values when not NULL. */
+void orc_matmul_q8(const void* x, int dtype, const uint8_t* w8, const uint16_t* ws, int64_t m, int64_t n, int64_t k,
+                   double* out, double* err, float* scale_out, int8_t* xq_out) {
+  float* sc = scale_out ? scale_out : (float*)malloc(sizeof(float) * (size_t)(m > 0 ? m : 1));
+  int8_t* q = xq_out ? xq_out : (int8_t*)malloc((size_t)(m * k > 0 ? m * k : 1));
+  orc_q8_row_scale(x, sc, m, k, dtype);
+  orc_q8_quantize(x, sc, q, m, k, dtype);
+  orc_matmul_q8_i8(q, sc, w8, ws, m, n, k, out, err);
+  if (!xq_out) free(q);
+  if (!scale_out) free(sc);
+}
+
 /* ---- layer-0 embedding + residual-add + RMSNorm -------------------------- */
 
 void orc_embedding_rms_norm(const int64_t* ids, int format, const void* table, const void* scales, int64_t tokens,

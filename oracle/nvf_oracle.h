@@ -33,6 +33,10 @@
  *                              zero rows give scale 0), truncation toward zero
  *   embedding + layer-0 norm . equal to the composition gather ->
  *                              rms_norm_add with a zero residual
+ *   Q8_0 GEMM ................ exact on power-of-two scales against a textbook
+ *                              matmul of the dequantized weights; the error bound
+ *                              holds for fp32 sums in every order; on the GPU box
+ *                              the reference's own hip_matmul_q8 lies within it
  */
 #ifndef NVF_ORACLE_H
 #define NVF_ORACLE_H
@@ -86,6 +90,14 @@ void orc_qk_norm_rope(void* q, void* k, const int64_t* positions, const void* q_
  * src/hip_ops.hip:244-245: q = (int8)min(127, max(-127, x * scale)) (truncation). */
 void orc_q8_row_scale(const void* x, float* scale, int64_t rows, int64_t hidden, int dtype);
 void orc_q8_quantize(const void* x, const float* scale, int8_t* q, int64_t rows, int64_t hidden, int dtype);
+
+/* Q8_0 GEMM, src/hip_ops.hip:639-686: out[r,c] = (sum_b ws[c,b] * I[r,c,b]) /
+ * scale[r] with exact integer block dots I, in double, and err[r,c], the fp32
+ * recursive-summation bound (k/32 + 4) * 2^-24 * sum_b |ws*I| / scale[r]. */
+void orc_matmul_q8_i8(const int8_t* xq, const float* scale, const uint8_t* w8, const uint16_t* ws, int64_t m,
+                      int64_t n, int64_t k, double* out, double* err);
+void orc_matmul_q8(const void* x, int dtype, const uint8_t* w8, const uint16_t* ws, int64_t m, int64_t n, int64_t k,
+                   double* out, double* err, float* scale_out, int8_t* xq_out);
 
 /* Layer-0 embedding + residual-add + RMSNorm (src/model.cpp:756 then :762 with
  * the zero-filled residual): residual = emb + 0, out = RMSNorm(residual) * w.

@@ -1,5 +1,5 @@
 // C-ABI shim over the reference's own HIP launchers (src/hip_ops.hip, C++
-// linkage, include/nanovllm/hip_ops.hpp:14-34), compiled for gfx950 from the
+// linkage, include/nanovllm/hip_ops.hpp:10-34), compiled for gfx950 from the
 // reference sources where they lie (see Makefile) into oracle/_ref/.
 // TEST INFRASTRUCTURE ONLY: GPU parity tests use it as a second checker beside
 // the C oracle.  Each wrapper launches on the null stream like the reference
@@ -35,6 +35,15 @@ void ref_hip_embedding_q8(const int64_t* ids, const uint8_t* w8, const uint16_t*
 void ref_hip_embedding_qk(const int64_t* ids, const uint8_t* wq, int tokens, int hidden, float* out, int kind) {
   hip_embedding_qk(ids, wq, tokens, hidden, out, kind);
   HIP_CHECK(hipDeviceSynchronize());
+}
+void ref_hip_matmul_q8(const float* x, const uint8_t* w8, const uint16_t* ws, int m, int n, int k, float* out) {
+  hip_matmul_q8(x, w8, ws, m, n, k, out);
+  HIP_CHECK(hipDeviceSynchronize());
+}
+// No synchronisation: for timing the reference's GEMM with events.
+void ref_hip_matmul_q8_async(const float* x, const uint8_t* w8, const uint16_t* ws, int m, int n, int k,
+                             float* out) {
+  hip_matmul_q8(x, w8, ws, m, n, k, out);
 }
 void ref_hip_embedding_u16(const int64_t* ids, const uint16_t* table, int tokens, int hidden, float* out,
                            int table_bf16) {

@@ -44,6 +44,8 @@ _ORACLE_SIGS = {
     "orc_q8_row_scale": (None, [_vp, _vp, _i64, _i64, _i32]),
     "orc_q8_quantize": (None, [_vp, _vp, _vp, _i64, _i64, _i32]),
     "orc_embedding_rms_norm": (None, [_vp, _i32, _vp, _vp, _i64, _i64, _vp, _vp, _vp, _f32, _i32]),
+    "orc_matmul_q8_i8": (None, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _vp]),
+    "orc_matmul_q8": (None, [_vp, _i32, _vp, _vp, _i64, _i64, _i64, _vp, _vp, _vp, _vp]),
 }
 
 _cache: dict[str, C.CDLL] = {}
@@ -92,6 +94,7 @@ def ref_hip() -> C.CDLL | None:
     h.ref_hip_embedding_q8.argtypes = [_vp, _vp, _vp, _i32, _i32, _vp]
     h.ref_hip_embedding_qk.argtypes = [_vp, _vp, _i32, _i32, _vp, _i32]
     h.ref_hip_embedding_u16.argtypes = [_vp, _vp, _i32, _i32, _vp, _i32]
+    h.ref_hip_matmul_q8.argtypes = [_vp, _vp, _vp, _i32, _i32, _i32, _vp]
     return h
 
 

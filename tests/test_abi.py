@@ -75,6 +75,27 @@ def test_host_argument_checks():
     rc, msg = _status(lib.nvf_stream_copy(p + 8, p, 32, None))
     assert rc == -1 and "unaligned" in msg
     assert lib.nvf_stream_copy(p, p, 0, None) == 0
+    # Q8_0 GEMM and its quantizer
+    rc, msg = _status(lib.nvf_matmul_q8_0(p, p, p, p, 4, 8, 48, p, 0, None))
+    assert rc == -1 and "multiple" in msg
+    rc, msg = _status(lib.nvf_matmul_q8_0(p, p, p, p, 4, 8, 64, p, 9, None))
+    assert rc == -1 and "dtype" in msg
+    rc, msg = _status(lib.nvf_matmul_q8_0(p, None, p, p, 4, 8, 64, p, 0, None))
+    assert rc == -1 and "null" in msg
+    rc, msg = _status(lib.nvf_matmul_q8_0(p + 4, p, p, p, 4, 8, 64, p, 0, None))
+    assert rc == -1 and "aligned" in msg
+    rc, msg = _status(lib.nvf_matmul_q8_0(p, p, p, p + 1, 4, 8, 64, p, 0, None))
+    assert rc == -1 and "aligned" in msg
+    rc, msg = _status(lib.nvf_matmul_q8_0(p, p, p, p, -4, 8, 64, p, 0, None))
+    assert rc == -1 and "negative" in msg
+    assert lib.nvf_matmul_q8_0(p, p, p, p, 0, 8, 64, p, 0, None) == 0
+    assert lib.nvf_matmul_q8_0(p, p, p, p, 4, 0, 64, p, 0, None) == 0
+    rc, msg = _status(lib.nvf_q8_quantize_rows(p, None, p, 4, 64, 0, None))
+    assert rc == -1 and "null" in msg
+    rc, msg = _status(lib.nvf_q8_quantize_rows(p, p, p, 4, 64, 5, None))
+    assert rc == -1 and "dtype" in msg
+    assert lib.nvf_q8_quantize_rows(p, p, p, 0, 64, 0, None) == 0
+    lib.hip_matmul_q8(p, p, p, 0, 8, 64, p)  # empty: returns before any HIP call
 
 
 def test_inv_freq_host_helper_matches_oracle():

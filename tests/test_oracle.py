@@ -439,3 +439,65 @@ def test_tolerance_rule_rejects_two_ulp():
     H.assert_close(refb + np.uint16(1), refb, H.BF16)
     with pytest.raises(AssertionError):
         H.assert_close(refb + np.uint16(2), refb, H.BF16)
+
+
+# ---------------------------------------------------------------------------
+# Q8_0 GEMM (src/hip_ops.hip:639-686)
+# ---------------------------------------------------------------------------
+def _gemm(o, x, dt, w8, ws, m, n, k):
+    out = np.empty((m, n), np.float64)
+    err = np.empty((m, n), np.float64)
+    sc = np.empty(m, np.float32)
+    xq = np.empty((m, k), np.int8)
+    o.orc_matmul_q8(H.ptr(x), dt, H.ptr(w8), H.ptr(ws), m, n, k, H.ptr(out), H.ptr(err), H.ptr(sc), H.ptr(xq))
+    return out, err, sc, xq
+
+
+@pytest.mark.parametrize("dt", [H.F32, H.F16, H.BF16])
+def test_matmul_q8_exact_against_dequantized_matmul(o, dt):
+    """Rows whose maximum is 127 quantize with scale 1 (xq == x) and power-of-two
+    block scales keep every product exact, so the oracle must equal a textbook
+    float64 matmul of the activations with the dequantized weight matrix
+    W[c,i] = ws[c, i // 32] * w8[c,i] -- a different route through the same
+    arithmetic (dequantize first, contract second).  A zero row gives scale 0."""
+    r = H.rng(11 + dt)
+    m, n, k = 6, 9, 160
+    x = r.integers(-127, 128, (m, k)).astype(np.float32)
+    x[:, 7] = 127.0
+    x[3] = 0.0
+    w8 = r.integers(-127, 128, n * k, dtype=np.int8)
+    exps = (np.arange(n)[:, None] + 3 * np.arange(k // 32)[None, :]) % 7 + 3
+    ws = np.ldexp(1.0, -exps).astype(np.float16).view(np.uint16).reshape(-1)
+    out, err, sc, xq = _gemm(o, H.to_storage(x, dt), dt, w8, ws, m, n, k)
+    W = ws.view(np.float16).astype(np.float64).reshape(n, k // 32).repeat(32, axis=1) * w8.reshape(n, k)
+    expect = x.astype(np.float64) @ W.T
+    expect[3] = 0.0
+    assert np.array_equal(sc, np.where(np.arange(m) == 3, 0.0, 1.0).astype(np.float32))
+    assert np.array_equal(xq, x.astype(np.int8))
+    assert np.array_equal(out, expect)
+    assert (err >= 0).all() and (err[3] == 0).all()
+
+
+def test_matmul_q8_bound_covers_fp32_summation_orders(o):
+    """The stated tolerance holds for fp32 sums of the block terms in the
+    reference's order (16-element halves, src/hip_ops.hip:297-302), in whole
+    blocks, and reversed -- each computed here in numpy float32."""
+    r = H.rng(12)
+    m, n, k = 5, 7, 512
+    x = r.standard_normal((m, k)).astype(np.float32)
+    w8, ws = H.gen_q8_0(r, n, k)
+    out, err, sc, xq = _gemm(o, x, H.F32, w8, ws, m, n, k)
+    s = ws.view(np.float16).astype(np.float32).reshape(n, k // 32)
+    q = xq.astype(np.int64).reshape(m, 1, k // 16, 16)
+    w = w8.astype(np.int64).reshape(1, n, k // 16, 16)
+    halves = (q * w).sum(-1)                                         # [m, n, k/16] exact
+    blocks = halves.reshape(m, n, k // 32, 2).sum(-1)
+    adq = np.where(sc > 0, np.float32(1) / sc, np.float32(0)).astype(np.float32)
+    for terms, sidx in ((halves, np.arange(k // 16) // 2), (blocks, np.arange(k // 32)),
+                        (blocks[..., ::-1], np.arange(k // 32)[::-1])):
+        acc = np.zeros((m, n), np.float32)
+        for j in range(terms.shape[-1]):
+            acc = (acc + s[:, sidx[j]][None, :] * terms[..., j].astype(np.float32)).astype(np.float32)
+        got = (acc * adq[:, None]).astype(np.float64)
+        assert (np.abs(got - out) <= err).all()
+    assert (np.abs(out) > 0).any()
