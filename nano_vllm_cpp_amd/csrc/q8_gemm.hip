@@ -27,6 +27,7 @@
 #include <hip/hip_runtime.h>
 
 #include <mutex>
+#include <type_traits>
 
 #include "nvf_device.hpp"
 #include "nvf_host.hpp"
@@ -38,12 +39,16 @@ typedef int i32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int kGemmBM = 128;                 // output rows per workgroup
 constexpr int kGemmBN = 128;                 // output columns per workgroup
-constexpr int kGemmKC = 128;                 // bytes of K per LDS stage (4 Q8_0 blocks)
-constexpr int kGemmRow = kGemmKC + 16;       // padded LDS row
+constexpr int kGemmKC = 64;                  // bytes of K per LDS stage (2 Q8_0 blocks)
+constexpr int kGemmCPR = kGemmKC / 16;       // 16-byte chunks per LDS row
+constexpr int kGemmRPI = 1024 / kGemmKC;     // rows per 1 KB wave DMA transfer
+constexpr int kGemmSwz = 256 / kGemmKC;      // rows sharing a bank offset
 constexpr int kGemmBlk = kGemmKC / 32;       // Q8_0 blocks per stage
-constexpr int kGemmStage = (kGemmBM + kGemmBN) * kGemmRow + kGemmBN * kGemmBlk * 4;  // + fp32 block scales
+constexpr int kGemmStage = (kGemmBM + kGemmBN) * kGemmKC + kGemmBN * kGemmBlk * 4;  // + fp32 block scales
 constexpr int kGemmLds = 2 * kGemmStage;     // double-buffered
 constexpr int kGemmThreads = 256;
+constexpr int kGemmGroupM = 8;               // tile rows per group of the tile order
+constexpr int kXcds = 8;                     // accelerator dies of an MI355X
 
 // ---------------------------------------------------------------------------
 // Row quantizer: scale[r] = 127 / max|x[r,:]| (0 for max <= 1e-8) and
@@ -101,46 +106,19 @@ __global__ __launch_bounds__(256) void q8_quantize_rows_kernel(const T* __restri
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ float fp16_bits_to_float(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
 
-// One thread's share of a stage's global loads: 16 bytes from each of 4 rows
-// (rows (t >> 3) + 32 * i of the tile, bytes (t & 7) * 16 of the K slice).  Every
-// load is unconditional: a row past the end is clamped to the last row and a K
-// offset past the end to the last 16 bytes, and the data are zeroed by a select,
-// so the loop has no branches and no early vmcnt waits.
-struct SliceLoader {
-  const int8_t* ptr[4];  // row base + this thread's byte offset in the slice
-  bool row_ok[4];
-  int64_t kb;            // K offset of this thread's 16 bytes in the current slice
-  bool k_ok;             // kb < k for the slice in flight
-  i32x4 r[4];            // raw data in flight (masked when stored)
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int64_t bytes) {
+  // raw buffer, 32-bit dwords; offsets at or past `bytes` read as zero
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
 
-  __device__ __forceinline__ void init(const int8_t* base, int64_t row0, int64_t rows, int64_t k) {
-    const int t = threadIdx.x;
-    kb = (t & 7) * 16;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int64_t row = row0 + (t >> 3) + 32 * i;
-      row_ok[i] = row < rows;
-      ptr[i] = base + (row_ok[i] ? row : rows - 1) * k;
-    }
-  }
-  __device__ __forceinline__ void load(int64_t k) {
-    k_ok = kb < k;
-    const int64_t off = k_ok ? kb : k - 16;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) r[i] = *reinterpret_cast<const i32x4*>(ptr[i] + off);
-  }
-  // Writes the slice in flight to LDS rows (t >> 3) + 32 * i, zeroing rows and
-  // bytes outside the matrix.
-  __device__ __forceinline__ void store(uint8_t* lds) const {
-    const int t = threadIdx.x;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const bool ok = k_ok && row_ok[i];
-      const i32x4 v = i32x4{ok ? r[i][0] : 0, ok ? r[i][1] : 0, ok ? r[i][2] : 0, ok ? r[i][3] : 0};
-      *reinterpret_cast<i32x4*>(lds + ((t >> 3) + 32 * i) * kGemmRow + (t & 7) * 16) = v;
-    }
-  }
-};
+constexpr uint32_t kOob = 0x80000000u;  // a buffer offset past every tile: reads zero
+
+// LDS rows hold kGemmKC bytes (kGemmCPR chunks of 16 B) with chunk c of row r at
+// position c ^ ((r / kGemmSwz) % kGemmCPR): rows kGemmKC bytes apart fall on
+// kGemmSwz distinct bank offsets, and the swizzle spreads the rest, so the 16
+// lanes of a ds_read_b128 phase (16 consecutive rows, one chunk) cover all 64
+// banks once.
+__device__ __forceinline__ int swz(int row, int chunk) { return chunk ^ ((row / kGemmSwz) % kGemmCPR); }
 
 template <typename TO>
 __device__ __forceinline__ void gemm_store_out(TO* p, float v) {
@@ -154,22 +132,39 @@ __device__ __forceinline__ void gemm_store_out(TO* p, float v) {
 // out[m][n] (row-major) = dequantized Q8_0 product; see the file header.
 // Grid: one workgroup per 128 x 128 output tile, tiles_n tiles per tile row.
 //
-// Per stage a wave issues 16 MFMAs (4 blocks x 2 x 2 tiles) through a ring of two
-// result registers: MFMA t+1 is issued before the scale of MFMA t is applied, so
-// the matrix core works while the VALU converts and accumulates.  The LDS
-// fragments of block b+1 are read while block b is applied.
+// Stage loads go straight from HBM to LDS (buffer_load ... lds): each wave moves
+// 32 activation rows and 32 weight rows per stage in 1 KB transfers, through
+// buffer resources spanning only this tile's rows, so rows past the matrix read
+// as zero; the stage's K offset rides in the scalar offset, so a full stage costs
+// no VALU.  Only a partial last stage (k not a multiple of kGemmKC) checks each
+// chunk against k.  Block scales take a register path (fp16 -> fp32 in LDS).
+//
+// One loop iteration per Q8_0 block; the first MFMA of block g + 1 is issued
+// while block g is applied, so each result is ready when its scale is applied.
 template <typename TO>
-__global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2))) void q8_gemm_kernel(
+__global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(3))) void q8_gemm_kernel(
     const int8_t* __restrict__ xq, const float* __restrict__ rscale, const int8_t* __restrict__ w8,
     const uint16_t* __restrict__ ws, TO* __restrict__ out, int64_t m, int64_t n, int64_t k, int tiles_n) {
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   __shared__ float inv_row[kGemmBM];
 
-  const int tile = blockIdx.x;
-  const int64_t row0 = (int64_t)(tile / tiles_n) * kGemmBM;
-  const int64_t col0 = (int64_t)(tile % tiles_n) * kGemmBN;
+  // XCD-aware tile order.  Workgroups are dealt to the 8 XCDs round-robin
+  // (blockIdx % 8); each XCD gets a contiguous range of a grouped tile order
+  // (kGemmGroupM tile rows at a time, column by column), so the workgroups
+  // resident on one XCD share activation and weight panels in its L2.
+  const int tiles = (int)gridDim.x;
+  const int tiles_m = tiles / tiles_n;
+  const int xcd = (int)blockIdx.x % kXcds, local = (int)blockIdx.x / kXcds;
+  const int per = tiles / kXcds, extra = tiles % kXcds;
+  const int id = xcd * per + (xcd < extra ? xcd : extra) + local;
+  const int gsz = kGemmGroupM * tiles_n;
+  const int first = (id / gsz) * kGemmGroupM;
+  const int rows_g = tiles_m - first < kGemmGroupM ? tiles_m - first : kGemmGroupM;
+  const int in_g = id % gsz;
+  const int64_t row0 = (int64_t)(first + in_g % rows_g) * kGemmBM;
+  const int64_t col0 = (int64_t)(in_g / rows_g) * kGemmBN;
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   const int wm = wave >> 1, wn = wave & 1;
   const int64_t nblk = k / 32;
 
@@ -187,101 +182,149 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2)
 #pragma unroll
       for (int j = 0; j < 16; ++j) acc[a][b][j] = 0.0f;
 
-  SliceLoader la, lb;
-  la.init(xq, row0, m, k);
-  lb.init(w8, col0, n, k);
-  // Block scales: thread t loads column col0 + (t & 127), blocks 2 * (t >> 7) + {0, 1}
-  // of each stage (clamped + selected like the slices), stored as fp32 [block][column].
+  // tile-local buffer resources (rows past m / n fall outside and read zero)
+  const int64_t a_rows = m - row0 < kGemmBM ? m - row0 : kGemmBM;
+  const int64_t b_rows = n - col0 < kGemmBN ? n - col0 : kGemmBN;
+  const __amdgpu_buffer_rsrc_t ra = make_rsrc(xq + row0 * k, a_rows * k);
+  const __amdgpu_buffer_rsrc_t rb = make_rsrc(w8 + col0 * k, b_rows * k);
+  const __amdgpu_buffer_rsrc_t rsc = make_rsrc(ws + col0 * nblk, b_rows * nblk * 2);
+
+  // This lane's DMA rows: wave w moves tile rows 32 w + kGemmRPI i + lane / kGemmCPR,
+  // fetching the chunk that belongs at LDS position lane % kGemmCPR of each.
+  constexpr int kDma = 32 / kGemmRPI;  // 1 KB transfers per wave and matrix per stage
+  uint32_t dma_off[kDma];
+  int dma_chunk[kDma];
+#pragma unroll
+  for (int i = 0; i < kDma; ++i) {
+    const int row = 32 * wave + kGemmRPI * i + lane / kGemmCPR;
+    dma_chunk[i] = swz(row, lane % kGemmCPR);
+    dma_off[i] = (uint32_t)(row * k) + (uint32_t)(dma_chunk[i] * 16);
+  }
+  // Block scales: thread t loads column col0 + (t & 127), blocks kSpt * (t >> 7) + e.
+  constexpr int kSpt = kGemmBlk / 2;
   const int sc_c = threadIdx.x & (kGemmBN - 1);
-  const int sc_b = 2 * (threadIdx.x >> 7);
-  const bool sc_col_ok = col0 + sc_c < n;
-  const uint16_t* sc_ptr = ws + (sc_col_ok ? col0 + sc_c : n - 1) * nblk;
-  uint16_t sc_raw[2];
-  bool sc_ok[2];
-  auto load_scales = [&](int64_t blk0) {
-#pragma unroll
-    for (int e = 0; e < 2; ++e) {
-      const int64_t b = blk0 + sc_b + e;
-      sc_ok[e] = sc_col_ok && b < nblk;
-      sc_raw[e] = sc_ptr[sc_ok[e] ? b : nblk - 1];
-    }
-  };
-  auto store_scales = [&](uint8_t* stage) {
-    float* s = reinterpret_cast<float*>(stage + (kGemmBM + kGemmBN) * kGemmRow);
-#pragma unroll
-    for (int e = 0; e < 2; ++e) s[(sc_b + e) * kGemmBN + sc_c] = sc_ok[e] ? fp16_bits_to_float(sc_raw[e]) : 0.0f;
-  };
+  const int sc_b = kSpt * (threadIdx.x >> 7);
+  const uint32_t sc_off = (uint32_t)((sc_c * nblk + sc_b) * 2);
+  uint32_t sc_raw[kSpt];
 
   const int nstages = (int)((k + kGemmKC - 1) / kGemmKC);
-  la.load(k);
-  lb.load(k);
-  load_scales(0);
-  la.store(lds);
-  lb.store(lds + kGemmBM * kGemmRow);
-  store_scales(lds);
-  __syncthreads();
+  const bool partial_last = k % kGemmKC != 0;
+  // Loads stage st into LDS buffer `buf` (DMA for the tiles, registers for the scales).
+  auto issue = [&](int st, int buf) {
+    uint8_t* stage = lds + buf * kGemmStage;
+    const uint32_t kc = (uint32_t)st * kGemmKC;
+    if (partial_last && st == nstages - 1) {  // uniform, at most once per tile
+#pragma unroll
+      for (int i = 0; i < kDma; ++i) {
+        const uint32_t off = (int64_t)kc + dma_chunk[i] * 16 < k ? dma_off[i] + kc : kOob;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            ra, (__attribute__((address_space(3))) void*)(stage + (32 * wave + kGemmRPI * i) * kGemmKC), 16, off, 0,
+            0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            rb,
+            (__attribute__((address_space(3))) void*)(stage + kGemmBM * kGemmKC +
+                                                      (32 * wave + kGemmRPI * i) * kGemmKC),
+            16, off, 0, 0, 0);
+      }
+#pragma unroll
+      for (int e = 0; e < kSpt; ++e) {
+        const int64_t b = (int64_t)st * kGemmBlk + sc_b + e;
+        sc_raw[e] = __builtin_amdgcn_raw_buffer_load_b16(rsc, b < nblk ? sc_off + 2 * e + st * kGemmBlk * 2 : kOob,
+                                                         0, 0);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < kDma; ++i) {
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            ra, (__attribute__((address_space(3))) void*)(stage + (32 * wave + kGemmRPI * i) * kGemmKC), 16,
+            dma_off[i], kc, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            rb,
+            (__attribute__((address_space(3))) void*)(stage + kGemmBM * kGemmKC +
+                                                      (32 * wave + kGemmRPI * i) * kGemmKC),
+            16, dma_off[i], kc, 0, 0);
+      }
+#pragma unroll
+      for (int e = 0; e < kSpt; ++e)
+        sc_raw[e] = __builtin_amdgcn_raw_buffer_load_b16(rsc, sc_off + 2 * e, (uint32_t)st * kGemmBlk * 2, 0);
+    }
+  };
+  auto store_scales = [&](int buf) {
+    float* s = reinterpret_cast<float*>(lds + buf * kGemmStage + (kGemmBM + kGemmBN) * kGemmKC);
+#pragma unroll
+    for (int e = 0; e < kSpt; ++e) s[(sc_b + e) * kGemmBN + sc_c] = fp16_bits_to_float((uint16_t)sc_raw[e]);
+  };
+  // This wave's LDS DMA (and scale loads) must land before the barrier that publishes a stage.
+  auto publish = [&](int buf) {
+    store_scales(buf);
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+    __syncthreads();
+  };
 
-  const int a_off = (wm * 64 + (lane & 31)) * kGemmRow + (lane >> 5) * 16;
-  const int b_off = kGemmBM * kGemmRow + (wn * 64 + (lane & 31)) * kGemmRow + (lane >> 5) * 16;
-  const int s_off = (kGemmBM + kGemmBN) * kGemmRow + (wn * 64 + (lane & 31)) * 4;
+  // fragment LDS offsets: tile row r = wm*64 + (lane & 31) (+32 for the second
+  // tile) and weight row wn*64 + (lane & 31), chunk 2*bi + (lane >> 5), swizzled.
+  // Block bi's offsets are block 0's with bit 5 flipped per bi bit (the chunk
+  // index moves by 2 bi under the xor swizzle).
+  const int fr = wm * 64 + (lane & 31);
+  const int fcol = wn * 64 + (lane & 31);
+  const int cx0 = swz(fr, lane >> 5) << 4;  // the weight row fcol has the same swizzle
+  const int fa_addr0 = fr * kGemmKC + cx0;
+  const int fb_addr0 = kGemmBM * kGemmKC + fcol * kGemmKC + cx0;
+  const int fs_addr0 = (kGemmBM + kGemmBN) * kGemmKC + fcol * 4;
 
-  // Fragments of one block g: stage buffer (g / kGemmBlk) & 1, block g % kGemmBlk.
   i32x4 fa0, fa1, fb0, fb1;
   float s0, s1;
   auto read_frags = [&](int g) {
-    const uint8_t* buf = lds + ((g / kGemmBlk) & 1) * kGemmStage;
+    const uint8_t* base = lds + ((g / kGemmBlk) & 1) * kGemmStage;
     const int bi = g % kGemmBlk;
-    fa0 = *reinterpret_cast<const i32x4*>(buf + a_off + bi * 32);
-    fa1 = *reinterpret_cast<const i32x4*>(buf + a_off + 32 * kGemmRow + bi * 32);
-    fb0 = *reinterpret_cast<const i32x4*>(buf + b_off + bi * 32);
-    fb1 = *reinterpret_cast<const i32x4*>(buf + b_off + 32 * kGemmRow + bi * 32);
-    s0 = *reinterpret_cast<const float*>(buf + s_off + bi * kGemmBN * 4);
-    s1 = *reinterpret_cast<const float*>(buf + s_off + bi * kGemmBN * 4 + 32 * 4);
+    const int fa_addr = fa_addr0 ^ (bi << 5), fb_addr = fb_addr0 ^ (bi << 5);
+    fa0 = *reinterpret_cast<const i32x4*>(base + fa_addr);
+    fa1 = *reinterpret_cast<const i32x4*>(base + fa_addr + 32 * kGemmKC);
+    fb0 = *reinterpret_cast<const i32x4*>(base + fb_addr);
+    fb1 = *reinterpret_cast<const i32x4*>(base + fb_addr + 32 * kGemmKC);
+    s0 = *reinterpret_cast<const float*>(base + fs_addr0 + bi * kGemmBN * 4);
+    s1 = *reinterpret_cast<const float*>(base + fs_addr0 + bi * kGemmBN * 4 + 32 * 4);
   };
   auto apply = [](float (&c)[16], const i32x16& d, float sc) {
 #pragma unroll
     for (int j = 0; j < 16; ++j) c[j] = fmaf(sc, (float)d[j], c[j]);
   };
 
-  // One iteration per Q8_0 block.  The first MFMA of block g + 1 is issued
-  // inside iteration g, so every result is ready when its scale is applied; a
-  // stage's global loads go out at its first block and land in LDS at its last.
+  issue(0, 0);
+  publish(0);
   const int nb = nstages * kGemmBlk;
   read_frags(0);
   i32x16 d0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa0, fb0, i32x16{}, 0, 0, 0);
+  // One iteration per Q8_0 block, 0 .. nb-2; the last block is peeled so that
+  // the loop body has no conditional MFMA (a conditional result costs register
+  // copies every iteration).  A stage's successor is loaded at its first block
+  // and published (scales stored, DMA drained, barrier) after its MFMAs of the
+  // last block are issued.
 #pragma unroll 1
-  for (int g = 0; g < nb; ++g) {
+  for (int g = 0; g < nb - 1; ++g) {
     const int bi = g % kGemmBlk;
     const int st = g / kGemmBlk;
-    const bool more = st + 1 < nstages;
-    if (bi == 0 && more) {
-      la.kb += kGemmKC;
-      lb.kb += kGemmKC;
-      la.load(k);
-      lb.load(k);
-      load_scales((int64_t)(st + 1) * kGemmBlk);
-    }
+    if (bi == 0) issue(st + 1, (st + 1) & 1);  // uniform; g < nb - 1 implies a successor
     const i32x16 d1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa0, fb1, i32x16{}, 0, 0, 0);
     const i32x16 d2 = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa1, fb0, i32x16{}, 0, 0, 0);
     const i32x16 d3 = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa1, fb1, i32x16{}, 0, 0, 0);
     const float c0 = s0, c1 = s1;
+    if (bi == kGemmBlk - 1) publish((st + 1) & 1);
+    read_frags(g + 1);  // LDS latency hides behind the first two applies
     apply(acc[0][0], d0, c0);
     apply(acc[0][1], d1, c1);
+    d0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa0, fb0, i32x16{}, 0, 0, 0);
     apply(acc[1][0], d2, c0);
-    if (bi == kGemmBlk - 1) {
-      if (more) {
-        uint8_t* nxt = lds + ((st + 1) & 1) * kGemmStage;
-        la.store(nxt);
-        lb.store(nxt + kGemmBM * kGemmRow);
-        store_scales(nxt);
-      }
-      __syncthreads();
-    }
-    if (g + 1 < nb) {
-      read_frags(g + 1);
-      d0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa0, fb0, i32x16{}, 0, 0, 0);
-    }
     apply(acc[1][1], d3, c1);
+  }
+  {
+    const i32x16 d1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa0, fb1, i32x16{}, 0, 0, 0);
+    const i32x16 d2 = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa1, fb0, i32x16{}, 0, 0, 0);
+    const i32x16 d3 = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa1, fb1, i32x16{}, 0, 0, 0);
+    apply(acc[0][0], d0, s0);
+    apply(acc[0][1], d1, s1);
+    apply(acc[1][0], d2, s0);
+    apply(acc[1][1], d3, s1);
   }
 
   // D layout of v_mfma_*_32x32: lane l, value j -> column l % 32,
@@ -307,6 +350,154 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2)
     }
 }
 
+// ---------------------------------------------------------------------------
+// Decode-shaped product (m <= kGemvMaxM rows): bound by streaming the weights
+// once from HBM, so the layout serves the loads.
+//
+// A wave owns C groups of 16 weight columns and a contiguous range of K; S waves
+// share a column set (splitting K) and meet in LDS at the end, summed in split
+// order.  A workgroup holds 8 / S column sets; the host picks S and C per shape.
+// The workgroup first stages the block scales of its columns in LDS (coalesced
+// rows of k/16 bytes), so the stream itself issues only weight and activation
+// loads.
+//
+// Per block pair (64 bytes of K) lane l = 16 q + j loads 16 contiguous bytes,
+// k in [16 q, 16 q + 16), of weight column j (of each group) and of activation
+// row j -- the operand layout of v_mfma_i32_16x16x64_i8; one activation load
+// serves the C groups.  Lanes q = 0, 1 hold the pair's first block, q = 2, 3 its
+// second; the block scales differ, so each pair and group takes two MFMAs, each
+// with the activation lanes of the other block zeroed (the K = 64 instruction
+// then sums exactly one block).  MFMA time is idle capacity here.
+constexpr int kGemvMaxM = 16;
+constexpr int kGemvWaves = 8;
+constexpr int kGemvUnroll = 4;          // block pairs in flight per lane
+constexpr int kGemvScaleLds = 32768;    // bytes of LDS for the staged scales
+
+template <int S, int C>
+constexpr int gemv_cols() { return kGemvWaves / S * C * 16; }  // columns per workgroup
+
+template <typename TO, int S, int C>
+__global__ __launch_bounds__(kGemvWaves * 64) void q8_gemv_kernel(const int8_t* __restrict__ xq,
+                                                                   const float* __restrict__ rscale,
+                                                                   const int8_t* __restrict__ w8,
+                                                                   const uint16_t* __restrict__ ws,
+                                                                   TO* __restrict__ out, int64_t m, int64_t n,
+                                                                   int64_t k) {
+  constexpr int kCols = gemv_cols<S, C>();
+  __shared__ float part[kGemvWaves][C][16][17];
+  extern __shared__ __attribute__((aligned(16))) uint16_t sc_lds[];  // [kCols][nblk]
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int set = wave / S, split = wave % S;
+  const int j = lane & 15, q = lane >> 4;
+  const int64_t wg_c0 = (int64_t)blockIdx.x * kCols;
+  const int64_t nblk = k / 32, npairs = (nblk + 1) / 2;
+  const int64_t wg_cols = n - wg_c0 < kCols ? n - wg_c0 : kCols;
+
+  {  // stage this workgroup's block scales: wg_cols rows of nblk fp16 values
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(ws + wg_c0 * nblk, wg_cols * nblk * 2);
+    // whole 4-byte words, then an odd last value by itself (a 4-byte load that
+    // straddles the end of the slab reads as zero entirely)
+    const int64_t cnt = wg_cols * nblk;
+    uint32_t* dst = reinterpret_cast<uint32_t*>(sc_lds);
+    for (int64_t i = threadIdx.x; i < cnt / 2; i += kGemvWaves * 64)
+      dst[i] = __builtin_amdgcn_raw_buffer_load_b32(rs, (uint32_t)(4 * i), 0, 0);
+    if ((cnt & 1) && threadIdx.x == 0)
+      sc_lds[cnt - 1] = (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(rs, (uint32_t)(2 * (cnt - 1)), 0, 0);
+    __syncthreads();
+  }
+
+  const int64_t c0 = wg_c0 + (int64_t)set * C * 16;  // this wave's first column
+  const int64_t cols = n - c0 < C * 16 ? n - c0 : C * 16;
+  const int64_t p_begin = npairs * split / S, p_end = npairs * (split + 1) / S;
+  float acc[C][4];
+#pragma unroll
+  for (int g = 0; g < C; ++g)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) acc[g][v] = 0.0f;
+
+  if (cols > 0) {  // uniform per wave
+    // rows past m / columns past n fall outside these resources and read zero
+    const __amdgpu_buffer_rsrc_t rw = make_rsrc(w8 + c0 * k, cols * k);
+    const __amdgpu_buffer_rsrc_t rx = make_rsrc(xq, m * k);
+    const uint32_t lane_off = (uint32_t)(j * k) + 16u * q;  // weight column j and activation row j
+    const uint16_t* sc_col = sc_lds + ((int64_t)set * C * 16 + j) * nblk;
+    for (int64_t p0 = p_begin; p0 < p_end; p0 += kGemvUnroll) {
+      i32x4 wv[kGemvUnroll][C], xv[kGemvUnroll];
+#pragma unroll
+      for (int u = 0; u < kGemvUnroll; ++u) {
+        const int64_t p = p0 + u;
+        const bool ok = p < p_end && 64 * p + 16 * q < k;
+        const uint32_t off = ok ? lane_off + (uint32_t)(64 * p) : kOob;
+        xv[u] = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, off, 0, 0));
+#pragma unroll
+        for (int g = 0; g < C; ++g)
+          wv[u][g] = __builtin_bit_cast(
+              i32x4, __builtin_amdgcn_raw_buffer_load_b128(rw, ok ? off + (uint32_t)(g * 16 * k) : kOob, 0, 0));
+      }
+#pragma unroll
+      for (int u = 0; u < kGemvUnroll; ++u) {
+        const int64_t p = p0 + u;
+        const i32x4 z = {0, 0, 0, 0};
+        const i32x4 x_lo = q < 2 ? xv[u] : z;  // first block of the pair
+        const i32x4 x_hi = q < 2 ? z : xv[u];  // second block
+        const int64_t b = p < p_end ? 2 * p : 0;  // past the range: zero data, any in-range scale
+#pragma unroll
+        for (int g = 0; g < C; ++g) {
+          const uint16_t* sg = sc_col + (int64_t)g * 16 * nblk;
+          const float s_lo = fp16_bits_to_float(sg[b]);
+          const float s_hi = b + 1 < nblk ? fp16_bits_to_float(sg[b + 1]) : 0.0f;
+          const i32x4 d_lo = __builtin_amdgcn_mfma_i32_16x16x64_i8(x_lo, wv[u][g], z, 0, 0, 0);
+          const i32x4 d_hi = __builtin_amdgcn_mfma_i32_16x16x64_i8(x_hi, wv[u][g], z, 0, 0, 0);
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            acc[g][v] = fmaf(s_lo, (float)d_lo[v], acc[g][v]);
+            acc[g][v] = fmaf(s_hi, (float)d_hi[v], acc[g][v]);
+          }
+        }
+      }
+    }
+  }
+  // D layout of v_mfma_*_16x16: lane l, value v -> column l % 16, row 4 * (l / 16) + v.
+#pragma unroll
+  for (int g = 0; g < C; ++g)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) part[wave][g][4 * q + v][j] = acc[g][v];
+  __syncthreads();
+  for (int o = threadIdx.x; o < kCols * 16; o += kGemvWaves * 64) {
+    const int c = o % kCols, r = o / kCols;  // consecutive threads -> consecutive columns
+    const int st = c / (C * 16), g = (c / 16) % C, cj = c % 16;
+    const int64_t col = wg_c0 + c;
+    if (r < m && col < n) {
+      float sum = 0.0f;
+#pragma unroll
+      for (int sp = 0; sp < S; ++sp) sum += part[st * S + sp][g][r][cj];
+      const float sc = rscale[r];
+      const float inv = sc > 0.0f ? 1.0f / sc : 0.0f;  // the reference's adq (:358)
+      gemm_store_out(out + r * n + col, sum * inv);
+    }
+  }
+}
+
+// Picks the K split S and the column groups per wave C for a decode-shaped call
+// and launches; false if no configuration fits the LDS scale budget.
+template <typename TO, int S, int C>
+bool try_gemv(const int8_t* xq, const float* rscale, const int8_t* w8, const uint16_t* ws, TO* out, int64_t m,
+              int64_t n, int64_t k, hipStream_t stream) {
+  constexpr int kCols = gemv_cols<S, C>();
+  const int64_t lds = kCols * (k / 32) * 2;
+  if (lds > kGemvScaleLds) return false;
+  static std::once_flag attr_once;
+  std::call_once(attr_once, [] {
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&q8_gemv_kernel<TO, S, C>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, kGemvScaleLds);
+  });
+  const int64_t wgs = (n + kCols - 1) / kCols;
+  q8_gemv_kernel<TO, S, C><<<dim3((unsigned)wgs), dim3(kGemvWaves * 64), (size_t)((lds + 3) & ~3), stream>>>(
+      xq, rscale, w8, ws, out, m, n, k);
+  return true;
+}
+
 }  // namespace nvf
 
 using namespace nvf;
@@ -318,6 +509,8 @@ int check_gemm(const void* xq, const float* rscale, const void* w8, const void* 
   if (m < 0 || n < 0 || k < 0) return fail(NVF_ERR_INVALID, "%s: negative size", who);
   if (k % 32 != 0) return fail(NVF_ERR_INVALID, "%s: k=%lld is not a multiple of the Q8_0 block (32)", who, (long long)k);
   if (!dtype_ok(dtype)) return fail(NVF_ERR_INVALID, "%s: bad out dtype %d", who, dtype);
+  if (k > (int64_t)1 << 24)  // buffer offsets within a 128-row tile stay below 2^31
+    return fail(NVF_ERR_INVALID, "%s: k=%lld exceeds 2^24", who, (long long)k);
   if (m == 0 || n == 0 || k == 0) return NVF_OK;
   if (!xq || !rscale || !w8 || !ws || !out) return fail(NVF_ERR_INVALID, "%s: null pointer", who);
   if (!aligned16(xq) || !aligned16(w8))
@@ -331,6 +524,18 @@ int check_gemm(const void* xq, const float* rscale, const void* w8, const void* 
 template <typename TO>
 int launch_gemm(const int8_t* xq, const float* rscale, const int8_t* w8, const uint16_t* ws, TO* out, int64_t m,
                 int64_t n, int64_t k, hipStream_t stream) {
+  if (m <= kGemvMaxM) {
+    // Wide n: 4 column groups per wave (one activation load feeds four weight
+    // loads) and the fewest K splits that still give >= ~4096 waves; narrow n:
+    // one group per wave, K split 8 ways.  Smaller column sets when the staged
+    // scales would not fit.
+    const int64_t sets4 = (n + 63) / 64;
+    bool ok = false;
+    if (sets4 * 4 >= 4096) ok = try_gemv<TO, 4, 4>(xq, rscale, w8, ws, out, m, n, k, stream);
+    if (!ok && sets4 * 8 >= 4096) ok = try_gemv<TO, 8, 4>(xq, rscale, w8, ws, out, m, n, k, stream);
+    if (!ok) ok = try_gemv<TO, 8, 1>(xq, rscale, w8, ws, out, m, n, k, stream);
+    if (ok) return launch_status("q8_gemv_kernel");
+  }
   static std::once_flag attr_once;
   std::call_once(attr_once, [] {
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&q8_gemm_kernel<TO>),
