@@ -43,6 +43,7 @@ HBM_PEAK_GBS = 8000.0
 INT8_PEAK_OPS = 5.0e15  # MI355X dense int8 MFMA
 METRIC = "fused-op HBM GB/s (% of peak) + layer-op tokens/s at Qwen2.5-7B shapes"
 POOL_BYTES = 1 << 30
+GEMV_M = 8  # decode rows for the GEMV line
 
 
 def parse() -> argparse.Namespace:
@@ -55,7 +56,8 @@ def parse() -> argparse.Namespace:
     p.add_argument("--emb", default="", choices=["", "q8_0", "q8_0_blocks", "q4_k", "q5_k", "q6_k", "f16"],
                    help="embedding table format (default: the config's)")
     p.add_argument("--only", default="",
-                   help="comma list of ops (default emb,rms,rope,silu,copy,gemm); also emb_rms, rms_q8 (fusions)")
+                   help="comma list of ops (default emb,rms,rope,silu,copy,gemm,gemv); also emb_rms, rms_q8, "
+                        "silu_q8 (fusions)")
     return p.parse_args()
 
 
@@ -74,7 +76,11 @@ def op_bytes(cfg, e: int, emb_fmt: str) -> dict[str, int]:
             # layer-0 gather + norm: table rows + ids + residual and out writes
             "emb_rms": int(T * Hd * TABLE_BYTES_PER_ELEM[emb_fmt]) + 8 * T + 2 * T * Hd * e + Hd * e,
             # residual-add + RMSNorm + Q8 row scale + int8 row
-            "rms_q8": 4 * T * Hd * e + Hd * e + T * Hd + 4 * T}
+            "rms_q8": 4 * T * Hd * e + Hd * e + T * Hd + 4 * T,
+            # SwiGLU writing only the down projection's int8 rows and row scales
+            "silu_q8": 2 * T * I * e + T * I + 4 * T,
+            # decode GEMV (m = GEMV_M) at the gate_up shape: the weights once, plus activations and output
+            "gemv": int(2 * I * Hd * 34 / 32) + GEMV_M * Hd + 4 * GEMV_M + GEMV_M * 2 * I * e}
 
 
 def main() -> int:
@@ -100,7 +106,7 @@ def main() -> int:
     g = torch.Generator(device=dev).manual_seed(cfg.seed)
     emb_fmt = args.emb or cfg.emb
     nbytes = op_bytes(cfg, e, emb_fmt)
-    only = set(filter(None, args.only.split(","))) or {"emb", "rms", "rope", "silu", "copy", "gemm"}
+    only = set(filter(None, args.only.split(","))) or {"emb", "rms", "rope", "silu", "copy", "gemm", "gemv"}
 
     def nsets(b: int) -> int:
         return max(2, -(-POOL_BYTES // b))
@@ -147,6 +153,17 @@ def main() -> int:
         gws = torch.empty(2 * I * Hd // 32, device=dev).uniform_(1e-3, 1e-2, generator=g).half().view(torch.int16)
         gsc, gxq = ops.q8_quantize_rows(randn((T, Hd)))
         gemm_in = (gxq, gsc, gw8, gws, torch.empty(T, 2 * I, dtype=tdt, device=dev))
+    sq_sets = [(randn((T, 2 * I)), torch.empty(T, dtype=torch.float32, device=dev),
+                torch.empty(T, I, dtype=torch.int8, device=dev)) for _ in range(nsets(nbytes["silu_q8"]))] \
+        if "silu_q8" in only else []
+    gemv_sets = []
+    if "gemv" in only:  # weights rotated over >= 1 GiB so every launch streams them from HBM
+        gsc1, gxq1 = ops.q8_quantize_rows(randn((GEMV_M, Hd)))
+        for _ in range(nsets(nbytes["gemv"])):
+            gemv_sets.append((torch.randint(-127, 128, (2 * I * Hd,), generator=g, device=dev, dtype=torch.int8),
+                              torch.empty(2 * I * Hd // 32, device=dev).uniform_(1e-3, 1e-2, generator=g).half()
+                              .view(torch.int16)))
+        gemv_out = torch.empty(GEMV_M, 2 * I, dtype=tdt, device=dev)
     copy_pair = None
     if "copy" in only:  # 1 GiB plain copy: the attainable-bandwidth and traffic-counter reference
         copy_pair = (torch.ones(1 << 28, dtype=torch.int32, device=dev),
@@ -198,11 +215,21 @@ def main() -> int:
         xq_, sc_, w8_, ws_, out_ = gemm_in
         ops.matmul_q8_0(xq_, sc_, w8_, ws_, 2 * I, out=out_)
 
+    def run_silu_q8(i):
+        gu, sc, q = sq_sets[i % len(sq_sets)]
+        ops._check(ops.lib().nvf_silu_and_mul_q8(gu.data_ptr(), None, sc.data_ptr(), q.data_ptr(), T, I, ops._dt(gu),
+                                                 ops._stream()), "silu_and_mul_q8")
+
+    def run_gemv(i):
+        w8_, ws_ = gemv_sets[i % len(gemv_sets)]
+        ops.matmul_q8_0(gxq1, gsc1, w8_, ws_, 2 * I, out=gemv_out)
+
     def run_copy(i):
         ops.stream_copy(copy_pair[1], copy_pair[0])
 
     table = [("emb", run_emb), ("rms", run_rms), ("rope", run_rope), ("silu", run_silu), ("emb_rms", run_emb_rms),
-             ("rms_q8", run_rms_q8), ("copy", run_copy), ("gemm", run_gemm)]
+             ("rms_q8", run_rms_q8), ("silu_q8", run_silu_q8), ("copy", run_copy), ("gemm", run_gemm),
+             ("gemv", run_gemv)]
     active = [(n, f) for n, f in table if n in only]
 
     for i in range(args.warmup):
@@ -239,6 +266,9 @@ def main() -> int:
             gbs = nbytes[n] / (t_us * 1e-6) / 1e9
             entry.update({"bytes": nbytes[n], "GB_s": round(gbs, 1), "frac_of_peak": round(gbs / HBM_PEAK_GBS, 4),
                           "tokens_per_s": round(T / (t_us * 1e-6), 1)})
+        if n == "gemv":
+            entry.pop("tokens_per_s")
+            entry["shape"] = f"m={GEMV_M} n={2 * I} k={Hd} (gate_up, decode)"
         elif n == "gemm":
             ops_n = 2.0 * T * (2 * I) * Hd
             entry.update({"shape": f"m={T} n={2 * I} k={Hd} (gate_up)", "TOP_s": round(ops_n / (t_us * 1e-6) / 1e12, 1),
@@ -295,12 +325,13 @@ def main() -> int:
                    "kv_heads": cfg.kv_heads, "head_dim": cfg.head_dim, "value_is": "tokens / GPU time of one step (HIP events around all timed steps)",
                    "step_us": round(step_us, 2)},
         "ops": {k: v for k, v in res_ops.items() if k in ("emb", "rms", "rope", "silu")},
-        "fused_ops": {k: v for k, v in res_ops.items() if k in ("emb_rms", "rms_q8")} or None,
+        "fused_ops": {k: v for k, v in res_ops.items() if k in ("emb_rms", "rms_q8", "silu_q8")} or None,
         "attainable": ({"kernel": "nvf_stream_copy (1 GiB, 16 B non-temporal loads/stores)",
                         "GB_s": res_ops["copy"]["GB_s"],
                         "frac_of_peak": round(res_ops["copy"]["GB_s"] / HBM_PEAK_GBS, 4)} if "copy" in res_ops else None),
         "roofline": roofline,
         "q8_gemm": res_ops.get("gemm"),
+        "q8_gemv": res_ops.get("gemv"),
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

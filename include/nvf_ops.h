@@ -162,6 +162,15 @@ int nvf_embedding_rms_norm(const int64_t* ids, int format, const void* table, co
                            int64_t hidden, int64_t vocab, const void* weight, void* residual, void* out, float eps,
                            int dtype, void* stream);
 
+/* SwiGLU (as nvf_silu_and_mul, replacing hip_silu_and_mul, hip_ops.hpp:17) that also
+ * writes the Q8_0 down projection's quantized input: row_scale[r] = 127 / max|v[r,:]|
+ * (0 when the maximum is <= 1e-8) and q_out[r,i] = (int8) min(127, max(-127,
+ * v[r,i] * row_scale[r])), v the SwiGLU output as stored in `dtype` -- the
+ * reference's q8_row_scale_kernel and quantizer (hip_ops.hip:205-217, :244-245)
+ * applied to silu_and_mul's output (hip_ops.hip:419-429).  out may be NULL. */
+int nvf_silu_and_mul_q8(const void* gate_up, void* out, float* row_scale, int8_t* q_out, int64_t rows,
+                        int64_t inter, int dtype, void* stream);
+
 /* Per-row int8 quantization of activations for the Q8_0 GEMM: row_scale[r] =
  * 127 / max|x[r,:]| (0 when the maximum is <= 1e-8) and xq[r,i] = (int8)
  * min(127, max(-127, x[r,i] * row_scale[r])), truncating -- q8_row_scale_kernel

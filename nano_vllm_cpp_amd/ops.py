@@ -44,6 +44,7 @@ SIGNATURES: dict[str, tuple] = {
     "nvf_rms_norm": (_i32, [_vp, _vp, _vp, _i64, _i64, _f32, _i32, _vp]),
     "nvf_rms_norm_q8": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _f32, _i32, _vp]),
     "nvf_silu_and_mul": (_i32, [_vp, _vp, _i64, _i64, _i32, _vp]),
+    "nvf_silu_and_mul_q8": (_i32, [_vp, _vp, _vp, _vp, _i64, _i64, _i32, _vp]),
     "nvf_qk_norm_rope": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i32, _i32, _i32, _i64, _i64, _f32, _i32, _vp]),
     "nvf_embedding_q8_0": (_i32, [_vp, _vp, _vp, _i64, _i64, _i64, _vp, _i32, _vp]),
     "nvf_embedding_q8_0_blocks": (_i32, [_vp, _vp, _i64, _i64, _i64, _vp, _i32, _vp]),
@@ -193,6 +194,22 @@ def silu_and_mul(gate_up: torch.Tensor, out: torch.Tensor | None = None) -> torc
     _check(lib().nvf_silu_and_mul(_dev(gate_up, "gate_up"), _dev(out, "out"), rows, inter, _dt(gate_up), _stream()),
            "silu_and_mul")
     return out
+
+
+def silu_and_mul_q8(gate_up: torch.Tensor, want_out: bool = False):
+    """SwiGLU that also emits the Q8_0 GEMM's row scale and int8 rows.
+    Returns (out | None, row_scale, q)."""
+    rows, two_i = gate_up.shape
+    if two_i % 2:
+        raise ValueError("gate_up width must be even")
+    inter = two_i // 2
+    out = torch.empty((rows, inter), dtype=gate_up.dtype, device=gate_up.device) if want_out else None
+    scale = torch.empty(rows, dtype=torch.float32, device=gate_up.device)
+    q = torch.empty((rows, inter), dtype=torch.int8, device=gate_up.device)
+    _check(lib().nvf_silu_and_mul_q8(_dev(gate_up, "gate_up"), _dev(out, "out") if out is not None else None,
+                                     _dev(scale, "row_scale"), _dev(q, "q_out"), rows, inter, _dt(gate_up),
+                                     _stream()), "silu_and_mul_q8")
+    return out, scale, q
 
 
 # ---------------------------------------------------------------------------

@@ -96,6 +96,11 @@ def test_host_argument_checks():
     assert rc == -1 and "dtype" in msg
     assert lib.nvf_q8_quantize_rows(p, p, p, 0, 64, 0, None) == 0
     lib.hip_matmul_q8(p, p, p, 0, 8, 64, p)  # empty: returns before any HIP call
+    rc, msg = _status(lib.nvf_silu_and_mul_q8(p, None, None, p, 4, 64, 1, None))
+    assert rc == -1 and "NULL" in msg
+    rc, msg = _status(lib.nvf_silu_and_mul_q8(p, None, p, p, 4, 64, 3, None))
+    assert rc == -1 and "dtype" in msg
+    assert lib.nvf_silu_and_mul_q8(p, None, p, p, 0, 64, 1, None) == 0
 
 
 def test_inv_freq_host_helper_matches_oracle():

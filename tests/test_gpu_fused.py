@@ -4,7 +4,9 @@
   activation row scale and int8 row (the reference's q8_row_scale_kernel pass,
   src/hip_ops.hip:205-217, and its GEMM's quantizer, :244-245);
 * nvf_embedding_rms_norm -- layer-0 gather + residual-add onto zeros + RMSNorm
-  (src/model.cpp:756 then :762).
+  (src/model.cpp:756 then :762);
+* nvf_silu_and_mul_q8 -- SwiGLU (src/hip_ops.hip:419-429) emitting the down
+  projection's row scale and int8 rows.
 
 Bars: the row scale and int8 row bit-exact against the oracle's quantizer
 applied to the kernel's own stored output (the quantizer is exact arithmetic on
@@ -124,3 +126,59 @@ def test_embedding_rms_norm_bad_ids_and_args(gpu):
     assert np.isfinite(o[0]).all() and np.isnan(o[1:]).all()
     with pytest.raises(ops.NvfError, match="hidden"):
         ops.embedding_rms_norm(H.to_dev(ids, gpu), ops.EMB_Q4_K, H.to_dev(w8, gpu), None, 500, w[:500], 1e-6, V)
+
+
+@pytest.mark.parametrize("dt", DTYPES, ids=DT_IDS)
+@pytest.mark.parametrize("rows,inter", [(64, 18944), (33, 4864), (7, 999), (5, 12288), (3, 40)])
+def test_silu_and_mul_q8(gpu, dt, rows, inter):
+    """SwiGLU + the down projection's quantizer: the fp output is bit-identical to
+    nvf_silu_and_mul's, the scale and int8 rows bit-exact against the oracle's
+    quantizer on that output, and the output within the SwiGLU tolerance."""
+    o = H.oracle()
+    r = H.rng(rows * inter + dt)
+    gu = H.gen_act(r, (rows, 2 * inter), dt, 0.0, 2.0)
+    gu[1] = H.to_storage(np.zeros(2 * inter, np.float32), dt)  # an all-zero SwiGLU row: scale 0
+    d_gu = H.to_dev(gu, gpu, dt)
+    case(f"silu_and_mul_q8 rows={rows} inter={inter} dt={dt}")
+    out, scale, q = ops.silu_and_mul_q8(d_gu, want_out=True)
+    plain = ops.silu_and_mul(d_gu)
+    got_out = H.to_host(out)
+    H.assert_bitexact(got_out, H.to_host(plain), "fused fp output vs nvf_silu_and_mul")
+    ref = np.empty((rows, inter), H.NP_STORAGE[dt])
+    o.orc_silu_and_mul(H.ptr(gu), H.ptr(ref), rows, inter, dt)
+    H.assert_close(got_out, ref, dt, what="fused silu")
+    exp_scale = np.empty(rows, np.float32)
+    o.orc_q8_row_scale(H.ptr(got_out), H.ptr(exp_scale), rows, inter, dt)
+    H.assert_bitexact(scale.cpu().numpy(), exp_scale, "row scale")
+    exp_q = np.empty((rows, inter), np.int8)
+    o.orc_q8_quantize(H.ptr(got_out), H.ptr(exp_scale), exp_q.ctypes.data, rows, inter, dt)
+    H.assert_bitexact(q.cpu().numpy(), exp_q, "int8 rows")
+    assert scale[1].item() == 0.0
+    # without the fp output: the same scale and int8 rows
+    none, scale2, q2 = ops.silu_and_mul_q8(d_gu)
+    assert none is None
+    H.assert_bitexact(scale2.cpu().numpy(), exp_scale, "row scale (no out)")
+    H.assert_bitexact(q2.cpu().numpy(), exp_q, "int8 rows (no out)")
+
+
+@pytest.mark.parametrize("dt", [H.F16, H.BF16], ids=["f16", "bf16"])
+def test_fused_quantizers_feed_the_gemm(gpu, dt):
+    """The norm and the SwiGLU hand the GEMM exactly what quantizing their stored
+    output would: the products are bit-identical to quantize-then-GEMM."""
+    r = H.rng(91 + dt)
+    rows, hidden, inter, n = 40, 1024, 2048, 384
+    x, res = H.gen_act(r, (rows, hidden), dt), H.gen_act(r, (rows, hidden), dt)
+    w = H.gen_act(r, (hidden,), dt, 1.0, 0.1)
+    w8a, wsa = H.gen_q8_0(r, n, hidden)
+    w8b, wsb = H.gen_q8_0(r, n, inter)
+    gu = H.gen_act(r, (rows, 2 * inter), dt)
+    case(f"norm -> gemm, swiglu -> gemm dt={dt}")
+    d_res = H.to_dev(res, gpu, dt)
+    out, sc, q = ops.rms_norm_q8(H.to_dev(x, gpu, dt), H.to_dev(w, gpu, dt), 1e-6, d_res)
+    fused = ops.matmul_q8_0(q, sc, H.to_dev(w8a, gpu), H.to_dev(wsa, gpu), n, torch.float32)
+    plain = ops.matmul_q8(out, H.to_dev(w8a, gpu), H.to_dev(wsa, gpu), n, torch.float32)
+    H.assert_bitexact(fused.cpu().numpy(), plain.cpu().numpy(), "norm -> gemm")
+    sout, ssc, sq = ops.silu_and_mul_q8(H.to_dev(gu, gpu, dt), want_out=True)
+    fused = ops.matmul_q8_0(sq, ssc, H.to_dev(w8b, gpu), H.to_dev(wsb, gpu), n, torch.float32)
+    plain = ops.matmul_q8(sout, H.to_dev(w8b, gpu), H.to_dev(wsb, gpu), n, torch.float32)
+    H.assert_bitexact(fused.cpu().numpy(), plain.cpu().numpy(), "swiglu -> gemm")
