@@ -94,6 +94,21 @@ void hip_embedding_qk(const int64_t* ids, const uint8_t* wq, int tokens, int hid
  * (the reference's own policy, hip_ops.hip:642-648). */
 void hip_matmul_q8(const float* x, const uint8_t* w8, const uint16_t* ws, int m, int n, int k, float* out);
 
+/* hip_ops.hpp:22-23 -- k_cache[slot_mapping[t], :] = key[t, :], same for values
+ * (rows of kv_heads * head_dim fp32 values); slots < 0 are skipped. */
+void hip_store_kv(const float* key, const float* value, float* k_cache, float* v_cache, const int32_t* slot_mapping,
+                  int tokens, int kv_heads, int head_dim);
+
+/* hip_ops.hpp:25-28 -- paged attention over the fp32 cache [blocks * block_size,
+ * kv_heads, head_dim]: token t attends the first query_key_len[t] keys of
+ * sequence query_seq[t] (block_tables[seq * max_blocks + j / block_size]);
+ * out = softmax(scale * q . K) . V per head, 0 when query_key_len[t] <= 0.
+ * head_dim <= 256. */
+void hip_paged_attention(const float* q, float* out, const float* k_cache, const float* v_cache,
+                         const int32_t* query_seq, const int32_t* query_key_len, const int32_t* block_tables,
+                         int tokens, int q_heads, int kv_heads, int head_dim, int block_size, int max_blocks,
+                         float scale);
+
 /* ---- 2. typed entry points ---------------------------------------------- */
 
 /* Residual-add + RMSNorm (replaces hip_rms_norm_add, hip_ops.hpp:15).  All four
@@ -185,6 +200,22 @@ int nvf_q8_quantize_rows(const void* x, float* row_scale, int8_t* xq, int64_t ro
  * k a multiple of 32. */
 int nvf_matmul_q8_0(const int8_t* xq, const float* row_scale, const uint8_t* w8, const uint16_t* ws, int64_t m,
                     int64_t n, int64_t k, void* out, int out_dtype, void* stream);
+
+/* KV store (replaces hip_store_kv, hip_ops.hpp:22-23) with the cache in `dtype`;
+ * key / value rows are key_stride / value_stride elements apart (>= kv_heads *
+ * head_dim), so views into a packed qkv row work. */
+int nvf_store_kv(const void* key, const void* value, void* k_cache, void* v_cache, const int32_t* slot_mapping,
+                 int64_t tokens, int kv_heads, int head_dim, int64_t key_stride, int64_t value_stride, int dtype,
+                 void* stream);
+
+/* Paged attention (replaces hip_paged_attention, hip_ops.hpp:25-28) with q, out and
+ * the cache in `dtype` (fp32 math, one rounding of the output).  q rows are
+ * q_stride elements apart (>= q_heads * head_dim); out is [tokens, q_heads *
+ * head_dim].  q_heads % kv_heads == 0, head_dim <= 256. */
+int nvf_paged_attention(const void* q, void* out, const void* k_cache, const void* v_cache, const int32_t* query_seq,
+                        const int32_t* query_key_len, const int32_t* block_tables, int64_t tokens, int q_heads,
+                        int kv_heads, int head_dim, int block_size, int max_blocks, float scale, int64_t q_stride,
+                        int dtype, void* stream);
 
 /* Host helper: inv_freq[i] = (float)(1 / theta^(2i/head_dim)) in double, the
  * table Qwen3Model builds in its constructor (src/model.cpp:416-420).

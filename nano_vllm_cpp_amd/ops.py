@@ -38,6 +38,11 @@ SIGNATURES: dict[str, tuple] = {
     "hip_embedding_q8": (None, [_vp, _vp, _vp, _i32, _i32, _vp]),
     "hip_embedding_qk": (None, [_vp, _vp, _i32, _i32, _vp, _i32]),
     "hip_matmul_q8": (None, [_vp, _vp, _vp, _i32, _i32, _i32, _vp]),
+    "hip_store_kv": (None, [_vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32]),
+    "hip_paged_attention": (None, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _i32, _f32]),
+    "nvf_store_kv": (_i32, [_vp, _vp, _vp, _vp, _vp, _i64, _i32, _i32, _i64, _i64, _i32, _vp]),
+    "nvf_paged_attention": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i32, _i32, _i32, _i32, _i32, _f32, _i64,
+                                   _i32, _vp]),
     "nvf_q8_quantize_rows": (_i32, [_vp, _vp, _vp, _i64, _i64, _i32, _vp]),
     "nvf_matmul_q8_0": (_i32, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _i32, _vp]),
     "nvf_rms_norm_add": (_i32, [_vp, _vp, _vp, _vp, _i64, _i64, _f32, _i32, _vp]),
@@ -98,6 +103,17 @@ def _dev(t: torch.Tensor, name: str) -> int:
         raise ValueError(f"{name} must be a GPU tensor")
     if not t.is_contiguous():
         raise ValueError(f"{name} must be contiguous")
+    return t.data_ptr()
+
+
+def _dev_rows(t: torch.Tensor, name: str) -> int:
+    """Device pointer of a tensor whose rows (dim 0) may be strided but whose
+    remaining dimensions are contiguous within a row."""
+    if not t.is_cuda:
+        raise ValueError(f"{name} must be a GPU tensor")
+    if not t[0:1].reshape(-1).is_contiguous() or t.stride(-1) != 1 or \
+            (t.dim() > 2 and t.stride(-2) != t.shape[-1]):
+        raise ValueError(f"{name} must have contiguous rows")
     return t.data_ptr()
 
 
@@ -180,6 +196,37 @@ def matmul_q8(x: torch.Tensor, w8: torch.Tensor, ws: torch.Tensor, n: int,
     quantize the rows, then the int8 GEMM.  Output in out_dtype (default x's)."""
     scale, xq = q8_quantize_rows(x)
     return matmul_q8_0(xq, scale, w8, ws, n, out_dtype or x.dtype)
+
+
+# ---------------------------------------------------------------------------
+# KV cache and paged attention
+# ---------------------------------------------------------------------------
+def store_kv(key: torch.Tensor, value: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+             slot_mapping: torch.Tensor) -> None:
+    """k_cache[slot, ...] = key[t] (and values) for slot = slot_mapping[t] >= 0.
+    key/value [tokens, kv_heads, head_dim] (row stride from the tensor), caches
+    [rows, kv_heads, head_dim] contiguous."""
+    tokens, kv_heads, head_dim = key.shape
+    _check(lib().nvf_store_kv(_dev_rows(key, "key"), _dev_rows(value, "value"), _dev(k_cache, "k_cache"),
+                              _dev(v_cache, "v_cache"), _dev(slot_mapping, "slot_mapping"), tokens, kv_heads, head_dim,
+                              key.stride(0), value.stride(0), _dt(key), _stream()), "store_kv")
+
+
+def paged_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, query_seq: torch.Tensor,
+                    query_key_len: torch.Tensor, block_tables: torch.Tensor, block_size: int, scale: float,
+                    out: torch.Tensor | None = None) -> torch.Tensor:
+    """q [tokens, q_heads, head_dim] (row stride from the tensor); caches
+    [rows, kv_heads, head_dim]; block_tables [seqs, max_blocks] int32.
+    Returns out [tokens, q_heads, head_dim] in q's dtype."""
+    tokens, q_heads, head_dim = q.shape
+    kv_heads = k_cache.shape[1]
+    out = torch.empty((tokens, q_heads, head_dim), dtype=q.dtype, device=q.device) if out is None else out
+    _check(lib().nvf_paged_attention(_dev_rows(q, "q"), _dev(out, "out"), _dev(k_cache, "k_cache"),
+                                     _dev(v_cache, "v_cache"), _dev(query_seq, "query_seq"),
+                                     _dev(query_key_len, "query_key_len"), _dev(block_tables, "block_tables"), tokens,
+                                     q_heads, kv_heads, head_dim, block_size, block_tables.shape[1], scale, q.stride(0),
+                                     _dt(q), _stream()), "paged_attention")
+    return out
 
 
 # ---------------------------------------------------------------------------

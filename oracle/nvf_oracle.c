@@ -434,6 +434,88 @@ void orc_matmul_q8(const void* x, int dtype, const uint8_t* w8, const uint16_t* 
   if (!scale_out) free(sc);
 }
 
+/* ---- KV cache store and paged attention ----------------------------------- */
+
+/* src/hip_ops.hip:452-466 (store_kv_kernel): for each token t with
+ * slot = slot_mapping[t] >= 0, k_cache[slot, :] = key[t, :] and
+ * v_cache[slot, :] = value[t, :] (kv_heads * head_dim values, a plain copy in
+ * the storage dtype); slots < 0 are skipped. */
+void orc_store_kv(const void* key, const void* value, void* k_cache, void* v_cache, const int32_t* slot_mapping,
+                  int64_t tokens, int kv_heads, int head_dim, int dtype) {
+  const int64_t d = (int64_t)kv_heads * head_dim;
+  const size_t e = dtype == ORC_F32 ? 4 : 2;
+  for (int64_t t = 0; t < tokens; ++t) {
+    const int32_t slot = slot_mapping[t];
+    if (slot < 0) continue;
+    memcpy((char*)k_cache + (size_t)slot * d * e, (const char*)key + (size_t)t * d * e, (size_t)d * e);
+    memcpy((char*)v_cache + (size_t)slot * d * e, (const char*)value + (size_t)t * d * e, (size_t)d * e);
+  }
+}
+
+/* src/hip_ops.hip:473-550 (paged_attention_kernel).  For query token t and head
+ * h: seq = query_seq[t], L = query_key_len[t], kv head h / (q_heads / kv_heads);
+ * key j < L lives at cache row block_tables[seq * max_blocks + j / block_size] *
+ * block_size + j % block_size (rows of kv_heads * head_dim values, :468-471);
+ * out = softmax_j(scale * q . K_j) . V, and 0 when L <= 0 (:488-491).  The
+ * reference accumulates an online softmax over 64-key chunks in fp32; this
+ * computes the same quantity in double (max-subtracted exp, one division) and
+ * rounds once to `dtype`.  out_exact (optional) receives the double values and
+ * vmax (optional) max |V| over the attended keys per (t, h), the scale of the
+ * tolerances. */
+void orc_paged_attention(const void* q, void* out, const void* k_cache, const void* v_cache, const int32_t* query_seq,
+                         const int32_t* query_key_len, const int32_t* block_tables, int64_t tokens, int q_heads,
+                         int kv_heads, int head_dim, int block_size, int max_blocks, float scale, int dtype,
+                         double* out_exact, float* vmax) {
+  const int group = q_heads / kv_heads;
+  const int64_t kv_stride = (int64_t)kv_heads * head_dim, q_stride = (int64_t)q_heads * head_dim;
+  int64_t cap = 64;
+  double* sc = (double*)malloc(sizeof(double) * (size_t)cap);
+  double* acc = (double*)malloc(sizeof(double) * (size_t)head_dim);
+  for (int64_t t = 0; t < tokens; ++t) {
+    const int32_t L = query_key_len[t];
+    const int32_t seq = query_seq[t];
+    if (L > cap) {
+      cap = L;
+      sc = (double*)realloc(sc, sizeof(double) * (size_t)cap);
+    }
+    for (int h = 0; h < q_heads; ++h) {
+      const int kvh = h / group;
+      const int64_t qo = t * q_stride + (int64_t)h * head_dim;
+      double m = -INFINITY, vm = 0.0;
+      for (int32_t j = 0; j < L; ++j) {
+        const int64_t row = (int64_t)block_tables[(int64_t)seq * max_blocks + j / block_size] * block_size +
+                            j % block_size;
+        double dot = 0.0;
+        for (int d = 0; d < head_dim; ++d)
+          dot += (double)orc_load(q, qo + d, dtype) * (double)orc_load(k_cache, row * kv_stride + kvh * head_dim + d, dtype);
+        sc[j] = dot * (double)scale;
+        if (sc[j] > m) m = sc[j];
+      }
+      double sum = 0.0;
+      for (int d = 0; d < head_dim; ++d) acc[d] = 0.0;
+      for (int32_t j = 0; j < L; ++j) {
+        const int64_t row = (int64_t)block_tables[(int64_t)seq * max_blocks + j / block_size] * block_size +
+                            j % block_size;
+        const double p = exp(sc[j] - m);
+        sum += p;
+        for (int d = 0; d < head_dim; ++d) {
+          const double v = (double)orc_load(v_cache, row * kv_stride + kvh * head_dim + d, dtype);
+          acc[d] += p * v;
+          if (fabs(v) > vm) vm = fabs(v);
+        }
+      }
+      for (int d = 0; d < head_dim; ++d) {
+        const double o = L > 0 ? acc[d] / sum : 0.0;
+        orc_store(out, qo + d, (float)o, dtype);
+        if (out_exact) out_exact[qo + d] = o;
+      }
+      if (vmax) vmax[t * q_heads + h] = (float)vm;
+    }
+  }
+  free(acc);
+  free(sc);
+}
+
 /* ---- layer-0 embedding + residual-add + RMSNorm -------------------------- */
 
 void orc_embedding_rms_norm(const int64_t* ids, int format, const void* table, const void* scales, int64_t tokens,

@@ -33,6 +33,12 @@
  *                              zero rows give scale 0), truncation toward zero
  *   embedding + layer-0 norm . equal to the composition gather ->
  *                              rms_norm_add with a zero residual
+ *   paged attention .......... one key -> that V row; q = 0 -> the mean of the
+ *                              attended V rows; L = 0 -> zeros; invariant under a
+ *                              permutation of physical blocks; equal to a dense
+ *                              numpy softmax(q K^T) V; on the GPU box within the
+ *                              tolerance of the reference's hip_paged_attention
+ *   KV store ................. a copy: rows land at their slots, slot -1 skipped
  *   Q8_0 GEMM ................ exact on power-of-two scales against a textbook
  *                              matmul of the dequantized weights; the error bound
  *                              holds for fp32 sums in every order; on the GPU box
@@ -98,6 +104,16 @@ void orc_matmul_q8_i8(const int8_t* xq, const float* scale, const uint8_t* w8, c
                       int64_t n, int64_t k, double* out, double* err);
 void orc_matmul_q8(const void* x, int dtype, const uint8_t* w8, const uint16_t* ws, int64_t m, int64_t n, int64_t k,
                    double* out, double* err, float* scale_out, int8_t* xq_out);
+
+/* KV store (src/hip_ops.hip:452-466) and paged attention (:468-550): see the
+ * definitions for the exact indexing; attention is computed in double and
+ * rounded once to dtype (out_exact / vmax optional). */
+void orc_store_kv(const void* key, const void* value, void* k_cache, void* v_cache, const int32_t* slot_mapping,
+                  int64_t tokens, int kv_heads, int head_dim, int dtype);
+void orc_paged_attention(const void* q, void* out, const void* k_cache, const void* v_cache, const int32_t* query_seq,
+                         const int32_t* query_key_len, const int32_t* block_tables, int64_t tokens, int q_heads,
+                         int kv_heads, int head_dim, int block_size, int max_blocks, float scale, int dtype,
+                         double* out_exact, float* vmax);
 
 /* Layer-0 embedding + residual-add + RMSNorm (src/model.cpp:756 then :762 with
  * the zero-filled residual): residual = emb + 0, out = RMSNorm(residual) * w.

@@ -45,6 +45,19 @@ void ref_hip_matmul_q8_async(const float* x, const uint8_t* w8, const uint16_t* 
                              float* out) {
   hip_matmul_q8(x, w8, ws, m, n, k, out);
 }
+void ref_hip_store_kv(const float* key, const float* value, float* k_cache, float* v_cache, const int32_t* slots,
+                      int tokens, int kv_heads, int head_dim) {
+  hip_store_kv(key, value, k_cache, v_cache, slots, tokens, kv_heads, head_dim);
+  HIP_CHECK(hipDeviceSynchronize());
+}
+void ref_hip_paged_attention(const float* q, float* out, const float* k_cache, const float* v_cache,
+                             const int32_t* query_seq, const int32_t* query_key_len, const int32_t* block_tables,
+                             int tokens, int q_heads, int kv_heads, int head_dim, int block_size, int max_blocks,
+                             float scale) {
+  hip_paged_attention(q, out, k_cache, v_cache, query_seq, query_key_len, block_tables, tokens, q_heads, kv_heads,
+                      head_dim, block_size, max_blocks, scale);
+  HIP_CHECK(hipDeviceSynchronize());
+}
 void ref_hip_embedding_u16(const int64_t* ids, const uint16_t* table, int tokens, int hidden, float* out,
                            int table_bf16) {
   hip_embedding_u16(ids, table, tokens, hidden, out, table_bf16 != 0);

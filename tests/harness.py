@@ -45,6 +45,9 @@ _ORACLE_SIGS = {
     "orc_q8_quantize": (None, [_vp, _vp, _vp, _i64, _i64, _i32]),
     "orc_embedding_rms_norm": (None, [_vp, _i32, _vp, _vp, _i64, _i64, _vp, _vp, _vp, _f32, _i32]),
     "orc_matmul_q8_i8": (None, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _vp]),
+    "orc_store_kv": (None, [_vp, _vp, _vp, _vp, _vp, _i64, _i32, _i32, _i32]),
+    "orc_paged_attention": (None, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i32, _i32, _i32, _i32, _i32, _f32,
+                                   _i32, _vp, _vp]),
     "orc_matmul_q8": (None, [_vp, _i32, _vp, _vp, _i64, _i64, _i64, _vp, _vp, _vp, _vp]),
 }
 
@@ -95,6 +98,8 @@ def ref_hip() -> C.CDLL | None:
     h.ref_hip_embedding_qk.argtypes = [_vp, _vp, _i32, _i32, _vp, _i32]
     h.ref_hip_embedding_u16.argtypes = [_vp, _vp, _i32, _i32, _vp, _i32]
     h.ref_hip_matmul_q8.argtypes = [_vp, _vp, _vp, _i32, _i32, _i32, _vp]
+    h.ref_hip_store_kv.argtypes = [_vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32]
+    h.ref_hip_paged_attention.argtypes = [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _i32, _f32]
     return h
 
 
@@ -371,3 +376,64 @@ def smoke_chain(device: str = "cuda:0") -> None:
     assert_close(host(out), ref, dt, what="smoke silu_and_mul")
     torch.cuda.synchronize(device)
 
+
+
+# ---------------------------------------------------------------------------
+# paged KV batches (src/model_runner.cpp:43-128 semantics)
+# ---------------------------------------------------------------------------
+@dataclass
+class PagedBatch:
+    """A batch of sequences over a paged KV cache: per-token (query_seq,
+    query_key_len), block tables of randomly permuted physical blocks, and caches
+    [num_blocks * block_size, kv_heads, head_dim] filled with N(0, 1) values
+    (the rows the queries attend hold the sequences' keys/values)."""
+    q: np.ndarray
+    k_cache: np.ndarray
+    v_cache: np.ndarray
+    query_seq: np.ndarray
+    query_key_len: np.ndarray
+    block_tables: np.ndarray
+    tokens: int
+    max_blocks: int
+    num_blocks: int
+
+
+def make_paged(r: np.random.Generator, ctx_lens: list[int], q_lens: list[int], q_heads: int, kv_heads: int,
+               head_dim: int, block_size: int, dt: int, spare_blocks: int = 3) -> PagedBatch:
+    """Sequence s has ctx_lens[s] keys in the cache and q_lens[s] query tokens at
+    its last positions (prefill: q_len = ctx_len; decode: q_len = 1), each
+    query's key_len = its position + 1, as prepare_prefill/prepare_decode build them."""
+    need = [-(-c // block_size) for c in ctx_lens]
+    max_blocks = max(max(need), 1)
+    num_blocks = sum(need) + spare_blocks
+    perm = r.permutation(num_blocks).astype(np.int32)
+    tables = np.full((len(ctx_lens), max_blocks), -1, np.int32)
+    o = 0
+    for s_, nb in enumerate(need):
+        tables[s_, :nb] = perm[o:o + nb]
+        o += nb
+    qs, ql = [], []
+    for s_, (c, n) in enumerate(zip(ctx_lens, q_lens)):
+        for i in range(n):
+            qs.append(s_)
+            ql.append(c - n + i + 1)
+    tokens = len(qs)
+    rows = num_blocks * block_size
+    k_cache = gen_act(r, (rows, kv_heads, head_dim), dt)
+    v_cache = gen_act(r, (rows, kv_heads, head_dim), dt)
+    q = gen_act(r, (tokens, q_heads, head_dim), dt)
+    return PagedBatch(q, k_cache, v_cache, np.array(qs, np.int32), np.array(ql, np.int32), tables, tokens,
+                      max_blocks, num_blocks)
+
+
+def oracle_attention(b: PagedBatch, q_heads: int, kv_heads: int, head_dim: int, block_size: int, scale: float,
+                     dt: int):
+    """(out in storage dtype, exact double values, vmax per (token, head))."""
+    o = oracle()
+    out = np.empty_like(b.q)
+    exact = np.empty(b.q.shape, np.float64)
+    vmax = np.empty((b.tokens, q_heads), np.float32)
+    o.orc_paged_attention(ptr(b.q), ptr(out), ptr(b.k_cache), ptr(b.v_cache), ptr(b.query_seq), ptr(b.query_key_len),
+                          ptr(b.block_tables), b.tokens, q_heads, kv_heads, head_dim, block_size, b.max_blocks, scale,
+                          dt, ptr(exact), ptr(vmax))
+    return out, exact, vmax

@@ -1,0 +1,154 @@
+"""GPU parity of the KV-cache store and paged attention (the reference's
+hip_store_kv / hip_paged_attention, src/hip_ops.hip:452-550, 724-744).
+
+Bars:
+* store: bit-exact (a copy), slot -1 skipped, strided key/value rows;
+* attention: |got - exact| <= tol with `exact` the oracle's double value and
+  tol = 1e-4 * max|V| over the attended keys (fp32 online-softmax rounding over
+  up to a few thousand keys; a typical error is two orders smaller), plus one
+  ulp of a 16-bit output; 0 rows for key_len 0, the V row itself for one key;
+* against the reference's own hip_paged_attention (fp32, same inputs): within
+  twice that tolerance.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from nano_vllm_cpp_amd import ops
+from tests import harness as H
+
+pytestmark = pytest.mark.gpu
+
+DTYPES = [H.F32, H.F16, H.BF16]
+DT_IDS = ["f32", "f16", "bf16"]
+
+
+def case(msg: str) -> None:
+    print(f"[case] {msg}", flush=True)
+
+
+def tol_for(exact: np.ndarray, vmax: np.ndarray, dt: int, rel: float = 1e-4) -> np.ndarray:
+    t = rel * vmax[..., None] * np.ones_like(exact) + 1e-7
+    if dt != H.F32:
+        t = t + H.ulp(exact, dt)
+    return t
+
+
+def assert_attn(got: np.ndarray, exact: np.ndarray, vmax: np.ndarray, dt: int, what: str, factor: float = 1.0):
+    g = H.from_storage(got, dt)
+    tol = factor * tol_for(exact, vmax, dt)
+    bad = ~(np.abs(g - exact) <= tol)
+    if bad.any():
+        i = tuple(np.argwhere(bad)[0])
+        raise AssertionError(f"{what}: {bad.sum()} of {bad.size} outside tolerance; first {i}: got {g[i]!r} "
+                             f"exact {exact[i]!r} tol {tol[i]!r}")
+
+
+def run_attention(gpu, b: H.PagedBatch, q_heads, kv_heads, hd, bs, scale, dt):
+    return ops.paged_attention(H.to_dev(b.q, gpu, dt), H.to_dev(b.k_cache, gpu, dt), H.to_dev(b.v_cache, gpu, dt),
+                               H.to_dev(b.query_seq, gpu), H.to_dev(b.query_key_len, gpu),
+                               H.to_dev(b.block_tables, gpu), bs, scale)
+
+
+@pytest.mark.parametrize("dt", DTYPES, ids=DT_IDS)
+def test_store_kv(gpu, dt):
+    r = H.rng(7 + dt)
+    T, kvh, hd, rows = 37, 4, 128, 64
+    qkv = H.gen_act(r, (T, (8 + 2 * kvh) * hd), dt)  # packed [q | k | v] rows: strided views
+    kc0 = H.gen_act(r, (rows, kvh, hd), dt)
+    vc0 = H.gen_act(r, (rows, kvh, hd), dt)
+    slots = r.permutation(rows)[:T].astype(np.int32)
+    slots[[3, 10]] = -1
+    o = H.oracle()
+    key = np.ascontiguousarray(qkv[:, 8 * hd:(8 + kvh) * hd])
+    val = np.ascontiguousarray(qkv[:, (8 + kvh) * hd:])
+    kc_ref, vc_ref = kc0.copy(), vc0.copy()
+    o.orc_store_kv(H.ptr(key), H.ptr(val), H.ptr(kc_ref), H.ptr(vc_ref), H.ptr(slots), T, kvh, hd, dt)
+    d_qkv = H.to_dev(qkv, gpu, dt)
+    kc, vc = H.to_dev(kc0, gpu, dt), H.to_dev(vc0, gpu, dt)
+    case(f"store_kv dt={dt}")
+    k_view = d_qkv[:, 8 * hd:(8 + kvh) * hd].view(T, kvh, hd)
+    v_view = d_qkv[:, (8 + kvh) * hd:].view(T, kvh, hd)
+    ops.store_kv(k_view, v_view, kc, vc, H.to_dev(slots, gpu))
+    H.assert_bitexact(H.to_host(kc), kc_ref, "k cache")
+    H.assert_bitexact(H.to_host(vc), vc_ref, "v cache")
+
+
+CASES = [
+    # (ctx_lens, q_lens, q_heads, kv_heads, head_dim, block_size)
+    ([17, 64, 130], [17, 64, 130], 8, 2, 128, 16),       # prefill, several blocks per sequence
+    ([300, 1, 77, 513], [1, 1, 1, 1], 28, 4, 128, 256),  # decode, Qwen2.5-7B heads
+    ([40, 200], [5, 200], 4, 4, 64, 32),                  # chunked prefill with a cached prefix
+    ([9, 33], [9, 2], 6, 3, 80, 8),                       # odd head_dim
+]
+
+
+@pytest.mark.parametrize("dt", DTYPES, ids=DT_IDS)
+@pytest.mark.parametrize("ci", range(len(CASES)))
+def test_paged_attention_vs_oracle(gpu, dt, ci):
+    ctx, ql, qh, kvh, hd, bs = CASES[ci]
+    r = H.rng(100 + ci * 3 + dt)
+    b = H.make_paged(r, ctx, ql, qh, kvh, hd, bs, dt)
+    scale = float(hd) ** -0.5
+    _, exact, vmax = H.oracle_attention(b, qh, kvh, hd, bs, scale, dt)
+    case(f"paged_attention case={ci} dt={dt}")
+    got = H.to_host(run_attention(gpu, b, qh, kvh, hd, bs, scale, dt))
+    assert_attn(got, exact, vmax, dt, "attention")
+
+
+def test_paged_attention_closed_forms(gpu):
+    """key_len 0 -> zeros; one key -> exactly that V row."""
+    r = H.rng(5)
+    b = H.make_paged(r, [1, 20], [1, 1], 4, 2, 128, 16, H.F32)
+    b.query_key_len[:] = [1, 0]
+    case("paged_attention closed forms")
+    got = run_attention(gpu, b, 4, 2, 128, 16, 0.1, H.F32).cpu().numpy()
+    row0 = b.block_tables[0, 0] * 16
+    for h in range(4):
+        assert np.array_equal(got[0, h], b.v_cache[row0, h // 2])
+    assert not got[1].any()
+
+
+def test_dropins_vs_oracle_and_reference(gpu):
+    ctx, ql, qh, kvh, hd, bs = [57, 130, 5], [57, 2, 5], 8, 2, 128, 32
+    r = H.rng(9)
+    b = H.make_paged(r, ctx, ql, qh, kvh, hd, bs, H.F32)
+    scale = float(hd) ** -0.5
+    _, exact, vmax = H.oracle_attention(b, qh, kvh, hd, bs, scale, H.F32)
+    dq, dk, dv = H.to_dev(b.q, gpu), H.to_dev(b.k_cache, gpu), H.to_dev(b.v_cache, gpu)
+    dqs, dql, dtab = H.to_dev(b.query_seq, gpu), H.to_dev(b.query_key_len, gpu), H.to_dev(b.block_tables, gpu)
+    out = torch.empty_like(dq)
+    case("hip_paged_attention drop-in")
+    ops.lib().hip_paged_attention(dq.data_ptr(), out.data_ptr(), dk.data_ptr(), dv.data_ptr(), dqs.data_ptr(),
+                                  dql.data_ptr(), dtab.data_ptr(), b.tokens, qh, kvh, hd, bs, b.max_blocks, scale)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    assert_attn(got, exact, vmax, H.F32, "drop-in")
+    # store: the new tokens' keys and values into fresh slots, drop-in vs oracle
+    T = 6
+    key, val = H.gen_act(r, (T, kvh, hd), H.F32), H.gen_act(r, (T, kvh, hd), H.F32)
+    slots = np.array([0, 5, -1, 40, 41, 90], np.int32)
+    kc_ref, vc_ref = b.k_cache.copy(), b.v_cache.copy()
+    H.oracle().orc_store_kv(H.ptr(key), H.ptr(val), H.ptr(kc_ref), H.ptr(vc_ref), H.ptr(slots), T, kvh, hd, H.F32)
+    dkey, dval, dsl = H.to_dev(key, gpu), H.to_dev(val, gpu), H.to_dev(slots, gpu)
+    case("hip_store_kv drop-in")
+    ops.lib().hip_store_kv(dkey.data_ptr(), dval.data_ptr(), dk.data_ptr(), dv.data_ptr(), dsl.data_ptr(), T, kvh, hd)
+    torch.cuda.synchronize()
+    H.assert_bitexact(dk.cpu().numpy(), kc_ref, "k cache")
+    H.assert_bitexact(dv.cpu().numpy(), vc_ref, "v cache")
+    ref = H.ref_hip()
+    if ref is None:
+        return
+    # the reference's own kernels on the same (pre-store) inputs
+    rk, rv = H.to_dev(b.k_cache, gpu), H.to_dev(b.v_cache, gpu)
+    rout = torch.empty_like(dq)
+    case("reference hip_paged_attention")
+    ref.ref_hip_paged_attention(dq.data_ptr(), rout.data_ptr(), rk.data_ptr(), rv.data_ptr(), dqs.data_ptr(),
+                                dql.data_ptr(), dtab.data_ptr(), b.tokens, qh, kvh, hd, bs, b.max_blocks, scale)
+    rg = rout.cpu().numpy()
+    assert_attn(rg, exact, vmax, H.F32, "reference vs oracle")
+    assert (np.abs(got.astype(np.float64) - rg) <= 2 * tol_for(exact, vmax, H.F32)).all()
+    ref.ref_hip_store_kv(dkey.data_ptr(), dval.data_ptr(), rk.data_ptr(), rv.data_ptr(), dsl.data_ptr(), T, kvh, hd)
+    H.assert_bitexact(rk.cpu().numpy(), kc_ref, "reference k cache")

@@ -501,3 +501,86 @@ def test_matmul_q8_bound_covers_fp32_summation_orders(o):
         got = (acc * adq[:, None]).astype(np.float64)
         assert (np.abs(got - out) <= err).all()
     assert (np.abs(out) > 0).any()
+
+
+# ---------------------------------------------------------------------------
+# KV store and paged attention (src/hip_ops.hip:452-550)
+# ---------------------------------------------------------------------------
+def _dense_reference(b, q_heads, kv_heads, hd, bs, scale):
+    """A textbook route: gather each sequence's keys densely, softmax(q K^T) V in numpy."""
+    qf = b.q.astype(np.float64)
+    kf = b.k_cache.astype(np.float64)
+    vf = b.v_cache.astype(np.float64)
+    out = np.zeros(qf.shape)
+    g = q_heads // kv_heads
+    for t in range(b.tokens):
+        L = int(b.query_key_len[t])
+        if L <= 0:
+            continue
+        s_ = int(b.query_seq[t])
+        rows = np.array([b.block_tables[s_, j // bs] * bs + j % bs for j in range(L)])
+        for h in range(q_heads):
+            K = kf[rows, h // g]
+            V = vf[rows, h // g]
+            sc = K @ qf[t, h] * scale
+            p = np.exp(sc - sc.max())
+            out[t, h] = p @ V / p.sum()
+    return out
+
+
+def test_paged_attention_matches_dense_softmax(o):
+    r = H.rng(40)
+    b = H.make_paged(r, [5, 17, 33], [5, 3, 1], 6, 2, 16, 8, H.F32)
+    out, exact, vmax = H.oracle_attention(b, 6, 2, 16, 8, 0.25, H.F32)
+    dense = _dense_reference(b, 6, 2, 16, 8, 0.25)
+    assert np.allclose(exact, dense, rtol=1e-12, atol=1e-12)
+    assert np.array_equal(out, exact.astype(np.float32))
+    assert (vmax > 0).all()
+
+
+def test_paged_attention_closed_forms(o):
+    """One key -> that V row exactly; q = 0 -> the mean of the attended V rows;
+    key_len 0 -> zeros."""
+    r = H.rng(41)
+    b = H.make_paged(r, [1, 9], [1, 1], 4, 4, 8, 4, H.F32)
+    b.q[1] = 0.0
+    b.query_key_len[:] = [1, 9]
+    out, exact, _ = H.oracle_attention(b, 4, 4, 8, 4, 0.3, H.F32)
+    row0 = b.block_tables[0, 0] * 4
+    assert np.array_equal(out[0], b.v_cache[row0])
+    rows = [b.block_tables[1, j // 4] * 4 + j % 4 for j in range(9)]
+    assert np.allclose(exact[1], b.v_cache[rows].astype(np.float64).mean(axis=0), rtol=1e-12, atol=1e-13)
+    b.query_key_len[:] = [0, 0]
+    out, _, _ = H.oracle_attention(b, 4, 4, 8, 4, 0.3, H.F32)
+    assert not out.any()
+
+
+def test_paged_attention_block_permutation_invariance(o):
+    """Relocating the physical blocks (and the table with them) changes nothing."""
+    r = H.rng(42)
+    b = H.make_paged(r, [24, 10], [4, 10], 4, 2, 8, 4, H.BF16)
+    out1, _, _ = H.oracle_attention(b, 4, 2, 8, 4, 0.35, H.BF16)
+    perm = r.permutation(b.num_blocks)
+    inv = np.argsort(perm)
+    kc = b.k_cache.reshape(b.num_blocks, 4, 2, 8)[perm].reshape(b.k_cache.shape)
+    vc = b.v_cache.reshape(b.num_blocks, 4, 2, 8)[perm].reshape(b.v_cache.shape)
+    tables = np.where(b.block_tables >= 0, inv[np.maximum(b.block_tables, 0)], -1).astype(np.int32)
+    b2 = H.PagedBatch(b.q, np.ascontiguousarray(kc), np.ascontiguousarray(vc), b.query_seq, b.query_key_len, tables,
+                      b.tokens, b.max_blocks, b.num_blocks)
+    out2, _, _ = H.oracle_attention(b2, 4, 2, 8, 4, 0.35, H.BF16)
+    assert np.array_equal(out1, out2)
+
+
+@pytest.mark.parametrize("dt", [H.F32, H.BF16])
+def test_store_kv_is_a_slot_copy(o, dt):
+    r = H.rng(43)
+    T, kvh, hd, rows = 6, 2, 8, 20
+    key, val = H.gen_act(r, (T, kvh, hd), dt), H.gen_act(r, (T, kvh, hd), dt)
+    kc, vc = np.zeros((rows, kvh, hd), H.NP_STORAGE[dt]), np.zeros((rows, kvh, hd), H.NP_STORAGE[dt])
+    slots = np.array([3, 0, -1, 19, 7, 8], np.int32)
+    o.orc_store_kv(H.ptr(key), H.ptr(val), H.ptr(kc), H.ptr(vc), H.ptr(slots), T, kvh, hd, dt)
+    for t, sl in enumerate(slots):
+        if sl >= 0:
+            assert np.array_equal(kc[sl], key[t]) and np.array_equal(vc[sl], val[t])
+    untouched = np.setdiff1d(np.arange(rows), slots[slots >= 0])
+    assert not kc[untouched].any() and not vc[untouched].any()
