@@ -56,8 +56,8 @@ def parse() -> argparse.Namespace:
     p.add_argument("--emb", default="", choices=["", "q8_0", "q8_0_blocks", "q4_k", "q5_k", "q6_k", "f16"],
                    help="embedding table format (default: the config's)")
     p.add_argument("--only", default="",
-                   help="comma list of ops (default emb,rms,rope,silu,copy,gemm,gemv); also emb_rms, rms_q8, "
-                        "silu_q8 (fusions)")
+                   help="comma list of ops (default emb,rms,rope,silu,copy,gemm,gemv,attn,attn_decode); "
+                        "also emb_rms, rms_q8, silu_q8 (fusions)")
     return p.parse_args()
 
 
@@ -106,7 +106,8 @@ def main() -> int:
     g = torch.Generator(device=dev).manual_seed(cfg.seed)
     emb_fmt = args.emb or cfg.emb
     nbytes = op_bytes(cfg, e, emb_fmt)
-    only = set(filter(None, args.only.split(","))) or {"emb", "rms", "rope", "silu", "copy", "gemm", "gemv"}
+    only = set(filter(None, args.only.split(","))) or {"emb", "rms", "rope", "silu", "copy", "gemm", "gemv", "attn",
+                                                       "attn_decode"}
 
     def nsets(b: int) -> int:
         return max(2, -(-POOL_BYTES // b))
@@ -164,6 +165,38 @@ def main() -> int:
                               torch.empty(2 * I * Hd // 32, device=dev).uniform_(1e-3, 1e-2, generator=g).half()
                               .view(torch.int16)))
         gemv_out = torch.empty(GEMV_M, 2 * I, dtype=tdt, device=dev)
+    attn_in = attn_dec = None
+    bs_kv = 256  # the reference's KV block size (a multiple of 256, config.hpp:254)
+    if "attn" in only:  # causal prefill over the config's sequences, KV already in the paged cache
+        pos = cfg.positions()
+        lens = [int(n) for n in np.diff(cfg.cu_seqlens())]
+        nblk = [-(-n // bs_kv) for n in lens]
+        tables = torch.full((len(lens), max(nblk)), -1, dtype=torch.int32)
+        perm = torch.randperm(sum(nblk), generator=torch.Generator().manual_seed(cfg.seed))
+        o_ = 0
+        for s_, nb in enumerate(nblk):
+            tables[s_, :nb] = perm[o_:o_ + nb]
+            o_ += nb
+        rows = sum(nblk) * bs_kv
+        attn_in = (randn((T, cfg.q_heads, cfg.head_dim)), randn((rows, cfg.kv_heads, cfg.head_dim)),
+                   randn((rows, cfg.kv_heads, cfg.head_dim)),
+                   torch.from_numpy(np.repeat(np.arange(len(lens), dtype=np.int32), lens)).to(dev),
+                   torch.from_numpy((pos + 1).astype(np.int32)).to(dev), tables.to(dev))
+        attn_flops = 4.0 * cfg.q_heads * cfg.head_dim * float((pos + 1).sum())
+    if "attn_decode" in only:  # one token per sequence, 256 sequences, context uniform in 1..4096
+        ctx = np.random.default_rng(cfg.seed + 11).integers(1, 4097, 256)
+        nblk = [-(-int(n) // bs_kv) for n in ctx]
+        tables = torch.full((256, max(nblk)), -1, dtype=torch.int32)
+        perm = torch.randperm(sum(nblk), generator=torch.Generator().manual_seed(cfg.seed + 1))
+        o_ = 0
+        for s_, nb in enumerate(nblk):
+            tables[s_, :nb] = perm[o_:o_ + nb]
+            o_ += nb
+        rows = sum(nblk) * bs_kv
+        attn_dec = (randn((256, cfg.q_heads, cfg.head_dim)), randn((rows, cfg.kv_heads, cfg.head_dim)),
+                    randn((rows, cfg.kv_heads, cfg.head_dim)), torch.arange(256, dtype=torch.int32, device=dev),
+                    torch.from_numpy(ctx.astype(np.int32)).to(dev), tables.to(dev))
+        dec_bytes = float(ctx.sum()) * cfg.kv_heads * cfg.head_dim * 2 * e + 2 * 256 * cfg.q_heads * cfg.head_dim * e
     copy_pair = None
     if "copy" in only:  # 1 GiB plain copy: the attainable-bandwidth and traffic-counter reference
         copy_pair = (torch.ones(1 << 28, dtype=torch.int32, device=dev),
@@ -224,12 +257,23 @@ def main() -> int:
         w8_, ws_ = gemv_sets[i % len(gemv_sets)]
         ops.matmul_q8_0(gxq1, gsc1, w8_, ws_, 2 * I, out=gemv_out)
 
+    def run_attn(i):
+        q_, kc_, vc_, qs_, ql_, tb_ = attn_in
+        ops.paged_attention(q_, kc_, vc_, qs_, ql_, tb_, bs_kv, cfg.head_dim ** -0.5, out=attn_out)
+
+    def run_attn_decode(i):
+        q_, kc_, vc_, qs_, ql_, tb_ = attn_dec
+        ops.paged_attention(q_, kc_, vc_, qs_, ql_, tb_, bs_kv, cfg.head_dim ** -0.5, out=dec_out, max_query_len=1)
+
+    attn_out = torch.empty_like(attn_in[0]) if attn_in is not None else None
+    dec_out = torch.empty_like(attn_dec[0]) if attn_dec is not None else None
+
     def run_copy(i):
         ops.stream_copy(copy_pair[1], copy_pair[0])
 
     table = [("emb", run_emb), ("rms", run_rms), ("rope", run_rope), ("silu", run_silu), ("emb_rms", run_emb_rms),
              ("rms_q8", run_rms_q8), ("silu_q8", run_silu_q8), ("copy", run_copy), ("gemm", run_gemm),
-             ("gemv", run_gemv)]
+             ("gemv", run_gemv), ("attn", run_attn), ("attn_decode", run_attn_decode)]
     active = [(n, f) for n, f in table if n in only]
 
     for i in range(args.warmup):
@@ -273,6 +317,16 @@ def main() -> int:
             ops_n = 2.0 * T * (2 * I) * Hd
             entry.update({"shape": f"m={T} n={2 * I} k={Hd} (gate_up)", "TOP_s": round(ops_n / (t_us * 1e-6) / 1e12, 1),
                           "frac_of_int8_peak": round(ops_n / (t_us * 1e-6) / INT8_PEAK_OPS, 4)})
+        elif n == "attn":
+            entry.update({"shape": f"causal prefill {len(np.diff(cfg.cu_seqlens()))} x {T // len(np.diff(cfg.cu_seqlens()))}"
+                                   f" tokens, {cfg.q_heads}/{cfg.kv_heads} heads x {cfg.head_dim}, KV block {bs_kv}",
+                          "TFLOP_s": round(attn_flops / (t_us * 1e-6) / 1e12, 1),
+                          "frac_of_16bit_peak": round(attn_flops / (t_us * 1e-6) / 2.5e15, 4)})
+        elif n == "attn_decode":
+            entry.update({"shape": f"decode 256 sequences, context uniform in 1..4096, {cfg.q_heads}/{cfg.kv_heads} "
+                                   f"heads x {cfg.head_dim}", "bytes": int(dec_bytes),
+                          "GB_s": round(dec_bytes / (t_us * 1e-6) / 1e9, 1),
+                          "frac_of_peak": round(dec_bytes / (t_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)})
         elif n == "copy":
             entry.update({"bytes": 2 * copy_pair[0].numel() * 4,
                           "GB_s": round(2 * copy_pair[0].numel() * 4 / (t_us * 1e-6) / 1e9, 1)})
@@ -332,6 +386,7 @@ def main() -> int:
         "roofline": roofline,
         "q8_gemm": res_ops.get("gemm"),
         "q8_gemv": res_ops.get("gemv"),
+        "paged_attention": {k: res_ops[k] for k in ("attn", "attn_decode") if k in res_ops} or None,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

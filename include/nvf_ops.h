@@ -211,11 +211,13 @@ int nvf_store_kv(const void* key, const void* value, void* k_cache, void* v_cach
 /* Paged attention (replaces hip_paged_attention, hip_ops.hpp:25-28) with q, out and
  * the cache in `dtype` (fp32 math, one rounding of the output).  q rows are
  * q_stride elements apart (>= q_heads * head_dim); out is [tokens, q_heads *
- * head_dim].  q_heads % kv_heads == 0, head_dim <= 256. */
+ * head_dim].  q_heads % kv_heads == 0, head_dim <= 256.  max_query_len is a
+ * scheduling hint: 1 promises one query token per sequence (a decode batch) and
+ * skips the prefill tiles; 0 (unknown) or any other value runs both paths. */
 int nvf_paged_attention(const void* q, void* out, const void* k_cache, const void* v_cache, const int32_t* query_seq,
                         const int32_t* query_key_len, const int32_t* block_tables, int64_t tokens, int q_heads,
                         int kv_heads, int head_dim, int block_size, int max_blocks, float scale, int64_t q_stride,
-                        int dtype, void* stream);
+                        int64_t max_query_len, int dtype, void* stream);
 
 /* Host helper: inv_freq[i] = (float)(1 / theta^(2i/head_dim)) in double, the
  * table Qwen3Model builds in its constructor (src/model.cpp:416-420).

@@ -13,11 +13,16 @@
 // * attn_wave_kernel: one wave per (token, head), any head_dim <= 256 and any
 //   dtype: scores 64 keys at a time (a lane per key, 16-byte K loads when
 //   aligned), an online softmax over the chunks, P . V with the lane owning
-//   head dimensions.  fp32 math; it serves the fp32 drop-in and the shapes the
-//   tiled kernel does not take.
+//   head dimensions.  fp32 math; it serves the fp32 drop-in, decode batches and
+//   the shapes and tiles the tiled kernel does not take.
+// * fa_prefill_kernel: 128-query tiles of one sequence on the matrix cores;
+//   fa_decode_kernel: the remaining (decode-shaped) tokens, one wave per
+//   (token, kv head) on the matrix cores.
 #include <hip/hip_runtime.h>
 
 #include <math.h>
+
+#include <mutex>
 
 #include "nvf_device.hpp"
 #include "nvf_host.hpp"
@@ -59,12 +64,416 @@ __global__ __launch_bounds__(256) void store_kv_generic_kernel(const T* __restri
 }
 
 // ---------------------------------------------------------------------------
+// Prefill tiles on the matrix cores: 16-bit q and cache, head_dim 128, block
+// sizes a multiple of 64 (the reference's are multiples of 256,
+// include/nanovllm/config.hpp:254).  A workgroup owns kFaBq = 128 consecutive
+// query tokens of one sequence and one query head (32 per wave) and walks the
+// keys in 64-key chunks staged in LDS (double-buffered, the next chunk's loads
+// in flight during the current chunk's math).
+//
+// Per wave and chunk, with 32x32x16 MFMAs:
+//   S^T = K . Q^T   (keys x queries: A = K rows from LDS, B = the wave's q rows,
+//                    held in registers for the whole tile)
+//   online softmax per query -- a query is a lane column of S^T, so its max,
+//                    sum and the O rescale are lane-local plus one swap with the
+//                    other lane half
+//   O^T += V^T . P^T (dims x queries: A = V^T from LDS, stored transposed; B = P^T,
+//                    which is S^T's own register layout: the 8 values a lane
+//                    holds for keys 16u + 4h + {0..3, 8..11} are its B operand
+//                    for key step u once both operands index keys that way)
+// P is rounded to the cache dtype for the MFMA; the row sums use the fp32 P.
+// Tiles whose tokens span sequences (or are partial at a sequence switch) are
+// left to attn_wave_kernel, which applies the same predicate.
+constexpr int kFaHd = 128;
+constexpr int kFaBq = 128;                       // query tokens per workgroup
+constexpr int kFaBk = 64;                        // keys per chunk
+constexpr int kFaKRow = kFaHd * 2 + 16;          // K row in LDS, padded (conflict-free 16 B reads)
+constexpr int kFaVRow = kFaBk * 2 + 8;           // V^T row in LDS, padded
+constexpr int kFaKBytes = kFaBk * kFaKRow;
+constexpr int kFaStage = kFaKBytes + kFaHd * kFaVRow;
+constexpr int kFaLds = 2 * kFaStage;
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+template <typename T>
+struct Mfma16;
+template <>
+struct Mfma16<__bf16> {
+  typedef __bf16 v8 __attribute__((ext_vector_type(8)));
+  static __device__ __forceinline__ f32x16 mma(v8 a, v8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  }
+};
+template <>
+struct Mfma16<_Float16> {
+  typedef _Float16 v8 __attribute__((ext_vector_type(8)));
+  static __device__ __forceinline__ f32x16 mma(v8 a, v8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  }
+};
+
+// True iff every token of the kFaBq-token tile `tile` (those < tokens) belongs to
+// one sequence.  Evaluated per wave; every wave of a workgroup gets the same answer.
+__device__ __forceinline__ bool fa_tile_uniform(const int32_t* __restrict__ qseq, int64_t tokens, int64_t tile) {
+  const int lane = threadIdx.x & 63;
+  const int64_t t0 = tile * kFaBq;
+  const int32_t s0 = qseq[t0];
+  bool same = true;
+#pragma unroll
+  for (int i = 0; i < kFaBq / 64; ++i) {
+    const int64_t t = t0 + lane + 64 * i;
+    if (t < tokens) same = same && qseq[t] == s0;
+  }
+  return __all(same);
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void fa_prefill_kernel(
+    const T* __restrict__ q, T* __restrict__ out, const T* __restrict__ kc, const T* __restrict__ vc,
+    const int32_t* __restrict__ qseq, const int32_t* __restrict__ qlen, const int32_t* __restrict__ tables,
+    int64_t tokens, int q_heads, int kv_heads, int bs, int max_blocks, float scale_log2, int64_t q_stride,
+    int64_t tiles) {
+  using M = Mfma16<T>;
+  using v8 = typename M::v8;
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int half = lane >> 5;
+  const int64_t bid = blockIdx.x;
+  const int64_t tile = tiles - 1 - bid / q_heads;  // the longest tiles (latest positions) first
+  const int h = (int)(bid % q_heads);
+  const int64_t t0 = tile * kFaBq;
+  if (!fa_tile_uniform(qseq, tokens, tile)) return;  // the whole workgroup: left to attn_wave_kernel
+  const int64_t seq = qseq[t0];
+  const int kvh = h / (q_heads / kv_heads);
+  const int64_t kv_stride = (int64_t)kv_heads * kFaHd;
+  const int32_t* tab = tables + seq * max_blocks;
+
+  // the tile's longest key range (every wave computes the same value)
+  float lmax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < kFaBq / 64; ++i) {
+    const int64_t t = t0 + lane + 64 * i;
+    if (t < tokens) lmax = fmaxf(lmax, (float)qlen[t]);
+  }
+  const int Lmax = (int)wave_max(lmax);
+  const int nchunks = (Lmax + kFaBk - 1) / kFaBk;
+
+  // this lane's query (a column of S^T and O^T)
+  const int64_t tq = t0 + 32 * wave + (lane & 31);
+  const bool q_ok = tq < tokens;
+  const int L = q_ok ? qlen[tq] : 0;
+  v8 qf[kFaHd / 16];
+#pragma unroll
+  for (int s = 0; s < kFaHd / 16; ++s) {
+    const u32x4 v = q_ok ? ld16(q + tq * q_stride + (int64_t)h * kFaHd + 16 * s + 8 * half) : u32x4{0, 0, 0, 0};
+    qf[s] = __builtin_bit_cast(v8, v);
+  }
+
+  // chunk loads: K row key = tid/16 + 16 i, dims 8 (tid%16); V keys 4 (tid/16) + e, dims 8 (tid%16)
+  const int tid = threadIdx.x;
+  const int ld_c = tid & 15, ld_r = tid >> 4;
+  u32x4 kreg[4], vreg[4];
+  auto load_chunk = [&](int c) {
+    const int k0 = c * kFaBk;
+    const int64_t row0 = (int64_t)tab[k0 / bs] * bs + k0 % bs;
+    const T* kb = kc + row0 * kv_stride + (int64_t)kvh * kFaHd + ld_c * 8;
+    const T* vb = vc + row0 * kv_stride + (int64_t)kvh * kFaHd + ld_c * 8;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      kreg[i] = ld16(kb + (int64_t)(ld_r + 16 * i) * kv_stride);
+      const int key = 4 * ld_r + i;
+      // keys past the tile's range may hold anything: zero their V (their p is 0)
+      vreg[i] = k0 + key < Lmax ? ld16(vb + (int64_t)key * kv_stride) : u32x4{0, 0, 0, 0};
+    }
+  };
+  auto store_chunk = [&](uint8_t* st) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) st16(st + (ld_r + 16 * i) * kFaKRow + ld_c * 16, kreg[i]);
+    // V^T: dim 8 ld_c + e, keys 4 ld_r .. 4 ld_r + 3 -> 8 bytes
+    uint8_t* vt = st + kFaKBytes;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int sh = (e & 1) * 16;
+      const uint32_t lo = ((vreg[0][e >> 1] >> sh) & 0xffffu) | (((vreg[1][e >> 1] >> sh) & 0xffffu) << 16);
+      const uint32_t hi = ((vreg[2][e >> 1] >> sh) & 0xffffu) | (((vreg[3][e >> 1] >> sh) & 0xffffu) << 16);
+      typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+      *reinterpret_cast<u32x2*>(vt + (8 * ld_c + e) * kFaVRow + 8 * ld_r) = u32x2{lo, hi};
+    }
+  };
+
+  f32x16 o[kFaHd / 32];
+#pragma unroll
+  for (int d = 0; d < kFaHd / 32; ++d) o[d] = f32x16{};
+  float m = -INFINITY, l = 0.0f;
+
+  if (nchunks > 0) {
+    load_chunk(0);
+    store_chunk(lds);
+  }
+  __syncthreads();
+  for (int c = 0; c < nchunks; ++c) {
+    const uint8_t* buf = lds + (c & 1) * kFaStage;
+    if (c + 1 < nchunks) load_chunk(c + 1);  // in flight during this chunk
+    // S^T = K . Q^T for keys [32 kt, 32 kt + 32)
+    f32x16 st[2];
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt) {
+      st[kt] = f32x16{};
+#pragma unroll
+      for (int s = 0; s < kFaHd / 16; ++s) {
+        const v8 a = __builtin_bit_cast(v8, ld16(buf + (32 * kt + (lane & 31)) * kFaKRow + (16 * s + 8 * half) * 2));
+        st[kt] = M::mma(a, qf[s], st[kt]);
+      }
+    }
+    // online softmax for this lane's query; element j of tile kt is key
+    // c*64 + 32 kt + 8 (j/4) + 4 half + j%4
+    float mx = -INFINITY;
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const int key = c * kFaBk + 32 * kt + 8 * (j >> 2) + 4 * half + (j & 3);
+        const float x = key < L ? st[kt][j] * scale_log2 : -INFINITY;
+        st[kt][j] = x;
+        mx = fmaxf(mx, x);
+      }
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    const float m_new = fmaxf(m, mx);
+    const float m_use = m_new == -INFINITY ? 0.0f : m_new;
+    const float alpha = __builtin_amdgcn_exp2f(m - m_use);
+    float ls = 0.0f;
+    v8 pb[2][2];
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const float p = __builtin_amdgcn_exp2f(st[kt][j] - m_use);
+        ls += p;
+        pb[kt][j >> 3][j & 7] = (T)p;
+      }
+    ls += __shfl_xor(ls, 32);
+    l = l * alpha + ls;
+    m = m_new;
+#pragma unroll
+    for (int d = 0; d < kFaHd / 32; ++d) o[d] *= alpha;
+    // O^T += V^T . P^T, key step u of tile kt: keys 32 kt + 16 u + 4 half + {0..3, 8..11}
+    const uint8_t* vt = buf + kFaKBytes;
+#pragma unroll
+    for (int d = 0; d < kFaHd / 32; ++d)
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+          const uint8_t* r = vt + (32 * d + (lane & 31)) * kFaVRow + (32 * kt + 16 * u + 4 * half) * 2;
+          const u32x2 lo = *reinterpret_cast<const u32x2*>(r);
+          const u32x2 hi = *reinterpret_cast<const u32x2*>(r + 16);
+          const v8 a = __builtin_bit_cast(v8, u32x4{lo[0], lo[1], hi[0], hi[1]});
+          o[d] = M::mma(a, pb[kt][u], o[d]);
+        }
+    if (c + 1 < nchunks) store_chunk(lds + ((c + 1) & 1) * kFaStage);
+    __syncthreads();
+  }
+
+  // O^T layout: lane column = query, dims 32 d + 8 (j/4) + 4 half + j%4
+  if (q_ok) {
+    const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+    T* orow = out + (tq * q_heads + h) * kFaHd;
+#pragma unroll
+    for (int d = 0; d < kFaHd / 32; ++d)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        typedef T t4 __attribute__((ext_vector_type(4)));
+        t4 v;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = (T)(o[d][4 * g + e] * inv);
+        *reinterpret_cast<t4*>(orow + 32 * d + 8 * g + 4 * half) = v;
+      }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Decode-shaped attention on the matrix cores (16-bit cache, head_dim 128,
+// block sizes a multiple of 64, at most 16 query heads per kv head): one wave
+// per (token, kv head) streams that head's keys in 64-key chunks.  The query
+// heads of the group are the 16 columns of v_mfma_f32_16x16x32 tiles:
+//   S^T = K . Q^T    (A = 16 keys x 32 dims straight from the cache, B = q)
+//   O^T += V^T . P^T (A = V^T from a wave-private LDS transpose of the chunk,
+//                     B = P^T, again S^T's own registers: a lane holds keys
+//                     32 u + 4 g + {0..3} and 32 u + 16 + 4 g + {0..3}, g = lane/16)
+// The next chunk's K and V loads are in flight during the current chunk's math.
+// A workgroup holds 4 waves (4 kv heads of one token).
+constexpr int kFdVRow = 64 * 2 + 8;              // V^T row: 64 keys, padded
+constexpr int kFdWaveLds = kFaHd * kFdVRow;      // per wave
+constexpr int kFdLds = 4 * kFdWaveLds;
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+template <typename T>
+struct Mfma16x16;
+template <>
+struct Mfma16x16<__bf16> {
+  typedef __bf16 v8 __attribute__((ext_vector_type(8)));
+  static __device__ __forceinline__ f32x4 mma(v8 a, v8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  }
+};
+template <>
+struct Mfma16x16<_Float16> {
+  typedef _Float16 v8 __attribute__((ext_vector_type(8)));
+  static __device__ __forceinline__ f32x4 mma(v8 a, v8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+  }
+};
+
+template <typename T>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void fa_decode_kernel(
+    const T* __restrict__ q, T* __restrict__ out, const T* __restrict__ kc, const T* __restrict__ vc,
+    const int32_t* __restrict__ qseq, const int32_t* __restrict__ qlen, const int32_t* __restrict__ tables,
+    int64_t tokens, int q_heads, int kv_heads, int bs, int max_blocks, float scale_log2, int64_t q_stride,
+    bool skip_uniform_tiles) {
+  using M = Mfma16x16<T>;
+  using v8 = typename M::v8;
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int64_t t = blockIdx.x;
+  const int kvh = blockIdx.y * 4 + wave;
+  if (kvh >= kv_heads) return;  // whole waves; no workgroup barrier below
+  if (skip_uniform_tiles && fa_tile_uniform(qseq, tokens, t / kFaBq)) return;  // fa_prefill_kernel's
+  const int G = q_heads / kv_heads;
+  const int col = lane & 15, g = lane >> 4;
+  const bool head_ok = col < G;
+  const int h = kvh * G + col;
+  const int L = qlen[t];
+  const int64_t seq = qseq[t];
+  const int64_t kv_stride = (int64_t)kv_heads * kFaHd;
+  const int32_t* tab = tables + seq * max_blocks;
+  uint8_t* vt = lds + wave * kFdWaveLds;
+
+  v8 qf[kFaHd / 32];  // B operand: head col, dims 32 s + 8 g
+#pragma unroll
+  for (int s = 0; s < kFaHd / 32; ++s) {
+    const u32x4 v = head_ok ? ld16(q + t * q_stride + (int64_t)h * kFaHd + 32 * s + 8 * g) : u32x4{0, 0, 0, 0};
+    qf[s] = __builtin_bit_cast(v8, v);
+  }
+  f32x4 o[kFaHd / 16];
+#pragma unroll
+  for (int d = 0; d < kFaHd / 16; ++d) o[d] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  float m = -INFINITY, l = 0.0f;
+
+  const int nchunks = L > 0 ? (L + 63) / 64 : 0;
+  // chunk loads: K as MFMA A operands (key 16 kt + col, dims 32 s + 8 g);
+  // V rows for the transpose (key 4 i + g... : lane l covers dims 8 (l % 16) of
+  // keys 16 i + (l / 16) * 4 + {0..3} over i < 4, 16 loads)
+  u32x4 kr[4][4], vr[16];
+  auto load_chunk = [&](int c) {
+    const int k0 = c * 64;
+    const int64_t row0 = (int64_t)tab[k0 / bs] * bs + k0 % bs;
+    const T* kb = kc + row0 * kv_stride + (int64_t)kvh * kFaHd;
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+      for (int s = 0; s < 4; ++s) kr[kt][s] = ld16(kb + (int64_t)(16 * kt + col) * kv_stride + 32 * s + 8 * g);
+    const T* vb = vc + row0 * kv_stride + (int64_t)kvh * kFaHd + 8 * col;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int key = 16 * (i >> 2) + 4 * g + (i & 3);
+      vr[i] = k0 + key < L ? ld16(vb + (int64_t)key * kv_stride) : u32x4{0, 0, 0, 0};  // past L: zero
+    }
+  };
+  if (nchunks > 0) load_chunk(0);
+  for (int c = 0; c < nchunks; ++c) {
+    // V^T into this wave's LDS: dim 8 col + e, keys 16 i4 + 4 g + {0..3}
+#pragma unroll
+    for (int i4 = 0; i4 < 4; ++i4)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int sh = (e & 1) * 16;
+        const uint32_t lo = ((vr[4 * i4][e >> 1] >> sh) & 0xffffu) | (((vr[4 * i4 + 1][e >> 1] >> sh) & 0xffffu) << 16);
+        const uint32_t hi = ((vr[4 * i4 + 2][e >> 1] >> sh) & 0xffffu) | (((vr[4 * i4 + 3][e >> 1] >> sh) & 0xffffu) << 16);
+        typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+        *reinterpret_cast<u32x2*>(vt + (8 * col + e) * kFdVRow + (16 * i4 + 4 * g) * 2) = u32x2{lo, hi};
+      }
+    // S^T = K . Q^T, 4 tiles of 16 keys
+    f32x4 st[4];
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt) {
+      st[kt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int s = 0; s < 4; ++s) st[kt] = M::mma(__builtin_bit_cast(v8, kr[kt][s]), qf[s], st[kt]);
+    }
+    if (c + 1 < nchunks) load_chunk(c + 1);  // in flight during the math below
+    __builtin_amdgcn_wave_barrier();
+    // online softmax per head (lane column); element j of tile kt is key 64 c + 16 kt + 4 g + j
+    float mx = -INFINITY;
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int key = c * 64 + 16 * kt + 4 * g + j;
+        const float x = key < L ? st[kt][j] * scale_log2 : -INFINITY;
+        st[kt][j] = x;
+        mx = fmaxf(mx, x);
+      }
+    mx = fmaxf(mx, __shfl_xor(mx, 16));
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    const float m_new = fmaxf(m, mx);
+    const float m_use = m_new == -INFINITY ? 0.0f : m_new;
+    const float alpha = __builtin_amdgcn_exp2f(m - m_use);
+    float ls = 0.0f;
+    v8 pb[2];
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float p = __builtin_amdgcn_exp2f(st[kt][j] - m_use);
+        ls += p;
+        pb[kt >> 1][(kt & 1) * 4 + j] = (T)p;
+      }
+    ls += __shfl_xor(ls, 16);
+    ls += __shfl_xor(ls, 32);
+    l = l * alpha + ls;
+    m = m_new;
+    // O^T += V^T . P^T: dims 16 d + col, key step u: keys 32 u + 4 g + {0..3}, 32 u + 16 + 4 g + {0..3}
+#pragma unroll
+    for (int d = 0; d < kFaHd / 16; ++d) {
+      o[d] *= alpha;
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+        const uint8_t* r = vt + (16 * d + col) * kFdVRow + (32 * u + 4 * g) * 2;
+        const u32x2 lo = *reinterpret_cast<const u32x2*>(r);
+        const u32x2 hi = *reinterpret_cast<const u32x2*>(r + 32);
+        o[d] = M::mma(__builtin_bit_cast(v8, u32x4{lo[0], lo[1], hi[0], hi[1]}), pb[u], o[d]);
+      }
+    }
+    __builtin_amdgcn_wave_barrier();  // this chunk's V^T reads before the next chunk's writes
+  }
+  // O^T: lane column = head col, dims 16 d + 4 g + j
+  if (head_ok) {
+    const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+    T* orow = out + (t * q_heads + h) * kFaHd;
+#pragma unroll
+    for (int d = 0; d < kFaHd / 16; ++d) {
+      typedef T t4 __attribute__((ext_vector_type(4)));
+      t4 v;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] = (T)(o[d][e] * inv);
+      *reinterpret_cast<t4*>(orow + 16 * d + 4 * g) = v;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // One wave per (token, head).  DPL = head dimensions per lane (head_dim <= 64 DPL).
 template <typename T, int DPL, bool VEC>
 __global__ __launch_bounds__(kAttnWaves * 64) void attn_wave_kernel(
     const T* __restrict__ q, T* __restrict__ out, const T* __restrict__ kc, const T* __restrict__ vc,
     const int32_t* __restrict__ qseq, const int32_t* __restrict__ qlen, const int32_t* __restrict__ tables,
-    int64_t tokens, int q_heads, int kv_heads, int hd, int bs, int max_blocks, float scale, int64_t q_stride) {
+    int64_t tokens, int q_heads, int kv_heads, int hd, int bs, int max_blocks, float scale, int64_t q_stride,
+    bool skip_uniform_tiles) {
   constexpr int N = Pack<T>::N;
   __shared__ float q_sh[kAttnWaves][64 * DPL];
   __shared__ float p_sh[kAttnWaves][64];
@@ -74,6 +483,7 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_wave_kernel(
   if (gw >= tokens * q_heads) return;  // whole waves only; no workgroup barrier below
   const int64_t t = gw / q_heads;
   const int h = (int)(gw - t * q_heads);
+  if (skip_uniform_tiles && fa_tile_uniform(qseq, tokens, t / kFaBq)) return;  // fa_prefill_kernel's
   const int kvh = h / (q_heads / kv_heads);
   const int L = qlen[t];
   T* o = out + (t * q_heads + h) * hd;
@@ -144,7 +554,7 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_wave_kernel(
 template <typename T, int DPL>
 void launch_attn_wave(const void* q, void* out, const void* kc, const void* vc, const int32_t* qseq,
                       const int32_t* qlen, const int32_t* tables, int64_t tokens, int q_heads, int kv_heads, int hd,
-                      int bs, int max_blocks, float scale, int64_t q_stride, bool vec, hipStream_t st) {
+                      int bs, int max_blocks, float scale, int64_t q_stride, bool vec, bool skip, hipStream_t st) {
   const int64_t waves = tokens * q_heads;
   const dim3 grid((unsigned)((waves + kAttnWaves - 1) / kAttnWaves)), block(kAttnWaves * 64);
   const T* qt = static_cast<const T*>(q);
@@ -153,29 +563,65 @@ void launch_attn_wave(const void* q, void* out, const void* kc, const void* vc, 
   const T* vt = static_cast<const T*>(vc);
   if (vec) {
     attn_wave_kernel<T, DPL, true><<<grid, block, 0, st>>>(qt, ot, kt, vt, qseq, qlen, tables, tokens, q_heads,
-                                                           kv_heads, hd, bs, max_blocks, scale, q_stride);
+                                                           kv_heads, hd, bs, max_blocks, scale, q_stride, skip);
   } else {
     attn_wave_kernel<T, DPL, false><<<grid, block, 0, st>>>(qt, ot, kt, vt, qseq, qlen, tables, tokens, q_heads,
-                                                            kv_heads, hd, bs, max_blocks, scale, q_stride);
+                                                            kv_heads, hd, bs, max_blocks, scale, q_stride, skip);
   }
 }
 
 template <typename T>
-int attention_generic(const void* q, void* out, const void* kc, const void* vc, const int32_t* qseq,
-                      const int32_t* qlen, const int32_t* tables, int64_t tokens, int q_heads, int kv_heads, int hd,
-                      int bs, int max_blocks, float scale, int64_t q_stride, hipStream_t st) {
+int attention_dispatch(const void* q, void* out, const void* kc, const void* vc, const int32_t* qseq,
+                       const int32_t* qlen, const int32_t* tables, int64_t tokens, int q_heads, int kv_heads, int hd,
+                       int bs, int max_blocks, float scale, int64_t q_stride, int64_t max_query_len, hipStream_t st) {
   constexpr int N = Pack<T>::N;
+  // matrix-core paths: 16-bit, head_dim 128, 64-key chunks inside one block, 16-byte rows, <= 16 heads per kv head
+  bool mfma = false;
+  if constexpr (sizeof(T) == 2) {
+    mfma = hd == kFaHd && bs % kFaBk == 0 && q_heads / kv_heads <= 16 && aligned16(q) && aligned16(out) &&
+           aligned16(kc) && aligned16(vc) && q_stride % N == 0;
+  }
+  if constexpr (sizeof(T) == 2) {
+    if (mfma) {
+      const float sl = scale * 1.4426950408889634f;
+      const bool tiles = max_query_len != 1;  // 1: every sequence has one query (decode): no tile can be uniform
+      if (tiles) {
+        static std::once_flag attr_once;
+        std::call_once(attr_once, [] {
+          (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&fa_prefill_kernel<T>),
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, kFaLds);
+        });
+        const int64_t ntiles = (tokens + kFaBq - 1) / kFaBq;
+        if (ntiles * q_heads > INT32_MAX) return fail(NVF_ERR_INVALID, "paged_attention: too many tiles");
+        fa_prefill_kernel<T><<<dim3((unsigned)(ntiles * q_heads)), 256, kFaLds, st>>>(
+            static_cast<const T*>(q), static_cast<T*>(out), static_cast<const T*>(kc), static_cast<const T*>(vc),
+            qseq, qlen, tables, tokens, q_heads, kv_heads, bs, max_blocks, sl, q_stride, ntiles);
+        const int rc = launch_status("paged_attention(tiles)");
+        if (rc != NVF_OK) return rc;
+      }
+      static std::once_flag dec_once;
+      std::call_once(dec_once, [] {
+        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&fa_decode_kernel<T>),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, kFdLds);
+      });
+      if (tokens > INT32_MAX) return fail(NVF_ERR_INVALID, "paged_attention: too many tokens");
+      fa_decode_kernel<T><<<dim3((unsigned)tokens, (unsigned)((kv_heads + 3) / 4)), 256, kFdLds, st>>>(
+          static_cast<const T*>(q), static_cast<T*>(out), static_cast<const T*>(kc), static_cast<const T*>(vc), qseq,
+          qlen, tables, tokens, q_heads, kv_heads, bs, max_blocks, sl, q_stride, tiles);
+      return launch_status("paged_attention(decode)");
+    }
+  }
   const bool vec = hd % N == 0 && aligned16(kc) && ((int64_t)kv_heads * hd) % N == 0;
   const int dpl = (hd + 63) / 64;
   switch (dpl) {
     case 1: launch_attn_wave<T, 1>(q, out, kc, vc, qseq, qlen, tables, tokens, q_heads, kv_heads, hd, bs, max_blocks,
-                                   scale, q_stride, vec, st); break;
+                                   scale, q_stride, vec, false, st); break;
     case 2: launch_attn_wave<T, 2>(q, out, kc, vc, qseq, qlen, tables, tokens, q_heads, kv_heads, hd, bs, max_blocks,
-                                   scale, q_stride, vec, st); break;
+                                   scale, q_stride, vec, false, st); break;
     case 3: launch_attn_wave<T, 3>(q, out, kc, vc, qseq, qlen, tables, tokens, q_heads, kv_heads, hd, bs, max_blocks,
-                                   scale, q_stride, vec, st); break;
+                                   scale, q_stride, vec, false, st); break;
     default: launch_attn_wave<T, 4>(q, out, kc, vc, qseq, qlen, tables, tokens, q_heads, kv_heads, hd, bs,
-                                    max_blocks, scale, q_stride, vec, st); break;
+                                    max_blocks, scale, q_stride, vec, false, st); break;
   }
   return launch_status("paged_attention");
 }
@@ -230,7 +676,7 @@ int nvf_store_kv(const void* key, const void* value, void* k_cache, void* v_cach
 int nvf_paged_attention(const void* q, void* out, const void* k_cache, const void* v_cache, const int32_t* query_seq,
                         const int32_t* query_key_len, const int32_t* block_tables, int64_t tokens, int q_heads,
                         int kv_heads, int head_dim, int block_size, int max_blocks, float scale, int64_t q_stride,
-                        int dtype, void* stream) {
+                        int64_t max_query_len, int dtype, void* stream) {
   if (!dtype_ok(dtype)) return fail(NVF_ERR_INVALID, "nvf_paged_attention: bad dtype %d", dtype);
   if (tokens < 0 || q_heads <= 0 || kv_heads <= 0 || head_dim <= 0 || block_size <= 0 || max_blocks <= 0)
     return fail(NVF_ERR_INVALID, "nvf_paged_attention: bad shape");
@@ -245,9 +691,10 @@ int nvf_paged_attention(const void* q, void* out, const void* k_cache, const voi
   if ((tokens * q_heads + kAttnWaves - 1) / kAttnWaves > INT32_MAX)
     return fail(NVF_ERR_INVALID, "nvf_paged_attention: too many (token, head) pairs");
   int rc = NVF_OK;
-  NVF_DISPATCH_DTYPE(dtype, T, rc = attention_generic<T>(q, out, k_cache, v_cache, query_seq, query_key_len,
+  NVF_DISPATCH_DTYPE(dtype, T, rc = attention_dispatch<T>(q, out, k_cache, v_cache, query_seq, query_key_len,
                                                          block_tables, tokens, q_heads, kv_heads, head_dim, block_size,
-                                                         max_blocks, scale, q_stride, as_stream(stream)));
+                                                         max_blocks, scale, q_stride, max_query_len,
+                                                         as_stream(stream)));
   return rc;
 }
 
@@ -268,7 +715,7 @@ void hip_paged_attention(const float* q, float* out, const float* k_cache, const
   if (tokens <= 0 || q_heads <= 0 || kv_heads <= 0) return;
   dropin_check(nvf_paged_attention(q, out, k_cache, v_cache, query_seq, query_key_len, block_tables, tokens, q_heads,
                                    kv_heads, head_dim, block_size, max_blocks, scale, (int64_t)q_heads * head_dim,
-                                   NVF_F32, nullptr),
+                                   0, NVF_F32, nullptr),
                "hip_paged_attention");
 }
 

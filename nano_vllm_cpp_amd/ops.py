@@ -42,7 +42,7 @@ SIGNATURES: dict[str, tuple] = {
     "hip_paged_attention": (None, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _i32, _f32]),
     "nvf_store_kv": (_i32, [_vp, _vp, _vp, _vp, _vp, _i64, _i32, _i32, _i64, _i64, _i32, _vp]),
     "nvf_paged_attention": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i32, _i32, _i32, _i32, _i32, _f32, _i64,
-                                   _i32, _vp]),
+                                   _i64, _i32, _vp]),
     "nvf_q8_quantize_rows": (_i32, [_vp, _vp, _vp, _i64, _i64, _i32, _vp]),
     "nvf_matmul_q8_0": (_i32, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _i32, _vp]),
     "nvf_rms_norm_add": (_i32, [_vp, _vp, _vp, _vp, _i64, _i64, _f32, _i32, _vp]),
@@ -214,9 +214,10 @@ def store_kv(key: torch.Tensor, value: torch.Tensor, k_cache: torch.Tensor, v_ca
 
 def paged_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, query_seq: torch.Tensor,
                     query_key_len: torch.Tensor, block_tables: torch.Tensor, block_size: int, scale: float,
-                    out: torch.Tensor | None = None) -> torch.Tensor:
+                    out: torch.Tensor | None = None, max_query_len: int = 0) -> torch.Tensor:
     """q [tokens, q_heads, head_dim] (row stride from the tensor); caches
     [rows, kv_heads, head_dim]; block_tables [seqs, max_blocks] int32.
+    max_query_len = 1 promises a decode batch (one query per sequence).
     Returns out [tokens, q_heads, head_dim] in q's dtype."""
     tokens, q_heads, head_dim = q.shape
     kv_heads = k_cache.shape[1]
@@ -225,7 +226,7 @@ def paged_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tenso
                                      _dev(v_cache, "v_cache"), _dev(query_seq, "query_seq"),
                                      _dev(query_key_len, "query_key_len"), _dev(block_tables, "block_tables"), tokens,
                                      q_heads, kv_heads, head_dim, block_size, block_tables.shape[1], scale, q.stride(0),
-                                     _dt(q), _stream()), "paged_attention")
+                                     max_query_len, _dt(q), _stream()), "paged_attention")
     return out
 
 

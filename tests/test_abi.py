@@ -101,6 +101,19 @@ def test_host_argument_checks():
     rc, msg = _status(lib.nvf_silu_and_mul_q8(p, None, p, p, 4, 64, 3, None))
     assert rc == -1 and "dtype" in msg
     assert lib.nvf_silu_and_mul_q8(p, None, p, p, 0, 64, 1, None) == 0
+    # KV store and paged attention
+    rc, msg = _status(lib.nvf_paged_attention(p, p, p, p, p, p, p, 4, 6, 4, 128, 64, 4, 0.1, 768, 0, 1, None))
+    assert rc == -1 and "multiple" in msg
+    rc, msg = _status(lib.nvf_paged_attention(p, p, p, p, p, p, p, 4, 8, 4, 512, 64, 4, 0.1, 4096, 0, 1, None))
+    assert rc == -1 and "256" in msg
+    rc, msg = _status(lib.nvf_paged_attention(p, p, p, p, p, p, p, 4, 8, 4, 128, 64, 4, 0.1, 100, 0, 1, None))
+    assert rc == -1 and "q_stride" in msg
+    rc, msg = _status(lib.nvf_paged_attention(p, None, p, p, p, p, p, 4, 8, 4, 128, 64, 4, 0.1, 1024, 0, 1, None))
+    assert rc == -1 and "NULL" in msg
+    assert lib.nvf_paged_attention(p, p, p, p, p, p, p, 0, 8, 4, 128, 64, 4, 0.1, 1024, 0, 1, None) == 0
+    rc, msg = _status(lib.nvf_store_kv(p, p, p, p, p, 4, 4, 128, 100, 512, 1, None))
+    assert rc == -1 and "stride" in msg
+    assert lib.nvf_store_kv(p, p, p, p, p, 0, 4, 128, 512, 512, 1, None) == 0
 
 
 def test_inv_freq_host_helper_matches_oracle():

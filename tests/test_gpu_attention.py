@@ -4,9 +4,13 @@ hip_store_kv / hip_paged_attention, src/hip_ops.hip:452-550, 724-744).
 Bars:
 * store: bit-exact (a copy), slot -1 skipped, strided key/value rows;
 * attention: |got - exact| <= tol with `exact` the oracle's double value and
-  tol = 1e-4 * max|V| over the attended keys (fp32 online-softmax rounding over
-  up to a few thousand keys; a typical error is two orders smaller), plus one
-  ulp of a 16-bit output; 0 rows for key_len 0, the V row itself for one key;
+  tol = rel * max|V| over the attended keys plus one ulp of a 16-bit output.
+  rel = 1e-4 for fp32 (online-softmax rounding over up to a few thousand keys;
+  a typical error is two orders smaller); for 16-bit caches the matrix-core path
+  rounds the softmax weights P to the cache dtype before P . V, an error of at
+  most 2^-8 (bf16) / 2^-11 (fp16) of max|V|, so rel = 2^-7 / 2^-10; 0 rows for
+  key_len 0, the V row itself for one key; a key just past a query's range
+  that would dominate its softmax must not reach it (masking);
 * against the reference's own hip_paged_attention (fp32, same inputs): within
   twice that tolerance.
 """
@@ -29,8 +33,11 @@ def case(msg: str) -> None:
     print(f"[case] {msg}", flush=True)
 
 
-def tol_for(exact: np.ndarray, vmax: np.ndarray, dt: int, rel: float = 1e-4) -> np.ndarray:
-    t = rel * vmax[..., None] * np.ones_like(exact) + 1e-7
+REL = {H.F32: 1e-4, H.F16: 2.0 ** -10, H.BF16: 2.0 ** -7}
+
+
+def tol_for(exact: np.ndarray, vmax: np.ndarray, dt: int) -> np.ndarray:
+    t = REL[dt] * vmax[..., None] * np.ones_like(exact) + 1e-7
     if dt != H.F32:
         t = t + H.ulp(exact, dt)
     return t
@@ -46,10 +53,10 @@ def assert_attn(got: np.ndarray, exact: np.ndarray, vmax: np.ndarray, dt: int, w
                              f"exact {exact[i]!r} tol {tol[i]!r}")
 
 
-def run_attention(gpu, b: H.PagedBatch, q_heads, kv_heads, hd, bs, scale, dt):
+def run_attention(gpu, b: H.PagedBatch, q_heads, kv_heads, hd, bs, scale, dt, max_query_len=0):
     return ops.paged_attention(H.to_dev(b.q, gpu, dt), H.to_dev(b.k_cache, gpu, dt), H.to_dev(b.v_cache, gpu, dt),
                                H.to_dev(b.query_seq, gpu), H.to_dev(b.query_key_len, gpu),
-                               H.to_dev(b.block_tables, gpu), bs, scale)
+                               H.to_dev(b.block_tables, gpu), bs, scale, max_query_len=max_query_len)
 
 
 @pytest.mark.parametrize("dt", DTYPES, ids=DT_IDS)
@@ -82,7 +89,30 @@ CASES = [
     ([300, 1, 77, 513], [1, 1, 1, 1], 28, 4, 128, 256),  # decode, Qwen2.5-7B heads
     ([40, 200], [5, 200], 4, 4, 64, 32),                  # chunked prefill with a cached prefix
     ([9, 33], [9, 2], 6, 3, 80, 8),                       # odd head_dim
+    # matrix-core tiles (16-bit, head_dim 128, block_size % 64 == 0): sequence
+    # switches mid-tile go to the wave kernel, the rest to the tiles
+    ([300, 130, 64], [300, 130, 64], 8, 2, 128, 64),
+    ([700, 90], [200, 90], 28, 4, 128, 256),              # chunked prefill after a 500-token prefix
+    ([256], [256], 4, 1, 128, 128),                       # exact tiles
+    ([33, 64, 1], [2, 1, 1], 32, 1, 128, 64),             # 32 heads per kv head: beyond the 16-column tiles
 ]
+
+
+@pytest.mark.parametrize("dt", [H.F16, H.BF16], ids=["f16", "bf16"])
+@pytest.mark.parametrize("heads", [(28, 4), (32, 8), (16, 1)], ids=["qwen25", "qwen3", "g16"])
+def test_paged_attention_decode_batch(gpu, dt, heads):
+    """A decode batch (one query per sequence) through the decode-only route
+    (max_query_len = 1) and through the automatic one."""
+    qh, kvh = heads
+    r = H.rng(300 + qh + dt)
+    ctx = [int(x) for x in r.integers(1, 1500, 24)] + [1, 64, 65, 2048]
+    b = H.make_paged(r, ctx, [1] * len(ctx), qh, kvh, 128, 256, dt)
+    scale = 128 ** -0.5
+    _, exact, vmax = H.oracle_attention(b, qh, kvh, 128, 256, scale, dt)
+    for mql in (1, 0):
+        case(f"paged_attention decode heads={heads} dt={dt} max_query_len={mql}")
+        got = H.to_host(run_attention(gpu, b, qh, kvh, 128, 256, scale, dt, max_query_len=mql))
+        assert_attn(got, exact, vmax, dt, f"decode (max_query_len={mql})")
 
 
 @pytest.mark.parametrize("dt", DTYPES, ids=DT_IDS)
@@ -152,3 +182,27 @@ def test_dropins_vs_oracle_and_reference(gpu):
     assert (np.abs(got.astype(np.float64) - rg) <= 2 * tol_for(exact, vmax, H.F32)).all()
     ref.ref_hip_store_kv(dkey.data_ptr(), dval.data_ptr(), rk.data_ptr(), rv.data_ptr(), dsl.data_ptr(), T, kvh, hd)
     H.assert_bitexact(rk.cpu().numpy(), kc_ref, "reference k cache")
+
+
+@pytest.mark.parametrize("dt", [H.F16, H.BF16], ids=["f16", "bf16"])
+def test_paged_attention_masks_keys_past_the_range(gpu, dt):
+    """Key 200 of a 256-token prefill carries a score that would dominate any
+    softmax it enters: queries at positions < 200 must not see it, later ones
+    must be pulled to its V row."""
+    r = H.rng(31 + dt)
+    b = H.make_paged(r, [256], [256], 4, 1, 128, 64, dt)
+    qf = np.full((256, 4, 128), 0.25, np.float32)
+    b.q[:] = H.to_storage(qf, dt)
+    kf = H.from_storage(b.k_cache, dt).astype(np.float32) * 0.1
+    row = b.block_tables[0, 200 // 64] * 64 + 200 % 64
+    kf[row] = 6.0
+    b.k_cache[:] = H.to_storage(kf, dt)
+    scale = 128 ** -0.5
+    _, exact, vmax = H.oracle_attention(b, 4, 1, 128, 64, scale, dt)
+    case(f"paged_attention masking spike dt={dt}")
+    got = H.to_host(run_attention(gpu, b, 4, 1, 128, 64, scale, dt))
+    assert_attn(got, exact, vmax, dt, "masking")
+    g = H.from_storage(got, dt)
+    spike_v = H.from_storage(b.v_cache[row, 0], dt)
+    assert np.abs(g[220:, 0] - spike_v).max() < 0.05 * np.abs(spike_v).max()  # pulled to the spike
+    assert np.abs(g[:199, 0] - spike_v).max() > 0.5                          # never saw it
