@@ -168,7 +168,7 @@ def main() -> int:
     attn_in = attn_dec = None
     bs_kv = 256  # the reference's KV block size (a multiple of 256, config.hpp:254)
     if "attn" in only:  # causal prefill over the config's sequences, KV already in the paged cache
-        pos = cfg.positions()
+        apos = cfg.positions()
         lens = [int(n) for n in np.diff(cfg.cu_seqlens())]
         nblk = [-(-n // bs_kv) for n in lens]
         tables = torch.full((len(lens), max(nblk)), -1, dtype=torch.int32)
@@ -181,8 +181,8 @@ def main() -> int:
         attn_in = (randn((T, cfg.q_heads, cfg.head_dim)), randn((rows, cfg.kv_heads, cfg.head_dim)),
                    randn((rows, cfg.kv_heads, cfg.head_dim)),
                    torch.from_numpy(np.repeat(np.arange(len(lens), dtype=np.int32), lens)).to(dev),
-                   torch.from_numpy((pos + 1).astype(np.int32)).to(dev), tables.to(dev))
-        attn_flops = 4.0 * cfg.q_heads * cfg.head_dim * float((pos + 1).sum())
+                   torch.from_numpy((apos + 1).astype(np.int32)).to(dev), tables.to(dev))
+        attn_flops = 4.0 * cfg.q_heads * cfg.head_dim * float((apos + 1).sum())
     if "attn_decode" in only:  # one token per sequence, 256 sequences, context uniform in 1..4096
         ctx = np.random.default_rng(cfg.seed + 11).integers(1, 4097, 256)
         nblk = [-(-int(n) // bs_kv) for n in ctx]
