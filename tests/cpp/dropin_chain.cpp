@@ -1,8 +1,11 @@
 // C++ caller of the drop-in entry points, in the order Qwen3Model::forward_logits
-// calls them (src/model.cpp:756-835), on a Qwen3-0.6B-like layer at 64 tokens.
+// calls them (src/model.cpp:756-844), on one Qwen3-0.6B-like layer: two 32-token
+// prefill sequences over a paged KV cache, every projection a Q8_0 GEMM, then the
+// final norm and the tied lm_head on the last token.
 // It includes only include/nvf_ops.h (the C ABI) and hip_runtime, exactly as
 // model.cpp would after the switch, and checks each stage against the C oracle
-// (test infrastructure).  Exit code 0 = every stage within its bound.
+// (test infrastructure), each stage fed the GPU's own input to that stage.
+// Exit code 0 = every stage within its bound.
 #include <hip/hip_runtime.h>
 
 #include <cmath>
@@ -47,6 +50,7 @@ struct Dev {  // the reference's DeviceBuf/DevVec role: caller-owned device memo
 
 static int failures = 0;
 
+// |got - ref| <= max(1e-5 |ref|, 1 fp32 ulp, floor), or bit-exact
 static void expect(const char* what, const std::vector<float>& got, const std::vector<float>& ref, bool exact,
                    float floor = 0.f) {
   size_t bad = 0;
@@ -66,85 +70,195 @@ static void expect(const char* what, const std::vector<float>& got, const std::v
     if (!(err <= tol)) ++bad;
     worst = std::fmax(worst, err);
   }
-  std::printf("%-34s %s  (%zu / %zu outside, max abs err %.3g)\n", what, bad ? "FAIL" : "ok", bad, ref.size(), worst);
+  std::printf("%-40s %s  (%zu / %zu outside, max abs err %.3g)\n", what, bad ? "FAIL" : "ok", bad, ref.size(), worst);
   if (bad) ++failures;
 }
 
-int main() {
-  const int T = 64, H = 1024, I = 3072, V = 4096, heads = 16, kv_heads = 8, hd = 128;
-  const int q_size = heads * hd, kv_size = kv_heads * hd;
-  const float eps = 1e-6f;
-  std::mt19937_64 rng(2024);
-  std::normal_distribution<float> n01(0.f, 1.f), g01(1.f, 0.1f);
-  std::uniform_real_distribution<float> us(1e-3f, 1e-2f);
+// |got - ideal| <= bound (elementwise), for the GEMM (the oracle's fp32 summation
+// bound) and attention (a fraction of max |V|)
+static void expect_within(const char* what, const std::vector<float>& got, const std::vector<double>& ideal,
+                          const std::vector<double>& bound) {
+  size_t bad = 0;
+  double worst = 0;
+  for (size_t i = 0; i < ideal.size(); ++i) {
+    const double err = std::fabs((double)got[i] - ideal[i]);
+    if (!(err <= bound[i] + 1e-30)) ++bad;
+    worst = std::fmax(worst, err / (bound[i] + 1e-30));
+  }
+  std::printf("%-40s %s  (%zu / %zu outside, worst err/bound %.3g)\n", what, bad ? "FAIL" : "ok", bad, ideal.size(),
+              worst);
+  if (bad) ++failures;
+}
+
+struct Q8W {  // a Q8_0 weight [n, k] as split planes (model.cpp:394-404)
+  std::vector<uint8_t> w8;
+  std::vector<uint16_t> ws;
+};
+
+static Q8W make_q8(std::mt19937_64& rng, int64_t n, int64_t k) {
   std::uniform_int_distribution<int> q8(-127, 127);
+  std::uniform_real_distribution<float> us(1e-3f, 1e-2f);
+  Q8W w;
+  w.w8.resize((size_t)(n * k));
+  w.ws.resize((size_t)(n * k / 32));
+  for (auto& b : w.w8) b = (uint8_t)(int8_t)q8(rng);
+  for (auto& s : w.ws) s = orc_f32_to_fp16(us(rng));
+  return w;
+}
+
+// The oracle's GEMM on the GPU's own input x [m, k]: ideal values and bounds.
+static void oracle_gemm(const std::vector<float>& x, const uint8_t* w8, const uint16_t* ws, int64_t m, int64_t n,
+                        int64_t k, std::vector<double>& ideal, std::vector<double>& bound) {
+  ideal.assign((size_t)(m * n), 0.0);
+  bound.assign((size_t)(m * n), 0.0);
+  orc_matmul_q8(x.data(), ORC_F32, w8, ws, m, n, k, ideal.data(), bound.data(), nullptr, nullptr);
+}
+
+int main() {
+  // a Qwen3-0.6B-like layer (head_dim 128, GQA 16/8, QK-norm), 2 sequences x 32 prefill tokens
+  const int S = 2, per = 32, T = S * per, H = 1024, I = 3072, V = 4096, heads = 16, kv_heads = 8, hd = 128;
+  const int q_size = heads * hd, kv_size = kv_heads * hd, bs = 16, max_blocks = per / bs, num_blocks = 8;
+  const float eps = 1e-6f, scale = 1.0f / std::sqrt((float)hd);
+  std::mt19937_64 rng(2024);
+  std::normal_distribution<float> g01(1.f, 0.1f);
   std::uniform_int_distribution<int64_t> vid(0, V - 1);
 
-  // weights: Q8_0 embedding split planes (model.cpp:394-404), norms, inv_freq
-  std::vector<uint8_t> w8((size_t)V * H);
-  std::vector<uint16_t> ws((size_t)V * H / 32);
-  for (auto& b : w8) b = (uint8_t)(int8_t)q8(rng);
-  for (auto& s : ws) s = orc_f32_to_fp16(us(rng));
+  // weights: Q8_0 embedding (tied lm_head) and projections, norms, inv_freq
+  Q8W emb = make_q8(rng, V, H), wqkv = make_q8(rng, q_size + 2 * kv_size, H), wo = make_q8(rng, H, q_size),
+      wgu = make_q8(rng, 2 * I, H), wdn = make_q8(rng, H, I);
   std::vector<float> in_ln(H), post_ln(H), q_norm(hd), k_norm(hd), final_ln(H), inv(hd / 2);
   for (auto* v : {&in_ln, &post_ln, &final_ln, &q_norm, &k_norm})
     for (auto& x : *v) x = g01(rng);
   if (nvf_rope_inv_freq(1e6, hd, inv.data()) != NVF_OK) return 2;  // model.cpp:416-420
+  // the prefill context (model_runner.cpp:43-98): positions, query_seq, key lengths,
+  // block tables over permuted physical blocks, slot mapping
   std::vector<int64_t> ids(T), pos(T);
-  for (int t = 0; t < T; ++t) ids[t] = vid(rng), pos[t] = t;
-  // stand-ins for the GEMM outputs between the ops (random, seeded)
-  std::vector<float> attn_out((size_t)T * H), q((size_t)T * q_size), k((size_t)T * kv_size), mlp_in((size_t)T * 2 * I),
-      down_out((size_t)T * H);
-  for (auto* v : {&attn_out, &q, &k, &mlp_in, &down_out})
-    for (auto& x : *v) x = n01(rng);
+  std::vector<int32_t> qseq(T), qlen(T), slots(T), tables(S * max_blocks);
+  const int32_t perm[num_blocks] = {5, 2, 7, 0, 3, 6, 1, 4};
+  for (int s = 0; s < S; ++s)
+    for (int b = 0; b < max_blocks; ++b) tables[s * max_blocks + b] = perm[s * max_blocks + b];
+  for (int t = 0; t < T; ++t) {
+    const int s = t / per, p = t % per;
+    ids[t] = vid(rng), pos[t] = p, qseq[t] = s, qlen[t] = p + 1;
+    slots[t] = tables[s * max_blocks + p / bs] * bs + p % bs;
+  }
 
-  Dev<uint8_t> d_w8(w8);
-  Dev<uint16_t> d_ws(ws);
+  Dev<uint8_t> d_emb8(emb.w8), d_qkv8(wqkv.w8), d_o8(wo.w8), d_gu8(wgu.w8), d_dn8(wdn.w8);
+  Dev<uint16_t> d_embs(emb.ws), d_qkvs(wqkv.ws), d_os(wo.ws), d_gus(wgu.ws), d_dns(wdn.ws);
   Dev<float> d_in_ln(in_ln), d_post_ln(post_ln), d_final_ln(final_ln), d_qn(q_norm), d_kn(k_norm), d_inv(inv);
   Dev<int64_t> d_ids(ids), d_pos(pos);
-  Dev<float> hidden((size_t)T * H), residual((size_t)T * H), norm((size_t)T * H);
-  Dev<float> d_q(q), d_k(k), d_gate(mlp_in), mlp((size_t)T * I);
+  Dev<int32_t> d_qseq(qseq), d_qlen(qlen), d_slots(slots), d_tables(tables);
+  Dev<float> hidden((size_t)T * H), residual((size_t)T * H), norm((size_t)T * H), d_q((size_t)T * q_size),
+      d_k((size_t)T * kv_size), d_v((size_t)T * kv_size), attn((size_t)T * q_size), gate((size_t)T * 2 * I),
+      mlp((size_t)T * I), logits((size_t)V);
+  Dev<float> k_cache((size_t)num_blocks * bs * kv_size), v_cache((size_t)num_blocks * bs * kv_size);
+  auto sync = [] { CHECK_HIP(hipDeviceSynchronize()); };
+  std::vector<double> ideal, bound;
 
-  // ---- the forward's op sequence, as model.cpp issues it ----
-  hip_embedding_q8(d_ids.d, d_w8.d, d_ws.d, T, H, hidden.d);                            // :756 via :689-696
-  hip_rms_norm_add(hidden.d, residual.d, d_in_ln.d, norm.d, T, H, eps);                 // :762 (residual = 0)
-  hip_rms_norm(d_q.d, d_qn.d, d_q.d, T * heads, hd, eps);                               // :774 QK-norm, in place
-  hip_rms_norm(d_k.d, d_kn.d, d_k.d, T * kv_heads, hd, eps);                            // :775
-  hip_rope_inplace(d_q.d, d_pos.d, T, heads, hd, q_size, d_inv.d);                      // :777
-  hip_rope_inplace(d_k.d, d_pos.d, T, kv_heads, hd, kv_size, d_inv.d);                  // :778
-  std::vector<float> emb_gpu = hidden.host(), res1 = residual.host(), norm1 = norm.host();
-  CHECK_HIP(hipMemcpy(hidden.d, attn_out.data(), attn_out.size() * 4, hipMemcpyHostToDevice));  // o_proj stand-in
-  hip_rms_norm_add(hidden.d, residual.d, d_post_ln.d, norm.d, T, H, eps);               // :787
-  std::vector<float> res2 = residual.host(), norm2 = norm.host();
-  hip_silu_and_mul(d_gate.d, mlp.d, T, I);                                              // :830
-  CHECK_HIP(hipMemcpy(hidden.d, down_out.data(), down_out.size() * 4, hipMemcpyHostToDevice));  // down stand-in
-  hip_rms_norm_add(hidden.d, residual.d, d_final_ln.d, norm.d, T, H, eps);              // :835 final norm
-  CHECK_HIP(hipDeviceSynchronize());
-  std::vector<float> q_gpu = d_q.host(), k_gpu = d_k.host(), mlp_gpu = mlp.host(), res3 = residual.host(),
-                     norm3 = norm.host();
+  // ---- the forward's op sequence, as model.cpp issues it, checked stage by stage ----
+  hip_embedding_q8(d_ids.d, d_emb8.d, d_embs.d, T, H, hidden.d);  // :756 via :689-696
+  sync();
+  std::vector<float> x = hidden.host(), r_emb((size_t)T * H);
+  orc_embedding_q8_split(ids.data(), emb.w8.data(), emb.ws.data(), T, H, r_emb.data(), ORC_F32);
+  expect("embedding (bit-exact)", x, r_emb, true);
 
-  // ---- the same sequence on the oracle ----
-  std::vector<float> r_emb((size_t)T * H), r_res((size_t)T * H, 0.f), r_norm((size_t)T * H), r_q = q, r_k = k,
-                     r_mlp((size_t)T * I);
-  orc_embedding_q8_split(ids.data(), w8.data(), ws.data(), T, H, r_emb.data(), ORC_F32);
-  expect("embedding (bit-exact)", emb_gpu, r_emb, true);
-  orc_rms_norm_add(r_emb.data(), r_res.data(), in_ln.data(), r_norm.data(), T, H, eps, ORC_F32);
-  expect("layer-0 residual (bit-exact)", res1, r_res, true);
-  expect("input_layernorm", norm1, r_norm, false);
-  std::vector<float> nq(r_q.size()), nk(r_k.size());
-  orc_rms_norm(r_q.data(), q_norm.data(), nq.data(), (int64_t)T * heads, hd, eps, ORC_F32);
-  orc_rms_norm(r_k.data(), k_norm.data(), nk.data(), (int64_t)T * kv_heads, hd, eps, ORC_F32);
+  auto norm_add = [&](const char* tag, const std::vector<float>& w, Dev<float>& wdev) {
+    std::vector<float> h = hidden.host(), r = residual.host(), n((size_t)T * H);
+    hip_rms_norm_add(hidden.d, residual.d, wdev.d, norm.d, T, H, eps);  // :762 / :787 / :835
+    sync();
+    orc_rms_norm_add(h.data(), r.data(), w.data(), n.data(), T, H, eps, ORC_F32);
+    char buf[96];
+    std::snprintf(buf, sizeof buf, "%s residual (bit-exact)", tag);
+    expect(buf, residual.host(), r, true);
+    std::snprintf(buf, sizeof buf, "%s norm", tag);
+    expect(buf, norm.host(), n, false);
+  };
+  norm_add("input_layernorm", in_ln, d_in_ln);
+
+  // qkv projections: one fused weight, row slices (:764-767)
+  std::vector<float> nx = norm.host();
+  hip_matmul_q8(norm.d, d_qkv8.d, d_qkvs.d, T, q_size, H, d_q.d);
+  hip_matmul_q8(norm.d, d_qkv8.d + (size_t)q_size * H, d_qkvs.d + (size_t)q_size * H / 32, T, kv_size, H, d_k.d);
+  hip_matmul_q8(norm.d, d_qkv8.d + (size_t)(q_size + kv_size) * H, d_qkvs.d + (size_t)(q_size + kv_size) * H / 32, T,
+                kv_size, H, d_v.d);
+  sync();
+  oracle_gemm(nx, wqkv.w8.data(), wqkv.ws.data(), T, q_size, H, ideal, bound);
+  expect_within("q projection (Q8_0 GEMM)", d_q.host(), ideal, bound);
+  oracle_gemm(nx, wqkv.w8.data() + (size_t)q_size * H, wqkv.ws.data() + (size_t)q_size * H / 32, T, kv_size, H, ideal,
+              bound);
+  expect_within("k projection (row slice)", d_k.host(), ideal, bound);
+  oracle_gemm(nx, wqkv.w8.data() + (size_t)(q_size + kv_size) * H,
+              wqkv.ws.data() + (size_t)(q_size + kv_size) * H / 32, T, kv_size, H, ideal, bound);
+  expect_within("v projection (row slice)", d_v.host(), ideal, bound);
+
+  // QK-norm then RoPE (:774-778)
+  std::vector<float> q = d_q.host(), k = d_k.host(), v = d_v.host();
+  hip_rms_norm(d_q.d, d_qn.d, d_q.d, T * heads, hd, eps);
+  hip_rms_norm(d_k.d, d_kn.d, d_k.d, T * kv_heads, hd, eps);
+  hip_rope_inplace(d_q.d, d_pos.d, T, heads, hd, q_size, d_inv.d);
+  hip_rope_inplace(d_k.d, d_pos.d, T, kv_heads, hd, kv_size, d_inv.d);
+  sync();
+  std::vector<float> nq(q.size()), nk(k.size());
+  orc_rms_norm(q.data(), q_norm.data(), nq.data(), (int64_t)T * heads, hd, eps, ORC_F32);
+  orc_rms_norm(k.data(), k_norm.data(), nk.data(), (int64_t)T * kv_heads, hd, eps, ORC_F32);
   orc_rope(nq.data(), pos.data(), T, heads, hd, q_size, inv.data(), ORC_F32);
   orc_rope(nk.data(), pos.data(), T, kv_heads, hd, kv_size, inv.data(), ORC_F32);
-  expect("q: QK-norm then RoPE", q_gpu, nq, false, 1e-6f);
-  expect("k: QK-norm then RoPE", k_gpu, nk, false, 1e-6f);
-  orc_rms_norm_add(attn_out.data(), r_res.data(), post_ln.data(), r_norm.data(), T, H, eps, ORC_F32);
-  expect("post-attention residual (bit-exact)", res2, r_res, true);
-  expect("post_attention_layernorm", norm2, r_norm, false);
-  orc_silu_and_mul(mlp_in.data(), r_mlp.data(), T, I, ORC_F32);
-  expect("silu_and_mul", mlp_gpu, r_mlp, false);
-  orc_rms_norm_add(down_out.data(), r_res.data(), final_ln.data(), r_norm.data(), T, H, eps, ORC_F32);
-  expect("final residual (bit-exact)", res3, r_res, true);
-  expect("final norm", norm3, r_norm, false);
+  expect("q: QK-norm then RoPE", d_q.host(), nq, false, 1e-6f);
+  expect("k: QK-norm then RoPE", d_k.host(), nk, false, 1e-6f);
+
+  // KV store, then paged attention (:780-784)
+  std::vector<float> qg = d_q.host(), kg = d_k.host();
+  hip_store_kv(d_k.d, d_v.d, k_cache.d, v_cache.d, d_slots.d, T, kv_heads, hd);
+  sync();
+  std::vector<float> kc_ref(k_cache.n, 0.f), vc_ref(v_cache.n, 0.f);
+  orc_store_kv(kg.data(), v.data(), kc_ref.data(), vc_ref.data(), slots.data(), T, kv_heads, hd, ORC_F32);
+  expect("k cache (bit-exact)", k_cache.host(), kc_ref, true);
+  expect("v cache (bit-exact)", v_cache.host(), vc_ref, true);
+  hip_paged_attention(d_q.d, attn.d, k_cache.d, v_cache.d, d_qseq.d, d_qlen.d, d_tables.d, T, heads, kv_heads, hd, bs,
+                      max_blocks, scale);
+  sync();
+  {
+    std::vector<float> ao((size_t)T * q_size), vmax((size_t)T * heads);
+    std::vector<double> ex((size_t)T * q_size), tol((size_t)T * q_size);
+    orc_paged_attention(qg.data(), ao.data(), kc_ref.data(), vc_ref.data(), qseq.data(), qlen.data(), tables.data(), T,
+                        heads, kv_heads, hd, bs, max_blocks, scale, ORC_F32, ex.data(), vmax.data());
+    for (size_t i = 0; i < tol.size(); ++i) tol[i] = 1e-4 * vmax[i / hd] + 1e-7;
+    expect_within("paged attention", attn.host(), ex, tol);
+  }
+
+  // o_proj, post-attention norm (:786-787)
+  std::vector<float> ax = attn.host();
+  hip_matmul_q8(attn.d, d_o8.d, d_os.d, T, H, q_size, hidden.d);
+  sync();
+  oracle_gemm(ax, wo.w8.data(), wo.ws.data(), T, H, q_size, ideal, bound);
+  expect_within("o projection", hidden.host(), ideal, bound);
+  norm_add("post_attention_layernorm", post_ln, d_post_ln);
+
+  // MLP (:828-830)
+  nx = norm.host();
+  hip_matmul_q8(norm.d, d_gu8.d, d_gus.d, T, 2 * I, H, gate.d);
+  sync();
+  oracle_gemm(nx, wgu.w8.data(), wgu.ws.data(), T, 2 * I, H, ideal, bound);
+  expect_within("gate_up projection", gate.host(), ideal, bound);
+  std::vector<float> gu = gate.host(), r_mlp((size_t)T * I);
+  hip_silu_and_mul(gate.d, mlp.d, T, I);
+  sync();
+  orc_silu_and_mul(gu.data(), r_mlp.data(), T, I, ORC_F32);
+  expect("silu_and_mul", mlp.host(), r_mlp, false);
+  std::vector<float> mx = mlp.host();
+  hip_matmul_q8(mlp.d, d_dn8.d, d_dns.d, T, H, I, hidden.d);
+  sync();
+  oracle_gemm(mx, wdn.w8.data(), wdn.ws.data(), T, H, I, ideal, bound);
+  expect_within("down projection", hidden.host(), ideal, bound);
+
+  // final norm (:835) and the tied lm_head on the last token (:840-844; m = 1, the decode GEMV)
+  norm_add("final norm", final_ln, d_final_ln);
+  std::vector<float> last(norm.host().begin() + (size_t)(T - 1) * H, norm.host().begin() + (size_t)T * H);
+  hip_matmul_q8(norm.d + (size_t)(T - 1) * H, d_emb8.d, d_embs.d, 1, V, H, logits.d);
+  sync();
+  oracle_gemm(last, emb.w8.data(), emb.ws.data(), 1, V, H, ideal, bound);
+  expect_within("lm_head logits (m = 1)", logits.host(), ideal, bound);
+
   std::printf(failures ? "DROPIN CHAIN FAILED\n" : "DROPIN CHAIN OK\n");
   return failures ? 1 : 0;
 }

@@ -1,6 +1,8 @@
 """Runs tests/cpp/dropin_chain: a C++ program that calls the drop-in C ABI in
-the order src/model.cpp:756-835 does and checks every stage against the C
-oracle (bit-exact gathers and residuals, tolerance elsewhere)."""
+the order src/model.cpp:756-844 does -- a whole layer: embedding, norms, the
+Q8_0 projections, QK-norm, RoPE, KV store, paged attention, SwiGLU, final norm,
+lm_head -- and checks every stage against the C oracle (bit-exact gathers,
+residuals and cache writes; the stated tolerance or bound elsewhere)."""
 from __future__ import annotations
 
 import subprocess
