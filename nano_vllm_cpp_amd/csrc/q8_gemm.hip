@@ -44,7 +44,9 @@ constexpr int kGemmCPR = kGemmKC / 16;       // 16-byte chunks per LDS row
 constexpr int kGemmRPI = 1024 / kGemmKC;     // rows per 1 KB wave DMA transfer
 constexpr int kGemmSwz = 256 / kGemmKC;      // rows sharing a bank offset
 constexpr int kGemmBlk = kGemmKC / 32;       // Q8_0 blocks per stage
-constexpr int kGemmStage = (kGemmBM + kGemmBN) * kGemmKC + kGemmBN * kGemmBlk * 4;  // + fp32 block scales
+// + the block scales: fp16 values in 4-byte slots (an LDS DMA of 2 bytes per lane
+// fills one dword per lane, zero-extended)
+constexpr int kGemmStage = (kGemmBM + kGemmBN) * kGemmKC + kGemmBN * kGemmBlk * 4;
 constexpr int kGemmLds = 2 * kGemmStage;     // double-buffered
 constexpr int kGemmThreads = 256;
 constexpr int kGemmGroupM = 8;               // tile rows per group of the tile order
@@ -200,19 +202,20 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(3)
     dma_chunk[i] = swz(row, lane % kGemmCPR);
     dma_off[i] = (uint32_t)(row * k) + (uint32_t)(dma_chunk[i] * 16);
   }
-  // Block scales: thread t loads column col0 + (t & 127), blocks kSpt * (t >> 7) + e.
-  constexpr int kSpt = kGemmBlk / 2;
+  // Block scales: [block][column] after the tiles, by LDS DMA as well (2 bytes per
+  // lane, landing in 4-byte slots): thread t moves column t % 128 of block t / 128.
+  static_assert(kGemmBlk * kGemmBN == kGemmThreads, "one scale per thread and stage");
   const int sc_c = threadIdx.x & (kGemmBN - 1);
-  const int sc_b = kSpt * (threadIdx.x >> 7);
+  const int sc_b = threadIdx.x >> 7;
   const uint32_t sc_off = (uint32_t)((sc_c * nblk + sc_b) * 2);
-  uint32_t sc_raw[kSpt];
 
   const int nstages = (int)((k + kGemmKC - 1) / kGemmKC);
   const bool partial_last = k % kGemmKC != 0;
-  // Loads stage st into LDS buffer `buf` (DMA for the tiles, registers for the scales).
+  // Loads stage st into LDS buffer `buf`, all by DMA.
   auto issue = [&](int st, int buf) {
     uint8_t* stage = lds + buf * kGemmStage;
     const uint32_t kc = (uint32_t)st * kGemmKC;
+    uint8_t* sc_dst = stage + (kGemmBM + kGemmBN) * kGemmKC + wave * 256;  // this wave's 64 scale slots
     if (partial_last && st == nstages - 1) {  // uniform, at most once per tile
 #pragma unroll
       for (int i = 0; i < kDma; ++i) {
@@ -226,12 +229,9 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(3)
                                                       (32 * wave + kGemmRPI * i) * kGemmKC),
             16, off, 0, 0, 0);
       }
-#pragma unroll
-      for (int e = 0; e < kSpt; ++e) {
-        const int64_t b = (int64_t)st * kGemmBlk + sc_b + e;
-        sc_raw[e] = __builtin_amdgcn_raw_buffer_load_b16(rsc, b < nblk ? sc_off + 2 * e + st * kGemmBlk * 2 : kOob,
-                                                         0, 0);
-      }
+      const int64_t b = (int64_t)st * kGemmBlk + sc_b;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsc, (__attribute__((address_space(3))) void*)sc_dst, 2,
+                                               b < nblk ? sc_off + st * kGemmBlk * 2 : kOob, 0, 0, 0);
     } else {
 #pragma unroll
       for (int i = 0; i < kDma; ++i) {
@@ -244,19 +244,12 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(3)
                                                       (32 * wave + kGemmRPI * i) * kGemmKC),
             16, dma_off[i], kc, 0, 0);
       }
-#pragma unroll
-      for (int e = 0; e < kSpt; ++e)
-        sc_raw[e] = __builtin_amdgcn_raw_buffer_load_b16(rsc, sc_off + 2 * e, (uint32_t)st * kGemmBlk * 2, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsc, (__attribute__((address_space(3))) void*)sc_dst, 2, sc_off,
+                                               (uint32_t)st * kGemmBlk * 2, 0, 0);
     }
   };
-  auto store_scales = [&](int buf) {
-    float* s = reinterpret_cast<float*>(lds + buf * kGemmStage + (kGemmBM + kGemmBN) * kGemmKC);
-#pragma unroll
-    for (int e = 0; e < kSpt; ++e) s[(sc_b + e) * kGemmBN + sc_c] = fp16_bits_to_float((uint16_t)sc_raw[e]);
-  };
-  // This wave's LDS DMA (and scale loads) must land before the barrier that publishes a stage.
-  auto publish = [&](int buf) {
-    store_scales(buf);
+  // This wave's LDS DMA must land before the barrier that publishes a stage.
+  auto publish = [&] {
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
     __syncthreads();
   };
@@ -282,8 +275,8 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(3)
     fa1 = *reinterpret_cast<const i32x4*>(base + fa_addr + 32 * kGemmKC);
     fb0 = *reinterpret_cast<const i32x4*>(base + fb_addr);
     fb1 = *reinterpret_cast<const i32x4*>(base + fb_addr + 32 * kGemmKC);
-    s0 = *reinterpret_cast<const float*>(base + fs_addr0 + bi * kGemmBN * 4);
-    s1 = *reinterpret_cast<const float*>(base + fs_addr0 + bi * kGemmBN * 4 + 32 * 4);
+    s0 = fp16_bits_to_float(*reinterpret_cast<const uint16_t*>(base + fs_addr0 + bi * kGemmBN * 4));
+    s1 = fp16_bits_to_float(*reinterpret_cast<const uint16_t*>(base + fs_addr0 + bi * kGemmBN * 4 + 32 * 4));
   };
   auto apply = [](float (&c)[16], const i32x16& d, float sc) {
 #pragma unroll
@@ -291,7 +284,7 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(3)
   };
 
   issue(0, 0);
-  publish(0);
+  publish();
   const int nb = nstages * kGemmBlk;
   read_frags(0);
   i32x16 d0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa0, fb0, i32x16{}, 0, 0, 0);
@@ -309,7 +302,7 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(3)
     const i32x16 d2 = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa1, fb0, i32x16{}, 0, 0, 0);
     const i32x16 d3 = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa1, fb1, i32x16{}, 0, 0, 0);
     const float c0 = s0, c1 = s1;
-    if (bi == kGemmBlk - 1) publish((st + 1) & 1);
+    if (bi == kGemmBlk - 1) publish();
     read_frags(g + 1);  // LDS latency hides behind the first two applies
     apply(acc[0][0], d0, c0);
     apply(acc[0][1], d1, c1);
