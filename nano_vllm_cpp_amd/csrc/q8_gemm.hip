@@ -347,124 +347,146 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(3)
 // Decode-shaped product (m <= kGemvMaxM rows): bound by streaming the weights
 // once from HBM, so the layout serves the loads.
 //
-// A wave owns C groups of 16 weight columns and a contiguous range of K; S waves
-// share a column set (splitting K) and meet in LDS at the end, summed in split
-// order.  A workgroup holds 8 / S column sets; the host picks S and C per shape.
-// The workgroup first stages the block scales of its columns in LDS (coalesced
-// rows of k/16 bytes), so the stream itself issues only weight and activation
-// loads.
+// A wave owns 16 weight columns and a contiguous range of K; S waves of a
+// workgroup share a column group (splitting K) and meet in LDS at the end,
+// summed in split order; a workgroup holds 4 / S column groups.  The weights go
+// HBM -> LDS by DMA in 256-byte runs per column (one 1 KB transfer = 4 columns x
+// 256 B, the K offset in the scalar offset, so a stage costs no VALU), into a
+// wave-private double buffer: the next stage is in flight while the current one
+// is computed.  16-byte chunk c of column j sits at position c ^ (j % 16), so the
+// 16 columns' reads of one chunk hit 16 distinct bank groups.  The block scales
+// of the workgroup's columns are staged in LDS once.
 //
-// Per block pair (64 bytes of K) lane l = 16 q + j loads 16 contiguous bytes,
-// k in [16 q, 16 q + 16), of weight column j (of each group) and of activation
-// row j -- the operand layout of v_mfma_i32_16x16x64_i8; one activation load
-// serves the C groups.  Lanes q = 0, 1 hold the pair's first block, q = 2, 3 its
-// second; the block scales differ, so each pair and group takes two MFMAs, each
-// with the activation lanes of the other block zeroed (the K = 64 instruction
-// then sums exactly one block).  MFMA time is idle capacity here.
+// Per block pair (64 bytes of K) lane l = 16 q + j holds 16 bytes, k in
+// [16 q, 16 q + 16), of weight column j and of activation row j -- the operand
+// layout of v_mfma_i32_16x16x64_i8.  Lanes q = 0, 1 hold the pair's first block,
+// q = 2, 3 its second; the block scales differ, so each pair takes two MFMAs,
+// each with the activation lanes of the other block zeroed (the K = 64
+// instruction then sums exactly one block).  MFMA time is idle capacity here.
 constexpr int kGemvMaxM = 16;
-constexpr int kGemvWaves = 8;
-constexpr int kGemvUnroll = 4;          // block pairs in flight per lane
-constexpr int kGemvScaleLds = 32768;    // bytes of LDS for the staged scales
+constexpr int kGvKC = 256;                        // bytes of K per stage (4 block pairs)
+constexpr int kGvWaveBuf = 16 * kGvKC;            // one stage of one wave's 16 columns
+constexpr int kGemvScaleLds = 32768;              // bytes of LDS for the staged scales
 
-template <int S, int C>
-constexpr int gemv_cols() { return kGemvWaves / S * C * 16; }  // columns per workgroup
+template <int W, int S>
+constexpr int gemv_cols() { return W / S * 16; }  // columns per workgroup of W waves
 
-template <typename TO, int S, int C>
-__global__ __launch_bounds__(kGemvWaves * 64) void q8_gemv_kernel(const int8_t* __restrict__ xq,
+template <typename TO, int W, int S>
+__global__ __launch_bounds__(W * 64) void q8_gemv_kernel(const int8_t* __restrict__ xq,
                                                                    const float* __restrict__ rscale,
                                                                    const int8_t* __restrict__ w8,
                                                                    const uint16_t* __restrict__ ws,
                                                                    TO* __restrict__ out, int64_t m, int64_t n,
                                                                    int64_t k) {
-  constexpr int kCols = gemv_cols<S, C>();
-  __shared__ float part[kGemvWaves][C][16][17];
-  extern __shared__ __attribute__((aligned(16))) uint16_t sc_lds[];  // [kCols][nblk]
+  constexpr int kCols = gemv_cols<W, S>();
+  constexpr int kGvDmaLds = W * 2 * kGvWaveBuf;
+  __shared__ float part[W][16][17];
+  extern __shared__ __attribute__((aligned(16))) uint8_t dyn[];  // [DMA buffers][scales]
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
-  const int set = wave / S, split = wave % S;
+  const int grp = wave / S, split = wave % S;
   const int j = lane & 15, q = lane >> 4;
   const int64_t wg_c0 = (int64_t)blockIdx.x * kCols;
   const int64_t nblk = k / 32, npairs = (nblk + 1) / 2;
   const int64_t wg_cols = n - wg_c0 < kCols ? n - wg_c0 : kCols;
+  uint16_t* sc_lds = reinterpret_cast<uint16_t*>(dyn + kGvDmaLds);
 
-  {  // stage this workgroup's block scales: wg_cols rows of nblk fp16 values
+  {  // stage this workgroup's block scales: wg_cols rows of nblk fp16 values,
+     // whole 4-byte words, then an odd last value by itself (a 4-byte load that
+     // straddles the end of the slab reads as zero entirely)
     const __amdgpu_buffer_rsrc_t rs = make_rsrc(ws + wg_c0 * nblk, wg_cols * nblk * 2);
-    // whole 4-byte words, then an odd last value by itself (a 4-byte load that
-    // straddles the end of the slab reads as zero entirely)
     const int64_t cnt = wg_cols * nblk;
     uint32_t* dst = reinterpret_cast<uint32_t*>(sc_lds);
-    for (int64_t i = threadIdx.x; i < cnt / 2; i += kGemvWaves * 64)
+    for (int64_t i = threadIdx.x; i < cnt / 2; i += W * 64)
       dst[i] = __builtin_amdgcn_raw_buffer_load_b32(rs, (uint32_t)(4 * i), 0, 0);
     if ((cnt & 1) && threadIdx.x == 0)
       sc_lds[cnt - 1] = (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(rs, (uint32_t)(2 * (cnt - 1)), 0, 0);
     __syncthreads();
   }
 
-  const int64_t c0 = wg_c0 + (int64_t)set * C * 16;  // this wave's first column
-  const int64_t cols = n - c0 < C * 16 ? n - c0 : C * 16;
+  const int64_t c0 = wg_c0 + (int64_t)grp * 16;  // this wave's first column
+  const int64_t cols = n - c0 < 16 ? n - c0 : 16;
   const int64_t p_begin = npairs * split / S, p_end = npairs * (split + 1) / S;
-  float acc[C][4];
-#pragma unroll
-  for (int g = 0; g < C; ++g)
-#pragma unroll
-    for (int v = 0; v < 4; ++v) acc[g][v] = 0.0f;
+  float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 
-  if (cols > 0) {  // uniform per wave
+  if (cols > 0 && p_end > p_begin) {  // uniform per wave
     // rows past m / columns past n fall outside these resources and read zero
     const __amdgpu_buffer_rsrc_t rw = make_rsrc(w8 + c0 * k, cols * k);
     const __amdgpu_buffer_rsrc_t rx = make_rsrc(xq, m * k);
-    const uint32_t lane_off = (uint32_t)(j * k) + 16u * q;  // weight column j and activation row j
-    const uint16_t* sc_col = sc_lds + ((int64_t)set * C * 16 + j) * nblk;
-    for (int64_t p0 = p_begin; p0 < p_end; p0 += kGemvUnroll) {
-      i32x4 wv[kGemvUnroll][C], xv[kGemvUnroll];
+    uint8_t* wbuf = dyn + wave * 2 * kGvWaveBuf;
+    // DMA lane l of transfer i: column 4 i + l / 16, LDS position l % 16, fetching chunk (l % 16) ^ column
+    uint32_t dma_off[4];
 #pragma unroll
-      for (int u = 0; u < kGemvUnroll; ++u) {
-        const int64_t p = p0 + u;
-        const bool ok = p < p_end && 64 * p + 16 * q < k;
-        const uint32_t off = ok ? lane_off + (uint32_t)(64 * p) : kOob;
-        xv[u] = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, off, 0, 0));
+    for (int i = 0; i < 4; ++i) {
+      const int col = 4 * i + (lane >> 4);
+      dma_off[i] = (uint32_t)(col * k) + 16u * (uint32_t)((lane & 15) ^ col);
+    }
+    const int64_t kb0 = 64 * p_begin;
+    const int nst = (int)((p_end - p_begin + 3) / 4);
+    auto issue = [&](int st) {
+      uint8_t* dst = wbuf + (st & 1) * kGvWaveBuf;
+      const uint32_t soff = (uint32_t)(kb0 + (int64_t)st * kGvKC);
 #pragma unroll
-        for (int g = 0; g < C; ++g)
-          wv[u][g] = __builtin_bit_cast(
-              i32x4, __builtin_amdgcn_raw_buffer_load_b128(rw, ok ? off + (uint32_t)(g * 16 * k) : kOob, 0, 0));
+      for (int i = 0; i < 4; ++i)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (__attribute__((address_space(3))) void*)(dst + i * 1024), 16,
+                                                 dma_off[i], soff, 0, 0);
+    };
+    const uint32_t x_off = (uint32_t)(j * k) + 16u * q;  // activation row j
+    const uint16_t* sc_col = sc_lds + ((int64_t)grp * 16 + j) * nblk;
+    issue(0);
+    for (int st = 0; st < nst; ++st) {
+      // this stage's activation loads first, then the next stage's transfers: one
+      // vmcnt(4) then covers both this stage's transfers and its activations
+      const int64_t pst = p_begin + 4 * st;
+      const int npp = p_end - pst < 4 ? (int)(p_end - pst) : 4;
+      i32x4 xv[4];
+#pragma unroll
+      for (int pp = 0; pp < 4; ++pp) {
+        const int64_t p = pst + pp;
+        const bool ok = pp < npp && 64 * p + 16 * q < k;
+        xv[pp] = __builtin_bit_cast(
+            i32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, ok ? x_off + (uint32_t)(64 * p) : kOob, 0, 0));
       }
+      if (st + 1 < nst) {
+        issue(st + 1);
+        __builtin_amdgcn_s_waitcnt(0x0F74);  // vmcnt(4): everything before the 4 transfers just issued
+      } else {
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+      }
+      const uint8_t* src = wbuf + (st & 1) * kGvWaveBuf + j * kGvKC;
 #pragma unroll
-      for (int u = 0; u < kGemvUnroll; ++u) {
-        const int64_t p = p0 + u;
+      for (int pp = 0; pp < 4; ++pp) {
+        if (pp >= npp) break;  // uniform
+        const int64_t p = pst + pp;
+        const i32x4 wv = *reinterpret_cast<const i32x4*>(src + 16 * ((4 * pp + q) ^ j));
         const i32x4 z = {0, 0, 0, 0};
-        const i32x4 x_lo = q < 2 ? xv[u] : z;  // first block of the pair
-        const i32x4 x_hi = q < 2 ? z : xv[u];  // second block
-        const int64_t b = p < p_end ? 2 * p : 0;  // past the range: zero data, any in-range scale
+        const i32x4 x_lo = q < 2 ? xv[pp] : z;  // first block of the pair
+        const i32x4 x_hi = q < 2 ? z : xv[pp];  // second block
+        const int64_t b = 2 * p;
+        const float s_lo = fp16_bits_to_float(sc_col[b]);
+        const float s_hi = b + 1 < nblk ? fp16_bits_to_float(sc_col[b + 1]) : 0.0f;
+        const i32x4 d_lo = __builtin_amdgcn_mfma_i32_16x16x64_i8(x_lo, wv, z, 0, 0, 0);
+        const i32x4 d_hi = __builtin_amdgcn_mfma_i32_16x16x64_i8(x_hi, wv, z, 0, 0, 0);
 #pragma unroll
-        for (int g = 0; g < C; ++g) {
-          const uint16_t* sg = sc_col + (int64_t)g * 16 * nblk;
-          const float s_lo = fp16_bits_to_float(sg[b]);
-          const float s_hi = b + 1 < nblk ? fp16_bits_to_float(sg[b + 1]) : 0.0f;
-          const i32x4 d_lo = __builtin_amdgcn_mfma_i32_16x16x64_i8(x_lo, wv[u][g], z, 0, 0, 0);
-          const i32x4 d_hi = __builtin_amdgcn_mfma_i32_16x16x64_i8(x_hi, wv[u][g], z, 0, 0, 0);
-#pragma unroll
-          for (int v = 0; v < 4; ++v) {
-            acc[g][v] = fmaf(s_lo, (float)d_lo[v], acc[g][v]);
-            acc[g][v] = fmaf(s_hi, (float)d_hi[v], acc[g][v]);
-          }
+        for (int v = 0; v < 4; ++v) {
+          acc[v] = fmaf(s_lo, (float)d_lo[v], acc[v]);
+          acc[v] = fmaf(s_hi, (float)d_hi[v], acc[v]);
         }
       }
     }
   }
   // D layout of v_mfma_*_16x16: lane l, value v -> column l % 16, row 4 * (l / 16) + v.
 #pragma unroll
-  for (int g = 0; g < C; ++g)
-#pragma unroll
-    for (int v = 0; v < 4; ++v) part[wave][g][4 * q + v][j] = acc[g][v];
+  for (int v = 0; v < 4; ++v) part[wave][4 * q + v][j] = acc[v];
   __syncthreads();
-  for (int o = threadIdx.x; o < kCols * 16; o += kGemvWaves * 64) {
+  for (int o = threadIdx.x; o < kCols * 16; o += W * 64) {
     const int c = o % kCols, r = o / kCols;  // consecutive threads -> consecutive columns
-    const int st = c / (C * 16), g = (c / 16) % C, cj = c % 16;
+    const int g = c / 16, cj = c % 16;
     const int64_t col = wg_c0 + c;
     if (r < m && col < n) {
       float sum = 0.0f;
 #pragma unroll
-      for (int sp = 0; sp < S; ++sp) sum += part[st * S + sp][g][r][cj];
+      for (int sp = 0; sp < S; ++sp) sum += part[g * S + sp][r][cj];
       const float sc = rscale[r];
       const float inv = sc > 0.0f ? 1.0f / sc : 0.0f;  // the reference's adq (:358)
       gemm_store_out(out + r * n + col, sum * inv);
@@ -472,21 +494,22 @@ __global__ __launch_bounds__(kGemvWaves * 64) void q8_gemv_kernel(const int8_t* 
   }
 }
 
-// Picks the K split S and the column groups per wave C for a decode-shaped call
-// and launches; false if no configuration fits the LDS scale budget.
-template <typename TO, int S, int C>
+// Launches the GEMV with W waves per workgroup and K split S; false if the
+// staged scales would not fit.
+template <typename TO, int W, int S>
 bool try_gemv(const int8_t* xq, const float* rscale, const int8_t* w8, const uint16_t* ws, TO* out, int64_t m,
               int64_t n, int64_t k, hipStream_t stream) {
-  constexpr int kCols = gemv_cols<S, C>();
-  const int64_t lds = kCols * (k / 32) * 2;
-  if (lds > kGemvScaleLds) return false;
+  constexpr int kCols = gemv_cols<W, S>();
+  constexpr int kDma = W * 2 * kGvWaveBuf;
+  const int64_t sc_bytes = (kCols * (k / 32) * 2 + 15) & ~15;
+  if (sc_bytes > kGemvScaleLds) return false;
   static std::once_flag attr_once;
   std::call_once(attr_once, [] {
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&q8_gemv_kernel<TO, S, C>),
-                              hipFuncAttributeMaxDynamicSharedMemorySize, kGemvScaleLds);
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&q8_gemv_kernel<TO, W, S>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, kDma + kGemvScaleLds);
   });
   const int64_t wgs = (n + kCols - 1) / kCols;
-  q8_gemv_kernel<TO, S, C><<<dim3((unsigned)wgs), dim3(kGemvWaves * 64), (size_t)((lds + 3) & ~3), stream>>>(
+  q8_gemv_kernel<TO, W, S><<<dim3((unsigned)wgs), dim3(W * 64), (size_t)(kDma + sc_bytes), stream>>>(
       xq, rscale, w8, ws, out, m, n, k);
   return true;
 }
@@ -518,15 +541,14 @@ template <typename TO>
 int launch_gemm(const int8_t* xq, const float* rscale, const int8_t* w8, const uint16_t* ws, TO* out, int64_t m,
                 int64_t n, int64_t k, hipStream_t stream) {
   if (m <= kGemvMaxM) {
-    // Wide n: 4 column groups per wave (one activation load feeds four weight
-    // loads) and the fewest K splits that still give >= ~4096 waves; narrow n:
-    // one group per wave, K split 8 ways.  Smaller column sets when the staged
-    // scales would not fit.
-    const int64_t sets4 = (n + 63) / 64;
+    // fewest K splits that still give >= ~2048 waves (16 columns each); more splits
+    // when the staged scales of a wider column set would not fit
+    const int64_t groups = (n + 15) / 16;
     bool ok = false;
-    if (sets4 * 4 >= 4096) ok = try_gemv<TO, 4, 4>(xq, rscale, w8, ws, out, m, n, k, stream);
-    if (!ok && sets4 * 8 >= 4096) ok = try_gemv<TO, 8, 4>(xq, rscale, w8, ws, out, m, n, k, stream);
-    if (!ok) ok = try_gemv<TO, 8, 1>(xq, rscale, w8, ws, out, m, n, k, stream);
+    if (groups >= 2048) ok = try_gemv<TO, 4, 1>(xq, rscale, w8, ws, out, m, n, k, stream);
+    if (!ok && groups >= 1024) ok = try_gemv<TO, 4, 2>(xq, rscale, w8, ws, out, m, n, k, stream);
+    if (!ok && groups >= 512) ok = try_gemv<TO, 4, 4>(xq, rscale, w8, ws, out, m, n, k, stream);
+    if (!ok) ok = try_gemv<TO, 8, 8>(xq, rscale, w8, ws, out, m, n, k, stream);
     if (ok) return launch_status("q8_gemv_kernel");
   }
   static std::once_flag attr_once;
