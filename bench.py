@@ -56,7 +56,7 @@ def parse() -> argparse.Namespace:
     p.add_argument("--emb", default="", choices=["", "q8_0", "q8_0_blocks", "q4_k", "q5_k", "q6_k", "f16"],
                    help="embedding table format (default: the config's)")
     p.add_argument("--only", default="",
-                   help="comma list of ops (default emb,rms,rope,silu,copy,gemm,gemv,attn,attn_decode); "
+                   help="comma list of ops (default emb,rms,rope,silu,copy,gemm,gemv,split,attn,attn_decode); "
                         "also emb_rms, rms_q8, silu_q8 (fusions)")
     return p.parse_args()
 
@@ -80,7 +80,9 @@ def op_bytes(cfg, e: int, emb_fmt: str) -> dict[str, int]:
             # SwiGLU writing only the down projection's int8 rows and row scales
             "silu_q8": 2 * T * I * e + T * I + 4 * T,
             # decode GEMV (m = GEMV_M) at the gate_up shape: the weights once, plus activations and output
-            "gemv": int(2 * I * Hd * 34 / 32) + GEMV_M * Hd + 4 * GEMV_M + GEMV_M * 2 * I * e}
+            "gemv": int(2 * I * Hd * 34 / 32) + GEMV_M * Hd + 4 * GEMV_M + GEMV_M * 2 * I * e,
+            # on-device Q8_0 block split of the gate_up weights: 34 bytes in and 34 out per block
+            "split": 2 * I * Hd // 32 * 68}
 
 
 def main() -> int:
@@ -106,8 +108,8 @@ def main() -> int:
     g = torch.Generator(device=dev).manual_seed(cfg.seed)
     emb_fmt = args.emb or cfg.emb
     nbytes = op_bytes(cfg, e, emb_fmt)
-    only = set(filter(None, args.only.split(","))) or {"emb", "rms", "rope", "silu", "copy", "gemm", "gemv", "attn",
-                                                       "attn_decode"}
+    only = set(filter(None, args.only.split(","))) or {"emb", "rms", "rope", "silu", "copy", "gemm", "gemv", "split",
+                                                       "attn", "attn_decode"}
 
     def nsets(b: int) -> int:
         return max(2, -(-POOL_BYTES // b))
@@ -165,6 +167,13 @@ def main() -> int:
                               torch.empty(2 * I * Hd // 32, device=dev).uniform_(1e-3, 1e-2, generator=g).half()
                               .view(torch.int16)))
         gemv_out = torch.empty(GEMV_M, 2 * I, dtype=tdt, device=dev)
+    split_sets = []
+    if "split" in only:  # gate_up weights as GGUF blocks, rotated like the GEMV's
+        nb_split = 2 * I * Hd // 32
+        for _ in range(nsets(nbytes["split"])):
+            split_sets.append((torch.randint(0, 256, (nb_split * 34,), generator=g, device=dev, dtype=torch.uint8),
+                               torch.empty(nb_split * 32, dtype=torch.int8, device=dev),
+                               torch.empty(nb_split, dtype=torch.int16, device=dev)))
     attn_in = attn_dec = None
     bs_kv = 256  # the reference's KV block size (a multiple of 256, config.hpp:254)
     if "attn" in only:  # causal prefill over the config's sequences, KV already in the paged cache
@@ -257,6 +266,11 @@ def main() -> int:
         w8_, ws_ = gemv_sets[i % len(gemv_sets)]
         ops.matmul_q8_0(gxq1, gsc1, w8_, ws_, 2 * I, out=gemv_out)
 
+    def run_split(i):
+        blk_, w8_, ws_ = split_sets[i % len(split_sets)]
+        ops._check(ops.lib().nvf_q8_0_split_blocks(blk_.data_ptr(), nb_split, w8_.data_ptr(), ws_.data_ptr(),
+                                                   ops._stream()), "q8_0_split_blocks")
+
     def run_attn(i):
         q_, kc_, vc_, qs_, ql_, tb_ = attn_in
         ops.paged_attention(q_, kc_, vc_, qs_, ql_, tb_, bs_kv, cfg.head_dim ** -0.5, out=attn_out)
@@ -273,7 +287,7 @@ def main() -> int:
 
     table = [("emb", run_emb), ("rms", run_rms), ("rope", run_rope), ("silu", run_silu), ("emb_rms", run_emb_rms),
              ("rms_q8", run_rms_q8), ("silu_q8", run_silu_q8), ("copy", run_copy), ("gemm", run_gemm),
-             ("gemv", run_gemv), ("attn", run_attn), ("attn_decode", run_attn_decode)]
+             ("gemv", run_gemv), ("split", run_split), ("attn", run_attn), ("attn_decode", run_attn_decode)]
     active = [(n, f) for n, f in table if n in only]
 
     for i in range(args.warmup):
@@ -313,6 +327,9 @@ def main() -> int:
         if n == "gemv":
             entry.pop("tokens_per_s")
             entry["shape"] = f"m={GEMV_M} n={2 * I} k={Hd} (gate_up, decode)"
+        elif n == "split":
+            entry.pop("tokens_per_s")
+            entry["shape"] = f"{2 * I * Hd // 32} Q8_0 blocks (gate_up [{2 * I}, {Hd}])"
         elif n == "gemm":
             ops_n = 2.0 * T * (2 * I) * Hd
             entry.update({"shape": f"m={T} n={2 * I} k={Hd} (gate_up)", "TOP_s": round(ops_n / (t_us * 1e-6) / 1e12, 1),
@@ -386,6 +403,7 @@ def main() -> int:
         "roofline": roofline,
         "q8_gemm": res_ops.get("gemm"),
         "q8_gemv": res_ops.get("gemv"),
+        "q8_0_split": res_ops.get("split"),
         "paged_attention": {k: res_ops[k] for k in ("attn", "attn_decode") if k in res_ops} or None,
         "cpu_baseline": cpu,
     }

@@ -186,6 +186,14 @@ int nvf_embedding_rms_norm(const int64_t* ids, int format, const void* table, co
 int nvf_silu_and_mul_q8(const void* gate_up, void* out, float* row_scale, int8_t* q_out, int64_t rows,
                         int64_t inter, int dtype, void* stream);
 
+/* Splits nblocks interleaved 34-byte GGUF Q8_0 blocks (fp16 scale, then 32
+ * int8 values; the bytes GGUFLoader::load_q8_0 reads, src/gguf.cpp:353-362) into
+ * the planes nvf_matmul_q8_0 and nvf_embedding_q8_0 read: w8 [nblocks*32] and
+ * ws [nblocks] fp16 bits.  Replaces the host loop upload_q8_split
+ * (src/model.cpp:396-405), so the raw GGUF bytes are uploaded as they are.
+ * blocks and w8 16-byte aligned, ws 4-byte aligned. */
+int nvf_q8_0_split_blocks(const uint8_t* blocks, int64_t nblocks, int8_t* w8, uint16_t* ws, void* stream);
+
 /* Per-row int8 quantization of activations for the Q8_0 GEMM: row_scale[r] =
  * 127 / max|x[r,:]| (0 when the maximum is <= 1e-8) and xq[r,i] = (int8)
  * min(127, max(-127, x[r,i] * row_scale[r])), truncating -- q8_row_scale_kernel

@@ -58,6 +58,7 @@ SIGNATURES: dict[str, tuple] = {
     "nvf_embedding_rms_norm": (_i32, [_vp, _i32, _vp, _vp, _i64, _i64, _i64, _vp, _vp, _vp, _f32, _i32, _vp]),
     "nvf_rope_inv_freq": (_i32, [_f64, _i32, _vp]),
     "nvf_stream_copy": (_i32, [_vp, _vp, _i64, _vp]),
+    "nvf_q8_0_split_blocks": (_i32, [_vp, _i64, _vp, _vp, _vp]),
     "nvf_last_error": (C.c_char_p, []),
     "nvf_abi_version": (_i32, []),
 }
@@ -169,6 +170,22 @@ def rms_norm_q8(x: torch.Tensor, weight: torch.Tensor, eps: float, residual: tor
 # ---------------------------------------------------------------------------
 # Q8_0 GEMM
 # ---------------------------------------------------------------------------
+def q8_0_split_blocks(blocks: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """Splits interleaved 34-byte GGUF Q8_0 blocks (uint8 [nblocks*34], on the
+    device) into the planes the GEMM and the split-plane gather read: (w8 int8
+    [nblocks*32], ws int16 holding the fp16 bits [nblocks]).  The device form of the
+    reference's host-side upload_q8_split (src/model.cpp:396-405)."""
+    nbytes = blocks.numel()
+    if blocks.dtype != torch.uint8 or nbytes % 34:
+        raise ValueError("q8_0_split_blocks: blocks must be uint8 with a multiple of 34 bytes")
+    nblk = nbytes // 34
+    w8 = torch.empty(nblk * 32, dtype=torch.int8, device=blocks.device)
+    ws = torch.empty(nblk, dtype=torch.int16, device=blocks.device)
+    _check(lib().nvf_q8_0_split_blocks(_dev(blocks, "blocks"), nblk, _dev(w8, "w8"), _dev(ws, "ws"), _stream()),
+           "q8_0_split_blocks")
+    return w8, ws
+
+
 def q8_quantize_rows(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
     """Per-row int8 quantization for the Q8_0 GEMM: (row_scale [rows] fp32, xq [rows, k] int8)."""
     rows, k = x.shape

@@ -217,6 +217,16 @@ void orc_embedding_q8_blocks(const int64_t* ids, const uint8_t* blocks, int64_t 
     }
 }
 
+/* src/model.cpp:396-405 (upload_q8_split): block b's first two bytes are its
+ * fp16 scale (little-endian), the next 32 its int8 values. */
+void orc_q8_0_split_blocks(const uint8_t* blocks, int64_t nblocks, int8_t* w8, uint16_t* ws) {
+  for (int64_t b = 0; b < nblocks; ++b) {
+    const uint8_t* p = blocks + b * 34;
+    ws[b] = (uint16_t)(p[0] | (p[1] << 8));
+    for (int i = 0; i < 32; ++i) w8[b * 32 + i] = (int8_t)p[2 + i];
+  }
+}
+
 /* src/hip_ops.hip:600-609 (+ qk_w :184-193): element e = ids[t]*H + c lives in
  * superblock e>>8 at offset e&255; kinds 12/13/14 = Q4_K/Q5_K/Q6_K. */
 void orc_embedding_qk(const int64_t* ids, const uint8_t* wq, int64_t tokens, int64_t hidden, int kind,

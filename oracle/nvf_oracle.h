@@ -15,7 +15,9 @@
  *   fp16/bf16 codecs ......... exhaustive 65536-code round trip vs numpy + RNE
  *                              midpoint cases
  *   Q8_0 ..................... hand vector vulkanised/test_gguf2vk.py:77-83;
- *                              split-plane == 34 B-block equivalence
+ *                              split-plane == 34 B-block equivalence;
+ *                              block split: hand-built block bytes and the
+ *                              split -> join round trip
  *   Q4_K / Q6_K .............. bytes produced by the reference's own
  *                              gguf.cpp dequant (oracle/_ref, tests/golden)
  *   Q5_K ..................... closed forms on hand-built blocks (the
@@ -75,6 +77,8 @@ void orc_embedding_q8_split(const int64_t* ids, const uint8_t* w8, const uint16_
                             int64_t hidden, void* out, int out_dtype);
 void orc_embedding_q8_blocks(const int64_t* ids, const uint8_t* blocks, int64_t tokens, int64_t hidden,
                              void* out, int out_dtype);
+/* src/model.cpp:396-405 (upload_q8_split): 34-byte blocks -> w8 [nblocks*32], ws [nblocks]. */
+void orc_q8_0_split_blocks(const uint8_t* blocks, int64_t nblocks, int8_t* w8, uint16_t* ws);
 void orc_embedding_qk(const int64_t* ids, const uint8_t* wq, int64_t tokens, int64_t hidden, int kind,
                       int layout, void* out, int out_dtype);
 void orc_embedding_u16(const int64_t* ids, const uint16_t* table, int64_t tokens, int64_t hidden,

@@ -34,6 +34,7 @@ _ORACLE_SIGS = {
     "orc_dequant_q6k_block": (None, [_vp, _vp]),
     "orc_embedding_q8_split": (None, [_vp, _vp, _vp, _i64, _i64, _vp, _i32]),
     "orc_embedding_q8_blocks": (None, [_vp, _vp, _i64, _i64, _vp, _i32]),
+    "orc_q8_0_split_blocks": (None, [_vp, _i64, _vp, _vp]),
     "orc_embedding_qk": (None, [_vp, _vp, _i64, _i64, _i32, _i32, _vp, _i32]),
     "orc_embedding_u16": (None, [_vp, _vp, _i64, _i64, _i32, _vp, _i32]),
     "orc_rms_norm": (None, [_vp, _vp, _vp, _i64, _i64, _f32, _i32]),

@@ -60,6 +60,11 @@ def test_host_argument_checks():
     assert rc == -1 and "kind" in msg
     rc, msg = _status(lib.nvf_embedding_qk(p, p, 4, 256, 0, 12, 5, p, 1, None))
     assert rc == -1 and "layout" in msg
+    rc, msg = _status(lib.nvf_q8_0_split_blocks(p, 3, p, p + 2, None))
+    assert rc == -1 and "aligned" in msg
+    rc, msg = _status(lib.nvf_q8_0_split_blocks(p, -1, p, p, None))
+    assert rc == -1
+    assert lib.nvf_q8_0_split_blocks(None, 0, None, None, None) == 0      # empty: no launch
     rc, msg = _status(lib.nvf_embedding_q8_0_blocks(p, p, 4, 48, 0, p, 1, None))
     assert rc == -1 and "multiple of 32" in msg
     rc, msg = _status(lib.nvf_embedding_q8_0(p, p, None, 4, 64, 0, p, 1, None))

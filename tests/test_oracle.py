@@ -106,6 +106,48 @@ def test_q8_0_gather_exact_product(o):
     assert np.array_equal(a, b)
 
 
+def test_q8_0_split_blocks_hand_block(o):
+    """A hand-built 34-byte block (fp16 2.0 = 0x4000 little-endian, then the
+    values of vulkanised/test_gguf2vk.py:77-83) splits into scale 0x4000 and
+    those int8 values; the split planes gather what the blocks gather."""
+    blk = np.zeros(2 * 34, np.uint8)
+    blk[0:2] = [0x00, 0x40]
+    blk[2:7] = [0, 1, 0xFF, 127, 0x81]
+    blk[34:36] = [0x01, 0x80]              # -2^-24: a subnormal scale, bits kept as they are
+    blk[36:68] = np.arange(32, dtype=np.uint8) * 7
+    w8 = np.empty(64, np.int8)
+    ws = np.empty(2, np.uint16)
+    o.orc_q8_0_split_blocks(H.ptr(blk), 2, H.ptr(w8), H.ptr(ws))
+    assert list(ws) == [0x4000, 0x8001]
+    assert list(w8[:5]) == [0, 1, -1, 127, -127] and not w8[5:32].any()
+    assert list(w8[32:].view(np.uint8)) == [(7 * i) & 0xFF for i in range(32)]
+    ids = np.array([0, 1], np.int64)
+    a = np.empty((2, 32), np.float32)
+    b = np.empty((2, 32), np.float32)
+    o.orc_embedding_q8_split(H.ptr(ids), H.ptr(w8), H.ptr(ws), 2, 32, H.ptr(a), H.F32)
+    o.orc_embedding_q8_blocks(H.ptr(ids), H.ptr(blk), 2, 32, H.ptr(b), H.F32)
+    assert list(a[0, :5]) == [0, 2, -2, 254, -254]
+    assert np.array_equal(a, b)
+
+
+def test_q8_0_split_blocks_round_trip(o):
+    """split(join(w8, ws)) == (w8, ws) for random planes, and join(split(bytes))
+    == bytes for random bytes."""
+    r = H.rng(34)
+    w8, ws = H.gen_q8_0(r, 13, 96)
+    blk = H.q8_split_to_blocks(w8, ws)
+    nb = ws.size
+    g8 = np.empty(nb * 32, np.int8)
+    gs = np.empty(nb, np.uint16)
+    o.orc_q8_0_split_blocks(H.ptr(blk), nb, H.ptr(g8), H.ptr(gs))
+    assert np.array_equal(g8, w8) and np.array_equal(gs, ws)
+    raw = r.integers(0, 256, 34 * 9, dtype=np.uint8)
+    g8 = np.empty(9 * 32, np.int8)
+    gs = np.empty(9, np.uint16)
+    o.orc_q8_0_split_blocks(H.ptr(raw), 9, H.ptr(g8), H.ptr(gs))
+    assert np.array_equal(H.q8_split_to_blocks(g8, gs), raw)
+
+
 # ---------------------------------------------------------------------------
 # K-quants
 # ---------------------------------------------------------------------------
