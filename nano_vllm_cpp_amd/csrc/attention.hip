@@ -163,6 +163,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
   const int64_t tq = t0 + 32 * wave + (lane & 31);
   const bool q_ok = tq < tokens;
   const int L = q_ok ? qlen[tq] : 0;
+  // the smallest key count among the wave's queries (chunks below it need no mask)
+  // (a wave with no query in range takes the masked path; its outputs are not stored)
+  const float lmin = -wave_max(q_ok ? -(float)L : -INFINITY);
+  const int Lmin = lmin < 2.0e9f ? (int)lmin : 0;
   v8 qf[kFaHd / 16];
 #pragma unroll
   for (int s = 0; s < kFaHd / 16; ++s) {
@@ -190,17 +194,25 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
   auto store_chunk = [&](uint8_t* st) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) st16(st + (ld_r + 16 * i) * kFaKRow + ld_c * 16, kreg[i]);
-    // V^T: dim 8 ld_c + e, keys 4 ld_r .. 4 ld_r + 3 -> 8 bytes
-    uint8_t* vt = st + kFaKBytes;
+    // V^T: dim 8 ld_c + e, keys 4 ld_r .. 4 ld_r + 3 -> 8 bytes, at key group
+    // ld_r ^ ((row >> 4) & 7) of row 8 ld_c + e (the swizzle below)
+    uint8_t* vt = st + kFaKBytes + 8 * (ld_r ^ ((ld_c >> 1) & 7));
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const int sh = (e & 1) * 16;
       const uint32_t lo = ((vreg[0][e >> 1] >> sh) & 0xffffu) | (((vreg[1][e >> 1] >> sh) & 0xffffu) << 16);
       const uint32_t hi = ((vreg[2][e >> 1] >> sh) & 0xffffu) | (((vreg[3][e >> 1] >> sh) & 0xffffu) << 16);
       typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-      *reinterpret_cast<u32x2*>(vt + (8 * ld_c + e) * kFaVRow + 8 * ld_r) = u32x2{lo, hi};
+      *reinterpret_cast<u32x2*>(vt + (8 * ld_c + e) * kFaVRow) = u32x2{lo, hi};
     }
   };
+
+  // V^T in LDS: row r (a dimension) holds 16 groups of 4 keys, group g stored at
+  // position g ^ ((r >> 4) & 7).  The 16 lanes of a write phase (rows 8 apart)
+  // and of a read phase (16 consecutive rows) then each cover all 32 banks.  For
+  // a read of row 32 d + (lane & 31), group g0 + half (g0 even), the position is
+  // (g0 ^ 2d) + (half ^ ((lane >> 4) & 1)): a constant plus this lane offset.
+  const int vt_lane = 8 * (half ^ ((lane >> 4) & 1));
 
   f32x16 o[kFaHd / 32];
 #pragma unroll
@@ -227,38 +239,54 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
       }
     }
     // online softmax for this lane's query; element j of tile kt is key
-    // c*64 + 32 kt + 8 (j/4) + 4 half + j%4
+    // c*64 + 32 kt + 8 (j/4) + 4 half + j%4.  The running max m is kept in
+    // exp2 units (score * scale_log2); since scale_log2 > 0 and rounding is
+    // monotonic, the max of the raw scores times scale_log2 is exactly the max
+    // of the scaled ones, and each p takes one fma into exp2.
     float mx = -INFINITY;
+    if ((c + 1) * kFaBk <= Lmin) {  // every key of the chunk is visible to every query of the wave
 #pragma unroll
-    for (int kt = 0; kt < 2; ++kt)
+      for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        const int key = c * kFaBk + 32 * kt + 8 * (j >> 2) + 4 * half + (j & 3);
-        const float x = key < L ? st[kt][j] * scale_log2 : -INFINITY;
-        st[kt][j] = x;
-        mx = fmaxf(mx, x);
-      }
+        for (int j = 0; j < 16; ++j) mx = fmaxf(mx, st[kt][j]);
+    } else {
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+          const int key = c * kFaBk + 32 * kt + 8 * (j >> 2) + 4 * half + (j & 3);
+          const float x = key < L ? st[kt][j] : -INFINITY;
+          st[kt][j] = x;
+          mx = fmaxf(mx, x);
+        }
+    }
     mx = fmaxf(mx, __shfl_xor(mx, 32));
-    const float m_new = fmaxf(m, mx);
+    const float m_new = fmaxf(m, mx * scale_log2);
     const float m_use = m_new == -INFINITY ? 0.0f : m_new;
-    const float alpha = __builtin_amdgcn_exp2f(m - m_use);
     float ls = 0.0f;
     v8 pb[2][2];
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
       for (int j = 0; j < 16; ++j) {
-        const float p = __builtin_amdgcn_exp2f(st[kt][j] - m_use);
+        const float p = __builtin_amdgcn_exp2f(fmaf(st[kt][j], scale_log2, -m_use));
         ls += p;
         pb[kt][j >> 3][j & 7] = (T)p;
       }
     ls += __shfl_xor(ls, 32);
-    l = l * alpha + ls;
-    m = m_new;
+    // the rescale factor is exactly 1 where the max did not move: skip it when
+    // that holds for every query of the wave
+    if (!__all(m_new == m)) {
+      const float alpha = __builtin_amdgcn_exp2f(m - m_use);
+      l *= alpha;
 #pragma unroll
-    for (int d = 0; d < kFaHd / 32; ++d) o[d] *= alpha;
-    // O^T += V^T . P^T, key step u of tile kt: keys 32 kt + 16 u + 4 half + {0..3, 8..11}
-    const uint8_t* vt = buf + kFaKBytes;
+      for (int d = 0; d < kFaHd / 32; ++d) o[d] *= alpha;
+    }
+    l += ls;
+    m = m_new;
+    // O^T += V^T . P^T, key step u of tile kt: keys 32 kt + 16 u + 4 half + {0..3, 8..11},
+    // key groups g0 + half and g0 + 2 + half (g0 = 8 kt + 4 u) of row 32 d + (lane & 31)
+    const uint8_t* vt = buf + kFaKBytes + vt_lane;
 #pragma unroll
     for (int d = 0; d < kFaHd / 32; ++d)
 #pragma unroll
@@ -266,9 +294,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
           typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-          const uint8_t* r = vt + (32 * d + (lane & 31)) * kFaVRow + (32 * kt + 16 * u + 4 * half) * 2;
-          const u32x2 lo = *reinterpret_cast<const u32x2*>(r);
-          const u32x2 hi = *reinterpret_cast<const u32x2*>(r + 16);
+          const int g0 = 8 * kt + 4 * u;
+          const uint8_t* r = vt + (32 * d + (lane & 31)) * kFaVRow;
+          const u32x2 lo = *reinterpret_cast<const u32x2*>(r + 8 * (g0 ^ (2 * d)));
+          const u32x2 hi = *reinterpret_cast<const u32x2*>(r + 8 * ((g0 + 2) ^ (2 * d)));
           const v8 a = __builtin_bit_cast(v8, u32x4{lo[0], lo[1], hi[0], hi[1]});
           o[d] = M::mma(a, pb[kt][u], o[d]);
         }
@@ -578,8 +607,9 @@ int attention_dispatch(const void* q, void* out, const void* kc, const void* vc,
   // matrix-core paths: 16-bit, head_dim 128, 64-key chunks inside one block, 16-byte rows, <= 16 heads per kv head
   bool mfma = false;
   if constexpr (sizeof(T) == 2) {
+    // (scale > 0: the kernels take the running max on unscaled scores)
     mfma = hd == kFaHd && bs % kFaBk == 0 && q_heads / kv_heads <= 16 && aligned16(q) && aligned16(out) &&
-           aligned16(kc) && aligned16(vc) && q_stride % N == 0;
+           aligned16(kc) && aligned16(vc) && q_stride % N == 0 && scale > 0.0f;
   }
   if constexpr (sizeof(T) == 2) {
     if (mfma) {

@@ -206,3 +206,36 @@ def test_paged_attention_masks_keys_past_the_range(gpu, dt):
     spike_v = H.from_storage(b.v_cache[row, 0], dt)
     assert np.abs(g[220:, 0] - spike_v).max() < 0.05 * np.abs(spike_v).max()  # pulled to the spike
     assert np.abs(g[:199, 0] - spike_v).max() > 0.5                          # never saw it
+
+
+@pytest.mark.parametrize("scale", [-0.09, 0.0], ids=["negative", "zero"])
+def test_paged_attention_nonpositive_scale(gpu, scale):
+    """A scale <= 0 at a matrix-core-eligible shape (those kernels keep the
+    running max on unscaled scores, valid for scale > 0) is still right: it takes
+    the wave kernel."""
+    r = H.rng(61)
+    b = H.make_paged(r, [300, 130], [300, 130], 8, 2, 128, 64, H.F16)
+    _, exact, vmax = H.oracle_attention(b, 8, 2, 128, 64, scale, H.F16)
+    case(f"paged_attention scale={scale}")
+    got = H.to_host(run_attention(gpu, b, 8, 2, 128, 64, scale, H.F16))
+    assert_attn(got, exact, vmax, H.F16, f"scale {scale}")
+
+
+@pytest.mark.parametrize("dt", [H.F16, H.BF16], ids=["f16", "bf16"])
+def test_paged_attention_late_rising_max(gpu, dt):
+    """Keys in a late block score far higher than the earlier ones, so each
+    query's running max rises after many chunks (the rescale of the partial sums
+    runs late) while other waves' maxima stay put."""
+    r = H.rng(62 + dt)
+    bs = 64
+    b = H.make_paged(r, [900], [900], 4, 1, 128, bs, dt)
+    kc = H.from_storage(b.k_cache, dt).astype(np.float32)
+    for lb in (9, 12):  # keys 576..639 and 768..831
+        blk = int(b.block_tables[0, lb])
+        kc[blk * bs:(blk + 1) * bs] *= 4.0
+    b.k_cache = H.to_storage(kc, dt)
+    scale = 128 ** -0.5
+    _, exact, vmax = H.oracle_attention(b, 4, 1, 128, bs, scale, dt)
+    case(f"paged_attention late rising max dt={dt}")
+    got = H.to_host(run_attention(gpu, b, 4, 1, 128, bs, scale, dt))
+    assert_attn(got, exact, vmax, dt, "late max")
