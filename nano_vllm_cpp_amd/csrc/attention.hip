@@ -94,6 +94,7 @@ constexpr int kFaStage = kFaKBytes + kFaHd * kFaVRow;
 constexpr int kFaLds = 2 * kFaStage;
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 template <typename T>
 struct Mfma16;
@@ -323,6 +324,172 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
 }
 
 // ---------------------------------------------------------------------------
+// fp32 caches (the reference's own KV dtype) on the fp32 matrix cores,
+// v_mfma_f32_32x32x2_f32 (exact fp32 products, fp32 sums).  The tiles are
+// fa_prefill_kernel's (128 queries of one head, 4 waves of 32 queries, the same
+// uniform-tile rule), over 32-key chunks:
+//   S^T = K . Q^T   64 MFMAs over the 128 dims.  MFMA s contracts dim
+//                   64 (lane / 32) + s, so a lane's A and B operands of 4
+//                   consecutive MFMAs are 16 consecutive bytes of its K row / q.
+//   O^T += V^T . P^T  MFMA s contracts key 8 (s / 4) + 4 (lane / 32) + s % 4,
+//                   the key S^T's register s of this lane holds, so P^T is
+//                   those registers as they are.  Row r of O^T tile d is dim
+//                   4 r + d: the 4 tiles' A operands for one key are 16
+//                   consecutive bytes of V's own row, read without a transpose.
+constexpr int kF32Bk = 32;                       // keys per chunk
+constexpr int kF32KRow = kFaHd * 4 + 16;         // K row in LDS: 528 B, the 8 lanes of a 16 B read phase on distinct banks
+constexpr int kF32VRow = kFaHd * 4;              // V row in LDS: 512 B (read along the row)
+constexpr int kF32KBytes = kF32Bk * kF32KRow;
+constexpr int kF32Stage = kF32KBytes + kF32Bk * kF32VRow;
+constexpr int kF32Lds = 2 * kF32Stage;           // 66560 B: two workgroups per CU
+
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void fa_prefill_f32_kernel(
+    const float* __restrict__ q, float* __restrict__ out, const float* __restrict__ kc, const float* __restrict__ vc,
+    const int32_t* __restrict__ qseq, const int32_t* __restrict__ qlen, const int32_t* __restrict__ tables,
+    int64_t tokens, int q_heads, int kv_heads, int bs, int max_blocks, float scale_log2, int64_t q_stride,
+    int64_t tiles) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int half = lane >> 5;
+  const int64_t bid = blockIdx.x;
+  const int64_t tile = tiles - 1 - bid / q_heads;  // the longest tiles (latest positions) first
+  const int h = (int)(bid % q_heads);
+  const int64_t t0 = tile * kFaBq;
+  if (!fa_tile_uniform(qseq, tokens, tile)) return;  // the whole workgroup: left to attn_wave_kernel
+  const int64_t seq = qseq[t0];
+  const int kvh = h / (q_heads / kv_heads);
+  const int64_t kv_stride = (int64_t)kv_heads * kFaHd;
+  const int32_t* tab = tables + seq * max_blocks;
+
+  float lmax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < kFaBq / 64; ++i) {
+    const int64_t t = t0 + lane + 64 * i;
+    if (t < tokens) lmax = fmaxf(lmax, (float)qlen[t]);
+  }
+  const int Lmax = (int)wave_max(lmax);
+  const int nchunks = (Lmax + kF32Bk - 1) / kF32Bk;
+
+  const int64_t tq = t0 + 32 * wave + (lane & 31);
+  const bool q_ok = tq < tokens;
+  const int L = q_ok ? qlen[tq] : 0;
+  const float lmin = -wave_max(q_ok ? -(float)L : -INFINITY);
+  const int Lmin = lmin < 2.0e9f ? (int)lmin : 0;
+  // B operand of S^T: this lane's query, dims 64 half + 4 i + e
+  f32x4 qf[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i)
+    qf[i] = q_ok ? __builtin_bit_cast(f32x4, ld16(q + tq * q_stride + (int64_t)h * kFaHd + 64 * half + 4 * i))
+                 : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+  // chunk loads: rows ld_r + 8 i (i < 4) of K and V, 16 B column ld_c of each
+  const int tid = threadIdx.x;
+  const int ld_c = tid & 31, ld_r = tid >> 5;
+  u32x4 kreg[4], vreg[4];
+  auto load_chunk = [&](int c) {
+    const int k0 = c * kF32Bk;
+    const int64_t row0 = (int64_t)tab[k0 / bs] * bs + k0 % bs;
+    const float* kb = kc + row0 * kv_stride + (int64_t)kvh * kFaHd + ld_c * 4;
+    const float* vb = vc + row0 * kv_stride + (int64_t)kvh * kFaHd + ld_c * 4;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int key = ld_r + 8 * i;
+      kreg[i] = ld16(kb + (int64_t)key * kv_stride);
+      // keys past the tile's range may hold anything: zero their V (their p is 0)
+      vreg[i] = k0 + key < Lmax ? ld16(vb + (int64_t)key * kv_stride) : u32x4{0, 0, 0, 0};
+    }
+  };
+  auto store_chunk = [&](uint8_t* st) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      st16(st + (ld_r + 8 * i) * kF32KRow + ld_c * 16, kreg[i]);
+      st16(st + kF32KBytes + (ld_r + 8 * i) * kF32VRow + ld_c * 16, vreg[i]);
+    }
+  };
+
+  f32x16 o[4];
+#pragma unroll
+  for (int d = 0; d < 4; ++d) o[d] = f32x16{};
+  float m = -INFINITY, l = 0.0f;
+
+  if (nchunks > 0) {
+    load_chunk(0);
+    store_chunk(lds);
+  }
+  __syncthreads();
+  for (int c = 0; c < nchunks; ++c) {
+    const uint8_t* buf = lds + (c & 1) * kF32Stage;
+    if (c + 1 < nchunks) load_chunk(c + 1);  // in flight during this chunk
+    // S^T: lane row (key) lane & 31 of the chunk, dims 64 half + ...
+    f32x16 st = f32x16{};
+    const uint8_t* krow = buf + (lane & 31) * kF32KRow + 256 * half;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const f32x4 a = __builtin_bit_cast(f32x4, ld16(krow + 16 * i));
+#pragma unroll
+      for (int e = 0; e < 4; ++e) st = __builtin_amdgcn_mfma_f32_32x32x2f32(a[e], qf[i][e], st, 0, 0, 0);
+    }
+    // online softmax for this lane's query over its keys c*32 + 8 (j/4) + 4 half + j%4
+    // (the running max in exp2 units, as in fa_prefill_kernel)
+    float mx = -INFINITY;
+    if ((c + 1) * kF32Bk <= Lmin) {
+#pragma unroll
+      for (int j = 0; j < 16; ++j) mx = fmaxf(mx, st[j]);
+    } else {
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const int key = c * kF32Bk + 8 * (j >> 2) + 4 * half + (j & 3);
+        const float x = key < L ? st[j] : -INFINITY;
+        st[j] = x;
+        mx = fmaxf(mx, x);
+      }
+    }
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    const float m_new = fmaxf(m, mx * scale_log2);
+    const float m_use = m_new == -INFINITY ? 0.0f : m_new;
+    float ls = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      st[j] = __builtin_amdgcn_exp2f(fmaf(st[j], scale_log2, -m_use));
+      ls += st[j];
+    }
+    ls += __shfl_xor(ls, 32);
+    if (!__all(m_new == m)) {
+      const float alpha = __builtin_amdgcn_exp2f(m - m_use);
+      l *= alpha;
+#pragma unroll
+      for (int d = 0; d < 4; ++d) o[d] *= alpha;
+    }
+    l += ls;
+    m = m_new;
+    // O^T += V^T . P^T: MFMA s takes key 8 (s/4) + 4 half + s%4 (P^T = st[s]); lane
+    // row r = lane & 31 of tile d is dim 4 r + d
+    const uint8_t* vrow = buf + kF32KBytes + 16 * (lane & 31);
+#pragma unroll
+    for (int s = 0; s < 16; ++s) {
+      const int key = 8 * (s >> 2) + 4 * half + (s & 3);
+      const f32x4 a = __builtin_bit_cast(f32x4, ld16(vrow + key * kF32VRow));
+#pragma unroll
+      for (int d = 0; d < 4; ++d) o[d] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[d], st[s], o[d], 0, 0, 0);
+    }
+    if (c + 1 < nchunks) store_chunk(lds + ((c + 1) & 1) * kF32Stage);
+    __syncthreads();
+  }
+
+  // O^T: lane column = query; register j of tile d is dim 4 (8 (j/4) + 4 half + j%4) + d
+  if (q_ok) {
+    const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+    float* orow = out + (tq * q_heads + h) * kFaHd;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const int r = 8 * (j >> 2) + 4 * half + (j & 3);
+      st16(orow + 4 * r, __builtin_bit_cast(u32x4, f32x4{o[0][j] * inv, o[1][j] * inv, o[2][j] * inv, o[3][j] * inv}));
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Decode-shaped attention on the matrix cores (16-bit cache, head_dim 128,
 // block sizes a multiple of 64, at most 16 query heads per kv head): one wave
 // per (token, kv head) streams that head's keys in 64-key chunks.  The query
@@ -337,7 +504,6 @@ constexpr int kFdVRow = 64 * 2 + 8;              // V^T row: 64 keys, padded
 constexpr int kFdWaveLds = kFaHd * kFdVRow;      // per wave
 constexpr int kFdLds = 4 * kFdWaveLds;
 
-typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 template <typename T>
 struct Mfma16x16;
@@ -643,15 +809,37 @@ int attention_dispatch(const void* q, void* out, const void* kc, const void* vc,
   }
   const bool vec = hd % N == 0 && aligned16(kc) && ((int64_t)kv_heads * hd) % N == 0;
   const int dpl = (hd + 63) / 64;
+  bool skip = false;  // the wave kernel leaves the matrix-core tiles' tokens alone
+  if constexpr (sizeof(T) == 4) {
+    // fp32 tiles: head_dim 128, 32-key chunks inside one block, 16-byte rows
+    const bool tiles = hd == kFaHd && bs % kF32Bk == 0 && aligned16(q) && aligned16(out) && aligned16(kc) &&
+                       aligned16(vc) && q_stride % N == 0 && scale > 0.0f && max_query_len != 1;
+    if (tiles) {
+      static std::once_flag f32_once;
+      std::call_once(f32_once, [] {
+        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&fa_prefill_f32_kernel),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, kF32Lds);
+      });
+      const int64_t ntiles = (tokens + kFaBq - 1) / kFaBq;
+      if (ntiles * q_heads > INT32_MAX) return fail(NVF_ERR_INVALID, "paged_attention: too many tiles");
+      fa_prefill_f32_kernel<<<dim3((unsigned)(ntiles * q_heads)), 256, kF32Lds, st>>>(
+          static_cast<const float*>(q), static_cast<float*>(out), static_cast<const float*>(kc),
+          static_cast<const float*>(vc), qseq, qlen, tables, tokens, q_heads, kv_heads, bs, max_blocks,
+          scale * 1.4426950408889634f, q_stride, ntiles);
+      const int rc = launch_status("paged_attention(f32 tiles)");
+      if (rc != NVF_OK) return rc;
+      skip = true;
+    }
+  }
   switch (dpl) {
     case 1: launch_attn_wave<T, 1>(q, out, kc, vc, qseq, qlen, tables, tokens, q_heads, kv_heads, hd, bs, max_blocks,
-                                   scale, q_stride, vec, false, st); break;
+                                   scale, q_stride, vec, skip, st); break;
     case 2: launch_attn_wave<T, 2>(q, out, kc, vc, qseq, qlen, tables, tokens, q_heads, kv_heads, hd, bs, max_blocks,
-                                   scale, q_stride, vec, false, st); break;
+                                   scale, q_stride, vec, skip, st); break;
     case 3: launch_attn_wave<T, 3>(q, out, kc, vc, qseq, qlen, tables, tokens, q_heads, kv_heads, hd, bs, max_blocks,
-                                   scale, q_stride, vec, false, st); break;
+                                   scale, q_stride, vec, skip, st); break;
     default: launch_attn_wave<T, 4>(q, out, kc, vc, qseq, qlen, tables, tokens, q_heads, kv_heads, hd, bs,
-                                    max_blocks, scale, q_stride, vec, false, st); break;
+                                    max_blocks, scale, q_stride, vec, skip, st); break;
   }
   return launch_status("paged_attention");
 }

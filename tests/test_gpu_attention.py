@@ -208,20 +208,21 @@ def test_paged_attention_masks_keys_past_the_range(gpu, dt):
     assert np.abs(g[:199, 0] - spike_v).max() > 0.5                          # never saw it
 
 
+@pytest.mark.parametrize("dt", [H.F32, H.F16], ids=["f32", "f16"])
 @pytest.mark.parametrize("scale", [-0.09, 0.0], ids=["negative", "zero"])
-def test_paged_attention_nonpositive_scale(gpu, scale):
+def test_paged_attention_nonpositive_scale(gpu, scale, dt):
     """A scale <= 0 at a matrix-core-eligible shape (those kernels keep the
     running max on unscaled scores, valid for scale > 0) is still right: it takes
     the wave kernel."""
     r = H.rng(61)
-    b = H.make_paged(r, [300, 130], [300, 130], 8, 2, 128, 64, H.F16)
-    _, exact, vmax = H.oracle_attention(b, 8, 2, 128, 64, scale, H.F16)
-    case(f"paged_attention scale={scale}")
-    got = H.to_host(run_attention(gpu, b, 8, 2, 128, 64, scale, H.F16))
-    assert_attn(got, exact, vmax, H.F16, f"scale {scale}")
+    b = H.make_paged(r, [300, 130], [300, 130], 8, 2, 128, 64, dt)
+    _, exact, vmax = H.oracle_attention(b, 8, 2, 128, 64, scale, dt)
+    case(f"paged_attention scale={scale} dt={dt}")
+    got = H.to_host(run_attention(gpu, b, 8, 2, 128, 64, scale, dt))
+    assert_attn(got, exact, vmax, dt, f"scale {scale}")
 
 
-@pytest.mark.parametrize("dt", [H.F16, H.BF16], ids=["f16", "bf16"])
+@pytest.mark.parametrize("dt", DTYPES, ids=DT_IDS)
 def test_paged_attention_late_rising_max(gpu, dt):
     """Keys in a late block score far higher than the earlier ones, so each
     query's running max rises after many chunks (the rescale of the partial sums
