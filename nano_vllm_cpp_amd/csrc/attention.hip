@@ -662,6 +662,143 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
 }
 
 // ---------------------------------------------------------------------------
+// Decode-shaped attention for fp32 caches on the fp32 matrix cores
+// (v_mfma_f32_16x16x4_f32), head_dim 128, at most 16 query heads per kv head:
+// one wave per (token, kv head), the group's query heads the 16 columns, 16-key
+// chunks straight from the cache into registers (the next chunk's loads in
+// flight during the current chunk's math; no LDS).
+//   S^T = K . Q^T   32 MFMAs; MFMA 4 i + e contracts dim 32 (lane / 16) + 4 i + e,
+//                   so a lane's operands are 16-byte runs of its key's K row / q.
+//   O^T += V^T . P^T  MFMA u contracts key 4 (lane / 16) + u, the key S^T's
+//                   register u of this lane holds (P^T = those registers); row r
+//                   of O^T tile dt is dim 8 r + dt, so one key's A operands for
+//                   the 8 tiles are 32 consecutive bytes of its V row.
+constexpr int kFd32Bk = 16;  // keys per chunk
+
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void fa_decode_f32_kernel(
+    const float* __restrict__ q, float* __restrict__ out, const float* __restrict__ kc, const float* __restrict__ vc,
+    const int32_t* __restrict__ qseq, const int32_t* __restrict__ qlen, const int32_t* __restrict__ tables,
+    int64_t tokens, int q_heads, int kv_heads, int bs, int max_blocks, float scale_log2, int64_t q_stride,
+    bool skip_uniform_tiles) {
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int64_t t = blockIdx.x;
+  const int kvh = blockIdx.y * 4 + wave;
+  if (kvh >= kv_heads) return;  // whole waves; no workgroup barrier below
+  if (skip_uniform_tiles && fa_tile_uniform(qseq, tokens, t / kFaBq)) return;  // fa_prefill_f32_kernel's
+  const int G = q_heads / kv_heads;
+  const int col = lane & 15, g = lane >> 4;
+  const bool head_ok = col < G;
+  const int h = kvh * G + col;
+  const int L = qlen[t];
+  const int64_t seq = qseq[t];
+  const int64_t kv_stride = (int64_t)kv_heads * kFaHd;
+  const int32_t* tab = tables + seq * max_blocks;
+
+  f32x4 qf[8];  // B operand: head col, dims 32 g + 4 i + e
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+    qf[i] = head_ok ? __builtin_bit_cast(f32x4, ld16(q + t * q_stride + (int64_t)h * kFaHd + 32 * g + 4 * i))
+                    : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  f32x4 o[8];
+#pragma unroll
+  for (int d = 0; d < 8; ++d) o[d] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  float m = -INFINITY, l = 0.0f;
+  const int nchunks = L > 0 ? (L + kFd32Bk - 1) / kFd32Bk : 0;
+
+  // chunk c: K row of key 16 c + col, dims 32 g + 4 i (A operands of S^T); V row
+  // of key 16 c + 4 g + u, dims 8 col .. 8 col + 7 (A operands of O^T, zero past L)
+  auto load = [&](int c, u32x4* kr, u32x4* vr) {
+    const int k0 = c * kFd32Bk;
+    const int64_t row0 = (int64_t)tab[k0 / bs] * bs + k0 % bs;
+    const float* kb = kc + (row0 + col) * kv_stride + (int64_t)kvh * kFaHd + 32 * g;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) kr[i] = ld16(kb + 4 * i);
+    const float* vb = vc + row0 * kv_stride + (int64_t)kvh * kFaHd + 8 * col;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int key = 4 * g + u;
+      const bool ok = k0 + key < L;
+      vr[2 * u] = ok ? ld16(vb + (int64_t)key * kv_stride) : u32x4{0, 0, 0, 0};
+      vr[2 * u + 1] = ok ? ld16(vb + (int64_t)key * kv_stride + 4) : u32x4{0, 0, 0, 0};
+    }
+  };
+  auto compute = [&](int c, const u32x4* kr, const u32x4* vr) {
+    f32x4 st = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const f32x4 a = __builtin_bit_cast(f32x4, kr[i]);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) st = __builtin_amdgcn_mfma_f32_16x16x4f32(a[e], qf[i][e], st, 0, 0, 0);
+    }
+    // online softmax per head (lane column); register v is key 16 c + 4 g + v
+    float mx = -INFINITY;
+    if ((c + 1) * kFd32Bk <= L) {
+#pragma unroll
+      for (int v = 0; v < 4; ++v) mx = fmaxf(mx, st[v]);
+    } else {
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const float x = c * kFd32Bk + 4 * g + v < L ? st[v] : -INFINITY;
+        st[v] = x;
+        mx = fmaxf(mx, x);
+      }
+    }
+    mx = fmaxf(mx, __shfl_xor(mx, 16));
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    const float m_new = fmaxf(m, mx * scale_log2);
+    const float m_use = m_new == -INFINITY ? 0.0f : m_new;
+    float ls = 0.0f;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      st[v] = __builtin_amdgcn_exp2f(fmaf(st[v], scale_log2, -m_use));
+      ls += st[v];
+    }
+    ls += __shfl_xor(ls, 16);
+    ls += __shfl_xor(ls, 32);
+    if (!__all(m_new == m)) {
+      const float alpha = __builtin_amdgcn_exp2f(m - m_use);
+      l *= alpha;
+#pragma unroll
+      for (int d = 0; d < 8; ++d) o[d] *= alpha;
+    }
+    l += ls;
+    m = m_new;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const f32x4 a0 = __builtin_bit_cast(f32x4, vr[2 * u]), a1 = __builtin_bit_cast(f32x4, vr[2 * u + 1]);
+#pragma unroll
+      for (int d = 0; d < 4; ++d) {
+        o[d] = __builtin_amdgcn_mfma_f32_16x16x4f32(a0[d], st[u], o[d], 0, 0, 0);
+        o[4 + d] = __builtin_amdgcn_mfma_f32_16x16x4f32(a1[d], st[u], o[4 + d], 0, 0, 0);
+      }
+    }
+  };
+
+  u32x4 ka[8], va[8], kb_[8], vb_[8];
+  if (nchunks > 0) load(0, ka, va);
+  for (int c = 0; c < nchunks; c += 2) {  // two chunks per trip: the register sets trade roles
+    if (c + 1 < nchunks) load(c + 1, kb_, vb_);
+    compute(c, ka, va);
+    if (c + 1 < nchunks) {
+      if (c + 2 < nchunks) load(c + 2, ka, va);
+      compute(c + 1, kb_, vb_);
+    }
+  }
+  // O^T: register v of tile d is dim 8 (4 g + v) + d of head col
+  if (head_ok) {
+    const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+    float* orow = out + (t * q_heads + h) * kFaHd;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      float* p = orow + 8 * (4 * g + v);
+      st16(p, __builtin_bit_cast(u32x4, f32x4{o[0][v] * inv, o[1][v] * inv, o[2][v] * inv, o[3][v] * inv}));
+      st16(p + 4, __builtin_bit_cast(u32x4, f32x4{o[4][v] * inv, o[5][v] * inv, o[6][v] * inv, o[7][v] * inv}));
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // One wave per (token, head).  DPL = head dimensions per lane (head_dim <= 64 DPL).
 template <typename T, int DPL, bool VEC>
 __global__ __launch_bounds__(kAttnWaves * 64) void attn_wave_kernel(
@@ -811,9 +948,12 @@ int attention_dispatch(const void* q, void* out, const void* kc, const void* vc,
   const int dpl = (hd + 63) / 64;
   bool skip = false;  // the wave kernel leaves the matrix-core tiles' tokens alone
   if constexpr (sizeof(T) == 4) {
-    // fp32 tiles: head_dim 128, 32-key chunks inside one block, 16-byte rows
-    const bool tiles = hd == kFaHd && bs % kF32Bk == 0 && aligned16(q) && aligned16(out) && aligned16(kc) &&
-                       aligned16(vc) && q_stride % N == 0 && scale > 0.0f && max_query_len != 1;
+    // fp32 matrix cores: head_dim 128, 16-byte rows, scale > 0; tiles need 32-key
+    // chunks inside one block, the decode kernel 16-key chunks and <= 16 heads per kv head
+    const bool base = hd == kFaHd && aligned16(q) && aligned16(out) && aligned16(kc) && aligned16(vc) &&
+                      q_stride % N == 0 && scale > 0.0f;
+    const bool tiles = base && bs % kF32Bk == 0 && max_query_len != 1;
+    const bool dec = base && bs % kFd32Bk == 0 && q_heads / kv_heads <= 16;
     if (tiles) {
       static std::once_flag f32_once;
       std::call_once(f32_once, [] {
@@ -829,6 +969,14 @@ int attention_dispatch(const void* q, void* out, const void* kc, const void* vc,
       const int rc = launch_status("paged_attention(f32 tiles)");
       if (rc != NVF_OK) return rc;
       skip = true;
+    }
+    if (dec) {
+      if (tokens > INT32_MAX) return fail(NVF_ERR_INVALID, "paged_attention: too many tokens");
+      fa_decode_f32_kernel<<<dim3((unsigned)tokens, (unsigned)((kv_heads + 3) / 4)), 256, 0, st>>>(
+          static_cast<const float*>(q), static_cast<float*>(out), static_cast<const float*>(kc),
+          static_cast<const float*>(vc), qseq, qlen, tables, tokens, q_heads, kv_heads, bs, max_blocks,
+          scale * 1.4426950408889634f, q_stride, tiles);
+      return launch_status("paged_attention(f32 decode)");
     }
   }
   switch (dpl) {

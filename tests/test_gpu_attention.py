@@ -98,7 +98,7 @@ CASES = [
 ]
 
 
-@pytest.mark.parametrize("dt", [H.F16, H.BF16], ids=["f16", "bf16"])
+@pytest.mark.parametrize("dt", DTYPES, ids=DT_IDS)
 @pytest.mark.parametrize("heads", [(28, 4), (32, 8), (16, 1)], ids=["qwen25", "qwen3", "g16"])
 def test_paged_attention_decode_batch(gpu, dt, heads):
     """A decode batch (one query per sequence) through the decode-only route
