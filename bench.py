@@ -41,6 +41,7 @@ sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0
 INT8_PEAK_OPS = 5.0e15  # MI355X dense int8 MFMA
+FP32_PEAK_FLOPS = 157.3e12  # MI355X dense fp32 matrix rate
 METRIC = "fused-op HBM GB/s (% of peak) + layer-op tokens/s at Qwen2.5-7B shapes"
 POOL_BYTES = 1 << 30
 GEMV_M = 8  # decode rows for the GEMV line
@@ -56,7 +57,8 @@ def parse() -> argparse.Namespace:
     p.add_argument("--emb", default="", choices=["", "q8_0", "q8_0_blocks", "q4_k", "q5_k", "q6_k", "f16"],
                    help="embedding table format (default: the config's)")
     p.add_argument("--only", default="",
-                   help="comma list of ops (default emb,rms,rope,silu,copy,gemm,gemv,split,attn,attn_decode); "
+                   help="comma list of ops (default emb,rms,rope,silu,copy,gemm,gemv,split,attn,attn_decode,attn_f32,"
+                        "attn_decode_f32); "
                         "also emb_rms, rms_q8, silu_q8 (fusions)")
     return p.parse_args()
 
@@ -109,7 +111,7 @@ def main() -> int:
     emb_fmt = args.emb or cfg.emb
     nbytes = op_bytes(cfg, e, emb_fmt)
     only = set(filter(None, args.only.split(","))) or {"emb", "rms", "rope", "silu", "copy", "gemm", "gemv", "split",
-                                                       "attn", "attn_decode"}
+                                                       "attn", "attn_decode", "attn_f32", "attn_decode_f32"}
 
     def nsets(b: int) -> int:
         return max(2, -(-POOL_BYTES // b))
@@ -176,7 +178,7 @@ def main() -> int:
                                torch.empty(nb_split, dtype=torch.int16, device=dev)))
     attn_in = attn_dec = None
     bs_kv = 256  # the reference's KV block size (a multiple of 256, config.hpp:254)
-    if "attn" in only:  # causal prefill over the config's sequences, KV already in the paged cache
+    if {"attn", "attn_f32"} & only:  # causal prefill over the config's sequences, KV already in the paged cache
         apos = cfg.positions()
         lens = [int(n) for n in np.diff(cfg.cu_seqlens())]
         nblk = [-(-n // bs_kv) for n in lens]
@@ -192,7 +194,7 @@ def main() -> int:
                    torch.from_numpy(np.repeat(np.arange(len(lens), dtype=np.int32), lens)).to(dev),
                    torch.from_numpy((apos + 1).astype(np.int32)).to(dev), tables.to(dev))
         attn_flops = 4.0 * cfg.q_heads * cfg.head_dim * float((apos + 1).sum())
-    if "attn_decode" in only:  # one token per sequence, 256 sequences, context uniform in 1..4096
+    if {"attn_decode", "attn_decode_f32"} & only:  # one token per sequence, 256 sequences, context uniform in 1..4096
         ctx = np.random.default_rng(cfg.seed + 11).integers(1, 4097, 256)
         nblk = [-(-int(n) // bs_kv) for n in ctx]
         tables = torch.full((256, max(nblk)), -1, dtype=torch.int32)
@@ -206,6 +208,11 @@ def main() -> int:
                     randn((rows, cfg.kv_heads, cfg.head_dim)), torch.arange(256, dtype=torch.int32, device=dev),
                     torch.from_numpy(ctx.astype(np.int32)).to(dev), tables.to(dev))
         dec_bytes = float(ctx.sum()) * cfg.kv_heads * cfg.head_dim * 2 * e + 2 * 256 * cfg.q_heads * cfg.head_dim * e
+        dec_bytes32 = dec_bytes * 4 / e
+    # the same inputs as fp32 caches (the reference's KV dtype; the drop-in's path)
+    f32ize = (lambda tup: tuple(x.float() if x.is_floating_point() else x for x in tup))
+    attn_in32 = f32ize(attn_in) if "attn_f32" in only else None
+    attn_dec32 = f32ize(attn_dec) if "attn_decode_f32" in only else None
     copy_pair = None
     if "copy" in only:  # 1 GiB plain copy: the attainable-bandwidth and traffic-counter reference
         copy_pair = (torch.ones(1 << 28, dtype=torch.int32, device=dev),
@@ -279,6 +286,16 @@ def main() -> int:
         q_, kc_, vc_, qs_, ql_, tb_ = attn_dec
         ops.paged_attention(q_, kc_, vc_, qs_, ql_, tb_, bs_kv, cfg.head_dim ** -0.5, out=dec_out, max_query_len=1)
 
+    def run_attn_f32(i):
+        q_, kc_, vc_, qs_, ql_, tb_ = attn_in32
+        ops.paged_attention(q_, kc_, vc_, qs_, ql_, tb_, bs_kv, cfg.head_dim ** -0.5, out=attn_out32)
+
+    def run_attn_decode_f32(i):
+        q_, kc_, vc_, qs_, ql_, tb_ = attn_dec32
+        ops.paged_attention(q_, kc_, vc_, qs_, ql_, tb_, bs_kv, cfg.head_dim ** -0.5, out=dec_out32, max_query_len=1)
+
+    attn_out32 = torch.empty_like(attn_in32[0]) if attn_in32 is not None else None
+    dec_out32 = torch.empty_like(attn_dec32[0]) if attn_dec32 is not None else None
     attn_out = torch.empty_like(attn_in[0]) if attn_in is not None else None
     dec_out = torch.empty_like(attn_dec[0]) if attn_dec is not None else None
 
@@ -287,7 +304,8 @@ def main() -> int:
 
     table = [("emb", run_emb), ("rms", run_rms), ("rope", run_rope), ("silu", run_silu), ("emb_rms", run_emb_rms),
              ("rms_q8", run_rms_q8), ("silu_q8", run_silu_q8), ("copy", run_copy), ("gemm", run_gemm),
-             ("gemv", run_gemv), ("split", run_split), ("attn", run_attn), ("attn_decode", run_attn_decode)]
+             ("gemv", run_gemv), ("split", run_split), ("attn", run_attn), ("attn_decode", run_attn_decode),
+             ("attn_f32", run_attn_f32), ("attn_decode_f32", run_attn_decode_f32)]
     active = [(n, f) for n, f in table if n in only]
 
     for i in range(args.warmup):
@@ -339,11 +357,16 @@ def main() -> int:
                                    f" tokens, {cfg.q_heads}/{cfg.kv_heads} heads x {cfg.head_dim}, KV block {bs_kv}",
                           "TFLOP_s": round(attn_flops / (t_us * 1e-6) / 1e12, 1),
                           "frac_of_16bit_peak": round(attn_flops / (t_us * 1e-6) / 2.5e15, 4)})
-        elif n == "attn_decode":
+        elif n == "attn_f32":
+            entry.update({"shape": f"as attn, fp32 cache and activations (the drop-in hip_paged_attention)",
+                          "TFLOP_s": round(attn_flops / (t_us * 1e-6) / 1e12, 1),
+                          "frac_of_fp32_peak": round(attn_flops / (t_us * 1e-6) / FP32_PEAK_FLOPS, 4)})
+        elif n in ("attn_decode", "attn_decode_f32"):
+            db = dec_bytes if n == "attn_decode" else dec_bytes32
             entry.update({"shape": f"decode 256 sequences, context uniform in 1..4096, {cfg.q_heads}/{cfg.kv_heads} "
-                                   f"heads x {cfg.head_dim}", "bytes": int(dec_bytes),
-                          "GB_s": round(dec_bytes / (t_us * 1e-6) / 1e9, 1),
-                          "frac_of_peak": round(dec_bytes / (t_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)})
+                                   f"heads x {cfg.head_dim}" + (", fp32 cache" if n != "attn_decode" else ""),
+                          "bytes": int(db), "GB_s": round(db / (t_us * 1e-6) / 1e9, 1),
+                          "frac_of_peak": round(db / (t_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)})
         elif n == "copy":
             entry.update({"bytes": 2 * copy_pair[0].numel() * 4,
                           "GB_s": round(2 * copy_pair[0].numel() * 4 / (t_us * 1e-6) / 1e9, 1)})
@@ -404,7 +427,8 @@ def main() -> int:
         "q8_gemm": res_ops.get("gemm"),
         "q8_gemv": res_ops.get("gemv"),
         "q8_0_split": res_ops.get("split"),
-        "paged_attention": {k: res_ops[k] for k in ("attn", "attn_decode") if k in res_ops} or None,
+        "paged_attention": {k: res_ops[k] for k in ("attn", "attn_decode", "attn_f32", "attn_decode_f32")
+                            if k in res_ops} or None,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
