@@ -244,12 +244,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
     // exp2 units (score * scale_log2); since scale_log2 > 0 and rounding is
     // monotonic, the max of the raw scores times scale_log2 is exactly the max
     // of the scaled ones, and each p takes one fma into exp2.
-    float mx = -INFINITY;
+    // (four independent max and sum chains, not one chain of 32 dependent ops)
+    float mx4[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
     if ((c + 1) * kFaBk <= Lmin) {  // every key of the chunk is visible to every query of the wave
 #pragma unroll
       for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-        for (int j = 0; j < 16; ++j) mx = fmaxf(mx, st[kt][j]);
+        for (int j = 0; j < 16; ++j) mx4[j & 3] = fmaxf(mx4[j & 3], st[kt][j]);
     } else {
 #pragma unroll
       for (int kt = 0; kt < 2; ++kt)
@@ -258,22 +259,24 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
           const int key = c * kFaBk + 32 * kt + 8 * (j >> 2) + 4 * half + (j & 3);
           const float x = key < L ? st[kt][j] : -INFINITY;
           st[kt][j] = x;
-          mx = fmaxf(mx, x);
+          mx4[j & 3] = fmaxf(mx4[j & 3], x);
         }
     }
+    float mx = fmaxf(fmaxf(mx4[0], mx4[1]), fmaxf(mx4[2], mx4[3]));
     mx = fmaxf(mx, __shfl_xor(mx, 32));
     const float m_new = fmaxf(m, mx * scale_log2);
     const float m_use = m_new == -INFINITY ? 0.0f : m_new;
-    float ls = 0.0f;
+    float ls4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     v8 pb[2][2];
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
       for (int j = 0; j < 16; ++j) {
         const float p = __builtin_amdgcn_exp2f(fmaf(st[kt][j], scale_log2, -m_use));
-        ls += p;
+        ls4[j & 3] += p;
         pb[kt][j >> 3][j & 7] = (T)p;
       }
+    float ls = (ls4[0] + ls4[1]) + (ls4[2] + ls4[3]);
     ls += __shfl_xor(ls, 32);
     // the rescale factor is exactly 1 where the max did not move: skip it when
     // that holds for every query of the wave
