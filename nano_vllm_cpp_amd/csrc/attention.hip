@@ -188,8 +188,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
     for (int i = 0; i < 4; ++i) {
       kreg[i] = ld16(kb + (int64_t)(ld_r + 16 * i) * kv_stride);
       const int key = 4 * ld_r + i;
-      // keys past the tile's range may hold anything: zero their V (their p is 0)
-      vreg[i] = k0 + key < Lmax ? ld16(vb + (int64_t)key * kv_stride) : u32x4{0, 0, 0, 0};
+      // keys past the tile's range may hold anything: zero their V (their p is 0).
+      // The row itself lies inside the chunk's block, so the load is unconditional
+      // and only the value is selected (no branch around the load).
+      const u32x4 v = ld16(vb + (int64_t)key * kv_stride);
+      vreg[i] = k0 + key < Lmax ? v : u32x4{0, 0, 0, 0};
     }
   };
   auto store_chunk = [&](uint8_t* st) {
@@ -399,8 +402,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
     for (int i = 0; i < 4; ++i) {
       const int key = ld_r + 8 * i;
       kreg[i] = ld16(kb + (int64_t)key * kv_stride);
-      // keys past the tile's range may hold anything: zero their V (their p is 0)
-      vreg[i] = k0 + key < Lmax ? ld16(vb + (int64_t)key * kv_stride) : u32x4{0, 0, 0, 0};
+      // keys past the tile's range may hold anything: zero their V (their p is 0).
+      // The row itself lies inside the chunk's block, so the load is unconditional
+      // and only the value is selected (no branch around the load).
+      const u32x4 v = ld16(vb + (int64_t)key * kv_stride);
+      vreg[i] = k0 + key < Lmax ? v : u32x4{0, 0, 0, 0};
     }
   };
   auto store_chunk = [&](uint8_t* st) {
