@@ -584,7 +584,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
       const int key = 16 * (i >> 2) + 4 * g + (i & 3);
-      vr[i] = k0 + key < L ? ld16(vb + (int64_t)key * kv_stride) : u32x4{0, 0, 0, 0};  // past L: zero
+      const u32x4 v = ld16(vb + (int64_t)key * kv_stride);  // inside the chunk's block: no branch
+      vr[i] = k0 + key < L ? v : u32x4{0, 0, 0, 0};           // past L: zero
     }
   };
   if (nchunks > 0) load_chunk(0);
@@ -728,8 +729,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
     for (int u = 0; u < 4; ++u) {
       const int key = 4 * g + u;
       const bool ok = k0 + key < L;
-      vr[2 * u] = ok ? ld16(vb + (int64_t)key * kv_stride) : u32x4{0, 0, 0, 0};
-      vr[2 * u + 1] = ok ? ld16(vb + (int64_t)key * kv_stride + 4) : u32x4{0, 0, 0, 0};
+      // (the rows lie inside the chunk's block: unconditional loads, selected values)
+      const u32x4 v0 = ld16(vb + (int64_t)key * kv_stride), v1 = ld16(vb + (int64_t)key * kv_stride + 4);
+      vr[2 * u] = ok ? v0 : u32x4{0, 0, 0, 0};
+      vr[2 * u + 1] = ok ? v1 : u32x4{0, 0, 0, 0};
     }
   };
   auto compute = [&](int c, const u32x4* kr, const u32x4* vr) {
