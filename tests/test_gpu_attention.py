@@ -240,3 +240,18 @@ def test_paged_attention_late_rising_max(gpu, dt):
     case(f"paged_attention late rising max dt={dt}")
     got = H.to_host(run_attention(gpu, b, 4, 1, 128, bs, scale, dt))
     assert_attn(got, exact, vmax, dt, "late max")
+
+
+@pytest.mark.parametrize("dt", DTYPES, ids=DT_IDS)
+def test_paged_attention_many_short_sequences(gpu, dt):
+    """700 five-token prefills: 3500 tokens, every 128-token tile spans several
+    sequences, so the tile launch does nothing and the decode kernel that follows
+    it takes every token."""
+    r = H.rng(70 + dt)
+    ctx = [5] * 700
+    b = H.make_paged(r, ctx, ctx, 8, 2, 128, 64, dt)
+    scale = 128 ** -0.5
+    _, exact, vmax = H.oracle_attention(b, 8, 2, 128, 64, scale, dt)
+    case(f"paged_attention 700 short sequences dt={dt}")
+    got = H.to_host(run_attention(gpu, b, 8, 2, 128, 64, scale, dt))
+    assert_attn(got, exact, vmax, dt, "many short sequences")
