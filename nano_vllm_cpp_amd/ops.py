@@ -290,7 +290,8 @@ def rope_inv_freq(theta: float, head_dim: int, device: str | torch.device = "cpu
 def qk_norm_rope(q: torch.Tensor, k: torch.Tensor | None, positions: torch.Tensor, q_w: torch.Tensor | None,
                  k_w: torch.Tensor | None, inv_freq: torch.Tensor, q_heads: int, kv_heads: int, head_dim: int,
                  eps: float = 1e-6) -> None:
-    """In place on q [T, q_stride] and k [T, k_stride] (row strides = the tensors' widths).
+    """In place on q [T, q_heads * head_dim] and k [T, kv_heads * head_dim] (row strides
+    from the tensors, so views into a packed qkv row work).
 
     q_w / k_w None -> plain NeoX RoPE.  positions: int64 [T] on the GPU."""
     tokens = q.shape[0]
@@ -298,13 +299,13 @@ def qk_norm_rope(q: torch.Tensor, k: torch.Tensor | None, positions: torch.Tenso
         raise ValueError("positions must be int64 [tokens]")
     if inv_freq.dtype != torch.float32 or inv_freq.numel() != head_dim // 2:
         raise ValueError("inv_freq must be float32 [head_dim/2]")
-    q2 = q.reshape(tokens, -1)
-    k2 = k.reshape(tokens, -1) if k is not None else None
+    # rows may be strided (e.g. the q and k columns of a packed [q | k | v] row); the
+    # heads within a row are contiguous
     _check(lib().nvf_qk_norm_rope(
-        _dev(q, "q"), _dev(k, "k") if k is not None else None, _dev(positions, "positions"),
+        _dev_rows(q, "q"), _dev_rows(k, "k") if k is not None else None, _dev(positions, "positions"),
         _dev(q_w, "q_w") if q_w is not None else None, _dev(k_w, "k_w") if k_w is not None else None,
-        _dev(inv_freq, "inv_freq"), tokens, q_heads, kv_heads, head_dim, q2.shape[1],
-        k2.shape[1] if k2 is not None else 0, eps, _dt(q), _stream()), "qk_norm_rope")
+        _dev(inv_freq, "inv_freq"), tokens, q_heads, kv_heads, head_dim, q.stride(0),
+        k.stride(0) if k is not None else 0, eps, _dt(q), _stream()), "qk_norm_rope")
 
 
 # ---------------------------------------------------------------------------
