@@ -254,6 +254,10 @@ def _rope_case(gpu, dt, T, hq, hk, hd, norm, packed, seed, positions=None):
         assert rc == 0, ops.lib().nvf_last_error()
         got = H.to_host(d)
         H.assert_close(got, ref, dt, floor=1e-6, what="qk_norm_rope packed")
+        # the same through the Python front end, on views of the packed row (v untouched)
+        d2 = H.to_dev(qkv, gpu, dt)
+        ops.qk_norm_rope(d2[:, :qs], d2[:, qs:qs + ks], d_pos, d_qw, d_kw, d_inv, hq, hk, hd)
+        H.assert_close(H.to_host(d2), ref, dt, floor=1e-6, what="qk_norm_rope packed views")
         return
     q, k = H.gen_act(r, (T, qs), dt), H.gen_act(r, (T, ks), dt)
     rq, rk = q.copy(), k.copy()
