@@ -531,12 +531,12 @@ struct Mfma16x16<_Float16> {
   }
 };
 
-template <typename T>
+template <typename T, bool SPLIT>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void fa_decode_kernel(
     const T* __restrict__ q, T* __restrict__ out, const T* __restrict__ kc, const T* __restrict__ vc,
     const int32_t* __restrict__ qseq, const int32_t* __restrict__ qlen, const int32_t* __restrict__ tables,
     int64_t tokens, int q_heads, int kv_heads, int bs, int max_blocks, float scale_log2, int64_t q_stride,
-    bool skip_uniform_tiles) {
+    bool skip_uniform_tiles, int split_keys, float* __restrict__ part) {
   using M = Mfma16x16<T>;
   using v8 = typename M::v8;
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
@@ -567,7 +567,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
   for (int d = 0; d < kFaHd / 16; ++d) o[d] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
   float m = -INFINITY, l = 0.0f;
 
-  const int nchunks = L > 0 ? (L + 63) / 64 : 0;
+  // this wave's chunks: all of the token's, or split blockIdx.z's split_keys keys of them
+  int c0 = 0, c1 = L > 0 ? (L + 63) / 64 : 0;
+  if constexpr (SPLIT) {
+    c0 = (int)blockIdx.z * (split_keys / 64);
+    c1 = min(c1, c0 + split_keys / 64);
+  }
   // chunk loads: K as MFMA A operands (key 16 kt + col, dims 32 s + 8 g);
   // V rows for the transpose (key 4 i + g... : lane l covers dims 8 (l % 16) of
   // keys 16 i + (l / 16) * 4 + {0..3} over i < 4, 16 loads)
@@ -588,8 +593,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
       vr[i] = k0 + key < L ? v : u32x4{0, 0, 0, 0};           // past L: zero
     }
   };
-  if (nchunks > 0) load_chunk(0);
-  for (int c = 0; c < nchunks; ++c) {
+  if (c0 < c1) load_chunk(c0);
+  for (int c = c0; c < c1; ++c) {
     // V^T into this wave's LDS: dim 8 col + e, keys 16 i4 + 4 g + {0..3}
 #pragma unroll
     for (int i4 = 0; i4 < 4; ++i4)
@@ -609,7 +614,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
 #pragma unroll
       for (int s = 0; s < 4; ++s) st[kt] = M::mma(__builtin_bit_cast(v8, kr[kt][s]), qf[s], st[kt]);
     }
-    if (c + 1 < nchunks) load_chunk(c + 1);  // in flight during the math below
+    if (c + 1 < c1) load_chunk(c + 1);  // in flight during the math below
     __builtin_amdgcn_wave_barrier();
     // online softmax per head (lane column); element j of tile kt is key 64 c + 16 kt + 4 g + j
     float mx = -INFINITY;
@@ -657,7 +662,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
     __builtin_amdgcn_wave_barrier();  // this chunk's V^T reads before the next chunk's writes
   }
   // O^T: lane column = head col, dims 16 d + 4 g + j
-  if (head_ok) {
+  if constexpr (SPLIT) {  // unnormalised partial O, running max (exp2 units) and sum
+    if (head_ok) {
+      const int64_t pi = (t * q_heads + h) * gridDim.z + blockIdx.z;
+      float* po = part + pi * kFaHd;
+#pragma unroll
+      for (int d = 0; d < kFaHd / 16; ++d) st16(po + 16 * d + 4 * g, __builtin_bit_cast(u32x4, o[d]));
+      if (g == 0) {
+        float* pml = part + tokens * q_heads * gridDim.z * kFaHd + 2 * pi;
+        pml[0] = m;
+        pml[1] = l;
+      }
+    }
+  } else if (head_ok) {
     const float inv = l > 0.0f ? 1.0f / l : 0.0f;
     T* orow = out + (t * q_heads + h) * kFaHd;
 #pragma unroll
@@ -685,11 +702,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
 //                   the 8 tiles are 32 consecutive bytes of its V row.
 constexpr int kFd32Bk = 16;  // keys per chunk
 
+template <bool SPLIT>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void fa_decode_f32_kernel(
     const float* __restrict__ q, float* __restrict__ out, const float* __restrict__ kc, const float* __restrict__ vc,
     const int32_t* __restrict__ qseq, const int32_t* __restrict__ qlen, const int32_t* __restrict__ tables,
     int64_t tokens, int q_heads, int kv_heads, int bs, int max_blocks, float scale_log2, int64_t q_stride,
-    bool skip_uniform_tiles) {
+    bool skip_uniform_tiles, int split_keys, float* __restrict__ part) {
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   const int64_t t = blockIdx.x;
@@ -714,7 +732,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
 #pragma unroll
   for (int d = 0; d < 8; ++d) o[d] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
   float m = -INFINITY, l = 0.0f;
-  const int nchunks = L > 0 ? (L + kFd32Bk - 1) / kFd32Bk : 0;
+  // this wave's chunks: all of the token's, or split blockIdx.z's split_keys keys of them
+  int c0 = 0, c1 = L > 0 ? (L + kFd32Bk - 1) / kFd32Bk : 0;
+  if constexpr (SPLIT) {
+    c0 = (int)blockIdx.z * (split_keys / kFd32Bk);
+    c1 = min(c1, c0 + split_keys / kFd32Bk);
+  }
 
   // chunk c: K row of key 16 c + col, dims 32 g + 4 i (A operands of S^T); V row
   // of key 16 c + 4 g + u, dims 8 col .. 8 col + 7 (A operands of O^T, zero past L)
@@ -788,17 +811,33 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
   };
 
   u32x4 ka[8], va[8], kb_[8], vb_[8];
-  if (nchunks > 0) load(0, ka, va);
-  for (int c = 0; c < nchunks; c += 2) {  // two chunks per trip: the register sets trade roles
-    if (c + 1 < nchunks) load(c + 1, kb_, vb_);
+  if (c0 < c1) load(c0, ka, va);
+  for (int c = c0; c < c1; c += 2) {  // two chunks per trip: the register sets trade roles
+    if (c + 1 < c1) load(c + 1, kb_, vb_);
     compute(c, ka, va);
-    if (c + 1 < nchunks) {
-      if (c + 2 < nchunks) load(c + 2, ka, va);
+    if (c + 1 < c1) {
+      if (c + 2 < c1) load(c + 2, ka, va);
       compute(c + 1, kb_, vb_);
     }
   }
   // O^T: register v of tile d is dim 8 (4 g + v) + d of head col
-  if (head_ok) {
+  if constexpr (SPLIT) {  // unnormalised partial O, running max (exp2 units) and sum
+    if (head_ok) {
+      const int64_t pi = (t * q_heads + h) * gridDim.z + blockIdx.z;
+      float* po = part + pi * kFaHd;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        float* p = po + 8 * (4 * g + v);
+        st16(p, __builtin_bit_cast(u32x4, f32x4{o[0][v], o[1][v], o[2][v], o[3][v]}));
+        st16(p + 4, __builtin_bit_cast(u32x4, f32x4{o[4][v], o[5][v], o[6][v], o[7][v]}));
+      }
+      if (g == 0) {
+        float* pml = part + tokens * q_heads * gridDim.z * kFaHd + 2 * pi;
+        pml[0] = m;
+        pml[1] = l;
+      }
+    }
+  } else if (head_ok) {
     const float inv = l > 0.0f ? 1.0f / l : 0.0f;
     float* orow = out + (t * q_heads + h) * kFaHd;
 #pragma unroll
@@ -895,6 +934,93 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_wave_kernel(
   }
 }
 
+// ---------------------------------------------------------------------------
+// Split decode (few (token, kv head) pairs, long contexts): the decode kernels run
+// with blockIdx.z = split, each over split_keys keys, writing an unnormalised
+// partial O (fp32, [token][q head][split][128]) and its running max (exp2 units)
+// and sum ([token][q head][split][2], after the O block); this kernel merges them:
+// out = sum_z 2^(m_z - M) O_z / sum_z 2^(m_z - M) l_z, M = max_z m_z.  One
+// workgroup per (token, q head): 4 waves take every 4th split, two dims per lane,
+// and meet in LDS.
+template <typename T>
+__global__ __launch_bounds__(256) void attn_split_combine_kernel(const float* __restrict__ part, T* __restrict__ out,
+                                                                 const int32_t* __restrict__ qseq, int64_t tokens,
+                                                                 int q_heads, int nsplit, bool skip_uniform_tiles) {
+  __shared__ float red[4][2 * 64 + 1];
+  __shared__ float wmax[4];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int64_t t = blockIdx.x;
+  const int h = (int)blockIdx.y;
+  if (skip_uniform_tiles && fa_tile_uniform(qseq, tokens, t / kFaBq)) return;  // the tiles' tokens (whole workgroup)
+  const int64_t p0 = (t * q_heads + h) * nsplit;
+  const float* pml = part + tokens * q_heads * nsplit * kFaHd + 2 * p0;
+  float mx = -INFINITY;
+  for (int z = threadIdx.x; z < nsplit; z += 256) mx = fmaxf(mx, pml[2 * z]);
+  mx = wave_max(mx);
+  if (lane == 0) wmax[wave] = mx;
+  __syncthreads();
+  mx = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+  T* o = out + (t * q_heads + h) * kFaHd + 2 * lane;
+  if (mx == -INFINITY) {  // no keys at all: zeros, as the unsplit kernels write
+    if (wave == 0) {
+      o[0] = from_f32<T>(0.0f);
+      o[1] = from_f32<T>(0.0f);
+    }
+    return;
+  }
+  // wave w: splits w, w + 4, ...; an empty split (m = -inf, O = 0, l = 0) weighs 0
+  float den = 0.0f, a0 = 0.0f, a1 = 0.0f;
+#pragma unroll 4
+  for (int z = wave; z < nsplit; z += 4) {
+    const float w = __builtin_amdgcn_exp2f(pml[2 * z] - mx);
+    den += w * pml[2 * z + 1];
+    const float2 v = *reinterpret_cast<const float2*>(part + (p0 + z) * kFaHd + 2 * lane);
+    a0 += w * v.x;
+    a1 += w * v.y;
+  }
+  red[wave][2 * lane] = a0;
+  red[wave][2 * lane + 1] = a1;
+  if (lane == 0) red[wave][128] = den;
+  __syncthreads();
+  if (wave == 0) {
+    a0 = (red[0][2 * lane] + red[1][2 * lane]) + (red[2][2 * lane] + red[3][2 * lane]);
+    a1 = (red[0][2 * lane + 1] + red[1][2 * lane + 1]) + (red[2][2 * lane + 1] + red[3][2 * lane + 1]);
+    den = (red[0][128] + red[1][128]) + (red[2][128] + red[3][128]);
+    const float inv = den > 0.0f ? 1.0f / den : 0.0f;
+    o[0] = from_f32<T>(a0 * inv);
+    o[1] = from_f32<T>(a1 * inv);
+  }
+}
+
+// How a decode launch is split: only when its (token, kv head) waves cannot fill
+// the GPU; then into enough key ranges (multiples of 64 keys) for
+// about kSplitTargetWaves waves.  The context bound is the block table's width.
+constexpr int64_t kSplitMinWaves = 1024;
+constexpr int64_t kSplitTargetWaves = 512;  // a decode wave keeps ~32 KB in flight: 512 cover HBM
+constexpr int64_t kSplitMinKeys = 64;
+struct SplitPlan {
+  int nsplit = 1;
+  int keys = 0;
+};
+inline SplitPlan split_plan(int64_t tokens, int q_heads, int kv_heads, int hd, int bs, int max_blocks) {
+  SplitPlan p;
+  const int64_t waves = tokens * kv_heads;
+  const int64_t ctx = (int64_t)bs * max_blocks;
+  if (hd != kFaHd || q_heads / kv_heads > 16 || bs % 64 != 0 || waves >= kSplitMinWaves || ctx < 2 * kSplitMinKeys)
+    return p;
+  int64_t n = std::min<int64_t>((kSplitTargetWaves + waves - 1) / waves, ctx / kSplitMinKeys);
+  int64_t keys = ((ctx + n - 1) / n + 63) / 64 * 64;
+  n = (ctx + keys - 1) / keys;
+  if (n <= 1 || n > 65535 || keys > INT32_MAX) return p;
+  p.nsplit = (int)n;
+  p.keys = (int)keys;
+  return p;
+}
+inline int64_t split_bytes(int64_t tokens, int q_heads, const SplitPlan& p) {
+  return p.nsplit > 1 ? tokens * q_heads * p.nsplit * (kFaHd + 2) * (int64_t)sizeof(float) : 0;
+}
+
 template <typename T, int DPL>
 void launch_attn_wave(const void* q, void* out, const void* kc, const void* vc, const int32_t* qseq,
                       const int32_t* qlen, const int32_t* tables, int64_t tokens, int q_heads, int kv_heads, int hd,
@@ -917,8 +1043,12 @@ void launch_attn_wave(const void* q, void* out, const void* kc, const void* vc, 
 template <typename T>
 int attention_dispatch(const void* q, void* out, const void* kc, const void* vc, const int32_t* qseq,
                        const int32_t* qlen, const int32_t* tables, int64_t tokens, int q_heads, int kv_heads, int hd,
-                       int bs, int max_blocks, float scale, int64_t q_stride, int64_t max_query_len, hipStream_t st) {
+                       int bs, int max_blocks, float scale, int64_t q_stride, int64_t max_query_len, void* ws,
+                       int64_t ws_bytes, hipStream_t st) {
   constexpr int N = Pack<T>::N;
+  // a decode split needs the caller's workspace (none: unsplit)
+  const SplitPlan sp = split_plan(tokens, q_heads, kv_heads, hd, bs, max_blocks);
+  const bool split = sp.nsplit > 1 && ws != nullptr && ws_bytes >= split_bytes(tokens, q_heads, sp);
   // matrix-core paths: 16-bit, head_dim 128, 64-key chunks inside one block, 16-byte rows, <= 16 heads per kv head
   bool mfma = false;
   if constexpr (sizeof(T) == 2) {
@@ -929,7 +1059,9 @@ int attention_dispatch(const void* q, void* out, const void* kc, const void* vc,
   if constexpr (sizeof(T) == 2) {
     if (mfma) {
       const float sl = scale * 1.4426950408889634f;
-      const bool tiles = max_query_len != 1;  // 1: every sequence has one query (decode): no tile can be uniform
+      // tiles: not for a promised decode batch (max_query_len 1: no tile can be uniform)
+      // nor for fewer tokens than one tile (a short batch goes to the decode kernel)
+      const bool tiles = max_query_len != 1 && tokens >= kFaBq;
       if (tiles) {
         static std::once_flag attr_once;
         std::call_once(attr_once, [] {
@@ -946,13 +1078,27 @@ int attention_dispatch(const void* q, void* out, const void* kc, const void* vc,
       }
       static std::once_flag dec_once;
       std::call_once(dec_once, [] {
-        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&fa_decode_kernel<T>),
+        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&fa_decode_kernel<T, false>),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, kFdLds);
+        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&fa_decode_kernel<T, true>),
                                   hipFuncAttributeMaxDynamicSharedMemorySize, kFdLds);
       });
       if (tokens > INT32_MAX) return fail(NVF_ERR_INVALID, "paged_attention: too many tokens");
-      fa_decode_kernel<T><<<dim3((unsigned)tokens, (unsigned)((kv_heads + 3) / 4)), 256, kFdLds, st>>>(
+      const unsigned kvg = (unsigned)((kv_heads + 3) / 4);
+      if (split) {
+        fa_decode_kernel<T, true><<<dim3((unsigned)tokens, kvg, (unsigned)sp.nsplit), 256, kFdLds, st>>>(
+            static_cast<const T*>(q), static_cast<T*>(out), static_cast<const T*>(kc), static_cast<const T*>(vc),
+            qseq, qlen, tables, tokens, q_heads, kv_heads, bs, max_blocks, sl, q_stride, tiles, sp.keys,
+            static_cast<float*>(ws));
+        const int rc = launch_status("paged_attention(split decode)");
+        if (rc != NVF_OK) return rc;
+        attn_split_combine_kernel<T><<<dim3((unsigned)tokens, (unsigned)q_heads), 256, 0, st>>>(
+            static_cast<const float*>(ws), static_cast<T*>(out), qseq, tokens, q_heads, sp.nsplit, tiles);
+        return launch_status("paged_attention(split combine)");
+      }
+      fa_decode_kernel<T, false><<<dim3((unsigned)tokens, kvg), 256, kFdLds, st>>>(
           static_cast<const T*>(q), static_cast<T*>(out), static_cast<const T*>(kc), static_cast<const T*>(vc), qseq,
-          qlen, tables, tokens, q_heads, kv_heads, bs, max_blocks, sl, q_stride, tiles);
+          qlen, tables, tokens, q_heads, kv_heads, bs, max_blocks, sl, q_stride, tiles, 0, nullptr);
       return launch_status("paged_attention(decode)");
     }
   }
@@ -964,7 +1110,7 @@ int attention_dispatch(const void* q, void* out, const void* kc, const void* vc,
     // chunks inside one block, the decode kernel 16-key chunks and <= 16 heads per kv head
     const bool base = hd == kFaHd && aligned16(q) && aligned16(out) && aligned16(kc) && aligned16(vc) &&
                       q_stride % N == 0 && scale > 0.0f;
-    const bool tiles = base && bs % kF32Bk == 0 && max_query_len != 1;
+    const bool tiles = base && bs % kF32Bk == 0 && max_query_len != 1 && tokens >= kFaBq;
     const bool dec = base && bs % kFd32Bk == 0 && q_heads / kv_heads <= 16;
     if (tiles) {
       static std::once_flag f32_once;
@@ -984,10 +1130,23 @@ int attention_dispatch(const void* q, void* out, const void* kc, const void* vc,
     }
     if (dec) {
       if (tokens > INT32_MAX) return fail(NVF_ERR_INVALID, "paged_attention: too many tokens");
-      fa_decode_f32_kernel<<<dim3((unsigned)tokens, (unsigned)((kv_heads + 3) / 4)), 256, 0, st>>>(
+      const unsigned kvg = (unsigned)((kv_heads + 3) / 4);
+      const float sl = scale * 1.4426950408889634f;
+      if (split) {
+        fa_decode_f32_kernel<true><<<dim3((unsigned)tokens, kvg, (unsigned)sp.nsplit), 256, 0, st>>>(
+            static_cast<const float*>(q), static_cast<float*>(out), static_cast<const float*>(kc),
+            static_cast<const float*>(vc), qseq, qlen, tables, tokens, q_heads, kv_heads, bs, max_blocks, sl,
+            q_stride, tiles, sp.keys, static_cast<float*>(ws));
+        const int rc = launch_status("paged_attention(f32 split decode)");
+        if (rc != NVF_OK) return rc;
+        attn_split_combine_kernel<float><<<dim3((unsigned)tokens, (unsigned)q_heads), 256, 0, st>>>(
+            static_cast<const float*>(ws), static_cast<float*>(out), qseq, tokens, q_heads, sp.nsplit, tiles);
+        return launch_status("paged_attention(f32 split combine)");
+      }
+      fa_decode_f32_kernel<false><<<dim3((unsigned)tokens, kvg), 256, 0, st>>>(
           static_cast<const float*>(q), static_cast<float*>(out), static_cast<const float*>(kc),
-          static_cast<const float*>(vc), qseq, qlen, tables, tokens, q_heads, kv_heads, bs, max_blocks,
-          scale * 1.4426950408889634f, q_stride, tiles);
+          static_cast<const float*>(vc), qseq, qlen, tables, tokens, q_heads, kv_heads, bs, max_blocks, sl,
+          q_stride, tiles, 0, nullptr);
       return launch_status("paged_attention(f32 decode)");
     }
   }
@@ -1051,10 +1210,11 @@ int nvf_store_kv(const void* key, const void* value, void* k_cache, void* v_cach
   return rc;
 }
 
-int nvf_paged_attention(const void* q, void* out, const void* k_cache, const void* v_cache, const int32_t* query_seq,
-                        const int32_t* query_key_len, const int32_t* block_tables, int64_t tokens, int q_heads,
-                        int kv_heads, int head_dim, int block_size, int max_blocks, float scale, int64_t q_stride,
-                        int64_t max_query_len, int dtype, void* stream) {
+int nvf_paged_attention_ws(const void* q, void* out, const void* k_cache, const void* v_cache,
+                           const int32_t* query_seq, const int32_t* query_key_len, const int32_t* block_tables,
+                           int64_t tokens, int q_heads, int kv_heads, int head_dim, int block_size, int max_blocks,
+                           float scale, int64_t q_stride, int64_t max_query_len, void* workspace,
+                           int64_t workspace_bytes, int dtype, void* stream) {
   if (!dtype_ok(dtype)) return fail(NVF_ERR_INVALID, "nvf_paged_attention: bad dtype %d", dtype);
   if (tokens < 0 || q_heads <= 0 || kv_heads <= 0 || head_dim <= 0 || block_size <= 0 || max_blocks <= 0)
     return fail(NVF_ERR_INVALID, "nvf_paged_attention: bad shape");
@@ -1066,14 +1226,32 @@ int nvf_paged_attention(const void* q, void* out, const void* k_cache, const voi
   if (tokens == 0) return NVF_OK;
   if (!q || !out || !k_cache || !v_cache || !query_seq || !query_key_len || !block_tables)
     return fail(NVF_ERR_INVALID, "nvf_paged_attention: NULL pointer");
+  if (workspace && !aligned16(workspace))
+    return fail(NVF_ERR_INVALID, "nvf_paged_attention: workspace must be 16-byte aligned");
   if ((tokens * q_heads + kAttnWaves - 1) / kAttnWaves > INT32_MAX)
     return fail(NVF_ERR_INVALID, "nvf_paged_attention: too many (token, head) pairs");
   int rc = NVF_OK;
   NVF_DISPATCH_DTYPE(dtype, T, rc = attention_dispatch<T>(q, out, k_cache, v_cache, query_seq, query_key_len,
                                                          block_tables, tokens, q_heads, kv_heads, head_dim, block_size,
-                                                         max_blocks, scale, q_stride, max_query_len,
-                                                         as_stream(stream)));
+                                                         max_blocks, scale, q_stride, max_query_len, workspace,
+                                                         workspace_bytes, as_stream(stream)));
   return rc;
+}
+
+int nvf_paged_attention(const void* q, void* out, const void* k_cache, const void* v_cache, const int32_t* query_seq,
+                        const int32_t* query_key_len, const int32_t* block_tables, int64_t tokens, int q_heads,
+                        int kv_heads, int head_dim, int block_size, int max_blocks, float scale, int64_t q_stride,
+                        int64_t max_query_len, int dtype, void* stream) {
+  return nvf_paged_attention_ws(q, out, k_cache, v_cache, query_seq, query_key_len, block_tables, tokens, q_heads,
+                                kv_heads, head_dim, block_size, max_blocks, scale, q_stride, max_query_len, nullptr, 0,
+                                dtype, stream);
+}
+
+int64_t nvf_paged_attention_workspace_size(int64_t tokens, int q_heads, int kv_heads, int head_dim, int block_size,
+                                           int max_blocks) {
+  if (tokens <= 0 || q_heads <= 0 || kv_heads <= 0 || block_size <= 0 || max_blocks <= 0 || q_heads % kv_heads)
+    return 0;
+  return split_bytes(tokens, q_heads, split_plan(tokens, q_heads, kv_heads, head_dim, block_size, max_blocks));
 }
 
 // Drop-ins: include/nanovllm/hip_ops.hpp:22-28 / src/hip_ops.hip:724-744 (fp32 cache, null stream).
@@ -1086,14 +1264,43 @@ void hip_store_kv(const float* key, const float* value, float* k_cache, float* v
                "hip_store_kv");
 }
 
+// Grow-only device workspace for the drop-in's split decode (the policy of the
+// reference's own hip_matmul_q8 scratch, src/hip_ops.hip:642-648): reallocated
+// only when a call needs more, or on another device.  Like the reference's ops it
+// assumes one calling thread; calls on several streams at once would share it.
+struct AttnScratch {
+  void* p = nullptr;
+  size_t cap = 0;
+  int device = -1;
+};
+AttnScratch g_attn_scratch;
+
 void hip_paged_attention(const float* q, float* out, const float* k_cache, const float* v_cache,
                          const int32_t* query_seq, const int32_t* query_key_len, const int32_t* block_tables,
                          int tokens, int q_heads, int kv_heads, int head_dim, int block_size, int max_blocks,
                          float scale) {
   if (tokens <= 0 || q_heads <= 0 || kv_heads <= 0) return;
-  dropin_check(nvf_paged_attention(q, out, k_cache, v_cache, query_seq, query_key_len, block_tables, tokens, q_heads,
-                                   kv_heads, head_dim, block_size, max_blocks, scale, (int64_t)q_heads * head_dim,
-                                   0, NVF_F32, nullptr),
+  const int64_t need = nvf_paged_attention_workspace_size(tokens, q_heads, kv_heads, head_dim, block_size, max_blocks);
+  if (need > 0) {
+    int dev = 0;
+    dropin_check(hipGetDevice(&dev) == hipSuccess ? NVF_OK : fail(NVF_ERR_LAUNCH, "hipGetDevice failed"),
+                 "hip_paged_attention");
+    if ((size_t)need > g_attn_scratch.cap || dev != g_attn_scratch.device) {
+      if (g_attn_scratch.p) (void)hipFree(g_attn_scratch.p);
+      g_attn_scratch.p = nullptr;
+      g_attn_scratch.cap = 0;
+      if (hipMalloc(&g_attn_scratch.p, (size_t)need) != hipSuccess)
+        dropin_check(fail(NVF_ERR_LAUNCH, "hip_paged_attention: workspace allocation of %lld bytes failed",
+                          (long long)need),
+                     "hip_paged_attention");
+      g_attn_scratch.cap = (size_t)need;
+      g_attn_scratch.device = dev;
+    }
+  }
+  dropin_check(nvf_paged_attention_ws(q, out, k_cache, v_cache, query_seq, query_key_len, block_tables, tokens,
+                                      q_heads, kv_heads, head_dim, block_size, max_blocks, scale,
+                                      (int64_t)q_heads * head_dim, 0, need > 0 ? g_attn_scratch.p : nullptr, need,
+                                      NVF_F32, nullptr),
                "hip_paged_attention");
 }
 

@@ -255,3 +255,57 @@ def test_paged_attention_many_short_sequences(gpu, dt):
     case(f"paged_attention 700 short sequences dt={dt}")
     got = H.to_host(run_attention(gpu, b, 8, 2, 128, 64, scale, dt))
     assert_attn(got, exact, vmax, dt, "many short sequences")
+
+
+SPLIT_CASES = [
+    # (context lengths of a decode batch, (q_heads, kv_heads)): few (token, kv head) pairs
+    ([4096], (28, 4)),
+    ([5000, 77, 1, 2049, 300], (28, 4)),   # ragged; one query also gets key_len 0 below
+    ([8192, 1024], (32, 8)),
+    ([640], (16, 1)),
+]
+
+
+@pytest.mark.parametrize("dt", DTYPES, ids=DT_IDS)
+@pytest.mark.parametrize("ci", range(len(SPLIT_CASES)))
+def test_paged_attention_split_decode(gpu, dt, ci):
+    """Small decode batches over long contexts take the split path (partial
+    softmax per key range, then a merge): within the same tolerance of the
+    oracle as the unsplit kernel, for a promised decode batch and an unhinted one."""
+    ctx, (qh, kvh) = SPLIT_CASES[ci]
+    r = H.rng(400 + ci * 3 + dt)
+    b = H.make_paged(r, ctx, [1] * len(ctx), qh, kvh, 128, 256, dt)
+    if len(ctx) > 2:
+        b.query_key_len[1] = 0
+    assert ops.lib().nvf_paged_attention_workspace_size(b.tokens, qh, kvh, 128, 256, b.max_blocks) > 0
+    scale = 128 ** -0.5
+    _, exact, vmax = H.oracle_attention(b, qh, kvh, 128, 256, scale, dt)
+    args = (H.to_dev(b.q, gpu, dt), H.to_dev(b.k_cache, gpu, dt), H.to_dev(b.v_cache, gpu, dt),
+            H.to_dev(b.query_seq, gpu), H.to_dev(b.query_key_len, gpu), H.to_dev(b.block_tables, gpu), 256, scale)
+    for mql in (1, 0):
+        case(f"paged_attention split decode case={ci} dt={dt} max_query_len={mql}")
+        got = H.to_host(ops.paged_attention(*args, max_query_len=mql))
+        assert_attn(got, exact, vmax, dt, f"split (max_query_len={mql})")
+        if len(ctx) > 2:
+            assert not H.from_storage(got, dt)[1].any()  # key_len 0: zeros
+    case(f"paged_attention unsplit case={ci} dt={dt}")
+    got = H.to_host(ops.paged_attention(*args, max_query_len=1, split=False))
+    assert_attn(got, exact, vmax, dt, "unsplit")
+
+
+def test_dropin_split_decode_grows_its_workspace(gpu):
+    """The fp32 drop-in splits small decode batches with its own grow-only
+    workspace: a short-context call, then a longer one needing more."""
+    for ctx, seed in (([700, 33], 1), ([6000, 4096, 17], 2)):
+        r = H.rng(500 + seed)
+        b = H.make_paged(r, ctx, [1] * len(ctx), 28, 4, 128, 256, H.F32)
+        scale = 128 ** -0.5
+        _, exact, vmax = H.oracle_attention(b, 28, 4, 128, 256, scale, H.F32)
+        dq, dk, dv = H.to_dev(b.q, gpu), H.to_dev(b.k_cache, gpu), H.to_dev(b.v_cache, gpu)
+        dqs, dql, dtab = H.to_dev(b.query_seq, gpu), H.to_dev(b.query_key_len, gpu), H.to_dev(b.block_tables, gpu)
+        out = torch.empty_like(dq)
+        case(f"hip_paged_attention split drop-in ctx={ctx}")
+        ops.lib().hip_paged_attention(dq.data_ptr(), out.data_ptr(), dk.data_ptr(), dv.data_ptr(), dqs.data_ptr(),
+                                      dql.data_ptr(), dtab.data_ptr(), b.tokens, 28, 4, 128, 256, b.max_blocks, scale)
+        torch.cuda.synchronize()
+        assert_attn(out.cpu().numpy(), exact, vmax, H.F32, "split drop-in")
