@@ -58,7 +58,7 @@ def parse() -> argparse.Namespace:
                    help="embedding table format (default: the config's)")
     p.add_argument("--only", default="",
                    help="comma list of ops (default emb,rms,rope,silu,copy,gemm,gemv,split,attn,attn_decode,attn_f32,"
-                        "attn_decode_f32,layer); "
+                        "attn_decode_f32,attn_decode_small,layer); "
                         "also emb_rms, rms_q8, silu_q8 (fusions)")
     return p.parse_args()
 
@@ -111,7 +111,7 @@ def main() -> int:
     emb_fmt = args.emb or cfg.emb
     nbytes = op_bytes(cfg, e, emb_fmt)
     only = set(filter(None, args.only.split(","))) or {"emb", "rms", "rope", "silu", "copy", "gemm", "gemv", "split",
-                                                       "attn", "attn_decode", "attn_f32", "attn_decode_f32", "layer"}
+                                                       "attn", "attn_decode", "attn_f32", "attn_decode_f32", "attn_decode_small", "layer"}
 
     def nsets(b: int) -> int:
         return max(2, -(-POOL_BYTES // b))
@@ -209,6 +209,17 @@ def main() -> int:
                     torch.from_numpy(ctx.astype(np.int32)).to(dev), tables.to(dev))
         dec_bytes = float(ctx.sum()) * cfg.kv_heads * cfg.head_dim * 2 * e + 2 * 256 * cfg.q_heads * cfg.head_dim * e
         dec_bytes32 = dec_bytes * 4 / e
+    attn_small = None
+    if "attn_decode_small" in only:  # 4 sequences x 32768 keys of context: the split decode path
+        sctx, sB = 32768, 4
+        snb = sctx // bs_kv
+        stab = torch.arange(sB * snb, dtype=torch.int32).view(sB, snb)
+        stab = stab[:, torch.randperm(snb, generator=torch.Generator().manual_seed(cfg.seed + 3))].contiguous()
+        srows = sB * snb * bs_kv
+        attn_small = (randn((sB, cfg.q_heads, cfg.head_dim)), randn((srows, cfg.kv_heads, cfg.head_dim)),
+                      randn((srows, cfg.kv_heads, cfg.head_dim)), torch.arange(sB, dtype=torch.int32, device=dev),
+                      torch.full((sB,), sctx, dtype=torch.int32, device=dev), stab.to(dev))
+        small_bytes = float(sB * sctx) * cfg.kv_heads * cfg.head_dim * 2 * e
     layer = None
     if "layer" in only:  # one whole decoder layer on this library's kernels (Q8_0 weights, random init)
         lpos = cfg.positions()
@@ -319,6 +330,12 @@ def main() -> int:
         q_, kc_, vc_, qs_, ql_, tb_ = attn_dec
         ops.paged_attention(q_, kc_, vc_, qs_, ql_, tb_, bs_kv, cfg.head_dim ** -0.5, out=dec_out, max_query_len=1)
 
+    def run_attn_decode_small(i):
+        q_, kc_, vc_, qs_, ql_, tb_ = attn_small
+        ops.paged_attention(q_, kc_, vc_, qs_, ql_, tb_, bs_kv, cfg.head_dim ** -0.5, out=small_out, max_query_len=1)
+
+    small_out = torch.empty_like(attn_small[0]) if attn_small is not None else None
+
     def run_layer(i):
         # model.cpp:758-833's per-layer sequence, Qwen2.5 (no QK-norm): input RMSNorm (writing the
         # qkv GEMM's int8 rows), qkv, RoPE on the q and k columns of the packed row, KV store,
@@ -359,7 +376,8 @@ def main() -> int:
     table = [("emb", run_emb), ("rms", run_rms), ("rope", run_rope), ("silu", run_silu), ("emb_rms", run_emb_rms),
              ("rms_q8", run_rms_q8), ("silu_q8", run_silu_q8), ("copy", run_copy), ("gemm", run_gemm),
              ("gemv", run_gemv), ("split", run_split), ("attn", run_attn), ("attn_decode", run_attn_decode),
-             ("attn_f32", run_attn_f32), ("attn_decode_f32", run_attn_decode_f32), ("layer", run_layer)]
+             ("attn_f32", run_attn_f32), ("attn_decode_f32", run_attn_decode_f32), ("attn_decode_small", run_attn_decode_small),
+             ("layer", run_layer)]
     active = [(n, f) for n, f in table if n in only]
 
     for i in range(args.warmup):
@@ -421,6 +439,11 @@ def main() -> int:
                                    f"heads x {cfg.head_dim}" + (", fp32 cache" if n != "attn_decode" else ""),
                           "bytes": int(db), "GB_s": round(db / (t_us * 1e-6) / 1e9, 1),
                           "frac_of_peak": round(db / (t_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)})
+        elif n == "attn_decode_small":
+            entry.update({"shape": f"decode 4 sequences x 32768 keys, {cfg.q_heads}/{cfg.kv_heads} heads x "
+                                   f"{cfg.head_dim} (split decode)", "bytes": int(small_bytes),
+                          "GB_s": round(small_bytes / (t_us * 1e-6) / 1e9, 1),
+                          "frac_of_peak": round(small_bytes / (t_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)})
         elif n == "layer":
             entry.update({"shape": f"one Qwen2.5-7B decoder layer, {T} tokens ({len(np.diff(cfg.cu_seqlens()))} "
                                    f"causal prefills), Q8_0 weights, fp16 activations and KV cache",
@@ -488,8 +511,8 @@ def main() -> int:
         "q8_gemv": res_ops.get("gemv"),
         "q8_0_split": res_ops.get("split"),
         "layer": res_ops.get("layer"),
-        "paged_attention": {k: res_ops[k] for k in ("attn", "attn_decode", "attn_f32", "attn_decode_f32")
-                            if k in res_ops} or None,
+        "paged_attention": {k: res_ops[k] for k in ("attn", "attn_decode", "attn_f32", "attn_decode_f32",
+                                                    "attn_decode_small") if k in res_ops} or None,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
