@@ -227,23 +227,24 @@ int nvf_paged_attention(const void* q, void* out, const void* k_cache, const voi
                         int kv_heads, int head_dim, int block_size, int max_blocks, float scale, int64_t q_stride,
                         int64_t max_query_len, int dtype, void* stream);
 
-/* nvf_paged_attention with a caller workspace for split decode (no counterpart
+/* nvf_paged_attention with a caller workspace for split attention (no counterpart
  * in the reference, whose kernel -- hip_ops.hip:452-550 -- walks each (token,
- * head)'s keys in one workgroup): when the batch's (token, kv head) pairs are too
- * few to fill the GPU (small-batch decode over long contexts), each pair's keys
- * are split into ranges processed in parallel and merged.  workspace (16-byte
- * aligned) of workspace_bytes >= nvf_paged_attention_workspace_size(...) enables
- * it; NULL or too small runs unsplit.  Same results to fp32 rounding. */
+ * head)'s keys in one workgroup): when the call has too little work to fill the
+ * GPU -- few decode (token, kv head) pairs, or few 128-token prefill tiles, over
+ * long contexts -- each one's keys are split into ranges processed in parallel
+ * and merged.  workspace (16-byte aligned) of workspace_bytes >=
+ * nvf_paged_attention_workspace_size(...) enables it; NULL or too small runs
+ * unsplit.  Same results to fp32 rounding. */
 int nvf_paged_attention_ws(const void* q, void* out, const void* k_cache, const void* v_cache,
                            const int32_t* query_seq, const int32_t* query_key_len, const int32_t* block_tables,
                            int64_t tokens, int q_heads, int kv_heads, int head_dim, int block_size, int max_blocks,
                            float scale, int64_t q_stride, int64_t max_query_len, void* workspace,
                            int64_t workspace_bytes, int dtype, void* stream);
 
-/* Bytes of workspace nvf_paged_attention_ws uses for this shape (0: it would not
- * split).  The context bound is block_size * max_blocks. */
+/* Bytes of workspace nvf_paged_attention_ws uses for this shape and max_query_len
+ * hint (0: it would not split).  The context bound is block_size * max_blocks. */
 int64_t nvf_paged_attention_workspace_size(int64_t tokens, int q_heads, int kv_heads, int head_dim, int block_size,
-                                           int max_blocks);
+                                           int max_blocks, int64_t max_query_len);
 
 /* Host helper: inv_freq[i] = (float)(1 / theta^(2i/head_dim)) in double, the
  * table Qwen3Model builds in its constructor (src/model.cpp:416-420).

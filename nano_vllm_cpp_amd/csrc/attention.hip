@@ -128,12 +128,12 @@ __device__ __forceinline__ bool fa_tile_uniform(const int32_t* __restrict__ qseq
   return __all(same);
 }
 
-template <typename T>
+template <typename T, bool SPLIT>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void fa_prefill_kernel(
     const T* __restrict__ q, T* __restrict__ out, const T* __restrict__ kc, const T* __restrict__ vc,
     const int32_t* __restrict__ qseq, const int32_t* __restrict__ qlen, const int32_t* __restrict__ tables,
     int64_t tokens, int q_heads, int kv_heads, int bs, int max_blocks, float scale_log2, int64_t q_stride,
-    int64_t tiles) {
+    int64_t tiles, int split_keys, float* __restrict__ part) {
   using M = Mfma16<T>;
   using v8 = typename M::v8;
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
@@ -223,14 +223,20 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
   for (int d = 0; d < kFaHd / 32; ++d) o[d] = f32x16{};
   float m = -INFINITY, l = 0.0f;
 
-  if (nchunks > 0) {
-    load_chunk(0);
+  // this workgroup's chunks: all of the tile's, or split blockIdx.z's split_keys keys
+  int c0 = 0, c1 = nchunks;
+  if constexpr (SPLIT) {
+    c0 = (int)blockIdx.z * (split_keys / kFaBk);
+    c1 = min(c1, c0 + split_keys / kFaBk);
+  }
+  if (c0 < c1) {
+    load_chunk(c0);
     store_chunk(lds);
   }
   __syncthreads();
-  for (int c = 0; c < nchunks; ++c) {
-    const uint8_t* buf = lds + (c & 1) * kFaStage;
-    if (c + 1 < nchunks) load_chunk(c + 1);  // in flight during this chunk
+  for (int c = c0; c < c1; ++c) {
+    const uint8_t* buf = lds + ((c - c0) & 1) * kFaStage;
+    if (c + 1 < c1) load_chunk(c + 1);  // in flight during this chunk
     // S^T = K . Q^T for keys [32 kt, 32 kt + 32)
     f32x16 st[2];
 #pragma unroll
@@ -308,12 +314,28 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
           const v8 a = __builtin_bit_cast(v8, u32x4{lo[0], lo[1], hi[0], hi[1]});
           o[d] = M::mma(a, pb[kt][u], o[d]);
         }
-    if (c + 1 < nchunks) store_chunk(lds + ((c + 1) & 1) * kFaStage);
+    if (c + 1 < c1) store_chunk(lds + ((c + 1 - c0) & 1) * kFaStage);
     __syncthreads();
   }
 
   // O^T layout: lane column = query, dims 32 d + 8 (j/4) + 4 half + j%4
-  if (q_ok) {
+  if constexpr (SPLIT) {  // unnormalised partial O, running max (exp2 units) and sum
+    if (q_ok) {
+      const int64_t pi = (tq * q_heads + h) * gridDim.z + blockIdx.z;
+      float* po = part + pi * kFaHd;
+#pragma unroll
+      for (int d = 0; d < kFaHd / 32; ++d)
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+          st16(po + 32 * d + 8 * g + 4 * half,
+               __builtin_bit_cast(u32x4, f32x4{o[d][4 * g], o[d][4 * g + 1], o[d][4 * g + 2], o[d][4 * g + 3]}));
+      if (half == 0) {
+        float* pml = part + tokens * q_heads * gridDim.z * kFaHd + 2 * pi;
+        pml[0] = m;
+        pml[1] = l;
+      }
+    }
+  } else if (q_ok) {
     const float inv = l > 0.0f ? 1.0f / l : 0.0f;
     T* orow = out + (tq * q_heads + h) * kFaHd;
 #pragma unroll
@@ -349,11 +371,12 @@ constexpr int kF32KBytes = kF32Bk * kF32KRow;
 constexpr int kF32Stage = kF32KBytes + kF32Bk * kF32VRow;
 constexpr int kF32Lds = 2 * kF32Stage;           // 66560 B: two workgroups per CU
 
+template <bool SPLIT>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void fa_prefill_f32_kernel(
     const float* __restrict__ q, float* __restrict__ out, const float* __restrict__ kc, const float* __restrict__ vc,
     const int32_t* __restrict__ qseq, const int32_t* __restrict__ qlen, const int32_t* __restrict__ tables,
     int64_t tokens, int q_heads, int kv_heads, int bs, int max_blocks, float scale_log2, int64_t q_stride,
-    int64_t tiles) {
+    int64_t tiles, int split_keys, float* __restrict__ part) {
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
@@ -422,14 +445,20 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
   for (int d = 0; d < 4; ++d) o[d] = f32x16{};
   float m = -INFINITY, l = 0.0f;
 
-  if (nchunks > 0) {
-    load_chunk(0);
+  // this workgroup's chunks: all of the tile's, or split blockIdx.z's split_keys keys
+  int c0 = 0, c1 = nchunks;
+  if constexpr (SPLIT) {
+    c0 = (int)blockIdx.z * (split_keys / kF32Bk);
+    c1 = min(c1, c0 + split_keys / kF32Bk);
+  }
+  if (c0 < c1) {
+    load_chunk(c0);
     store_chunk(lds);
   }
   __syncthreads();
-  for (int c = 0; c < nchunks; ++c) {
-    const uint8_t* buf = lds + (c & 1) * kF32Stage;
-    if (c + 1 < nchunks) load_chunk(c + 1);  // in flight during this chunk
+  for (int c = c0; c < c1; ++c) {
+    const uint8_t* buf = lds + ((c - c0) & 1) * kF32Stage;
+    if (c + 1 < c1) load_chunk(c + 1);  // in flight during this chunk
     // S^T: lane row (key) lane & 31 of the chunk, dims 64 half + ...
     f32x16 st = f32x16{};
     const uint8_t* krow = buf + (lane & 31) * kF32KRow + 256 * half;
@@ -482,12 +511,27 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
 #pragma unroll
       for (int d = 0; d < 4; ++d) o[d] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[d], st[s], o[d], 0, 0, 0);
     }
-    if (c + 1 < nchunks) store_chunk(lds + ((c + 1) & 1) * kF32Stage);
+    if (c + 1 < c1) store_chunk(lds + ((c + 1 - c0) & 1) * kF32Stage);
     __syncthreads();
   }
 
   // O^T: lane column = query; register j of tile d is dim 4 (8 (j/4) + 4 half + j%4) + d
-  if (q_ok) {
+  if constexpr (SPLIT) {  // unnormalised partial O, running max (exp2 units) and sum
+    if (q_ok) {
+      const int64_t pi = (tq * q_heads + h) * gridDim.z + blockIdx.z;
+      float* po = part + pi * kFaHd;
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const int r = 8 * (j >> 2) + 4 * half + (j & 3);
+        st16(po + 4 * r, __builtin_bit_cast(u32x4, f32x4{o[0][j], o[1][j], o[2][j], o[3][j]}));
+      }
+      if (half == 0) {
+        float* pml = part + tokens * q_heads * gridDim.z * kFaHd + 2 * pi;
+        pml[0] = m;
+        pml[1] = l;
+      }
+    }
+  } else if (q_ok) {
     const float inv = l > 0.0f ? 1.0f / l : 0.0f;
     float* orow = out + (tq * q_heads + h) * kFaHd;
 #pragma unroll
@@ -935,8 +979,10 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_wave_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// Split decode (few (token, kv head) pairs, long contexts): the decode kernels run
-// with blockIdx.z = split, each over split_keys keys, writing an unnormalised
+// Split attention (too little work to fill the GPU: few (token, kv head) pairs or
+// few tiles, long contexts): the tile and decode kernels run with blockIdx.z =
+// split, each over split_keys keys; every token is written by exactly one of them,
+// as an unnormalised
 // partial O (fp32, [token][q head][split][128]) and its running max (exp2 units)
 // and sum ([token][q head][split][2], after the O block); this kernel merges them:
 // out = sum_z 2^(m_z - M) O_z / sum_z 2^(m_z - M) l_z, M = max_z m_z.  One
@@ -944,15 +990,14 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_wave_kernel(
 // and meet in LDS.
 template <typename T>
 __global__ __launch_bounds__(256) void attn_split_combine_kernel(const float* __restrict__ part, T* __restrict__ out,
-                                                                 const int32_t* __restrict__ qseq, int64_t tokens,
-                                                                 int q_heads, int nsplit, bool skip_uniform_tiles) {
+                                                                 int64_t tokens,
+                                                                 int q_heads, int nsplit) {
   __shared__ float red[4][2 * 64 + 1];
   __shared__ float wmax[4];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   const int64_t t = blockIdx.x;
   const int h = (int)blockIdx.y;
-  if (skip_uniform_tiles && fa_tile_uniform(qseq, tokens, t / kFaBq)) return;  // the tiles' tokens (whole workgroup)
   const int64_t p0 = (t * q_heads + h) * nsplit;
   const float* pml = part + tokens * q_heads * nsplit * kFaHd + 2 * p0;
   float mx = -INFINITY;
@@ -993,23 +1038,39 @@ __global__ __launch_bounds__(256) void attn_split_combine_kernel(const float* __
   }
 }
 
-// How a decode launch is split: only when its (token, kv head) waves cannot fill
-// the GPU; then into enough key ranges (multiples of 64 keys) for
-// about kSplitTargetWaves waves.  The context bound is the block table's width.
+// How an attention call is split: only when its work cannot fill the GPU --
+// fewer than 512 tiles (one round of resident tile workgroups) when tiles run,
+// else fewer than 1024 (token, kv head) decode waves -- and the context is long;
+// then into key ranges (multiples of 64 keys; at least 512 keys per range for
+// tiles) for about 1024 tile workgroups or 512 decode waves.  The context bound is
+// the block table's width.
 constexpr int64_t kSplitMinWaves = 1024;
 constexpr int64_t kSplitTargetWaves = 512;  // a decode wave keeps ~32 KB in flight: 512 cover HBM
 constexpr int64_t kSplitMinKeys = 64;
+constexpr int64_t kSplitMinTiles = 512;
+constexpr int64_t kSplitTargetTiles = 1024;
+constexpr int64_t kSplitMinTileKeys = 512;
 struct SplitPlan {
   int nsplit = 1;
   int keys = 0;
 };
-inline SplitPlan split_plan(int64_t tokens, int q_heads, int kv_heads, int hd, int bs, int max_blocks) {
+inline bool attn_tiles(int64_t tokens, int64_t max_query_len) { return max_query_len != 1 && tokens >= kFaBq; }
+inline SplitPlan split_plan(int64_t tokens, int q_heads, int kv_heads, int hd, int bs, int max_blocks,
+                            int64_t max_query_len) {
   SplitPlan p;
-  const int64_t waves = tokens * kv_heads;
   const int64_t ctx = (int64_t)bs * max_blocks;
-  if (hd != kFaHd || q_heads / kv_heads > 16 || bs % 64 != 0 || waves >= kSplitMinWaves || ctx < 2 * kSplitMinKeys)
-    return p;
-  int64_t n = std::min<int64_t>((kSplitTargetWaves + waves - 1) / waves, ctx / kSplitMinKeys);
+  if (hd != kFaHd || q_heads / kv_heads > 16 || bs % 64 != 0) return p;
+  int64_t n;
+  if (attn_tiles(tokens, max_query_len)) {
+    const int64_t wgs = (tokens + kFaBq - 1) / kFaBq * q_heads;
+    if (wgs >= kSplitMinTiles) return p;
+    n = std::min<int64_t>((kSplitTargetTiles + wgs - 1) / wgs, ctx / kSplitMinTileKeys);
+  } else {
+    const int64_t waves = tokens * kv_heads;
+    if (waves >= kSplitMinWaves) return p;
+    n = std::min<int64_t>((kSplitTargetWaves + waves - 1) / waves, ctx / kSplitMinKeys);
+  }
+  if (n <= 1) return p;
   int64_t keys = ((ctx + n - 1) / n + 63) / 64 * 64;
   n = (ctx + keys - 1) / keys;
   if (n <= 1 || n > 65535 || keys > INT32_MAX) return p;
@@ -1046,36 +1107,72 @@ int attention_dispatch(const void* q, void* out, const void* kc, const void* vc,
                        int bs, int max_blocks, float scale, int64_t q_stride, int64_t max_query_len, void* ws,
                        int64_t ws_bytes, hipStream_t st) {
   constexpr int N = Pack<T>::N;
-  // a decode split needs the caller's workspace (none: unsplit)
-  const SplitPlan sp = split_plan(tokens, q_heads, kv_heads, hd, bs, max_blocks);
-  const bool split = sp.nsplit > 1 && ws != nullptr && ws_bytes >= split_bytes(tokens, q_heads, sp);
-  // matrix-core paths: 16-bit, head_dim 128, 64-key chunks inside one block, 16-byte rows, <= 16 heads per kv head
-  bool mfma = false;
-  if constexpr (sizeof(T) == 2) {
-    // (scale > 0: the kernels take the running max on unscaled scores)
-    mfma = hd == kFaHd && bs % kFaBk == 0 && q_heads / kv_heads <= 16 && aligned16(q) && aligned16(out) &&
-           aligned16(kc) && aligned16(vc) && q_stride % N == 0 && scale > 0.0f;
+  if (tokens > INT32_MAX) return fail(NVF_ERR_INVALID, "paged_attention: too many tokens");
+  const float sl = scale * 1.4426950408889634f;
+  const int64_t ntiles = (tokens + kFaBq - 1) / kFaBq;
+  if (ntiles * q_heads > INT32_MAX) return fail(NVF_ERR_INVALID, "paged_attention: too many tiles");
+  const unsigned kvg = (unsigned)((kv_heads + 3) / 4);
+  // Matrix-core paths (head_dim 128, 16-byte rows, scale > 0: the kernels take the
+  // running max on unscaled scores).  Tiles: 128 tokens of one sequence, unless the
+  // caller promised a decode batch (max_query_len 1) or there are fewer tokens
+  // than one tile; the decode kernel takes every other token.  A split (the
+  // caller's workspace) runs both over key ranges and merges.
+  const bool base = hd == kFaHd && aligned16(q) && aligned16(out) && aligned16(kc) && aligned16(vc) &&
+                    q_stride % N == 0 && scale > 0.0f;
+  const bool dec = base && q_heads / kv_heads <= 16 && bs % (sizeof(T) == 2 ? kFaBk : kFd32Bk) == 0;
+  const bool tiles = base && attn_tiles(tokens, max_query_len) && bs % (sizeof(T) == 2 ? kFaBk : kF32Bk) == 0 &&
+                     (sizeof(T) == 4 || dec);
+  const SplitPlan sp = split_plan(tokens, q_heads, kv_heads, hd, bs, max_blocks, max_query_len);
+  const bool split = dec && sp.nsplit > 1 && ws != nullptr && ws_bytes >= split_bytes(tokens, q_heads, sp);
+  const unsigned nz = split ? (unsigned)sp.nsplit : 1u;
+  const int skeys = split ? sp.keys : 0;
+  float* part = split ? static_cast<float*>(ws) : nullptr;
+  const T* qt = static_cast<const T*>(q);
+  T* ot = static_cast<T*>(out);
+  const T* kt = static_cast<const T*>(kc);
+  const T* vt = static_cast<const T*>(vc);
+  if (tiles) {
+    if constexpr (sizeof(T) == 2) {
+      static std::once_flag attr_once;
+      std::call_once(attr_once, [] {
+        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&fa_prefill_kernel<T, false>),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, kFaLds);
+        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&fa_prefill_kernel<T, true>),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, kFaLds);
+      });
+      const dim3 grid((unsigned)(ntiles * q_heads), 1, nz);
+      if (split)
+        fa_prefill_kernel<T, true><<<grid, 256, kFaLds, st>>>(qt, ot, kt, vt, qseq, qlen, tables, tokens, q_heads,
+                                                              kv_heads, bs, max_blocks, sl, q_stride, ntiles, skeys,
+                                                              part);
+      else
+        fa_prefill_kernel<T, false><<<grid, 256, kFaLds, st>>>(qt, ot, kt, vt, qseq, qlen, tables, tokens, q_heads,
+                                                               kv_heads, bs, max_blocks, sl, q_stride, ntiles, 0,
+                                                               nullptr);
+    } else {
+      static std::once_flag f32_once;
+      std::call_once(f32_once, [] {
+        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&fa_prefill_f32_kernel<false>),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, kF32Lds);
+        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&fa_prefill_f32_kernel<true>),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, kF32Lds);
+      });
+      const dim3 grid((unsigned)(ntiles * q_heads), 1, nz);
+      if (split)
+        fa_prefill_f32_kernel<true><<<grid, 256, kF32Lds, st>>>(qt, ot, kt, vt, qseq, qlen, tables, tokens, q_heads,
+                                                                kv_heads, bs, max_blocks, sl, q_stride, ntiles, skeys,
+                                                                part);
+      else
+        fa_prefill_f32_kernel<false><<<grid, 256, kF32Lds, st>>>(qt, ot, kt, vt, qseq, qlen, tables, tokens,
+                                                                 q_heads, kv_heads, bs, max_blocks, sl, q_stride,
+                                                                 ntiles, 0, nullptr);
+    }
+    const int rc = launch_status("paged_attention(tiles)");
+    if (rc != NVF_OK) return rc;
   }
-  if constexpr (sizeof(T) == 2) {
-    if (mfma) {
-      const float sl = scale * 1.4426950408889634f;
-      // tiles: not for a promised decode batch (max_query_len 1: no tile can be uniform)
-      // nor for fewer tokens than one tile (a short batch goes to the decode kernel)
-      const bool tiles = max_query_len != 1 && tokens >= kFaBq;
-      if (tiles) {
-        static std::once_flag attr_once;
-        std::call_once(attr_once, [] {
-          (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&fa_prefill_kernel<T>),
-                                    hipFuncAttributeMaxDynamicSharedMemorySize, kFaLds);
-        });
-        const int64_t ntiles = (tokens + kFaBq - 1) / kFaBq;
-        if (ntiles * q_heads > INT32_MAX) return fail(NVF_ERR_INVALID, "paged_attention: too many tiles");
-        fa_prefill_kernel<T><<<dim3((unsigned)(ntiles * q_heads)), 256, kFaLds, st>>>(
-            static_cast<const T*>(q), static_cast<T*>(out), static_cast<const T*>(kc), static_cast<const T*>(vc),
-            qseq, qlen, tables, tokens, q_heads, kv_heads, bs, max_blocks, sl, q_stride, ntiles);
-        const int rc = launch_status("paged_attention(tiles)");
-        if (rc != NVF_OK) return rc;
-      }
+  if (dec) {
+    const dim3 grid((unsigned)tokens, kvg, nz);
+    if constexpr (sizeof(T) == 2) {
       static std::once_flag dec_once;
       std::call_once(dec_once, [] {
         (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&fa_decode_kernel<T, false>),
@@ -1083,74 +1180,33 @@ int attention_dispatch(const void* q, void* out, const void* kc, const void* vc,
         (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&fa_decode_kernel<T, true>),
                                   hipFuncAttributeMaxDynamicSharedMemorySize, kFdLds);
       });
-      if (tokens > INT32_MAX) return fail(NVF_ERR_INVALID, "paged_attention: too many tokens");
-      const unsigned kvg = (unsigned)((kv_heads + 3) / 4);
-      if (split) {
-        fa_decode_kernel<T, true><<<dim3((unsigned)tokens, kvg, (unsigned)sp.nsplit), 256, kFdLds, st>>>(
-            static_cast<const T*>(q), static_cast<T*>(out), static_cast<const T*>(kc), static_cast<const T*>(vc),
-            qseq, qlen, tables, tokens, q_heads, kv_heads, bs, max_blocks, sl, q_stride, tiles, sp.keys,
-            static_cast<float*>(ws));
-        const int rc = launch_status("paged_attention(split decode)");
-        if (rc != NVF_OK) return rc;
-        attn_split_combine_kernel<T><<<dim3((unsigned)tokens, (unsigned)q_heads), 256, 0, st>>>(
-            static_cast<const float*>(ws), static_cast<T*>(out), qseq, tokens, q_heads, sp.nsplit, tiles);
-        return launch_status("paged_attention(split combine)");
-      }
-      fa_decode_kernel<T, false><<<dim3((unsigned)tokens, kvg), 256, kFdLds, st>>>(
-          static_cast<const T*>(q), static_cast<T*>(out), static_cast<const T*>(kc), static_cast<const T*>(vc), qseq,
-          qlen, tables, tokens, q_heads, kv_heads, bs, max_blocks, sl, q_stride, tiles, 0, nullptr);
-      return launch_status("paged_attention(decode)");
+      if (split)
+        fa_decode_kernel<T, true><<<grid, 256, kFdLds, st>>>(qt, ot, kt, vt, qseq, qlen, tables, tokens, q_heads,
+                                                             kv_heads, bs, max_blocks, sl, q_stride, tiles, skeys,
+                                                             part);
+      else
+        fa_decode_kernel<T, false><<<grid, 256, kFdLds, st>>>(qt, ot, kt, vt, qseq, qlen, tables, tokens, q_heads,
+                                                              kv_heads, bs, max_blocks, sl, q_stride, tiles, 0,
+                                                              nullptr);
+    } else {
+      if (split)
+        fa_decode_f32_kernel<true><<<grid, 256, 0, st>>>(qt, ot, kt, vt, qseq, qlen, tables, tokens, q_heads,
+                                                         kv_heads, bs, max_blocks, sl, q_stride, tiles, skeys, part);
+      else
+        fa_decode_f32_kernel<false><<<grid, 256, 0, st>>>(qt, ot, kt, vt, qseq, qlen, tables, tokens, q_heads,
+                                                          kv_heads, bs, max_blocks, sl, q_stride, tiles, 0, nullptr);
     }
+    int rc = launch_status("paged_attention(decode)");
+    if (rc != NVF_OK || !split) return rc;
+    attn_split_combine_kernel<T><<<dim3((unsigned)tokens, (unsigned)q_heads), 256, 0, st>>>(part, ot, tokens,
+                                                                                            q_heads, sp.nsplit);
+    return launch_status("paged_attention(split merge)");
   }
+  // everything else (other head sizes, block sizes or head groups, scale <= 0),
+  // leaving the fp32 tiles' tokens alone
   const bool vec = hd % N == 0 && aligned16(kc) && ((int64_t)kv_heads * hd) % N == 0;
-  const int dpl = (hd + 63) / 64;
-  bool skip = false;  // the wave kernel leaves the matrix-core tiles' tokens alone
-  if constexpr (sizeof(T) == 4) {
-    // fp32 matrix cores: head_dim 128, 16-byte rows, scale > 0; tiles need 32-key
-    // chunks inside one block, the decode kernel 16-key chunks and <= 16 heads per kv head
-    const bool base = hd == kFaHd && aligned16(q) && aligned16(out) && aligned16(kc) && aligned16(vc) &&
-                      q_stride % N == 0 && scale > 0.0f;
-    const bool tiles = base && bs % kF32Bk == 0 && max_query_len != 1 && tokens >= kFaBq;
-    const bool dec = base && bs % kFd32Bk == 0 && q_heads / kv_heads <= 16;
-    if (tiles) {
-      static std::once_flag f32_once;
-      std::call_once(f32_once, [] {
-        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&fa_prefill_f32_kernel),
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, kF32Lds);
-      });
-      const int64_t ntiles = (tokens + kFaBq - 1) / kFaBq;
-      if (ntiles * q_heads > INT32_MAX) return fail(NVF_ERR_INVALID, "paged_attention: too many tiles");
-      fa_prefill_f32_kernel<<<dim3((unsigned)(ntiles * q_heads)), 256, kF32Lds, st>>>(
-          static_cast<const float*>(q), static_cast<float*>(out), static_cast<const float*>(kc),
-          static_cast<const float*>(vc), qseq, qlen, tables, tokens, q_heads, kv_heads, bs, max_blocks,
-          scale * 1.4426950408889634f, q_stride, ntiles);
-      const int rc = launch_status("paged_attention(f32 tiles)");
-      if (rc != NVF_OK) return rc;
-      skip = true;
-    }
-    if (dec) {
-      if (tokens > INT32_MAX) return fail(NVF_ERR_INVALID, "paged_attention: too many tokens");
-      const unsigned kvg = (unsigned)((kv_heads + 3) / 4);
-      const float sl = scale * 1.4426950408889634f;
-      if (split) {
-        fa_decode_f32_kernel<true><<<dim3((unsigned)tokens, kvg, (unsigned)sp.nsplit), 256, 0, st>>>(
-            static_cast<const float*>(q), static_cast<float*>(out), static_cast<const float*>(kc),
-            static_cast<const float*>(vc), qseq, qlen, tables, tokens, q_heads, kv_heads, bs, max_blocks, sl,
-            q_stride, tiles, sp.keys, static_cast<float*>(ws));
-        const int rc = launch_status("paged_attention(f32 split decode)");
-        if (rc != NVF_OK) return rc;
-        attn_split_combine_kernel<float><<<dim3((unsigned)tokens, (unsigned)q_heads), 256, 0, st>>>(
-            static_cast<const float*>(ws), static_cast<float*>(out), qseq, tokens, q_heads, sp.nsplit, tiles);
-        return launch_status("paged_attention(f32 split combine)");
-      }
-      fa_decode_f32_kernel<false><<<dim3((unsigned)tokens, kvg), 256, 0, st>>>(
-          static_cast<const float*>(q), static_cast<float*>(out), static_cast<const float*>(kc),
-          static_cast<const float*>(vc), qseq, qlen, tables, tokens, q_heads, kv_heads, bs, max_blocks, sl,
-          q_stride, tiles, 0, nullptr);
-      return launch_status("paged_attention(f32 decode)");
-    }
-  }
-  switch (dpl) {
+  const bool skip = tiles;
+  switch ((hd + 63) / 64) {
     case 1: launch_attn_wave<T, 1>(q, out, kc, vc, qseq, qlen, tables, tokens, q_heads, kv_heads, hd, bs, max_blocks,
                                    scale, q_stride, vec, skip, st); break;
     case 2: launch_attn_wave<T, 2>(q, out, kc, vc, qseq, qlen, tables, tokens, q_heads, kv_heads, hd, bs, max_blocks,
@@ -1248,10 +1304,11 @@ int nvf_paged_attention(const void* q, void* out, const void* k_cache, const voi
 }
 
 int64_t nvf_paged_attention_workspace_size(int64_t tokens, int q_heads, int kv_heads, int head_dim, int block_size,
-                                           int max_blocks) {
+                                           int max_blocks, int64_t max_query_len) {
   if (tokens <= 0 || q_heads <= 0 || kv_heads <= 0 || block_size <= 0 || max_blocks <= 0 || q_heads % kv_heads)
     return 0;
-  return split_bytes(tokens, q_heads, split_plan(tokens, q_heads, kv_heads, head_dim, block_size, max_blocks));
+  return split_bytes(tokens, q_heads,
+                     split_plan(tokens, q_heads, kv_heads, head_dim, block_size, max_blocks, max_query_len));
 }
 
 // Drop-ins: include/nanovllm/hip_ops.hpp:22-28 / src/hip_ops.hip:724-744 (fp32 cache, null stream).
@@ -1280,7 +1337,8 @@ void hip_paged_attention(const float* q, float* out, const float* k_cache, const
                          int tokens, int q_heads, int kv_heads, int head_dim, int block_size, int max_blocks,
                          float scale) {
   if (tokens <= 0 || q_heads <= 0 || kv_heads <= 0) return;
-  const int64_t need = nvf_paged_attention_workspace_size(tokens, q_heads, kv_heads, head_dim, block_size, max_blocks);
+  const int64_t need =
+      nvf_paged_attention_workspace_size(tokens, q_heads, kv_heads, head_dim, block_size, max_blocks, 0);
   if (need > 0) {
     int dev = 0;
     dropin_check(hipGetDevice(&dev) == hipSuccess ? NVF_OK : fail(NVF_ERR_LAUNCH, "hipGetDevice failed"),

@@ -45,7 +45,7 @@ SIGNATURES: dict[str, tuple] = {
                                    _i64, _i32, _vp]),
     "nvf_paged_attention_ws": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i32, _i32, _i32, _i32, _i32, _f32,
                                       _i64, _i64, _vp, _i64, _i32, _vp]),
-    "nvf_paged_attention_workspace_size": (_i64, [_i64, _i32, _i32, _i32, _i32, _i32]),
+    "nvf_paged_attention_workspace_size": (_i64, [_i64, _i32, _i32, _i32, _i32, _i32, _i64]),
     "nvf_q8_quantize_rows": (_i32, [_vp, _vp, _vp, _i64, _i64, _i32, _vp]),
     "nvf_matmul_q8_0": (_i32, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _i32, _vp]),
     "nvf_rms_norm_add": (_i32, [_vp, _vp, _vp, _vp, _i64, _i64, _f32, _i32, _vp]),
@@ -238,15 +238,15 @@ def paged_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tenso
     """q [tokens, q_heads, head_dim] (row stride from the tensor); caches
     [rows, kv_heads, head_dim]; block_tables [seqs, max_blocks] int32.
     max_query_len = 1 promises a decode batch (one query per sequence).  split:
-    give the library the workspace for split decode when the shape calls for it
-    (small batches over long contexts); False runs unsplit.
+    give the library the workspace for split attention when the shape calls for
+    it (little work over long contexts); False runs unsplit.
     Returns out [tokens, q_heads, head_dim] in q's dtype."""
     tokens, q_heads, head_dim = q.shape
     kv_heads = k_cache.shape[1]
     max_blocks = block_tables.shape[1]
     out = torch.empty((tokens, q_heads, head_dim), dtype=q.dtype, device=q.device) if out is None else out
     ws_bytes = lib().nvf_paged_attention_workspace_size(tokens, q_heads, kv_heads, head_dim, block_size,
-                                                       max_blocks) if split else 0
+                                                       max_blocks, max_query_len) if split else 0
     ws = torch.empty((ws_bytes + 15) // 16 * 4, dtype=torch.float32, device=q.device) if ws_bytes > 0 else None
     _check(lib().nvf_paged_attention_ws(_dev_rows(q, "q"), _dev(out, "out"), _dev(k_cache, "k_cache"),
                                         _dev(v_cache, "v_cache"), _dev(query_seq, "query_seq"),

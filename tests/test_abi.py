@@ -60,10 +60,10 @@ def test_host_argument_checks():
     assert rc == -1 and "kind" in msg
     rc, msg = _status(lib.nvf_embedding_qk(p, p, 4, 256, 0, 12, 5, p, 1, None))
     assert rc == -1 and "layout" in msg
-    assert lib.nvf_paged_attention_workspace_size(1, 28, 4, 128, 256, 16) > 0     # one long-context decode: split
-    assert lib.nvf_paged_attention_workspace_size(256, 28, 4, 128, 256, 16) == 0  # enough (token, kv head) pairs
-    assert lib.nvf_paged_attention_workspace_size(1, 28, 4, 64, 256, 16) == 0     # not a matrix-core shape
-    assert lib.nvf_paged_attention_workspace_size(1, 28, 3, 128, 256, 16) == 0    # bad heads: 0, no error
+    assert lib.nvf_paged_attention_workspace_size(1, 28, 4, 128, 256, 16, 1) > 0     # one long-context decode: split
+    assert lib.nvf_paged_attention_workspace_size(256, 28, 4, 128, 256, 16, 1) == 0  # enough (token, kv head) pairs
+    assert lib.nvf_paged_attention_workspace_size(1, 28, 4, 64, 256, 16, 1) == 0     # not a matrix-core shape
+    assert lib.nvf_paged_attention_workspace_size(1, 28, 3, 128, 256, 16, 1) == 0    # bad heads: 0, no error
     rc, msg = _status(lib.nvf_paged_attention_ws(p, p, p, p, p, p, p, 1, 28, 4, 128, 256, 16, 0.1, 3584, 1,
                                                  p + 4, 1 << 20, 1, None))
     assert rc == -1 and "workspace" in msg

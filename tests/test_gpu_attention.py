@@ -277,7 +277,7 @@ def test_paged_attention_split_decode(gpu, dt, ci):
     b = H.make_paged(r, ctx, [1] * len(ctx), qh, kvh, 128, 256, dt)
     if len(ctx) > 2:
         b.query_key_len[1] = 0
-    assert ops.lib().nvf_paged_attention_workspace_size(b.tokens, qh, kvh, 128, 256, b.max_blocks) > 0
+    assert ops.lib().nvf_paged_attention_workspace_size(b.tokens, qh, kvh, 128, 256, b.max_blocks, 1) > 0
     scale = 128 ** -0.5
     _, exact, vmax = H.oracle_attention(b, qh, kvh, 128, 256, scale, dt)
     args = (H.to_dev(b.q, gpu, dt), H.to_dev(b.k_cache, gpu, dt), H.to_dev(b.v_cache, gpu, dt),
@@ -309,3 +309,30 @@ def test_dropin_split_decode_grows_its_workspace(gpu):
                                       dql.data_ptr(), dtab.data_ptr(), b.tokens, 28, 4, 128, 256, b.max_blocks, scale)
         torch.cuda.synchronize()
         assert_attn(out.cpu().numpy(), exact, vmax, H.F32, "split drop-in")
+
+
+TILE_SPLIT_CASES = [
+    # (context lengths, query counts): few 128-token tiles over long contexts
+    ([8192], [256]),                 # a 256-token chunk after a 7936-token prefix
+    ([4000, 3000], [200, 60]),       # uniform tiles (split tiles) and a mixed tile (split decode) together
+    ([2048, 5], [300, 5]),
+]
+
+
+@pytest.mark.parametrize("dt", DTYPES, ids=DT_IDS)
+@pytest.mark.parametrize("ci", range(len(TILE_SPLIT_CASES)))
+def test_paged_attention_split_tiles(gpu, dt, ci):
+    """Chunked prefill with few tiles over long contexts takes the split path for
+    the tiles (and for the decode kernel's mixed-tile tokens), merged once."""
+    ctx, ql = TILE_SPLIT_CASES[ci]
+    r = H.rng(600 + ci * 3 + dt)
+    b = H.make_paged(r, ctx, ql, 8, 2, 128, 256, dt)
+    assert ops.lib().nvf_paged_attention_workspace_size(b.tokens, 8, 2, 128, 256, b.max_blocks, 0) > 0
+    scale = 128 ** -0.5
+    _, exact, vmax = H.oracle_attention(b, 8, 2, 128, 256, scale, dt)
+    args = (H.to_dev(b.q, gpu, dt), H.to_dev(b.k_cache, gpu, dt), H.to_dev(b.v_cache, gpu, dt),
+            H.to_dev(b.query_seq, gpu), H.to_dev(b.query_key_len, gpu), H.to_dev(b.block_tables, gpu), 256, scale)
+    case(f"paged_attention split tiles case={ci} dt={dt}")
+    assert_attn(H.to_host(ops.paged_attention(*args)), exact, vmax, dt, "split tiles")
+    case(f"paged_attention unsplit tiles case={ci} dt={dt}")
+    assert_attn(H.to_host(ops.paged_attention(*args, split=False)), exact, vmax, dt, "unsplit tiles")
