@@ -58,7 +58,7 @@ def parse() -> argparse.Namespace:
                    help="embedding table format (default: the config's)")
     p.add_argument("--only", default="",
                    help="comma list of ops (default emb,rms,rope,silu,copy,gemm,gemv,split,attn,attn_decode,attn_f32,"
-                        "attn_decode_f32,attn_decode_small,layer); "
+                        "attn_decode_f32,attn_decode_small,layer,layer_decode); "
                         "also emb_rms, rms_q8, silu_q8 (fusions)")
     return p.parse_args()
 
@@ -111,7 +111,7 @@ def main() -> int:
     emb_fmt = args.emb or cfg.emb
     nbytes = op_bytes(cfg, e, emb_fmt)
     only = set(filter(None, args.only.split(","))) or {"emb", "rms", "rope", "silu", "copy", "gemm", "gemv", "split",
-                                                       "attn", "attn_decode", "attn_f32", "attn_decode_f32", "attn_decode_small", "layer"}
+                                                       "attn", "attn_decode", "attn_f32", "attn_decode_f32", "attn_decode_small", "layer", "layer_decode"}
 
     def nsets(b: int) -> int:
         return max(2, -(-POOL_BYTES // b))
@@ -221,38 +221,56 @@ def main() -> int:
                       torch.full((sB,), sctx, dtype=torch.int32, device=dev), stab.to(dev))
         small_bytes = float(sB * sctx) * cfg.kv_heads * cfg.head_dim * 2 * e
     layer = None
-    if "layer" in only:  # one whole decoder layer on this library's kernels (Q8_0 weights, random init)
-        lpos = cfg.positions()
-        llens = [int(n) for n in np.diff(cfg.cu_seqlens())]
-        lnb = [-(-n // bs_kv) for n in llens]
-        ltab = np.full((len(llens), max(lnb)), -1, np.int32)
-        lperm = np.random.default_rng(cfg.seed + 5).permutation(sum(lnb)).astype(np.int32)
-        o_ = 0
-        for s_, nb in enumerate(lnb):
-            ltab[s_, :nb] = lperm[o_:o_ + nb]
-            o_ += nb
-        lseq = np.repeat(np.arange(len(llens), dtype=np.int32), llens)
-        lslots = (ltab[lseq, lpos // bs_kv].astype(np.int64) * bs_kv + lpos % bs_kv).astype(np.int32)
-        lrows = sum(lnb) * bs_kv
+    layer_dec = None
+    if {"layer", "layer_decode"} & only:  # one whole decoder layer on this library's kernels
 
-        def q8w(n_, k_, lo=1e-3, hi=1e-2):
+        def q8w(n_, k_, lo=1e-3, hi=1e-2):  # random Q8_0 weight planes
             return (torch.randint(-127, 128, (n_ * k_,), generator=g, device=dev, dtype=torch.int8),
                     torch.empty(n_ * k_ // 32, device=dev).uniform_(lo, hi, generator=g).half().view(torch.int16))
-        layer = {
-            "h": randn((T, Hd)), "r": randn((T, Hd)), "w_in": randn((Hd,), 1.0, 0.1), "w_post": randn((Hd,), 1.0, 0.1),
-            # (o adds into r on every call: small scales keep r within fp16)
-            "qkv": q8w(qs + 2 * ks, Hd), "o": q8w(Hd, qs, 1e-5, 1e-4), "gu": q8w(2 * I, Hd), "down": q8w(Hd, I),
-            "kc": torch.zeros(lrows, cfg.kv_heads, cfg.head_dim, dtype=tdt, device=dev),
-            "vc": torch.zeros(lrows, cfg.kv_heads, cfg.head_dim, dtype=tdt, device=dev),
-            "qseq": torch.from_numpy(lseq).to(dev), "qlen": torch.from_numpy((lpos + 1).astype(np.int32)).to(dev),
-            "tab": torch.from_numpy(ltab).to(dev), "slots": torch.from_numpy(lslots).to(dev),
-            "qkv_out": torch.empty(T, qs + 2 * ks, dtype=tdt, device=dev),
-            "attn_out": torch.empty(T, cfg.q_heads, cfg.head_dim, dtype=tdt, device=dev),
-            "o_out": torch.empty(T, Hd, dtype=tdt, device=dev), "gu_out": torch.empty(T, 2 * I, dtype=tdt, device=dev),
-            "down_out": torch.empty(T, Hd, dtype=tdt, device=dev),
-        }
-        layer_ops = 2.0 * T * Hd * (qs + 2 * ks + 2 * I) + 2.0 * T * qs * Hd + 2.0 * T * I * Hd
-        layer_attn_flops = 4.0 * cfg.q_heads * cfg.head_dim * float((lpos + 1).sum())
+        lw = {"w_in": randn((Hd,), 1.0, 0.1), "w_post": randn((Hd,), 1.0, 0.1),
+              # (o adds into the residual on every call: small scales keep it within fp16)
+              "qkv": q8w(qs + 2 * ks, Hd), "o": q8w(Hd, qs, 1e-5, 1e-4), "gu": q8w(2 * I, Hd), "down": q8w(Hd, I)}
+
+        def build_layer(lpos, lseq, seq_ctx, mql, seed):
+            """Activations, a paged KV cache and metadata for tokens at positions lpos
+            of sequences lseq (sequence s holds seq_ctx[s] keys once they are stored)."""
+            n_ = len(lpos)
+            lnb = [-(-int(c) // bs_kv) for c in seq_ctx]
+            ltab = np.full((len(seq_ctx), max(lnb)), -1, np.int32)
+            lperm = np.random.default_rng(seed).permutation(sum(lnb)).astype(np.int32)
+            o_ = 0
+            for s_, nb in enumerate(lnb):
+                ltab[s_, :nb] = lperm[o_:o_ + nb]
+                o_ += nb
+            lslots = (ltab[lseq, lpos // bs_kv].astype(np.int64) * bs_kv + lpos % bs_kv).astype(np.int32)
+            lrows = sum(lnb) * bs_kv
+            return dict(lw, T=n_, mql=mql, h=randn((n_, Hd)), r=randn((n_, Hd)),
+                        pos=torch.from_numpy(lpos.astype(np.int64)).to(dev),
+                        kc=torch.zeros(lrows, cfg.kv_heads, cfg.head_dim, dtype=tdt, device=dev),
+                        vc=torch.zeros(lrows, cfg.kv_heads, cfg.head_dim, dtype=tdt, device=dev),
+                        qseq=torch.from_numpy(lseq.astype(np.int32)).to(dev),
+                        qlen=torch.from_numpy((lpos + 1).astype(np.int32)).to(dev),
+                        tab=torch.from_numpy(ltab).to(dev), slots=torch.from_numpy(lslots).to(dev),
+                        qkv_out=torch.empty(n_, qs + 2 * ks, dtype=tdt, device=dev),
+                        attn_out=torch.empty(n_, cfg.q_heads, cfg.head_dim, dtype=tdt, device=dev),
+                        o_out=torch.empty(n_, Hd, dtype=tdt, device=dev),
+                        gu_out=torch.empty(n_, 2 * I, dtype=tdt, device=dev),
+                        down_out=torch.empty(n_, Hd, dtype=tdt, device=dev))
+
+        def layer_flops(n_, lpos):
+            return (2.0 * n_ * Hd * (qs + 2 * ks + 2 * I) + 2.0 * n_ * qs * Hd + 2.0 * n_ * I * Hd,
+                    4.0 * cfg.q_heads * cfg.head_dim * float((lpos + 1).sum()))
+        if "layer" in only:  # the config's prefill
+            lpos = cfg.positions()
+            llens = [int(n) for n in np.diff(cfg.cu_seqlens())]
+            lseq = np.repeat(np.arange(len(llens), dtype=np.int32), llens)
+            layer = build_layer(lpos, lseq, llens, 0, cfg.seed + 5)
+            layer_ops, layer_attn_flops = layer_flops(T, lpos)
+        if "layer_decode" in only:  # a decode step: 256 sequences, one new token each, context U[1, 4096]
+            dctx = np.random.default_rng(cfg.seed + 7).integers(1, 4097, 256)
+            layer_dec = build_layer(dctx - 1, np.arange(256), dctx, 1, cfg.seed + 8)
+            dec_ops, dec_attn_flops = layer_flops(256, dctx - 1)
+            dec_kv_bytes = float(dctx.sum()) * cfg.kv_heads * cfg.head_dim * 2 * e
     # the same inputs as fp32 caches (the reference's KV dtype; the drop-in's path)
     f32ize = (lambda tup: tuple(x.float() if x.is_floating_point() else x for x in tup))
     attn_in32 = f32ize(attn_in) if "attn_f32" in only else None
@@ -336,26 +354,33 @@ def main() -> int:
 
     small_out = torch.empty_like(attn_small[0]) if attn_small is not None else None
 
-    def run_layer(i):
+    def run_layer_on(L_):
         # model.cpp:758-833's per-layer sequence, Qwen2.5 (no QK-norm): input RMSNorm (writing the
         # qkv GEMM's int8 rows), qkv, RoPE on the q and k columns of the packed row, KV store,
         # paged attention, o (quantize + GEMM), post-attention residual-add RMSNorm (int8 rows),
         # gate_up, SwiGLU (int8 rows), down
-        L_ = layer
+        n_ = L_["T"]
         _, sc, xq = ops.rms_norm_q8(L_["h"], L_["w_in"], cfg.eps, residual=L_["r"], want_out=False)
         qkv = ops.matmul_q8_0(xq, sc, *L_["qkv"], qs + 2 * ks, tdt, out=L_["qkv_out"])
-        ops.qk_norm_rope(qkv[:, :qs], qkv[:, qs:qs + ks], pos, None, None, inv, cfg.q_heads, cfg.kv_heads,
+        ops.qk_norm_rope(qkv[:, :qs], qkv[:, qs:qs + ks], L_["pos"], None, None, inv, cfg.q_heads, cfg.kv_heads,
                          cfg.head_dim, cfg.eps)
-        kv3 = (T, cfg.kv_heads, cfg.head_dim)
+        kv3 = (n_, cfg.kv_heads, cfg.head_dim)
         ops.store_kv(qkv[:, qs:qs + ks].view(kv3), qkv[:, qs + ks:].view(kv3), L_["kc"], L_["vc"], L_["slots"])
-        att = ops.paged_attention(qkv[:, :qs].view(T, cfg.q_heads, cfg.head_dim), L_["kc"], L_["vc"], L_["qseq"],
-                                  L_["qlen"], L_["tab"], bs_kv, cfg.head_dim ** -0.5, out=L_["attn_out"])
-        sc2, xq2 = ops.q8_quantize_rows(att.view(T, qs))
+        att = ops.paged_attention(qkv[:, :qs].view(n_, cfg.q_heads, cfg.head_dim), L_["kc"], L_["vc"], L_["qseq"],
+                                  L_["qlen"], L_["tab"], bs_kv, cfg.head_dim ** -0.5, out=L_["attn_out"],
+                                  max_query_len=L_["mql"])
+        sc2, xq2 = ops.q8_quantize_rows(att.view(n_, qs))
         o = ops.matmul_q8_0(xq2, sc2, *L_["o"], Hd, tdt, out=L_["o_out"])
         _, sc3, xq3 = ops.rms_norm_q8(o, L_["w_post"], cfg.eps, residual=L_["r"], want_out=False)
         gu = ops.matmul_q8_0(xq3, sc3, *L_["gu"], 2 * I, tdt, out=L_["gu_out"])
         _, sc4, xq4 = ops.silu_and_mul_q8(gu)
         ops.matmul_q8_0(xq4, sc4, *L_["down"], Hd, tdt, out=L_["down_out"])
+
+    def run_layer(i):
+        run_layer_on(layer)
+
+    def run_layer_decode(i):
+        run_layer_on(layer_dec)
 
     def run_attn_f32(i):
         q_, kc_, vc_, qs_, ql_, tb_ = attn_in32
@@ -377,7 +402,7 @@ def main() -> int:
              ("rms_q8", run_rms_q8), ("silu_q8", run_silu_q8), ("copy", run_copy), ("gemm", run_gemm),
              ("gemv", run_gemv), ("split", run_split), ("attn", run_attn), ("attn_decode", run_attn_decode),
              ("attn_f32", run_attn_f32), ("attn_decode_f32", run_attn_decode_f32), ("attn_decode_small", run_attn_decode_small),
-             ("layer", run_layer)]
+             ("layer", run_layer), ("layer_decode", run_layer_decode)]
     active = [(n, f) for n, f in table if n in only]
 
     for i in range(args.warmup):
@@ -444,6 +469,12 @@ def main() -> int:
                                    f"{cfg.head_dim} (split decode)", "bytes": int(small_bytes),
                           "GB_s": round(small_bytes / (t_us * 1e-6) / 1e9, 1),
                           "frac_of_peak": round(small_bytes / (t_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)})
+        elif n == "layer_decode":
+            entry.update({"shape": "one Qwen2.5-7B decoder layer, decode step of 256 sequences (context U[1, 4096]), "
+                                   "Q8_0 weights, fp16 activations and KV cache",
+                          "tokens_per_s": round(256 / (t_us * 1e-6), 1),
+                          "weights_and_kv_GB_s": round((dec_ops / 2 / 256 * 34 / 32 + dec_kv_bytes) / (t_us * 1e-6) / 1e9,
+                                                       1)})
         elif n == "layer":
             entry.update({"shape": f"one Qwen2.5-7B decoder layer, {T} tokens ({len(np.diff(cfg.cu_seqlens()))} "
                                    f"causal prefills), Q8_0 weights, fp16 activations and KV cache",
@@ -511,6 +542,7 @@ def main() -> int:
         "q8_gemv": res_ops.get("gemv"),
         "q8_0_split": res_ops.get("split"),
         "layer": res_ops.get("layer"),
+        "layer_decode": res_ops.get("layer_decode"),
         "paged_attention": {k: res_ops[k] for k in ("attn", "attn_decode", "attn_f32", "attn_decode_f32",
                                                     "attn_decode_small") if k in res_ops} or None,
         "cpu_baseline": cpu,

@@ -209,6 +209,20 @@ int nvf_q8_quantize_rows(const void* x, float* row_scale, int8_t* xq, int64_t ro
 int nvf_matmul_q8_0(const int8_t* xq, const float* row_scale, const uint8_t* w8, const uint16_t* ws, int64_t m,
                     int64_t n, int64_t k, void* out, int out_dtype, void* stream);
 
+/* nvf_matmul_q8_0 with a caller workspace for split-K (no counterpart in the
+ * reference; its hip_matmul_q8 tiles the output only): when the output has too
+ * few 128 x 128 tiles to fill the GPU (e.g. decode batches of a few hundred rows
+ * against 3584-wide outputs), K is cut into ranges whose fp32 partial sums are
+ * summed in order by a reduction.  workspace (16-byte aligned) of workspace_bytes
+ * >= nvf_matmul_q8_0_workspace_size(m, n, k) enables it; NULL or too small runs
+ * unsplit.  Same results within the fp32 summation bound. */
+int nvf_matmul_q8_0_ws(const int8_t* xq, const float* row_scale, const uint8_t* w8, const uint16_t* ws, int64_t m,
+                       int64_t n, int64_t k, void* out, int out_dtype, void* workspace, int64_t workspace_bytes,
+                       void* stream);
+
+/* Bytes of workspace nvf_matmul_q8_0_ws uses for this shape (0: it would not split). */
+int64_t nvf_matmul_q8_0_workspace_size(int64_t m, int64_t n, int64_t k);
+
 /* KV store (replaces hip_store_kv, hip_ops.hpp:22-23) with the cache in `dtype`;
  * key / value rows are key_stride / value_stride elements apart (>= kv_heads *
  * head_dim), so views into a packed qkv row work. */

@@ -26,6 +26,7 @@
 // application, not the MFMA, bounds this kernel (VALU : MFMA time is about 4:1).
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <mutex>
 #include <type_traits>
 
@@ -36,6 +37,7 @@ namespace nvf {
 
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef int i32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kGemmBM = 128;                 // output rows per workgroup
 constexpr int kGemmBN = 128;                 // output columns per workgroup
@@ -143,10 +145,11 @@ __device__ __forceinline__ void gemm_store_out(TO* p, float v) {
 //
 // One loop iteration per Q8_0 block; the first MFMA of block g + 1 is issued
 // while block g is applied, so each result is ready when its scale is applied.
-template <typename TO>
+template <typename TO, bool SPLIT>
 __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(3))) void q8_gemm_kernel(
     const int8_t* __restrict__ xq, const float* __restrict__ rscale, const int8_t* __restrict__ w8,
-    const uint16_t* __restrict__ ws, TO* __restrict__ out, int64_t m, int64_t n, int64_t k, int tiles_n) {
+    const uint16_t* __restrict__ ws, TO* __restrict__ out, int64_t m, int64_t n, int64_t k, int tiles_n,
+    int st_per_split, float* __restrict__ part) {
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   __shared__ float inv_row[kGemmBM];
 
@@ -210,9 +213,13 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(3)
   const uint32_t sc_off = (uint32_t)((sc_c * nblk + sc_b) * 2);
 
   const int nstages = (int)((k + kGemmKC - 1) / kGemmKC);
+  // this workgroup's K stages: all, or split blockIdx.y's st_per_split of them (every
+  // split is non-empty: the host sizes the split count so)
+  const int st0 = SPLIT ? (int)blockIdx.y * st_per_split : 0;
+  const int st1 = SPLIT ? min(nstages, st0 + st_per_split) : nstages;
   const bool partial_last = k % kGemmKC != 0;
   // Loads stage st into LDS buffer `buf`, all by DMA.
-  auto issue = [&](int st, int buf) {
+  auto issue = [&](int st, int buf) {  // st: absolute stage; buf: its double-buffer slot
     uint8_t* stage = lds + buf * kGemmStage;
     const uint32_t kc = (uint32_t)st * kGemmKC;
     uint8_t* sc_dst = stage + (kGemmBM + kGemmBN) * kGemmKC + wave * 256;  // this wave's 64 scale slots
@@ -283,9 +290,9 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(3)
     for (int j = 0; j < 16; ++j) c[j] = fmaf(sc, (float)d[j], c[j]);
   };
 
-  issue(0, 0);
+  issue(st0, 0);
   publish();
-  const int nb = nstages * kGemmBlk;
+  const int nb = (st1 - st0) * kGemmBlk;  // blocks g = 0 .. nb - 1 of this workgroup's stages
   read_frags(0);
   i32x16 d0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa0, fb0, i32x16{}, 0, 0, 0);
   // One iteration per Q8_0 block, 0 .. nb-2; the last block is peeled so that
@@ -297,7 +304,7 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(3)
   for (int g = 0; g < nb - 1; ++g) {
     const int bi = g % kGemmBlk;
     const int st = g / kGemmBlk;
-    if (bi == 0) issue(st + 1, (st + 1) & 1);  // uniform; g < nb - 1 implies a successor
+    if (bi == 0) issue(st0 + st + 1, (st + 1) & 1);  // uniform; g < nb - 1 implies a successor
     const i32x16 d1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa0, fb1, i32x16{}, 0, 0, 0);
     const i32x16 d2 = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa1, fb0, i32x16{}, 0, 0, 0);
     const i32x16 d3 = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa1, fb1, i32x16{}, 0, 0, 0);
@@ -336,6 +343,12 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(3)
       const int rl = wm * 64 + a * 32 + 8 * (j >> 2) + 4 * (lane >> 5) + (j & 3);
       const int64_t r = row0 + rl;
       if (r >= m) continue;
+      if constexpr (SPLIT) {  // fp32 partial sums of this split; the reduction scales
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+          if (col_ok[b]) part[((int64_t)blockIdx.y * m + r) * n + col[b]] = acc[a][b][j];
+        continue;
+      }
       const float inv = inv_row[rl];
 #pragma unroll
       for (int b = 0; b < 2; ++b)
@@ -514,6 +527,66 @@ bool try_gemv(const int8_t* xq, const float* rscale, const int8_t* w8, const uin
   return true;
 }
 
+// Split-K reduction: out[r][c] = (sum over splits, in order, of part[split][r][c]) /
+// row_scale[r] (0 where the scale is 0, as the tile kernel), in the output dtype.
+// Four consecutive columns per thread where the row allows.
+template <typename TO>
+__global__ __launch_bounds__(256) void q8_gemm_reduce_kernel(const float* __restrict__ part,
+                                                             const float* __restrict__ rscale, TO* __restrict__ out,
+                                                             int64_t m, int64_t n, int splits) {
+  const int64_t nq = (n + 3) / 4;
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= m * nq) return;
+  const int64_t r = i / nq, c0 = (i % nq) * 4;
+  const float s = rscale[r];
+  const float inv = s > 0.0f ? 1.0f / s : 0.0f;
+  const int64_t mn = m * n;
+  const float* p = part + r * n + c0;
+  if (n % 4 == 0) {  // 16-byte rows: one vector load per split
+    f32x4 acc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll 4
+    for (int z = 0; z < splits; ++z) acc += __builtin_bit_cast(f32x4, ld16(p + z * mn));
+#pragma unroll
+    for (int e = 0; e < 4; ++e) gemm_store_out(out + r * n + c0 + e, acc[e] * inv);
+    return;
+  }
+  for (int64_t c = 0; c < 4 && c0 + c < n; ++c) {
+    float acc = 0.0f;
+    for (int z = 0; z < splits; ++z) acc += p[z * mn + c];
+    gemm_store_out(out + r * n + c0 + c, acc * inv);
+  }
+}
+
+// Split-K plan for the tile GEMM: when the output has fewer than kGemmSplitBelow
+// tiles (half a round of the 768 resident workgroups), K is cut into ranges of
+// whole stages (at least 8) for about kGemmSplitTarget workgroups.  (At 592 tiles
+// the partial-sum traffic costs more than the idle CUs: measured.)
+constexpr int64_t kGemmSplitBelow = 384;
+constexpr int64_t kGemmSplitTarget = 768;
+constexpr int64_t kGemmSplitMinStages = 8;
+struct GemmSplit {
+  int splits = 1;
+  int st_per_split = 0;
+};
+inline GemmSplit gemm_split_plan(int64_t m, int64_t n, int64_t k) {
+  GemmSplit p;
+  if (m <= kGemvMaxM || k % 32 != 0 || k > ((int64_t)1 << 24)) return p;
+  const int64_t tiles = ((m + kGemmBM - 1) / kGemmBM) * ((n + kGemmBN - 1) / kGemmBN);
+  const int64_t nstages = (k + kGemmKC - 1) / kGemmKC;
+  if (tiles >= kGemmSplitBelow) return p;
+  int64_t s = std::min<int64_t>((kGemmSplitTarget + tiles - 1) / tiles, nstages / kGemmSplitMinStages);
+  if (s <= 1) return p;
+  const int64_t per = (nstages + s - 1) / s;
+  s = (nstages + per - 1) / per;  // every split non-empty
+  if (s <= 1 || s > 65535) return p;
+  p.splits = (int)s;
+  p.st_per_split = (int)per;
+  return p;
+}
+inline int64_t gemm_split_bytes(int64_t m, int64_t n, const GemmSplit& p) {
+  return p.splits > 1 ? p.splits * m * n * (int64_t)sizeof(float) : 0;
+}
+
 }  // namespace nvf
 
 using namespace nvf;
@@ -539,7 +612,7 @@ int check_gemm(const void* xq, const float* rscale, const void* w8, const void* 
 
 template <typename TO>
 int launch_gemm(const int8_t* xq, const float* rscale, const int8_t* w8, const uint16_t* ws, TO* out, int64_t m,
-                int64_t n, int64_t k, hipStream_t stream) {
+                int64_t n, int64_t k, void* work, int64_t work_bytes, hipStream_t stream) {
   if (m <= kGemvMaxM) {
     // fewest K splits that still give >= ~2048 waves (16 columns each); more splits
     // when the staged scales of a wider column set would not fit
@@ -553,13 +626,27 @@ int launch_gemm(const int8_t* xq, const float* rscale, const int8_t* w8, const u
   }
   static std::once_flag attr_once;
   std::call_once(attr_once, [] {
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&q8_gemm_kernel<TO>),
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&q8_gemm_kernel<TO, false>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, kGemmLds);
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&q8_gemm_kernel<TO, true>),
                               hipFuncAttributeMaxDynamicSharedMemorySize, kGemmLds);
   });
   const int tiles_n = (int)((n + kGemmBN - 1) / kGemmBN);
   const int64_t tiles = ((m + kGemmBM - 1) / kGemmBM) * tiles_n;
-  q8_gemm_kernel<TO><<<dim3((unsigned)tiles), dim3(kGemmThreads), kGemmLds, stream>>>(xq, rscale, w8, ws, out, m, n,
-                                                                                      k, tiles_n);
+  const GemmSplit sp = gemm_split_plan(m, n, k);
+  if (sp.splits > 1 && work && work_bytes >= gemm_split_bytes(m, n, sp)) {
+    float* part = static_cast<float*>(work);
+    q8_gemm_kernel<TO, true><<<dim3((unsigned)tiles, (unsigned)sp.splits), dim3(kGemmThreads), kGemmLds, stream>>>(
+        xq, rscale, w8, ws, out, m, n, k, tiles_n, sp.st_per_split, part);
+    const int rc = launch_status("q8_gemm_kernel(split)");
+    if (rc != NVF_OK) return rc;
+    const int64_t threads = m * ((n + 3) / 4);
+    q8_gemm_reduce_kernel<TO><<<dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, stream>>>(part, rscale, out, m,
+                                                                                                 n, sp.splits);
+    return launch_status("q8_gemm_reduce_kernel");
+  }
+  q8_gemm_kernel<TO, false><<<dim3((unsigned)tiles), dim3(kGemmThreads), kGemmLds, stream>>>(
+      xq, rscale, w8, ws, out, m, n, k, tiles_n, 0, nullptr);
   return launch_status("q8_gemm_kernel");
 }
 
@@ -603,15 +690,29 @@ int nvf_q8_quantize_rows(const void* x, float* row_scale, int8_t* xq, int64_t ro
   return quantize_rows(x, dtype, row_scale, xq, rows, k, as_stream(stream));
 }
 
-int nvf_matmul_q8_0(const int8_t* xq, const float* row_scale, const uint8_t* w8, const uint16_t* ws, int64_t m,
-                    int64_t n, int64_t k, void* out, int out_dtype, void* stream) {
+int nvf_matmul_q8_0_ws(const int8_t* xq, const float* row_scale, const uint8_t* w8, const uint16_t* ws, int64_t m,
+                       int64_t n, int64_t k, void* out, int out_dtype, void* workspace, int64_t workspace_bytes,
+                       void* stream) {
   const int st = check_gemm(xq, row_scale, w8, ws, m, n, k, out, out_dtype, "matmul_q8_0");
   if (st != NVF_OK || m == 0 || n == 0 || k == 0) return st;
+  if (workspace && !aligned16(workspace))
+    return fail(NVF_ERR_INVALID, "matmul_q8_0: workspace must be 16-byte aligned");
+  if (m * ((n + 3) / 4) / 256 >= INT32_MAX) return fail(NVF_ERR_INVALID, "matmul_q8_0: output too large");
   const int8_t* w = reinterpret_cast<const int8_t*>(w8);
   int rc = NVF_OK;
   NVF_DISPATCH_DTYPE(out_dtype, TO, rc = launch_gemm<TO>(xq, row_scale, w, ws, static_cast<TO*>(out), m, n, k,
-                                                        as_stream(stream)));
+                                                        workspace, workspace_bytes, as_stream(stream)));
   return rc;
+}
+
+int nvf_matmul_q8_0(const int8_t* xq, const float* row_scale, const uint8_t* w8, const uint16_t* ws, int64_t m,
+                    int64_t n, int64_t k, void* out, int out_dtype, void* stream) {
+  return nvf_matmul_q8_0_ws(xq, row_scale, w8, ws, m, n, k, out, out_dtype, nullptr, 0, stream);
+}
+
+int64_t nvf_matmul_q8_0_workspace_size(int64_t m, int64_t n, int64_t k) {
+  if (m <= 0 || n <= 0 || k <= 0) return 0;
+  return gemm_split_bytes(m, n, gemm_split_plan(m, n, k));
 }
 
 // Drop-in for src/hip_ops.hip:639-686 (declared at include/nanovllm/hip_ops.hpp:10):
@@ -623,7 +724,9 @@ void hip_matmul_q8(const float* x, const uint8_t* w8, const uint16_t* ws, int m,
   dropin_check(hipGetDevice(&dev) == hipSuccess ? NVF_OK : fail(NVF_ERR_LAUNCH, "hipGetDevice failed"),
                "hip_matmul_q8");
   const size_t q_bytes = ((size_t)m * (size_t)k + 255) & ~(size_t)255;
-  const size_t need = q_bytes + (size_t)m * sizeof(float);
+  const size_t s_bytes = ((size_t)m * sizeof(float) + 255) & ~(size_t)255;
+  const size_t w_bytes = (size_t)nvf_matmul_q8_0_workspace_size(m, n, k);  // split-K partials (0: unsplit)
+  const size_t need = q_bytes + s_bytes + w_bytes;
   if (need > g_scratch.cap || dev != g_scratch.device) {
     if (g_scratch.p) (void)hipFree(g_scratch.p);
     g_scratch.p = nullptr;
@@ -637,7 +740,9 @@ void hip_matmul_q8(const float* x, const uint8_t* w8, const uint16_t* ws, int m,
   int8_t* xq = static_cast<int8_t*>(g_scratch.p);
   float* rs = reinterpret_cast<float*>(static_cast<uint8_t*>(g_scratch.p) + q_bytes);
   dropin_check(nvf_q8_quantize_rows(x, rs, xq, m, k, NVF_F32, nullptr), "hip_matmul_q8");
-  dropin_check(nvf_matmul_q8_0(xq, rs, w8, ws, m, n, k, out, NVF_F32, nullptr), "hip_matmul_q8");
+  void* work = w_bytes ? static_cast<uint8_t*>(g_scratch.p) + q_bytes + s_bytes : nullptr;
+  dropin_check(nvf_matmul_q8_0_ws(xq, rs, w8, ws, m, n, k, out, NVF_F32, work, (int64_t)w_bytes, nullptr),
+               "hip_matmul_q8");
 }
 
 }  // extern "C"

@@ -48,6 +48,8 @@ SIGNATURES: dict[str, tuple] = {
     "nvf_paged_attention_workspace_size": (_i64, [_i64, _i32, _i32, _i32, _i32, _i32, _i64]),
     "nvf_q8_quantize_rows": (_i32, [_vp, _vp, _vp, _i64, _i64, _i32, _vp]),
     "nvf_matmul_q8_0": (_i32, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _i32, _vp]),
+    "nvf_matmul_q8_0_ws": (_i32, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _i32, _vp, _i64, _vp]),
+    "nvf_matmul_q8_0_workspace_size": (_i64, [_i64, _i64, _i64]),
     "nvf_rms_norm_add": (_i32, [_vp, _vp, _vp, _vp, _i64, _i64, _f32, _i32, _vp]),
     "nvf_rms_norm": (_i32, [_vp, _vp, _vp, _i64, _i64, _f32, _i32, _vp]),
     "nvf_rms_norm_q8": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _f32, _i32, _vp]),
@@ -200,13 +202,19 @@ def q8_quantize_rows(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
 
 
 def matmul_q8_0(xq: torch.Tensor, row_scale: torch.Tensor, w8: torch.Tensor, ws: torch.Tensor, n: int,
-                out_dtype: torch.dtype = torch.float32, out: torch.Tensor | None = None) -> torch.Tensor:
+                out_dtype: torch.dtype = torch.float32, out: torch.Tensor | None = None,
+                split: bool = True) -> torch.Tensor:
     """out [m, n] = dequantized Q8_0 product of pre-quantized activations xq [m, k]
-    (int8, with row_scale) and split-plane weights w8 [n*k] int8, ws [n*k/32] fp16 bits."""
+    (int8, with row_scale) and split-plane weights w8 [n*k] int8, ws [n*k/32] fp16 bits.
+    split: give the library a workspace for split-K when the output is too small to
+    fill the GPU; False runs unsplit."""
     m, k = xq.shape
     out = torch.empty((m, n), dtype=out_dtype, device=xq.device) if out is None else out
-    _check(lib().nvf_matmul_q8_0(_dev(xq, "xq"), _dev(row_scale, "row_scale"), _dev(w8, "w8"), _dev(ws, "ws"), m, n,
-                                 k, _dev(out, "out"), _dt(out), _stream()), "matmul_q8_0")
+    wb = lib().nvf_matmul_q8_0_workspace_size(m, n, k) if split else 0
+    work = torch.empty((wb + 15) // 16 * 4, dtype=torch.float32, device=xq.device) if wb > 0 else None
+    _check(lib().nvf_matmul_q8_0_ws(_dev(xq, "xq"), _dev(row_scale, "row_scale"), _dev(w8, "w8"), _dev(ws, "ws"), m,
+                                    n, k, _dev(out, "out"), _dt(out), work.data_ptr() if work is not None else None,
+                                    wb, _stream()), "matmul_q8_0")
     return out
 
 

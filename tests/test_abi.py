@@ -60,6 +60,11 @@ def test_host_argument_checks():
     assert rc == -1 and "kind" in msg
     rc, msg = _status(lib.nvf_embedding_qk(p, p, 4, 256, 0, 12, 5, p, 1, None))
     assert rc == -1 and "layout" in msg
+    assert lib.nvf_matmul_q8_0_workspace_size(256, 3584, 3584) > 0      # 56 output tiles: split-K
+    assert lib.nvf_matmul_q8_0_workspace_size(16384, 37888, 3584) == 0  # enough tiles
+    assert lib.nvf_matmul_q8_0_workspace_size(8, 3584, 3584) == 0       # the GEMV's rows
+    rc, msg = _status(lib.nvf_matmul_q8_0_ws(p, p, p, p, 256, 3584, 3584, p, 1, p + 8, 1 << 26, None))
+    assert rc == -1 and "workspace" in msg
     assert lib.nvf_paged_attention_workspace_size(1, 28, 4, 128, 256, 16, 1) > 0     # one long-context decode: split
     assert lib.nvf_paged_attention_workspace_size(256, 28, 4, 128, 256, 16, 1) == 0  # enough (token, kv head) pairs
     assert lib.nvf_paged_attention_workspace_size(1, 28, 4, 64, 256, 16, 1) == 0     # not a matrix-core shape

@@ -175,3 +175,29 @@ def test_dropin_matmul_q8_grows_scratch(gpu):
         ops.lib().hip_matmul_q8(xd.data_ptr(), w8d.data_ptr(), wsd.data_ptr(), m, n, k, out.data_ptr())
         torch.cuda.synchronize()
         assert_within(out.cpu().numpy(), ideal, err, H.F32, "drop-in")
+
+
+SPLITK = [(130, 300, 2048), (40, 1000, 4096), (300, 257, 1024), (256, 3584, 3584)]
+
+
+@pytest.mark.parametrize("out_dt", DTYPES, ids=DT_IDS)
+@pytest.mark.parametrize("m,n,k", SPLITK)
+def test_matmul_q8_0_split_k(gpu, out_dt, m, n, k):
+    """Outputs with too few 128 x 128 tiles to fill the GPU split K (fp32 partial
+    sums, then an in-order reduction): within the oracle's summation bound, like
+    the unsplit kernel; odd n exercises the reduction's column tail."""
+    assert ops.lib().nvf_matmul_q8_0_workspace_size(m, n, k) > 0
+    x, w8, ws = make(m * 5 + n + k + out_dt, m, n, k, H.F32)
+    x[1] = 0.0
+    rows = np.arange(m) if m * n * k <= 1 << 30 else np.array([0, 1, 2, 63, 64, 127, 128, 200, m - 1])
+    ideal, err, sc, xq = oracle_gemm(np.ascontiguousarray(x[rows]), H.F32, w8, ws, rows.size, n, k)
+    _, _, sc_all, xq_all = oracle_gemm(x, H.F32, w8, ws[: (k // 32)], m, 1, k)  # all rows' scale and int8 row
+    args = (H.to_dev(xq_all, gpu), H.to_dev(sc_all, gpu), H.to_dev(w8, gpu), H.to_dev(ws, gpu), n,
+            H.torch_dtype(out_dt))
+    case(f"matmul_q8_0 split-K m={m} n={n} k={k} out_dt={out_dt}")
+    got = H.to_host(ops.matmul_q8_0(*args))
+    assert_within(got[rows], ideal, err, out_dt, "split-K gemm")
+    assert (H.from_storage(got, out_dt)[1] == 0).all()
+    case(f"matmul_q8_0 unsplit m={m} n={n} k={k} out_dt={out_dt}")
+    got = H.to_host(ops.matmul_q8_0(*args, split=False))
+    assert_within(got[rows], ideal, err, out_dt, "unsplit gemm")
