@@ -58,7 +58,7 @@ def parse() -> argparse.Namespace:
                    help="embedding table format (default: the config's)")
     p.add_argument("--only", default="",
                    help="comma list of ops (default emb,rms,rope,silu,copy,gemm,gemv,split,attn,attn_decode,attn_f32,"
-                        "attn_decode_f32,attn_decode_small,layer,layer_decode); "
+                        "attn_decode_f32,attn_decode_small,layer,layer_decode,layer_b1,layer_b1_graph); "
                         "also emb_rms, rms_q8, silu_q8 (fusions)")
     return p.parse_args()
 
@@ -111,7 +111,7 @@ def main() -> int:
     emb_fmt = args.emb or cfg.emb
     nbytes = op_bytes(cfg, e, emb_fmt)
     only = set(filter(None, args.only.split(","))) or {"emb", "rms", "rope", "silu", "copy", "gemm", "gemv", "split",
-                                                       "attn", "attn_decode", "attn_f32", "attn_decode_f32", "attn_decode_small", "layer", "layer_decode"}
+                                                       "attn", "attn_decode", "attn_f32", "attn_decode_f32", "attn_decode_small", "layer", "layer_decode", "layer_b1", "layer_b1_graph"}
 
     def nsets(b: int) -> int:
         return max(2, -(-POOL_BYTES // b))
@@ -222,7 +222,8 @@ def main() -> int:
         small_bytes = float(sB * sctx) * cfg.kv_heads * cfg.head_dim * 2 * e
     layer = None
     layer_dec = None
-    if {"layer", "layer_decode"} & only:  # one whole decoder layer on this library's kernels
+    layer_b1 = None
+    if {"layer", "layer_decode", "layer_b1", "layer_b1_graph"} & only:  # one whole decoder layer on this library's kernels
 
         def q8w(n_, k_, lo=1e-3, hi=1e-2):  # random Q8_0 weight planes
             return (torch.randint(-127, 128, (n_ * k_,), generator=g, device=dev, dtype=torch.int8),
@@ -271,6 +272,8 @@ def main() -> int:
             layer_dec = build_layer(dctx - 1, np.arange(256), dctx, 1, cfg.seed + 8)
             dec_ops, dec_attn_flops = layer_flops(256, dctx - 1)
             dec_kv_bytes = float(dctx.sum()) * cfg.kv_heads * cfg.head_dim * 2 * e
+        if {"layer_b1", "layer_b1_graph"} & only:  # latency: one sequence, one new token, 4096 keys of context
+            layer_b1 = build_layer(np.array([4095]), np.array([0]), [4096], 1, cfg.seed + 9)
     # the same inputs as fp32 caches (the reference's KV dtype; the drop-in's path)
     f32ize = (lambda tup: tuple(x.float() if x.is_floating_point() else x for x in tup))
     attn_in32 = f32ize(attn_in) if "attn_f32" in only else None
@@ -382,6 +385,26 @@ def main() -> int:
     def run_layer_decode(i):
         run_layer_on(layer_dec)
 
+    def run_layer_b1(i):
+        run_layer_on(layer_b1)
+
+    b1_graph = None
+    if "layer_b1_graph" in only:  # the same step captured once into a HIP graph, then replayed
+        cs = torch.cuda.Stream()
+        cs.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(cs):
+            for _ in range(3):  # warm: one-time attribute calls and allocator pools before capture
+                run_layer_on(layer_b1)
+        torch.cuda.current_stream().wait_stream(cs)
+        torch.cuda.synchronize()
+        b1_graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(b1_graph):
+            run_layer_on(layer_b1)
+        torch.cuda.synchronize()
+
+    def run_layer_b1_graph(i):
+        b1_graph.replay()
+
     def run_attn_f32(i):
         q_, kc_, vc_, qs_, ql_, tb_ = attn_in32
         ops.paged_attention(q_, kc_, vc_, qs_, ql_, tb_, bs_kv, cfg.head_dim ** -0.5, out=attn_out32)
@@ -402,7 +425,8 @@ def main() -> int:
              ("rms_q8", run_rms_q8), ("silu_q8", run_silu_q8), ("copy", run_copy), ("gemm", run_gemm),
              ("gemv", run_gemv), ("split", run_split), ("attn", run_attn), ("attn_decode", run_attn_decode),
              ("attn_f32", run_attn_f32), ("attn_decode_f32", run_attn_decode_f32), ("attn_decode_small", run_attn_decode_small),
-             ("layer", run_layer), ("layer_decode", run_layer_decode)]
+             ("layer", run_layer), ("layer_decode", run_layer_decode), ("layer_b1", run_layer_b1),
+             ("layer_b1_graph", run_layer_b1_graph)]
     active = [(n, f) for n, f in table if n in only]
 
     for i in range(args.warmup):
@@ -475,6 +499,9 @@ def main() -> int:
                           "tokens_per_s": round(256 / (t_us * 1e-6), 1),
                           "weights_and_kv_GB_s": round((dec_ops / 2 / 256 * 34 / 32 + dec_kv_bytes) / (t_us * 1e-6) / 1e9,
                                                        1)})
+        elif n in ("layer_b1", "layer_b1_graph"):
+            entry["shape"] = ("one Qwen2.5-7B decoder layer, decode step of 1 sequence with 4096 keys of context"
+                              + (", replayed from a captured HIP graph" if n == "layer_b1_graph" else ", eager launches"))
         elif n == "layer":
             entry.update({"shape": f"one Qwen2.5-7B decoder layer, {T} tokens ({len(np.diff(cfg.cu_seqlens()))} "
                                    f"causal prefills), Q8_0 weights, fp16 activations and KV cache",
@@ -543,6 +570,8 @@ def main() -> int:
         "q8_0_split": res_ops.get("split"),
         "layer": res_ops.get("layer"),
         "layer_decode": res_ops.get("layer_decode"),
+        "layer_b1": res_ops.get("layer_b1"),
+        "layer_b1_graph": res_ops.get("layer_b1_graph"),
         "paged_attention": {k: res_ops[k] for k in ("attn", "attn_decode", "attn_f32", "attn_decode_f32",
                                                     "attn_decode_small") if k in res_ops} or None,
         "cpu_baseline": cpu,

@@ -1,0 +1,106 @@
+"""A decode-step layer captured into a HIP graph (torch.cuda.CUDAGraph) and
+replayed: every replay is bit-identical to the eager run of the same layer (the
+kernels are deterministic and record no memset), with the program's own eager
+work (restoring the residual) and synchronizations between the replays.
+
+The layer is model.cpp:758-833's sequence on this library's ops: input RMSNorm
+writing int8 rows, qkv GEMM (the decode GEMV at these row counts), RoPE on views
+of the packed row, KV store, paged attention (split across key ranges at this
+batch size), row quantizer + o GEMM, residual-add RMSNorm, gate_up, SwiGLU writing
+int8 rows, down.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from nano_vllm_cpp_amd import ops
+
+pytestmark = pytest.mark.gpu
+
+HID, QH, KVH, HD, INTER, BS = 512, 4, 1, 128, 1024, 64
+
+
+def case(msg: str) -> None:
+    print(f"[case] {msg}", flush=True)
+
+
+def _q8w(g, n, k, dev):
+    return (torch.randint(-127, 128, (n * k,), generator=g, device=dev, dtype=torch.int8),
+            torch.empty(n * k // 32, device=dev).uniform_(1e-3, 1e-2, generator=g).half().view(torch.int16))
+
+
+def _build(dev, batch, ctx):
+    g = torch.Generator(device=dev).manual_seed(11)
+    qs, ks = QH * HD, KVH * HD
+    nb = -(-ctx // BS)
+    tab = torch.arange(batch * nb, dtype=torch.int32, device=dev).view(batch, nb)
+    rows = batch * nb * BS
+    pos = torch.full((batch,), ctx - 1, dtype=torch.int64, device=dev)
+    slots = (tab[:, (ctx - 1) // BS].to(torch.int64) * BS + (ctx - 1) % BS).to(torch.int32)
+    L = dict(h=torch.randn(batch, HID, generator=g, device=dev).half(),
+             r=torch.randn(batch, HID, generator=g, device=dev).half(),
+             w_in=(1 + 0.1 * torch.randn(HID, generator=g, device=dev)).half(),
+             w_post=(1 + 0.1 * torch.randn(HID, generator=g, device=dev)).half(),
+             qkv=_q8w(g, qs + 2 * ks, HID, dev), o=_q8w(g, HID, qs, dev), gu=_q8w(g, 2 * INTER, HID, dev),
+             down=_q8w(g, HID, INTER, dev),
+             kc=torch.randn(rows, KVH, HD, generator=g, device=dev).half(),
+             vc=torch.randn(rows, KVH, HD, generator=g, device=dev).half(),
+             pos=pos, qseq=torch.arange(batch, dtype=torch.int32, device=dev),
+             qlen=torch.full((batch,), ctx, dtype=torch.int32, device=dev), tab=tab, slots=slots,
+             inv=ops.rope_inv_freq(1e6, HD, dev), out=torch.empty(batch, HID, dtype=torch.float16, device=dev))
+    return L
+
+
+def _layer(L):
+    qs, ks = QH * HD, KVH * HD
+    n = L["h"].shape[0]
+    _, sc, xq = ops.rms_norm_q8(L["h"], L["w_in"], 1e-6, residual=L["r"], want_out=False)
+    qkv = ops.matmul_q8_0(xq, sc, *L["qkv"], qs + 2 * ks, torch.float16)
+    ops.qk_norm_rope(qkv[:, :qs], qkv[:, qs:qs + ks], L["pos"], None, None, L["inv"], QH, KVH, HD)
+    ops.store_kv(qkv[:, qs:qs + ks].view(n, KVH, HD), qkv[:, qs + ks:].view(n, KVH, HD), L["kc"], L["vc"],
+                 L["slots"])
+    att = ops.paged_attention(qkv[:, :qs].view(n, QH, HD), L["kc"], L["vc"], L["qseq"], L["qlen"], L["tab"], BS,
+                              HD ** -0.5, max_query_len=1)
+    sc2, xq2 = ops.q8_quantize_rows(att.view(n, qs))
+    o = ops.matmul_q8_0(xq2, sc2, *L["o"], HID, torch.float16)
+    _, sc3, xq3 = ops.rms_norm_q8(o, L["w_post"], 1e-6, residual=L["r"], want_out=False)
+    gu = ops.matmul_q8_0(xq3, sc3, *L["gu"], 2 * INTER, torch.float16)
+    _, sc4, xq4 = ops.silu_and_mul_q8(gu)
+    ops.matmul_q8_0(xq4, sc4, *L["down"], HID, torch.float16, out=L["out"])
+
+
+@pytest.mark.parametrize("batch,ctx", [(1, 4096), (3, 1500)])
+def test_decode_layer_graph_replays_match_eager(gpu, batch, ctx):
+    L = _build(gpu, batch, ctx)
+    assert ops.lib().nvf_paged_attention_workspace_size(batch, QH, KVH, HD, BS, L["tab"].shape[1], 1) > 0
+    r0 = L["r"].clone()
+    case(f"decode layer eager batch={batch} ctx={ctx}")
+    _layer(L)
+    torch.cuda.synchronize()
+    want_out, want_r, want_kc = L["out"].clone(), L["r"].clone(), L["kc"].clone()
+    cs = torch.cuda.Stream()
+    cs.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(cs):  # warm the side stream the capture uses
+        for _ in range(2):
+            L["r"].copy_(r0)
+            _layer(L)
+    torch.cuda.current_stream().wait_stream(cs)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    case(f"decode layer capture batch={batch} ctx={ctx}")
+    with torch.cuda.graph(graph):
+        _layer(L)
+    torch.cuda.synchronize()
+    for rep in range(4):
+        L["r"].copy_(r0)           # eager work between the replays
+        L["out"].fill_(float("nan"))
+        torch.cuda.synchronize()
+        case(f"decode layer replay {rep} batch={batch} ctx={ctx}")
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(L["out"].view(torch.int16), want_out.view(torch.int16)), f"replay {rep}: output"
+        assert torch.equal(L["r"].view(torch.int16), want_r.view(torch.int16)), f"replay {rep}: residual"
+        assert torch.equal(L["kc"].view(torch.int16), want_kc.view(torch.int16)), f"replay {rep}: k cache"
+        assert not torch.isnan(L["out"]).any()
