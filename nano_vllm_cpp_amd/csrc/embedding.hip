@@ -399,14 +399,15 @@ struct StagedQ6K {
                      (float)(int8_t)blk[192 + 8 * h + (l0 >> 4) + 2 * slot];
     const uint8_t* ql = blk + 64 * h + 32 * (slot & 1) + l0;
     const uint8_t* qh = blk + 128 + 32 * h + l0;
+    // four 6-bit values per dword at once (low nibbles | high 2 bits << 4), then per
+    // byte an exact byte-to-float, an exact - 32 and the product, as the reference
+    // (an fma with -32 ds folded in would give +0 where the reference gives -0)
 #pragma unroll
     for (int w = 0; w < N / 4; ++w) {
       const uint32_t a = lds_u32_a2(ql + 4 * w), b = lds_u32_a2(qh + 4 * w);
+      const uint32_t q4 = ((a >> lsh) & 0x0f0f0f0fu) | (((b >> hsh) & 0x03030303u) << 4);
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const int q = (int)(((byte_of(a, k) >> lsh) & 0xfu) | (((byte_of(b, k) >> hsh) & 3u) << 4));
-        v[4 * w + k] = ds * (float)(q - 32);
-      }
+      for (int k = 0; k < 4; ++k) v[4 * w + k] = ((float)byte_of(q4, k) - 32.0f) * ds;
     }
   }
 };
@@ -423,14 +424,14 @@ struct StagedQ5K {
     const float m = half_bits_to_f32(hd[0] >> 16) * (float)mn;
     const uint32_t* ql = reinterpret_cast<const uint32_t*>(blk + 48 + 32 * (i >> 6) + l0);
     const uint32_t* qh = reinterpret_cast<const uint32_t*>(blk + 16 + l0);
+    // four 5-bit values per dword at once; s * q is exact (22 bits), so fma(q, s, -m)
+    // rounds the same exact difference once, as s * q - m does
 #pragma unroll
     for (int w = 0; w < N / 4; ++w) {
       const uint32_t a = ql[w], b = qh[w];
+      const uint32_t q4 = ((a >> sh) & 0x0f0f0f0fu) | (((b >> j) & 0x01010101u) << 4);
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const uint32_t q = ((byte_of(a, k) >> sh) & 0xfu) | (((byte_of(b, k) >> j) & 1u) << 4);
-        v[4 * w + k] = s * (float)q - m;
-      }
+      for (int k = 0; k < 4; ++k) v[4 * w + k] = fmaf((float)byte_of(q4, k), s, -m);
     }
   }
 };
