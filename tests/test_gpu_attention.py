@@ -336,3 +336,26 @@ def test_paged_attention_split_tiles(gpu, dt, ci):
     assert_attn(H.to_host(ops.paged_attention(*args)), exact, vmax, dt, "split tiles")
     case(f"paged_attention unsplit tiles case={ci} dt={dt}")
     assert_attn(H.to_host(ops.paged_attention(*args, split=False)), exact, vmax, dt, "unsplit tiles")
+
+
+def test_paged_attention_ws_too_small_runs_unsplit(gpu):
+    """nvf_paged_attention_ws with a workspace one byte short of the size query's
+    answer takes the unsplit path: the same results, no out-of-bounds writes."""
+    r = H.rng(77)
+    b = H.make_paged(r, [4096, 300], [1, 1], 28, 4, 128, 256, H.F16)
+    need = ops.lib().nvf_paged_attention_workspace_size(b.tokens, 28, 4, 128, 256, b.max_blocks, 1)
+    assert need > 0
+    scale = 128 ** -0.5
+    _, exact, vmax = H.oracle_attention(b, 28, 4, 128, 256, scale, H.F16)
+    dq, dk, dv = H.to_dev(b.q, gpu, H.F16), H.to_dev(b.k_cache, gpu, H.F16), H.to_dev(b.v_cache, gpu, H.F16)
+    dqs, dql, dtab = H.to_dev(b.query_seq, gpu), H.to_dev(b.query_key_len, gpu), H.to_dev(b.block_tables, gpu)
+    guard = torch.full(((need + 15) // 16 * 4 + 64,), 7.0, dtype=torch.float32, device=gpu)
+    out = torch.empty_like(dq)
+    case("paged_attention_ws one byte short")
+    rc = ops.lib().nvf_paged_attention_ws(dq.data_ptr(), out.data_ptr(), dk.data_ptr(), dv.data_ptr(), dqs.data_ptr(),
+                                          dql.data_ptr(), dtab.data_ptr(), b.tokens, 28, 4, 128, 256, b.max_blocks,
+                                          scale, 28 * 128, 1, guard.data_ptr(), need - 1, H.F16, None)
+    assert rc == 0
+    torch.cuda.synchronize()
+    assert_attn(H.to_host(out), exact, vmax, H.F16, "unsplit fallback")
+    assert (guard == 7.0).all()  # the workspace was not touched
