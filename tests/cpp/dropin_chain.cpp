@@ -259,6 +259,38 @@ int main() {
   oracle_gemm(last, emb.w8.data(), emb.ws.data(), 1, V, H, ideal, bound);
   expect_within("lm_head logits (m = 1)", logits.host(), ideal, bound);
 
+  // a decode step over a longer cache (model_runner.cpp:100-128: one query per
+  // sequence, key_len = its context) in 64-key blocks: few (token, kv head) pairs,
+  // so the drop-in splits the keys over its own workspace and merges
+  {
+    const int ds = 2, dbs = 64, dmax = 12;
+    const int ctx[ds] = {300, 700};
+    const int rows = ds * dmax * dbs;
+    std::vector<float> dq((size_t)ds * q_size), dk((size_t)rows * kv_size), dv((size_t)rows * kv_size);
+    std::normal_distribution<float> n01(0.f, 1.f);
+    for (auto* a : {&dq, &dk, &dv})
+      for (auto& e : *a) e = n01(rng);
+    std::vector<int32_t> dqs(ds), dql(ds), dtab((size_t)ds * dmax);
+    for (int s2 = 0; s2 < ds; ++s2) {
+      dqs[s2] = s2, dql[s2] = ctx[s2];
+      for (int b = 0; b < dmax; ++b) dtab[s2 * dmax + b] = (s2 * dmax + b * 5) % (ds * dmax);  // a permutation
+    }
+    if (nvf_paged_attention_workspace_size(ds, heads, kv_heads, hd, dbs, dmax, 0) <= 0) {
+      std::printf("decode step: expected a split plan\n");
+      ++failures;
+    }
+    Dev<float> g_q(dq), g_k(dk), g_v(dv), g_o((size_t)ds * q_size);
+    Dev<int32_t> g_qs(dqs), g_ql(dql), g_tab(dtab);
+    hip_paged_attention(g_q.d, g_o.d, g_k.d, g_v.d, g_qs.d, g_ql.d, g_tab.d, ds, heads, kv_heads, hd, dbs, dmax, scale);
+    sync();
+    std::vector<float> ao((size_t)ds * q_size), vmax((size_t)ds * heads);
+    std::vector<double> ex((size_t)ds * q_size), tol((size_t)ds * q_size);
+    orc_paged_attention(dq.data(), ao.data(), dk.data(), dv.data(), dqs.data(), dql.data(), dtab.data(), ds, heads,
+                        kv_heads, hd, dbs, dmax, scale, ORC_F32, ex.data(), vmax.data());
+    for (size_t i = 0; i < tol.size(); ++i) tol[i] = 1e-4 * vmax[i / hd] + 1e-7;
+    expect_within("decode step: split paged attention", g_o.host(), ex, tol);
+  }
+
   std::printf(failures ? "DROPIN CHAIN FAILED\n" : "DROPIN CHAIN OK\n");
   return failures ? 1 : 0;
 }

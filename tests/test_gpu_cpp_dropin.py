@@ -1,7 +1,8 @@
 """Runs tests/cpp/dropin_chain: a C++ program that calls the drop-in C ABI in
 the order src/model.cpp:756-844 does -- a whole layer: embedding, norms, the
 Q8_0 projections, QK-norm, RoPE, KV store, paged attention, SwiGLU, final norm,
-lm_head -- and checks every stage against the C oracle (bit-exact gathers,
+lm_head -- then a decode step over a longer cache that the drop-in splits over its
+own workspace, and checks every stage against the C oracle (bit-exact gathers,
 residuals and cache writes; the stated tolerance or bound elsewhere)."""
 from __future__ import annotations
 
