@@ -180,8 +180,12 @@ def main() -> int:
     bs_kv = 256  # the reference's KV block size (a multiple of 256, config.hpp:254)
     if {"attn", "attn_f32"} & only:  # causal prefill over the config's sequences, KV already in the paged cache
         apos = cfg.positions()
-        lens = [int(n) for n in np.diff(cfg.cu_seqlens())]
-        nblk = [-(-n // bs_kv) for n in lens]
+        cu = cfg.cu_seqlens()
+        lens = [int(n) for n in np.diff(cu)]
+        # a sequence's cache holds every key its queries attend: max position + 1 (config 1's
+        # one-token sequences sit at random positions, so this is not the sequence's length)
+        sctx = [int(apos[cu[s_]:cu[s_ + 1]].max()) + 1 for s_ in range(len(lens))]
+        nblk = [-(-n // bs_kv) for n in sctx]
         tables = torch.full((len(lens), max(nblk)), -1, dtype=torch.int32)
         perm = torch.randperm(sum(nblk), generator=torch.Generator().manual_seed(cfg.seed))
         o_ = 0
@@ -194,6 +198,9 @@ def main() -> int:
                    torch.from_numpy(np.repeat(np.arange(len(lens), dtype=np.int32), lens)).to(dev),
                    torch.from_numpy((apos + 1).astype(np.int32)).to(dev), tables.to(dev))
         attn_flops = 4.0 * cfg.q_heads * cfg.head_dim * float((apos + 1).sum())
+        # host-side guard before any kernel runs: every key a query attends has a block
+        aseq = np.repeat(np.arange(len(lens)), lens)
+        assert ((apos + 1) <= np.array(nblk)[aseq] * bs_kv).all(), "attention inputs: keys past the block tables"
     if {"attn_decode", "attn_decode_f32"} & only:  # one token per sequence, 256 sequences, context uniform in 1..4096
         ctx = np.random.default_rng(cfg.seed + 11).integers(1, 4097, 256)
         nblk = [-(-int(n) // bs_kv) for n in ctx]
@@ -243,6 +250,8 @@ def main() -> int:
             for s_, nb in enumerate(lnb):
                 ltab[s_, :nb] = lperm[o_:o_ + nb]
                 o_ += nb
+            # host-side guard: every key a query attends has a block
+            assert ((lpos + 1) <= np.array(lnb)[lseq] * bs_kv).all(), "layer inputs: keys past the block tables"
             lslots = (ltab[lseq, lpos // bs_kv].astype(np.int64) * bs_kv + lpos % bs_kv).astype(np.int32)
             lrows = sum(lnb) * bs_kv
             return dict(lw, T=n_, mql=mql, h=randn((n_, Hd)), r=randn((n_, Hd)),
@@ -263,9 +272,11 @@ def main() -> int:
                     4.0 * cfg.q_heads * cfg.head_dim * float((lpos + 1).sum()))
         if "layer" in only:  # the config's prefill
             lpos = cfg.positions()
-            llens = [int(n) for n in np.diff(cfg.cu_seqlens())]
+            lcu = cfg.cu_seqlens()
+            llens = [int(n) for n in np.diff(lcu)]
             lseq = np.repeat(np.arange(len(llens), dtype=np.int32), llens)
-            layer = build_layer(lpos, lseq, llens, 0, cfg.seed + 5)
+            lctx = [int(lpos[lcu[s_]:lcu[s_ + 1]].max()) + 1 for s_ in range(len(llens))]  # keys each sequence holds
+            layer = build_layer(lpos, lseq, lctx, 0, cfg.seed + 5)
             layer_ops, layer_attn_flops = layer_flops(T, lpos)
         if "layer_decode" in only:  # a decode step: 256 sequences, one new token each, context U[1, 4096]
             dctx = np.random.default_rng(cfg.seed + 7).integers(1, 4097, 256)
