@@ -449,6 +449,9 @@ def main() -> int:
     # stream the kernels run on (rotating buffer sets), averaged per launch.
     stream = torch.cuda.current_stream()
     res_ops = {}
+    _lens = np.diff(cfg.cu_seqlens())
+    batch_desc = (f"{len(_lens)} one-token queries at random positions" if int(_lens.max()) == 1
+                  else f"causal prefill {len(_lens)} x {T // len(_lens)} tokens")
     for n, f in active:
         a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         torch.cuda.synchronize()
@@ -485,8 +488,7 @@ def main() -> int:
             entry.update({"shape": f"m={T} n={2 * I} k={Hd} (gate_up)", "TOP_s": round(ops_n / (t_us * 1e-6) / 1e12, 1),
                           "frac_of_int8_peak": round(ops_n / (t_us * 1e-6) / INT8_PEAK_OPS, 4)})
         elif n == "attn":
-            entry.update({"shape": f"causal prefill {len(np.diff(cfg.cu_seqlens()))} x {T // len(np.diff(cfg.cu_seqlens()))}"
-                                   f" tokens, {cfg.q_heads}/{cfg.kv_heads} heads x {cfg.head_dim}, KV block {bs_kv}",
+            entry.update({"shape": f"{batch_desc}, {cfg.q_heads}/{cfg.kv_heads} heads x {cfg.head_dim}, KV block {bs_kv}",
                           "TFLOP_s": round(attn_flops / (t_us * 1e-6) / 1e12, 1),
                           "frac_of_16bit_peak": round(attn_flops / (t_us * 1e-6) / 2.5e15, 4)})
         elif n == "attn_f32":
@@ -514,8 +516,8 @@ def main() -> int:
             entry["shape"] = ("one Qwen2.5-7B decoder layer, decode step of 1 sequence with 4096 keys of context"
                               + (", replayed from a captured HIP graph" if n == "layer_b1_graph" else ", eager launches"))
         elif n == "layer":
-            entry.update({"shape": f"one Qwen2.5-7B decoder layer, {T} tokens ({len(np.diff(cfg.cu_seqlens()))} "
-                                   f"causal prefills), Q8_0 weights, fp16 activations and KV cache",
+            entry.update({"shape": f"one Qwen2.5-7B decoder layer, {T} tokens ({batch_desc}), Q8_0 weights, "
+                                   f"fp16 activations and KV cache",
                           "tokens_per_s": round(T / (t_us * 1e-6), 1),
                           "gemm_TOP_s": round(layer_ops / (t_us * 1e-6) / 1e12, 1),
                           "effective_TOP_s_incl_attention": round((layer_ops + layer_attn_flops) / (t_us * 1e-6) / 1e12, 1)})
