@@ -376,25 +376,37 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(3)
 // q = 2, 3 its second; the block scales differ, so each pair takes two MFMAs,
 // each with the activation lanes of the other block zeroed (the K = 64
 // instruction then sums exactly one block).  MFMA time is idle capacity here.
+//
+// The activations come one of two ways.  With XL (K split over the waves) the workgroup's m rows are
+// staged in LDS once, by DMA in the prologue (rows padded by 16 bytes, so the 16
+// rows of a ds_read_b128 phase fall in distinct banks).  The loop then holds LDS
+// reads only, and its vmcnt waits are the explicit ones, which leave the next
+// weight stage in flight.  Without XL (when those rows would cost the launch
+// resident workgroups) they are register loads per stage; the compiler does not
+// count LDS DMA in its own vmcnt waits for those registers, so they also drain
+// part of the next stage.
 constexpr int kGemvMaxM = 16;
 constexpr int kGvKC = 256;                        // bytes of K per stage (4 block pairs)
 constexpr int kGvWaveBuf = 16 * kGvKC;            // one stage of one wave's 16 columns
 constexpr int kGemvScaleLds = 32768;              // bytes of LDS for the staged scales
+constexpr int kGemvXLdsMax = 65536;               // bytes of LDS for staged activation rows
+constexpr int64_t kLdsPerCu = 160 * 1024;
 
 template <int W, int S>
 constexpr int gemv_cols() { return W / S * 16; }  // columns per workgroup of W waves
 
-template <typename TO, int W, int S>
+template <typename TO, int W, int S, bool XL>
 __global__ __launch_bounds__(W * 64) void q8_gemv_kernel(const int8_t* __restrict__ xq,
-                                                                   const float* __restrict__ rscale,
-                                                                   const int8_t* __restrict__ w8,
-                                                                   const uint16_t* __restrict__ ws,
-                                                                   TO* __restrict__ out, int64_t m, int64_t n,
-                                                                   int64_t k) {
+                                                         const float* __restrict__ rscale,
+                                                         const int8_t* __restrict__ w8,
+                                                         const uint16_t* __restrict__ ws,
+                                                         TO* __restrict__ out, int64_t m, int64_t n, int64_t k,
+                                                         int sc_bytes) {
   constexpr int kCols = gemv_cols<W, S>();
   constexpr int kGvDmaLds = W * 2 * kGvWaveBuf;
-  __shared__ float part[W][16][17];
-  extern __shared__ __attribute__((aligned(16))) uint8_t dyn[];  // [DMA buffers][scales]
+  // [DMA buffers][scales][activation rows (XL)]; after the loop each wave's partial
+  // sums reuse its own DMA buffers
+  extern __shared__ __attribute__((aligned(16))) uint8_t dyn[];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   const int grp = wave / S, split = wave % S;
@@ -403,94 +415,172 @@ __global__ __launch_bounds__(W * 64) void q8_gemv_kernel(const int8_t* __restric
   const int64_t nblk = k / 32, npairs = (nblk + 1) / 2;
   const int64_t wg_cols = n - wg_c0 < kCols ? n - wg_c0 : kCols;
   uint16_t* sc_lds = reinterpret_cast<uint16_t*>(dyn + kGvDmaLds);
-
-  {  // stage this workgroup's block scales: wg_cols rows of nblk fp16 values,
-     // whole 4-byte words, then an odd last value by itself (a 4-byte load that
-     // straddles the end of the slab reads as zero entirely)
-    const __amdgpu_buffer_rsrc_t rs = make_rsrc(ws + wg_c0 * nblk, wg_cols * nblk * 2);
-    const int64_t cnt = wg_cols * nblk;
-    uint32_t* dst = reinterpret_cast<uint32_t*>(sc_lds);
-    for (int64_t i = threadIdx.x; i < cnt / 2; i += W * 64)
-      dst[i] = __builtin_amdgcn_raw_buffer_load_b32(rs, (uint32_t)(4 * i), 0, 0);
-    if ((cnt & 1) && threadIdx.x == 0)
-      sc_lds[cnt - 1] = (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(rs, (uint32_t)(2 * (cnt - 1)), 0, 0);
-    __syncthreads();
-  }
+  uint8_t* x_lds = dyn + kGvDmaLds + sc_bytes;
+  const int64_t xrow = k + 16;  // LDS bytes per staged activation row
 
   const int64_t c0 = wg_c0 + (int64_t)grp * 16;  // this wave's first column
   const int64_t cols = n - c0 < 16 ? n - c0 : 16;
   const int64_t p_begin = npairs * split / S, p_end = npairs * (split + 1) / S;
+  const bool active = cols > 0 && p_end > p_begin;  // uniform per wave
   float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 
-  if (cols > 0 && p_end > p_begin) {  // uniform per wave
-    // rows past m / columns past n fall outside these resources and read zero
-    const __amdgpu_buffer_rsrc_t rw = make_rsrc(w8 + c0 * k, cols * k);
-    const __amdgpu_buffer_rsrc_t rx = make_rsrc(xq, m * k);
-    uint8_t* wbuf = dyn + wave * 2 * kGvWaveBuf;
-    // DMA lane l of transfer i: column 4 i + l / 16, LDS position l % 16, fetching chunk (l % 16) ^ column
-    uint32_t dma_off[4];
+  // rows past m / columns past n fall outside these resources and read zero
+  const __amdgpu_buffer_rsrc_t rw = make_rsrc(w8 + (active ? c0 * k : 0), active ? cols * k : 0);
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(xq, m * k);
+  uint8_t* wbuf = dyn + wave * 2 * kGvWaveBuf;
+  // DMA lane l of transfer i: column 4 i + l / 16, LDS position l % 16, fetching chunk (l % 16) ^ column
+  uint32_t dma_off[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int col = 4 * i + (lane >> 4);
-      dma_off[i] = (uint32_t)(col * k) + 16u * (uint32_t)((lane & 15) ^ col);
+  for (int i = 0; i < 4; ++i) {
+    const int col = 4 * i + (lane >> 4);
+    dma_off[i] = (uint32_t)(col * k) + 16u * (uint32_t)((lane & 15) ^ col);
+  }
+  const int64_t kb0 = 64 * p_begin;
+  const int nst = (int)((p_end - p_begin + 3) / 4);
+  auto issue = [&](int st) {
+    uint8_t* dst = wbuf + (st & 1) * kGvWaveBuf;
+    const uint32_t soff = (uint32_t)(kb0 + (int64_t)st * kGvKC);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (__attribute__((address_space(3))) void*)(dst + i * 1024), 16,
+                                               dma_off[i], soff, 0, 0);
+  };
+  const uint32_t x_off = (uint32_t)(j * k) + 16u * q;  // activation row j
+  i32x4 xv[4];
+  auto load_x = [&](int st) {  // register path: 16 bytes of each of the stage's 4 pairs (zero past k)
+    const int64_t pst = p_begin + 4 * st;
+#pragma unroll
+    for (int pp = 0; pp < 4; ++pp) {
+      const int64_t p = pst + pp;
+      const bool ok = p < p_end && 64 * p + 16 * q < k;
+      xv[pp] = __builtin_bit_cast(
+          i32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, ok ? x_off + (uint32_t)(64 * p) : kOob, 0, 0));
     }
-    const int64_t kb0 = 64 * p_begin;
-    const int nst = (int)((p_end - p_begin + 3) / 4);
-    auto issue = [&](int st) {
-      uint8_t* dst = wbuf + (st & 1) * kGvWaveBuf;
-      const uint32_t soff = (uint32_t)(kb0 + (int64_t)st * kGvKC);
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (__attribute__((address_space(3))) void*)(dst + i * 1024), 16,
-                                                 dma_off[i], soff, 0, 0);
-    };
-    const uint32_t x_off = (uint32_t)(j * k) + 16u * q;  // activation row j
+  };
+  // Issue order: weight stage 0, the scales (and XL rows), stage 0's register
+  // activations, weight stage 1.  vmcnt counts in issue order, so vmcnt(4) waits
+  // for everything but stage 1, which stays in flight; the prologue's HBM
+  // latencies overlap.  LDS DMA lane l of a transfer fills 4 (or 16) bytes at
+  // base + 4 l (16 l).
+  if (active) issue(0);
+  {
+    // the block scales: wg_cols rows of nblk fp16 values, whole 4-byte words, then
+    // an odd last value by itself (a 4-byte load that straddles the end of the
+    // slab reads as zero entirely, so that word is never loaded whole)
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(ws + wg_c0 * nblk, wg_cols * nblk * 2);
+    const int64_t cnt = wg_cols * nblk;
+    uint32_t* dst = reinterpret_cast<uint32_t*>(sc_lds);
+    for (int64_t i0 = 0; i0 < cnt / 2; i0 += W * 64) {
+      const int64_t i = i0 + threadIdx.x;
+      if (i < cnt / 2)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            rs, (__attribute__((address_space(3))) void*)(dst + i0 + 64 * wave), 4, (uint32_t)(4 * i), 0, 0, 0);
+    }
+    if constexpr (XL) {  // m rows of k bytes (k % 32 == 0), 1 KB transfers spread over the waves
+      const int per_row = (int)((k + 1023) / 1024);
+      for (int t = wave; t < m * per_row; t += W) {
+        const int r = t / per_row, c = t % per_row;
+        const int64_t kb = 1024 * (int64_t)c + 16 * lane;
+        if (kb < k)
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(
+              rx, (__attribute__((address_space(3))) void*)(x_lds + r * xrow + 1024 * c), 16,
+              (uint32_t)(r * k + kb), 0, 0, 0);
+      }
+    }
+    if (active) {
+      if constexpr (!XL) load_x(0);
+      if (nst > 1) issue(1);
+    }
+    if (active && nst > 1)
+      __builtin_amdgcn_s_waitcnt(0x0F74);  // vmcnt(4): all but weight stage 1
+    else
+      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+    if ((cnt & 1) && threadIdx.x == 0)
+      sc_lds[cnt - 1] = (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(rs, (uint32_t)(2 * (cnt - 1)), 0, 0);
+    // Every wave's DMA writes are complete (its vmcnt wait above) and the one LDS
+    // store is waited by lgkmcnt(0), so a bare barrier publishes the scales; a
+    // workgroup-scope fence here would add a vmcnt(0) and drain weight stage 1.
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  }
+
+  if (active) {
     const uint16_t* sc_col = sc_lds + ((int64_t)grp * 16 + j) * nblk;
-    issue(0);
+    // XL: lane (j, q) reads row j (rows past m hold zero: the address is clamped
+    // to row 0 and the value selected away)
+    const bool x_row_ok = j < m;
+    const uint8_t* x_src = x_lds + (x_row_ok ? j : 0) * xrow + 16 * q;
     for (int st = 0; st < nst; ++st) {
-      // this stage's activation loads first, then the next stage's transfers: one
-      // vmcnt(4) then covers both this stage's transfers and its activations
+      // weight stage st (and its register activations) are here; stage st + 1 is in flight
       const int64_t pst = p_begin + 4 * st;
       const int npp = p_end - pst < 4 ? (int)(p_end - pst) : 4;
-      i32x4 xv[4];
-#pragma unroll
-      for (int pp = 0; pp < 4; ++pp) {
-        const int64_t p = pst + pp;
-        const bool ok = pp < npp && 64 * p + 16 * q < k;
-        xv[pp] = __builtin_bit_cast(
-            i32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, ok ? x_off + (uint32_t)(64 * p) : kOob, 0, 0));
-      }
-      if (st + 1 < nst) {
-        issue(st + 1);
-        __builtin_amdgcn_s_waitcnt(0x0F74);  // vmcnt(4): everything before the 4 transfers just issued
-      } else {
-        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
-      }
       const uint8_t* src = wbuf + (st & 1) * kGvWaveBuf + j * kGvKC;
-#pragma unroll
-      for (int pp = 0; pp < 4; ++pp) {
-        if (pp >= npp) break;  // uniform
+      // one block pair: operands from LDS (or registers), then its two MFMAs and applies
+      struct Operands {
+        i32x4 wv, x;
+        float s_lo, s_hi;
+      };
+      auto fetch = [&](int pp) {
         const int64_t p = pst + pp;
-        const i32x4 wv = *reinterpret_cast<const i32x4*>(src + 16 * ((4 * pp + q) ^ j));
-        const i32x4 z = {0, 0, 0, 0};
-        const i32x4 x_lo = q < 2 ? xv[pp] : z;  // first block of the pair
-        const i32x4 x_hi = q < 2 ? z : xv[pp];  // second block
         const int64_t b = 2 * p;
-        const float s_lo = fp16_bits_to_float(sc_col[b]);
-        const float s_hi = b + 1 < nblk ? fp16_bits_to_float(sc_col[b + 1]) : 0.0f;
-        const i32x4 d_lo = __builtin_amdgcn_mfma_i32_16x16x64_i8(x_lo, wv, z, 0, 0, 0);
-        const i32x4 d_hi = __builtin_amdgcn_mfma_i32_16x16x64_i8(x_hi, wv, z, 0, 0, 0);
+        Operands o;
+        o.wv = *reinterpret_cast<const i32x4*>(src + 16 * ((4 * pp + q) ^ j));
+        if constexpr (XL) {
+          const i32x4 xr = *reinterpret_cast<const i32x4*>(x_src + 64 * p);
+          o.x = x_row_ok && 64 * p + 16 * q < k ? xr : i32x4{0, 0, 0, 0};
+        } else {
+          o.x = xv[pp];
+        }
+        o.s_lo = fp16_bits_to_float(sc_col[b]);
+        const float s1 = fp16_bits_to_float(sc_col[b + 1 < nblk ? b + 1 : b]);  // read unconditionally
+        o.s_hi = b + 1 < nblk ? s1 : 0.0f;
+        return o;
+      };
+      auto apply = [&](const Operands& o) {
+        const i32x4 z = {0, 0, 0, 0};
+        const i32x4 x_lo = q < 2 ? o.x : z;  // first block of the pair
+        const i32x4 x_hi = q < 2 ? z : o.x;  // second block
+        const i32x4 d_lo = __builtin_amdgcn_mfma_i32_16x16x64_i8(x_lo, o.wv, z, 0, 0, 0);
+        const i32x4 d_hi = __builtin_amdgcn_mfma_i32_16x16x64_i8(x_hi, o.wv, z, 0, 0, 0);
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
-          acc[v] = fmaf(s_lo, (float)d_lo[v], acc[v]);
-          acc[v] = fmaf(s_hi, (float)d_hi[v], acc[v]);
+          acc[v] = fmaf(o.s_lo, (float)d_lo[v], acc[v]);
+          acc[v] = fmaf(o.s_hi, (float)d_hi[v], acc[v]);
+        }
+      };
+      if (npp == 4) {  // uniform: a full stage reads all its operands first, then computes
+        Operands o[4];
+#pragma unroll
+        for (int pp = 0; pp < 4; ++pp) o[pp] = fetch(pp);
+#pragma unroll
+        for (int pp = 0; pp < 4; ++pp) apply(o[pp]);
+      } else {
+        for (int pp = 0; pp < npp; ++pp) apply(fetch(pp));
+      }
+      if (st + 1 < nst) {
+        // the next stage's register activations, then weight stage st + 2 into the
+        // buffer just read (its values are in registers); vmcnt(4) leaves that one
+        // in flight
+        if constexpr (!XL) load_x(st + 1);
+        if (st + 2 < nst) {
+          issue(st + 2);
+          __builtin_amdgcn_s_waitcnt(0x0F74);
+        } else {
+          __builtin_amdgcn_s_waitcnt(0x0F70);
         }
       }
     }
   }
   // D layout of v_mfma_*_16x16: lane l, value v -> column l % 16, row 4 * (l / 16) + v.
+  // Partial sums [wave][16 rows][17] in the wave's own DMA buffers (all its
+  // transfers completed at its last vmcnt wait).
+  auto part = [&](int w, int r, int c) -> float& {
+    return reinterpret_cast<float*>(dyn + w * 2 * kGvWaveBuf)[r * 17 + c];
+  };
 #pragma unroll
-  for (int v = 0; v < 4; ++v) part[wave][4 * q + v][j] = acc[v];
+  for (int v = 0; v < 4; ++v) part(wave, 4 * q + v, j) = acc[v];
   __syncthreads();
   for (int o = threadIdx.x; o < kCols * 16; o += W * 64) {
     const int c = o % kCols, r = o / kCols;  // consecutive threads -> consecutive columns
@@ -499,7 +589,7 @@ __global__ __launch_bounds__(W * 64) void q8_gemv_kernel(const int8_t* __restric
     if (r < m && col < n) {
       float sum = 0.0f;
 #pragma unroll
-      for (int sp = 0; sp < S; ++sp) sum += part[g * S + sp][r][cj];
+      for (int sp = 0; sp < S; ++sp) sum += part(g * S + sp, r, cj);
       const float sc = rscale[r];
       const float inv = sc > 0.0f ? 1.0f / sc : 0.0f;  // the reference's adq (:358)
       gemm_store_out(out + r * n + col, sum * inv);
@@ -508,7 +598,8 @@ __global__ __launch_bounds__(W * 64) void q8_gemv_kernel(const int8_t* __restric
 }
 
 // Launches the GEMV with W waves per workgroup and K split S; false if the
-// staged scales would not fit.
+// staged scales would not fit.  The activation rows go to LDS (XL) when they fit
+// and cost no resident workgroups the launch can use.
 template <typename TO, int W, int S>
 bool try_gemv(const int8_t* xq, const float* rscale, const int8_t* w8, const uint16_t* ws, TO* out, int64_t m,
               int64_t n, int64_t k, hipStream_t stream) {
@@ -516,14 +607,32 @@ bool try_gemv(const int8_t* xq, const float* rscale, const int8_t* w8, const uin
   constexpr int kDma = W * 2 * kGvWaveBuf;
   const int64_t sc_bytes = (kCols * (k / 32) * 2 + 15) & ~15;
   if (sc_bytes > kGemvScaleLds) return false;
+  const int64_t x_bytes = m * (k + 16);
+  const int64_t wgs = (n + kCols - 1) / kCols;
+  const int64_t cus = 256;
+  auto resident = [&](int64_t lds) {  // workgroups per CU, by LDS and by wave slots (8 per SIMD)
+    return std::min<int64_t>(kLdsPerCu / lds, 32 / W);
+  };
+  const int64_t need = (wgs + cus - 1) / cus;  // workgroups per CU the launch can use
+  const int64_t lds_r = kDma + sc_bytes, lds_x = lds_r + x_bytes;
+  // (S = 1: a wave's long run of stages keeps enough in flight; its register
+  // activations measured faster than the extra LDS reads)
+  const bool xl = S > 1 && x_bytes <= kGemvXLdsMax &&
+                  std::min(resident(lds_x), need) >= std::min(resident(lds_r), need);
   static std::once_flag attr_once;
   std::call_once(attr_once, [] {
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&q8_gemv_kernel<TO, W, S>),
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&q8_gemv_kernel<TO, W, S, false>),
                               hipFuncAttributeMaxDynamicSharedMemorySize, kDma + kGemvScaleLds);
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&q8_gemv_kernel<TO, W, S, true>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize,
+                              (int)std::min<int64_t>(kLdsPerCu, kDma + kGemvScaleLds + kGemvXLdsMax));
   });
-  const int64_t wgs = (n + kCols - 1) / kCols;
-  q8_gemv_kernel<TO, W, S><<<dim3((unsigned)wgs), dim3(W * 64), (size_t)(kDma + sc_bytes), stream>>>(
-      xq, rscale, w8, ws, out, m, n, k);
+  if (xl)
+    q8_gemv_kernel<TO, W, S, true><<<dim3((unsigned)wgs), dim3(W * 64), (size_t)lds_x, stream>>>(
+        xq, rscale, w8, ws, out, m, n, k, (int)sc_bytes);
+  else
+    q8_gemv_kernel<TO, W, S, false><<<dim3((unsigned)wgs), dim3(W * 64), (size_t)lds_r, stream>>>(
+        xq, rscale, w8, ws, out, m, n, k, (int)sc_bytes);
   return true;
 }
 

@@ -79,7 +79,10 @@ def test_quantize_rows_bitexact(gpu, dt, m, k):
 
 @pytest.mark.parametrize("out_dt", DTYPES, ids=DT_IDS)
 @pytest.mark.parametrize("m,n,k", [(1, 32, 32), (5, 7, 96), (130, 250, 320), (257, 129, 1056), (64, 4608, 3584),
-                                   (8, 1000, 4864), (16, 500, 352), (17, 64, 128), (3, 3584, 18944), (12, 37, 160)])
+                                   (8, 1000, 4864), (16, 500, 352), (17, 64, 128), (3, 3584, 18944), (12, 37, 160),
+                                   # decode GEMV: batch-1 qkv (activation rows staged in LDS) and a wide output
+                                   # whose staged rows would cost resident workgroups (register activations)
+                                   (1, 4608, 3584), (8, 20000, 3584)])
 def test_matmul_q8_0_vs_oracle(gpu, out_dt, m, n, k):
     x, w8, ws = make(m + 3 * n + k + out_dt, m, n, k, H.F32)
     zero_row = 2 if m > 2 else None
