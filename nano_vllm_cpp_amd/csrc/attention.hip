@@ -16,8 +16,8 @@
 //   head dimensions.  fp32 math; it serves the fp32 drop-in, decode batches and
 //   the shapes and tiles the tiled kernel does not take.
 // * fa_prefill_kernel: 128-query tiles of one sequence on the matrix cores;
-//   fa_decode_kernel: the remaining (decode-shaped) tokens, one wave per
-//   (token, kv head) on the matrix cores.
+//   fa_decode_kernel: the remaining (decode-shaped) tokens, one workgroup per
+//   (token, kv head) on the matrix cores, its 4 waves splitting the keys.
 #include <hip/hip_runtime.h>
 
 #include <math.h>
@@ -544,15 +544,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
 
 // ---------------------------------------------------------------------------
 // Decode-shaped attention on the matrix cores (16-bit cache, head_dim 128,
-// block sizes a multiple of 64, at most 16 query heads per kv head): one wave
-// per (token, kv head) streams that head's keys in 64-key chunks.  The query
+// block sizes a multiple of 64, at most 16 query heads per kv head): a wave
+// streams its share of one (token, kv head)'s keys in 64-key chunks.  The query
 // heads of the group are the 16 columns of v_mfma_f32_16x16x32 tiles:
 //   S^T = K . Q^T    (A = 16 keys x 32 dims straight from the cache, B = q)
 //   O^T += V^T . P^T (A = V^T from a wave-private LDS transpose of the chunk,
 //                     B = P^T, again S^T's own registers: a lane holds keys
 //                     32 u + 4 g + {0..3} and 32 u + 16 + 4 g + {0..3}, g = lane/16)
 // The next chunk's K and V loads are in flight during the current chunk's math.
-// A workgroup holds 4 waves (4 kv heads of one token).
+// A workgroup is one (token, kv head): its 4 waves take the chunks in turn (wave w
+// chunks w, w + 4, ...) and merge their softmax states through LDS at the end, so
+// the longest contexts, which set a decode batch's tail, take a quarter of the
+// time, without a second launch.
 constexpr int kFdVRow = 64 * 2 + 8;              // V^T row: 64 keys, padded
 constexpr int kFdWaveLds = kFaHd * kFdVRow;      // per wave
 constexpr int kFdLds = 4 * kFdWaveLds;
@@ -587,9 +590,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   const int64_t t = blockIdx.x;
-  const int kvh = blockIdx.y * 4 + wave;
-  if (kvh >= kv_heads) return;  // whole waves; no workgroup barrier below
-  if (skip_uniform_tiles && fa_tile_uniform(qseq, tokens, t / kFaBq)) return;  // fa_prefill_kernel's
+  const int kvh = blockIdx.y;
+  // workgroup-uniform: the whole workgroup leaves (fa_prefill_kernel's tile)
+  if (skip_uniform_tiles && fa_tile_uniform(qseq, tokens, t / kFaBq)) return;
   const int G = q_heads / kv_heads;
   const int col = lane & 15, g = lane >> 4;
   const bool head_ok = col < G;
@@ -637,8 +640,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
       vr[i] = k0 + key < L ? v : u32x4{0, 0, 0, 0};           // past L: zero
     }
   };
-  if (c0 < c1) load_chunk(c0);
-  for (int c = c0; c < c1; ++c) {
+  if (c0 + wave < c1) load_chunk(c0 + wave);
+  for (int c = c0 + wave; c < c1; c += 4) {
     // V^T into this wave's LDS: dim 8 col + e, keys 16 i4 + 4 g + {0..3}
 #pragma unroll
     for (int i4 = 0; i4 < 4; ++i4)
@@ -658,7 +661,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
 #pragma unroll
       for (int s = 0; s < 4; ++s) st[kt] = M::mma(__builtin_bit_cast(v8, kr[kt][s]), qf[s], st[kt]);
     }
-    if (c + 1 < c1) load_chunk(c + 1);  // in flight during the math below
+    if (c + 4 < c1) load_chunk(c + 4);  // in flight during the math below
     __builtin_amdgcn_wave_barrier();
     // online softmax per head (lane column); element j of tile kt is key 64 c + 16 kt + 4 g + j
     float mx = -INFINITY;
@@ -705,30 +708,56 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
     }
     __builtin_amdgcn_wave_barrier();  // this chunk's V^T reads before the next chunk's writes
   }
-  // O^T: lane column = head col, dims 16 d + 4 g + j
+  // Merge the 4 waves' states.  Each wave's V^T area is free now and takes its
+  // O^T [128 dims][16 heads] (lane column = head col, dims 16 d + 4 g + j), then
+  // m[16] and l[16]; m is in exp2 units, -inf for a wave without keys.
+  float* pw = reinterpret_cast<float*>(vt);
+#pragma unroll
+  for (int d = 0; d < kFaHd / 16; ++d)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) pw[(16 * d + 4 * g + j) * 16 + col] = o[d][j];
+  if (g == 0) {
+    pw[kFaHd * 16 + col] = m;
+    pw[kFaHd * 16 + 16 + col] = l;
+  }
+  __syncthreads();
+  // thread: head hc, dims d0 .. d0 + 7
+  const int hc = threadIdx.x & 15, d0 = 8 * (threadIdx.x >> 4);
+  auto wpart = [&](int w) { return reinterpret_cast<const float*>(lds + w * kFdWaveLds); };
+  float mw[4], mall = -INFINITY;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    mw[w] = wpart(w)[kFaHd * 16 + hc];
+    mall = fmaxf(mall, mw[w]);
+  }
+  float lsum = 0.0f, ov[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    const float sc = mw[w] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mw[w] - mall);
+    const float* pv = wpart(w);
+    lsum += sc * pv[kFaHd * 16 + 16 + hc];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ov[e] += sc * pv[(d0 + e) * 16 + hc];
+  }
+  if (hc >= G) return;
+  const int hq = kvh * G + hc;
   if constexpr (SPLIT) {  // unnormalised partial O, running max (exp2 units) and sum
-    if (head_ok) {
-      const int64_t pi = (t * q_heads + h) * gridDim.z + blockIdx.z;
-      float* po = part + pi * kFaHd;
-#pragma unroll
-      for (int d = 0; d < kFaHd / 16; ++d) st16(po + 16 * d + 4 * g, __builtin_bit_cast(u32x4, o[d]));
-      if (g == 0) {
-        float* pml = part + tokens * q_heads * gridDim.z * kFaHd + 2 * pi;
-        pml[0] = m;
-        pml[1] = l;
-      }
+    const int64_t pi = (t * q_heads + hq) * gridDim.z + blockIdx.z;
+    float* po = part + pi * kFaHd + d0;
+    st16(po, __builtin_bit_cast(u32x4, f32x4{ov[0], ov[1], ov[2], ov[3]}));
+    st16(po + 4, __builtin_bit_cast(u32x4, f32x4{ov[4], ov[5], ov[6], ov[7]}));
+    if (d0 == 0) {
+      float* pml = part + tokens * q_heads * gridDim.z * kFaHd + 2 * pi;
+      pml[0] = mall;
+      pml[1] = lsum;
     }
-  } else if (head_ok) {
-    const float inv = l > 0.0f ? 1.0f / l : 0.0f;
-    T* orow = out + (t * q_heads + h) * kFaHd;
+  } else {
+    const float inv = lsum > 0.0f ? 1.0f / lsum : 0.0f;
+    typedef T t8 __attribute__((ext_vector_type(8)));
+    t8 v;
 #pragma unroll
-    for (int d = 0; d < kFaHd / 16; ++d) {
-      typedef T t4 __attribute__((ext_vector_type(4)));
-      t4 v;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) v[e] = (T)(o[d][e] * inv);
-      *reinterpret_cast<t4*>(orow + 16 * d + 4 * g) = v;
-    }
+    for (int e = 0; e < 8; ++e) v[e] = (T)(ov[e] * inv);
+    *reinterpret_cast<t8*>(out + (t * q_heads + hq) * kFaHd + d0) = v;
   }
 }
 
@@ -1171,8 +1200,8 @@ int attention_dispatch(const void* q, void* out, const void* kc, const void* vc,
     if (rc != NVF_OK) return rc;
   }
   if (dec) {
-    const dim3 grid((unsigned)tokens, kvg, nz);
     if constexpr (sizeof(T) == 2) {
+      const dim3 grid((unsigned)tokens, (unsigned)kv_heads, nz);  // one workgroup per (token, kv head)
       static std::once_flag dec_once;
       std::call_once(dec_once, [] {
         (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&fa_decode_kernel<T, false>),
@@ -1189,6 +1218,7 @@ int attention_dispatch(const void* q, void* out, const void* kc, const void* vc,
                                                               kv_heads, bs, max_blocks, sl, q_stride, tiles, 0,
                                                               nullptr);
     } else {
+      const dim3 grid((unsigned)tokens, kvg, nz);  // 4 kv heads of one token per workgroup
       if (split)
         fa_decode_f32_kernel<true><<<grid, 256, 0, st>>>(qt, ot, kt, vt, qseq, qlen, tables, tokens, q_heads,
                                                          kv_heads, bs, max_blocks, sl, q_stride, tiles, skeys, part);
