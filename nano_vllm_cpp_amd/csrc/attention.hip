@@ -543,6 +543,65 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
 }
 
 // ---------------------------------------------------------------------------
+// The decode kernels' end: a workgroup is one (token, kv head) whose 4 waves each
+// hold a softmax state over their share of the keys.  Each wave has written its
+// unnormalised O^T as [128 dims][16 heads] floats at pw(w), then m[16] (exp2
+// units, -inf for a wave without keys) and l[16].  After the barrier, thread
+// (head hc = tid % 16, dims d0 = 8 (tid / 16) .. + 7) merges the 4 states and
+// stores either the normalised output or the merged partial of split blockIdx.z.
+template <typename TO, bool SPLIT, typename PW>
+__device__ __forceinline__ void decode_merge_store(PW pw, TO* __restrict__ out, float* __restrict__ part, int64_t t,
+                                                   int64_t tokens, int q_heads, int kvh, int G) {
+  __syncthreads();
+  const int hc = threadIdx.x & 15, d0 = 8 * (threadIdx.x >> 4);
+  float mw[4], mall = -INFINITY;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    mw[w] = pw(w)[kFaHd * 16 + hc];
+    mall = fmaxf(mall, mw[w]);
+  }
+  float lsum = 0.0f, ov[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    const float sc = mw[w] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mw[w] - mall);
+    const float* pv = pw(w);
+    lsum += sc * pv[kFaHd * 16 + 16 + hc];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ov[e] += sc * pv[(d0 + e) * 16 + hc];
+  }
+  if (hc >= G) return;
+  const int hq = kvh * G + hc;
+  if constexpr (SPLIT) {  // unnormalised partial O, running max (exp2 units) and sum
+    const int64_t pi = (t * q_heads + hq) * gridDim.z + blockIdx.z;
+    float* po = part + pi * kFaHd + d0;
+    st16(po, __builtin_bit_cast(u32x4, f32x4{ov[0], ov[1], ov[2], ov[3]}));
+    st16(po + 4, __builtin_bit_cast(u32x4, f32x4{ov[4], ov[5], ov[6], ov[7]}));
+    if (d0 == 0) {
+      float* pml = part + tokens * q_heads * gridDim.z * kFaHd + 2 * pi;
+      pml[0] = mall;
+      pml[1] = lsum;
+    }
+  } else {
+    const float inv = lsum > 0.0f ? 1.0f / lsum : 0.0f;
+    float v[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = ov[e] * inv;
+    TO* orow = out + (t * q_heads + hq) * kFaHd + d0;
+    if constexpr (sizeof(TO) == 4) {
+      st16(orow, __builtin_bit_cast(u32x4, f32x4{v[0], v[1], v[2], v[3]}));
+      st16(orow + 4, __builtin_bit_cast(u32x4, f32x4{v[4], v[5], v[6], v[7]}));
+    } else {
+      typedef TO t8 __attribute__((ext_vector_type(8)));
+      t8 r;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) r[e] = (TO)v[e];
+      *reinterpret_cast<t8*>(orow) = r;
+    }
+  }
+}
+constexpr int kDecMergeFloats = kFaHd * 16 + 32;  // one wave's state in the merge
+
+// ---------------------------------------------------------------------------
 // Decode-shaped attention on the matrix cores (16-bit cache, head_dim 128,
 // block sizes a multiple of 64, at most 16 query heads per kv head): a wave
 // streams its share of one (token, kv head)'s keys in 64-key chunks.  The query
@@ -720,51 +779,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
     pw[kFaHd * 16 + col] = m;
     pw[kFaHd * 16 + 16 + col] = l;
   }
-  __syncthreads();
-  // thread: head hc, dims d0 .. d0 + 7
-  const int hc = threadIdx.x & 15, d0 = 8 * (threadIdx.x >> 4);
-  auto wpart = [&](int w) { return reinterpret_cast<const float*>(lds + w * kFdWaveLds); };
-  float mw[4], mall = -INFINITY;
-#pragma unroll
-  for (int w = 0; w < 4; ++w) {
-    mw[w] = wpart(w)[kFaHd * 16 + hc];
-    mall = fmaxf(mall, mw[w]);
-  }
-  float lsum = 0.0f, ov[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-  for (int w = 0; w < 4; ++w) {
-    const float sc = mw[w] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mw[w] - mall);
-    const float* pv = wpart(w);
-    lsum += sc * pv[kFaHd * 16 + 16 + hc];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) ov[e] += sc * pv[(d0 + e) * 16 + hc];
-  }
-  if (hc >= G) return;
-  const int hq = kvh * G + hc;
-  if constexpr (SPLIT) {  // unnormalised partial O, running max (exp2 units) and sum
-    const int64_t pi = (t * q_heads + hq) * gridDim.z + blockIdx.z;
-    float* po = part + pi * kFaHd + d0;
-    st16(po, __builtin_bit_cast(u32x4, f32x4{ov[0], ov[1], ov[2], ov[3]}));
-    st16(po + 4, __builtin_bit_cast(u32x4, f32x4{ov[4], ov[5], ov[6], ov[7]}));
-    if (d0 == 0) {
-      float* pml = part + tokens * q_heads * gridDim.z * kFaHd + 2 * pi;
-      pml[0] = mall;
-      pml[1] = lsum;
-    }
-  } else {
-    const float inv = lsum > 0.0f ? 1.0f / lsum : 0.0f;
-    typedef T t8 __attribute__((ext_vector_type(8)));
-    t8 v;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) v[e] = (T)(ov[e] * inv);
-    *reinterpret_cast<t8*>(out + (t * q_heads + hq) * kFaHd + d0) = v;
-  }
+  decode_merge_store<T, SPLIT>([&](int w) { return reinterpret_cast<const float*>(lds + w * kFdWaveLds); }, out, part,
+                               t, tokens, q_heads, kvh, G);
 }
 
 // ---------------------------------------------------------------------------
 // Decode-shaped attention for fp32 caches on the fp32 matrix cores
 // (v_mfma_f32_16x16x4_f32), head_dim 128, at most 16 query heads per kv head:
-// one wave per (token, kv head), the group's query heads the 16 columns, 16-key
+// one workgroup per (token, kv head) whose 4 waves take the chunks in turn and
+// merge in LDS (as fa_decode_kernel), the group's query heads the 16 columns, 16-key
 // chunks straight from the cache into registers (the next chunk's loads in
 // flight during the current chunk's math; no LDS).
 //   S^T = K . Q^T   32 MFMAs; MFMA 4 i + e contracts dim 32 (lane / 16) + 4 i + e,
@@ -783,10 +806,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
     bool skip_uniform_tiles, int split_keys, float* __restrict__ part) {
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  __shared__ float merge[4][kDecMergeFloats];
   const int64_t t = blockIdx.x;
-  const int kvh = blockIdx.y * 4 + wave;
-  if (kvh >= kv_heads) return;  // whole waves; no workgroup barrier below
-  if (skip_uniform_tiles && fa_tile_uniform(qseq, tokens, t / kFaBq)) return;  // fa_prefill_f32_kernel's
+  const int kvh = blockIdx.y;
+  // workgroup-uniform: the whole workgroup leaves (fa_prefill_f32_kernel's tile)
+  if (skip_uniform_tiles && fa_tile_uniform(qseq, tokens, t / kFaBq)) return;
   const int G = q_heads / kv_heads;
   const int col = lane & 15, g = lane >> 4;
   const bool head_ok = col < G;
@@ -883,43 +907,29 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
     }
   };
 
+  // wave w takes chunks w, w + 4, ...; two per trip, the register sets trading roles
   u32x4 ka[8], va[8], kb_[8], vb_[8];
-  if (c0 < c1) load(c0, ka, va);
-  for (int c = c0; c < c1; c += 2) {  // two chunks per trip: the register sets trade roles
-    if (c + 1 < c1) load(c + 1, kb_, vb_);
+  if (c0 + wave < c1) load(c0 + wave, ka, va);
+  for (int c = c0 + wave; c < c1; c += 8) {
+    if (c + 4 < c1) load(c + 4, kb_, vb_);
     compute(c, ka, va);
-    if (c + 1 < c1) {
-      if (c + 2 < c1) load(c + 2, ka, va);
-      compute(c + 1, kb_, vb_);
+    if (c + 4 < c1) {
+      if (c + 8 < c1) load(c + 8, ka, va);
+      compute(c + 4, kb_, vb_);
     }
   }
   // O^T: register v of tile d is dim 8 (4 g + v) + d of head col
-  if constexpr (SPLIT) {  // unnormalised partial O, running max (exp2 units) and sum
-    if (head_ok) {
-      const int64_t pi = (t * q_heads + h) * gridDim.z + blockIdx.z;
-      float* po = part + pi * kFaHd;
+  float* pw = merge[wave];
 #pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        float* p = po + 8 * (4 * g + v);
-        st16(p, __builtin_bit_cast(u32x4, f32x4{o[0][v], o[1][v], o[2][v], o[3][v]}));
-        st16(p + 4, __builtin_bit_cast(u32x4, f32x4{o[4][v], o[5][v], o[6][v], o[7][v]}));
-      }
-      if (g == 0) {
-        float* pml = part + tokens * q_heads * gridDim.z * kFaHd + 2 * pi;
-        pml[0] = m;
-        pml[1] = l;
-      }
-    }
-  } else if (head_ok) {
-    const float inv = l > 0.0f ? 1.0f / l : 0.0f;
-    float* orow = out + (t * q_heads + h) * kFaHd;
+  for (int d = 0; d < 8; ++d)
 #pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      float* p = orow + 8 * (4 * g + v);
-      st16(p, __builtin_bit_cast(u32x4, f32x4{o[0][v] * inv, o[1][v] * inv, o[2][v] * inv, o[3][v] * inv}));
-      st16(p + 4, __builtin_bit_cast(u32x4, f32x4{o[4][v] * inv, o[5][v] * inv, o[6][v] * inv, o[7][v] * inv}));
-    }
+    for (int v = 0; v < 4; ++v) pw[(8 * (4 * g + v) + d) * 16 + col] = o[d][v];
+  if (g == 0) {
+    pw[kFaHd * 16 + col] = m;
+    pw[kFaHd * 16 + 16 + col] = l;
   }
+  decode_merge_store<float, SPLIT>([&](int w) { return static_cast<const float*>(merge[w]); }, out, part, t, tokens,
+                                   q_heads, kvh, G);
 }
 
 // ---------------------------------------------------------------------------
@@ -1140,7 +1150,6 @@ int attention_dispatch(const void* q, void* out, const void* kc, const void* vc,
   const float sl = scale * 1.4426950408889634f;
   const int64_t ntiles = (tokens + kFaBq - 1) / kFaBq;
   if (ntiles * q_heads > INT32_MAX) return fail(NVF_ERR_INVALID, "paged_attention: too many tiles");
-  const unsigned kvg = (unsigned)((kv_heads + 3) / 4);
   // Matrix-core paths (head_dim 128, 16-byte rows, scale > 0: the kernels take the
   // running max on unscaled scores).  Tiles: 128 tokens of one sequence, unless the
   // caller promised a decode batch (max_query_len 1) or there are fewer tokens
@@ -1218,7 +1227,7 @@ int attention_dispatch(const void* q, void* out, const void* kc, const void* vc,
                                                               kv_heads, bs, max_blocks, sl, q_stride, tiles, 0,
                                                               nullptr);
     } else {
-      const dim3 grid((unsigned)tokens, kvg, nz);  // 4 kv heads of one token per workgroup
+      const dim3 grid((unsigned)tokens, (unsigned)kv_heads, nz);  // one workgroup per (token, kv head)
       if (split)
         fa_decode_f32_kernel<true><<<grid, 256, 0, st>>>(qt, ot, kt, vt, qseq, qlen, tables, tokens, q_heads,
                                                          kv_heads, bs, max_blocks, sl, q_stride, tiles, skeys, part);
