@@ -569,7 +569,7 @@ __device__ __forceinline__ void decode_merge_store(PW pw, TO* __restrict__ out, 
 #pragma unroll
     for (int e = 0; e < 8; ++e) ov[e] += sc * pv[(d0 + e) * 16 + hc];
   }
-  if (hc >= G) return;
+  if (hc >= G) return;  // (callers that loop re-converge at their own barrier)
   const int hq = kvh * G + hc;
   if constexpr (SPLIT) {  // unnormalised partial O, running max (exp2 units) and sum
     const int64_t pi = (t * q_heads + hq) * gridDim.z + blockIdx.z;
@@ -637,150 +637,159 @@ struct Mfma16x16<_Float16> {
   }
 };
 
-template <typename T, bool SPLIT>
+template <typename T, bool SPLIT, bool SKIP>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void fa_decode_kernel(
     const T* __restrict__ q, T* __restrict__ out, const T* __restrict__ kc, const T* __restrict__ vc,
     const int32_t* __restrict__ qseq, const int32_t* __restrict__ qlen, const int32_t* __restrict__ tables,
     int64_t tokens, int q_heads, int kv_heads, int bs, int max_blocks, float scale_log2, int64_t q_stride,
-    bool skip_uniform_tiles, int split_keys, float* __restrict__ part) {
+    int split_keys, float* __restrict__ part) {
   using M = Mfma16x16<T>;
   using v8 = typename M::v8;
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   const int64_t t = blockIdx.x;
-  const int kvh = blockIdx.y;
   // workgroup-uniform: the whole workgroup leaves (fa_prefill_kernel's tile)
-  if (skip_uniform_tiles && fa_tile_uniform(qseq, tokens, t / kFaBq)) return;
-  const int G = q_heads / kv_heads;
-  const int col = lane & 15, g = lane >> 4;
-  const bool head_ok = col < G;
-  const int h = kvh * G + col;
-  const int L = qlen[t];
-  const int64_t seq = qseq[t];
-  const int64_t kv_stride = (int64_t)kv_heads * kFaHd;
-  const int32_t* tab = tables + seq * max_blocks;
-  uint8_t* vt = lds + wave * kFdWaveLds;
+  if (SKIP && fa_tile_uniform(qseq, tokens, t / kFaBq)) return;
+  // The tiles' second launch (SKIP) has one workgroup per token, so that its many
+  // exiting workgroups stay few, and walks the kv heads; otherwise blockIdx.y is
+  // the kv head (one trip, known at compile time).
+  const int kvh0 = SKIP ? 0 : (int)blockIdx.y;
+  const int kvh1 = SKIP ? kv_heads : kvh0 + 1;
+  for (int kvh = kvh0; kvh < kvh1; ++kvh) {
+    const int G = q_heads / kv_heads;
+    const int col = lane & 15, g = lane >> 4;
+    const bool head_ok = col < G;
+    const int h = kvh * G + col;
+    const int L = qlen[t];
+    const int64_t seq = qseq[t];
+    const int64_t kv_stride = (int64_t)kv_heads * kFaHd;
+    const int32_t* tab = tables + seq * max_blocks;
+    uint8_t* vt = lds + wave * kFdWaveLds;
 
-  v8 qf[kFaHd / 32];  // B operand: head col, dims 32 s + 8 g
-#pragma unroll
-  for (int s = 0; s < kFaHd / 32; ++s) {
-    const u32x4 v = head_ok ? ld16(q + t * q_stride + (int64_t)h * kFaHd + 32 * s + 8 * g) : u32x4{0, 0, 0, 0};
-    qf[s] = __builtin_bit_cast(v8, v);
-  }
-  f32x4 o[kFaHd / 16];
-#pragma unroll
-  for (int d = 0; d < kFaHd / 16; ++d) o[d] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-  float m = -INFINITY, l = 0.0f;
+    v8 qf[kFaHd / 32];  // B operand: head col, dims 32 s + 8 g
+  #pragma unroll
+    for (int s = 0; s < kFaHd / 32; ++s) {
+      const u32x4 v = head_ok ? ld16(q + t * q_stride + (int64_t)h * kFaHd + 32 * s + 8 * g) : u32x4{0, 0, 0, 0};
+      qf[s] = __builtin_bit_cast(v8, v);
+    }
+    f32x4 o[kFaHd / 16];
+  #pragma unroll
+    for (int d = 0; d < kFaHd / 16; ++d) o[d] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    float m = -INFINITY, l = 0.0f;
 
-  // this wave's chunks: all of the token's, or split blockIdx.z's split_keys keys of them
-  int c0 = 0, c1 = L > 0 ? (L + 63) / 64 : 0;
-  if constexpr (SPLIT) {
-    c0 = (int)blockIdx.z * (split_keys / 64);
-    c1 = min(c1, c0 + split_keys / 64);
-  }
-  // chunk loads: K as MFMA A operands (key 16 kt + col, dims 32 s + 8 g);
-  // V rows for the transpose (key 4 i + g... : lane l covers dims 8 (l % 16) of
-  // keys 16 i + (l / 16) * 4 + {0..3} over i < 4, 16 loads)
-  u32x4 kr[4][4], vr[16];
-  auto load_chunk = [&](int c) {
-    const int k0 = c * 64;
-    const int64_t row0 = (int64_t)tab[k0 / bs] * bs + k0 % bs;
-    const T* kb = kc + row0 * kv_stride + (int64_t)kvh * kFaHd;
-#pragma unroll
-    for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-      for (int s = 0; s < 4; ++s) kr[kt][s] = ld16(kb + (int64_t)(16 * kt + col) * kv_stride + 32 * s + 8 * g);
-    const T* vb = vc + row0 * kv_stride + (int64_t)kvh * kFaHd + 8 * col;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int key = 16 * (i >> 2) + 4 * g + (i & 3);
-      const u32x4 v = ld16(vb + (int64_t)key * kv_stride);  // inside the chunk's block: no branch
-      vr[i] = k0 + key < L ? v : u32x4{0, 0, 0, 0};           // past L: zero
+    // this wave's chunks: all of the token's, or split blockIdx.z's split_keys keys of them
+    int c0 = 0, c1 = L > 0 ? (L + 63) / 64 : 0;
+    if constexpr (SPLIT) {
+      c0 = (int)blockIdx.z * (split_keys / 64);
+      c1 = min(c1, c0 + split_keys / 64);
     }
-  };
-  if (c0 + wave < c1) load_chunk(c0 + wave);
-  for (int c = c0 + wave; c < c1; c += 4) {
-    // V^T into this wave's LDS: dim 8 col + e, keys 16 i4 + 4 g + {0..3}
-#pragma unroll
-    for (int i4 = 0; i4 < 4; ++i4)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int sh = (e & 1) * 16;
-        const uint32_t lo = ((vr[4 * i4][e >> 1] >> sh) & 0xffffu) | (((vr[4 * i4 + 1][e >> 1] >> sh) & 0xffffu) << 16);
-        const uint32_t hi = ((vr[4 * i4 + 2][e >> 1] >> sh) & 0xffffu) | (((vr[4 * i4 + 3][e >> 1] >> sh) & 0xffffu) << 16);
-        typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-        *reinterpret_cast<u32x2*>(vt + (8 * col + e) * kFdVRow + (16 * i4 + 4 * g) * 2) = u32x2{lo, hi};
+    // chunk loads: K as MFMA A operands (key 16 kt + col, dims 32 s + 8 g);
+    // V rows for the transpose (key 4 i + g... : lane l covers dims 8 (l % 16) of
+    // keys 16 i + (l / 16) * 4 + {0..3} over i < 4, 16 loads)
+    u32x4 kr[4][4], vr[16];
+    auto load_chunk = [&](int c) {
+      const int k0 = c * 64;
+      const int64_t row0 = (int64_t)tab[k0 / bs] * bs + k0 % bs;
+      const T* kb = kc + row0 * kv_stride + (int64_t)kvh * kFaHd;
+  #pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+  #pragma unroll
+        for (int s = 0; s < 4; ++s) kr[kt][s] = ld16(kb + (int64_t)(16 * kt + col) * kv_stride + 32 * s + 8 * g);
+      const T* vb = vc + row0 * kv_stride + (int64_t)kvh * kFaHd + 8 * col;
+  #pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int key = 16 * (i >> 2) + 4 * g + (i & 3);
+        const u32x4 v = ld16(vb + (int64_t)key * kv_stride);  // inside the chunk's block: no branch
+        vr[i] = k0 + key < L ? v : u32x4{0, 0, 0, 0};           // past L: zero
       }
-    // S^T = K . Q^T, 4 tiles of 16 keys
-    f32x4 st[4];
-#pragma unroll
-    for (int kt = 0; kt < 4; ++kt) {
-      st[kt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-      for (int s = 0; s < 4; ++s) st[kt] = M::mma(__builtin_bit_cast(v8, kr[kt][s]), qf[s], st[kt]);
+    };
+    if (c0 + wave < c1) load_chunk(c0 + wave);
+    for (int c = c0 + wave; c < c1; c += 4) {
+      // V^T into this wave's LDS: dim 8 col + e, keys 16 i4 + 4 g + {0..3}
+  #pragma unroll
+      for (int i4 = 0; i4 < 4; ++i4)
+  #pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int sh = (e & 1) * 16;
+          const uint32_t lo =
+              ((vr[4 * i4][e >> 1] >> sh) & 0xffffu) | (((vr[4 * i4 + 1][e >> 1] >> sh) & 0xffffu) << 16);
+          const uint32_t hi =
+              ((vr[4 * i4 + 2][e >> 1] >> sh) & 0xffffu) | (((vr[4 * i4 + 3][e >> 1] >> sh) & 0xffffu) << 16);
+          typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+          *reinterpret_cast<u32x2*>(vt + (8 * col + e) * kFdVRow + (16 * i4 + 4 * g) * 2) = u32x2{lo, hi};
+        }
+      // S^T = K . Q^T, 4 tiles of 16 keys
+      f32x4 st[4];
+  #pragma unroll
+      for (int kt = 0; kt < 4; ++kt) {
+        st[kt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  #pragma unroll
+        for (int s = 0; s < 4; ++s) st[kt] = M::mma(__builtin_bit_cast(v8, kr[kt][s]), qf[s], st[kt]);
+      }
+      if (c + 4 < c1) load_chunk(c + 4);  // in flight during the math below
+      __builtin_amdgcn_wave_barrier();
+      // online softmax per head (lane column); element j of tile kt is key 64 c + 16 kt + 4 g + j
+      float mx = -INFINITY;
+  #pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+  #pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int key = c * 64 + 16 * kt + 4 * g + j;
+          const float x = key < L ? st[kt][j] * scale_log2 : -INFINITY;
+          st[kt][j] = x;
+          mx = fmaxf(mx, x);
+        }
+      mx = fmaxf(mx, __shfl_xor(mx, 16));
+      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      const float m_new = fmaxf(m, mx);
+      const float m_use = m_new == -INFINITY ? 0.0f : m_new;
+      const float alpha = __builtin_amdgcn_exp2f(m - m_use);
+      float ls = 0.0f;
+      v8 pb[2];
+  #pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+  #pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float p = __builtin_amdgcn_exp2f(st[kt][j] - m_use);
+          ls += p;
+          pb[kt >> 1][(kt & 1) * 4 + j] = (T)p;
+        }
+      ls += __shfl_xor(ls, 16);
+      ls += __shfl_xor(ls, 32);
+      l = l * alpha + ls;
+      m = m_new;
+      // O^T += V^T . P^T: dims 16 d + col, key step u: keys 32 u + 4 g + {0..3}, 32 u + 16 + 4 g + {0..3}
+  #pragma unroll
+      for (int d = 0; d < kFaHd / 16; ++d) {
+        o[d] *= alpha;
+  #pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+          const uint8_t* r = vt + (16 * d + col) * kFdVRow + (32 * u + 4 * g) * 2;
+          const u32x2 lo = *reinterpret_cast<const u32x2*>(r);
+          const u32x2 hi = *reinterpret_cast<const u32x2*>(r + 32);
+          o[d] = M::mma(__builtin_bit_cast(v8, u32x4{lo[0], lo[1], hi[0], hi[1]}), pb[u], o[d]);
+        }
+      }
+      __builtin_amdgcn_wave_barrier();  // this chunk's V^T reads before the next chunk's writes
     }
-    if (c + 4 < c1) load_chunk(c + 4);  // in flight during the math below
-    __builtin_amdgcn_wave_barrier();
-    // online softmax per head (lane column); element j of tile kt is key 64 c + 16 kt + 4 g + j
-    float mx = -INFINITY;
-#pragma unroll
-    for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int key = c * 64 + 16 * kt + 4 * g + j;
-        const float x = key < L ? st[kt][j] * scale_log2 : -INFINITY;
-        st[kt][j] = x;
-        mx = fmaxf(mx, x);
-      }
-    mx = fmaxf(mx, __shfl_xor(mx, 16));
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
-    const float m_new = fmaxf(m, mx);
-    const float m_use = m_new == -INFINITY ? 0.0f : m_new;
-    const float alpha = __builtin_amdgcn_exp2f(m - m_use);
-    float ls = 0.0f;
-    v8 pb[2];
-#pragma unroll
-    for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const float p = __builtin_amdgcn_exp2f(st[kt][j] - m_use);
-        ls += p;
-        pb[kt >> 1][(kt & 1) * 4 + j] = (T)p;
-      }
-    ls += __shfl_xor(ls, 16);
-    ls += __shfl_xor(ls, 32);
-    l = l * alpha + ls;
-    m = m_new;
-    // O^T += V^T . P^T: dims 16 d + col, key step u: keys 32 u + 4 g + {0..3}, 32 u + 16 + 4 g + {0..3}
-#pragma unroll
-    for (int d = 0; d < kFaHd / 16; ++d) {
-      o[d] *= alpha;
-#pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-        const uint8_t* r = vt + (16 * d + col) * kFdVRow + (32 * u + 4 * g) * 2;
-        const u32x2 lo = *reinterpret_cast<const u32x2*>(r);
-        const u32x2 hi = *reinterpret_cast<const u32x2*>(r + 32);
-        o[d] = M::mma(__builtin_bit_cast(v8, u32x4{lo[0], lo[1], hi[0], hi[1]}), pb[u], o[d]);
-      }
+    // Merge the 4 waves' states.  Each wave's V^T area is free now and takes its
+    // O^T [128 dims][16 heads] (lane column = head col, dims 16 d + 4 g + j), then
+    // m[16] and l[16]; m is in exp2 units, -inf for a wave without keys.
+    float* pw = reinterpret_cast<float*>(vt);
+  #pragma unroll
+    for (int d = 0; d < kFaHd / 16; ++d)
+  #pragma unroll
+      for (int j = 0; j < 4; ++j) pw[(16 * d + 4 * g + j) * 16 + col] = o[d][j];
+    if (g == 0) {
+      pw[kFaHd * 16 + col] = m;
+      pw[kFaHd * 16 + 16 + col] = l;
     }
-    __builtin_amdgcn_wave_barrier();  // this chunk's V^T reads before the next chunk's writes
+    decode_merge_store<T, SPLIT>([&](int w) { return reinterpret_cast<const float*>(lds + w * kFdWaveLds); }, out, part,
+                                 t, tokens, q_heads, kvh, G);
+    __syncthreads();  // the merge's LDS reads before the next kv head's writes
   }
-  // Merge the 4 waves' states.  Each wave's V^T area is free now and takes its
-  // O^T [128 dims][16 heads] (lane column = head col, dims 16 d + 4 g + j), then
-  // m[16] and l[16]; m is in exp2 units, -inf for a wave without keys.
-  float* pw = reinterpret_cast<float*>(vt);
-#pragma unroll
-  for (int d = 0; d < kFaHd / 16; ++d)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) pw[(16 * d + 4 * g + j) * 16 + col] = o[d][j];
-  if (g == 0) {
-    pw[kFaHd * 16 + col] = m;
-    pw[kFaHd * 16 + 16 + col] = l;
-  }
-  decode_merge_store<T, SPLIT>([&](int w) { return reinterpret_cast<const float*>(lds + w * kFdWaveLds); }, out, part,
-                               t, tokens, q_heads, kvh, G);
 }
 
 // ---------------------------------------------------------------------------
@@ -798,138 +807,143 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
 //                   the 8 tiles are 32 consecutive bytes of its V row.
 constexpr int kFd32Bk = 16;  // keys per chunk
 
-template <bool SPLIT>
+template <bool SPLIT, bool SKIP>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void fa_decode_f32_kernel(
     const float* __restrict__ q, float* __restrict__ out, const float* __restrict__ kc, const float* __restrict__ vc,
     const int32_t* __restrict__ qseq, const int32_t* __restrict__ qlen, const int32_t* __restrict__ tables,
     int64_t tokens, int q_heads, int kv_heads, int bs, int max_blocks, float scale_log2, int64_t q_stride,
-    bool skip_uniform_tiles, int split_keys, float* __restrict__ part) {
+    int split_keys, float* __restrict__ part) {
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   __shared__ float merge[4][kDecMergeFloats];
   const int64_t t = blockIdx.x;
-  const int kvh = blockIdx.y;
   // workgroup-uniform: the whole workgroup leaves (fa_prefill_f32_kernel's tile)
-  if (skip_uniform_tiles && fa_tile_uniform(qseq, tokens, t / kFaBq)) return;
-  const int G = q_heads / kv_heads;
-  const int col = lane & 15, g = lane >> 4;
-  const bool head_ok = col < G;
-  const int h = kvh * G + col;
-  const int L = qlen[t];
-  const int64_t seq = qseq[t];
-  const int64_t kv_stride = (int64_t)kv_heads * kFaHd;
-  const int32_t* tab = tables + seq * max_blocks;
+  if (SKIP && fa_tile_uniform(qseq, tokens, t / kFaBq)) return;
+  // as fa_decode_kernel: the tiles' second launch walks the kv heads per token
+  const int kvh0 = SKIP ? 0 : (int)blockIdx.y;
+  const int kvh1 = SKIP ? kv_heads : kvh0 + 1;
+  for (int kvh = kvh0; kvh < kvh1; ++kvh) {
+    const int G = q_heads / kv_heads;
+    const int col = lane & 15, g = lane >> 4;
+    const bool head_ok = col < G;
+    const int h = kvh * G + col;
+    const int L = qlen[t];
+    const int64_t seq = qseq[t];
+    const int64_t kv_stride = (int64_t)kv_heads * kFaHd;
+    const int32_t* tab = tables + seq * max_blocks;
 
-  f32x4 qf[8];  // B operand: head col, dims 32 g + 4 i + e
-#pragma unroll
-  for (int i = 0; i < 8; ++i)
-    qf[i] = head_ok ? __builtin_bit_cast(f32x4, ld16(q + t * q_stride + (int64_t)h * kFaHd + 32 * g + 4 * i))
-                    : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-  f32x4 o[8];
-#pragma unroll
-  for (int d = 0; d < 8; ++d) o[d] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-  float m = -INFINITY, l = 0.0f;
-  // this wave's chunks: all of the token's, or split blockIdx.z's split_keys keys of them
-  int c0 = 0, c1 = L > 0 ? (L + kFd32Bk - 1) / kFd32Bk : 0;
-  if constexpr (SPLIT) {
-    c0 = (int)blockIdx.z * (split_keys / kFd32Bk);
-    c1 = min(c1, c0 + split_keys / kFd32Bk);
-  }
+    f32x4 qf[8];  // B operand: head col, dims 32 g + 4 i + e
+  #pragma unroll
+    for (int i = 0; i < 8; ++i)
+      qf[i] = head_ok ? __builtin_bit_cast(f32x4, ld16(q + t * q_stride + (int64_t)h * kFaHd + 32 * g + 4 * i))
+                      : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    f32x4 o[8];
+  #pragma unroll
+    for (int d = 0; d < 8; ++d) o[d] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    float m = -INFINITY, l = 0.0f;
+    // this wave's chunks: all of the token's, or split blockIdx.z's split_keys keys of them
+    int c0 = 0, c1 = L > 0 ? (L + kFd32Bk - 1) / kFd32Bk : 0;
+    if constexpr (SPLIT) {
+      c0 = (int)blockIdx.z * (split_keys / kFd32Bk);
+      c1 = min(c1, c0 + split_keys / kFd32Bk);
+    }
 
-  // chunk c: K row of key 16 c + col, dims 32 g + 4 i (A operands of S^T); V row
-  // of key 16 c + 4 g + u, dims 8 col .. 8 col + 7 (A operands of O^T, zero past L)
-  auto load = [&](int c, u32x4* kr, u32x4* vr) {
-    const int k0 = c * kFd32Bk;
-    const int64_t row0 = (int64_t)tab[k0 / bs] * bs + k0 % bs;
-    const float* kb = kc + (row0 + col) * kv_stride + (int64_t)kvh * kFaHd + 32 * g;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) kr[i] = ld16(kb + 4 * i);
-    const float* vb = vc + row0 * kv_stride + (int64_t)kvh * kFaHd + 8 * col;
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int key = 4 * g + u;
-      const bool ok = k0 + key < L;
-      // (the rows lie inside the chunk's block: unconditional loads, selected values)
-      const u32x4 v0 = ld16(vb + (int64_t)key * kv_stride), v1 = ld16(vb + (int64_t)key * kv_stride + 4);
-      vr[2 * u] = ok ? v0 : u32x4{0, 0, 0, 0};
-      vr[2 * u + 1] = ok ? v1 : u32x4{0, 0, 0, 0};
-    }
-  };
-  auto compute = [&](int c, const u32x4* kr, const u32x4* vr) {
-    f32x4 st = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const f32x4 a = __builtin_bit_cast(f32x4, kr[i]);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) st = __builtin_amdgcn_mfma_f32_16x16x4f32(a[e], qf[i][e], st, 0, 0, 0);
-    }
-    // online softmax per head (lane column); register v is key 16 c + 4 g + v
-    float mx = -INFINITY;
-    if ((c + 1) * kFd32Bk <= L) {
-#pragma unroll
-      for (int v = 0; v < 4; ++v) mx = fmaxf(mx, st[v]);
-    } else {
-#pragma unroll
+    // chunk c: K row of key 16 c + col, dims 32 g + 4 i (A operands of S^T); V row
+    // of key 16 c + 4 g + u, dims 8 col .. 8 col + 7 (A operands of O^T, zero past L)
+    auto load = [&](int c, u32x4* kr, u32x4* vr) {
+      const int k0 = c * kFd32Bk;
+      const int64_t row0 = (int64_t)tab[k0 / bs] * bs + k0 % bs;
+      const float* kb = kc + (row0 + col) * kv_stride + (int64_t)kvh * kFaHd + 32 * g;
+  #pragma unroll
+      for (int i = 0; i < 8; ++i) kr[i] = ld16(kb + 4 * i);
+      const float* vb = vc + row0 * kv_stride + (int64_t)kvh * kFaHd + 8 * col;
+  #pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int key = 4 * g + u;
+        const bool ok = k0 + key < L;
+        // (the rows lie inside the chunk's block: unconditional loads, selected values)
+        const u32x4 v0 = ld16(vb + (int64_t)key * kv_stride), v1 = ld16(vb + (int64_t)key * kv_stride + 4);
+        vr[2 * u] = ok ? v0 : u32x4{0, 0, 0, 0};
+        vr[2 * u + 1] = ok ? v1 : u32x4{0, 0, 0, 0};
+      }
+    };
+    auto compute = [&](int c, const u32x4* kr, const u32x4* vr) {
+      f32x4 st = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  #pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const f32x4 a = __builtin_bit_cast(f32x4, kr[i]);
+  #pragma unroll
+        for (int e = 0; e < 4; ++e) st = __builtin_amdgcn_mfma_f32_16x16x4f32(a[e], qf[i][e], st, 0, 0, 0);
+      }
+      // online softmax per head (lane column); register v is key 16 c + 4 g + v
+      float mx = -INFINITY;
+      if ((c + 1) * kFd32Bk <= L) {
+  #pragma unroll
+        for (int v = 0; v < 4; ++v) mx = fmaxf(mx, st[v]);
+      } else {
+  #pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const float x = c * kFd32Bk + 4 * g + v < L ? st[v] : -INFINITY;
+          st[v] = x;
+          mx = fmaxf(mx, x);
+        }
+      }
+      mx = fmaxf(mx, __shfl_xor(mx, 16));
+      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      const float m_new = fmaxf(m, mx * scale_log2);
+      const float m_use = m_new == -INFINITY ? 0.0f : m_new;
+      float ls = 0.0f;
+  #pragma unroll
       for (int v = 0; v < 4; ++v) {
-        const float x = c * kFd32Bk + 4 * g + v < L ? st[v] : -INFINITY;
-        st[v] = x;
-        mx = fmaxf(mx, x);
+        st[v] = __builtin_amdgcn_exp2f(fmaf(st[v], scale_log2, -m_use));
+        ls += st[v];
       }
-    }
-    mx = fmaxf(mx, __shfl_xor(mx, 16));
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
-    const float m_new = fmaxf(m, mx * scale_log2);
-    const float m_use = m_new == -INFINITY ? 0.0f : m_new;
-    float ls = 0.0f;
-#pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      st[v] = __builtin_amdgcn_exp2f(fmaf(st[v], scale_log2, -m_use));
-      ls += st[v];
-    }
-    ls += __shfl_xor(ls, 16);
-    ls += __shfl_xor(ls, 32);
-    if (!__all(m_new == m)) {
-      const float alpha = __builtin_amdgcn_exp2f(m - m_use);
-      l *= alpha;
-#pragma unroll
-      for (int d = 0; d < 8; ++d) o[d] *= alpha;
-    }
-    l += ls;
-    m = m_new;
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const f32x4 a0 = __builtin_bit_cast(f32x4, vr[2 * u]), a1 = __builtin_bit_cast(f32x4, vr[2 * u + 1]);
-#pragma unroll
-      for (int d = 0; d < 4; ++d) {
-        o[d] = __builtin_amdgcn_mfma_f32_16x16x4f32(a0[d], st[u], o[d], 0, 0, 0);
-        o[4 + d] = __builtin_amdgcn_mfma_f32_16x16x4f32(a1[d], st[u], o[4 + d], 0, 0, 0);
+      ls += __shfl_xor(ls, 16);
+      ls += __shfl_xor(ls, 32);
+      if (!__all(m_new == m)) {
+        const float alpha = __builtin_amdgcn_exp2f(m - m_use);
+        l *= alpha;
+  #pragma unroll
+        for (int d = 0; d < 8; ++d) o[d] *= alpha;
       }
-    }
-  };
+      l += ls;
+      m = m_new;
+  #pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const f32x4 a0 = __builtin_bit_cast(f32x4, vr[2 * u]), a1 = __builtin_bit_cast(f32x4, vr[2 * u + 1]);
+  #pragma unroll
+        for (int d = 0; d < 4; ++d) {
+          o[d] = __builtin_amdgcn_mfma_f32_16x16x4f32(a0[d], st[u], o[d], 0, 0, 0);
+          o[4 + d] = __builtin_amdgcn_mfma_f32_16x16x4f32(a1[d], st[u], o[4 + d], 0, 0, 0);
+        }
+      }
+    };
 
-  // wave w takes chunks w, w + 4, ...; two per trip, the register sets trading roles
-  u32x4 ka[8], va[8], kb_[8], vb_[8];
-  if (c0 + wave < c1) load(c0 + wave, ka, va);
-  for (int c = c0 + wave; c < c1; c += 8) {
-    if (c + 4 < c1) load(c + 4, kb_, vb_);
-    compute(c, ka, va);
-    if (c + 4 < c1) {
-      if (c + 8 < c1) load(c + 8, ka, va);
-      compute(c + 4, kb_, vb_);
+    // wave w takes chunks w, w + 4, ...; two per trip, the register sets trading roles
+    u32x4 ka[8], va[8], kb_[8], vb_[8];
+    if (c0 + wave < c1) load(c0 + wave, ka, va);
+    for (int c = c0 + wave; c < c1; c += 8) {
+      if (c + 4 < c1) load(c + 4, kb_, vb_);
+      compute(c, ka, va);
+      if (c + 4 < c1) {
+        if (c + 8 < c1) load(c + 8, ka, va);
+        compute(c + 4, kb_, vb_);
+      }
     }
+    // O^T: register v of tile d is dim 8 (4 g + v) + d of head col
+    float* pw = merge[wave];
+  #pragma unroll
+    for (int d = 0; d < 8; ++d)
+  #pragma unroll
+      for (int v = 0; v < 4; ++v) pw[(8 * (4 * g + v) + d) * 16 + col] = o[d][v];
+    if (g == 0) {
+      pw[kFaHd * 16 + col] = m;
+      pw[kFaHd * 16 + 16 + col] = l;
+    }
+    decode_merge_store<float, SPLIT>([&](int w) { return static_cast<const float*>(merge[w]); }, out, part, t, tokens,
+                                     q_heads, kvh, G);
+    __syncthreads();  // the merge's LDS reads before the next kv head's writes
   }
-  // O^T: register v of tile d is dim 8 (4 g + v) + d of head col
-  float* pw = merge[wave];
-#pragma unroll
-  for (int d = 0; d < 8; ++d)
-#pragma unroll
-    for (int v = 0; v < 4; ++v) pw[(8 * (4 * g + v) + d) * 16 + col] = o[d][v];
-  if (g == 0) {
-    pw[kFaHd * 16 + col] = m;
-    pw[kFaHd * 16 + 16 + col] = l;
-  }
-  decode_merge_store<float, SPLIT>([&](int w) { return static_cast<const float*>(merge[w]); }, out, part, t, tokens,
-                                   q_heads, kvh, G);
 }
 
 // ---------------------------------------------------------------------------
@@ -1209,32 +1223,34 @@ int attention_dispatch(const void* q, void* out, const void* kc, const void* vc,
     if (rc != NVF_OK) return rc;
   }
   if (dec) {
+    // one workgroup per (token, kv head); for the tiles' second launch (SKIP), one
+    // per token walking the kv heads, since nearly all of its workgroups exit at once
+    const dim3 grid((unsigned)tokens, tiles ? 1u : (unsigned)kv_heads, nz);
+    const int kk = split ? skeys : 0;
+    float* pp = split ? part : nullptr;
+#define NVF_DEC_LAUNCH(KERN, LDS)                                                                              \
+  KERN<<<grid, 256, LDS, st>>>(qt, ot, kt, vt, qseq, qlen, tables, tokens, q_heads, kv_heads, bs, max_blocks, sl, \
+                               q_stride, kk, pp)
     if constexpr (sizeof(T) == 2) {
-      const dim3 grid((unsigned)tokens, (unsigned)kv_heads, nz);  // one workgroup per (token, kv head)
       static std::once_flag dec_once;
       std::call_once(dec_once, [] {
-        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&fa_decode_kernel<T, false>),
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, kFdLds);
-        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&fa_decode_kernel<T, true>),
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, kFdLds);
+        const void* ks[4] = {reinterpret_cast<const void*>(&fa_decode_kernel<T, false, false>),
+                             reinterpret_cast<const void*>(&fa_decode_kernel<T, false, true>),
+                             reinterpret_cast<const void*>(&fa_decode_kernel<T, true, false>),
+                             reinterpret_cast<const void*>(&fa_decode_kernel<T, true, true>)};
+        for (const void* k : ks) (void)hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, kFdLds);
       });
-      if (split)
-        fa_decode_kernel<T, true><<<grid, 256, kFdLds, st>>>(qt, ot, kt, vt, qseq, qlen, tables, tokens, q_heads,
-                                                             kv_heads, bs, max_blocks, sl, q_stride, tiles, skeys,
-                                                             part);
-      else
-        fa_decode_kernel<T, false><<<grid, 256, kFdLds, st>>>(qt, ot, kt, vt, qseq, qlen, tables, tokens, q_heads,
-                                                              kv_heads, bs, max_blocks, sl, q_stride, tiles, 0,
-                                                              nullptr);
+      if (split && tiles) NVF_DEC_LAUNCH((fa_decode_kernel<T, true, true>), kFdLds);
+      else if (split) NVF_DEC_LAUNCH((fa_decode_kernel<T, true, false>), kFdLds);
+      else if (tiles) NVF_DEC_LAUNCH((fa_decode_kernel<T, false, true>), kFdLds);
+      else NVF_DEC_LAUNCH((fa_decode_kernel<T, false, false>), kFdLds);
     } else {
-      const dim3 grid((unsigned)tokens, (unsigned)kv_heads, nz);  // one workgroup per (token, kv head)
-      if (split)
-        fa_decode_f32_kernel<true><<<grid, 256, 0, st>>>(qt, ot, kt, vt, qseq, qlen, tables, tokens, q_heads,
-                                                         kv_heads, bs, max_blocks, sl, q_stride, tiles, skeys, part);
-      else
-        fa_decode_f32_kernel<false><<<grid, 256, 0, st>>>(qt, ot, kt, vt, qseq, qlen, tables, tokens, q_heads,
-                                                          kv_heads, bs, max_blocks, sl, q_stride, tiles, 0, nullptr);
+      if (split && tiles) NVF_DEC_LAUNCH((fa_decode_f32_kernel<true, true>), 0);
+      else if (split) NVF_DEC_LAUNCH((fa_decode_f32_kernel<true, false>), 0);
+      else if (tiles) NVF_DEC_LAUNCH((fa_decode_f32_kernel<false, true>), 0);
+      else NVF_DEC_LAUNCH((fa_decode_f32_kernel<false, false>), 0);
     }
+#undef NVF_DEC_LAUNCH
     int rc = launch_status("paged_attention(decode)");
     if (rc != NVF_OK || !split) return rc;
     attn_split_combine_kernel<T><<<dim3((unsigned)tokens, (unsigned)q_heads), 256, 0, st>>>(part, ot, tokens,
