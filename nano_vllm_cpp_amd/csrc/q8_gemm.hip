@@ -20,7 +20,7 @@
 // Tiling: a 256-thread workgroup owns a 128 x 128 output tile; each of its four
 // waves owns 64 x 64 (2 x 2 MFMA tiles of 32 x 32).  The K loop stages
 // kGemmKC-byte slices of the 128 activation rows and the 128 weight rows through
-// LDS (double-buffered, rows padded to 16 B past the slice so that the 16 lanes
+// LDS (double-buffered, 16-byte chunks XOR-swizzled by row so that the 16 lanes
 // of a ds_read_b128 phase hit 16 distinct 4-bank groups).  Per block and wave:
 // 4 MFMAs and 64 (cvt + fma) per lane to apply the block scale -- the scale
 // application, not the MFMA, bounds this kernel (VALU : MFMA time is about 4:1).
@@ -134,14 +134,16 @@ __device__ __forceinline__ void gemm_store_out(TO* p, float v) {
 }
 
 // out[m][n] (row-major) = dequantized Q8_0 product; see the file header.
-// Grid: one workgroup per 128 x 128 output tile, tiles_n tiles per tile row.
+// Grid: one workgroup per 128 x 128 output tile, tiles_n tiles per tile row;
+// with SPLIT, blockIdx.y is a range of st_per_split K stages whose fp32 partial
+// sums go to part [split][m][n] (q8_gemm_reduce_kernel finishes them).
 //
 // Stage loads go straight from HBM to LDS (buffer_load ... lds): each wave moves
 // 32 activation rows and 32 weight rows per stage in 1 KB transfers, through
 // buffer resources spanning only this tile's rows, so rows past the matrix read
 // as zero; the stage's K offset rides in the scalar offset, so a full stage costs
 // no VALU.  Only a partial last stage (k not a multiple of kGemmKC) checks each
-// chunk against k.  Block scales take a register path (fp16 -> fp32 in LDS).
+// chunk against k.  The block scales come by LDS DMA too (fp16 in 4-byte slots).
 //
 // One loop iteration per Q8_0 block; the first MFMA of block g + 1 is issued
 // while block g is applied, so each result is ready when its scale is applied.
