@@ -1099,7 +1099,7 @@ __global__ __launch_bounds__(256) void attn_split_combine_kernel(const float* __
 // the block table's width.
 constexpr int64_t kSplitMinWaves = 1024;
 constexpr int64_t kSplitTargetWaves = 512;  // a decode wave keeps ~32 KB in flight: 512 cover HBM
-constexpr int64_t kSplitMinKeys = 64;
+constexpr int64_t kSplitMinKeys = 256;  // 4 waves per split workgroup, each with whole chunks
 constexpr int64_t kSplitMinTiles = 512;
 constexpr int64_t kSplitTargetTiles = 1024;
 constexpr int64_t kSplitMinTileKeys = 512;

@@ -95,11 +95,12 @@ CASES = [
     ([700, 90], [200, 90], 28, 4, 128, 256),              # chunked prefill after a 500-token prefix
     ([256], [256], 4, 1, 128, 128),                       # exact tiles
     ([33, 64, 1], [2, 1, 1], 32, 1, 128, 64),             # 32 heads per kv head: beyond the 16-column tiles
+    ([150, 70], [150, 70], 21, 3, 128, 64),               # 3 kv heads; a tile spans the sequence switch
 ]
 
 
 @pytest.mark.parametrize("dt", DTYPES, ids=DT_IDS)
-@pytest.mark.parametrize("heads", [(28, 4), (32, 8), (16, 1)], ids=["qwen25", "qwen3", "g16"])
+@pytest.mark.parametrize("heads", [(28, 4), (32, 8), (16, 1), (21, 3)], ids=["qwen25", "qwen3", "g16", "kv3"])
 def test_paged_attention_decode_batch(gpu, dt, heads):
     """A decode batch (one query per sequence) through the decode-only route
     (max_query_len = 1) and through the automatic one."""
