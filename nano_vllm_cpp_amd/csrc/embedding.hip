@@ -389,13 +389,18 @@ __device__ __forceinline__ uint32_t lds_u32_a2(const uint8_t* p) {  // 4 bytes a
   return (uint32_t)h[0] | ((uint32_t)h[1] << 16);
 }
 
+// Q6_K superblocks are 210 bytes, so flat staging leaves every other one 2 bytes
+// off dword alignment, and 8-byte LDS reads there take the hardware's unaligned
+// path (measured: 47x the LDS issue stalls of Q5_K).  The staged kernel gives
+// each one a 224-byte slot instead (kSlotBytes): bytes 0..207 at 0..207, and
+// bytes 194..209 at 208..223 (so d sits at 222), every read aligned.
 template <int N>
 struct StagedQ6K {
-  static constexpr int kBlockBytes = 210, kBlockElems = 256;
+  static constexpr int kBlockBytes = 210, kBlockElems = 256, kSlotBytes = 224;
   __device__ __forceinline__ static void decode(const uint8_t* blk, int i, float* v) {
     const int h = i >> 7, t = i & 127, l0 = t & 31, slot = t >> 5;
     const int lsh = (slot >> 1) * 4, hsh = 2 * slot;
-    const float ds = half_bits_to_f32(*reinterpret_cast<const uint16_t*>(blk + 208)) *
+    const float ds = half_bits_to_f32(*reinterpret_cast<const uint16_t*>(blk + 222)) *
                      (float)(int8_t)blk[192 + 8 * h + (l0 >> 4) + 2 * slot];
     const uint8_t* ql = blk + 64 * h + 32 * (slot & 1) + l0;
     const uint8_t* qh = blk + 128 + 32 * h + l0;
@@ -474,6 +479,16 @@ struct StagedQ8Blocks {
 
 constexpr int kStageMaxBytesPerWave = 16384;  // LDS per wave: rows up to 16 KiB of blocks
 
+// kSlotBytes of a format (0: flat staging of the row's bytes)
+template <typename F, typename = void>
+struct SlotBytes {
+  static constexpr int value = 0;
+};
+template <typename F>
+struct SlotBytes<F, decltype((void)F::kSlotBytes)> {
+  static constexpr int value = F::kSlotBytes;
+};
+
 template <typename TO, typename Fmt, int L16>  // L16: 16-byte loads per lane to stage a row
 __global__ __launch_bounds__(kEmbThreads) void embed_rows_staged_kernel(const int64_t* __restrict__ ids,
                                                                         const uint8_t* __restrict__ table,
@@ -497,6 +512,40 @@ __global__ __launch_bounds__(kEmbThreads) void embed_rows_staged_kernel(const in
   }
   const int nblk = hidden / Fmt::kBlockElems;
   const uint8_t* row = table + id * (int64_t)nblk * Fmt::kBlockBytes;
+  constexpr int kSlot = SlotBytes<Fmt>::value;
+  if constexpr (kSlot > 0) {
+    // 16-byte loads k = 0 .. kPer - 1 of block b: bytes 16 k (the last one 16
+    // bytes back from the block's end), into slot bytes 16 k; none reads past the
+    // block, so none leaves the table
+    constexpr int kPer = kSlot / 16;
+    uint8_t* my = stage + wave * stage_bytes;
+    const int nld = nblk * kPer;
+    u32x4 r[L16];
+#pragma unroll
+    for (int u = 0; u < L16; ++u) {
+      const int c = u * kWave + lane;
+      if (c < nld) {
+        const int b = c / kPer, k = c - kPer * b;
+        const int off = Fmt::kBlockBytes * b + (k < kPer - 1 ? 16 * k : Fmt::kBlockBytes - 16);
+        __builtin_memcpy(&r[u], row + off, 16);  // 2-byte aligned: an unaligned 16-byte load
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < L16; ++u) {
+      const int c = u * kWave + lane;
+      if (c < nld) *reinterpret_cast<u32x4*>(my + 16 * c) = r[u];  // slot b, chunk k: byte 16 (kPer b + k)
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    for (int c = lane; c < nch; c += kWave) {
+      const int e = c * N;
+      float v[N];
+      Fmt::decode(my + (e / Fmt::kBlockElems) * kSlot, e % Fmt::kBlockElems, v);
+      st16_nt(dst + (int64_t)c * N, Pack<TO>::pack(v));
+    }
+    return;
+  }
   const uintptr_t a16 = reinterpret_cast<uintptr_t>(row) & ~uintptr_t(15);
   const int delta = (int)(reinterpret_cast<uintptr_t>(row) - a16);
   const int n16 = (delta + nblk * Fmt::kBlockBytes + 15) >> 4;
@@ -527,8 +576,10 @@ __global__ __launch_bounds__(kEmbThreads) void embed_rows_staged_kernel(const in
 template <typename TO, typename Fmt>
 static bool launch_staged(const int64_t* ids, const uint8_t* table, TO* out, int64_t tokens, int64_t hidden,
                           int64_t vocab, hipStream_t st) {
-  const int64_t row_bytes = hidden / Fmt::kBlockElems * Fmt::kBlockBytes;
-  const int64_t n16 = (15 + row_bytes + 15) / 16;
+  constexpr int kSlot = SlotBytes<Fmt>::value;
+  const int64_t row_bytes = hidden / Fmt::kBlockElems * (kSlot > 0 ? kSlot : Fmt::kBlockBytes);
+  // flat staging reads from the 16-byte boundary at or below the row: one chunk more
+  const int64_t n16 = kSlot > 0 ? row_bytes / 16 : (15 + row_bytes + 15) / 16;
   if (hidden % Fmt::kBlockElems != 0 || n16 * 16 > kStageMaxBytesPerWave || hidden > INT32_MAX) return false;
   const int stage_bytes = (int)(n16 * 16);
   const size_t lds = (size_t)stage_bytes * kEmbWaves;
