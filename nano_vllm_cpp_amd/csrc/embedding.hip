@@ -382,13 +382,11 @@ static int launch_rows(const int64_t* ids, const Src& src, TO* out, int64_t toke
 // the few extra bytes read never leave those granules (no fault is possible).
 // A format supplies
 //   kBlockBytes, kBlockElems, decode(const uint8_t* blk, int i, float* v)
-// reading the block from LDS (elements i .. i+N-1 of the block).
+// reading the block from LDS (elements i .. i+N-1 of the block), and may supply
+//   kSlotBytes, slot_src(k)
+// to be staged block by block into aligned slots of kSlotBytes (16-byte chunk k
+// of a slot taken from block byte slot_src(k)) instead of as the flat row.
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ uint32_t lds_u32_a2(const uint8_t* p) {  // 4 bytes at a 2-byte-aligned LDS address
-  const uint16_t* h = reinterpret_cast<const uint16_t*>(p);
-  return (uint32_t)h[0] | ((uint32_t)h[1] << 16);
-}
-
 // Q6_K superblocks are 210 bytes, so flat staging leaves every other one 2 bytes
 // off dword alignment, and 8-byte LDS reads there take the hardware's unaligned
 // path (measured: 47x the LDS issue stalls of Q5_K).  The staged kernel gives
@@ -397,6 +395,8 @@ __device__ __forceinline__ uint32_t lds_u32_a2(const uint8_t* p) {  // 4 bytes a
 template <int N>
 struct StagedQ6K {
   static constexpr int kBlockBytes = 210, kBlockElems = 256, kSlotBytes = 224;
+  // block byte that slot chunk k starts at
+  __device__ __forceinline__ static int slot_src(int k) { return k < kSlotBytes / 16 - 1 ? 16 * k : 194; }
   __device__ __forceinline__ static void decode(const uint8_t* blk, int i, float* v) {
     const int h = i >> 7, t = i & 127, l0 = t & 31, slot = t >> 5;
     const int lsh = (slot >> 1) * 4, hsh = 2 * slot;
@@ -409,7 +409,8 @@ struct StagedQ6K {
     // (an fma with -32 ds folded in would give +0 where the reference gives -0)
 #pragma unroll
     for (int w = 0; w < N / 4; ++w) {
-      const uint32_t a = lds_u32_a2(ql + 4 * w), b = lds_u32_a2(qh + 4 * w);
+      const uint32_t a = *reinterpret_cast<const uint32_t*>(ql + 4 * w);  // dword-aligned in the slot
+      const uint32_t b = *reinterpret_cast<const uint32_t*>(qh + 4 * w);
       const uint32_t q4 = ((a >> lsh) & 0x0f0f0f0fu) | (((b >> hsh) & 0x03030303u) << 4);
 #pragma unroll
       for (int k = 0; k < 4; ++k) v[4 * w + k] = ((float)byte_of(q4, k) - 32.0f) * ds;
@@ -463,6 +464,10 @@ struct StagedQ4K {
   }
 };
 
+// Staged flat: every other 34-byte block sits 2 bytes off dword alignment and its
+// reads take the unaligned path (17x the LDS issue stalls of Q5_K), but 48-byte
+// aligned slots, at three 16-byte loads per block, measured slower (38.5 against
+// ~33 us at Qwen2.5-7B prefill shape): for 34-byte blocks the extra loads cost more.
 template <int N>
 struct StagedQ8Blocks {
   static constexpr int kBlockBytes = 34, kBlockElems = 32;
@@ -470,7 +475,8 @@ struct StagedQ8Blocks {
     const float s = half_bits_to_f32(*reinterpret_cast<const uint16_t*>(blk));
 #pragma unroll
     for (int w = 0; w < N / 4; ++w) {
-      const uint32_t a = lds_u32_a2(blk + 2 + i + 4 * w);
+      uint32_t a;
+      __builtin_memcpy(&a, blk + 2 + i + 4 * w, 4);  // 2-byte aligned
 #pragma unroll
       for (int k = 0; k < 4; ++k) v[4 * w + k] = s * sbyte(a, k);
     }
@@ -514,9 +520,8 @@ __global__ __launch_bounds__(kEmbThreads) void embed_rows_staged_kernel(const in
   const uint8_t* row = table + id * (int64_t)nblk * Fmt::kBlockBytes;
   constexpr int kSlot = SlotBytes<Fmt>::value;
   if constexpr (kSlot > 0) {
-    // 16-byte loads k = 0 .. kPer - 1 of block b: bytes 16 k (the last one 16
-    // bytes back from the block's end), into slot bytes 16 k; none reads past the
-    // block, so none leaves the table
+    // 16-byte loads k = 0 .. kPer - 1 of block b: from block byte Fmt::slot_src(k)
+    // into slot bytes 16 k; none reads past the block, so none leaves the table
     constexpr int kPer = kSlot / 16;
     uint8_t* my = stage + wave * stage_bytes;
     const int nld = nblk * kPer;
@@ -526,7 +531,7 @@ __global__ __launch_bounds__(kEmbThreads) void embed_rows_staged_kernel(const in
       const int c = u * kWave + lane;
       if (c < nld) {
         const int b = c / kPer, k = c - kPer * b;
-        const int off = Fmt::kBlockBytes * b + (k < kPer - 1 ? 16 * k : Fmt::kBlockBytes - 16);
+        const int off = Fmt::kBlockBytes * b + Fmt::slot_src(k);
         __builtin_memcpy(&r[u], row + off, 16);  // 2-byte aligned: an unaligned 16-byte load
       }
     }
