@@ -1040,55 +1040,58 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_wave_kernel(
 // and sum ([token][q head][split][2], after the O block); this kernel merges them:
 // out = sum_z 2^(m_z - M) O_z / sum_z 2^(m_z - M) l_z, M = max_z m_z.  One
 // workgroup per (token, q head): 4 waves take every 4th split, two dims per lane,
-// and meet in LDS.
+// each merging its splits online in one round of loads, and meet in LDS.
 template <typename T>
 __global__ __launch_bounds__(256) void attn_split_combine_kernel(const float* __restrict__ part, T* __restrict__ out,
                                                                  int64_t tokens,
                                                                  int q_heads, int nsplit) {
-  __shared__ float red[4][2 * 64 + 1];
-  __shared__ float wmax[4];
+  __shared__ float red[4][2 * 64 + 2];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   const int64_t t = blockIdx.x;
   const int h = (int)blockIdx.y;
   const int64_t p0 = (t * q_heads + h) * nsplit;
   const float* pml = part + tokens * q_heads * nsplit * kFaHd + 2 * p0;
-  float mx = -INFINITY;
-  for (int z = threadIdx.x; z < nsplit; z += 256) mx = fmaxf(mx, pml[2 * z]);
-  mx = wave_max(mx);
-  if (lane == 0) wmax[wave] = mx;
-  __syncthreads();
-  mx = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
-  T* o = out + (t * q_heads + h) * kFaHd + 2 * lane;
-  if (mx == -INFINITY) {  // no keys at all: zeros, as the unsplit kernels write
-    if (wave == 0) {
-      o[0] = from_f32<T>(0.0f);
-      o[1] = from_f32<T>(0.0f);
-    }
-    return;
-  }
-  // wave w: splits w, w + 4, ...; an empty split (m = -inf, O = 0, l = 0) weighs 0
-  float den = 0.0f, a0 = 0.0f, a1 = 0.0f;
+  // wave w merges splits w, w + 4, ... online (its loads independent of the
+  // arithmetic, so they go out together): state (mw, den, a0, a1) relative to its
+  // running max mw; an empty split (m = -inf, O = 0, l = 0) weighs 0
+  float mw = -INFINITY, den = 0.0f, a0 = 0.0f, a1 = 0.0f;
 #pragma unroll 4
   for (int z = wave; z < nsplit; z += 4) {
-    const float w = __builtin_amdgcn_exp2f(pml[2 * z] - mx);
-    den += w * pml[2 * z + 1];
+    const float mz = pml[2 * z], lz = pml[2 * z + 1];
     const float2 v = *reinterpret_cast<const float2*>(part + (p0 + z) * kFaHd + 2 * lane);
-    a0 += w * v.x;
-    a1 += w * v.y;
+    const float mn = fmaxf(mw, mz);
+    const float so = mw == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mw - mn);
+    const float sn = mz == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mz - mn);
+    den = den * so + lz * sn;
+    a0 = a0 * so + v.x * sn;
+    a1 = a1 * so + v.y * sn;
+    mw = mn;
   }
   red[wave][2 * lane] = a0;
   red[wave][2 * lane + 1] = a1;
-  if (lane == 0) red[wave][128] = den;
-  __syncthreads();
-  if (wave == 0) {
-    a0 = (red[0][2 * lane] + red[1][2 * lane]) + (red[2][2 * lane] + red[3][2 * lane]);
-    a1 = (red[0][2 * lane + 1] + red[1][2 * lane + 1]) + (red[2][2 * lane + 1] + red[3][2 * lane + 1]);
-    den = (red[0][128] + red[1][128]) + (red[2][128] + red[3][128]);
-    const float inv = den > 0.0f ? 1.0f / den : 0.0f;
-    o[0] = from_f32<T>(a0 * inv);
-    o[1] = from_f32<T>(a1 * inv);
+  if (lane == 0) {
+    red[wave][128] = mw;
+    red[wave][129] = den;
   }
+  __syncthreads();
+  if (wave != 0) return;
+  // the 4 wave states, rescaled to their common max; no keys at all gives zeros,
+  // as the unsplit kernels write
+  float mx = -INFINITY;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) mx = fmaxf(mx, red[w][128]);
+  float sc[4];
+#pragma unroll
+  for (int w = 0; w < 4; ++w) sc[w] = red[w][128] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(red[w][128] - mx);
+  a0 = (red[0][2 * lane] * sc[0] + red[1][2 * lane] * sc[1]) + (red[2][2 * lane] * sc[2] + red[3][2 * lane] * sc[3]);
+  a1 = (red[0][2 * lane + 1] * sc[0] + red[1][2 * lane + 1] * sc[1]) +
+       (red[2][2 * lane + 1] * sc[2] + red[3][2 * lane + 1] * sc[3]);
+  den = (red[0][129] * sc[0] + red[1][129] * sc[1]) + (red[2][129] * sc[2] + red[3][129] * sc[3]);
+  const float inv = den > 0.0f ? 1.0f / den : 0.0f;
+  T* o = out + (t * q_heads + h) * kFaHd + 2 * lane;
+  o[0] = from_f32<T>(a0 * inv);
+  o[1] = from_f32<T>(a1 * inv);
 }
 
 // How an attention call is split: only when its work cannot fill the GPU --
