@@ -605,12 +605,13 @@ def traffic_from_profiles(op: str, config: int):
         return None
 
 
-def cpu_baseline(cfg, budget_s: float, H) -> dict:
-    """The C oracle (scalar, 1 thread, -O2) on a bounded sample of the same chain."""
+def cpu_chain_sample(cfg, H, seed: int):
+    """Buffers for one S-token sample of the chain and a function running it once
+    through the C oracle; returns (run, S).  run() returns the four ops' seconds."""
     o = H.oracle()
-    r = np.random.default_rng(cfg.seed)
+    r = np.random.default_rng(seed)
     S = 256  # sample tokens per chain call
-    T, Hd, I, dt = S, cfg.hidden, cfg.inter, cfg.dtype
+    Hd, I, dt = cfg.hidden, cfg.inter, cfg.dtype
     Vs = 4096  # gathered rows come from a 4096-row slice of the table: same per-row work
     ids = r.integers(0, Vs, S).astype(np.int64)
     if cfg.emb == "q8_0":
@@ -630,10 +631,8 @@ def cpu_baseline(cfg, budget_s: float, H) -> dict:
     kw = H.gen_act(r, (cfg.head_dim,), dt, 1.0, 0.1) if cfg.qk_norm else None
     gu = H.gen_act(r, (S, 2 * I), dt)
     so = np.empty((S, I), H.NP_STORAGE[dt])
-    per = {"emb": 0.0, "rms": 0.0, "rope": 0.0, "silu": 0.0}
-    calls = 0
-    t_start = time.perf_counter()
-    while True:
+
+    def run():
         t = time.perf_counter()
         if cfg.emb == "q8_0":
             o.orc_embedding_q8_split(H.ptr(ids), H.ptr(w8), H.ptr(ws), S, Hd, H.ptr(emb), dt)
@@ -647,15 +646,28 @@ def cpu_baseline(cfg, budget_s: float, H) -> dict:
         t3 = time.perf_counter()
         o.orc_silu_and_mul(H.ptr(gu), H.ptr(so), S, I, dt)
         t4 = time.perf_counter()
-        per["emb"] += t1 - t
-        per["rms"] += t2 - t1
-        per["rope"] += t3 - t2
-        per["silu"] += t4 - t3
+        return t1 - t, t2 - t1, t3 - t2, t4 - t3
+
+    return run, S
+
+
+def cpu_baseline(cfg, budget_s: float, H) -> dict:
+    """The C oracle (scalar, 1 thread, -O2) on a bounded sample of the same chain,
+    then the same oracle on every host core the box gives this job (threads, each
+    on its own sample; ctypes releases the GIL), reported under "all_cores"."""
+    run, S = cpu_chain_sample(cfg, H, cfg.seed)
+    per = {"emb": 0.0, "rms": 0.0, "rope": 0.0, "silu": 0.0}
+    calls = 0
+    t_start = time.perf_counter()
+    while True:
+        d = run()
+        for k_, v in zip(per, d):
+            per[k_] += v
         calls += 1
-        if t4 - t_start >= budget_s:
+        if time.perf_counter() - t_start >= budget_s:
             break
     total = sum(per.values())
-    e = 2 if dt != H.F32 else 4
+    e = 2 if cfg.dtype != H.F32 else 4
     scale = {k_: v * S / cfg.tokens for k_, v in op_bytes(cfg, e, "q8_0").items()}  # bytes of one S-token call
     cpu_model = ""
     try:
@@ -665,11 +677,33 @@ def cpu_baseline(cfg, budget_s: float, H) -> dict:
                 break
     except OSError:
         pass
-    return {"value": round(calls * S / total, 1), "unit": "tokens/s", "cores": 1, "kind": "port",
-            "sample": f"{calls} x the {S}-token chain of the same config (table rows from a {Vs}-row slice), "
-                      f"{total:.1f} s of single-thread C oracle (-O2) on {cpu_model or 'this host'}, "
-                      f"nproc={os.cpu_count()}",
-            "ops_GB_s": {k_: round(scale[k_] * calls / per[k_] / 1e9, 3) for k_ in per}}
+    result = {"value": round(calls * S / total, 1), "unit": "tokens/s", "cores": 1, "kind": "port",
+              "sample": f"{calls} x the {S}-token chain of the same config (table rows from a 4096-row slice), "
+                        f"{total:.1f} s of single-thread C oracle (-O2) on {cpu_model or 'this host'}, "
+                        f"nproc={os.cpu_count()}",
+              "ops_GB_s": {k_: round(scale[k_] * calls / per[k_] / 1e9, 3) for k_ in per}}
+
+    # all cores: at most 16 threads (the box's CPU share per GPU), half the budget
+    import concurrent.futures as cf
+    n = max(1, min(16, os.cpu_count() or 1))
+    runs = [cpu_chain_sample(cfg, H, cfg.seed + 1 + i)[0] for i in range(n)]
+    all_budget = budget_s / 2
+
+    def worker(fn):
+        c, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < all_budget:
+            fn()
+            c += 1
+        return c
+
+    t0 = time.perf_counter()
+    with cf.ThreadPoolExecutor(max_workers=n) as ex:
+        counts = list(ex.map(worker, runs))
+    wall = time.perf_counter() - t0
+    result["all_cores"] = {"value": round(sum(counts) * S / wall, 1), "unit": "tokens/s", "cores": n,
+                           "kind": "port",
+                           "sample": f"{sum(counts)} x the {S}-token chain over {n} threads, {wall:.1f} s wall"}
+    return result
 
 
 if __name__ == "__main__":
