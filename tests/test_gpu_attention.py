@@ -100,7 +100,8 @@ CASES = [
 
 
 @pytest.mark.parametrize("dt", DTYPES, ids=DT_IDS)
-@pytest.mark.parametrize("heads", [(28, 4), (32, 8), (16, 1), (21, 3)], ids=["qwen25", "qwen3", "g16", "kv3"])
+@pytest.mark.parametrize("heads", [(28, 4), (32, 8), (16, 1), (21, 3), (8, 8)],
+                         ids=["qwen25", "qwen3", "g16", "kv3", "mha"])
 def test_paged_attention_decode_batch(gpu, dt, heads):
     """A decode batch (one query per sequence) through the decode-only route
     (max_query_len = 1) and through the automatic one."""
@@ -264,6 +265,7 @@ SPLIT_CASES = [
     ([5000, 77, 1, 2049, 300], (28, 4)),   # ragged; one query also gets key_len 0 below
     ([8192, 1024], (32, 8)),
     ([640], (16, 1)),
+    ([3000, 40], (8, 8)),                  # one query head per kv head
 ]
 
 
