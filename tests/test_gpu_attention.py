@@ -362,3 +362,41 @@ def test_paged_attention_ws_too_small_runs_unsplit(gpu):
     torch.cuda.synchronize()
     assert_attn(H.to_host(out), exact, vmax, H.F16, "unsplit fallback")
     assert (guard == 7.0).all()  # the workspace was not touched
+
+
+@pytest.mark.parametrize("dt", [H.F16, H.F32], ids=["f16", "f32"])
+def test_paged_attention_config2_full_vs_torch(gpu, dt):
+    """BASELINE config 2's causal prefill at full size (4 x 4096 tokens, 28 / 4
+    heads x 128, KV blocks of 256 in a permuted cache) against torch's fp32
+    scaled_dot_product_attention of the gathered keys.  Tolerance as the other
+    attention tests, with vmax the largest |V| of the sequence's kv head (at least
+    the largest |V| a query attends)."""
+    S, L, qh, kvh, hd, bs = 4, 4096, 28, 4, 128, 256
+    g = torch.Generator(device=gpu)
+    g.manual_seed(12)
+    tdt = H.torch_dtype(dt)
+    nb = L // bs
+    q = torch.randn(S * L, qh, hd, device=gpu, generator=g).to(tdt)
+    kc = torch.randn(S * nb * bs, kvh, hd, device=gpu, generator=g).to(tdt)
+    vc = torch.randn(S * nb * bs, kvh, hd, device=gpu, generator=g).to(tdt)
+    tab = torch.randperm(S * nb, device=gpu, generator=g).to(torch.int32).view(S, nb)
+    qs = torch.arange(S, device=gpu, dtype=torch.int32).repeat_interleave(L)
+    ql = (torch.arange(L, device=gpu, dtype=torch.int32) + 1).repeat(S)
+    scale = hd ** -0.5
+    case(f"paged_attention config 2 full size dt={dt}")
+    out = ops.paged_attention(q, kc, vc, qs, ql, tab, bs, scale).float()
+    rel = REL[dt]
+    for s_ in range(S):
+        rows = (tab[s_].long()[:, None] * bs + torch.arange(bs, device=gpu)[None, :]).reshape(-1)  # key order
+        k_ = kc[rows].float().permute(1, 0, 2).repeat_interleave(qh // kvh, dim=0)[None]
+        v_ = vc[rows].float().permute(1, 0, 2).repeat_interleave(qh // kvh, dim=0)[None]
+        q_ = q[s_ * L:(s_ + 1) * L].float().permute(1, 0, 2)[None]
+        ref = torch.nn.functional.scaled_dot_product_attention(q_, k_, v_, is_causal=True, scale=scale)[0]
+        ref = ref.permute(1, 0, 2)  # [L, qh, hd]
+        vmax = v_[0].abs().amax(dim=(1, 2))  # per q head
+        got = out[s_ * L:(s_ + 1) * L]
+        tol = rel * vmax[None, :, None] + 1e-6
+        if dt != H.F32:
+            tol = tol + ref.abs() * 2.0 ** -10  # one ulp of the fp16 output
+        bad = ((got - ref).abs() > tol).sum().item()
+        assert bad == 0, f"sequence {s_}: {bad} of {got.numel()} outputs outside tolerance"

@@ -204,3 +204,29 @@ def test_matmul_q8_0_split_k(gpu, out_dt, m, n, k):
     case(f"matmul_q8_0 unsplit m={m} n={n} k={k} out_dt={out_dt}")
     got = H.to_host(ops.matmul_q8_0(*args, split=False))
     assert_within(got[rows], ideal, err, out_dt, "unsplit gemm")
+
+
+def test_matmul_q8_config2_full_vs_torch(gpu):
+    """BASELINE config 2's gate_up GEMM at full size (16384 x 37888 x 3584, every
+    tile of the XCD-aware order) against a torch fp32 matmul of the exactly
+    dequantized weights (x int8 and ws * w8 are exact in fp32).  Every element is
+    within both sides' summation bounds: this kernel's (nblk + 2) u S, torch's
+    (k + 1) u S, with S = (|x| |w|^T) / row_scale and u = 2^-24."""
+    m, n, k = 16384, 37888, 3584
+    g = torch.Generator(device=gpu)
+    g.manual_seed(11)
+    xq = torch.randint(-127, 128, (m, k), device=gpu, dtype=torch.int8, generator=g)
+    sc = torch.rand(m, device=gpu, generator=g) * 10.0 + 1.0
+    w8 = torch.randint(-127, 128, (n, k), device=gpu, dtype=torch.int8, generator=g)
+    ws = (torch.rand(n, k // 32, device=gpu, generator=g) * 9e-3 + 1e-3).half()
+    case("matmul_q8_0 config 2 gate_up, full size, vs torch fp32")
+    out = ops.matmul_q8_0(xq, sc, w8.view(-1), ws.view(-1), n, torch.float32)
+    torch.backends.cuda.matmul.allow_tf32 = False
+    w = (w8.float().view(n, k // 32, 32) * ws.float().view(n, k // 32, 1)).view(n, k)
+    x = xq.float()
+    ideal = (x @ w.t()) / sc[:, None]
+    bound = (x.abs() @ w.abs().t()) / sc[:, None]
+    del x, w
+    tol = (k + k // 32 + 3) * 2.0 ** -24 * bound + 1e-30
+    bad = ((out - ideal).abs() > tol).sum().item()
+    assert bad == 0, f"{bad} of {m * n} outputs outside the summation bounds"
