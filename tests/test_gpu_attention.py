@@ -400,3 +400,45 @@ def test_paged_attention_config2_full_vs_torch(gpu, dt):
             tol = tol + ref.abs() * 2.0 ** -10  # one ulp of the fp16 output
         bad = ((got - ref).abs() > tol).sum().item()
         assert bad == 0, f"sequence {s_}: {bad} of {got.numel()} outputs outside tolerance"
+
+
+@pytest.mark.parametrize("shape", ["config1", "long"], ids=["config1_decode", "split_4x32768"])
+def test_paged_attention_decode_full_vs_torch(gpu, shape):
+    """Decode batches at full size against torch's fp32 attention of each
+    sequence's gathered keys: config 1 (256 sequences, context U[1, 4096], 28 / 4
+    heads) and a split long-context batch (4 x 32768 keys), fp16 caches."""
+    qh, kvh, hd, bs = 28, 4, 128, 256
+    g = torch.Generator(device=gpu)
+    g.manual_seed(13)
+    if shape == "config1":
+        ctx = (torch.randint(1, 4097, (256,), generator=g, device=gpu)).tolist()
+    else:
+        ctx = [32768] * 4
+    nbk = [-(-c // bs) for c in ctx]
+    mb = max(nbk)
+    total = sum(nbk)
+    perm = torch.randperm(total, device=gpu, generator=g).to(torch.int32)
+    tab = torch.full((len(ctx), mb), -1, dtype=torch.int32, device=gpu)
+    o = 0
+    for s_, n_ in enumerate(nbk):
+        tab[s_, :n_] = perm[o:o + n_]
+        o += n_
+    kc = torch.randn(total * bs, kvh, hd, device=gpu, generator=g).half()
+    vc = torch.randn(total * bs, kvh, hd, device=gpu, generator=g).half()
+    B = len(ctx)
+    q = torch.randn(B, qh, hd, device=gpu, generator=g).half()
+    qs = torch.arange(B, dtype=torch.int32, device=gpu)
+    ql = torch.tensor(ctx, dtype=torch.int32, device=gpu)
+    scale = hd ** -0.5
+    case(f"paged_attention decode full size {shape}")
+    out = ops.paged_attention(q, kc, vc, qs, ql, tab, bs, scale, max_query_len=1).float()
+    for s_, c in enumerate(ctx):
+        rows = (tab[s_, :nbk[s_]].long()[:, None] * bs + torch.arange(bs, device=gpu)[None, :]).reshape(-1)[:c]
+        k_ = kc[rows].float().permute(1, 0, 2).repeat_interleave(qh // kvh, dim=0)  # [qh, c, hd]
+        v_ = vc[rows].float().permute(1, 0, 2).repeat_interleave(qh // kvh, dim=0)
+        p = torch.softmax((k_ @ q[s_].float()[:, :, None])[..., 0] * scale, dim=-1)  # [qh, c]
+        ref = (p[:, None, :] @ v_)[:, 0, :]  # [qh, hd]
+        vmax = v_.abs().amax(dim=(1, 2))
+        tol = REL[H.F16] * vmax[:, None] + ref.abs() * 2.0 ** -10 + 1e-6
+        bad = ((out[s_] - ref).abs() > tol).sum().item()
+        assert bad == 0, f"sequence {s_} (context {c}): {bad} outputs outside tolerance"
