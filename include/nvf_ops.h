@@ -103,7 +103,9 @@ void hip_store_kv(const float* key, const float* value, float* k_cache, float* v
  * kv_heads, head_dim]: token t attends the first query_key_len[t] keys of
  * sequence query_seq[t] (block_tables[seq * max_blocks + j / block_size]);
  * out = softmax(scale * q . K) . V per head, 0 when query_key_len[t] <= 0.
- * head_dim <= 256. */
+ * head_dim <= 256.  Like the reference's kernel, this trusts its metadata: the
+ * table entries a query reaches must name cache blocks, and query_key_len <=
+ * block_size * max_blocks (the caller's prepare_prefill/prepare_decode builds them so). */
 void hip_paged_attention(const float* q, float* out, const float* k_cache, const float* v_cache,
                          const int32_t* query_seq, const int32_t* query_key_len, const int32_t* block_tables,
                          int tokens, int q_heads, int kv_heads, int head_dim, int block_size, int max_blocks,
