@@ -303,6 +303,8 @@ struct Table {  // plain fp32 / fp16 / bf16 rows
 };
 
 constexpr int kEmbWaves = kEmbThreads / kWave;
+constexpr int64_t kEmbCapMinGroups = 4096;  // two rounds of 256 CUs x 8 resident workgroups
+constexpr size_t kEmbCapLds = 40 * 1024;    // 160 KiB LDS per CU / 40 KiB = 4 workgroups per CU
 
 // WPR waves per row: wave w of a row covers its chunk groups w, w + WPR, ...
 // Measured at Qwen2.5-7B prefill shapes: Q8_0 and tables gather best with one
@@ -351,7 +353,7 @@ __global__ __launch_bounds__(kEmbThreads) void embed_rows_kernel(const int64_t* 
 
 template <typename TO, typename Src, int WPR>
 static int launch_rows(const int64_t* ids, const Src& src, TO* out, int64_t tokens, int64_t hidden, int64_t vocab,
-                       hipStream_t st, const char* what) {
+                       hipStream_t st, const char* what, size_t occ_lds = 0) {
   constexpr int N = Pack<TO>::N;
   const int64_t per_lane = (hidden / N + WPR * kWave - 1) / (WPR * kWave);  // chunks per lane
   const int64_t rows_per_block = kEmbWaves / WPR;
@@ -360,7 +362,7 @@ static int launch_rows(const int64_t* ids, const Src& src, TO* out, int64_t toke
   switch (per_lane < 8 ? per_lane : 8) {  // exact up to 8 chunks per lane, then the row loops
 #define NVF_EMB_CASE(UU)                                                                                          \
   case UU:                                                                                                        \
-    embed_rows_kernel<TO, Src, UU, WPR><<<grid, kEmbThreads, 0, st>>>(ids, src, out, tokens, h, vocab); \
+    embed_rows_kernel<TO, Src, UU, WPR><<<grid, kEmbThreads, occ_lds, st>>>(ids, src, out, tokens, h, vocab); \
     break;
     NVF_EMB_CASE(1) NVF_EMB_CASE(2) NVF_EMB_CASE(3) NVF_EMB_CASE(4)
     NVF_EMB_CASE(5) NVF_EMB_CASE(6) NVF_EMB_CASE(7) NVF_EMB_CASE(8)
@@ -869,7 +871,16 @@ static int launch_q8(const int64_t* ids, const uint8_t* w8, const uint16_t* ws, 
       return launch_rows<TO, Q8Blocks<N>, 1>(ids, Q8Blocks<N>{blocks}, o, tokens, hidden, vocab, st,
                                                  "embedding_q8_0_blocks");
   } else if (row_ok && (reinterpret_cast<uintptr_t>(w8) & 7u) == 0 && (reinterpret_cast<uintptr_t>(ws) & 1u) == 0) {
-    return launch_rows<TO, Q8Split<N>, 1>(ids, Q8Split<N>{w8, ws}, o, tokens, hidden, vocab, st, "embedding_q8_0");
+    // Residency cap for long gathers: the table rows are cold random HBM reads, and with every wave
+    // slot filled (8 workgroups per CU) the reads of 8192 rows are in flight at once.  Measured on
+    // MI355X at 16384 x 3584 with the rows not in the Infinity Cache: 4 workgroups per CU (forced
+    // by 40 KiB of unused dynamic LDS out of 160 KiB) take 31.5 us against 32.5 us; 3 or fewer
+    // take 40 us.  A grid that fits in about one round at full residency (8192 x 4096: 2048
+    // workgroups) gains nothing and keeps every slot.
+    const int64_t groups = (tokens + kEmbWaves - 1) / kEmbWaves;
+    const size_t occ_lds = groups >= kEmbCapMinGroups ? kEmbCapLds : 0;
+    return launch_rows<TO, Q8Split<N>, 1>(ids, Q8Split<N>{w8, ws}, o, tokens, hidden, vocab, st, "embedding_q8_0",
+                                          occ_lds);
   }
   const int64_t total = tokens * hidden;
   embed_q8_generic_kernel<TO><<<grid_for(total), kEmbThreads, 0, st>>>(ids, w8, ws, blocks, o, total, hidden, vocab);
