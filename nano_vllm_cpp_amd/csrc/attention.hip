@@ -87,6 +87,7 @@ __global__ __launch_bounds__(256) void store_kv_generic_kernel(const T* __restri
 constexpr int kFaHd = 128;
 constexpr int kFaBq = 128;                       // query tokens per workgroup
 constexpr int kFaBk = 64;                        // keys per chunk
+constexpr float kFaLazy = 8.0f;                  // exp2 units the running max may lag behind (16-bit tiles)
 constexpr int kFaKRow = kFaHd * 2 + 16;          // K row in LDS, padded (conflict-free 16 B reads)
 constexpr int kFaVRow = kFaBk * 2 + 8;           // V^T row in LDS, padded
 constexpr int kFaKBytes = kFaBk * kFaKRow;
@@ -179,6 +180,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
   const int tid = threadIdx.x;
   const int ld_c = tid & 15, ld_r = tid >> 4;
   u32x4 kreg[4], vreg[4];
+  int vlive = 0;  // keys 4 ld_r .. 4 ld_r + 3 of the loaded chunk that lie inside the tile's range
   auto load_chunk = [&](int c) {
     const int k0 = c * kFaBk;
     const int64_t row0 = (int64_t)tab[k0 / bs] * bs + k0 % bs;
@@ -187,15 +189,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       kreg[i] = ld16(kb + (int64_t)(ld_r + 16 * i) * kv_stride);
-      const int key = 4 * ld_r + i;
-      // keys past the tile's range may hold anything: zero their V (their p is 0).
-      // The row itself lies inside the chunk's block, so the load is unconditional
-      // and only the value is selected (no branch around the load).
-      const u32x4 v = ld16(vb + (int64_t)key * kv_stride);
-      vreg[i] = k0 + key < Lmax ? v : u32x4{0, 0, 0, 0};
+      // The row lies inside the chunk's block, so the load is unconditional.
+      vreg[i] = ld16(vb + (int64_t)(4 * ld_r + i) * kv_stride);
     }
+    vlive = Lmax - k0 - 4 * ld_r;
   };
   auto store_chunk = [&](uint8_t* st) {
+    // keys past the tile's range may hold anything: zero their V (their p is 0).  The
+    // select happens here, when the chunk goes to LDS, and not after the loads: a use
+    // of the loaded registers right after issuing them would wait for the loads there.
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      if (i >= vlive) vreg[i] = u32x4{0, 0, 0, 0};
 #pragma unroll
     for (int i = 0; i < 4; ++i) st16(st + (ld_r + 16 * i) * kFaKRow + ld_c * 16, kreg[i]);
     // V^T: dim 8 ld_c + e, keys 4 ld_r .. 4 ld_r + 3 -> 8 bytes, at key group
@@ -236,7 +241,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
   __syncthreads();
   for (int c = c0; c < c1; ++c) {
     const uint8_t* buf = lds + ((c - c0) & 1) * kFaStage;
-    if (c + 1 < c1) load_chunk(c + 1);  // in flight during this chunk
     // S^T = K . Q^T for keys [32 kt, 32 kt + 32)
     f32x16 st[2];
 #pragma unroll
@@ -248,6 +252,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
         st[kt] = M::mma(a, qf[s], st[kt]);
       }
     }
+    if (c + 1 < c1) load_chunk(c + 1);  // in flight during the softmax and O^T += V^T . P^T
     // online softmax for this lane's query; element j of tile kt is key
     // c*64 + 32 kt + 8 (j/4) + 4 half + j%4.  The running max m is kept in
     // exp2 units (score * scale_log2); since scale_log2 > 0 and rounding is
@@ -273,8 +278,21 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
     }
     float mx = fmaxf(fmaxf(mx4[0], mx4[1]), fmaxf(mx4[2], mx4[3]));
     mx = fmaxf(mx, __shfl_xor(mx, 32));
-    const float m_new = fmaxf(m, mx * scale_log2);
-    const float m_use = m_new == -INFINITY ? 0.0f : m_new;
+    // Lazy running max: m moves (and O and l are rescaled) only when some query of the
+    // wave would see a weight above 2^kFaLazy under the current m.  Otherwise the chunk's
+    // weights are taken against the stale m, at most 2^kFaLazy.  O and l always share one
+    // m, so out = O / l is unchanged; only the point where the 16-bit P rounds moves,
+    // with the same relative precision.  With m = -inf (every key so far masked) any
+    // finite candidate moves it.
+    const float m_cand = fmaxf(m, mx * scale_log2);
+    if (__any(m_cand > m + kFaLazy)) {
+      const float alpha = __builtin_amdgcn_exp2f(m - (m_cand == -INFINITY ? 0.0f : m_cand));
+      l *= alpha;
+#pragma unroll
+      for (int d = 0; d < kFaHd / 32; ++d) o[d] *= alpha;
+      m = m_cand;
+    }
+    const float m_use = m == -INFINITY ? 0.0f : m;
     float ls4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     v8 pb[2][2];
 #pragma unroll
@@ -287,16 +305,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
       }
     float ls = (ls4[0] + ls4[1]) + (ls4[2] + ls4[3]);
     ls += __shfl_xor(ls, 32);
-    // the rescale factor is exactly 1 where the max did not move: skip it when
-    // that holds for every query of the wave
-    if (!__all(m_new == m)) {
-      const float alpha = __builtin_amdgcn_exp2f(m - m_use);
-      l *= alpha;
-#pragma unroll
-      for (int d = 0; d < kFaHd / 32; ++d) o[d] *= alpha;
-    }
     l += ls;
-    m = m_new;
     // O^T += V^T . P^T, key step u of tile kt: keys 32 kt + 16 u + 4 half + {0..3, 8..11},
     // key groups g0 + half and g0 + 2 + half (g0 = 8 kt + 4 u) of row 32 d + (lane & 31)
     const uint8_t* vt = buf + kFaKBytes + vt_lane;
