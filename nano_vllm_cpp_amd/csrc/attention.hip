@@ -181,6 +181,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
   const int ld_c = tid & 15, ld_r = tid >> 4;
   u32x4 kreg[4], vreg[4];
   int vlive = 0;  // keys 4 ld_r .. 4 ld_r + 3 of the loaded chunk that lie inside the tile's range
+  bool vlast = false;
   auto load_chunk = [&](int c) {
     const int k0 = c * kFaBk;
     const int64_t row0 = (int64_t)tab[k0 / bs] * bs + k0 % bs;
@@ -193,14 +194,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
       vreg[i] = ld16(vb + (int64_t)(4 * ld_r + i) * kv_stride);
     }
     vlive = Lmax - k0 - 4 * ld_r;
+    vlast = k0 + kFaBk > Lmax;
   };
   auto store_chunk = [&](uint8_t* st) {
     // keys past the tile's range may hold anything: zero their V (their p is 0).  The
     // select happens here, when the chunk goes to LDS, and not after the loads: a use
     // of the loaded registers right after issuing them would wait for the loads there.
+    if (vlast) {  // wave-uniform: only the tile's last chunk can reach past its range
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      if (i >= vlive) vreg[i] = u32x4{0, 0, 0, 0};
+      for (int i = 0; i < 4; ++i)
+        if (i >= vlive) vreg[i] = u32x4{0, 0, 0, 0};
+    }
 #pragma unroll
     for (int i = 0; i < 4; ++i) st16(st + (ld_r + 16 * i) * kFaKRow + ld_c * 16, kreg[i]);
     // V^T: dim 8 ld_c + e, keys 4 ld_r .. 4 ld_r + 3 -> 8 bytes, at key group
@@ -308,6 +312,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
     l += ls;
     // O^T += V^T . P^T, key step u of tile kt: keys 32 kt + 16 u + 4 half + {0..3, 8..11},
     // key groups g0 + half and g0 + 2 + half (g0 = 8 kt + 4 u) of row 32 d + (lane & 31)
+    // For odd d the swizzle puts the +8 key group at the lower address; those MFMAs take
+    // the groups in address order, (+8, +0), with P's halves swapped to match (the same
+    // contraction with its k order permuted), so the paired LDS read lands in operand order.
+    v8 pbx[2][2];
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int u = 0; u < 2; ++u) pbx[kt][u] = __builtin_shufflevector(pb[kt][u], pb[kt][u], 4, 5, 6, 7, 0, 1, 2, 3);
     const uint8_t* vt = buf + kFaKBytes + vt_lane;
 #pragma unroll
     for (int d = 0; d < kFaHd / 32; ++d)
@@ -320,8 +332,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
           const uint8_t* r = vt + (32 * d + (lane & 31)) * kFaVRow;
           const u32x2 lo = *reinterpret_cast<const u32x2*>(r + 8 * (g0 ^ (2 * d)));
           const u32x2 hi = *reinterpret_cast<const u32x2*>(r + 8 * ((g0 + 2) ^ (2 * d)));
-          const v8 a = __builtin_bit_cast(v8, u32x4{lo[0], lo[1], hi[0], hi[1]});
-          o[d] = M::mma(a, pb[kt][u], o[d]);
+          if (d & 1) {
+            o[d] = M::mma(__builtin_bit_cast(v8, u32x4{hi[0], hi[1], lo[0], lo[1]}), pbx[kt][u], o[d]);
+          } else {
+            o[d] = M::mma(__builtin_bit_cast(v8, u32x4{lo[0], lo[1], hi[0], hi[1]}), pb[kt][u], o[d]);
+          }
         }
     if (c + 1 < c1) store_chunk(lds + ((c + 1 - c0) & 1) * kFaStage);
     __syncthreads();
@@ -493,8 +508,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
       }
     }
     mx = fmaxf(mx, __shfl_xor(mx, 32));
-    const float m_new = fmaxf(m, mx * scale_log2);
-    const float m_use = m_new == -INFINITY ? 0.0f : m_new;
+    // lazy running max, as in fa_prefill_kernel (P stays fp32 here: no rounding moves)
+    const float m_cand = fmaxf(m, mx * scale_log2);
+    if (__any(m_cand > m + kFaLazy)) {
+      const float alpha = __builtin_amdgcn_exp2f(m - (m_cand == -INFINITY ? 0.0f : m_cand));
+      l *= alpha;
+#pragma unroll
+      for (int d = 0; d < 4; ++d) o[d] *= alpha;
+      m = m_cand;
+    }
+    const float m_use = m == -INFINITY ? 0.0f : m;
     float ls = 0.0f;
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
@@ -502,14 +525,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
       ls += st[j];
     }
     ls += __shfl_xor(ls, 32);
-    if (!__all(m_new == m)) {
-      const float alpha = __builtin_amdgcn_exp2f(m - m_use);
-      l *= alpha;
-#pragma unroll
-      for (int d = 0; d < 4; ++d) o[d] *= alpha;
-    }
     l += ls;
-    m = m_new;
     // O^T += V^T . P^T: MFMA s takes key 8 (s/4) + 4 half + s%4 (P^T = st[s]); lane
     // row r = lane & 31 of tile d is dim 4 r + d
     const uint8_t* vrow = buf + kF32KBytes + 16 * (lane & 31);
@@ -771,7 +787,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
       // O^T += V^T . P^T: dims 16 d + col, key step u: keys 32 u + 4 g + {0..3}, 32 u + 16 + 4 g + {0..3}
   #pragma unroll
       for (int d = 0; d < kFaHd / 16; ++d) {
-        o[d] *= alpha;
+        o[d] *= alpha;  // unconditional here: interleaved with the MFMAs it costs less than a wave vote
   #pragma unroll
         for (int u = 0; u < 2; ++u) {
           typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
@@ -899,8 +915,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
       }
       mx = fmaxf(mx, __shfl_xor(mx, 16));
       mx = fmaxf(mx, __shfl_xor(mx, 32));
-      const float m_new = fmaxf(m, mx * scale_log2);
-      const float m_use = m_new == -INFINITY ? 0.0f : m_new;
+      // lazy running max, as in fa_prefill_kernel
+      const float m_cand = fmaxf(m, mx * scale_log2);
+      if (__any(m_cand > m + kFaLazy)) {
+        const float alpha = __builtin_amdgcn_exp2f(m - (m_cand == -INFINITY ? 0.0f : m_cand));
+        l *= alpha;
+  #pragma unroll
+        for (int d = 0; d < 8; ++d) o[d] *= alpha;
+        m = m_cand;
+      }
+      const float m_use = m == -INFINITY ? 0.0f : m;
       float ls = 0.0f;
   #pragma unroll
       for (int v = 0; v < 4; ++v) {
@@ -909,14 +933,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
       }
       ls += __shfl_xor(ls, 16);
       ls += __shfl_xor(ls, 32);
-      if (!__all(m_new == m)) {
-        const float alpha = __builtin_amdgcn_exp2f(m - m_use);
-        l *= alpha;
-  #pragma unroll
-        for (int d = 0; d < 8; ++d) o[d] *= alpha;
-      }
       l += ls;
-      m = m_new;
   #pragma unroll
       for (int u = 0; u < 4; ++u) {
         const f32x4 a0 = __builtin_bit_cast(f32x4, vr[2 * u]), a1 = __builtin_bit_cast(f32x4, vr[2 * u + 1]);
