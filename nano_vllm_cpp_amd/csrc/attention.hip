@@ -246,16 +246,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
   for (int c = c0; c < c1; ++c) {
     const uint8_t* buf = lds + ((c - c0) & 1) * kFaStage;
     // S^T = K . Q^T for keys [32 kt, 32 kt + 32)
-    f32x16 st[2];
+    // (the two key tiles' MFMA chains interleaved: neither waits on its own accumulator)
+    f32x16 st[2] = {f32x16{}, f32x16{}};
 #pragma unroll
-    for (int kt = 0; kt < 2; ++kt) {
-      st[kt] = f32x16{};
+    for (int s = 0; s < kFaHd / 16; ++s)
 #pragma unroll
-      for (int s = 0; s < kFaHd / 16; ++s) {
+      for (int kt = 0; kt < 2; ++kt) {
         const v8 a = __builtin_bit_cast(v8, ld16(buf + (32 * kt + (lane & 31)) * kFaKRow + (16 * s + 8 * half) * 2));
         st[kt] = M::mma(a, qf[s], st[kt]);
       }
-    }
     if (c + 1 < c1) load_chunk(c + 1);  // in flight during the softmax and O^T += V^T . P^T
     // online softmax for this lane's query; element j of tile kt is key
     // c*64 + 32 kt + 8 (j/4) + 4 half + j%4.  The running max m is kept in
@@ -321,12 +320,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
 #pragma unroll
       for (int u = 0; u < 2; ++u) pbx[kt][u] = __builtin_shufflevector(pb[kt][u], pb[kt][u], 4, 5, 6, 7, 0, 1, 2, 3);
     const uint8_t* vt = buf + kFaKBytes + vt_lane;
+    // (the four dim tiles' MFMA chains interleaved)
 #pragma unroll
-    for (int d = 0; d < kFaHd / 32; ++d)
+    for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-      for (int kt = 0; kt < 2; ++kt)
+      for (int u = 0; u < 2; ++u)
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
+        for (int d = 0; d < kFaHd / 32; ++d) {
           typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
           const int g0 = 8 * kt + 4 * u;
           const uint8_t* r = vt + (32 * d + (lane & 31)) * kFaVRow;
