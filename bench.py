@@ -370,16 +370,14 @@ def main() -> int:
 
     def run_layer_on(L_):
         # model.cpp:758-833's per-layer sequence, Qwen2.5 (no QK-norm): input RMSNorm (writing the
-        # qkv GEMM's int8 rows), qkv, RoPE on the q and k columns of the packed row, KV store,
+        # qkv GEMM's int8 rows), qkv, RoPE on the q and k columns of the packed row fused with the KV store,
         # paged attention, o (quantize + GEMM), post-attention residual-add RMSNorm (int8 rows),
         # gate_up, SwiGLU (int8 rows), down
         n_ = L_["T"]
         _, sc, xq = ops.rms_norm_q8(L_["h"], L_["w_in"], cfg.eps, residual=L_["r"], want_out=False)
         qkv = ops.matmul_q8_0(xq, sc, *L_["qkv"], qs + 2 * ks, tdt, out=L_["qkv_out"])
-        ops.qk_norm_rope(qkv[:, :qs], qkv[:, qs:qs + ks], L_["pos"], None, None, inv, cfg.q_heads, cfg.kv_heads,
-                         cfg.head_dim, cfg.eps)
-        kv3 = (n_, cfg.kv_heads, cfg.head_dim)
-        ops.store_kv(qkv[:, qs:qs + ks].view(kv3), qkv[:, qs + ks:].view(kv3), L_["kc"], L_["vc"], L_["slots"])
+        ops.qk_norm_rope_store_kv(qkv[:, :qs], qkv[:, qs:qs + ks], qkv[:, qs + ks:], L_["pos"], None, None, inv,
+                                  cfg.q_heads, cfg.kv_heads, cfg.head_dim, L_["kc"], L_["vc"], L_["slots"], cfg.eps)
         att = ops.paged_attention(qkv[:, :qs].view(n_, cfg.q_heads, cfg.head_dim), L_["kc"], L_["vc"], L_["qseq"],
                                   L_["qlen"], L_["tab"], bs_kv, cfg.head_dim ** -0.5, out=L_["attn_out"],
                                   max_query_len=L_["mql"])

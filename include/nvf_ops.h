@@ -147,6 +147,17 @@ int nvf_qk_norm_rope(void* q, void* k, const int64_t* positions, const void* q_w
                      const float* inv_freq, int64_t tokens, int q_heads, int kv_heads, int head_dim,
                      int64_t q_stride, int64_t k_stride, float eps, int dtype, void* stream);
 
+/* nvf_qk_norm_rope followed by nvf_store_kv(k, v, ...) in one launch where the shape
+ * allows (head_dim 64/128/256, 16-byte aligned rows, kv_heads * head_dim <= 4096), the
+ * two launches otherwise; the results are those of the pair.  The reference calls the
+ * RoPE (src/model.cpp:777-778) and then the store (hip_store_kv, hip_ops.hpp:22-23)
+ * on the same k and v; this fuses that sequence, so it has no single counterpart.
+ * k is rotated in place as well as stored; slot < 0 skips a token's store. */
+int nvf_qk_norm_rope_store_kv(void* q, void* k, const void* v, const int64_t* positions, const void* q_w,
+                              const void* k_w, const float* inv_freq, int64_t tokens, int q_heads, int kv_heads,
+                              int head_dim, int64_t q_stride, int64_t k_stride, int64_t v_stride, float eps,
+                              void* k_cache, void* v_cache, const int32_t* slot_mapping, int dtype, void* stream);
+
 /* Q8_0 gather, split planes (as hip_embedding_q8) -> out in out_dtype.
  * vocab > 0: ids outside [0, vocab) produce a NaN row instead of a read;
  * vocab <= 0: ids are trusted (the reference validates them on the host,

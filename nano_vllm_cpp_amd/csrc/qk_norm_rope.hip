@@ -28,12 +28,24 @@ namespace nvf {
 constexpr int kRopeThreads = 256;     // generic kernel
 constexpr int kRopeVecThreads = 256;   // vector kernel: a token's heads in passes of 256 / LPH
 
-template <typename T, int HD, bool NORM>
+// KV store fused in (STORE; nvf_qk_norm_rope_store_kv): the rotated k heads also go
+// to k_cache row slots[t], and the token's v row to v_cache row slots[t] (cache rows
+// [kv_heads * HD]; slot < 0 skips the token), exactly what nvf_store_kv does after
+// the RoPE launch.  The v row is loaded with the heads and stored at the end.
+struct KvStoreArgs {
+  const void* v;
+  int64_t v_stride;
+  void* kc;
+  void* vc;
+  const int32_t* slots;
+};
+
+template <typename T, int HD, bool NORM, bool STORE>
 __global__ __launch_bounds__(kRopeVecThreads) void qk_norm_rope_kernel(T* q, T* k, const int64_t* __restrict__ positions,
                                                                     const T* __restrict__ qw, const T* __restrict__ kw,
                                                                     const float* __restrict__ inv_freq, int q_heads,
                                                                     int kv_heads, int64_t q_stride, int64_t k_stride,
-                                                                    float eps) {
+                                                                    float eps, KvStoreArgs kv) {
   constexpr int N = Pack<T>::N;
   constexpr int HALF = HD / 2;
   constexpr int LPH = HALF / N;                   // lanes per head
@@ -52,6 +64,21 @@ __global__ __launch_bounds__(kRopeVecThreads) void qk_norm_rope_kernel(T* q, T* 
 
   // The first pass's loads go out before the (cos, sin) table is built, so
   // the HBM latency overlaps the sincos work and the barrier.
+  // the fused store: slot of this token; the v row's 16-byte chunks, kVPer per thread
+  constexpr int kVPer = 2;  // up to 2 * 256 chunks: kv_heads * HD <= 4096 elements (host-checked)
+  int32_t slot = -1;
+  u32x4 vrow[kVPer];
+  const int64_t row = (int64_t)kv_heads * HD;
+  if constexpr (STORE) {
+    slot = kv.slots[t];
+    const T* vsrc = static_cast<const T*>(kv.v) + t * kv.v_stride;
+#pragma unroll
+    for (int i = 0; i < kVPer; ++i) {
+      const int64_t c = threadIdx.x + (int64_t)i * kRopeVecThreads;
+      if (slot >= 0 && c * N < row) vrow[i] = ld16_nt(vsrc + c * N);
+    }
+  }
+
   int h = threadIdx.x / LPH;
   u32x4 a, b;
   if (h < total_heads) {
@@ -111,10 +138,26 @@ __global__ __launch_bounds__(kRopeVecThreads) void qk_norm_rope_kernel(T* q, T* 
       y1[j] = x1[j] * c[j] - x2[j] * s[j];
       y2[j] = x2[j] * c[j] + x1[j] * s[j];
     }
-    st16_nt(base + d0, Pack<T>::pack(y1));
-    st16_nt(base + HALF + d0, Pack<T>::pack(y2));
+    const u32x4 p1 = Pack<T>::pack(y1), p2 = Pack<T>::pack(y2);
+    st16_nt(base + d0, p1);
+    st16_nt(base + HALF + d0, p2);
+    if constexpr (STORE) {
+      if (!is_q && slot >= 0) {
+        T* dst = static_cast<T*>(kv.kc) + (int64_t)slot * row + (int64_t)(h - q_heads) * HD;
+        st16(dst + d0, p1);
+        st16(dst + HALF + d0, p2);
+      }
+    }
     a = an;
     b = bn;
+  }
+  if constexpr (STORE) {
+    T* vdst = static_cast<T*>(kv.vc) + (int64_t)slot * row;
+#pragma unroll
+    for (int i = 0; i < kVPer; ++i) {
+      const int64_t c = threadIdx.x + (int64_t)i * kRopeVecThreads;
+      if (slot >= 0 && c * N < row) st16(vdst + c * N, vrow[i]);
+    }
   }
 }
 
@@ -159,10 +202,12 @@ __global__ __launch_bounds__(kRopeThreads) void qk_norm_rope_generic_kernel(
   }
 }
 
+// kv != nullptr: launch the fused RoPE + KV store kernel when the vector kernel takes
+// the shape (returns 1 without launching otherwise: the caller then runs the two ops)
 template <typename T, bool NORM>
 static int launch_rope(void* q, void* k, const int64_t* pos, const void* qw, const void* kw, const float* inv_freq,
                        int64_t tokens, int q_heads, int kv_heads, int head_dim, int64_t q_stride, int64_t k_stride,
-                       float eps, hipStream_t st) {
+                       float eps, hipStream_t st, const KvStoreArgs* kv = nullptr) {
   constexpr int N = Pack<T>::N;
   T* qp = static_cast<T*>(q);
   T* kp = static_cast<T*>(k);
@@ -171,12 +216,22 @@ static int launch_rope(void* q, void* k, const int64_t* pos, const void* qw, con
   bool vec_ok = (q_heads == 0 || (aligned16(q) && q_stride % N == 0)) &&
                 (kv_heads == 0 || (aligned16(k) && k_stride % N == 0)) &&
                 (!NORM || (aligned16(qw) && aligned16(kw)));
+  if (kv) {
+    const int64_t row = (int64_t)kv_heads * head_dim;
+    vec_ok = vec_ok && kv_heads > 0 && aligned16(kv->v) && kv->v_stride % N == 0 && aligned16(kv->kc) &&
+             aligned16(kv->vc) && row <= 2 * kRopeVecThreads * N;
+  }
   if (vec_ok && (head_dim == 64 || head_dim == 128 || head_dim == 256)) {
     const dim3 grid((unsigned)tokens);
     const unsigned block = kRopeVecThreads;
-#define NVF_ROPE_LAUNCH(HDV)                                                                                 \
-  qk_norm_rope_kernel<T, HDV, NORM><<<grid, block, 0, st>>>(qp, kp, pos, qwp, kwp, inv_freq, q_heads, \
-                                                                   kv_heads, q_stride, k_stride, eps)
+    const KvStoreArgs none{};
+#define NVF_ROPE_LAUNCH(HDV)                                                                                        \
+  if (kv)                                                                                                           \
+    qk_norm_rope_kernel<T, HDV, NORM, true><<<grid, block, 0, st>>>(qp, kp, pos, qwp, kwp, inv_freq, q_heads,       \
+                                                                     kv_heads, q_stride, k_stride, eps, *kv);       \
+  else                                                                                                              \
+    qk_norm_rope_kernel<T, HDV, NORM, false><<<grid, block, 0, st>>>(qp, kp, pos, qwp, kwp, inv_freq, q_heads,      \
+                                                                      kv_heads, q_stride, k_stride, eps, none)
     if (head_dim == 64) {
       NVF_ROPE_LAUNCH(64);
       return launch_status("qk_norm_rope");
@@ -191,6 +246,7 @@ static int launch_rope(void* q, void* k, const int64_t* pos, const void* qw, con
     }
 #undef NVF_ROPE_LAUNCH
   }
+  if (kv) return 1;  // not launched: the caller runs RoPE and the store separately
   const int64_t items = tokens * (q_heads + kv_heads);
   const int per_block = kRopeThreads / kWave;
   const dim3 grid((unsigned)((items + per_block - 1) / per_block));
@@ -201,34 +257,67 @@ static int launch_rope(void* q, void* k, const int64_t* pos, const void* qw, con
 
 }  // namespace nvf
 
-extern "C" int nvf_qk_norm_rope(void* q, void* k, const int64_t* positions, const void* q_w, const void* k_w,
-                                const float* inv_freq, int64_t tokens, int q_heads, int kv_heads, int head_dim,
-                                int64_t q_stride, int64_t k_stride, float eps, int dtype, void* stream) {
-  using namespace nvf;
-  if (!dtype_ok(dtype)) return fail(NVF_ERR_INVALID, "nvf_qk_norm_rope: bad dtype %d", dtype);
+namespace nvf {
+// nvf_qk_norm_rope's checks and dispatch; with kv, the fused kernel (1: shape not
+// taken by it, nothing launched)
+static int rope_entry(const char* name, void* q, void* k, const int64_t* positions, const void* q_w, const void* k_w,
+                      const float* inv_freq, int64_t tokens, int q_heads, int kv_heads, int head_dim,
+                      int64_t q_stride, int64_t k_stride, float eps, int dtype, void* stream, const KvStoreArgs* kv) {
+  if (!dtype_ok(dtype)) return fail(NVF_ERR_INVALID, "%s: bad dtype %d", name, dtype);
   if (tokens < 0 || q_heads < 0 || kv_heads < 0 || head_dim < 2 || tokens > INT32_MAX)
-    return fail(NVF_ERR_INVALID, "nvf_qk_norm_rope: bad shape tokens=%lld q_heads=%d kv_heads=%d head_dim=%d",
+    return fail(NVF_ERR_INVALID, "%s: bad shape tokens=%lld q_heads=%d kv_heads=%d head_dim=%d", name,
                 (long long)tokens, q_heads, kv_heads, head_dim);
   if (tokens == 0 || q_heads + kv_heads == 0) return NVF_OK;
   if ((q_heads > 0 && (!q || q_stride < (int64_t)q_heads * head_dim)) ||
       (kv_heads > 0 && (!k || k_stride < (int64_t)kv_heads * head_dim)))
-    return fail(NVF_ERR_INVALID, "nvf_qk_norm_rope: NULL tensor or stride smaller than heads*head_dim");
-  if (!positions || !inv_freq) return fail(NVF_ERR_INVALID, "nvf_qk_norm_rope: NULL positions or inv_freq");
+    return fail(NVF_ERR_INVALID, "%s: NULL tensor or stride smaller than heads*head_dim", name);
+  if (!positions || !inv_freq) return fail(NVF_ERR_INVALID, "%s: NULL positions or inv_freq", name);
   const bool norm = q_w || k_w;
   if (norm && ((q_heads > 0 && !q_w) || (kv_heads > 0 && !k_w)))
-    return fail(NVF_ERR_INVALID, "nvf_qk_norm_rope: q_w and k_w must both be given (or both NULL)");
+    return fail(NVF_ERR_INVALID, "%s: q_w and k_w must both be given (or both NULL)", name);
   int s = NVF_OK;
   hipStream_t st = as_stream(stream);
   if (norm)
     NVF_DISPATCH_DTYPE(dtype, T, s = (launch_rope<T, true>(q, k, positions, q_w, k_w, inv_freq, tokens, q_heads,
-                                                           kv_heads, head_dim, q_stride, k_stride, eps, st)));
+                                                           kv_heads, head_dim, q_stride, k_stride, eps, st, kv)));
   else
     NVF_DISPATCH_DTYPE(dtype, T, s = (launch_rope<T, false>(q, k, positions, nullptr, nullptr, inv_freq, tokens,
-                                                            q_heads, kv_heads, head_dim, q_stride, k_stride, eps, st)));
+                                                            q_heads, kv_heads, head_dim, q_stride, k_stride, eps, st,
+                                                            kv)));
   return s;
 }
+}  // namespace nvf
 
-// Drop-in: include/nanovllm/hip_ops.hpp:19-20 / src/hip_ops.hip:715-722.
+extern "C" int nvf_qk_norm_rope(void* q, void* k, const int64_t* positions, const void* q_w, const void* k_w,
+                                const float* inv_freq, int64_t tokens, int q_heads, int kv_heads, int head_dim,
+                                int64_t q_stride, int64_t k_stride, float eps, int dtype, void* stream) {
+  return nvf::rope_entry("nvf_qk_norm_rope", q, k, positions, q_w, k_w, inv_freq, tokens, q_heads, kv_heads, head_dim,
+                         q_stride, k_stride, eps, dtype, stream, nullptr);
+}
+
+extern "C" int nvf_qk_norm_rope_store_kv(void* q, void* k, const void* v, const int64_t* positions, const void* q_w,
+                                         const void* k_w, const float* inv_freq, int64_t tokens, int q_heads,
+                                         int kv_heads, int head_dim, int64_t q_stride, int64_t k_stride,
+                                         int64_t v_stride, float eps, void* k_cache, void* v_cache,
+                                         const int32_t* slot_mapping, int dtype, void* stream) {
+  using namespace nvf;
+  static const char* name = "nvf_qk_norm_rope_store_kv";
+  if (kv_heads <= 0 || head_dim <= 0) return fail(NVF_ERR_INVALID, "%s: kv_heads=%d head_dim=%d", name, kv_heads, head_dim);
+  if (v_stride < (int64_t)kv_heads * head_dim)
+    return fail(NVF_ERR_INVALID, "%s: v_stride must be >= kv_heads * head_dim", name);
+  if (tokens > 0 && (!v || !k_cache || !v_cache || !slot_mapping)) return fail(NVF_ERR_INVALID, "%s: NULL pointer", name);
+  const KvStoreArgs kv{v, v_stride, k_cache, v_cache, slot_mapping};
+  const int s = rope_entry(name, q, k, positions, q_w, k_w, inv_freq, tokens, q_heads, kv_heads, head_dim, q_stride,
+                           k_stride, eps, dtype, stream, &kv);
+  if (s != 1) return s;
+  // a shape the fused kernel does not take: the same two ops, one after the other
+  const int r = nvf_qk_norm_rope(q, k, positions, q_w, k_w, inv_freq, tokens, q_heads, kv_heads, head_dim, q_stride,
+                                 k_stride, eps, dtype, stream);
+  if (r != NVF_OK) return r;
+  return nvf_store_kv(k, v, k_cache, v_cache, slot_mapping, tokens, kv_heads, head_dim, k_stride, v_stride, dtype,
+                      stream);
+}
+
 extern "C" void hip_rope_inplace(float* data, const int64_t* positions, int tokens, int heads, int head_dim,
                                  int64_t stride, const float* inv_freq) {
   if (tokens <= 0 || heads <= 0 || head_dim / 2 <= 0) return;

@@ -56,6 +56,8 @@ SIGNATURES: dict[str, tuple] = {
     "nvf_silu_and_mul": (_i32, [_vp, _vp, _i64, _i64, _i32, _vp]),
     "nvf_silu_and_mul_q8": (_i32, [_vp, _vp, _vp, _vp, _i64, _i64, _i32, _vp]),
     "nvf_qk_norm_rope": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i32, _i32, _i32, _i64, _i64, _f32, _i32, _vp]),
+    "nvf_qk_norm_rope_store_kv": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i32, _i32, _i32, _i64, _i64, _i64,
+                                         _f32, _vp, _vp, _vp, _i32, _vp]),
     "nvf_embedding_q8_0": (_i32, [_vp, _vp, _vp, _i64, _i64, _i64, _vp, _i32, _vp]),
     "nvf_embedding_q8_0_blocks": (_i32, [_vp, _vp, _i64, _i64, _i64, _vp, _i32, _vp]),
     "nvf_embedding_qk": (_i32, [_vp, _vp, _i64, _i64, _i64, _i32, _i32, _vp, _i32, _vp]),
@@ -324,6 +326,26 @@ def qk_norm_rope(q: torch.Tensor, k: torch.Tensor | None, positions: torch.Tenso
         _dev(q_w, "q_w") if q_w is not None else None, _dev(k_w, "k_w") if k_w is not None else None,
         _dev(inv_freq, "inv_freq"), tokens, q_heads, kv_heads, head_dim, q.stride(0),
         k.stride(0) if k is not None else 0, eps, _dt(q), _stream()), "qk_norm_rope")
+
+
+def qk_norm_rope_store_kv(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, positions: torch.Tensor,
+                          q_w: torch.Tensor | None, k_w: torch.Tensor | None, inv_freq: torch.Tensor, q_heads: int,
+                          kv_heads: int, head_dim: int, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                          slot_mapping: torch.Tensor, eps: float = 1e-6) -> None:
+    """qk_norm_rope(q, k, ...) then store_kv(k, v, k_cache, v_cache, slot_mapping), in one
+    launch where the shape allows.  q [T, q_heads * head_dim], k and v [T, kv_heads *
+    head_dim] (row strides from the tensors); caches [rows, kv_heads, head_dim]."""
+    tokens = q.shape[0]
+    if positions.dtype != torch.int64 or positions.shape != (tokens,):
+        raise ValueError("positions must be int64 [tokens]")
+    if inv_freq.dtype != torch.float32 or inv_freq.numel() != head_dim // 2:
+        raise ValueError("inv_freq must be float32 [head_dim/2]")
+    _check(lib().nvf_qk_norm_rope_store_kv(
+        _dev_rows(q, "q"), _dev_rows(k, "k"), _dev_rows(v, "v"), _dev(positions, "positions"),
+        _dev(q_w, "q_w") if q_w is not None else None, _dev(k_w, "k_w") if k_w is not None else None,
+        _dev(inv_freq, "inv_freq"), tokens, q_heads, kv_heads, head_dim, q.stride(0), k.stride(0), v.stride(0), eps,
+        _dev(k_cache, "k_cache"), _dev(v_cache, "v_cache"), _dev(slot_mapping, "slot_mapping"), _dt(q), _stream()),
+        "qk_norm_rope_store_kv")
 
 
 # ---------------------------------------------------------------------------

@@ -182,3 +182,68 @@ def test_fused_quantizers_feed_the_gemm(gpu, dt):
     fused = ops.matmul_q8_0(sq, ssc, H.to_dev(w8b, gpu), H.to_dev(wsb, gpu), n, torch.float32)
     plain = ops.matmul_q8(sout, H.to_dev(w8b, gpu), H.to_dev(wsb, gpu), n, torch.float32)
     H.assert_bitexact(fused.cpu().numpy(), plain.cpu().numpy(), "swiglu -> gemm")
+
+
+@pytest.mark.parametrize("dt", DTYPES, ids=DT_IDS)
+@pytest.mark.parametrize("tokens,qh,kvh,hd,norm", [
+    (37, 28, 4, 128, False),   # Qwen2.5-7B heads, packed [q | k | v] rows
+    (5, 32, 8, 128, True),     # Qwen3-8B: QK-norm fused as well
+    (9, 14, 2, 64, False),     # Qwen2.5-0.5B heads
+    (3, 4, 1, 256, True),
+    (6, 4, 2, 80, False),      # head_dim 80: the two-launch fallback
+    (4, 8, 40, 128, False),    # kv row of 5120 elements: past the fused kernel's v row, the fallback
+])
+def test_qk_norm_rope_store_kv(gpu, dt, tokens, qh, kvh, hd, norm):
+    """The fused RoPE + KV store equals nvf_qk_norm_rope followed by nvf_store_kv bit for
+    bit: q and k in place, both caches (slot -1 rows untouched, including their prior
+    contents)."""
+    r = H.rng(tokens * 131 + qh * 7 + kvh + hd + dt)
+    tdt = H.torch_dtype(dt)
+    width = (qh + 2 * kvh) * hd
+    qkv = H.to_dev(H.gen_act(r, (tokens, width), dt, 0.0, 1.0), gpu, dt)
+    pos = torch.from_numpy(r.integers(0, 8192, tokens).astype(np.int64)).to(gpu)
+    inv = ops.rope_inv_freq(1e6, hd, gpu)
+    qw = torch.randn(hd, device=gpu).mul(0.1).add(1.0).to(tdt) if norm else None
+    kw = torch.randn(hd, device=gpu).mul(0.1).add(1.0).to(tdt) if norm else None
+    rows = 2 * tokens + 3
+    slots = r.permutation(rows)[:tokens].astype(np.int32)
+    slots[1 % tokens] = -1
+    d_slots = torch.from_numpy(slots).to(gpu)
+    kc0 = torch.randn(rows, kvh, hd, device=gpu).to(tdt)
+    vc0 = torch.randn(rows, kvh, hd, device=gpu).to(tdt)
+    qs, ks = qh * hd, kvh * hd
+
+    case(f"qk_norm_rope_store_kv tokens={tokens} heads={qh}/{kvh} hd={hd} norm={norm} dt={dt}")
+    a = qkv.clone()
+    kc_a, vc_a = kc0.clone(), vc0.clone()
+    ops.qk_norm_rope(a[:, :qs], a[:, qs:qs + ks], pos, qw, kw, inv, qh, kvh, hd, 1e-6)
+    kv3 = (tokens, kvh, hd)
+    ops.store_kv(a[:, qs:qs + ks].view(kv3), a[:, qs + ks:].view(kv3), kc_a, vc_a, d_slots)
+
+    b = qkv.clone()
+    kc_b, vc_b = kc0.clone(), vc0.clone()
+    ops.qk_norm_rope_store_kv(b[:, :qs], b[:, qs:qs + ks], b[:, qs + ks:], pos, qw, kw, inv, qh, kvh, hd,
+                              kc_b, vc_b, d_slots, 1e-6)
+    torch.cuda.synchronize()
+    H.assert_bitexact(H.to_host(b), H.to_host(a), "q, k in place (and v untouched)")
+    H.assert_bitexact(H.to_host(kc_b), H.to_host(kc_a), "k cache")
+    H.assert_bitexact(H.to_host(vc_b), H.to_host(vc_a), "v cache")
+    untouched = np.setdiff1d(np.arange(rows), slots[slots >= 0])
+    H.assert_bitexact(H.to_host(kc_b[untouched]), H.to_host(kc0[untouched]), "rows without a slot")
+
+
+def test_qk_norm_rope_store_kv_bad_args(gpu):
+    q = torch.zeros(2, 256, dtype=torch.float16, device=gpu)
+    k = torch.zeros(2, 128, dtype=torch.float16, device=gpu)
+    pos = torch.zeros(2, dtype=torch.int64, device=gpu)
+    inv = ops.rope_inv_freq(1e6, 128, gpu)
+    kc = torch.zeros(4, 1, 128, dtype=torch.float16, device=gpu)
+    slots = torch.zeros(2, dtype=torch.int32, device=gpu)
+    v_narrow = torch.zeros(2, 64, dtype=torch.float16, device=gpu)  # row stride 64 < kv_heads * head_dim
+    with pytest.raises(RuntimeError):
+        ops.qk_norm_rope_store_kv(q, k, v_narrow, pos, None, None, inv, 2, 1, 128, kc, kc.clone(), slots)
+    with pytest.raises(RuntimeError):  # no slot mapping
+        lib_rc = ops.lib().nvf_qk_norm_rope_store_kv(q.data_ptr(), k.data_ptr(), k.data_ptr(), pos.data_ptr(), None,
+                                                     None, inv.data_ptr(), 2, 2, 1, 128, 256, 128, 128, 1e-6,
+                                                     kc.data_ptr(), kc.data_ptr(), None, 1, None)
+        ops._check(lib_rc, "qk_norm_rope_store_kv")
