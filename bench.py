@@ -277,6 +277,7 @@ def main() -> int:
             lseq = np.repeat(np.arange(len(llens), dtype=np.int32), llens)
             lctx = [int(lpos[lcu[s_]:lcu[s_ + 1]].max()) + 1 for s_ in range(len(llens))]  # keys each sequence holds
             layer = build_layer(lpos, lseq, lctx, 0, cfg.seed + 5)
+            layer["cu"] = lcu  # the prefill's packing, held on the host like the engine's
             layer_ops, layer_attn_flops = layer_flops(T, lpos)
         if "layer_decode" in only:  # a decode step: 256 sequences, one new token each, context U[1, 4096]
             dctx = np.random.default_rng(cfg.seed + 7).integers(1, 4097, 256)
@@ -356,7 +357,9 @@ def main() -> int:
 
     def run_attn(i):
         q_, kc_, vc_, qs_, ql_, tb_ = attn_in
-        ops.paged_attention(q_, kc_, vc_, qs_, ql_, tb_, bs_kv, cfg.head_dim ** -0.5, out=attn_out)
+        # the engine holds the batch's cu_seqlens on the host (model_runner.cpp:43-128)
+        ops.paged_attention(q_, kc_, vc_, qs_, ql_, tb_, bs_kv, cfg.head_dim ** -0.5, out=attn_out,
+                            cu_seqlens=cfg.cu_seqlens())
 
     def run_attn_decode(i):
         q_, kc_, vc_, qs_, ql_, tb_ = attn_dec
@@ -380,7 +383,7 @@ def main() -> int:
                                   cfg.q_heads, cfg.kv_heads, cfg.head_dim, L_["kc"], L_["vc"], L_["slots"], cfg.eps)
         att = ops.paged_attention(qkv[:, :qs].view(n_, cfg.q_heads, cfg.head_dim), L_["kc"], L_["vc"], L_["qseq"],
                                   L_["qlen"], L_["tab"], bs_kv, cfg.head_dim ** -0.5, out=L_["attn_out"],
-                                  max_query_len=L_["mql"])
+                                  max_query_len=L_["mql"], cu_seqlens=L_.get("cu"))
         sc2, xq2 = ops.q8_quantize_rows(att.view(n_, qs))
         o = ops.matmul_q8_0(xq2, sc2, *L_["o"], Hd, tdt, out=L_["o_out"])
         _, sc3, xq3 = ops.rms_norm_q8(o, L_["w_post"], cfg.eps, residual=L_["r"], want_out=False)

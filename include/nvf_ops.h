@@ -268,6 +268,20 @@ int nvf_paged_attention_ws(const void* q, void* out, const void* k_cache, const 
                            float scale, int64_t q_stride, int64_t max_query_len, void* workspace,
                            int64_t workspace_bytes, int dtype, void* stream);
 
+/* nvf_paged_attention_ws for a batch whose token layout the caller also holds on the
+ * host: cu_seqlens_host [num_seqs + 1] (0, then each sequence's end; the last entry is
+ * tokens), the packing that query_seq describes on the device (the reference's
+ * cu_seqlens_q, include/nanovllm/context.hpp:8-25, built on the host by
+ * ModelRunner::prepare_prefill, src/model_runner.cpp:43-128).  When every sequence
+ * starts at a multiple of 128 tokens, every 128-token tile holds one sequence and the
+ * launch for tokens of mixed tiles is not made.  Results equal nvf_paged_attention_ws's. */
+int nvf_paged_attention_seqs_ws(const void* q, void* out, const void* k_cache, const void* v_cache,
+                                const int32_t* query_seq, const int32_t* query_key_len, const int32_t* block_tables,
+                                const int32_t* cu_seqlens_host, int num_seqs, int64_t tokens, int q_heads,
+                                int kv_heads, int head_dim, int block_size, int max_blocks, float scale,
+                                int64_t q_stride, int64_t max_query_len, void* workspace, int64_t workspace_bytes,
+                                int dtype, void* stream);
+
 /* Bytes of workspace nvf_paged_attention_ws uses for this shape and max_query_len
  * hint (0: it would not split).  The context bound is block_size * max_blocks. */
 int64_t nvf_paged_attention_workspace_size(int64_t tokens, int q_heads, int kv_heads, int head_dim, int block_size,

@@ -1187,7 +1187,10 @@ template <typename T>
 int attention_dispatch(const void* q, void* out, const void* kc, const void* vc, const int32_t* qseq,
                        const int32_t* qlen, const int32_t* tables, int64_t tokens, int q_heads, int kv_heads, int hd,
                        int bs, int max_blocks, float scale, int64_t q_stride, int64_t max_query_len, void* ws,
-                       int64_t ws_bytes, hipStream_t st) {
+                       int64_t ws_bytes, hipStream_t st, bool aligned = false) {
+  // aligned: every sequence starts at a multiple of kFaBq tokens (checked on the host
+  // from the caller's cu_seqlens), so every tile is uniform and the tiles' second
+  // launch, whose workgroups would all exit, is not made
   constexpr int N = Pack<T>::N;
   if (tokens > INT32_MAX) return fail(NVF_ERR_INVALID, "paged_attention: too many tokens");
   const float sl = scale * 1.4426950408889634f;
@@ -1250,6 +1253,12 @@ int attention_dispatch(const void* q, void* out, const void* kc, const void* vc,
     }
     const int rc = launch_status("paged_attention(tiles)");
     if (rc != NVF_OK) return rc;
+  }
+  if (tiles && aligned) {
+    if (!split) return NVF_OK;
+    attn_split_combine_kernel<T><<<dim3((unsigned)tokens, (unsigned)q_heads), 256, 0, st>>>(part, ot, tokens,
+                                                                                            q_heads, sp.nsplit);
+    return launch_status("paged_attention(split merge)");
   }
   if (dec) {
     // one workgroup per (token, kv head); for the tiles' second launch (SKIP), one
@@ -1350,11 +1359,11 @@ int nvf_store_kv(const void* key, const void* value, void* k_cache, void* v_cach
   return rc;
 }
 
-int nvf_paged_attention_ws(const void* q, void* out, const void* k_cache, const void* v_cache,
-                           const int32_t* query_seq, const int32_t* query_key_len, const int32_t* block_tables,
-                           int64_t tokens, int q_heads, int kv_heads, int head_dim, int block_size, int max_blocks,
-                           float scale, int64_t q_stride, int64_t max_query_len, void* workspace,
-                           int64_t workspace_bytes, int dtype, void* stream) {
+static int paged_attention_entry(const void* q, void* out, const void* k_cache, const void* v_cache,
+                                 const int32_t* query_seq, const int32_t* query_key_len, const int32_t* block_tables,
+                                 int64_t tokens, int q_heads, int kv_heads, int head_dim, int block_size,
+                                 int max_blocks, float scale, int64_t q_stride, int64_t max_query_len, void* workspace,
+                                 int64_t workspace_bytes, int dtype, void* stream, bool aligned) {
   if (!dtype_ok(dtype)) return fail(NVF_ERR_INVALID, "nvf_paged_attention: bad dtype %d", dtype);
   if (tokens < 0 || q_heads <= 0 || kv_heads <= 0 || head_dim <= 0 || block_size <= 0 || max_blocks <= 0)
     return fail(NVF_ERR_INVALID, "nvf_paged_attention: bad shape");
@@ -1374,8 +1383,40 @@ int nvf_paged_attention_ws(const void* q, void* out, const void* k_cache, const 
   NVF_DISPATCH_DTYPE(dtype, T, rc = attention_dispatch<T>(q, out, k_cache, v_cache, query_seq, query_key_len,
                                                          block_tables, tokens, q_heads, kv_heads, head_dim, block_size,
                                                          max_blocks, scale, q_stride, max_query_len, workspace,
-                                                         workspace_bytes, as_stream(stream)));
+                                                         workspace_bytes, as_stream(stream), aligned));
   return rc;
+}
+
+int nvf_paged_attention_ws(const void* q, void* out, const void* k_cache, const void* v_cache,
+                           const int32_t* query_seq, const int32_t* query_key_len, const int32_t* block_tables,
+                           int64_t tokens, int q_heads, int kv_heads, int head_dim, int block_size, int max_blocks,
+                           float scale, int64_t q_stride, int64_t max_query_len, void* workspace,
+                           int64_t workspace_bytes, int dtype, void* stream) {
+  return paged_attention_entry(q, out, k_cache, v_cache, query_seq, query_key_len, block_tables, tokens, q_heads,
+                               kv_heads, head_dim, block_size, max_blocks, scale, q_stride, max_query_len, workspace,
+                               workspace_bytes, dtype, stream, false);
+}
+
+int nvf_paged_attention_seqs_ws(const void* q, void* out, const void* k_cache, const void* v_cache,
+                                const int32_t* query_seq, const int32_t* query_key_len, const int32_t* block_tables,
+                                const int32_t* cu_seqlens_host, int num_seqs, int64_t tokens, int q_heads,
+                                int kv_heads, int head_dim, int block_size, int max_blocks, float scale,
+                                int64_t q_stride, int64_t max_query_len, void* workspace, int64_t workspace_bytes,
+                                int dtype, void* stream) {
+  if (!cu_seqlens_host || num_seqs <= 0)
+    return fail(NVF_ERR_INVALID, "nvf_paged_attention_seqs_ws: cu_seqlens_host and num_seqs > 0 are required");
+  if (cu_seqlens_host[0] != 0 || cu_seqlens_host[num_seqs] != tokens)
+    return fail(NVF_ERR_INVALID, "nvf_paged_attention_seqs_ws: cu_seqlens must run from 0 to tokens=%lld",
+                (long long)tokens);
+  bool aligned = true;
+  for (int s = 1; s <= num_seqs; ++s) {
+    if (cu_seqlens_host[s] < cu_seqlens_host[s - 1])
+      return fail(NVF_ERR_INVALID, "nvf_paged_attention_seqs_ws: cu_seqlens must not decrease");
+    if (s < num_seqs && cu_seqlens_host[s] % kFaBq != 0) aligned = false;
+  }
+  return paged_attention_entry(q, out, k_cache, v_cache, query_seq, query_key_len, block_tables, tokens, q_heads,
+                               kv_heads, head_dim, block_size, max_blocks, scale, q_stride, max_query_len, workspace,
+                               workspace_bytes, dtype, stream, aligned);
 }
 
 int nvf_paged_attention(const void* q, void* out, const void* k_cache, const void* v_cache, const int32_t* query_seq,

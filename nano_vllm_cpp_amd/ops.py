@@ -14,6 +14,7 @@ import ctypes as C
 import threading
 from pathlib import Path
 
+import numpy as np
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "lib" / "libnvf_ops.so"
@@ -45,6 +46,8 @@ SIGNATURES: dict[str, tuple] = {
                                    _i64, _i32, _vp]),
     "nvf_paged_attention_ws": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i32, _i32, _i32, _i32, _i32, _f32,
                                       _i64, _i64, _vp, _i64, _i32, _vp]),
+    "nvf_paged_attention_seqs_ws": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i64, _i32, _i32, _i32,
+                                           _i32, _i32, _f32, _i64, _i64, _vp, _i64, _i32, _vp]),
     "nvf_paged_attention_workspace_size": (_i64, [_i64, _i32, _i32, _i32, _i32, _i32, _i64]),
     "nvf_q8_quantize_rows": (_i32, [_vp, _vp, _vp, _i64, _i64, _i32, _vp]),
     "nvf_matmul_q8_0": (_i32, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _i32, _vp]),
@@ -244,12 +247,16 @@ def store_kv(key: torch.Tensor, value: torch.Tensor, k_cache: torch.Tensor, v_ca
 
 def paged_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, query_seq: torch.Tensor,
                     query_key_len: torch.Tensor, block_tables: torch.Tensor, block_size: int, scale: float,
-                    out: torch.Tensor | None = None, max_query_len: int = 0, split: bool = True) -> torch.Tensor:
+                    out: torch.Tensor | None = None, max_query_len: int = 0, split: bool = True,
+                    cu_seqlens=None) -> torch.Tensor:
     """q [tokens, q_heads, head_dim] (row stride from the tensor); caches
     [rows, kv_heads, head_dim]; block_tables [seqs, max_blocks] int32.
     max_query_len = 1 promises a decode batch (one query per sequence).  split:
     give the library the workspace for split attention when the shape calls for
-    it (little work over long contexts); False runs unsplit.
+    it (little work over long contexts); False runs unsplit.  cu_seqlens: the
+    batch's packing on the host ([seqs + 1] ints, 0 .. tokens), if the caller has it
+    (nvf_paged_attention_seqs_ws: no launch for mixed tiles when every sequence
+    starts at a multiple of 128 tokens).
     Returns out [tokens, q_heads, head_dim] in q's dtype."""
     tokens, q_heads, head_dim = q.shape
     kv_heads = k_cache.shape[1]
@@ -258,6 +265,15 @@ def paged_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tenso
     ws_bytes = lib().nvf_paged_attention_workspace_size(tokens, q_heads, kv_heads, head_dim, block_size,
                                                        max_blocks, max_query_len) if split else 0
     ws = torch.empty((ws_bytes + 15) // 16 * 4, dtype=torch.float32, device=q.device) if ws_bytes > 0 else None
+    if cu_seqlens is not None:
+        cu = np.ascontiguousarray(np.asarray(cu_seqlens, dtype=np.int32))
+        _check(lib().nvf_paged_attention_seqs_ws(
+            _dev_rows(q, "q"), _dev(out, "out"), _dev(k_cache, "k_cache"), _dev(v_cache, "v_cache"),
+            _dev(query_seq, "query_seq"), _dev(query_key_len, "query_key_len"), _dev(block_tables, "block_tables"),
+            cu.ctypes.data, len(cu) - 1, tokens, q_heads, kv_heads, head_dim, block_size, max_blocks, scale,
+            q.stride(0), max_query_len, ws.data_ptr() if ws is not None else None, ws_bytes, _dt(q), _stream()),
+            "paged_attention")
+        return out
     _check(lib().nvf_paged_attention_ws(_dev_rows(q, "q"), _dev(out, "out"), _dev(k_cache, "k_cache"),
                                         _dev(v_cache, "v_cache"), _dev(query_seq, "query_seq"),
                                         _dev(query_key_len, "query_key_len"), _dev(block_tables, "block_tables"),

@@ -442,3 +442,42 @@ def test_paged_attention_decode_full_vs_torch(gpu, shape):
         tol = REL[H.F16] * vmax[:, None] + ref.abs() * 2.0 ** -10 + 1e-6
         bad = ((out[s_] - ref).abs() > tol).sum().item()
         assert bad == 0, f"sequence {s_} (context {c}): {bad} outputs outside tolerance"
+
+
+@pytest.mark.parametrize("dt", [H.F16, H.BF16, H.F32], ids=["f16", "bf16", "f32"])
+@pytest.mark.parametrize("lens,prefix", [([256, 384, 128], 0),      # every start a multiple of 128
+                                         ([200, 312, 100], 0),      # mixed tiles: the second launch runs
+                                         ([256], 8192),             # a chunk after a long prefix: split tiles
+                                         ([384, 130], 64)])         # a partial last tile
+def test_paged_attention_host_cu_seqlens(gpu, dt, lens, prefix):
+    """nvf_paged_attention_seqs_ws (host cu_seqlens) gives the bit-identical output of
+    nvf_paged_attention_ws: with 128-aligned sequence starts it only leaves out the
+    launch whose workgroups would all exit."""
+    g = torch.Generator(device=gpu)
+    g.manual_seed(sum(lens) + prefix + dt)
+    tdt = H.torch_dtype(dt)
+    qh, kvh, hd, bs = 28, 4, 128, 256
+    ctx = [prefix + n for n in lens]
+    nbs = [-(-c // bs) for c in ctx]
+    rows = sum(nbs) * bs
+    kc = torch.randn(rows, kvh, hd, device=gpu, generator=g).to(tdt)
+    vc = torch.randn(rows, kvh, hd, device=gpu, generator=g).to(tdt)
+    tab = torch.full((len(lens), max(nbs)), -1, dtype=torch.int32)
+    perm = torch.randperm(sum(nbs), generator=torch.Generator().manual_seed(3)).to(torch.int32)
+    o = 0
+    for s_, nb in enumerate(nbs):
+        tab[s_, :nb] = perm[o:o + nb]
+        o += nb
+    tab = tab.to(gpu)
+    T = sum(lens)
+    qs = torch.cat([torch.full((n,), s_, dtype=torch.int32) for s_, n in enumerate(lens)]).to(gpu)
+    ql = torch.cat([torch.arange(prefix + 1, prefix + n + 1, dtype=torch.int32) for n in lens]).to(gpu)
+    q = torch.randn(T, qh, hd, device=gpu, generator=g).to(tdt)
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    case(f"paged_attention host cu_seqlens lens={lens} prefix={prefix} dt={dt}")
+    ref = ops.paged_attention(q, kc, vc, qs, ql, tab, bs, hd ** -0.5)
+    got = ops.paged_attention(q, kc, vc, qs, ql, tab, bs, hd ** -0.5, cu_seqlens=cu)
+    torch.cuda.synchronize()
+    H.assert_bitexact(H.to_host(got), H.to_host(ref), "host cu_seqlens vs device-only metadata")
+    with pytest.raises(RuntimeError):  # the last entry must be the token count
+        ops.paged_attention(q, kc, vc, qs, ql, tab, bs, hd ** -0.5, cu_seqlens=cu[:-1])
