@@ -237,7 +237,13 @@ def main() -> int:
                     torch.empty(n_ * k_ // 32, device=dev).uniform_(lo, hi, generator=g).half().view(torch.int16))
         lw = {"w_in": randn((Hd,), 1.0, 0.1), "w_post": randn((Hd,), 1.0, 0.1),
               # (o adds into the residual on every call: small scales keep it within fp16)
-              "qkv": q8w(qs + 2 * ks, Hd), "o": q8w(Hd, qs, 1e-5, 1e-4), "gu": q8w(2 * I, Hd), "down": q8w(Hd, I)}
+              "qkv": q8w(qs + 2 * ks, Hd), "o": q8w(Hd, qs, 1e-5, 1e-4), "gu": q8w(2 * I, Hd), "down": q8w(Hd, I),
+              # Qwen3 (config 3): per-head QK-norm gammas, no qkv bias (model.cpp:611-616);
+              # Qwen2.5: the fp32 qkv bias (model.cpp:768-772), no QK-norm
+              "qn": randn((cfg.head_dim,), 1.0, 0.1) if cfg.qk_norm else None,
+              "kn": randn((cfg.head_dim,), 1.0, 0.1) if cfg.qk_norm else None,
+              "bias": None if cfg.qk_norm else torch.randn(qs + 2 * ks, generator=g, device=dev) * 0.5}
+        model_name = cfg.name.split(" ")[0].replace("qwen", "Qwen").replace("b", "B")
 
         def build_layer(lpos, lseq, seq_ctx, mql, seed):
             """Activations, a paged KV cache and metadata for tokens at positions lpos
@@ -372,15 +378,16 @@ def main() -> int:
     small_out = torch.empty_like(attn_small[0]) if attn_small is not None else None
 
     def run_layer_on(L_):
-        # model.cpp:758-833's per-layer sequence, Qwen2.5 (no QK-norm): input RMSNorm (writing the
-        # qkv GEMM's int8 rows), qkv, RoPE on the q and k columns of the packed row fused with the KV store,
-        # paged attention, o (quantize + GEMM), post-attention residual-add RMSNorm (int8 rows),
-        # gate_up, SwiGLU (int8 rows), down
+        # model.cpp:758-833's per-layer sequence: input RMSNorm (writing the qkv GEMM's int8 rows),
+        # qkv, then in one launch the qkv bias (Qwen2.5) or the QK-norm (Qwen3), RoPE on the q and k
+        # columns of the packed row and the KV store, paged attention, o (quantize + GEMM),
+        # post-attention residual-add RMSNorm (int8 rows), gate_up, SwiGLU (int8 rows), down
         n_ = L_["T"]
         _, sc, xq = ops.rms_norm_q8(L_["h"], L_["w_in"], cfg.eps, residual=L_["r"], want_out=False)
         qkv = ops.matmul_q8_0(xq, sc, *L_["qkv"], qs + 2 * ks, tdt, out=L_["qkv_out"])
-        ops.qk_norm_rope_store_kv(qkv[:, :qs], qkv[:, qs:qs + ks], qkv[:, qs + ks:], L_["pos"], None, None, inv,
-                                  cfg.q_heads, cfg.kv_heads, cfg.head_dim, L_["kc"], L_["vc"], L_["slots"], cfg.eps)
+        ops.qk_norm_rope_store_kv(qkv[:, :qs], qkv[:, qs:qs + ks], qkv[:, qs + ks:], L_["pos"], L_["qn"], L_["kn"],
+                                  inv, cfg.q_heads, cfg.kv_heads, cfg.head_dim, L_["kc"], L_["vc"], L_["slots"],
+                                  cfg.eps, qkv_bias=L_["bias"])
         att = ops.paged_attention(qkv[:, :qs].view(n_, cfg.q_heads, cfg.head_dim), L_["kc"], L_["vc"], L_["qseq"],
                                   L_["qlen"], L_["tab"], bs_kv, cfg.head_dim ** -0.5, out=L_["attn_out"],
                                   max_query_len=L_["mql"], cu_seqlens=L_.get("cu"))
@@ -455,6 +462,7 @@ def main() -> int:
     # spin; "eager_us" is the plain back-to-back mean with the host in the loop.
     stream = torch.cuda.current_stream()
     res_ops = {}
+    act_name = {H.F16: "fp16", H.BF16: "bf16", H.F32: "fp32"}[dt]
     _lens = np.diff(cfg.cu_seqlens())
     batch_desc = (f"{len(_lens)} one-token queries at random positions" if int(_lens.max()) == 1
                   else f"causal prefill {len(_lens)} x {T // len(_lens)} tokens")
@@ -516,17 +524,17 @@ def main() -> int:
                           "GB_s": round(small_bytes / (t_us * 1e-6) / 1e9, 1),
                           "frac_of_peak": round(small_bytes / (t_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)})
         elif n == "layer_decode":
-            entry.update({"shape": "one Qwen2.5-7B decoder layer, decode step of 256 sequences (context U[1, 4096]), "
-                                   "Q8_0 weights, fp16 activations and KV cache",
+            entry.update({"shape": f"one {model_name} decoder layer, decode step of 256 sequences (context U[1, 4096]), "
+                                   f"Q8_0 weights, {act_name} activations and KV cache",
                           "tokens_per_s": round(256 / (t_us * 1e-6), 1),
                           "weights_and_kv_GB_s": round((dec_ops / 2 / 256 * 34 / 32 + dec_kv_bytes) / (t_us * 1e-6) / 1e9,
                                                        1)})
         elif n in ("layer_b1", "layer_b1_graph"):
-            entry["shape"] = ("one Qwen2.5-7B decoder layer, decode step of 1 sequence with 4096 keys of context"
+            entry["shape"] = (f"one {model_name} decoder layer, decode step of 1 sequence with 4096 keys of context"
                               + (", replayed from a captured HIP graph" if n == "layer_b1_graph" else ", eager launches"))
         elif n == "layer":
-            entry.update({"shape": f"one Qwen2.5-7B decoder layer, {T} tokens ({batch_desc}), Q8_0 weights, "
-                                   f"fp16 activations and KV cache",
+            entry.update({"shape": f"one {model_name} decoder layer, {T} tokens ({batch_desc}), Q8_0 weights, "
+                                   f"{act_name} activations and KV cache",
                           "tokens_per_s": round(T / (t_us * 1e-6), 1),
                           "gemm_TOP_s": round(layer_ops / (t_us * 1e-6) / 1e12, 1),
                           "effective_TOP_s_incl_attention": round((layer_ops + layer_attn_flops) / (t_us * 1e-6) / 1e12, 1)})

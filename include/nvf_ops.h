@@ -66,6 +66,10 @@ void hip_rms_norm(const float* x, const float* weight, float* out, int rows, int
 void hip_rms_norm_add(const float* x, float* residual, const float* weight, float* out, int rows, int hidden,
                       float eps);
 
+/* hip_ops.hpp:12 -- x[r,c] += bias[c] over rows x cols (the Qwen2.5 qkv bias,
+ * src/model.cpp:768-772; kernel src/hip_ops.hip:366-371). */
+void hip_add_bias_inplace(float* x, const float* bias, int rows, int cols);
+
 /* hip_ops.hpp:17 -- out[r,c] = silu(gate_up[r,c]) * gate_up[r,I+c]. */
 void hip_silu_and_mul(const float* gate_up, float* out, int rows, int intermediate);
 
@@ -157,6 +161,25 @@ int nvf_qk_norm_rope_store_kv(void* q, void* k, const void* v, const int64_t* po
                               const void* k_w, const float* inv_freq, int64_t tokens, int q_heads, int kv_heads,
                               int head_dim, int64_t q_stride, int64_t k_stride, int64_t v_stride, float eps,
                               void* k_cache, void* v_cache, const int32_t* slot_mapping, int dtype, void* stream);
+
+/* nvf_qk_norm_rope_store_kv with the Qwen2.5 qkv bias added first: the reference's
+ * src/model.cpp:768-778 sequence (hip_add_bias_inplace on q, k and v, then QK-norm,
+ * RoPE and hip_store_kv) in one launch where the shape allows.  qkv_bias: device fp32
+ * [q_heads*head_dim | kv_heads*head_dim | kv_heads*head_dim] (16-byte aligned for the
+ * fused launch); NULL = no bias (then exactly nvf_qk_norm_rope_store_kv).  The bias
+ * is added in fp32 to the loaded value, which stays fp32 through the norm and the
+ * rotation (one rounding at the store; in fp32 storage this equals the reference's
+ * separate passes bit for bit).  q and k hold the biased, rotated heads afterwards;
+ * v + v_bias goes to v_cache and the v tensor itself is left unchanged. */
+int nvf_qkv_bias_qk_norm_rope_store_kv(void* q, void* k, const void* v, const float* qkv_bias,
+                                       const int64_t* positions, const void* q_w, const void* k_w,
+                                       const float* inv_freq, int64_t tokens, int q_heads, int kv_heads, int head_dim,
+                                       int64_t q_stride, int64_t k_stride, int64_t v_stride, float eps, void* k_cache,
+                                       void* v_cache, const int32_t* slot_mapping, int dtype, void* stream);
+
+/* x[r*stride + c] += bias[c] for r < rows, c < cols (replaces hip_add_bias_inplace,
+ * hip_ops.hpp:12): x in `dtype`, bias fp32 [cols], one rounding per element. */
+int nvf_add_bias(void* x, const float* bias, int64_t rows, int64_t cols, int64_t stride, int dtype, void* stream);
 
 /* Q8_0 gather, split planes (as hip_embedding_q8) -> out in out_dtype.
  * vocab > 0: ids outside [0, vocab) produce a NaN row instead of a read;

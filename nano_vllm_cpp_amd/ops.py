@@ -34,6 +34,7 @@ SIGNATURES: dict[str, tuple] = {
     "hip_rms_norm_add": (None, [_vp, _vp, _vp, _vp, _i32, _i32, _f32]),
     "hip_silu_and_mul": (None, [_vp, _vp, _i32, _i32]),
     "hip_rope_inplace": (None, [_vp, _vp, _i32, _i32, _i32, _i64, _vp]),
+    "hip_add_bias_inplace": (None, [_vp, _vp, _i32, _i32]),
     "hip_embedding": (None, [_vp, _vp, _i32, _i32, _vp]),
     "hip_embedding_u16": (None, [_vp, _vp, _i32, _i32, _vp, C.c_bool]),
     "hip_embedding_q8": (None, [_vp, _vp, _vp, _i32, _i32, _vp]),
@@ -61,6 +62,9 @@ SIGNATURES: dict[str, tuple] = {
     "nvf_qk_norm_rope": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i32, _i32, _i32, _i64, _i64, _f32, _i32, _vp]),
     "nvf_qk_norm_rope_store_kv": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i32, _i32, _i32, _i64, _i64, _i64,
                                          _f32, _vp, _vp, _vp, _i32, _vp]),
+    "nvf_qkv_bias_qk_norm_rope_store_kv": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i32, _i32, _i32,
+                                                  _i64, _i64, _i64, _f32, _vp, _vp, _vp, _i32, _vp]),
+    "nvf_add_bias": (_i32, [_vp, _vp, _i64, _i64, _i64, _i32, _vp]),
     "nvf_embedding_q8_0": (_i32, [_vp, _vp, _vp, _i64, _i64, _i64, _vp, _i32, _vp]),
     "nvf_embedding_q8_0_blocks": (_i32, [_vp, _vp, _i64, _i64, _i64, _vp, _i32, _vp]),
     "nvf_embedding_qk": (_i32, [_vp, _vp, _i64, _i64, _i64, _i32, _i32, _vp, _i32, _vp]),
@@ -347,21 +351,50 @@ def qk_norm_rope(q: torch.Tensor, k: torch.Tensor | None, positions: torch.Tenso
 def qk_norm_rope_store_kv(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, positions: torch.Tensor,
                           q_w: torch.Tensor | None, k_w: torch.Tensor | None, inv_freq: torch.Tensor, q_heads: int,
                           kv_heads: int, head_dim: int, k_cache: torch.Tensor, v_cache: torch.Tensor,
-                          slot_mapping: torch.Tensor, eps: float = 1e-6) -> None:
-    """qk_norm_rope(q, k, ...) then store_kv(k, v, k_cache, v_cache, slot_mapping), in one
-    launch where the shape allows.  q [T, q_heads * head_dim], k and v [T, kv_heads *
-    head_dim] (row strides from the tensors); caches [rows, kv_heads, head_dim]."""
+                          slot_mapping: torch.Tensor, eps: float = 1e-6, qkv_bias: torch.Tensor | None = None) -> None:
+    """(qkv bias +) qk_norm_rope(q, k, ...) then store_kv(k, v, k_cache, v_cache, slot_mapping),
+    in one launch where the shape allows.  q [T, q_heads * head_dim], k and v [T, kv_heads *
+    head_dim] (row strides from the tensors); caches [rows, kv_heads, head_dim] contiguous;
+    slot_mapping int32 [T].  qkv_bias: fp32 [(q_heads + 2 * kv_heads) * head_dim] (Qwen2.5),
+    added to q, k and the stored v before the norm and rotation; v itself is left unchanged."""
     tokens = q.shape[0]
     if positions.dtype != torch.int64 or positions.shape != (tokens,):
         raise ValueError("positions must be int64 [tokens]")
     if inv_freq.dtype != torch.float32 or inv_freq.numel() != head_dim // 2:
         raise ValueError("inv_freq must be float32 [head_dim/2]")
-    _check(lib().nvf_qk_norm_rope_store_kv(
-        _dev_rows(q, "q"), _dev_rows(k, "k"), _dev_rows(v, "v"), _dev(positions, "positions"),
+    kn = kv_heads * head_dim
+    if q.dim() != 2 or q.shape[1] != q_heads * head_dim:
+        raise ValueError("q must be [tokens, q_heads * head_dim]")
+    for name, x in (("k", k), ("v", v)):
+        if x.dim() != 2 or x.shape != (tokens, kn):
+            raise ValueError(f"{name} must be [tokens, kv_heads * head_dim] = [{tokens}, {kn}]")
+    for name, x in (("k", k), ("v", v), ("k_cache", k_cache), ("v_cache", v_cache)):
+        if x.dtype != q.dtype:
+            raise ValueError(f"{name} must have q's dtype {q.dtype}")
+    for name, c in (("k_cache", k_cache), ("v_cache", v_cache)):
+        if c.dim() != 3 or tuple(c.shape[1:]) != (kv_heads, head_dim):
+            raise ValueError(f"{name} must be [rows, kv_heads, head_dim]")
+    if slot_mapping.dtype != torch.int32 or slot_mapping.shape != (tokens,):
+        raise ValueError("slot_mapping must be int32 [tokens]")
+    if qkv_bias is not None and (qkv_bias.dtype != torch.float32 or
+                                 qkv_bias.numel() != (q_heads + 2 * kv_heads) * head_dim):
+        raise ValueError("qkv_bias must be float32 [(q_heads + 2 * kv_heads) * head_dim]")
+    _check(lib().nvf_qkv_bias_qk_norm_rope_store_kv(
+        _dev_rows(q, "q"), _dev_rows(k, "k"), _dev_rows(v, "v"),
+        _dev(qkv_bias, "qkv_bias") if qkv_bias is not None else None, _dev(positions, "positions"),
         _dev(q_w, "q_w") if q_w is not None else None, _dev(k_w, "k_w") if k_w is not None else None,
         _dev(inv_freq, "inv_freq"), tokens, q_heads, kv_heads, head_dim, q.stride(0), k.stride(0), v.stride(0), eps,
         _dev(k_cache, "k_cache"), _dev(v_cache, "v_cache"), _dev(slot_mapping, "slot_mapping"), _dt(q), _stream()),
         "qk_norm_rope_store_kv")
+
+
+def add_bias(x: torch.Tensor, bias: torch.Tensor) -> None:
+    """x[r, :] += bias in place (x [rows, cols] with a row stride; bias fp32 [cols])."""
+    rows, cols = x.shape
+    if bias.dtype != torch.float32 or bias.shape != (cols,):
+        raise ValueError("bias must be float32 [cols]")
+    _check(lib().nvf_add_bias(_dev_rows(x, "x"), _dev(bias, "bias"), rows, cols, x.stride(0), _dt(x), _stream()),
+           "add_bias")
 
 
 # ---------------------------------------------------------------------------

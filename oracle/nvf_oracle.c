@@ -350,13 +350,16 @@ void orc_rope(void* data, const int64_t* positions, int64_t tokens, int heads, i
  * normalised head stays fp32 between the two steps; one rounding at the end.
  * A NULL gamma skips the norm for that tensor. */
 static void qk_one(void* buf, const int64_t* positions, const void* gw, const float* inv_freq,
-                   int64_t tokens, int heads, int head_dim, int64_t stride, float eps, int dtype) {
+                   int64_t tokens, int heads, int head_dim, int64_t stride, float eps, int dtype,
+                   const float* bias) {
   float* hv = (float*)malloc(sizeof(float) * (size_t)head_dim * 2);
   float* nv = hv + head_dim;
   for (int64_t t = 0; t < tokens; ++t)
     for (int h = 0; h < heads; ++h) {
       int64_t base = t * stride + (int64_t)h * head_dim;
       for (int d = 0; d < head_dim; ++d) hv[d] = orc_load(buf, base + d, dtype);
+      if (bias)
+        for (int d = 0; d < head_dim; ++d) hv[d] += bias[(int64_t)h * head_dim + d];
       if (gw) {
         rms_row(hv, gw, nv, head_dim, eps, dtype);
         memcpy(hv, nv, sizeof(float) * (size_t)head_dim);
@@ -370,8 +373,44 @@ static void qk_one(void* buf, const int64_t* positions, const void* gw, const fl
 void orc_qk_norm_rope(void* q, void* k, const int64_t* positions, const void* q_w, const void* k_w,
                       const float* inv_freq, int64_t tokens, int q_heads, int kv_heads, int head_dim,
                       int64_t q_stride, int64_t k_stride, float eps, int dtype) {
-  if (q && q_heads > 0) qk_one(q, positions, q_w, inv_freq, tokens, q_heads, head_dim, q_stride, eps, dtype);
-  if (k && kv_heads > 0) qk_one(k, positions, k_w, inv_freq, tokens, kv_heads, head_dim, k_stride, eps, dtype);
+  if (q && q_heads > 0) qk_one(q, positions, q_w, inv_freq, tokens, q_heads, head_dim, q_stride, eps, dtype, NULL);
+  if (k && kv_heads > 0) qk_one(k, positions, k_w, inv_freq, tokens, kv_heads, head_dim, k_stride, eps, dtype, NULL);
+}
+
+/* ---- qkv bias ------------------------------------------------------------- */
+
+/* src/hip_ops.hip:366-371 (add_bias_kernel, called by hip_add_bias_inplace :688-692):
+ * x[r, c] += bias[c], fp32 bias, one rounding to the storage type. */
+void orc_add_bias(void* x, const float* bias, int64_t rows, int64_t cols, int64_t stride, int dtype) {
+  for (int64_t r = 0; r < rows; ++r)
+    for (int64_t c = 0; c < cols; ++c)
+      orc_store(x, r * stride + c, orc_load(x, r * stride + c, dtype) + bias[c], dtype);
+}
+
+/* src/model.cpp:768-778 then hip_store_kv (:780-781): qkv bias on q, k and v, QK-norm
+ * (gammas optional), RoPE, then the KV store, as one op.  The biased head stays fp32
+ * through the norm and the rotation (in fp32 storage the reference's separate passes
+ * give the same bits); v + v_bias is rounded once into v_cache and v is not written.
+ * bias: fp32 [q_heads*hd | kv_heads*hd | kv_heads*hd] or NULL. */
+void orc_qkv_bias_qk_norm_rope_store_kv(void* q, void* k, const void* v, const float* bias,
+                                        const int64_t* positions, const void* q_w, const void* k_w,
+                                        const float* inv_freq, int64_t tokens, int q_heads, int kv_heads,
+                                        int head_dim, int64_t q_stride, int64_t k_stride, int64_t v_stride,
+                                        float eps, void* k_cache, void* v_cache, const int32_t* slot_mapping,
+                                        int dtype) {
+  const int64_t qn = (int64_t)q_heads * head_dim, kn = (int64_t)kv_heads * head_dim;
+  if (q && q_heads > 0)
+    qk_one(q, positions, q_w, inv_freq, tokens, q_heads, head_dim, q_stride, eps, dtype, bias);
+  qk_one(k, positions, k_w, inv_freq, tokens, kv_heads, head_dim, k_stride, eps, dtype, bias ? bias + qn : NULL);
+  for (int64_t t = 0; t < tokens; ++t) {
+    const int32_t slot = slot_mapping[t];
+    if (slot < 0) continue;
+    for (int64_t c = 0; c < kn; ++c) {
+      orc_store(k_cache, (int64_t)slot * kn + c, orc_load(k, t * k_stride + c, dtype), dtype);
+      const float vv = orc_load(v, t * v_stride + c, dtype) + (bias ? bias[qn + kn + c] : 0.0f);
+      orc_store(v_cache, (int64_t)slot * kn + c, vv, dtype);
+    }
+  }
 }
 
 /* ---- Q8 activation row scale (for the Q8_0 GEMM) ------------------------ */

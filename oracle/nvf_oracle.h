@@ -29,6 +29,10 @@
  *                              homogeneity and gamma-linearity invariants
  *   RoPE / QK-norm ........... pos=0 identity, pair-norm preservation,
  *                              rotate(p) then rotate(-p) identity, composition
+ *   qkv bias ................. closed form x + b (one rounding); the fused bias +
+ *                              norm + RoPE + store equals, in fp32 storage, the
+ *                              composition add_bias -> qk_norm_rope -> store_kv,
+ *                              and with a zero bias the unbiased op
  *   SiLU*up .................. silu(0)=0, silu(g)-silu(-g)=g, double-exp
  *                              brute force
  *   Q8 row scale / quantize .. closed forms (the row maximum maps to +-127,
@@ -94,6 +98,17 @@ void orc_rope(void* data, const int64_t* positions, int64_t tokens, int heads, i
 void orc_qk_norm_rope(void* q, void* k, const int64_t* positions, const void* q_w, const void* k_w,
                       const float* inv_freq, int64_t tokens, int q_heads, int kv_heads, int head_dim,
                       int64_t q_stride, int64_t k_stride, float eps, int dtype);
+
+/* src/hip_ops.hip:366-371 (add_bias_kernel): x[r*stride + c] += bias[c], one rounding.
+ * orc_qkv_bias_qk_norm_rope_store_kv: src/model.cpp:768-781 (bias on q, k, v; QK-norm;
+ * RoPE; KV store) as one op with the biased head kept in fp32 until its store. */
+void orc_add_bias(void* x, const float* bias, int64_t rows, int64_t cols, int64_t stride, int dtype);
+void orc_qkv_bias_qk_norm_rope_store_kv(void* q, void* k, const void* v, const float* bias,
+                                        const int64_t* positions, const void* q_w, const void* k_w,
+                                        const float* inv_freq, int64_t tokens, int q_heads, int kv_heads,
+                                        int head_dim, int64_t q_stride, int64_t k_stride, int64_t v_stride,
+                                        float eps, void* k_cache, void* v_cache, const int32_t* slot_mapping,
+                                        int dtype);
 
 /* src/hip_ops.hip:205-217 (q8_row_scale_kernel): scale[r] = 127 / max|x[r,:]|,
  * 0 when the maximum is <= 1e-8; and the int8 values its GEMM forms from them,

@@ -50,6 +50,10 @@ void ref_hip_store_kv(const float* key, const float* value, float* k_cache, floa
   hip_store_kv(key, value, k_cache, v_cache, slots, tokens, kv_heads, head_dim);
   HIP_CHECK(hipDeviceSynchronize());
 }
+void ref_hip_add_bias_inplace(float* x, const float* bias, int rows, int cols) {
+  hip_add_bias_inplace(x, bias, rows, cols);
+  HIP_CHECK(hipDeviceSynchronize());
+}
 void ref_hip_paged_attention(const float* q, float* out, const float* k_cache, const float* v_cache,
                              const int32_t* query_seq, const int32_t* query_key_len, const int32_t* block_tables,
                              int tokens, int q_heads, int kv_heads, int head_dim, int block_size, int max_blocks,

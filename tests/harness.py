@@ -47,6 +47,9 @@ _ORACLE_SIGS = {
     "orc_embedding_rms_norm": (None, [_vp, _i32, _vp, _vp, _i64, _i64, _vp, _vp, _vp, _f32, _i32]),
     "orc_matmul_q8_i8": (None, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _vp]),
     "orc_store_kv": (None, [_vp, _vp, _vp, _vp, _vp, _i64, _i32, _i32, _i32]),
+    "orc_add_bias": (None, [_vp, _vp, _i64, _i64, _i64, _i32]),
+    "orc_qkv_bias_qk_norm_rope_store_kv": (None, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i32, _i32, _i32,
+                                                  _i64, _i64, _i64, _f32, _vp, _vp, _vp, _i32]),
     "orc_paged_attention": (None, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i32, _i32, _i32, _i32, _i32, _f32,
                                    _i32, _vp, _vp]),
     "orc_matmul_q8": (None, [_vp, _i32, _vp, _vp, _i64, _i64, _i64, _vp, _vp, _vp, _vp]),
@@ -100,6 +103,7 @@ def ref_hip() -> C.CDLL | None:
     h.ref_hip_embedding_u16.argtypes = [_vp, _vp, _i32, _i32, _vp, _i32]
     h.ref_hip_matmul_q8.argtypes = [_vp, _vp, _vp, _i32, _i32, _i32, _vp]
     h.ref_hip_store_kv.argtypes = [_vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32]
+    h.ref_hip_add_bias_inplace.argtypes = [_vp, _vp, _i32, _i32]
     h.ref_hip_paged_attention.argtypes = [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _i32, _f32]
     return h
 

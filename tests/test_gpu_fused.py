@@ -232,6 +232,99 @@ def test_qk_norm_rope_store_kv(gpu, dt, tokens, qh, kvh, hd, norm):
     H.assert_bitexact(H.to_host(kc_b[untouched]), H.to_host(kc0[untouched]), "rows without a slot")
 
 
+@pytest.mark.parametrize("dt", DTYPES, ids=DT_IDS)
+@pytest.mark.parametrize("tokens,qh,kvh,hd,norm", [
+    (37, 28, 4, 128, False),   # Qwen2.5-7B heads, packed [q | k | v] rows: the bias is Qwen2.5's
+    (5, 32, 8, 128, True),     # Qwen3-8B heads with QK-norm (bias and norm together)
+    (9, 14, 2, 64, False),     # Qwen2.5-0.5B heads
+    (3, 4, 1, 256, True),
+    (6, 4, 2, 80, False),      # head_dim 80: the separate-op fallback (add bias, RoPE, store)
+    (4, 8, 40, 128, False),    # kv row of 5120 elements: the fallback
+])
+def test_qkv_bias_qk_norm_rope_store_kv(gpu, dt, tokens, qh, kvh, hd, norm):
+    """nvf_qkv_bias_qk_norm_rope_store_kv against the oracle (model.cpp:768-781 with the
+    biased head kept in fp32): q, k within the RoPE tolerance, the v cache bit-exact
+    (v + b, one rounding), the k cache equal to the stored k, the v tensor unchanged and
+    rows without a slot untouched."""
+    o = H.oracle()
+    r = H.rng(tokens * 173 + qh * 5 + kvh + hd + dt + 11 * norm)
+    tdt = H.torch_dtype(dt)
+    qs, ks = qh * hd, kvh * hd
+    width = qs + 2 * ks
+    qkv_h = H.gen_act(r, (tokens, width), dt, 0.0, 1.0)
+    bias = r.normal(0, 0.5, width).astype(np.float32)
+    pos = r.integers(0, 8192, tokens).astype(np.int64)
+    inv = ops.rope_inv_freq(1e6, hd)
+    qw_h = H.gen_act(r, (hd,), dt, 1.0, 0.1) if norm else None
+    kw_h = H.gen_act(r, (hd,), dt, 1.0, 0.1) if norm else None
+    rows = 2 * tokens + 3
+    slots = r.permutation(rows)[:tokens].astype(np.int32)
+    slots[1 % tokens] = -1
+    kc0 = H.gen_act(r, (rows, ks), dt)
+    vc0 = H.gen_act(r, (rows, ks), dt)
+
+    # oracle on separate q, k, v copies
+    rq = np.ascontiguousarray(qkv_h[:, :qs])
+    rk = np.ascontiguousarray(qkv_h[:, qs:qs + ks])
+    rv = np.ascontiguousarray(qkv_h[:, qs + ks:])
+    rkc, rvc = kc0.copy(), vc0.copy()
+    o.orc_qkv_bias_qk_norm_rope_store_kv(H.ptr(rq), H.ptr(rk), H.ptr(rv), H.ptr(bias), H.ptr(pos), H.ptr(qw_h),
+                                         H.ptr(kw_h), H.ptr(inv.numpy()), tokens, qh, kvh, hd, qs, ks, ks, 1e-6,
+                                         H.ptr(rkc), H.ptr(rvc), H.ptr(slots), dt)
+
+    case(f"qkv_bias_qk_norm_rope_store_kv tokens={tokens} heads={qh}/{kvh} hd={hd} norm={norm} dt={dt}")
+    qkv = H.to_dev(qkv_h, gpu, dt)
+    kc, vc = H.to_dev(kc0, gpu, dt).view(rows, kvh, hd), H.to_dev(vc0, gpu, dt).view(rows, kvh, hd)
+    ops.qk_norm_rope_store_kv(qkv[:, :qs], qkv[:, qs:qs + ks], qkv[:, qs + ks:], torch.from_numpy(pos).to(gpu),
+                              H.to_dev(qw_h, gpu, dt) if norm else None, H.to_dev(kw_h, gpu, dt) if norm else None,
+                              inv.to(gpu), qh, kvh, hd, kc, vc, torch.from_numpy(slots).to(gpu), 1e-6,
+                              qkv_bias=torch.from_numpy(bias).to(gpu))
+    torch.cuda.synchronize()
+    got = H.to_host(qkv)
+    H.assert_close(np.ascontiguousarray(got[:, :qs]), rq, dt, floor=1e-6, what="q")
+    H.assert_close(np.ascontiguousarray(got[:, qs:qs + ks]), rk, dt, floor=1e-6, what="k")
+    H.assert_bitexact(np.ascontiguousarray(got[:, qs + ks:]), rv, "v tensor unchanged")
+    gkc, gvc = H.to_host(kc).reshape(rows, ks), H.to_host(vc).reshape(rows, ks)
+    live = slots[slots >= 0]
+    H.assert_bitexact(gvc, rvc, "v cache (v + b)")
+    H.assert_bitexact(gkc[live], np.ascontiguousarray(got[:, qs:qs + ks])[slots >= 0], "k cache == stored k")
+    untouched = np.setdiff1d(np.arange(rows), live)
+    H.assert_bitexact(gkc[untouched], kc0[untouched], "k rows without a slot")
+
+
+def test_add_bias_vs_reference_kernel(gpu):
+    """hip_add_bias_inplace (drop-in) bit-exact against the reference's own add_bias_kernel
+    (src/hip_ops.hip:366-371) and the oracle; the typed nvf_add_bias on strided 16-bit rows
+    bit-exact against the oracle."""
+    ref = H.ref_hip()
+    r = H.rng(21)
+    rows, cols = 37, 4608
+    x = r.normal(0, 1, (rows, cols)).astype(np.float32)
+    b = r.normal(0, 1, cols).astype(np.float32)
+    want = x.copy()
+    H.oracle().orc_add_bias(H.ptr(want), H.ptr(b), rows, cols, cols, H.F32)
+    db = torch.from_numpy(b).to(gpu)
+    mine = torch.from_numpy(x).to(gpu)
+    case("hip_add_bias_inplace")
+    ops.lib().hip_add_bias_inplace(mine.data_ptr(), db.data_ptr(), rows, cols)
+    torch.cuda.synchronize()
+    H.assert_bitexact(mine.cpu().numpy(), want, "drop-in vs oracle")
+    if ref is not None:
+        theirs = torch.from_numpy(x).to(gpu)
+        case("reference add_bias kernel")
+        ref.ref_hip_add_bias_inplace(theirs.data_ptr(), db.data_ptr(), rows, cols)
+        H.assert_bitexact(mine.cpu().numpy(), theirs.cpu().numpy(), "drop-in vs reference kernel")
+    for dt in (H.F16, H.BF16):
+        xs = H.gen_act(r, (rows, cols + 64), dt)
+        want = xs.copy()
+        H.oracle().orc_add_bias(H.ptr(want), H.ptr(b), rows, cols, cols + 64, dt)
+        d = H.to_dev(xs, gpu, dt)
+        case(f"nvf_add_bias dt={dt}")
+        ops.add_bias(d[:, :cols], db)
+        torch.cuda.synchronize()
+        H.assert_bitexact(H.to_host(d), want, f"nvf_add_bias dt={dt}")
+
+
 def test_qk_norm_rope_store_kv_bad_args(gpu):
     q = torch.zeros(2, 256, dtype=torch.float16, device=gpu)
     k = torch.zeros(2, 128, dtype=torch.float16, device=gpu)
@@ -240,8 +333,17 @@ def test_qk_norm_rope_store_kv_bad_args(gpu):
     kc = torch.zeros(4, 1, 128, dtype=torch.float16, device=gpu)
     slots = torch.zeros(2, dtype=torch.int32, device=gpu)
     v_narrow = torch.zeros(2, 64, dtype=torch.float16, device=gpu)  # row stride 64 < kv_heads * head_dim
-    with pytest.raises(RuntimeError):
+    with pytest.raises(ValueError):  # the Python front end checks v's shape
         ops.qk_norm_rope_store_kv(q, k, v_narrow, pos, None, None, inv, 2, 1, 128, kc, kc.clone(), slots)
+    with pytest.raises(ValueError):  # an int64 slot mapping
+        ops.qk_norm_rope_store_kv(q, k, k, pos, None, None, inv, 2, 1, 128, kc, kc.clone(), slots.long())
+    with pytest.raises(ValueError):  # a cache of another dtype
+        ops.qk_norm_rope_store_kv(q, k, k, pos, None, None, inv, 2, 1, 128, kc.float(), kc.clone(), slots)
+    with pytest.raises(RuntimeError):  # and so does the C ABI (v row stride 64 < kv_heads * head_dim)
+        ops._check(ops.lib().nvf_qk_norm_rope_store_kv(q.data_ptr(), k.data_ptr(), v_narrow.data_ptr(),
+                                                       pos.data_ptr(), None, None, inv.data_ptr(), 2, 2, 1, 128, 256,
+                                                       128, 64, 1e-6, kc.data_ptr(), kc.data_ptr(), slots.data_ptr(),
+                                                       1, None), "qk_norm_rope_store_kv")
     with pytest.raises(RuntimeError):  # no slot mapping
         lib_rc = ops.lib().nvf_qk_norm_rope_store_kv(q.data_ptr(), k.data_ptr(), k.data_ptr(), pos.data_ptr(), None,
                                                      None, inv.data_ptr(), 2, 2, 1, 128, 256, 128, 128, 1e-6,

@@ -420,6 +420,98 @@ def test_qk_norm_rope_is_the_composition(o):
     assert np.array_equal(fq, uq) and np.array_equal(fk, uk)
 
 
+@pytest.mark.parametrize("dt", [H.F32, H.F16, H.BF16])
+def test_add_bias_closed_form(o, dt):
+    """x + b in fp32, one rounding to the storage type; rows with a stride (the columns
+    past cols untouched)."""
+    r = H.rng(13)
+    rows, cols, stride = 7, 96, 100
+    x = H.gen_act(r, (rows, stride), dt)
+    b = r.normal(0, 1, cols).astype(np.float32)
+    y = x.copy()
+    o.orc_add_bias(H.ptr(y), H.ptr(b), rows, cols, stride, dt)
+    want = H.to_storage(H.from_storage(x[:, :cols], dt).astype(np.float32) + b[None, :], dt)
+    assert np.array_equal(y[:, :cols], want) and np.array_equal(y[:, cols:], x[:, cols:])
+    # hand values: 1.5 + 0.25 = 1.75 exactly; 1 + 2^-11 rounds to 1 in fp16 (a tie, to even)
+    if dt == H.F16:
+        hx = H.to_storage(np.array([[1.5, 1.0]], np.float32), dt)
+        o.orc_add_bias(H.ptr(hx), H.ptr(np.array([0.25, 2.0 ** -11], np.float32)), 1, 2, 2, dt)
+        assert np.array_equal(H.from_storage(hx, dt).astype(np.float32), np.array([[1.75, 1.0]], np.float32))
+
+
+def _qkv_case(r, dt, T=9, hq=4, hk=2, hd=128, norm=True):
+    q = H.gen_act(r, (T, hq * hd), dt)
+    k = H.gen_act(r, (T, hk * hd), dt)
+    v = H.gen_act(r, (T, hk * hd), dt)
+    bias = r.normal(0, 0.5, (hq + 2 * hk) * hd).astype(np.float32)
+    qw = H.gen_act(r, (hd,), dt, 1.0, 0.1) if norm else None
+    kw = H.gen_act(r, (hd,), dt, 1.0, 0.1) if norm else None
+    pos = r.integers(0, 4096, T).astype(np.int64)
+    slots = r.permutation(2 * T)[:T].astype(np.int32)
+    slots[1] = -1  # a skipped token
+    return q, k, v, bias, qw, kw, pos, slots
+
+
+def _fused_qkv(o, q, k, v, bias, qw, kw, pos, slots, inv, hq, hk, hd, dt):
+    T = q.shape[0]
+    fq, fk = q.copy(), k.copy()
+    kc = np.zeros((2 * T, hk * hd), q.dtype)
+    vc = np.zeros((2 * T, hk * hd), q.dtype)
+    v0 = v.copy()
+    o.orc_qkv_bias_qk_norm_rope_store_kv(H.ptr(fq), H.ptr(fk), H.ptr(v), H.ptr(bias), H.ptr(pos), H.ptr(qw),
+                                         H.ptr(kw), H.ptr(inv), T, hq, hk, hd, hq * hd, hk * hd, hk * hd, 1e-6,
+                                         H.ptr(kc), H.ptr(vc), H.ptr(slots), dt)
+    assert np.array_equal(v, v0)  # v is read, not written
+    return fq, fk, kc, vc
+
+
+@pytest.mark.parametrize("norm", [True, False])
+def test_qkv_bias_fused_is_the_composition_fp32(o, norm):
+    """fp32: bias + QK-norm + RoPE + store == add_bias (q, k, v) -> qk_norm_rope -> store_kv
+    (model.cpp:768-781 as separate passes), bit for bit."""
+    r = H.rng(14)
+    hq, hk, hd = 4, 2, 128
+    inv = _inv(o, 1e6, hd)
+    q, k, v, bias, qw, kw, pos, slots = _qkv_case(r, H.F32, hq=hq, hk=hk, hd=hd, norm=norm)
+    T = q.shape[0]
+    fq, fk, kc, vc = _fused_qkv(o, q, k, v, bias, qw, kw, pos, slots, inv, hq, hk, hd, H.F32)
+    uq, uk, uv = q.copy(), k.copy(), v.copy()
+    o.orc_add_bias(H.ptr(uq), H.ptr(bias), T, hq * hd, hq * hd, H.F32)
+    o.orc_add_bias(H.ptr(uk), H.ptr(bias[hq * hd:]), T, hk * hd, hk * hd, H.F32)
+    o.orc_add_bias(H.ptr(uv), H.ptr(bias[(hq + hk) * hd:]), T, hk * hd, hk * hd, H.F32)
+    o.orc_qk_norm_rope(H.ptr(uq), H.ptr(uk), H.ptr(pos), H.ptr(qw), H.ptr(kw), H.ptr(inv), T, hq, hk, hd,
+                       hq * hd, hk * hd, 1e-6, H.F32)
+    ukc, uvc = np.zeros_like(kc), np.zeros_like(vc)
+    o.orc_store_kv(H.ptr(uk), H.ptr(uv), H.ptr(ukc), H.ptr(uvc), H.ptr(slots), T, hk, hd, H.F32)
+    assert np.array_equal(fq, uq) and np.array_equal(fk, uk)
+    assert np.array_equal(kc, ukc) and np.array_equal(vc, uvc)
+
+
+@pytest.mark.parametrize("dt", [H.F16, H.BF16])
+def test_qkv_bias_fused_zero_bias_and_identity(o, dt):
+    """16-bit storage: a zero bias gives the unbiased qk_norm_rope + store_kv exactly; at
+    position 0 without norm the op is x + b rounded once (RoPE is the identity there)."""
+    r = H.rng(15)
+    hq, hk, hd = 4, 2, 128
+    inv = _inv(o, 1e6, hd)
+    q, k, v, bias, qw, kw, pos, slots = _qkv_case(r, dt, hq=hq, hk=hk, hd=hd)
+    T = q.shape[0]
+    fq, fk, kc, vc = _fused_qkv(o, q, k, v, np.zeros_like(bias), qw, kw, pos, slots, inv, hq, hk, hd, dt)
+    uq, uk = q.copy(), k.copy()
+    o.orc_qk_norm_rope(H.ptr(uq), H.ptr(uk), H.ptr(pos), H.ptr(qw), H.ptr(kw), H.ptr(inv), T, hq, hk, hd,
+                       hq * hd, hk * hd, 1e-6, dt)
+    ukc, uvc = np.zeros_like(kc), np.zeros_like(vc)
+    o.orc_store_kv(H.ptr(uk), H.ptr(v), H.ptr(ukc), H.ptr(uvc), H.ptr(slots), T, hk, hd, dt)
+    assert np.array_equal(fq, uq) and np.array_equal(fk, uk) and np.array_equal(kc, ukc) and np.array_equal(vc, uvc)
+    pos0 = np.zeros(T, np.int64)
+    fq, fk, kc, vc = _fused_qkv(o, q, k, v, bias, None, None, pos0, slots, inv, hq, hk, hd, dt)
+    assert np.array_equal(fq, H.to_storage(H.from_storage(q, dt).astype(np.float32) + bias[None, :hq * hd], dt))
+    assert np.array_equal(fk, H.to_storage(H.from_storage(k, dt).astype(np.float32) + bias[None, hq * hd:(hq + hk) * hd], dt))
+    live = slots >= 0
+    assert np.array_equal(vc[slots[live]], H.to_storage(H.from_storage(v[live], dt).astype(np.float32) + bias[None, (hq + hk) * hd:], dt))
+    assert np.array_equal(kc[slots[live]], fk[live])
+
+
 # ---------------------------------------------------------------------------
 # Q8 activation row scale / quantize, fused layer-0 embedding + norm
 # ---------------------------------------------------------------------------
