@@ -310,6 +310,21 @@ int nvf_paged_attention_seqs_ws(const void* q, void* out, const void* k_cache, c
 int64_t nvf_paged_attention_workspace_size(int64_t tokens, int q_heads, int kv_heads, int head_dim, int block_size,
                                            int max_blocks, int64_t max_query_len);
 
+/* No counterpart in the reference: for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  nvf_paged_attention_ws with the split workspace taken from a static
+ * device scratch of nvf_paged_attention_noalloc_max_bytes() (32 MiB) that each GPU
+ * holds until the process ends; nothing is allocated.  A call whose split needs more
+ * (nvf_paged_attention_workspace_size > that) fails with NVF_ERR_INVALID.  Results
+ * equal nvf_paged_attention_ws's with a workspace.  All calls on one GPU share the
+ * scratch: calls that overlap on one GPU (several streams or threads) race. */
+int nvf_paged_attention_noalloc(const void* q, void* out, const void* k_cache, const void* v_cache,
+                                const int32_t* query_seq, const int32_t* query_key_len, const int32_t* block_tables,
+                                int64_t tokens, int q_heads, int kv_heads, int head_dim, int block_size,
+                                int max_blocks, float scale, int64_t q_stride, int64_t max_query_len, int dtype,
+                                void* stream);
+int64_t nvf_paged_attention_noalloc_max_bytes(void);
+
 /* Host helper: inv_freq[i] = (float)(1 / theta^(2i/head_dim)) in double, the
  * table Qwen3Model builds in its constructor (src/model.cpp:416-420).
  * out is HOST memory of head_dim/2 floats. */

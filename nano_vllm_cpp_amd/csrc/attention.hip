@@ -1436,6 +1436,70 @@ int64_t nvf_paged_attention_workspace_size(int64_t tokens, int q_heads, int kv_h
                      split_plan(tokens, q_heads, kv_heads, head_dim, block_size, max_blocks, max_query_len));
 }
 
+// ---------------------------------------------------------------------------
+// nvf_paged_attention_noalloc: nvf_paged_attention_ws for callers that cannot
+// allocate (HIP graph capture, serving loops, harnesses that forbid hipMalloc).
+// The split partials go to `scratch`, a file-scope device array of
+// kAttnScratchBytes that every GPU this library runs on holds until the process
+// ends.  On the host the array's name is only a stand-in for its symbol: its
+// device address (one per GPU) comes from hipGetSymbolAddress, taken on the
+// entry's first call on each device with that device current, and only that
+// address is passed to kernels.  Every call on a GPU shares the one array and
+// leaves its contents behind (every split writes all of its partials, so no
+// clearing is needed); calls that overlap on one GPU (several streams or
+// threads at once) race on it.
+// ---------------------------------------------------------------------------
+constexpr int64_t kAttnScratchBytes = 32ll << 20;  // split decode needs <= 12.8 MB; short prefill chunks after long contexts more
+static __device__ __align__(256) float scratch[kAttnScratchBytes / sizeof(float)];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// scratch's device address on the current device (NULL + last error on failure)
+void* scratch_ptr() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    fail(NVF_ERR_LAUNCH, "nvf_paged_attention_noalloc: no usable current device");
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+      fail(NVF_ERR_LAUNCH, "nvf_paged_attention_noalloc: hipGetSymbolAddress(scratch) failed on device %d: %s", dev,
+           hipGetErrorString(e));
+      return nullptr;
+    }
+    g_scratch_ptr[dev] = p;
+  }
+  return g_scratch_ptr[dev];
+}
+}  // namespace
+
+int64_t nvf_paged_attention_noalloc_max_bytes(void) { return kAttnScratchBytes; }
+
+int nvf_paged_attention_noalloc(const void* q, void* out, const void* k_cache, const void* v_cache,
+                                const int32_t* query_seq, const int32_t* query_key_len, const int32_t* block_tables,
+                                int64_t tokens, int q_heads, int kv_heads, int head_dim, int block_size,
+                                int max_blocks, float scale, int64_t q_stride, int64_t max_query_len, int dtype,
+                                void* stream) {
+  const int64_t need = nvf_paged_attention_workspace_size(tokens, q_heads, kv_heads, head_dim, block_size, max_blocks,
+                                                          max_query_len);
+  if (need > kAttnScratchBytes)
+    return fail(NVF_ERR_INVALID,
+                "nvf_paged_attention_noalloc: this call's split needs %lld bytes of scratch, more than the %lld-byte "
+                "static scratch (use nvf_paged_attention_ws with a workspace)",
+                (long long)need, (long long)kAttnScratchBytes);
+  void* ws = nullptr;
+  if (need > 0 && !(ws = scratch_ptr())) return NVF_ERR_LAUNCH;
+  return paged_attention_entry(q, out, k_cache, v_cache, query_seq, query_key_len, block_tables, tokens, q_heads,
+                               kv_heads, head_dim, block_size, max_blocks, scale, q_stride, max_query_len, ws, need,
+                               dtype, stream, false);
+}
+
 // Drop-ins: include/nanovllm/hip_ops.hpp:22-28 / src/hip_ops.hip:724-744 (fp32 cache, null stream).
 void hip_store_kv(const float* key, const float* value, float* k_cache, float* v_cache, const int32_t* slot_mapping,
                   int tokens, int kv_heads, int head_dim) {

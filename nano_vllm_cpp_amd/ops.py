@@ -49,6 +49,9 @@ SIGNATURES: dict[str, tuple] = {
                                       _i64, _i64, _vp, _i64, _i32, _vp]),
     "nvf_paged_attention_seqs_ws": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i64, _i32, _i32, _i32,
                                            _i32, _i32, _f32, _i64, _i64, _vp, _i64, _i32, _vp]),
+    "nvf_paged_attention_noalloc": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i32, _i32, _i32, _i32, _i32,
+                                           _f32, _i64, _i64, _i32, _vp]),
+    "nvf_paged_attention_noalloc_max_bytes": (_i64, []),
     "nvf_paged_attention_workspace_size": (_i64, [_i64, _i32, _i32, _i32, _i32, _i32, _i64]),
     "nvf_q8_quantize_rows": (_i32, [_vp, _vp, _vp, _i64, _i64, _i32, _vp]),
     "nvf_matmul_q8_0": (_i32, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _i32, _vp]),
