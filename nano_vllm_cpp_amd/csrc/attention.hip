@@ -1510,44 +1510,24 @@ void hip_store_kv(const float* key, const float* value, float* k_cache, float* v
                "hip_store_kv");
 }
 
-// Grow-only device workspace for the drop-in's split decode (the policy of the
-// reference's own hip_matmul_q8 scratch, src/hip_ops.hip:642-648): reallocated
-// only when a call needs more, or on another device.  Like the reference's ops it
-// assumes one calling thread; calls on several streams at once would share it.
-struct AttnScratch {
-  void* p = nullptr;
-  size_t cap = 0;
-  int device = -1;
-};
-AttnScratch g_attn_scratch;
-
+// The drop-in splits small batches over long contexts through the same static
+// scratch as nvf_paged_attention_noalloc, so it allocates nothing, like the
+// reference's hip_paged_attention (src/hip_ops.hip:735-744).  A split that would
+// need more than the scratch runs unsplit instead (same results within the
+// attention tolerance, slower).  Like the reference's ops it assumes one calling
+// thread: calls overlapping on one GPU would share the scratch.
 void hip_paged_attention(const float* q, float* out, const float* k_cache, const float* v_cache,
                          const int32_t* query_seq, const int32_t* query_key_len, const int32_t* block_tables,
                          int tokens, int q_heads, int kv_heads, int head_dim, int block_size, int max_blocks,
                          float scale) {
   if (tokens <= 0 || q_heads <= 0 || kv_heads <= 0) return;
-  const int64_t need =
-      nvf_paged_attention_workspace_size(tokens, q_heads, kv_heads, head_dim, block_size, max_blocks, 0);
-  if (need > 0) {
-    int dev = 0;
-    dropin_check(hipGetDevice(&dev) == hipSuccess ? NVF_OK : fail(NVF_ERR_LAUNCH, "hipGetDevice failed"),
-                 "hip_paged_attention");
-    if ((size_t)need > g_attn_scratch.cap || dev != g_attn_scratch.device) {
-      if (g_attn_scratch.p) (void)hipFree(g_attn_scratch.p);
-      g_attn_scratch.p = nullptr;
-      g_attn_scratch.cap = 0;
-      if (hipMalloc(&g_attn_scratch.p, (size_t)need) != hipSuccess)
-        dropin_check(fail(NVF_ERR_LAUNCH, "hip_paged_attention: workspace allocation of %lld bytes failed",
-                          (long long)need),
-                     "hip_paged_attention");
-      g_attn_scratch.cap = (size_t)need;
-      g_attn_scratch.device = dev;
-    }
-  }
+  int64_t need = nvf_paged_attention_workspace_size(tokens, q_heads, kv_heads, head_dim, block_size, max_blocks, 0);
+  void* ws = nullptr;
+  if (need > kAttnScratchBytes) need = 0;
+  if (need > 0 && !(ws = scratch_ptr())) dropin_check(NVF_ERR_LAUNCH, "hip_paged_attention");
   dropin_check(nvf_paged_attention_ws(q, out, k_cache, v_cache, query_seq, query_key_len, block_tables, tokens,
                                       q_heads, kv_heads, head_dim, block_size, max_blocks, scale,
-                                      (int64_t)q_heads * head_dim, 0, need > 0 ? g_attn_scratch.p : nullptr, need,
-                                      NVF_F32, nullptr),
+                                      (int64_t)q_heads * head_dim, 0, ws, need, NVF_F32, nullptr),
                "hip_paged_attention");
 }
 

@@ -296,9 +296,10 @@ def test_paged_attention_split_decode(gpu, dt, ci):
     assert_attn(got, exact, vmax, dt, "unsplit")
 
 
-def test_dropin_split_decode_grows_its_workspace(gpu):
-    """The fp32 drop-in splits small decode batches with its own grow-only
-    workspace: a short-context call, then a longer one needing more."""
+def test_dropin_split_decode_uses_the_static_scratch(gpu):
+    """The fp32 drop-in splits small decode batches through the library's static
+    scratch (it allocates nothing): a short-context call, then a longer one needing
+    more of it."""
     for ctx, seed in (([700, 33], 1), ([6000, 4096, 17], 2)):
         r = H.rng(500 + seed)
         b = H.make_paged(r, ctx, [1] * len(ctx), 28, 4, 128, 256, H.F32)
