@@ -56,6 +56,8 @@ def parse() -> argparse.Namespace:
     p.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU-baseline budget (0 = skip)")
     p.add_argument("--emb", default="", choices=["", "q8_0", "q8_0_blocks", "q4_k", "q5_k", "q6_k", "f16"],
                    help="embedding table format (default: the config's)")
+    p.add_argument("--write-traffic", default="", metavar="DIR",
+                   help="no benchmark: build profiles/traffic.json from rocprofv3 FETCH_SIZE / WRITE_SIZE runs under DIR")
     p.add_argument("--only", default="",
                    help="comma list of ops (default emb,rms,rope,silu,copy,gemm,gemv,split,attn,attn_decode,attn_f32,"
                         "attn_decode_f32,attn_decode_small,layer,layer_decode,layer_b1,layer_b1_graph); "
@@ -89,6 +91,9 @@ def op_bytes(cfg, e: int, emb_fmt: str) -> dict[str, int]:
 
 def main() -> int:
     args = parse()
+    if args.write_traffic:
+        print(json.dumps(write_traffic(args.write_traffic, args.config)[f"c{args.config}"], indent=1))
+        return 0
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print(json.dumps({"error": "this build measures one GPU only; run with --gpus 1",
                           "n_gpus_requested": args.gpus}))
@@ -110,7 +115,8 @@ def main() -> int:
     g = torch.Generator(device=dev).manual_seed(cfg.seed)
     emb_fmt = args.emb or cfg.emb
     nbytes = op_bytes(cfg, e, emb_fmt)
-    only = set(filter(None, args.only.split(","))) or {"emb", "rms", "rope", "silu", "copy", "gemm", "gemv", "split",
+    only = set(filter(None, args.only.split(","))) or {"emb", "rms", "rope", "silu", "copy", "copy12", "copy12_emb",
+                                                       "gemm", "gemv", "split",
                                                        "attn", "attn_decode", "attn_f32", "attn_decode_f32", "attn_decode_small", "layer", "layer_decode", "layer_b1", "layer_b1_graph"}
 
     def nsets(b: int) -> int:
@@ -297,9 +303,14 @@ def main() -> int:
     attn_in32 = f32ize(attn_in) if "attn_f32" in only else None
     attn_dec32 = f32ize(attn_dec) if "attn_decode_f32" in only else None
     copy_pair = None
-    if "copy" in only:  # 1 GiB plain copy: the attainable-bandwidth and traffic-counter reference
+    if {"copy", "copy12"} & only:  # 1 GiB plain copy: the attainable-bandwidth and traffic-counter reference
         copy_pair = (torch.ones(1 << 28, dtype=torch.int32, device=dev),
                      torch.empty(1 << 28, dtype=torch.int32, device=dev))
+    # the gather's 1:2 read:write mix (nvf_stream_expand): 0.5 GiB in / 1 GiB out, and at the
+    # gather's own size (T*H bytes in, T*H*2 out) rotating over >= 1 GiB of sets like the gather
+    exp_sets = [(torch.ones(T * Hd // 4, dtype=torch.int32, device=dev), torch.empty(T * Hd // 2, dtype=torch.int32,
+                                                                                    device=dev))
+                for _ in range(nsets(3 * T * Hd))] if "copy12_emb" in only else []
     torch.cuda.synchronize()
 
     def run_emb(i):
@@ -440,8 +451,16 @@ def main() -> int:
     def run_copy(i):
         ops.stream_copy(copy_pair[1], copy_pair[0])
 
+    def run_copy12(i):
+        ops.stream_expand(copy_pair[1], copy_pair[0][:1 << 27])
+
+    def run_copy12_emb(i):
+        src_, dst_ = exp_sets[i % len(exp_sets)]
+        ops.stream_expand(dst_, src_)
+
     table = [("emb", run_emb), ("rms", run_rms), ("rope", run_rope), ("silu", run_silu), ("emb_rms", run_emb_rms),
-             ("rms_q8", run_rms_q8), ("silu_q8", run_silu_q8), ("copy", run_copy), ("gemm", run_gemm),
+             ("rms_q8", run_rms_q8), ("silu_q8", run_silu_q8), ("copy", run_copy),
+             ("copy12", run_copy12), ("copy12_emb", run_copy12_emb), ("gemm", run_gemm),
              ("gemv", run_gemv), ("split", run_split), ("attn", run_attn), ("attn_decode", run_attn_decode),
              ("attn_f32", run_attn_f32), ("attn_decode_f32", run_attn_decode_f32), ("attn_decode_small", run_attn_decode_small),
              ("layer", run_layer), ("layer_decode", run_layer_decode), ("layer_b1", run_layer_b1),
@@ -538,9 +557,10 @@ def main() -> int:
                           "tokens_per_s": round(T / (t_us * 1e-6), 1),
                           "gemm_TOP_s": round(layer_ops / (t_us * 1e-6) / 1e12, 1),
                           "effective_TOP_s_incl_attention": round((layer_ops + layer_attn_flops) / (t_us * 1e-6) / 1e12, 1)})
-        elif n == "copy":
-            entry.update({"bytes": 2 * copy_pair[0].numel() * 4,
-                          "GB_s": round(2 * copy_pair[0].numel() * 4 / (t_us * 1e-6) / 1e9, 1)})
+        elif n in ("copy", "copy12", "copy12_emb"):
+            nb = {"copy": 2 << 30, "copy12": 3 << 29, "copy12_emb": 3 * T * Hd}[n]
+            entry.update({"bytes": nb, "GB_s": round(nb / (t_us * 1e-6) / 1e9, 1),
+                          "frac_of_peak": round(nb / (t_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)})
         res_ops[n] = entry
 
     # The step: the whole chain, `steps` times, bracketed by synchronize + events.
@@ -593,7 +613,13 @@ def main() -> int:
         "fused_ops": {k: v for k, v in res_ops.items() if k in ("emb_rms", "rms_q8", "silu_q8")} or None,
         "attainable": ({"kernel": "nvf_stream_copy (1 GiB, 16 B non-temporal loads/stores)",
                         "GB_s": res_ops["copy"]["GB_s"],
-                        "frac_of_peak": round(res_ops["copy"]["GB_s"] / HBM_PEAK_GBS, 4)} if "copy" in res_ops else None),
+                        "frac_of_peak": round(res_ops["copy"]["GB_s"] / HBM_PEAK_GBS, 4),
+                        **({"read1_write2_1GiB": {k_: res_ops["copy12"][k_] for k_ in ("us", "GB_s", "frac_of_peak")}}
+                           if "copy12" in res_ops else {}),
+                        **({"read1_write2_at_emb_size": {k_: res_ops["copy12_emb"][k_]
+                                                         for k_ in ("us", "GB_s", "frac_of_peak")}}
+                           if "copy12_emb" in res_ops else {})}
+                       if "copy" in res_ops else None),
         "roofline": roofline,
         "q8_gemm": res_ops.get("gemm"),
         "q8_gemv": res_ops.get("gemv"),
@@ -651,16 +677,104 @@ def timed_launches(torch, stream, f, first: int, n: int, cyc_per_us: float, grou
             return np.array([evs[g_].elapsed_time(evs[g_ + 1]) * 1e3 / group for g_ in range(ng)])
     raise RuntimeError("timed_launches: the host could not stay ahead of the GPU")
 
+# the chain's kernels as rocprofv3 names them (prefix of the mangled name) -> bench op
+CHAIN_KERNELS = {"emb": "_ZN3nvf17embed_rows_kernel", "rms": "_ZN3nvf19rms_norm_vec_kernel",
+                 "rope": "_ZN3nvf19qk_norm_rope_kernel", "silu": "_ZN3nvf19silu_mul_vec_kernel",
+                 "copy": "nvf::stream_copy_kernel"}
+LIB_PATH = ROOT / "nano_vllm_cpp_amd" / "lib" / "libnvf_ops.so"
+
+
+def _kernel_in_library(name: str) -> bool:
+    """True if the built library holds a kernel of this (mangled) name: its code object
+    names each kernel's descriptor, so the bytes of the name appear in the .so."""
+    try:
+        return name.encode() in LIB_PATH.read_bytes()
+    except OSError:
+        return False
+
+
 def traffic_from_profiles(op: str, config: int):
-    """HBM bytes per launch from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary, if present."""
+    """HBM bytes per launch from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary,
+    or None when there is none for this op, or when the kernel it was counted on is not
+    a kernel of the library built now (a summary of an older binary is not used)."""
     f = ROOT / "profiles" / "traffic.json"
     if not f.exists():
         return None
     try:
-        d = json.loads(f.read_text())
-        return d.get(f"c{config}", {}).get(op, {}).get("hbm_bytes_per_launch")
+        e = json.loads(f.read_text()).get(f"c{config}", {}).get(op, {})
     except (ValueError, AttributeError):
         return None
+    name = e.get("kernel", "")
+    if not name or not _kernel_in_library(name):
+        return None
+    return e.get("hbm_bytes_per_launch")
+
+
+def write_traffic(prof_dir: str, config: int) -> dict:
+    """Builds profiles/traffic.json from two rocprofv3 passes over the chain and the copy,
+    <prof_dir>/FETCH_SIZE/*counter_collection.csv and <prof_dir>/WRITE_SIZE/..., made by
+      rocprofv3 --pmc FETCH_SIZE -f csv -d <prof_dir>/FETCH_SIZE -o FETCH_SIZE -- \
+          python3 bench.py --config <c> --only emb,rms,rope,silu,copy --steps 10 --warmup 2 --cpu-seconds 0
+    (and the same with WRITE_SIZE).  Per op: the mean counter over the dispatches of the
+    op's kernel at its largest grid (the bench's launch), scaled by what the counter reads
+    for the 1 GiB copy against the bytes it moves.  Records the source commit."""
+    import csv
+    import subprocess
+
+    cfg_ops = {}
+    for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+        files = sorted(Path(prof_dir, counter).glob("*counter_collection.csv"))
+        if not files:
+            raise SystemExit(f"no {counter} counter_collection.csv under {prof_dir}/{counter}")
+        per = {}
+        for row in csv.DictReader(open(files[0])):
+            if row["Counter_Name"] != counter:
+                continue
+            for op, prefix in CHAIN_KERNELS.items():
+                if row["Kernel_Name"].startswith(prefix):
+                    per.setdefault(op, {}).setdefault(int(row["Grid_Size"]), (row["Kernel_Name"], []))[1].append(
+                        float(row["Counter_Value"]))
+        for op, grids in per.items():
+            g = max(grids)
+            name, vals = grids[g]
+            cfg_ops.setdefault(op, {"kernel": name, "grid": g})[counter] = sum(vals) / len(vals)
+    copy_bytes = 1 << 30
+    cal = cfg_ops.pop("copy")
+    ff = copy_bytes / (cal["FETCH_SIZE"] * 1024)
+    wf = copy_bytes / (cal["WRITE_SIZE"] * 1024)
+    from tests import harness as H
+    cfg = H.CONFIGS[config]
+    alg = op_bytes(cfg, 2 if cfg.dtype != H.F32 else 4, cfg.emb)
+    try:
+        head = subprocess.run(["git", "-C", str(ROOT), "rev-parse", "HEAD"], capture_output=True, text=True,
+                              check=True).stdout.strip()
+        dirty = bool(subprocess.run(["git", "-C", str(ROOT), "status", "--porcelain", "--", "nano_vllm_cpp_amd/csrc"],
+                                    capture_output=True, text=True).stdout.strip())
+    except (OSError, subprocess.CalledProcessError):
+        head, dirty = "unknown", True
+    out = {"_source": {"commit": head, "kernel_sources_modified": dirty,
+                       "command": "rocprofv3 --pmc <FETCH_SIZE|WRITE_SIZE> -f csv -d <dir>/<counter> -o <counter> -- "
+                                  f"python3 bench.py --config {config} --only emb,rms,rope,silu,copy --steps 10 "
+                                  "--warmup 2 --cpu-seconds 0"},
+           "_calibration": {"reference": "nvf_stream_copy of 1 GiB (16 B non-temporal loads/stores)",
+                            "copy_fetch_kib": round(cal["FETCH_SIZE"], 1), "copy_write_kib": round(cal["WRITE_SIZE"], 1),
+                            "fetch_factor": round(ff, 4), "write_factor": round(wf, 4)},
+           "_note": "hbm_bytes_per_launch = FETCH_SIZE[KiB]*1024*fetch_factor + WRITE_SIZE[KiB]*1024*write_factor"}
+    entry = {}
+    for op, d in sorted(cfg_ops.items()):
+        hbm = d["FETCH_SIZE"] * 1024 * ff + d["WRITE_SIZE"] * 1024 * wf
+        entry[op] = {"kernel": d["kernel"], "grid": d["grid"], "fetch_kib_raw": round(d["FETCH_SIZE"], 1),
+                     "write_kib_raw": round(d["WRITE_SIZE"], 1), "hbm_bytes_per_launch": int(hbm),
+                     "algorithmic_bytes": alg[op], "ratio_to_algorithmic": round(hbm / alg[op], 4)}
+    f = ROOT / "profiles" / "traffic.json"
+    try:
+        whole = json.loads(f.read_text())
+    except (OSError, ValueError):
+        whole = {}
+    whole.update({k: v for k, v in out.items()})
+    whole[f"c{config}"] = entry
+    f.write_text(json.dumps(whole, indent=1) + "\n")
+    return whole
 
 
 def cpu_chain_sample(cfg, H, seed: int):

@@ -336,6 +336,11 @@ int nvf_rope_inv_freq(double theta, int head_dim, float* out);
  * the op kernels' HBM figures are calibrated against. */
 int nvf_stream_copy(void* dst, const void* src, int64_t bytes, void* stream);
 
+/* Measurement reference with the Q8_0 gather's read:write mix (no reference
+ * counterpart): dst[16 i .. 16 i + 15] = src[8 i .. 8 i + 7] twice, for
+ * src_bytes / 8 items (dst holds 2 * src_bytes; 16-byte aligned dst, 8-byte src). */
+int nvf_stream_expand(void* dst, const void* src, int64_t src_bytes, void* stream);
+
 /* Text of the calling thread's last failure ("" if none). */
 const char* nvf_last_error(void);
 

@@ -75,6 +75,7 @@ SIGNATURES: dict[str, tuple] = {
     "nvf_embedding_rms_norm": (_i32, [_vp, _i32, _vp, _vp, _i64, _i64, _i64, _vp, _vp, _vp, _f32, _i32, _vp]),
     "nvf_rope_inv_freq": (_i32, [_f64, _i32, _vp]),
     "nvf_stream_copy": (_i32, [_vp, _vp, _i64, _vp]),
+    "nvf_stream_expand": (_i32, [_vp, _vp, _i64, _vp]),
     "nvf_q8_0_split_blocks": (_i32, [_vp, _i64, _vp, _vp, _vp]),
     "nvf_last_error": (C.c_char_p, []),
     "nvf_abi_version": (_i32, []),
@@ -465,3 +466,12 @@ def stream_copy(dst: torch.Tensor, src: torch.Tensor) -> None:
     if dst.numel() * dst.element_size() != n:
         raise ValueError("size mismatch")
     _check(lib().nvf_stream_copy(_dev(dst, "dst"), _dev(src, "src"), n, _stream()), "stream_copy")
+
+
+def stream_expand(dst: torch.Tensor, src: torch.Tensor) -> None:
+    """dst (2x src's bytes) <- each 8 bytes of src written as 16 (the gather's 1:2 mix)."""
+    if dst.numel() * dst.element_size() != 2 * src.numel() * src.element_size():
+        raise ValueError("dst must hold twice src's bytes")
+    _check(lib().nvf_stream_expand(_dev(dst, "dst"), _dev(src, "src"), src.numel() * src.element_size(), _stream()),
+           "stream_expand")
+

@@ -314,3 +314,12 @@ def test_stream_copy(gpu):
     case("stream_copy 4 MiB")
     ops.stream_copy(dst, src)
     assert torch.equal(dst, src)
+
+
+def test_stream_expand(gpu):
+    src = torch.arange(1 << 18, dtype=torch.int32, device=gpu)
+    dst = torch.zeros(1 << 19, dtype=torch.int32, device=gpu)
+    case("stream_expand 1 MiB -> 2 MiB")
+    ops.stream_expand(dst, src)
+    # each 8 bytes (two int32) written twice into 16 bytes
+    assert torch.equal(dst.view(-1, 4), src.view(-1, 2).repeat(1, 2))
