@@ -402,12 +402,18 @@ def main() -> int:
         att = ops.paged_attention(qkv[:, :qs].view(n_, cfg.q_heads, cfg.head_dim), L_["kc"], L_["vc"], L_["qseq"],
                                   L_["qlen"], L_["tab"], bs_kv, cfg.head_dim ** -0.5, out=L_["attn_out"],
                                   max_query_len=L_["mql"], cu_seqlens=L_.get("cu"))
-        sc2, xq2 = ops.q8_quantize_rows(att.view(n_, qs))
-        o = ops.matmul_q8_0(xq2, sc2, *L_["o"], Hd, tdt, out=L_["o_out"])
+        if n_ <= 16:  # decode GEMV: the o and down projections quantize their own input rows
+            o = ops.matmul_q8_0_act(att.view(n_, qs), *L_["o"], Hd, out=L_["o_out"])
+        else:
+            sc2, xq2 = ops.q8_quantize_rows(att.view(n_, qs))
+            o = ops.matmul_q8_0(xq2, sc2, *L_["o"], Hd, tdt, out=L_["o_out"])
         _, sc3, xq3 = ops.rms_norm_q8(o, L_["w_post"], cfg.eps, residual=L_["r"], want_out=False)
         gu = ops.matmul_q8_0(xq3, sc3, *L_["gu"], 2 * I, tdt, out=L_["gu_out"])
-        _, sc4, xq4 = ops.silu_and_mul_q8(gu)
-        ops.matmul_q8_0(xq4, sc4, *L_["down"], Hd, tdt, out=L_["down_out"])
+        if n_ <= 16:  # SwiGLU + its quantizer inside the down GEMV
+            ops.matmul_q8_0_act(gu, *L_["down"], Hd, swiglu=True, out=L_["down_out"])
+        else:
+            _, sc4, xq4 = ops.silu_and_mul_q8(gu)
+            ops.matmul_q8_0(xq4, sc4, *L_["down"], Hd, tdt, out=L_["down_out"])
 
     def run_layer(i):
         run_layer_on(layer)

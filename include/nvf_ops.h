@@ -257,6 +257,19 @@ int nvf_matmul_q8_0_ws(const int8_t* xq, const float* row_scale, const uint8_t* 
                        void* stream);
 
 /* Bytes of workspace nvf_matmul_q8_0_ws uses for this shape (0: it would not split). */
+/* Decode GEMV (m <= 16 rows) on fp activations, no separate quantize pass: out [m, n]
+ * (dtype) = the Q8_0 product of the rows quantized as nvf_q8_quantize_rows would
+ * (act 0: x [m, k]) or as nvf_silu_and_mul_q8 would (act 1: x = [gate | up] rows
+ * [m, 2k], the SwiGLU taken first).  Each workgroup quantizes the rows into its own
+ * LDS while the weights stream in, so the int8 rows and scales, and the result, are
+ * bit-identical to the separate quantize launch followed by nvf_matmul_q8_0.  This
+ * fuses what the reference does in one call, hip_matmul_q8's quantizer and GEMV
+ * (src/hip_ops.hip:205-217, :317-364), and for act 1 also hip_silu_and_mul before it
+ * (src/model.cpp:830).  x: 16-byte aligned rows, x_stride elements apart (>= k, or
+ * 2k for act 1).  m > 16 or rows too long for the workgroup's LDS: NVF_ERR_INVALID. */
+int nvf_matmul_q8_0_act(const void* x, int64_t x_stride, int act, const uint8_t* w8, const uint16_t* ws, int64_t m,
+                        int64_t n, int64_t k, void* out, int dtype, void* stream);
+
 int64_t nvf_matmul_q8_0_workspace_size(int64_t m, int64_t n, int64_t k);
 
 /* KV store (replaces hip_store_kv, hip_ops.hpp:22-23) with the cache in `dtype`;

@@ -165,6 +165,26 @@ __device__ __forceinline__ float wave_sum(float v) {
          __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32));
 }
 
+// SiLU(g) * u, the reference's g / (1 + expf(-g)) * u (src/hip_ops.hip:419-429).
+// fp32 keeps the exact expression (IEEE divide, precise expf); fp16/bf16 use
+// v_exp_f32 + v_rcp_f32 (a few fp32 ulp, far below one 16-bit ulp).  Every
+// kernel that computes SwiGLU (the SwiGLU kernels, the decode GEMV's fused
+// prologue) calls this one function, so they all produce the same bits.
+template <typename T>
+__device__ __forceinline__ float silu_mul(float g, float u) {
+  if constexpr (sizeof(T) == 4) {
+    return g / (1.0f + expf(-g)) * u;
+  } else {
+    const float e = __builtin_amdgcn_exp2f(g * -1.4426950408889634f);
+    float v = g * __builtin_amdgcn_rcpf(1.0f + e) * u;
+    // The fp32 product is the value: an empty asm keeps the compiler from folding
+    // the last multiply into the 16-bit conversion (v_fma_mix rounds once where
+    // multiply-then-convert rounds twice), so every kernel stores the same bits.
+    asm("" : "+v"(v));
+    return v;
+  }
+}
+
 // Q8 activation quantizer of the reference's INT8 GEMM path: per-row scale
 // 127 / max|x| (0 for an all-~zero row) and q = (int8)clamp(x * scale, +-127)
 // with C truncation (src/hip_ops.hip:205-217, :244-245).

@@ -397,13 +397,21 @@ constexpr int64_t kLdsPerCu = 160 * 1024;
 template <int W, int S>
 constexpr int gemv_cols() { return W / S * 16; }  // columns per workgroup of W waves
 
-template <typename TO, int W, int S, bool XL>
+// XF (fused activation quantizer, needs XL): the m rows arrive as 16-bit or fp32
+// activations in TO (xf, row stride xf_ld elements) instead of int8 rows + scales;
+// each workgroup quantizes them into its staged LDS rows itself, exactly as
+// nvf_q8_quantize_rows (XF = 1) or nvf_silu_and_mul_q8 over [gate | up] rows
+// (XF = 2) would: the row maximum is order-independent and each value is quantized
+// alone, so the int8 rows and scales are bit-identical to the separate pass's.
+template <typename TO, int W, int S, bool XL, int XF = 0>
 __global__ __launch_bounds__(W * 64) void q8_gemv_kernel(const int8_t* __restrict__ xq,
                                                          const float* __restrict__ rscale,
                                                          const int8_t* __restrict__ w8,
                                                          const uint16_t* __restrict__ ws,
                                                          TO* __restrict__ out, int64_t m, int64_t n, int64_t k,
-                                                         int sc_bytes) {
+                                                         int sc_bytes, const TO* __restrict__ xf = nullptr,
+                                                         int64_t xf_ld = 0) {
+  static_assert(XF == 0 || XL, "the fused quantizer writes the staged LDS rows");
   constexpr int kCols = gemv_cols<W, S>();
   constexpr int kGvDmaLds = W * 2 * kGvWaveBuf;
   // [DMA buffers][scales][activation rows (XL)]; after the loop each wave's partial
@@ -418,6 +426,10 @@ __global__ __launch_bounds__(W * 64) void q8_gemv_kernel(const int8_t* __restric
   const int64_t wg_cols = n - wg_c0 < kCols ? n - wg_c0 : kCols;
   uint16_t* sc_lds = reinterpret_cast<uint16_t*>(dyn + kGvDmaLds);
   uint8_t* x_lds = dyn + kGvDmaLds + sc_bytes;
+  // XF: per-wave row maxima and the rows' scales, after the staged rows (dynamic LDS
+  // only, so the kernel may take the whole 160 KiB)
+  float* xf_max = reinterpret_cast<float*>(x_lds + ((m * (k + 16) + 15) & ~int64_t(15)));
+  float* xf_scale = xf_max + W * kGemvMaxM;
   const int64_t xrow = k + 16;  // LDS bytes per staged activation row
 
   const int64_t c0 = wg_c0 + (int64_t)grp * 16;  // this wave's first column
@@ -478,7 +490,7 @@ __global__ __launch_bounds__(W * 64) void q8_gemv_kernel(const int8_t* __restric
         __builtin_amdgcn_raw_ptr_buffer_load_lds(
             rs, (__attribute__((address_space(3))) void*)(dst + i0 + 64 * wave), 4, (uint32_t)(4 * i), 0, 0, 0);
     }
-    if constexpr (XL) {  // m rows of k bytes (k % 32 == 0), 1 KB transfers spread over the waves
+    if constexpr (XL && XF == 0) {  // m rows of k bytes (k % 32 == 0), 1 KB transfers spread over the waves
       const int per_row = (int)((k + 1023) / 1024);
       for (int t = wave; t < m * per_row; t += W) {
         const int r = t / per_row, c = t % per_row;
@@ -499,6 +511,93 @@ __global__ __launch_bounds__(W * 64) void q8_gemv_kernel(const int8_t* __restric
       __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
     if ((cnt & 1) && threadIdx.x == 0)
       sc_lds[cnt - 1] = (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(rs, (uint32_t)(2 * (cnt - 1)), 0, 0);
+    if constexpr (XF != 0) {
+      // Pass 1: each row's max |value| (wave maxima to LDS); pass 2, after a barrier:
+      // the scale, then every value quantized into the staged row (the values are
+      // computed twice rather than held: up to 16 rows of k).  Weight stage 1 stays
+      // in flight meanwhile.
+      constexpr int N = Pack<TO>::N;
+      const int64_t nv = k / N;
+      auto act = [&](int64_t r, int64_t c, float* v) {
+        const TO* row = xf + r * xf_ld;
+        Pack<TO>::unpack(ld16(row + c * N), v);
+        if constexpr (XF == 2) {
+          float u[N];
+          Pack<TO>::unpack(ld16(row + k + c * N), u);
+#pragma unroll
+          for (int e = 0; e < N; ++e) v[e] = to_f32(from_f32<TO>(silu_mul<TO>(v[e], u[e])));  // the stored value
+        }
+      };
+      constexpr int kHold = 8;  // a single row of up to kHold vectors per thread stays in registers
+      const bool hold = m == 1 && nv <= (int64_t)kHold * W * 64;
+      float hv[kHold][N];
+      if (hold) {
+        float mx = 0.0f;
+#pragma unroll
+        for (int i = 0; i < kHold; ++i) {
+          const int64_t c = threadIdx.x + (int64_t)i * W * 64;
+          if (c < nv) {
+            act(0, c, hv[i]);
+#pragma unroll
+            for (int e = 0; e < N; ++e) mx = fmaxf(mx, fabsf(hv[i][e]));
+          }
+        }
+        mx = wave_max(mx);
+        if (lane == 0) xf_max[wave * kGemvMaxM] = mx;
+      }
+      for (int64_t r = 0; r < (hold ? 0 : m); ++r) {
+        float mx = 0.0f;
+        for (int64_t c = threadIdx.x; c < nv; c += W * 64) {
+          float v[N];
+          act(r, c, v);
+#pragma unroll
+          for (int e = 0; e < N; ++e) mx = fmaxf(mx, fabsf(v[e]));
+        }
+        mx = wave_max(mx);
+        if (lane == 0) xf_max[wave * kGemvMaxM + r] = mx;
+      }
+      // publish the maxima: a bare barrier (no workgroup fence, whose vmcnt(0) wait
+      // the loads above have already forced anyway)
+      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_s_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      auto quant_store = [&](int64_t r, int64_t c, const float* v, float sc) {
+        uint32_t q4[N / 4];
+#pragma unroll
+        for (int d = 0; d < N / 4; ++d) {
+          q4[d] = 0;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) q4[d] |= (uint32_t)(q8_quantize(v[4 * d + e], sc) & 0xff) << (8 * e);
+        }
+#pragma unroll
+        for (int d = 0; d < N / 4; ++d) reinterpret_cast<uint32_t*>(x_lds + r * xrow + c * N)[d] = q4[d];
+      };
+      if (hold) {
+        float mx = xf_max[0];
+#pragma unroll
+        for (int w = 1; w < W; ++w) mx = fmaxf(mx, xf_max[w * kGemvMaxM]);
+        const float sc = q8_row_scale(mx);
+        if (threadIdx.x == 0) xf_scale[0] = sc;
+#pragma unroll
+        for (int i = 0; i < kHold; ++i) {
+          const int64_t c = threadIdx.x + (int64_t)i * W * 64;
+          if (c < nv) quant_store(0, c, hv[i], sc);
+        }
+      }
+      for (int64_t r = 0; r < (hold ? 0 : m); ++r) {
+        float mx = xf_max[r];
+#pragma unroll
+        for (int w = 1; w < W; ++w) mx = fmaxf(mx, xf_max[w * kGemvMaxM + r]);
+        const float sc = q8_row_scale(mx);
+        if (threadIdx.x == 0) xf_scale[r] = sc;
+        for (int64_t c = threadIdx.x; c < nv; c += W * 64) {
+          float v[N];
+          act(r, c, v);
+          quant_store(r, c, v, sc);
+        }
+      }
+    }
     // Every wave's DMA writes are complete (its vmcnt wait above) and the one LDS
     // store is waited by lgkmcnt(0), so a bare barrier publishes the scales; a
     // workgroup-scope fence here would add a vmcnt(0) and drain weight stage 1.
@@ -592,7 +691,7 @@ __global__ __launch_bounds__(W * 64) void q8_gemv_kernel(const int8_t* __restric
       float sum = 0.0f;
 #pragma unroll
       for (int sp = 0; sp < S; ++sp) sum += part(g * S + sp, r, cj);
-      const float sc = rscale[r];
+      const float sc = XF != 0 ? xf_scale[r] : rscale[r];
       const float inv = sc > 0.0f ? 1.0f / sc : 0.0f;  // the reference's adq (:358)
       gemm_store_out(out + r * n + col, sum * inv);
     }
@@ -635,6 +734,28 @@ bool try_gemv(const int8_t* xq, const float* rscale, const int8_t* w8, const uin
   else
     q8_gemv_kernel<TO, W, S, false><<<dim3((unsigned)wgs), dim3(W * 64), (size_t)lds_r, stream>>>(
         xq, rscale, w8, ws, out, m, n, k, (int)sc_bytes);
+  return true;
+}
+
+// The GEMV with the fused activation quantizer (XF 1 or 2): always the staged-row
+// form; false when the rows or the scales would not fit the workgroup's LDS.
+template <typename TO, int W, int S, int XF>
+bool try_gemv_act(const TO* xf, int64_t xf_ld, const int8_t* w8, const uint16_t* ws, TO* out, int64_t m, int64_t n,
+                  int64_t k, hipStream_t stream) {
+  constexpr int kDma = W * 2 * kGvWaveBuf;
+  constexpr int kCols = gemv_cols<W, S>();
+  const int64_t sc_bytes = (kCols * (k / 32) * 2 + 15) & ~15;
+  const int64_t x_bytes = ((m * (k + 16) + 15) & ~int64_t(15)) + (W + 1) * kGemvMaxM * 4;  // rows, maxima, scales
+  if (sc_bytes > kGemvScaleLds || x_bytes > kGemvXLdsMax || kDma + sc_bytes + x_bytes > kLdsPerCu) return false;
+  static std::once_flag attr_once;
+  std::call_once(attr_once, [] {
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&q8_gemv_kernel<TO, W, S, true, XF>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize,
+                              (int)std::min<int64_t>(kLdsPerCu, kDma + kGemvScaleLds + kGemvXLdsMax));
+  });
+  const int64_t wgs = (n + kCols - 1) / kCols;
+  q8_gemv_kernel<TO, W, S, true, XF><<<dim3((unsigned)wgs), dim3(W * 64), (size_t)(kDma + sc_bytes + x_bytes),
+                                        stream>>>(nullptr, nullptr, w8, ws, out, m, n, k, (int)sc_bytes, xf, xf_ld);
   return true;
 }
 
@@ -761,6 +882,24 @@ int launch_gemm(const int8_t* xq, const float* rscale, const int8_t* w8, const u
   return launch_status("q8_gemm_kernel");
 }
 
+// The decode GEMV (m <= 16) on fp activations, quantized in its prologue (XF 1:
+// rows [m, k]; XF 2: SwiGLU over [gate | up] rows [m, 2k]).  The same (W, S)
+// choice as launch_gemm; NVF_ERR_INVALID when no GEMV form fits.
+template <typename TO, int XF>
+int launch_gemv_act(const TO* xf, int64_t xf_ld, const int8_t* w8, const uint16_t* ws, TO* out, int64_t m, int64_t n,
+                    int64_t k, hipStream_t stream) {
+  const int64_t groups = (n + 15) / 16;
+  bool ok = false;
+  if (groups >= 2048) ok = try_gemv_act<TO, 4, 1, XF>(xf, xf_ld, w8, ws, out, m, n, k, stream);
+  if (!ok && groups >= 1024) ok = try_gemv_act<TO, 4, 2, XF>(xf, xf_ld, w8, ws, out, m, n, k, stream);
+  if (!ok && groups >= 512) ok = try_gemv_act<TO, 4, 4, XF>(xf, xf_ld, w8, ws, out, m, n, k, stream);
+  if (!ok) ok = try_gemv_act<TO, 8, 8, XF>(xf, xf_ld, w8, ws, out, m, n, k, stream);
+  if (!ok)
+    return fail(NVF_ERR_INVALID, "matmul_q8_0_act: m=%lld rows of k=%lld do not fit the GEMV's LDS (quantize "
+                "separately and use nvf_matmul_q8_0)", (long long)m, (long long)k);
+  return launch_status("q8_gemv_kernel(act)");
+}
+
 template <typename T>
 void launch_quantize(const void* x, float* scale, int8_t* xq, int64_t rows, int64_t k, bool vec, hipStream_t stream) {
   const T* xt = static_cast<const T*>(x);
@@ -819,6 +958,33 @@ int nvf_matmul_q8_0_ws(const int8_t* xq, const float* row_scale, const uint8_t* 
 int nvf_matmul_q8_0(const int8_t* xq, const float* row_scale, const uint8_t* w8, const uint16_t* ws, int64_t m,
                     int64_t n, int64_t k, void* out, int out_dtype, void* stream) {
   return nvf_matmul_q8_0_ws(xq, row_scale, w8, ws, m, n, k, out, out_dtype, nullptr, 0, stream);
+}
+
+int nvf_matmul_q8_0_act(const void* x, int64_t x_stride, int act, const uint8_t* w8, const uint16_t* ws, int64_t m,
+                        int64_t n, int64_t k, void* out, int dtype, void* stream) {
+  static const char* who = "matmul_q8_0_act";
+  if (m < 0 || n < 0 || k < 0) return fail(NVF_ERR_INVALID, "%s: negative size", who);
+  if (k % 32 != 0) return fail(NVF_ERR_INVALID, "%s: k=%lld is not a multiple of the Q8_0 block (32)", who, (long long)k);
+  if (!dtype_ok(dtype)) return fail(NVF_ERR_INVALID, "%s: bad dtype %d", who, dtype);
+  if (act != 0 && act != 1) return fail(NVF_ERR_INVALID, "%s: act=%d (0: rows, 1: SwiGLU over gate | up)", who, act);
+  if (m > kGemvMaxM)
+    return fail(NVF_ERR_INVALID, "%s: m=%lld > %d rows (the decode GEMV's; quantize separately and use "
+                "nvf_matmul_q8_0)", who, (long long)m, kGemvMaxM);
+  if (x_stride < (act ? 2 : 1) * k) return fail(NVF_ERR_INVALID, "%s: x_stride=%lld too small", who, (long long)x_stride);
+  if (m == 0 || n == 0 || k == 0) return NVF_OK;
+  if (!x || !w8 || !ws || !out) return fail(NVF_ERR_INVALID, "%s: null pointer", who);
+  if (!aligned16(x) || !aligned16(w8) || (x_stride * dtype_bytes(dtype)) % 16 != 0)
+    return fail(NVF_ERR_INVALID, "%s: x (and its rows) and w8 must be 16-byte aligned", who);
+  if ((reinterpret_cast<uintptr_t>(ws) & 1u) != 0) return fail(NVF_ERR_INVALID, "%s: ws must be 2-byte aligned", who);
+  const int8_t* w = reinterpret_cast<const int8_t*>(w8);
+  int rc = NVF_OK;
+  if (act == 0)
+    NVF_DISPATCH_DTYPE(dtype, T, rc = (launch_gemv_act<T, 1>(static_cast<const T*>(x), x_stride, w, ws,
+                                                            static_cast<T*>(out), m, n, k, as_stream(stream))));
+  else
+    NVF_DISPATCH_DTYPE(dtype, T, rc = (launch_gemv_act<T, 2>(static_cast<const T*>(x), x_stride, w, ws,
+                                                            static_cast<T*>(out), m, n, k, as_stream(stream))));
+  return rc;
 }
 
 int64_t nvf_matmul_q8_0_workspace_size(int64_t m, int64_t n, int64_t k) {

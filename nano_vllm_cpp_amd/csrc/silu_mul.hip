@@ -22,21 +22,6 @@ constexpr int kSiluThreads = 256;
 constexpr int kSiluUnroll = 1;
 
 template <typename T>
-__device__ __forceinline__ float silu_mul(float g, float u) {
-  if constexpr (sizeof(T) == 4) {
-    return g / (1.0f + expf(-g)) * u;
-  } else {
-    const float e = __builtin_amdgcn_exp2f(g * -1.4426950408889634f);
-    float v = g * __builtin_amdgcn_rcpf(1.0f + e) * u;
-    // The fp32 product is the value: an empty asm keeps the compiler from folding
-    // the last multiply into the 16-bit conversion (v_fma_mix rounds once where
-    // multiply-then-convert rounds twice), so every kernel stores the same bits.
-    asm("" : "+v"(v));
-    return v;
-  }
-}
-
-template <typename T>
 __global__ __launch_bounds__(kSiluThreads) void silu_mul_vec_kernel(const T* __restrict__ gu, T* __restrict__ out,
                                                                     uint32_t total_vec, FastDiv vpr, int64_t inter) {
   constexpr int N = Pack<T>::N;

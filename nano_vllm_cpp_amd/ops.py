@@ -57,6 +57,7 @@ SIGNATURES: dict[str, tuple] = {
     "nvf_matmul_q8_0": (_i32, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _i32, _vp]),
     "nvf_matmul_q8_0_ws": (_i32, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _i32, _vp, _i64, _vp]),
     "nvf_matmul_q8_0_workspace_size": (_i64, [_i64, _i64, _i64]),
+    "nvf_matmul_q8_0_act": (_i32, [_vp, _i64, _i32, _vp, _vp, _i64, _i64, _i64, _vp, _i32, _vp]),
     "nvf_rms_norm_add": (_i32, [_vp, _vp, _vp, _vp, _i64, _i64, _f32, _i32, _vp]),
     "nvf_rms_norm": (_i32, [_vp, _vp, _vp, _i64, _i64, _f32, _i32, _vp]),
     "nvf_rms_norm_q8": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _f32, _i32, _vp]),
@@ -228,6 +229,21 @@ def matmul_q8_0(xq: torch.Tensor, row_scale: torch.Tensor, w8: torch.Tensor, ws:
     _check(lib().nvf_matmul_q8_0_ws(_dev(xq, "xq"), _dev(row_scale, "row_scale"), _dev(w8, "w8"), _dev(ws, "ws"), m,
                                     n, k, _dev(out, "out"), _dt(out), work.data_ptr() if work is not None else None,
                                     wb, _stream()), "matmul_q8_0")
+    return out
+
+
+def matmul_q8_0_act(x: torch.Tensor, w8: torch.Tensor, ws: torch.Tensor, n: int, swiglu: bool = False,
+                    out: torch.Tensor | None = None) -> torch.Tensor:
+    """Decode GEMV (x.shape[0] <= 16 rows) on fp activations quantized inside the kernel:
+    x [m, k] (or [gate | up] rows [m, 2k] with swiglu) in fp32/fp16/bf16; out [m, n] in x's
+    dtype, bit-identical to quantize-then-matmul_q8_0.  Rows may be strided."""
+    m, width = x.shape
+    k = width // 2 if swiglu else width
+    out = torch.empty((m, n), dtype=x.dtype, device=x.device) if out is None else out
+    if out.dtype != x.dtype or out.shape != (m, n):
+        raise ValueError("out must be [m, n] in x's dtype")
+    _check(lib().nvf_matmul_q8_0_act(_dev_rows(x, "x"), x.stride(0), 1 if swiglu else 0, _dev(w8, "w8"),
+                                     _dev(ws, "ws"), m, n, k, _dev(out, "out"), _dt(x), _stream()), "matmul_q8_0_act")
     return out
 
 

@@ -185,6 +185,56 @@ def test_fused_quantizers_feed_the_gemm(gpu, dt):
 
 
 @pytest.mark.parametrize("dt", DTYPES, ids=DT_IDS)
+@pytest.mark.parametrize("m,k,n,swiglu", [
+    (1, 3584, 3584, False),    # batch-1 o projection (W8 S8 workgroups)
+    (1, 3584, 37888, False),   # batch-1 gate_up (W4 S1)
+    (1, 18944, 3584, True),    # batch-1 down over the SwiGLU of gate | up
+    (3, 18944, 3584, True),
+    (16, 3584, 4608, False),   # 16 rows: the GEMV's most
+    (5, 1024, 520, True),      # ragged column count
+])
+def test_gemv_with_fused_quantizer(gpu, dt, m, k, n, swiglu):
+    """nvf_matmul_q8_0_act (the decode GEMV quantizing fp rows in its prologue) is
+    bit-identical to the separate quantizer (nvf_q8_quantize_rows, or nvf_silu_and_mul_q8
+    over [gate | up]) followed by nvf_matmul_q8_0; rows may be strided."""
+    r = H.rng(m * 7 + k + n + dt + 3 * swiglu)
+    w8, ws = H.gen_q8_0(r, n, k)
+    d_w8, d_ws = H.to_dev(w8, gpu), H.to_dev(ws, gpu)
+    width = 2 * k if swiglu else k
+    x_full = H.to_dev(H.gen_act(r, (m, width + 64), dt), gpu, dt)
+    x = x_full[:, :width]  # strided rows
+    case(f"gemv act m={m} k={k} n={n} swiglu={swiglu} dt={dt}")
+    got = ops.matmul_q8_0_act(x, d_w8, d_ws, n, swiglu=swiglu)
+    if swiglu:
+        _, sc, q = ops.silu_and_mul_q8(x.contiguous())
+    else:
+        sc, q = ops.q8_quantize_rows(x.contiguous())
+    want = ops.matmul_q8_0(q, sc, d_w8, d_ws, n, x.dtype)
+    torch.cuda.synchronize()
+    H.assert_bitexact(H.to_host(got), H.to_host(want), "fused quantizer vs separate pass")
+    # the product against the oracle's bound (fp32 summation of exact block dots)
+    o = H.oracle()
+    exact = np.empty((m, n), np.float64)
+    err = np.empty((m, n), np.float64)
+    q_h, sc_h = np.ascontiguousarray(q.cpu().numpy()), sc.cpu().numpy()  # kept alive across the call
+    o.orc_matmul_q8_i8(H.ptr(q_h), H.ptr(sc_h), H.ptr(w8), H.ptr(ws), m, n, k, H.ptr(exact), H.ptr(err))
+    g = H.from_storage(H.to_host(got), dt)
+    assert (np.abs(g - exact) <= err + (0.0 if dt == H.F32 else 0.5 * H.ulp(exact, dt))).all()
+
+
+def test_gemv_with_fused_quantizer_rejects(gpu):
+    x = torch.zeros(17, 1024, dtype=torch.float16, device=gpu)
+    w8 = torch.zeros(64 * 1024, dtype=torch.int8, device=gpu)
+    ws = torch.zeros(64 * 32, dtype=torch.int16, device=gpu)
+    with pytest.raises(RuntimeError, match="m=17"):
+        ops.matmul_q8_0_act(x, w8, ws, 64)
+    with pytest.raises(RuntimeError, match="do not fit"):  # 8 rows of 18944 bytes: past the staged-row LDS
+        ops.matmul_q8_0_act(torch.zeros(8, 2 * 18944, dtype=torch.float16, device=gpu),
+                            torch.zeros(64 * 18944, dtype=torch.int8, device=gpu),
+                            torch.zeros(64 * 592, dtype=torch.int16, device=gpu), 64, swiglu=True)
+
+
+@pytest.mark.parametrize("dt", DTYPES, ids=DT_IDS)
 @pytest.mark.parametrize("tokens,qh,kvh,hd,norm", [
     (37, 28, 4, 128, False),   # Qwen2.5-7B heads, packed [q | k | v] rows
     (5, 32, 8, 128, True),     # Qwen3-8B: QK-norm fused as well

@@ -435,7 +435,8 @@ def test_add_bias_closed_form(o, dt):
     # hand values: 1.5 + 0.25 = 1.75 exactly; 1 + 2^-11 rounds to 1 in fp16 (a tie, to even)
     if dt == H.F16:
         hx = H.to_storage(np.array([[1.5, 1.0]], np.float32), dt)
-        o.orc_add_bias(H.ptr(hx), H.ptr(np.array([0.25, 2.0 ** -11], np.float32)), 1, 2, 2, dt)
+        hb = np.array([0.25, 2.0 ** -11], np.float32)
+        o.orc_add_bias(H.ptr(hx), H.ptr(hb), 1, 2, 2, dt)
         assert np.array_equal(H.from_storage(hx, dt).astype(np.float32), np.array([[1.75, 1.0]], np.float32))
 
 
