@@ -89,8 +89,14 @@ void hip_embedding_u16(const int64_t* ids, const uint16_t* table, int tokens, in
 void hip_embedding_q8(const int64_t* ids, const uint8_t* w8, const uint16_t* ws, int tokens, int hidden,
                       float* out);
 
-/* hip_ops.hpp:33 -- K-quant gather (kind 12/13/14) to fp32; Q4_K in GGML order. */
+/* hip_ops.hpp:33 -- K-quant gather (kind 12/13/14) to fp32.  Q4_K in GGML (GGUF) order by
+ * default, which differs from the reference's device decoder (src/hip_ops.hip:130-140);
+ * nvf_set_dropin_q4k_layout(NVF_QK_LAYOUT_HIP_LEGACY) makes it read the reference's order. */
 void hip_embedding_qk(const int64_t* ids, const uint8_t* wq, int tokens, int hidden, float* out, int kind);
+
+/* No reference counterpart: selects the Q4_K nibble order hip_embedding_qk reads,
+ * process-wide (NVF_QK_LAYOUT_GGML, the default, or NVF_QK_LAYOUT_HIP_LEGACY). */
+int nvf_set_dropin_q4k_layout(int layout);
 
 /* hip_ops.hpp:10 -- Q8_0 GEMM, out[m,n] = x[m,k] * dequant(w8, ws)^T in fp32, with
  * the reference's per-row int8 activation quantization (hip_ops.hip:639-686).
@@ -310,7 +316,11 @@ int nvf_paged_attention_ws(const void* q, void* out, const void* k_cache, const 
  * cu_seqlens_q, include/nanovllm/context.hpp:8-25, built on the host by
  * ModelRunner::prepare_prefill, src/model_runner.cpp:43-128).  When every sequence
  * starts at a multiple of 128 tokens, every 128-token tile holds one sequence and the
- * launch for tokens of mixed tiles is not made.  Results equal nvf_paged_attention_ws's. */
+ * launch for tokens of mixed tiles is not made.  Results equal nvf_paged_attention_ws's.
+ * Contract: cu_seqlens_host must describe exactly the packing of query_seq (token t
+ * belongs to sequence s iff cu_seqlens_host[s] <= t < cu_seqlens_host[s + 1]).  Only
+ * its monotonicity and end points are checked; if it claims 128-aligned sequences
+ * that query_seq does not have, the tokens of the mixed tiles are left unwritten. */
 int nvf_paged_attention_seqs_ws(const void* q, void* out, const void* k_cache, const void* v_cache,
                                 const int32_t* query_seq, const int32_t* query_key_len, const int32_t* block_tables,
                                 const int32_t* cu_seqlens_host, int num_seqs, int64_t tokens, int q_heads,

@@ -25,6 +25,8 @@
 //     direct per-chunk loads (Q4_K/Q5_K/Q6_K split a row over 4 waves there).
 //   * A hidden that is not a multiple of the block takes a per-element kernel
 //     (correct, not tuned).
+#include <atomic>
+
 #include "nvf_device.hpp"
 #include "nvf_host.hpp"
 
@@ -1053,8 +1055,20 @@ extern "C" void hip_embedding_q8(const int64_t* ids, const uint8_t* w8, const ui
   dropin_check(nvf_embedding_q8_0(ids, w8, ws, tokens, hidden, 0, out, NVF_F32, nullptr), "hip_embedding_q8");
 }
 
+// The nibble order the drop-in hip_embedding_qk reads Q4_K in: GGML (GGUF files) by
+// default, or HIP_LEGACY to reproduce the reference's own device decoder
+// (src/hip_ops.hip:130-140) bit for bit.  Process-wide.
+static std::atomic<int> g_dropin_q4k_layout{NVF_QK_LAYOUT_GGML};
+
+extern "C" int nvf_set_dropin_q4k_layout(int layout) {
+  if (layout != NVF_QK_LAYOUT_GGML && layout != NVF_QK_LAYOUT_HIP_LEGACY)
+    return fail(NVF_ERR_INVALID, "nvf_set_dropin_q4k_layout: bad layout %d", layout);
+  g_dropin_q4k_layout.store(layout);
+  return NVF_OK;
+}
+
 extern "C" void hip_embedding_qk(const int64_t* ids, const uint8_t* wq, int tokens, int hidden, float* out, int kind) {
   if (tokens <= 0 || hidden <= 0) return;
-  dropin_check(nvf_embedding_qk(ids, wq, tokens, hidden, 0, kind, NVF_QK_LAYOUT_GGML, out, NVF_F32, nullptr),
+  dropin_check(nvf_embedding_qk(ids, wq, tokens, hidden, 0, kind, g_dropin_q4k_layout.load(), out, NVF_F32, nullptr),
                "hip_embedding_qk");
 }

@@ -78,6 +78,7 @@ SIGNATURES: dict[str, tuple] = {
     "nvf_stream_copy": (_i32, [_vp, _vp, _i64, _vp]),
     "nvf_stream_expand": (_i32, [_vp, _vp, _i64, _vp]),
     "nvf_q8_0_split_blocks": (_i32, [_vp, _i64, _vp, _vp, _vp]),
+    "nvf_set_dropin_q4k_layout": (_i32, [_i32]),
     "nvf_last_error": (C.c_char_p, []),
     "nvf_abi_version": (_i32, []),
 }

@@ -176,6 +176,15 @@ def test_dropin_vs_reference_kernels_embeddings(gpu, ref):
         ops.lib().hip_embedding_qk(dptr(d_ids), dptr(d_b), T, hidden, dptr(mine), kind)
         torch.cuda.synchronize()
         H.assert_bitexact(mine.cpu().numpy(), oref, f"hip_embedding_qk kind {kind} vs oracle")
+        if kind == 12:  # switched to the reference's nibble order, the drop-in matches its kernel too
+            ops._check(ops.lib().nvf_set_dropin_q4k_layout(H.HIP_LEGACY), "set layout")
+            try:
+                case("hip_embedding_qk kind=12 in the reference's nibble order")
+                ops.lib().hip_embedding_qk(dptr(d_ids), dptr(d_b), T, hidden, dptr(mine), kind)
+                torch.cuda.synchronize()
+            finally:
+                ops._check(ops.lib().nvf_set_dropin_q4k_layout(H.GGML), "set layout")
+            H.assert_bitexact(mine.cpu().numpy(), theirs.cpu().numpy(), "hip_embedding_qk legacy vs reference kernel")
 
     for bf16 in (0, 1):
         table = H.gen_act(r, (V, hidden), H.BF16 if bf16 else H.F16)
