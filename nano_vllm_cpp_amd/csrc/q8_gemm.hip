@@ -147,7 +147,9 @@ __device__ __forceinline__ void gemm_store_out(TO* p, float v) {
 //
 // One loop iteration per Q8_0 block; the first MFMA of block g + 1 is issued
 // while block g is applied, so each result is ready when its scale is applied.
-template <typename TO, bool SPLIT>
+// PL: k is not a multiple of the 64-byte stage, so the last stage is partial (known
+// at launch; without it the loop carries none of the partial stage's address selects).
+template <typename TO, bool SPLIT, bool PL = true>
 __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(3))) void q8_gemm_kernel(
     const int8_t* __restrict__ xq, const float* __restrict__ rscale, const int8_t* __restrict__ w8,
     const uint16_t* __restrict__ ws, TO* __restrict__ out, int64_t m, int64_t n, int64_t k, int tiles_n,
@@ -219,7 +221,7 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(3)
   // split is non-empty: the host sizes the split count so)
   const int st0 = SPLIT ? (int)blockIdx.y * st_per_split : 0;
   const int st1 = SPLIT ? min(nstages, st0 + st_per_split) : nstages;
-  const bool partial_last = k % kGemmKC != 0;
+  const bool partial_last = PL && k % kGemmKC != 0;
   // Loads stage st into LDS buffer `buf`, all by DMA.
   auto issue = [&](int st, int buf) {  // st: absolute stage; buf: its double-buffer slot
     uint8_t* stage = lds + buf * kGemmStage;
@@ -858,18 +860,24 @@ int launch_gemm(const int8_t* xq, const float* rscale, const int8_t* w8, const u
   }
   static std::once_flag attr_once;
   std::call_once(attr_once, [] {
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&q8_gemm_kernel<TO, false>),
-                              hipFuncAttributeMaxDynamicSharedMemorySize, kGemmLds);
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&q8_gemm_kernel<TO, true>),
-                              hipFuncAttributeMaxDynamicSharedMemorySize, kGemmLds);
+    for (const void* f : {reinterpret_cast<const void*>(&q8_gemm_kernel<TO, false, true>),
+                          reinterpret_cast<const void*>(&q8_gemm_kernel<TO, true, true>),
+                          reinterpret_cast<const void*>(&q8_gemm_kernel<TO, false, false>),
+                          reinterpret_cast<const void*>(&q8_gemm_kernel<TO, true, false>)})
+      (void)hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, kGemmLds);
   });
   const int tiles_n = (int)((n + kGemmBN - 1) / kGemmBN);
   const int64_t tiles = ((m + kGemmBM - 1) / kGemmBM) * tiles_n;
   const GemmSplit sp = gemm_split_plan(m, n, k);
   if (sp.splits > 1 && work && work_bytes >= gemm_split_bytes(m, n, sp)) {
     float* part = static_cast<float*>(work);
-    q8_gemm_kernel<TO, true><<<dim3((unsigned)tiles, (unsigned)sp.splits), dim3(kGemmThreads), kGemmLds, stream>>>(
-        xq, rscale, w8, ws, out, m, n, k, tiles_n, sp.st_per_split, part);
+    const dim3 grid((unsigned)tiles, (unsigned)sp.splits);
+    if (k % kGemmKC != 0)
+      q8_gemm_kernel<TO, true, true><<<grid, dim3(kGemmThreads), kGemmLds, stream>>>(
+          xq, rscale, w8, ws, out, m, n, k, tiles_n, sp.st_per_split, part);
+    else
+      q8_gemm_kernel<TO, true, false><<<grid, dim3(kGemmThreads), kGemmLds, stream>>>(
+          xq, rscale, w8, ws, out, m, n, k, tiles_n, sp.st_per_split, part);
     const int rc = launch_status("q8_gemm_kernel(split)");
     if (rc != NVF_OK) return rc;
     const int64_t threads = m * ((n + 3) / 4);
@@ -877,8 +885,12 @@ int launch_gemm(const int8_t* xq, const float* rscale, const int8_t* w8, const u
                                                                                                  n, sp.splits);
     return launch_status("q8_gemm_reduce_kernel");
   }
-  q8_gemm_kernel<TO, false><<<dim3((unsigned)tiles), dim3(kGemmThreads), kGemmLds, stream>>>(
-      xq, rscale, w8, ws, out, m, n, k, tiles_n, 0, nullptr);
+  if (k % kGemmKC != 0)
+    q8_gemm_kernel<TO, false, true><<<dim3((unsigned)tiles), dim3(kGemmThreads), kGemmLds, stream>>>(
+        xq, rscale, w8, ws, out, m, n, k, tiles_n, 0, nullptr);
+  else
+    q8_gemm_kernel<TO, false, false><<<dim3((unsigned)tiles), dim3(kGemmThreads), kGemmLds, stream>>>(
+        xq, rscale, w8, ws, out, m, n, k, tiles_n, 0, nullptr);
   return launch_status("q8_gemm_kernel");
 }
 

@@ -265,6 +265,16 @@ def store_kv(key: torch.Tensor, value: torch.Tensor, k_cache: torch.Tensor, v_ca
     key/value [tokens, kv_heads, head_dim] (row stride from the tensor), caches
     [rows, kv_heads, head_dim] contiguous."""
     tokens, kv_heads, head_dim = key.shape
+    if value.shape != key.shape:
+        raise ValueError("value must have key's shape [tokens, kv_heads, head_dim]")
+    for name, x in (("value", value), ("k_cache", k_cache), ("v_cache", v_cache)):
+        if x.dtype != key.dtype:
+            raise ValueError(f"{name} must have key's dtype {key.dtype}")
+    for name, c in (("k_cache", k_cache), ("v_cache", v_cache)):
+        if c.dim() != 3 or tuple(c.shape[1:]) != (kv_heads, head_dim):
+            raise ValueError(f"{name} must be [rows, kv_heads, head_dim]")
+    if slot_mapping.dtype != torch.int32 or slot_mapping.shape != (tokens,):
+        raise ValueError("slot_mapping must be int32 [tokens]")
     _check(lib().nvf_store_kv(_dev_rows(key, "key"), _dev_rows(value, "value"), _dev(k_cache, "k_cache"),
                               _dev(v_cache, "v_cache"), _dev(slot_mapping, "slot_mapping"), tokens, kv_heads, head_dim,
                               key.stride(0), value.stride(0), _dt(key), _stream()), "store_kv")
