@@ -479,10 +479,10 @@ def main() -> int:
     torch.cuda.synchronize()
 
     # Per-op timing.  The GPU is first held by a spin kernel (torch.cuda._sleep) while the
-    # host enqueues n >= 50 launches in groups of 10 with an event between groups, so the
+    # host enqueues n >= 200 launches in groups of 25 with an event between groups, so the
     # launches then run back to back with no host gap between them (a Python launch costs
     # ~15-25 us of host time, more than some of these kernels take).  "us" is the mean over
-    # all n launches, "p50_us" the median of the groups' mean launch times (the timing rule),
+    # all n launches, "p50_us" the median of the 8 groups' mean launch times (the timing rule),
     # p10/p90 their spread.  An op whose enqueue outran the spin is retried with a longer
     # spin; "eager_us" is the plain back-to-back mean with the host in the loop.
     stream = torch.cuda.current_stream()
@@ -491,7 +491,8 @@ def main() -> int:
     _lens = np.diff(cfg.cu_seqlens())
     batch_desc = (f"{len(_lens)} one-token queries at random positions" if int(_lens.max()) == 1
                   else f"causal prefill {len(_lens)} x {T // len(_lens)} tokens")
-    n_launch = -(-max(args.steps, 50) // 10) * 10
+    group = 25
+    n_launch = -(-max(args.steps, 200) // group) * group
     cyc_per_us = sleep_rate(torch, stream)
     for n, f in active:
         a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -505,14 +506,14 @@ def main() -> int:
         if n == "layer_b1":  # host in the loop by design: eager launches (against layer_b1_graph's replays)
             per, t_us = None, eager_us
         else:
-            per = timed_launches(torch, stream, f, args.warmup, n_launch, cyc_per_us)
+            per = timed_launches(torch, stream, f, args.warmup, n_launch, cyc_per_us, group)
             t_us = float(per.mean())
         entry = {"us": round(t_us, 2)}
         if per is not None:
             entry.update({"p10_us": round(float(np.percentile(per, 10)), 2),
                           "p50_us": round(float(np.percentile(per, 50)), 2),
                           "p90_us": round(float(np.percentile(per, 90)), 2), "launches": n_launch,
-                          "p_over": "groups of 10 back-to-back launches",
+                          "p_over": f"groups of {group} back-to-back launches",
                           "eager_us": round(eager_us, 2)})
         if n in nbytes:
             gbs = nbytes[n] / (t_us * 1e-6) / 1e9
@@ -654,7 +655,7 @@ def sleep_rate(torch, stream) -> float:
     return 1_000_000 / (a.elapsed_time(b) * 1e3)
 
 
-def timed_launches(torch, stream, f, first: int, n: int, cyc_per_us: float, group: int = 10):
+def timed_launches(torch, stream, f, first: int, n: int, cyc_per_us: float, group: int = 25):
     """n launches f(first), f(first + 1), ... (n a multiple of group) run back to back
     behind a spin kernel that holds the GPU while the host enqueues them.  An event
     sits between groups of `group` launches only (an event record between every two
