@@ -401,7 +401,8 @@ def main() -> int:
                                   cfg.eps, qkv_bias=L_["bias"])
         att = ops.paged_attention(qkv[:, :qs].view(n_, cfg.q_heads, cfg.head_dim), L_["kc"], L_["vc"], L_["qseq"],
                                   L_["qlen"], L_["tab"], bs_kv, cfg.head_dim ** -0.5, out=L_["attn_out"],
-                                  max_query_len=L_["mql"], cu_seqlens=L_.get("cu"))
+                                  max_query_len=L_["mql"], cu_seqlens=L_.get("cu"),
+                                  noalloc=L_["mql"] == 1)  # decode: the split's partials in the static scratch
         if n_ <= 16:  # decode GEMV: the o and down projections quantize their own input rows
             o = ops.matmul_q8_0_act(att.view(n_, qs), *L_["o"], Hd, out=L_["o_out"])
         else:

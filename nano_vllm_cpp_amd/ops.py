@@ -283,7 +283,7 @@ def store_kv(key: torch.Tensor, value: torch.Tensor, k_cache: torch.Tensor, v_ca
 def paged_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, query_seq: torch.Tensor,
                     query_key_len: torch.Tensor, block_tables: torch.Tensor, block_size: int, scale: float,
                     out: torch.Tensor | None = None, max_query_len: int = 0, split: bool = True,
-                    cu_seqlens=None) -> torch.Tensor:
+                    cu_seqlens=None, noalloc: bool = False) -> torch.Tensor:
     """q [tokens, q_heads, head_dim] (row stride from the tensor); caches
     [rows, kv_heads, head_dim]; block_tables [seqs, max_blocks] int32.
     max_query_len = 1 promises a decode batch (one query per sequence).  split:
@@ -291,12 +291,23 @@ def paged_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tenso
     it (little work over long contexts); False runs unsplit.  cu_seqlens: the
     batch's packing on the host ([seqs + 1] ints, 0 .. tokens), if the caller has it
     (nvf_paged_attention_seqs_ws: no launch for mixed tiles when every sequence
-    starts at a multiple of 128 tokens).
+    starts at a multiple of 128 tokens).  noalloc: nvf_paged_attention_noalloc (the
+    split's partials in the library's static device scratch, no workspace
+    allocated).
     Returns out [tokens, q_heads, head_dim] in q's dtype."""
     tokens, q_heads, head_dim = q.shape
     kv_heads = k_cache.shape[1]
     max_blocks = block_tables.shape[1]
     out = torch.empty((tokens, q_heads, head_dim), dtype=q.dtype, device=q.device) if out is None else out
+    if noalloc:
+        if cu_seqlens is not None or not split:
+            raise ValueError("noalloc takes neither cu_seqlens nor split=False")
+        _check(lib().nvf_paged_attention_noalloc(
+            _dev_rows(q, "q"), _dev(out, "out"), _dev(k_cache, "k_cache"), _dev(v_cache, "v_cache"),
+            _dev(query_seq, "query_seq"), _dev(query_key_len, "query_key_len"), _dev(block_tables, "block_tables"),
+            tokens, q_heads, kv_heads, head_dim, block_size, max_blocks, scale, q.stride(0), max_query_len, _dt(q),
+            _stream()), "paged_attention_noalloc")
+        return out
     ws_bytes = lib().nvf_paged_attention_workspace_size(tokens, q_heads, kv_heads, head_dim, block_size,
                                                        max_blocks, max_query_len) if split else 0
     ws = torch.empty((ws_bytes + 15) // 16 * 4, dtype=torch.float32, device=q.device) if ws_bytes > 0 else None

@@ -53,7 +53,7 @@ def _build(dev, batch, ctx):
     return L
 
 
-def _layer(L):
+def _layer(L, noalloc=False):
     qs, ks = QH * HD, KVH * HD
     n = L["h"].shape[0]
     _, sc, xq = ops.rms_norm_q8(L["h"], L["w_in"], 1e-6, residual=L["r"], want_out=False)
@@ -62,7 +62,7 @@ def _layer(L):
     ops.store_kv(qkv[:, qs:qs + ks].view(n, KVH, HD), qkv[:, qs + ks:].view(n, KVH, HD), L["kc"], L["vc"],
                  L["slots"])
     att = ops.paged_attention(qkv[:, :qs].view(n, QH, HD), L["kc"], L["vc"], L["qseq"], L["qlen"], L["tab"], BS,
-                              HD ** -0.5, max_query_len=1)
+                              HD ** -0.5, max_query_len=1, noalloc=noalloc)
     sc2, xq2 = ops.q8_quantize_rows(att.view(n, qs))
     o = ops.matmul_q8_0(xq2, sc2, *L["o"], HID, torch.float16)
     _, sc3, xq3 = ops.rms_norm_q8(o, L["w_post"], 1e-6, residual=L["r"], want_out=False)
@@ -71,13 +71,17 @@ def _layer(L):
     ops.matmul_q8_0(xq4, sc4, *L["down"], HID, torch.float16, out=L["out"])
 
 
+@pytest.mark.parametrize("noalloc", [False, True], ids=["ws", "noalloc"])
 @pytest.mark.parametrize("batch,ctx", [(1, 4096), (3, 1500)])
-def test_decode_layer_graph_replays_match_eager(gpu, batch, ctx):
+def test_decode_layer_graph_replays_match_eager(gpu, batch, ctx, noalloc):
+    """noalloc: the attention through nvf_paged_attention_noalloc, its split partials
+    in the library's static device scratch rather than a pool allocation made during
+    the capture."""
     L = _build(gpu, batch, ctx)
     assert ops.lib().nvf_paged_attention_workspace_size(batch, QH, KVH, HD, BS, L["tab"].shape[1], 1) > 0
     r0 = L["r"].clone()
-    case(f"decode layer eager batch={batch} ctx={ctx}")
-    _layer(L)
+    case(f"decode layer eager batch={batch} ctx={ctx} noalloc={noalloc}")
+    _layer(L, noalloc)
     torch.cuda.synchronize()
     want_out, want_r, want_kc = L["out"].clone(), L["r"].clone(), L["kc"].clone()
     cs = torch.cuda.Stream()
@@ -85,13 +89,13 @@ def test_decode_layer_graph_replays_match_eager(gpu, batch, ctx):
     with torch.cuda.stream(cs):  # warm the side stream the capture uses
         for _ in range(2):
             L["r"].copy_(r0)
-            _layer(L)
+            _layer(L, noalloc)
     torch.cuda.current_stream().wait_stream(cs)
     torch.cuda.synchronize()
     graph = torch.cuda.CUDAGraph()
-    case(f"decode layer capture batch={batch} ctx={ctx}")
+    case(f"decode layer capture batch={batch} ctx={ctx} noalloc={noalloc}")
     with torch.cuda.graph(graph):
-        _layer(L)
+        _layer(L, noalloc)
     torch.cuda.synchronize()
     for rep in range(4):
         L["r"].copy_(r0)           # eager work between the replays
