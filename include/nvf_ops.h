@@ -41,6 +41,17 @@ enum nvf_qk_layout { NVF_QK_LAYOUT_GGML = 0, NVF_QK_LAYOUT_HIP_LEGACY = 1 };
 /* K-quant kinds, the GGML type ids the reference passes (src/model.cpp:163). */
 enum nvf_qk_kind { NVF_Q4_K = 12, NVF_Q5_K = 13, NVF_Q6_K = 14 };
 
+/* Weight formats of nvf_matmul (row-major [n][k] element arrays; the K-quants are
+ * 256-element superblocks over the flat element index, src/hip_ops.hip:184-193). */
+enum nvf_w_format {
+  NVF_W_F32 = 0,
+  NVF_W_F16 = 1,
+  NVF_W_BF16 = 2,
+  NVF_W_Q4_K = 12,
+  NVF_W_Q5_K = 13,
+  NVF_W_Q6_K = 14
+};
+
 /* Table formats of the fused embedding entry point. */
 enum nvf_emb_format {
   NVF_EMB_Q8_0 = 0,        /* split planes: table = int8 [V*H], scales = fp16 [V*H/32] */
@@ -93,6 +104,21 @@ void hip_embedding_q8(const int64_t* ids, const uint8_t* w8, const uint16_t* ws,
  * default, which differs from the reference's device decoder (src/hip_ops.hip:130-140);
  * nvf_set_dropin_q4k_layout(NVF_QK_LAYOUT_HIP_LEGACY) makes it read the reference's order. */
 void hip_embedding_qk(const int64_t* ids, const uint8_t* wq, int tokens, int hidden, float* out, int kind);
+
+/* hip_ops.hpp:8 -- out[m,n] = x[m,k] . w[n,k]^T, fp32 weights. */
+void hip_matmul(const float* x, const float* w, int m, int n, int k, float* out);
+
+/* hip_ops.hpp:9 -- as hip_matmul with fp16 (w_bf16 false) or bf16 weights, widened exactly. */
+void hip_matmul_u16(const float* x, const uint16_t* w, int m, int n, int k, float* out, bool w_bf16);
+
+/* hip_ops.hpp:11 -- as hip_matmul with K-quant weights (kind 12/13/14: Q4_K/Q5_K/Q6_K
+ * superblocks over the flat [n][k] element index), decoded exactly.  Q4_K nibble order
+ * as hip_embedding_qk (nvf_set_dropin_q4k_layout).  Needs k % 16 == 0. */
+void hip_matmul_qk(const float* x, const uint8_t* wq, int m, int n, int k, float* out, int kind);
+
+/* hip_ops.hpp:34 -- out[r,:] = rows[indices[r],:] for r < out_rows (the last-token rows
+ * ahead of the LM head, src/model.cpp:839); rows_count is unused, as in the reference. */
+void hip_gather_rows(const float* rows, const int32_t* indices, int rows_count, int cols, int out_rows, float* out);
 
 /* No reference counterpart: selects the Q4_K nibble order hip_embedding_qk reads,
  * process-wide (NVF_QK_LAYOUT_GGML, the default, or NVF_QK_LAYOUT_HIP_LEGACY). */
@@ -186,6 +212,21 @@ int nvf_qkv_bias_qk_norm_rope_store_kv(void* q, void* k, const void* v, const fl
 /* x[r*stride + c] += bias[c] for r < rows, c < cols (replaces hip_add_bias_inplace,
  * hip_ops.hpp:12): x in `dtype`, bias fp32 [cols], one rounding per element. */
 int nvf_add_bias(void* x, const float* bias, int64_t rows, int64_t cols, int64_t stride, int dtype, void* stream);
+
+/* GEMM on dense or K-quant weights (replaces hip_matmul, hip_matmul_u16 and
+ * hip_matmul_qk, hip_ops.hpp:8-11): out[m,n] (out_dtype) = x[m,k] (x_dtype) . w^T with
+ * w in `w_format` (nvf_w_format; Q4_K nibble order `qk_layout`) decoded exactly to fp32,
+ * fp32 products and sums on the matrix cores.  k % 16 == 0; K-quants: n*k a multiple of
+ * 256.  x and dense weights 16-byte aligned; Q4_K/Q5_K blocks 16-byte, Q6_K 2-byte. */
+int nvf_matmul(const void* x, int x_dtype, const void* w, int w_format, int qk_layout, int64_t m, int64_t n,
+               int64_t k, void* out, int out_dtype, void* stream);
+
+/* Row gather (replaces hip_gather_rows, hip_ops.hpp:34): out[r,:] = rows[indices[r],:]
+ * for r < out_rows, cols wide, rows and out in `dtype` (a bit-exact copy).
+ * rows_count > 0: an index outside [0, rows_count) gives a NaN row instead of a
+ * read; rows_count <= 0: indices are trusted, as the reference does. */
+int nvf_gather_rows(const void* rows, const int32_t* indices, int64_t rows_count, int64_t cols, int64_t out_rows,
+                    void* out, int dtype, void* stream);
 
 /* Q8_0 gather, split planes (as hip_embedding_q8) -> out in out_dtype.
  * vocab > 0: ids outside [0, vocab) produce a NaN row instead of a read;

@@ -19,6 +19,10 @@ int launch_status(const char* what);
 // entry points: print and exit(1) on a nonzero status.
 void dropin_check(int status, const char* what);
 
+// The Q4_K nibble order the drop-ins read (hip_embedding_qk, hip_matmul_qk), set
+// process-wide by nvf_set_dropin_q4k_layout.
+int dropin_q4k_layout();
+
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }

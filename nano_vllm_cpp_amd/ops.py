@@ -23,6 +23,7 @@ F32, F16, BF16 = 0, 1, 2
 EMB_Q8_0, EMB_Q8_0_BLOCKS, EMB_Q4_K, EMB_Q5_K, EMB_Q6_K = 0, 1, 12, 13, 14
 QK_LAYOUT_GGML, QK_LAYOUT_HIP_LEGACY = 0, 1
 Q4_K, Q5_K, Q6_K = 12, 13, 14
+W_F32, W_F16, W_BF16 = 0, 1, 2
 
 _DT = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16}
 
@@ -39,6 +40,12 @@ SIGNATURES: dict[str, tuple] = {
     "hip_embedding_u16": (None, [_vp, _vp, _i32, _i32, _vp, C.c_bool]),
     "hip_embedding_q8": (None, [_vp, _vp, _vp, _i32, _i32, _vp]),
     "hip_embedding_qk": (None, [_vp, _vp, _i32, _i32, _vp, _i32]),
+    "hip_gather_rows": (None, [_vp, _vp, _i32, _i32, _i32, _vp]),
+    "hip_matmul": (None, [_vp, _vp, _i32, _i32, _i32, _vp]),
+    "hip_matmul_u16": (None, [_vp, _vp, _i32, _i32, _i32, _vp, C.c_bool]),
+    "hip_matmul_qk": (None, [_vp, _vp, _i32, _i32, _i32, _vp, _i32]),
+    "nvf_matmul": (_i32, [_vp, _i32, _vp, _i32, _i32, _i64, _i64, _i64, _vp, _i32, _vp]),
+    "nvf_gather_rows": (_i32, [_vp, _vp, _i64, _i64, _i64, _vp, _i32, _vp]),
     "hip_matmul_q8": (None, [_vp, _vp, _vp, _i32, _i32, _i32, _vp]),
     "hip_store_kv": (None, [_vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32]),
     "hip_paged_attention": (None, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _i32, _f32]),
@@ -513,3 +520,32 @@ def stream_expand(dst: torch.Tensor, src: torch.Tensor) -> None:
     _check(lib().nvf_stream_expand(_dev(dst, "dst"), _dev(src, "src"), src.numel() * src.element_size(), _stream()),
            "stream_expand")
 
+
+def gather_rows(rows: torch.Tensor, indices: torch.Tensor, out: torch.Tensor | None = None,
+                check: bool = True) -> torch.Tensor:
+    """out[r] = rows[indices[r]] (rows [n, cols]; indices int32 [out_rows]).  check: an
+    index outside [0, n) gives a NaN row (otherwise indices are trusted)."""
+    n, cols = rows.shape
+    if indices.dtype != torch.int32 or indices.dim() != 1:
+        raise ValueError("indices must be int32 [out_rows]")
+    out_rows = indices.numel()
+    out = torch.empty((out_rows, cols), dtype=rows.dtype, device=rows.device) if out is None else out
+    if out.shape != (out_rows, cols) or out.dtype != rows.dtype:
+        raise ValueError("out must be [out_rows, cols] in rows' dtype")
+    _check(lib().nvf_gather_rows(_dev(rows, "rows"), _dev(indices, "indices"), n if check else 0, cols, out_rows,
+                                 _dev(out, "out"), _dt(rows), _stream()), "gather_rows")
+    return out
+
+
+def matmul(x: torch.Tensor, w: torch.Tensor, n: int, w_format: int, out_dtype=None, qk_layout: int = QK_LAYOUT_GGML,
+           out: torch.Tensor | None = None) -> torch.Tensor:
+    """out [m, n] = x [m, k] . W^T, W [n, k] in `w_format` (W_F32/W_F16/W_BF16 as a tensor of that
+    dtype, or Q4_K/Q5_K/Q6_K as a uint8 tensor of superblocks) decoded exactly to fp32."""
+    m, k = x.shape
+    out_dtype = out_dtype or x.dtype
+    out = torch.empty((m, n), dtype=out_dtype, device=x.device) if out is None else out
+    if out.shape != (m, n) or out.dtype != out_dtype:
+        raise ValueError("out must be [m, n] in out_dtype")
+    _check(lib().nvf_matmul(_dev(x, "x"), _dt(x), _dev(w, "w"), w_format, qk_layout, m, n, k, _dev(out, "out"),
+                            _DT[out_dtype], _stream()), "matmul")
+    return out

@@ -469,6 +469,76 @@ void orc_matmul_q8_i8(const int8_t* xq, const float* scale, const uint8_t* w8, c
   }
 }
 
+/* The weight element w(c, i) = element c*k + i of the flat weight array, decoded
+ * exactly to fp32: fp32 rows (src/hip_ops.hip:43-64 matmul_kernel<float>), fp16/bf16
+ * rows widened (matmul_kernel<uint16_t>, wt_load :38-41), or K-quant superblocks over
+ * the flat index (matmul_qk_kernel :577-598 via qk_w :184-193; Q4_K in `layout`). */
+static void dense_weight_row(const void* w, int w_format, int layout, int64_t c, int64_t k, float* row) {
+  if (w_format == 0) {
+    for (int64_t i = 0; i < k; ++i) row[i] = ((const float*)w)[c * k + i];
+  } else if (w_format == 1 || w_format == 2) {
+    for (int64_t i = 0; i < k; ++i) {
+      const uint16_t h = ((const uint16_t*)w)[c * k + i];
+      row[i] = w_format == 2 ? orc_bf16_to_f32(h) : orc_fp16_to_f32(h);
+    }
+  } else {
+    const int64_t bb = w_format == 12 ? 144 : (w_format == 13 ? 176 : 210);
+    float y[256];
+    int64_t cached = -1;
+    for (int64_t i = 0; i < k; ++i) {
+      const int64_t e = c * k + i, b = e >> 8;
+      if (b != cached) {
+        const uint8_t* blk = (const uint8_t*)w + b * bb;
+        if (w_format == 12)
+          orc_dequant_q4k_block(blk, y, layout);
+        else if (w_format == 13)
+          orc_dequant_q5k_block(blk, y);
+        else
+          orc_dequant_q6k_block(blk, y);
+        cached = b;
+      }
+      row[i] = y[e & 255];
+    }
+  }
+}
+
+/* hip_matmul / hip_matmul_u16 / hip_matmul_qk (src/hip_ops.hip:746-777):
+ * out[r][c] = sum_i x[r][i] * w(c, i), x [m,k] in x_dtype.  The reference sums the
+ * fp32 products in k order (16-element tiles, one output per thread); this sums
+ * them in double, and err[r][c] = (k + 2) u sum_i |x w| bounds every fp32 summation
+ * order (one rounding per product and per addition). */
+void orc_matmul_w(const void* x, int x_dtype, const void* w, int w_format, int layout, int64_t m, int64_t n,
+                  int64_t k, double* out, double* err) {
+  float* row = (float*)malloc(sizeof(float) * (size_t)(k > 0 ? k : 1));
+  float* xr = (float*)malloc(sizeof(float) * (size_t)(m * k > 0 ? m * k : 1));
+  for (int64_t i = 0; i < m * k; ++i) xr[i] = orc_load(x, i, x_dtype);
+  for (int64_t c = 0; c < n; ++c) {
+    dense_weight_row(w, w_format, layout, c, k, row);
+    for (int64_t r = 0; r < m; ++r) {
+      double sum = 0.0, mag = 0.0;
+      for (int64_t i = 0; i < k; ++i) {
+        const double t = (double)xr[r * k + i] * (double)row[i];
+        sum += t;
+        mag += fabs(t);
+      }
+      out[r * n + c] = sum;
+      err[r * n + c] = (double)(k + 2) * ldexp(1.0, -24) * mag;
+    }
+  }
+  free(row);
+  free(xr);
+}
+
+/* src/hip_ops.hip:611-619 (gather_rows_kernel): out[r][c] = rows[indices[r]][c], a copy
+ * in the storage dtype. */
+void orc_gather_rows(const void* rows, const int32_t* indices, int64_t cols, int64_t out_rows, void* out,
+                     int dtype) {
+  const size_t e = dtype == ORC_F32 ? 4 : 2;
+  for (int64_t r = 0; r < out_rows; ++r)
+    memcpy((char*)out + (size_t)(r * cols) * e, (const char*)rows + (size_t)((int64_t)indices[r] * cols) * e,
+           (size_t)cols * e);
+}
+
 /* The reference's whole hip_matmul_q8 on activations x [m,k] in `dtype`: row
  * scales (:205-217), quantization (:244-245), then orc_matmul_q8_i8.  scale_out
  * [m] and xq_out [m,k] receive the intermediate values when not NULL. */

@@ -45,6 +45,12 @@
  *                              numpy softmax(q K^T) V; on the GPU box within the
  *                              tolerance of the reference's hip_paged_attention
  *   KV store ................. a copy: rows land at their slots, slot -1 skipped
+ *   dense / K-quant GEMM ..... exact on power-of-two weights and small integers
+ *                              (every partial sum exact); equal to a textbook
+ *                              matmul of the dequantized weights (numpy); on the
+ *                              GPU box the reference's own hip_matmul* lie within
+ *                              the bound
+ *   row gather ............... a copy: equal to numpy fancy indexing
  *   Q8_0 GEMM ................ exact on power-of-two scales against a textbook
  *                              matmul of the dequantized weights; the error bound
  *                              holds for fp32 sums in every order; on the GPU box
@@ -119,6 +125,10 @@ void orc_q8_quantize(const void* x, const float* scale, int8_t* q, int64_t rows,
 /* Q8_0 GEMM, src/hip_ops.hip:639-686: out[r,c] = (sum_b ws[c,b] * I[r,c,b]) /
  * scale[r] with exact integer block dots I, in double, and err[r,c], the fp32
  * recursive-summation bound (k/32 + 4) * 2^-24 * sum_b |ws*I| / scale[r]. */
+void orc_matmul_w(const void* x, int x_dtype, const void* w, int w_format, int layout, int64_t m, int64_t n,
+                  int64_t k, double* out, double* err);
+void orc_gather_rows(const void* rows, const int32_t* indices, int64_t cols, int64_t out_rows, void* out,
+                     int dtype);
 void orc_matmul_q8_i8(const int8_t* xq, const float* scale, const uint8_t* w8, const uint16_t* ws, int64_t m,
                       int64_t n, int64_t k, double* out, double* err);
 void orc_matmul_q8(const void* x, int dtype, const uint8_t* w8, const uint16_t* ws, int64_t m, int64_t n, int64_t k,

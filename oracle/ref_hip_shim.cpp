@@ -45,6 +45,32 @@ void ref_hip_matmul_q8_async(const float* x, const uint8_t* w8, const uint16_t* 
                              float* out) {
   hip_matmul_q8(x, w8, ws, m, n, k, out);
 }
+void ref_hip_matmul(const float* x, const float* w, int m, int n, int k, float* out) {
+  hip_matmul(x, w, m, n, k, out);
+  HIP_CHECK(hipDeviceSynchronize());
+}
+void ref_hip_matmul_u16(const float* x, const uint16_t* w, int m, int n, int k, float* out, bool w_bf16) {
+  hip_matmul_u16(x, w, m, n, k, out, w_bf16);
+  HIP_CHECK(hipDeviceSynchronize());
+}
+void ref_hip_matmul_qk(const float* x, const uint8_t* wq, int m, int n, int k, float* out, int kind) {
+  hip_matmul_qk(x, wq, m, n, k, out, kind);
+  HIP_CHECK(hipDeviceSynchronize());
+}
+// No synchronisation, for timing: w_format 0 fp32, 1 fp16, 2 bf16, 12/13/14 K-quants.
+void ref_hip_matmul_any_async(int w_format, const float* x, const void* w, int m, int n, int k, float* out) {
+  if (w_format == 0)
+    hip_matmul(x, static_cast<const float*>(w), m, n, k, out);
+  else if (w_format == 1 || w_format == 2)
+    hip_matmul_u16(x, static_cast<const uint16_t*>(w), m, n, k, out, w_format == 2);
+  else
+    hip_matmul_qk(x, static_cast<const uint8_t*>(w), m, n, k, out, w_format);
+}
+void ref_hip_gather_rows(const float* rows, const int32_t* indices, int rows_count, int cols, int out_rows,
+                         float* out) {
+  hip_gather_rows(rows, indices, rows_count, cols, out_rows, out);
+  HIP_CHECK(hipDeviceSynchronize());
+}
 void ref_hip_store_kv(const float* key, const float* value, float* k_cache, float* v_cache, const int32_t* slots,
                       int tokens, int kv_heads, int head_dim) {
   hip_store_kv(key, value, k_cache, v_cache, slots, tokens, kv_heads, head_dim);

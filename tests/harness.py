@@ -53,6 +53,8 @@ _ORACLE_SIGS = {
     "orc_paged_attention": (None, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i32, _i32, _i32, _i32, _i32, _f32,
                                    _i32, _vp, _vp]),
     "orc_matmul_q8": (None, [_vp, _i32, _vp, _vp, _i64, _i64, _i64, _vp, _vp, _vp, _vp]),
+    "orc_matmul_w": (None, [_vp, _i32, _vp, _i32, _i32, _i64, _i64, _i64, _vp, _vp]),
+    "orc_gather_rows": (None, [_vp, _vp, _i64, _i64, _vp, _i32]),
 }
 
 _cache: dict[str, C.CDLL] = {}
@@ -105,6 +107,11 @@ def ref_hip() -> C.CDLL | None:
     h.ref_hip_store_kv.argtypes = [_vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32]
     h.ref_hip_add_bias_inplace.argtypes = [_vp, _vp, _i32, _i32]
     h.ref_hip_paged_attention.argtypes = [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _i32, _f32]
+    h.ref_hip_matmul.argtypes = [_vp, _vp, _i32, _i32, _i32, _vp]
+    h.ref_hip_matmul_u16.argtypes = [_vp, _vp, _i32, _i32, _i32, _vp, C.c_bool]
+    h.ref_hip_matmul_qk.argtypes = [_vp, _vp, _i32, _i32, _i32, _vp, _i32]
+    h.ref_hip_matmul_any_async.argtypes = [_i32, _vp, _vp, _i32, _i32, _i32, _vp]
+    h.ref_hip_gather_rows.argtypes = [_vp, _vp, _i32, _i32, _i32, _vp]
     return h
 
 
@@ -291,6 +298,18 @@ def gen_raw_blocks(r: np.random.Generator, nblocks: int, block_bytes: int, fp16_
     for off in fp16_offsets:
         blk[:, off:off + 2] = r.uniform(1e-3, 1e-2, nblocks).astype(np.float16).view(np.uint8).reshape(nblocks, 2)
     return blk.reshape(-1)
+
+
+KQ_BLOCK = {12: (144, (0, 2)), 13: (176, (0, 2)), 14: (210, (208,))}  # bytes, fp16 field offsets
+
+
+def gen_weights(r: np.random.Generator, n: int, k: int, w_format: int) -> np.ndarray:
+    """A weight matrix [n, k] in nvf_matmul's format: fp32 N(0, 0.05), fp16/bf16 bits of the
+    same, or K-quant superblocks (fp16 fields U[1e-3, 1e-2], other bytes uniform)."""
+    if w_format in (F32, F16, BF16):
+        return to_storage(r.normal(0.0, 0.05, (n, k)).astype(np.float32), w_format)
+    bb, offs = KQ_BLOCK[w_format]
+    return gen_q4_k(r, n * k // 256) if w_format == 12 else gen_raw_blocks(r, n * k // 256, bb, offs)
 
 
 def gen_act(r: np.random.Generator, shape, dt: int, mean: float = 0.0, std: float = 1.0) -> np.ndarray:

@@ -719,3 +719,104 @@ def test_store_kv_is_a_slot_copy(o, dt):
             assert np.array_equal(kc[sl], key[t]) and np.array_equal(vc[sl], val[t])
     untouched = np.setdiff1d(np.arange(rows), slots[slots >= 0])
     assert not kc[untouched].any() and not vc[untouched].any()
+
+
+# ---------------------------------------------------------------------------
+# dense / K-quant weight GEMM (src/hip_ops.hip:43-64, :577-598) and row gather (:611-619)
+# ---------------------------------------------------------------------------
+def _dequant_matrix(o, w, w_format, n, k, layout=H.GGML):
+    """W [n, k] as float64, dense formats by numpy, K-quants block by block through the
+    pinned orc_dequant_*_block functions (a route independent of orc_matmul_w's)."""
+    if w_format == H.F32:
+        return w.reshape(n, k).astype(np.float64)
+    if w_format in (H.F16, H.BF16):
+        return H.from_storage(w.reshape(n, k), w_format).astype(np.float64)
+    bb = H.KQ_BLOCK[w_format][0]
+    flat = np.empty(n * k, np.float32)
+    for b in range(n * k // 256):
+        blk = np.ascontiguousarray(w[b * bb:(b + 1) * bb])
+        y = flat[b * 256:(b + 1) * 256]
+        if w_format == 12:
+            o.orc_dequant_q4k_block(H.ptr(blk), y.ctypes.data, layout)
+        elif w_format == 13:
+            o.orc_dequant_q5k_block(H.ptr(blk), y.ctypes.data)
+        else:
+            o.orc_dequant_q6k_block(H.ptr(blk), y.ctypes.data)
+    return flat.reshape(n, k).astype(np.float64)
+
+
+def _matmul_w(o, x, x_dt, w, w_format, m, n, k, layout=H.GGML):
+    out = np.empty((m, n), np.float64)
+    err = np.empty((m, n), np.float64)
+    o.orc_matmul_w(H.ptr(x), x_dt, H.ptr(w), w_format, layout, m, n, k, H.ptr(out), H.ptr(err))
+    return out, err
+
+
+@pytest.mark.parametrize("w_format", [H.F32, H.F16, H.BF16, 12, 13, 14], ids=["f32", "f16", "bf16", "q4k", "q5k", "q6k"])
+def test_matmul_w_equals_dequantized_matmul(o, w_format):
+    """Against a textbook float64 matmul of the dequantized weight matrix.  Exact when
+    every product and partial sum is exact in fp32 (small integer activations and
+    dense weights that are small multiples of a power of two); within the bound in
+    general (K-quant weights are products of fp16 scales and small integers)."""
+    r = H.rng(40 + w_format)
+    m, n, k = 5, 6, 512
+    x = r.integers(-8, 9, (m, k)).astype(np.float32)
+    if w_format in (H.F32, H.F16, H.BF16):
+        w = H.to_storage((r.integers(-16, 17, (n, k)) * 0.125).astype(np.float32), w_format)
+    else:
+        w = H.gen_weights(r, n, k, w_format)
+    out, err = _matmul_w(o, x, H.F32, w, w_format, m, n, k)
+    expect = x.astype(np.float64) @ _dequant_matrix(o, w, w_format, n, k).T
+    if w_format in (H.F32, H.F16, H.BF16):
+        assert np.array_equal(out, expect)
+    else:
+        assert (np.abs(out - expect) <= 1e-12 * np.abs(expect).max()).all()
+    assert (err >= 0).all()
+
+
+def test_matmul_w_q4k_layout_reaches_the_decoder(o):
+    """The layout argument selects the Q4_K nibble order: the two orders give the
+    products of their own dequantized matrices, and differ."""
+    r = H.rng(47)
+    m, n, k = 3, 4, 256
+    x = r.standard_normal((m, k)).astype(np.float32)
+    w = H.gen_weights(r, n, k, 12)
+    for layout in (H.GGML, H.HIP_LEGACY):
+        out, _ = _matmul_w(o, x, H.F32, w, 12, m, n, k, layout)
+        expect = x.astype(np.float64) @ _dequant_matrix(o, w, 12, n, k, layout).T
+        assert np.allclose(out, expect, rtol=1e-12, atol=1e-12)
+    a, _ = _matmul_w(o, x, H.F32, w, 12, m, n, k, H.GGML)
+    b, _ = _matmul_w(o, x, H.F32, w, 12, m, n, k, H.HIP_LEGACY)
+    assert not np.allclose(a, b)
+
+
+def test_matmul_w_bound_covers_fp32_summation_orders(o):
+    """The stated tolerance holds for fp32 sums of the products in the reference's
+    order (k ascending, fp32 products), reversed, and pairwise, computed in numpy."""
+    r = H.rng(48)
+    m, n, k = 4, 5, 1024                     # a power of two for the pairwise tree
+    x = H.to_storage(r.standard_normal((m, k)).astype(np.float32), H.BF16)
+    w = H.gen_weights(r, n, k, 14)
+    out, err = _matmul_w(o, x, H.BF16, w, 14, m, n, k)
+    xf = H.from_storage(x, H.BF16).astype(np.float32)
+    W = _dequant_matrix(o, w, 14, n, k).astype(np.float32)
+    prods = (xf[:, None, :] * W[None, :, :]).astype(np.float32)       # [m, n, k], fp32 products
+    for order in (np.arange(k), np.arange(k)[::-1]):
+        acc = np.zeros((m, n), np.float32)
+        for i in order:
+            acc = (acc + prods[..., i]).astype(np.float32)
+        assert (np.abs(acc.astype(np.float64) - out) <= err).all()
+    pw = prods.copy()
+    while pw.shape[-1] > 1:
+        pw = (pw[..., 0::2] + pw[..., 1::2]).astype(np.float32)
+    assert (np.abs(pw[..., 0].astype(np.float64) - out) <= err).all()
+
+
+@pytest.mark.parametrize("dt", [H.F32, H.F16, H.BF16], ids=["f32", "f16", "bf16"])
+def test_gather_rows_is_indexing(o, dt):
+    r = H.rng(49 + dt)
+    rows = H.gen_act(r, (11, 40), dt)
+    idx = np.array([3, 0, 10, 3, 7], np.int32)
+    out = np.empty((5, 40), rows.dtype)
+    o.orc_gather_rows(H.ptr(rows), H.ptr(idx), 40, 5, H.ptr(out), dt)
+    assert np.array_equal(out, rows[idx])
