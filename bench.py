@@ -86,7 +86,10 @@ def op_bytes(cfg, e: int, emb_fmt: str) -> dict[str, int]:
             # decode GEMV (m = GEMV_M) at the gate_up shape: the weights once, plus activations and output
             "gemv": int(2 * I * Hd * 34 / 32) + GEMV_M * Hd + 4 * GEMV_M + GEMV_M * 2 * I * e,
             # on-device Q8_0 block split of the gate_up weights: 34 bytes in and 34 out per block
-            "split": 2 * I * Hd // 32 * 68}
+            "split": 2 * I * Hd // 32 * 68,
+            # LM head at decode (m = 1): the [vocab, hidden] weights once (bf16 or Q4_K superblocks), x, fp32 logits
+            "lm_head": cfg.vocab * Hd * 2 + Hd * e + 4 * cfg.vocab,
+            "lm_head_q4k": cfg.vocab * Hd // 256 * 144 + Hd * e + 4 * cfg.vocab}
 
 
 def main() -> int:
@@ -116,7 +119,7 @@ def main() -> int:
     emb_fmt = args.emb or cfg.emb
     nbytes = op_bytes(cfg, e, emb_fmt)
     only = set(filter(None, args.only.split(","))) or {"emb", "rms", "rope", "silu", "copy", "copy12", "copy12_emb",
-                                                       "gemm", "gemv", "split",
+                                                       "gemm", "gemv", "split", "lm_head", "lm_head_q4k",
                                                        "attn", "attn_decode", "attn_f32", "attn_decode_f32", "attn_decode_small", "layer", "layer_decode", "layer_b1", "layer_b1_graph"}
 
     def nsets(b: int) -> int:
@@ -176,6 +179,16 @@ def main() -> int:
                               .view(torch.int16)))
         gemv_out = torch.empty(GEMV_M, 2 * I, dtype=tdt, device=dev)
     split_sets = []
+    lm_sets = {}
+    for n_, wf_ in (("lm_head", ops.W_BF16), ("lm_head_q4k", 12)):
+        if n_ in only:  # one [vocab, hidden] matrix (>= 0.3 GB, beyond the caches), m = 1, fp32 logits
+            if wf_ == 12:
+                blk = torch.randint(0, 256, (V * Hd // 256, 144), generator=g, device=dev, dtype=torch.uint8)
+                blk[:, :4] = torch.tensor([0x1e, 0x1c, 0x1e, 0x1c], dtype=torch.uint8, device=dev)  # d, dmin ~ 4e-3
+                lm_w = blk.reshape(-1)
+            else:
+                lm_w = (torch.randn(V, Hd, generator=g, device=dev) * 0.05).to(torch.bfloat16)
+            lm_sets[n_] = (lm_w, wf_, randn((1, Hd)), torch.empty(1, V, dtype=torch.float32, device=dev))
     if "split" in only:  # gate_up weights as GGUF blocks, rotated like the GEMV's
         nb_split = 2 * I * Hd // 32
         for _ in range(nsets(nbytes["split"])):
@@ -367,6 +380,12 @@ def main() -> int:
         w8_, ws_ = gemv_sets[i % len(gemv_sets)]
         ops.matmul_q8_0(gxq1, gsc1, w8_, ws_, 2 * I, out=gemv_out)
 
+    def run_lm(name):
+        def f(i):
+            w_, wf_, x_, o_ = lm_sets[name]
+            ops.matmul(x_, w_, V, wf_, out_dtype=torch.float32, out=o_)
+        return f
+
     def run_split(i):
         blk_, w8_, ws_ = split_sets[i % len(split_sets)]
         ops._check(ops.lib().nvf_q8_0_split_blocks(blk_.data_ptr(), nb_split, w8_.data_ptr(), ws_.data_ptr(),
@@ -468,7 +487,8 @@ def main() -> int:
     table = [("emb", run_emb), ("rms", run_rms), ("rope", run_rope), ("silu", run_silu), ("emb_rms", run_emb_rms),
              ("rms_q8", run_rms_q8), ("silu_q8", run_silu_q8), ("copy", run_copy),
              ("copy12", run_copy12), ("copy12_emb", run_copy12_emb), ("gemm", run_gemm),
-             ("gemv", run_gemv), ("split", run_split), ("attn", run_attn), ("attn_decode", run_attn_decode),
+             ("gemv", run_gemv), ("split", run_split), ("lm_head", run_lm("lm_head")),
+             ("lm_head_q4k", run_lm("lm_head_q4k")), ("attn", run_attn), ("attn_decode", run_attn_decode),
              ("attn_f32", run_attn_f32), ("attn_decode_f32", run_attn_decode_f32), ("attn_decode_small", run_attn_decode_small),
              ("layer", run_layer), ("layer_decode", run_layer_decode), ("layer_b1", run_layer_b1),
              ("layer_b1_graph", run_layer_b1_graph)]
@@ -526,6 +546,10 @@ def main() -> int:
         if n == "gemv":
             entry.pop("tokens_per_s")
             entry["shape"] = f"m={GEMV_M} n={2 * I} k={Hd} (gate_up, decode)"
+        elif n in ("lm_head", "lm_head_q4k"):
+            entry.pop("tokens_per_s")
+            entry["shape"] = (f"m=1 n={V} k={Hd} (LM head at decode, {'Q4_K' if n == 'lm_head_q4k' else 'bf16'} "
+                              "weights, fp32 logits)")
         elif n == "split":
             entry.pop("tokens_per_s")
             entry["shape"] = f"{2 * I * Hd // 32} Q8_0 blocks (gate_up [{2 * I}, {Hd}])"
@@ -634,6 +658,7 @@ def main() -> int:
         "q8_gemm": res_ops.get("gemm"),
         "q8_gemv": res_ops.get("gemv"),
         "q8_0_split": res_ops.get("split"),
+        "weight_gemv": {k: res_ops[k] for k in ("lm_head", "lm_head_q4k") if k in res_ops} or None,
         "layer": res_ops.get("layer"),
         "layer_decode": res_ops.get("layer_decode"),
         "layer_b1": res_ops.get("layer_b1"),

@@ -245,83 +245,283 @@ __global__ __launch_bounds__(kDgThreads) __attribute__((amdgpu_waves_per_eu(2)))
 }
 
 // ---------------------------------------------------------------------------
-// Decode-shaped products (m <= 16 rows, k % 8 == 0): bound by streaming the
+// 32-element group sources for the decode products: one lane decodes a whole
+// 32-element group of a K-quant superblock per load (e0 % 32 == 0), so the
+// superblock header and the group's scale / min are read and decoded once per 32
+// values instead of once per 8.  Values are bit-identical to Q4K / Q5K / Q6K
+// (weight_formats.hpp): the same formulas on the same bytes.
+template <typename S>
+struct RunOf;  // elements one load of a source yields
+template <typename T>
+struct RunOf<Table<8, T>> {
+  static constexpr int value = 8;
+};
+
+// a & 0x0f0f0f0f kept as one instruction: the byte-wise conversions that follow
+// (v_cvt_f32_ubyte0..3) then take the masked bytes directly, where the compiler
+// would otherwise fold a variable shift and the mask into a bit-field extract per
+// nibble
+__device__ __forceinline__ uint32_t low_nibbles(uint32_t a) {
+  uint32_t r;
+  asm("v_and_b32 %0, 0x0f0f0f0f, %1" : "=v"(r) : "v"(a));
+  return r;
+}
+
+template <int LAYOUT>
+struct Q4KGroup {  // GGML: group j = bytes 32 (j / 2) .. +32, nibble j % 2; HIP_LEGACY: bytes 16 j .. +16, both nibbles
+  const uint8_t* wq;
+  static constexpr int kQ = LAYOUT == NVF_QK_LAYOUT_GGML ? 8 : 4;
+  struct Raw {
+    u32x4 hdr;
+    uint32_t q[kQ];
+    int j;
+  };
+  __device__ __forceinline__ Raw load(int64_t e0) const {
+    const uint8_t* blk = wq + (e0 >> 8) * 144;
+    Raw r;
+    r.j = (int)((e0 & 255) >> 5);
+    r.hdr = ld16(blk);
+    if constexpr (LAYOUT == NVF_QK_LAYOUT_GGML) {
+      const u32x4 a = ld16(blk + 16 + 32 * (r.j >> 1)), b = ld16(blk + 32 + 32 * (r.j >> 1));
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        r.q[i] = a[i];
+        r.q[4 + i] = b[i];
+      }
+    } else {
+      const u32x4 a = ld16(blk + 16 + 16 * r.j);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) r.q[i] = a[i];
+    }
+    return r;
+  }
+  __device__ __forceinline__ void decode(const Raw& r, float* v) const {
+    uint32_t sc, mn;
+    q4k_sm(r.hdr[1], r.hdr[2], r.hdr[3], r.j, sc, mn);
+    const float s = half_bits_to_f32(r.hdr[0] & 0xffffu) * (float)sc;
+    const float m = half_bits_to_f32(r.hdr[0] >> 16) * (float)mn;
+    if constexpr (LAYOUT == NVF_QK_LAYOUT_GGML) {
+      const int sh = (r.j & 1) * 4;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const uint32_t w = low_nibbles(r.q[i] >> sh);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) v[4 * i + k] = s * (float)byte_of(w, k) - m;
+      }
+    } else {
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const uint32_t w = (r.q[i] >> (4 * h)) & 0x0f0f0f0fu;
+#pragma unroll
+          for (int k = 0; k < 4; ++k) v[16 * h + 4 * i + k] = s * (float)byte_of(w, k) - m;
+        }
+    }
+  }
+};
+
+struct Q5KGroup {  // group j = 2 g + s: low bits nibble s of ql[32 g .. +32], bit 4 = bit j of qh[0 .. 32]
+  const uint8_t* wq;
+  struct Raw {
+    u32x4 hdr;
+    uint32_t ql[8], qh[8];
+    int j;
+  };
+  __device__ __forceinline__ Raw load(int64_t e0) const {
+    const uint8_t* blk = wq + (e0 >> 8) * 176;
+    Raw r;
+    r.j = (int)((e0 & 255) >> 5);
+    r.hdr = ld16(blk);
+    const u32x4 a = ld16(blk + 48 + 32 * (r.j >> 1)), b = ld16(blk + 64 + 32 * (r.j >> 1));
+    const u32x4 c = ld16(blk + 16), d = ld16(blk + 32);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      r.ql[i] = a[i];
+      r.ql[4 + i] = b[i];
+      r.qh[i] = c[i];
+      r.qh[4 + i] = d[i];
+    }
+    return r;
+  }
+  __device__ __forceinline__ void decode(const Raw& r, float* v) const {
+    uint32_t sc, mn;
+    q4k_sm(r.hdr[1], r.hdr[2], r.hdr[3], r.j, sc, mn);
+    const float s = half_bits_to_f32(r.hdr[0] & 0xffffu) * (float)sc;
+    const float m = half_bits_to_f32(r.hdr[0] >> 16) * (float)mn;
+    const int sh = (r.j & 1) * 4;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const uint32_t w = low_nibbles(r.ql[i] >> sh) | (((r.qh[i] >> r.j) & 0x01010101u) << 4);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) v[4 * i + k] = s * (float)byte_of(w, k) - m;
+    }
+  }
+};
+
+struct Q6KGroup {  // elements 128 h + 32 s + l: ql[64 h + 32 (s & 1) + l] nibble s / 2, qh[32 h + l] bits 2 s;
+                   // scales sc[8 h + 2 s + l / 16]; 2-byte aligned superblocks
+  const uint8_t* wq;
+  struct Raw {
+    uint32_t ql[8], qh[8];
+    uint32_t sd;  // two int8 scales | fp16 d << 16
+    int slot;
+  };
+  __device__ __forceinline__ Raw load(int64_t e0) const {
+    const uint8_t* blk = wq + (e0 >> 8) * 210;
+    Raw r;
+    const int i = (int)(e0 & 255), h = i >> 7;
+    r.slot = (i & 127) >> 5;
+    load_a2<32>(blk + 64 * h + 32 * (r.slot & 1), r.ql);
+    load_a2<32>(blk + 128 + 32 * h, r.qh);
+    r.sd = (uint32_t)*reinterpret_cast<const uint16_t*>(blk + 192 + 8 * h + 2 * r.slot) |
+           ((uint32_t)*reinterpret_cast<const uint16_t*>(blk + 208) << 16);
+    return r;
+  }
+  __device__ __forceinline__ void decode(const Raw& r, float* v) const {
+    const int lsh = (r.slot >> 1) * 4, hsh = 2 * r.slot;
+    const float d = half_bits_to_f32(r.sd >> 16);
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+      const float ds = d * (float)(int8_t)((r.sd >> (8 * half)) & 0xffu);  // (d * sc) first, as the reference
+#pragma unroll
+      for (int i = 4 * half; i < 4 * half + 4; ++i)
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const int q = (int)(((byte_of(r.ql[i], k) >> lsh) & 0xfu) | (((byte_of(r.qh[i], k) >> hsh) & 3u) << 4));
+          v[4 * i + k] = ds * (float)(q - 32);
+        }
+    }
+  }
+};
+
+template <int L>
+struct RunOf<Q4KGroup<L>> {
+  static constexpr int value = 32;
+};
+template <>
+struct RunOf<Q5KGroup> {
+  static constexpr int value = 32;
+};
+template <>
+struct RunOf<Q6KGroup> {
+  static constexpr int value = 32;
+};
+
+// ---------------------------------------------------------------------------
+// Decode-shaped products (m <= 16 rows, k a multiple of the run below): bound by streaming the
 // weights once from HBM.  Every fp32 matrix-core shape consumes at most 64 weight
 // elements per 32 cycles per SIMD (8 per clock per CU), below what HBM delivers
 // for K-quant weights (~23 elements per clock per CU for Q4_K), so the smallest
 // batches use plain FMAs.  The 4 waves of a workgroup split K (contiguous ranges
 // of steps) and meet in LDS, summed in wave order.  The activations are read from
-// global memory (L2-resident: every workgroup reads the same m rows).
+// global memory (L2-resident: every workgroup reads the same m rows).  A lane
+// takes runs of R = 8 consecutive weights (dense rows) or R = 32 (one K-quant
+// group: header and scale decoded once per run).
 //
-// m <= 2 (dense_gemv_fma_kernel): lane l = 4 b + j streams 8 consecutive weights
-// of column j of each of its C column quads at k offset 8 b (16 lanes read 128
-// contiguous k of one column per step) with the same 8 k of each of the m rows,
-// and accumulates m x C fp32 sums; the 16 lanes of a column are summed at the end.
+// m <= 2 (dense_gemv_fma_kernel): LPC = 16 (dense) or 8 (K-quants) lanes per
+// column; lane l = CPS b + j (CPS = 64 / LPC columns per set) streams run b of
+// column j of each of its C column sets (LPC runs: 128 or 256 contiguous k of one
+// column per step) with the same k of each of the m rows, accumulating m x C fp32
+// sums; the LPC lanes of a column are summed at the end.
 //
 // 2 < m <= 16 (dense_gemv_mfma_kernel): v_mfma_f32_16x16x4_f32, lane l = 16 s + j
 // giving activation row j and weight column j at k slot s.  Lane l streams 16
-// consecutive k (two 8-runs) at offset 16 s of column j of each of C 16-column
-// groups (64 contiguous k per column per step); run h, value i is MFMA step
-// 8 h + i with k slot s <-> k = 16 s + 8 h + i.  The matrix core sums the k slots,
-// so only the waves are summed at the end.
+// (dense: two runs of 8) or 32 consecutive k at offset (16 or 32) s of column j of
+// each of C 16-column groups; value i of the lane's span is MFMA step i, with
+// k slot s <-> k = span s + i.  The matrix core sums the k slots, so only the
+// waves are summed at the end.
 constexpr int kGvWaves = 4;
 constexpr int kGemvRows = 16;
 
-template <typename TX, typename Src, int MR, int C, typename TO>
+template <typename TX, int R>
+__device__ __forceinline__ void load_x_run(const Table<8, TX>& xs, int64_t e0, typename Table<8, TX>::Raw* xr) {
+#pragma unroll
+  for (int u = 0; u < R / 8; ++u) xr[u] = xs.load(e0 + 8 * u);
+}
+template <typename TX, int R>
+__device__ __forceinline__ void decode_x_run(const Table<8, TX>& xs, const typename Table<8, TX>::Raw* xr, float* v) {
+#pragma unroll
+  for (int u = 0; u < R / 8; ++u) xs.decode(xr[u], v + 8 * u);
+}
+
+template <typename TX, typename Src, int MR, int C, int S, typename TO>
 __global__ __launch_bounds__(kGvWaves * 64) void dense_gemv_fma_kernel(const TX* __restrict__ x, Src w,
                                                                        TO* __restrict__ out, int64_t m, int64_t n,
                                                                        int64_t k) {
-  __shared__ float part[kGvWaves][MR][C][4];  // [wave][row][quad][column]
-  const int lane = threadIdx.x & 63, j = lane & 3, b = lane >> 2;
+  constexpr int R = RunOf<Src>::value, LPC = R == 8 ? 16 : 8, CPS = 64 / LPC, KS = LPC * R;
+  constexpr int G = kGvWaves / S;               // column groups per workgroup (S waves split K in each)
+  __shared__ float part[kGvWaves][MR][C][CPS];  // [wave][row][set][column]
+  const int lane = threadIdx.x & 63, j = lane % CPS, b = lane / CPS;
   const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
-  const int64_t c0 = (int64_t)blockIdx.x * 4 * C;
-  const int64_t nsteps = (k + 127) / 128;
-  const int64_t s_begin = nsteps * wave / kGvWaves, s_end = nsteps * (wave + 1) / kGvWaves;
+  const int grp = wave / S, split = wave % S;
+  const int64_t c0 = ((int64_t)blockIdx.x * G + grp) * CPS * C;
+  const int64_t nsteps = (k + KS - 1) / KS, full = k / KS;  // steps; steps every lane's run is inside
+  const int64_t s_begin = nsteps * split / S, s_end = nsteps * (split + 1) / S;
+  const int64_t f_end = s_end < full ? s_end : full;
   const Table<8, TX> xs{x};
+  // columns past n read column n - 1 (their sums are never stored): no per-lane
+  // branches in the loop
+  int64_t wrow[C];
+#pragma unroll
+  for (int q = 0; q < C; ++q) {
+    const int64_t c = c0 + CPS * q + j;
+    wrow[q] = (c < n ? c : n - 1) * k + (int64_t)R * b;
+  }
+  const int64_t xrow = (int64_t)R * b;
   float acc[MR][C];
 #pragma unroll
   for (int r = 0; r < MR; ++r)
 #pragma unroll
     for (int q = 0; q < C; ++q) acc[r][q] = 0.0f;
-  bool col_ok[C];
-#pragma unroll
-  for (int q = 0; q < C; ++q) col_ok[q] = c0 + 4 * q + j < n;
 
-  for (int64_t s = s_begin; s < s_end; ++s) {
-    const int64_t kk = s * 128 + 8 * b;  // this lane's 8 k (k % 8 == 0: all or none are inside)
-    if (kk >= k) continue;
-    typename Src::Raw wr[C];
-    typename Table<8, TX>::Raw xr[MR];
+  struct Buf {
+    typename Src::Raw w[C];
+    typename Table<8, TX>::Raw x[MR][R / 8];
+  };
+  auto load = [&](Buf& f, int64_t st) {
+    const int64_t kk = st * KS;
 #pragma unroll
-    for (int q = 0; q < C; ++q)
-      if (col_ok[q]) wr[q] = w.load((c0 + 4 * q + j) * k + kk);
+    for (int q = 0; q < C; ++q) f.w[q] = w.load(wrow[q] + kk);
 #pragma unroll
-    for (int r = 0; r < MR; ++r)
-      if (r < m) xr[r] = xs.load((int64_t)r * k + kk);
-    float xv[MR][8];
+    for (int r = 0; r < MR; ++r) load_x_run<TX, R>(xs, (int64_t)r * k + xrow + kk, f.x[r]);
+  };
+  auto compute = [&](const Buf& f) {
+    float xv[MR][R];
 #pragma unroll
-    for (int r = 0; r < MR; ++r) {
-      if (r < m) {
-        xs.decode(xr[r], xv[r]);
-      } else {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) xv[r][i] = 0.0f;
-      }
-    }
+    for (int r = 0; r < MR; ++r) decode_x_run<TX, R>(xs, f.x[r], xv[r]);
 #pragma unroll
     for (int q = 0; q < C; ++q) {
-      float wv[8];
-      if (col_ok[q]) {
-        w.decode(wr[q], wv);
-      } else {
+      float wv[R];
+      w.decode(f.w[q], wv);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) wv[i] = 0.0f;
-      }
-#pragma unroll
-      for (int i = 0; i < 8; ++i)
+      for (int i = 0; i < R; ++i)
 #pragma unroll
         for (int r = 0; r < MR; ++r) acc[r][q] = __builtin_fmaf(xv[r][i], wv[i], acc[r][q]);
     }
+  };
+  // full steps, two raw buffers in turn: the next step's loads are in flight
+  // while the current one is decoded.  The prefetch is unconditional (the last
+  // step reloads itself), so the memory counter waits stay exact: a load that
+  // may or may not have been issued makes the compiler wait for all of them.
+  Buf fa, fb;
+  int64_t st = s_begin;
+  if (st < f_end) {
+    const int64_t last = f_end - 1;
+    load(fa, st);
+    while (true) {
+      load(fb, st + 1 < last ? st + 1 : last);
+      compute(fa);
+      if (++st >= f_end) break;
+      load(fa, st + 1 < last ? st + 1 : last);
+      compute(fb);
+      if (++st >= f_end) break;
+    }
+  }
+  // the last, partial step (k not a multiple of the step): lanes past k add nothing
+  if (f_end < s_end && xrow + f_end * KS < k) {
+    load(fa, f_end);
+    compute(fa);
   }
 
 #pragma unroll
@@ -330,17 +530,17 @@ __global__ __launch_bounds__(kGvWaves * 64) void dense_gemv_fma_kernel(const TX*
     for (int q = 0; q < C; ++q) {
       float v = acc[r][q];
 #pragma unroll
-      for (int d = 0; d < 4; ++d) v += __shfl_xor(v, 4 << d, 64);
-      if (lane < 4) part[wave][r][q][j] = v;
+      for (int d = CPS; d < 64; d *= 2) v += __shfl_xor(v, d, 64);
+      if (lane < CPS) part[wave][r][q][j] = v;
     }
   __syncthreads();
-  for (int t = (int)threadIdx.x; t < MR * C * 4; t += kGvWaves * 64) {
-    const int jj = t & 3, q = (t >> 2) % C, r = (t >> 2) / C;
-    const int64_t col = c0 + 4 * q + jj;
+  for (int t = (int)threadIdx.x; t < G * MR * C * CPS; t += kGvWaves * 64) {
+    const int jj = t % CPS, q = (t / CPS) % C, r = (t / (CPS * C)) % MR, g = t / (CPS * C * MR);
+    const int64_t col = ((int64_t)blockIdx.x * G + g) * CPS * C + CPS * q + jj;
     if (r >= m || col >= n) continue;
-    float v = part[0][r][q][jj];
+    float v = part[g * S][r][q][jj];
 #pragma unroll
-    for (int wv = 1; wv < kGvWaves; ++wv) v += part[wv][r][q][jj];
+    for (int wv = 1; wv < S; ++wv) v += part[g * S + wv][r][q][jj];
     out[(int64_t)r * n + col] = from_f32<TO>(v);
   }
 }
@@ -349,11 +549,12 @@ template <typename TX, typename Src, int C, typename TO>
 __global__ __launch_bounds__(kGvWaves * 64) void dense_gemv_mfma_kernel(const TX* __restrict__ x, Src w,
                                                                         TO* __restrict__ out, int64_t m, int64_t n,
                                                                         int64_t k) {
+  constexpr int R = RunOf<Src>::value, H = R == 8 ? 2 : 1, SPAN = H * R, KS = 4 * SPAN;
   __shared__ float part[kGvWaves][C][16][17];  // [wave][group][row][column] (padded)
   const int lane = threadIdx.x & 63, j = lane & 15, ks = lane >> 4;
   const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   const int64_t c0 = (int64_t)blockIdx.x * 16 * C;
-  const int64_t nsteps = (k + 63) / 64;
+  const int64_t nsteps = (k + KS - 1) / KS;
   const int64_t s_begin = nsteps * wave / kGvWaves, s_end = nsteps * (wave + 1) / kGvWaves;
   const Table<8, TX> xs{x};
   const bool row_ok = j < m;
@@ -365,38 +566,38 @@ __global__ __launch_bounds__(kGvWaves * 64) void dense_gemv_mfma_kernel(const TX
   for (int q = 0; q < C; ++q) acc[q] = f32x4{};
 
   for (int64_t s = s_begin; s < s_end; ++s) {
-    const int64_t kk = s * 64 + 16 * ks;
-    typename Src::Raw wr[C][2];
-    typename Table<8, TX>::Raw xr[2];
-    bool h_ok[2];
+    const int64_t kk = s * KS + (int64_t)SPAN * ks;
+    typename Src::Raw wr[C][H];
+    typename Table<8, TX>::Raw xr[H][R / 8];
+    bool h_ok[H];
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      h_ok[h] = kk + 8 * h < k;
+    for (int h = 0; h < H; ++h) {
+      h_ok[h] = kk + R * h < k;
 #pragma unroll
       for (int q = 0; q < C; ++q)
-        if (h_ok[h] && col_ok[q]) wr[q][h] = w.load((c0 + 16 * q + j) * k + kk + 8 * h);
-      if (h_ok[h] && row_ok) xr[h] = xs.load((int64_t)j * k + kk + 8 * h);
+        if (h_ok[h] && col_ok[q]) wr[q][h] = w.load((c0 + 16 * q + j) * k + kk + R * h);
+      if (h_ok[h] && row_ok) load_x_run<TX, R>(xs, (int64_t)j * k + kk + R * h, xr[h]);
     }
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      float xv[8];
+    for (int h = 0; h < H; ++h) {
+      float xv[R];
       if (h_ok[h] && row_ok) {
-        xs.decode(xr[h], xv);
+        decode_x_run<TX, R>(xs, xr[h], xv);
       } else {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) xv[i] = 0.0f;
+        for (int i = 0; i < R; ++i) xv[i] = 0.0f;
       }
 #pragma unroll
       for (int q = 0; q < C; ++q) {
-        float wv[8];
+        float wv[R];
         if (h_ok[h] && col_ok[q]) {
           w.decode(wr[q][h], wv);
         } else {
 #pragma unroll
-          for (int i = 0; i < 8; ++i) wv[i] = 0.0f;
+          for (int i = 0; i < R; ++i) wv[i] = 0.0f;
         }
 #pragma unroll
-        for (int i = 0; i < 8; ++i) acc[q] = __builtin_amdgcn_mfma_f32_16x16x4f32(xv[i], wv[i], acc[q], 0, 0, 0);
+        for (int i = 0; i < R; ++i) acc[q] = __builtin_amdgcn_mfma_f32_16x16x4f32(xv[i], wv[i], acc[q], 0, 0, 0);
       }
     }
   }
@@ -418,29 +619,65 @@ __global__ __launch_bounds__(kGvWaves * 64) void dense_gemv_mfma_kernel(const TX
   }
 }
 
-// Column quads / groups per wave: 4 when that leaves >= ~1000 workgroups, fewer
-// for narrow outputs.
+// Column sets / groups per wave: 4 (dense) or 2 (K-quants, larger runs) when that
+// leaves >= ~1000 workgroups, fewer for narrow outputs.
 template <typename TX, typename Src, int MR, typename TO>
 int launch_gemv_fma(const TX* x, const Src& src, TO* out, int64_t m, int64_t n, int64_t k, hipStream_t st) {
-  if (n >= 16 * 1024)
-    dense_gemv_fma_kernel<TX, Src, MR, 4, TO><<<dim3((unsigned)((n + 15) / 16)), kGvWaves * 64, 0, st>>>(x, src, out, m, n, k);
-  else if (n >= 8 * 1024)
-    dense_gemv_fma_kernel<TX, Src, MR, 2, TO><<<dim3((unsigned)((n + 7) / 8)), kGvWaves * 64, 0, st>>>(x, src, out, m, n, k);
+  constexpr int CPS = RunOf<Src>::value == 8 ? 4 : 8;
+  constexpr int CMAX = RunOf<Src>::value == 8 ? 4 : 2;
+  const dim3 blk(kGvWaves * 64);
+  auto grid = [&](int cols) { return dim3((unsigned)((n + cols - 1) / cols)); };
+  // wide outputs: each wave walks the whole K of its own columns (S = 1); narrow
+  // ones split K over the 4 waves to fill the GPU
+  if (n >= (int64_t)CPS * CMAX * kGvWaves * 1024)
+    dense_gemv_fma_kernel<TX, Src, MR, CMAX, 1, TO><<<grid(CPS * CMAX * kGvWaves), blk, 0, st>>>(x, src, out, m, n, k);
+  else if (n >= (int64_t)CPS * CMAX * 1024)
+    dense_gemv_fma_kernel<TX, Src, MR, CMAX, 4, TO><<<grid(CPS * CMAX), blk, 0, st>>>(x, src, out, m, n, k);
   else
-    dense_gemv_fma_kernel<TX, Src, MR, 1, TO><<<dim3((unsigned)((n + 3) / 4)), kGvWaves * 64, 0, st>>>(x, src, out, m, n, k);
+    dense_gemv_fma_kernel<TX, Src, MR, 1, 4, TO><<<grid(CPS), blk, 0, st>>>(x, src, out, m, n, k);
   return launch_status("dense_gemv_fma");
 }
 
 template <typename TX, typename Src, typename TO>
 int launch_gemv_mfma(const TX* x, const Src& src, TO* out, int64_t m, int64_t n, int64_t k, hipStream_t st) {
+  const dim3 blk(kGvWaves * 64);
   if (n >= 64 * 1024)
-    dense_gemv_mfma_kernel<TX, Src, 4, TO><<<dim3((unsigned)((n + 63) / 64)), kGvWaves * 64, 0, st>>>(x, src, out, m, n, k);
+    dense_gemv_mfma_kernel<TX, Src, 4, TO><<<dim3((unsigned)((n + 63) / 64)), blk, 0, st>>>(x, src, out, m, n, k);
   else if (n >= 32 * 1024)
-    dense_gemv_mfma_kernel<TX, Src, 2, TO><<<dim3((unsigned)((n + 31) / 32)), kGvWaves * 64, 0, st>>>(x, src, out, m, n, k);
+    dense_gemv_mfma_kernel<TX, Src, 2, TO><<<dim3((unsigned)((n + 31) / 32)), blk, 0, st>>>(x, src, out, m, n, k);
   else
-    dense_gemv_mfma_kernel<TX, Src, 1, TO><<<dim3((unsigned)((n + 15) / 16)), kGvWaves * 64, 0, st>>>(x, src, out, m, n, k);
+    dense_gemv_mfma_kernel<TX, Src, 1, TO><<<dim3((unsigned)((n + 15) / 16)), blk, 0, st>>>(x, src, out, m, n, k);
   return launch_status("dense_gemv_mfma");
 }
+
+// The decode product for a weight format: dense rows by 8-element runs, K-quants
+// by 32-element groups.
+template <typename TX, typename G, typename TO>
+int launch_gemv(const TX* x, const G& src, TO* out, int64_t m, int64_t n, int64_t k, hipStream_t st) {
+  if (m == 1) return launch_gemv_fma<TX, G, 1, TO>(x, src, out, m, n, k, st);
+  if (m == 2) return launch_gemv_fma<TX, G, 2, TO>(x, src, out, m, n, k, st);
+  return launch_gemv_mfma<TX, G, TO>(x, src, out, m, n, k, st);
+}
+template <typename S>
+struct GemvSource {  // dense rows: the gather source itself
+  using type = S;
+  static type make(const S& s) { return s; }
+};
+template <int L>
+struct GemvSource<Q4K<8, L>> {
+  using type = Q4KGroup<L>;
+  static type make(const Q4K<8, L>& s) { return type{s.wq}; }
+};
+template <>
+struct GemvSource<Q5K<8>> {
+  using type = Q5KGroup;
+  static type make(const Q5K<8>& s) { return type{s.wq}; }
+};
+template <>
+struct GemvSource<Q6K<8>> {
+  using type = Q6KGroup;
+  static type make(const Q6K<8>& s) { return type{s.wq}; }
+};
 
 template <typename TX, typename Src, typename TO>
 int launch_dense(const void* x, const Src& src, void* out, int64_t m, int64_t n, int64_t k, bool vec,
@@ -448,11 +685,9 @@ int launch_dense(const void* x, const Src& src, void* out, int64_t m, int64_t n,
   const int tiles_n = (int)((n + kDgBN - 1) / kDgBN);
   const TX* xp = static_cast<const TX*>(x);
   TO* op = static_cast<TO*>(out);
-  if (vec && m <= kGemvRows && k % 8 == 0) {
-    if (m == 1) return launch_gemv_fma<TX, Src, 1, TO>(xp, src, op, m, n, k, st);
-    if (m == 2) return launch_gemv_fma<TX, Src, 2, TO>(xp, src, op, m, n, k, st);
-    return launch_gemv_mfma<TX, Src, TO>(xp, src, op, m, n, k, st);
-  }
+  // decode product: whole runs per row (8 elements for dense rows, a 32-element group for K-quants)
+  if (vec && m <= kGemvRows && k % RunOf<typename GemvSource<Src>::type>::value == 0)
+    return launch_gemv<TX>(xp, GemvSource<Src>::make(src), op, m, n, k, st);
   const bool ragged = !vec || k % kDgKC != 0;
   if (m <= 32) {
     const dim3 g((unsigned)tiles_n);

@@ -15,7 +15,10 @@ from tests import harness as H
 def test_op_bytes_all_formats(fmt):
     cfg = H.CONFIGS[2]
     b = bench.op_bytes(cfg, 2, fmt)
-    assert set(b) == {"emb", "rms", "rope", "silu", "emb_rms", "rms_q8", "silu_q8", "gemv", "split"}
+    assert set(b) == {"emb", "rms", "rope", "silu", "emb_rms", "rms_q8", "silu_q8", "gemv", "split", "lm_head",
+                      "lm_head_q4k"}
+    # the decode LM head streams the [vocab, hidden] weights once: 2 bytes (bf16) or 144 per 256 (Q4_K)
+    assert b["lm_head"] - b["lm_head_q4k"] == cfg.vocab * cfg.hidden * 2 - cfg.vocab * cfg.hidden // 256 * 144
     # the fused SwiGLU reads gate_up once and writes one int8 row and a scale per token
     assert b["silu_q8"] == 2 * cfg.tokens * cfg.inter * 2 + cfg.tokens * cfg.inter + 4 * cfg.tokens
     # the residual-add + RMSNorm moves x, residual in/out and out: 4 rows of fp16
