@@ -113,12 +113,31 @@ void hip_matmul_u16(const float* x, const uint16_t* w, int m, int n, int k, floa
 
 /* hip_ops.hpp:11 -- as hip_matmul with K-quant weights (kind 12/13/14: Q4_K/Q5_K/Q6_K
  * superblocks over the flat [n][k] element index), decoded exactly.  Q4_K nibble order
- * as hip_embedding_qk (nvf_set_dropin_q4k_layout).  Needs k % 16 == 0. */
+ * as hip_embedding_qk (nvf_set_dropin_q4k_layout).  Needs n*k a multiple of 256. */
 void hip_matmul_qk(const float* x, const uint8_t* wq, int m, int n, int k, float* out, int kind);
 
 /* hip_ops.hpp:34 -- out[r,:] = rows[indices[r],:] for r < out_rows (the last-token rows
  * ahead of the LM head, src/model.cpp:839); rows_count is unused, as in the reference. */
 void hip_gather_rows(const float* rows, const int32_t* indices, int rows_count, int cols, int out_rows, float* out);
+
+/* hip_ops.hpp:37 -- top-K experts per row of fp32 router logits [rows, E]: softmax in
+ * double, the reference's selection sort (its tie order), optional renormalisation of the
+ * K scores; idx [rows, K] int32, score [rows, K] fp32.  E <= 4096. */
+void hip_moe_route(const float* logits, int rows, int E, int K, bool norm, int32_t* idx, float* score);
+
+/* hip_ops.hpp:38-40 -- out[t] += sum_k score[t,k] * down(silu(gate(x[t])) * up(x[t])) for the
+ * expert slot slot_of[idx[t,k]] (gu slot [2I, H] gate rows then up rows, dn slot [H, I],
+ * fp16 or bf16), pairs with score 0 skipped.  Expert slots below 65536; a pair whose slot
+ * is negative or beyond is skipped (the reference would read outside its slot arrays).
+ * Runs through a static 64 MiB device scratch in row chunks: allocates nothing. */
+void hip_moe_ffn(const float* x, const int32_t* idx, const float* score, const uint16_t* gu, const uint16_t* dn,
+                 const int32_t* slot_of, int rows, int H, int I, int K, bool bf16, float* out);
+
+/* hip_ops.hpp:41 -- dst[i] += src[i], fp32. */
+void hip_add_inplace(float* dst, const float* src, size_t n);
+
+/* hip_ops.hpp:42 -- dst[t, c] *= 1 / (1 + expf(-s[t])), fp32 (Qwen2-MoE shared-expert gate). */
+void hip_scale_rows_sigmoid(float* dst, const float* s, int rows, int cols);
 
 /* No reference counterpart: selects the Q4_K nibble order hip_embedding_qk reads,
  * process-wide (NVF_QK_LAYOUT_GGML, the default, or NVF_QK_LAYOUT_HIP_LEGACY). */
@@ -216,8 +235,9 @@ int nvf_add_bias(void* x, const float* bias, int64_t rows, int64_t cols, int64_t
 /* GEMM on dense or K-quant weights (replaces hip_matmul, hip_matmul_u16 and
  * hip_matmul_qk, hip_ops.hpp:8-11): out[m,n] (out_dtype) = x[m,k] (x_dtype) . w^T with
  * w in `w_format` (nvf_w_format; Q4_K nibble order `qk_layout`) decoded exactly to fp32,
- * fp32 products and sums on the matrix cores.  k % 16 == 0; K-quants: n*k a multiple of
- * 256.  x and dense weights 16-byte aligned; Q4_K/Q5_K blocks 16-byte, Q6_K 2-byte. */
+ * fp32 products and sums on the matrix cores.  Any k; K-quants: n*k a multiple of 256,
+ * Q4_K/Q5_K blocks 16-byte aligned, Q6_K 2-byte.  Vector loads when x and dense
+ * weights are 16-byte aligned, element-wise staging otherwise. */
 int nvf_matmul(const void* x, int x_dtype, const void* w, int w_format, int qk_layout, int64_t m, int64_t n,
                int64_t k, void* out, int out_dtype, void* stream);
 
@@ -227,6 +247,28 @@ int nvf_matmul(const void* x, int x_dtype, const void* w, int w_format, int qk_l
  * read; rows_count <= 0: indices are trusted, as the reference does. */
 int nvf_gather_rows(const void* rows, const int32_t* indices, int64_t rows_count, int64_t cols, int64_t out_rows,
                     void* out, int dtype, void* stream);
+
+/* MoE routing (replaces hip_moe_route, hip_ops.hpp:37) on `stream`; E <= 4096, K <= E. */
+int nvf_moe_route(const float* logits, int64_t rows, int64_t E, int64_t K, int norm, int32_t* idx, float* score,
+                  void* stream);
+
+/* Workspace bytes nvf_moe_ffn_ws needs for rows x K (token, expert) pairs. */
+int64_t nvf_moe_ffn_workspace_size(int64_t rows, int64_t H, int64_t I, int64_t K, int64_t slots);
+
+/* MoE expert FFN (replaces hip_moe_ffn, hip_ops.hpp:38-40): x [rows, H] in x_dtype, out
+ * [rows, H] in out_dtype (out += ...), expert weights fp16 (w_bf16 0) or bf16, expert slots
+ * in [0, slots) (slots <= 65536; other pairs and pairs with score 0 are skipped).  The pairs
+ * are grouped by slot and run as matrix products on the fp32 matrix cores; the k results of
+ * a token are summed in k order.  `work`: 16-byte aligned, nvf_moe_ffn_workspace_size bytes. */
+int nvf_moe_ffn_ws(const void* x, int x_dtype, const int32_t* idx, const float* score, const void* gu,
+                   const void* dn, int w_bf16, const int32_t* slot_of, int64_t rows, int64_t H, int64_t I, int64_t K,
+                   int64_t slots, void* out, int out_dtype, void* work, int64_t work_bytes, void* stream);
+
+/* dst[i] += src[i] (replaces hip_add_inplace, hip_ops.hpp:41), fp32, on `stream`. */
+int nvf_add_inplace(float* dst, const float* src, int64_t n, void* stream);
+
+/* dst[t, c] *= 1 / (1 + expf(-s[t])) (replaces hip_scale_rows_sigmoid, hip_ops.hpp:42). */
+int nvf_scale_rows_sigmoid(float* dst, const float* s, int64_t rows, int64_t cols, void* stream);
 
 /* Q8_0 gather, split planes (as hip_embedding_q8) -> out in out_dtype.
  * vocab > 0: ids outside [0, vocab) produce a NaN row instead of a read;

@@ -10,239 +10,17 @@
 // fp32 sums in k order; weights w(c, i) = element c*k + i of the flat weight array
 // (row-major [n][k]; K-quant superblocks cover 256 consecutive elements).
 //
-// Design for gfx950: v_mfma_f32_32x32x2_f32 (fp32 products and sums, 157 TFLOP/s
-// dense).  A 256-thread workgroup owns a BM x 128 output tile: BM = 128 as 2 x 2
-// waves of 64 x 64, or BM = 32 (m <= 32: decode batches) as 1 x 4 waves of 32 x 32,
-// so a small m does not multiply the matrix-core work.  K moves in 16-element
-// stages through LDS, double-buffered, with the next stage's loads in flight
-// during the current stage's MFMAs:
-//   * activation rows, upconverted to fp32 (8 elements per thread);
-//   * weight rows, decoded to fp32 by the same element sources as the embedding
-//     gathers (weight_formats.hpp; 8 elements per thread, bit-exact values);
-//   * LDS rows padded to 20 floats, so the 16 lanes of a ds_read_b128 phase hit
-//     16 distinct 4-bank groups.
-// Inside a stage the k order is permuted (the dot product does not care): MFMA
-// step s contracts k = s on lanes 0-31 and k = 8 + s on lanes 32-63 for both
-// operands, so each lane reads its 8 values of a row as two 16-byte LDS reads.
-// The sums are fp32 in a different order from the reference's, so results agree
-// within the recursive-summation bound the tests state.
-//
-// A k that is not a multiple of 16 (the reference takes any k) runs the RAGGED
-// variant: the same tiles and MFMAs, but every staged value is read on its own,
-// k beyond the row's end staged as zero, weights decoded through 4-element aligned
-// runs of the same sources (rows no longer start on 8-element boundaries).
+// Design for gfx950: the fp32 matrix-core tile kernel of gemm_tile.hpp for m > 16
+// (m <= 32 takes 32-row tiles, so a small m does not multiply the matrix-core work),
+// and the weight-streaming decode products below for m <= 16.  The sums are fp32
+// in a different order from the reference's, so results agree within the
+// recursive-summation bound the tests state.
 
 #include "nvf_device.hpp"
 #include "nvf_host.hpp"
-#include "weight_formats.hpp"
+#include "gemm_tile.hpp"
 
 namespace nvf {
-
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-typedef float f32x16 __attribute__((ext_vector_type(16)));
-
-constexpr int kDgBN = 128;           // output columns per workgroup
-constexpr int kDgKC = 16;            // k elements per LDS stage
-constexpr int kDgRow = kDgKC + 4;    // LDS floats per staged row (padded)
-constexpr int kDgThreads = 256;
-constexpr int kDgXcds = 8;
-
-template <int BM>
-constexpr int dg_stage_floats() {
-  return (BM + kDgBN) * kDgRow;
-}
-
-// Workgroup -> output tile, XCD-aware: workgroups are dealt to the 8 XCDs
-// round-robin, and each XCD takes a contiguous range of an order that walks 8
-// tile rows at a time column by column, so its resident workgroups share weight
-// and activation panels in its L2.
-__device__ __forceinline__ void dg_tile(int tiles_n, int64_t& tm, int64_t& tn) {
-  const int tiles = (int)gridDim.x;
-  const int tiles_m = tiles / tiles_n;
-  const int xcd = (int)blockIdx.x % kDgXcds, local = (int)blockIdx.x / kDgXcds;
-  const int per = tiles / kDgXcds, extra = tiles % kDgXcds;
-  const int id = xcd * per + (xcd < extra ? xcd : extra) + local;
-  const int gsz = 8 * tiles_n;
-  const int first = (id / gsz) * 8;
-  const int rows_g = tiles_m - first < 8 ? tiles_m - first : 8;
-  const int in_g = id % gsz;
-  tm = first + in_g % rows_g;
-  tn = in_g / rows_g;
-}
-
-// The 4-element form of an 8-element weight source, for the ragged-k staging.
-template <typename S>
-struct Narrow;
-template <typename T>
-struct Narrow<Table<8, T>> {
-  using type = Table<4, T>;
-  __device__ static type make(const Table<8, T>& s) { return type{s.table}; }
-};
-template <int L>
-struct Narrow<Q4K<8, L>> {
-  using type = Q4K<4, L>;
-  __device__ static type make(const Q4K<8, L>& s) { return type{s.wq}; }
-};
-template <>
-struct Narrow<Q5K<8>> {
-  using type = Q5K<4>;
-  __device__ static type make(const Q5K<8>& s) { return type{s.wq}; }
-};
-template <>
-struct Narrow<Q6K<8>> {
-  using type = Q6K<4>;
-  __device__ static type make(const Q6K<8>& s) { return type{s.wq}; }
-};
-
-// Element e of a weight source: K-quants decode the aligned 4-run that holds it
-// (inside e's 256-element superblock); plain rows read the element alone, so
-// nothing past the table's end is touched.
-template <typename S4>
-__device__ __forceinline__ float element_at(const S4& s, int64_t e) {
-  float v[4];
-  s.decode(s.load(e & ~int64_t(3)), v);
-  return v[e & 3];
-}
-template <typename T>
-__device__ __forceinline__ float element_at(const Table<4, T>& s, int64_t e) {
-  return to_f32(s.table[e]);
-}
-
-template <typename TX, typename Src, int BM, typename TO, bool RAGGED>
-__global__ __launch_bounds__(kDgThreads) __attribute__((amdgpu_waves_per_eu(2))) void dense_gemm_kernel(
-    const TX* __restrict__ x, Src w, TO* __restrict__ out, int64_t m, int64_t n, int64_t k, int tiles_n) {
-  constexpr int WN = BM == 128 ? 2 : 4;              // waves along n
-  constexpr int TM = BM == 128 ? 2 : 1;              // 32-row MFMA tiles per wave
-  constexpr int TN = BM == 128 ? 2 : 1;              // 32-column MFMA tiles per wave
-  constexpr int kStage = dg_stage_floats<BM>();
-  __shared__ float lds[2 * kStage];
-  int64_t tm, tn;
-  dg_tile(tiles_n, tm, tn);
-  const int64_t row0 = tm * BM, col0 = tn * kDgBN;
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wave / WN, wn = wave % WN;
-
-  // staging roles: thread t moves 8 k-values (half t & 1 of the stage) of activation
-  // row t >> 1 (t < 2 BM) and of weight column t >> 1
-  const int sr = tid >> 1, sh = (tid & 1) * 8;
-  const bool a_role = sr < BM, a_ok = a_role && row0 + sr < m;
-  const bool b_ok = col0 + sr < n;
-  const Table<8, TX> xs{x};
-  typename Table<8, TX>::Raw ar;
-  typename Src::Raw br;
-  const int64_t a_e0 = (row0 + sr) * k + sh;  // element offsets at stage 0
-  const int64_t b_e0 = (col0 + sr) * k + sh;
-  int staged = 0;  // RAGGED: the stage the next store writes
-  auto load = [&](int st) {
-    const int64_t kc = (int64_t)st * kDgKC;
-    if constexpr (RAGGED) {
-      staged = st;
-    } else {
-      if (a_ok) ar = xs.load(a_e0 + kc);
-      if (b_ok) br = w.load(b_e0 + kc);
-    }
-  };
-  auto store = [&](int buf) {
-    float* s = lds + buf * kStage;
-    float v[8];
-    if constexpr (RAGGED) {
-      const int64_t i0 = (int64_t)staged * kDgKC + sh;  // k index of v[0]
-      if (a_role) {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) v[i] = a_ok && i0 + i < k ? to_f32(x[a_e0 - sh + i0 + i]) : 0.0f;
-        float* d = s + sr * kDgRow + sh;
-        st16(d, Pack<float>::pack(v));
-        st16(d + 4, Pack<float>::pack(v + 4));
-      }
-      const auto w4 = Narrow<Src>::make(w);
-#pragma unroll
-      for (int i = 0; i < 8; ++i) v[i] = b_ok && i0 + i < k ? element_at(w4, b_e0 - sh + i0 + i) : 0.0f;
-      float* d = s + (BM + sr) * kDgRow + sh;
-      st16(d, Pack<float>::pack(v));
-      st16(d + 4, Pack<float>::pack(v + 4));
-      return;
-    }
-    if (a_role) {
-      if (a_ok) {
-        xs.decode(ar, v);
-      } else {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) v[i] = 0.0f;
-      }
-      float* d = s + sr * kDgRow + sh;
-      st16(d, Pack<float>::pack(v));
-      st16(d + 4, Pack<float>::pack(v + 4));
-    }
-    if (b_ok) {
-      w.decode(br, v);
-    } else {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) v[i] = 0.0f;
-    }
-    float* d = s + (BM + sr) * kDgRow + sh;
-    st16(d, Pack<float>::pack(v));
-    st16(d + 4, Pack<float>::pack(v + 4));
-  };
-
-  f32x16 acc[TM][TN];
-#pragma unroll
-  for (int a = 0; a < TM; ++a)
-#pragma unroll
-    for (int b = 0; b < TN; ++b) acc[a][b] = f32x16{};
-  // fragment rows: MFMA tile a of this wave covers rows 32 (TM wm + a) + (lane & 31)
-  const int half = lane >> 5;
-  const int fa = (TM * 32 * wm + (lane & 31)) * kDgRow + 8 * half;
-  const int fb = (BM + TN * 32 * wn + (lane & 31)) * kDgRow + 8 * half;
-
-  const int nst = (int)((k + kDgKC - 1) / kDgKC);
-  load(0);
-  store(0);
-  __syncthreads();
-#pragma unroll 1
-  for (int st = 0; st < nst; ++st) {
-    const float* s = lds + (st & 1) * kStage;
-    if (st + 1 < nst) load(st + 1);  // in flight during this stage's MFMAs
-    f32x4 av[TM][2], bv[TN][2];
-#pragma unroll
-    for (int a = 0; a < TM; ++a) {
-      av[a][0] = __builtin_bit_cast(f32x4, ld16(s + fa + a * 32 * kDgRow));
-      av[a][1] = __builtin_bit_cast(f32x4, ld16(s + fa + a * 32 * kDgRow + 4));
-    }
-#pragma unroll
-    for (int b = 0; b < TN; ++b) {
-      bv[b][0] = __builtin_bit_cast(f32x4, ld16(s + fb + b * 32 * kDgRow));
-      bv[b][1] = __builtin_bit_cast(f32x4, ld16(s + fb + b * 32 * kDgRow + 4));
-    }
-#pragma unroll
-    for (int step = 0; step < 8; ++step)
-#pragma unroll
-      for (int a = 0; a < TM; ++a)
-#pragma unroll
-        for (int b = 0; b < TN; ++b)
-          acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[a][step >> 2][step & 3], bv[b][step >> 2][step & 3],
-                                                         acc[a][b], 0, 0, 0);
-    if (st + 1 < nst) {
-      store((st + 1) & 1);  // the other buffer: its last readers passed the previous barrier
-      __syncthreads();
-    }
-  }
-
-  // D layout of v_mfma_f32_32x32x2f32: lane l, value j -> column l % 32,
-  // row 8 (j / 4) + 4 (l / 32) + j % 4
-#pragma unroll
-  for (int a = 0; a < TM; ++a)
-#pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      const int64_t r = row0 + TM * 32 * wm + 32 * a + 8 * (j >> 2) + 4 * half + (j & 3);
-      if (r >= m) continue;
-#pragma unroll
-      for (int b = 0; b < TN; ++b) {
-        const int64_t c = col0 + TN * 32 * wn + 32 * b + (lane & 31);
-        if (c < n) out[r * n + c] = from_f32<TO>(acc[a][b][j]);
-      }
-    }
-}
 
 // ---------------------------------------------------------------------------
 // 32-element group sources for the decode products: one lane decodes a whole
@@ -250,12 +28,6 @@ __global__ __launch_bounds__(kDgThreads) __attribute__((amdgpu_waves_per_eu(2)))
 // superblock header and the group's scale / min are read and decoded once per 32
 // values instead of once per 8.  Values are bit-identical to Q4K / Q5K / Q6K
 // (weight_formats.hpp): the same formulas on the same bytes.
-template <typename S>
-struct RunOf;  // elements one load of a source yields
-template <typename T>
-struct RunOf<Table<8, T>> {
-  static constexpr int value = 8;
-};
 
 // a & 0x0f0f0f0f kept as one instruction: the byte-wise conversions that follow
 // (v_cvt_f32_ubyte0..3) then take the masked bytes directly, where the compiler
@@ -425,25 +197,9 @@ struct RunOf<Q6KGroup> {
 // column per step) with the same k of each of the m rows, accumulating m x C fp32
 // sums; the LPC lanes of a column are summed at the end.
 //
-// 2 < m <= 16 (dense_gemv_mfma_kernel): v_mfma_f32_16x16x4_f32, lane l = 16 s + j
-// giving activation row j and weight column j at k slot s.  Lane l streams 16
-// (dense: two runs of 8) or 32 consecutive k at offset (16 or 32) s of column j of
-// each of C 16-column groups; value i of the lane's span is MFMA step i, with
-// k slot s <-> k = span s + i.  The matrix core sums the k slots, so only the
-// waves are summed at the end.
-constexpr int kGvWaves = 4;
+// 2 < m <= 16: gemv_mfma_kernel (gemm_tile.hpp, v_mfma_f32_16x16x4_f32) with the
+// plain problem policy.
 constexpr int kGemvRows = 16;
-
-template <typename TX, int R>
-__device__ __forceinline__ void load_x_run(const Table<8, TX>& xs, int64_t e0, typename Table<8, TX>::Raw* xr) {
-#pragma unroll
-  for (int u = 0; u < R / 8; ++u) xr[u] = xs.load(e0 + 8 * u);
-}
-template <typename TX, int R>
-__device__ __forceinline__ void decode_x_run(const Table<8, TX>& xs, const typename Table<8, TX>::Raw* xr, float* v) {
-#pragma unroll
-  for (int u = 0; u < R / 8; ++u) xs.decode(xr[u], v + 8 * u);
-}
 
 template <typename TX, typename Src, int MR, int C, int S, typename TO>
 __global__ __launch_bounds__(kGvWaves * 64) void dense_gemv_fma_kernel(const TX* __restrict__ x, Src w,
@@ -545,80 +301,6 @@ __global__ __launch_bounds__(kGvWaves * 64) void dense_gemv_fma_kernel(const TX*
   }
 }
 
-template <typename TX, typename Src, int C, typename TO>
-__global__ __launch_bounds__(kGvWaves * 64) void dense_gemv_mfma_kernel(const TX* __restrict__ x, Src w,
-                                                                        TO* __restrict__ out, int64_t m, int64_t n,
-                                                                        int64_t k) {
-  constexpr int R = RunOf<Src>::value, H = R == 8 ? 2 : 1, SPAN = H * R, KS = 4 * SPAN;
-  __shared__ float part[kGvWaves][C][16][17];  // [wave][group][row][column] (padded)
-  const int lane = threadIdx.x & 63, j = lane & 15, ks = lane >> 4;
-  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
-  const int64_t c0 = (int64_t)blockIdx.x * 16 * C;
-  const int64_t nsteps = (k + KS - 1) / KS;
-  const int64_t s_begin = nsteps * wave / kGvWaves, s_end = nsteps * (wave + 1) / kGvWaves;
-  const Table<8, TX> xs{x};
-  const bool row_ok = j < m;
-  bool col_ok[C];
-#pragma unroll
-  for (int q = 0; q < C; ++q) col_ok[q] = c0 + 16 * q + j < n;
-  f32x4 acc[C];
-#pragma unroll
-  for (int q = 0; q < C; ++q) acc[q] = f32x4{};
-
-  for (int64_t s = s_begin; s < s_end; ++s) {
-    const int64_t kk = s * KS + (int64_t)SPAN * ks;
-    typename Src::Raw wr[C][H];
-    typename Table<8, TX>::Raw xr[H][R / 8];
-    bool h_ok[H];
-#pragma unroll
-    for (int h = 0; h < H; ++h) {
-      h_ok[h] = kk + R * h < k;
-#pragma unroll
-      for (int q = 0; q < C; ++q)
-        if (h_ok[h] && col_ok[q]) wr[q][h] = w.load((c0 + 16 * q + j) * k + kk + R * h);
-      if (h_ok[h] && row_ok) load_x_run<TX, R>(xs, (int64_t)j * k + kk + R * h, xr[h]);
-    }
-#pragma unroll
-    for (int h = 0; h < H; ++h) {
-      float xv[R];
-      if (h_ok[h] && row_ok) {
-        decode_x_run<TX, R>(xs, xr[h], xv);
-      } else {
-#pragma unroll
-        for (int i = 0; i < R; ++i) xv[i] = 0.0f;
-      }
-#pragma unroll
-      for (int q = 0; q < C; ++q) {
-        float wv[R];
-        if (h_ok[h] && col_ok[q]) {
-          w.decode(wr[q][h], wv);
-        } else {
-#pragma unroll
-          for (int i = 0; i < R; ++i) wv[i] = 0.0f;
-        }
-#pragma unroll
-        for (int i = 0; i < R; ++i) acc[q] = __builtin_amdgcn_mfma_f32_16x16x4f32(xv[i], wv[i], acc[q], 0, 0, 0);
-      }
-    }
-  }
-
-  // D of v_mfma_f32_16x16x4_f32: lane l, value r -> row 4 (l / 16) + r, column l % 16
-#pragma unroll
-  for (int q = 0; q < C; ++q)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) part[wave][q][4 * ks + r][j] = acc[q][r];
-  __syncthreads();
-  for (int t = (int)threadIdx.x; t < C * 256; t += kGvWaves * 64) {
-    const int jj = t & 15, row = (t >> 4) & 15, q = t >> 8;
-    const int64_t col = c0 + 16 * q + jj;
-    if (row >= m || col >= n) continue;
-    float v = part[0][q][row][jj];
-#pragma unroll
-    for (int wv = 1; wv < kGvWaves; ++wv) v += part[wv][q][row][jj];
-    out[(int64_t)row * n + col] = from_f32<TO>(v);
-  }
-}
-
 // Column sets / groups per wave: 4 (dense) or 2 (K-quants, larger runs) when that
 // leaves >= ~1000 workgroups, fewer for narrow outputs.
 template <typename TX, typename Src, int MR, typename TO>
@@ -641,12 +323,13 @@ int launch_gemv_fma(const TX* x, const Src& src, TO* out, int64_t m, int64_t n, 
 template <typename TX, typename Src, typename TO>
 int launch_gemv_mfma(const TX* x, const Src& src, TO* out, int64_t m, int64_t n, int64_t k, hipStream_t st) {
   const dim3 blk(kGvWaves * 64);
+  const PlainGemvProb<TO> prob{out, m, n, k};
   if (n >= 64 * 1024)
-    dense_gemv_mfma_kernel<TX, Src, 4, TO><<<dim3((unsigned)((n + 63) / 64)), blk, 0, st>>>(x, src, out, m, n, k);
+    gemv_mfma_kernel<TX, Src, 4><<<dim3((unsigned)((n + 63) / 64)), blk, 0, st>>>(x, src, prob, k);
   else if (n >= 32 * 1024)
-    dense_gemv_mfma_kernel<TX, Src, 2, TO><<<dim3((unsigned)((n + 31) / 32)), blk, 0, st>>>(x, src, out, m, n, k);
+    gemv_mfma_kernel<TX, Src, 2><<<dim3((unsigned)((n + 31) / 32)), blk, 0, st>>>(x, src, prob, k);
   else
-    dense_gemv_mfma_kernel<TX, Src, 1, TO><<<dim3((unsigned)((n + 15) / 16)), blk, 0, st>>>(x, src, out, m, n, k);
+    gemv_mfma_kernel<TX, Src, 1><<<dim3((unsigned)((n + 15) / 16)), blk, 0, st>>>(x, src, prob, k);
   return launch_status("dense_gemv_mfma");
 }
 
@@ -691,16 +374,18 @@ int launch_dense(const void* x, const Src& src, void* out, int64_t m, int64_t n,
   const bool ragged = !vec || k % kDgKC != 0;
   if (m <= 32) {
     const dim3 g((unsigned)tiles_n);
+    const PlainProb<32, TO> prob{op, m, n, k};
     if (ragged)
-      dense_gemm_kernel<TX, Src, 32, TO, true><<<g, kDgThreads, 0, st>>>(xp, src, op, m, n, k, tiles_n);
+      gemm_tile_kernel<TX, Src, 32, true><<<g, kDgThreads, 0, st>>>(xp, src, prob, k, tiles_n);
     else
-      dense_gemm_kernel<TX, Src, 32, TO, false><<<g, kDgThreads, 0, st>>>(xp, src, op, m, n, k, tiles_n);
+      gemm_tile_kernel<TX, Src, 32, false><<<g, kDgThreads, 0, st>>>(xp, src, prob, k, tiles_n);
   } else {
     const dim3 g((unsigned)(((m + 127) / 128) * tiles_n));
+    const PlainProb<128, TO> prob{op, m, n, k};
     if (ragged)
-      dense_gemm_kernel<TX, Src, 128, TO, true><<<g, kDgThreads, 0, st>>>(xp, src, op, m, n, k, tiles_n);
+      gemm_tile_kernel<TX, Src, 128, true><<<g, kDgThreads, 0, st>>>(xp, src, prob, k, tiles_n);
     else
-      dense_gemm_kernel<TX, Src, 128, TO, false><<<g, kDgThreads, 0, st>>>(xp, src, op, m, n, k, tiles_n);
+      gemm_tile_kernel<TX, Src, 128, false><<<g, kDgThreads, 0, st>>>(xp, src, prob, k, tiles_n);
   }
   return launch_status("dense_gemm");
 }

@@ -1,0 +1,400 @@
+// The fp32 matrix-core tile kernel shared by the weight GEMM (dense_gemm.hip) and
+// the MoE expert products (moe.hip): v_mfma_f32_32x32x2_f32 over BM x 128 output
+// tiles (BM = 128: 2 x 2 waves of 64 x 64; BM = 32: 1 x 4 waves of 32 x 32), K in
+// 16-element LDS stages, double-buffered with the next stage's loads in flight.
+//   * activation rows, upconverted to fp32 (8 elements per thread);
+//   * weight rows, decoded to fp32 by the element sources of weight_formats.hpp
+//     (8 elements per thread, bit-exact values);
+//   * LDS rows padded to 20 floats, so the 16 lanes of a ds_read_b128 phase hit
+//     16 distinct 4-bank groups.
+// Inside a stage the k order is permuted (the dot product does not care): MFMA
+// step s contracts k = s on lanes 0-31 and k = 8 + s on lanes 32-63 for both
+// operands, so each lane reads its 8 values of a row as two 16-byte LDS reads.
+// A k that is not a multiple of 16, or a misaligned operand, runs the RAGGED
+// variant: the same tiles and MFMAs, every staged value read on its own, k beyond
+// the row's end staged as zero, weights decoded through 4-element aligned runs.
+#pragma once
+
+#include "nvf_device.hpp"
+#include "nvf_host.hpp"
+#include "weight_formats.hpp"
+
+namespace nvf {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int kDgBN = 128;           // output columns per workgroup
+constexpr int kDgKC = 16;            // k elements per LDS stage
+constexpr int kDgRow = kDgKC + 4;    // LDS floats per staged row (padded)
+constexpr int kDgThreads = 256;
+constexpr int kDgXcds = 8;
+
+template <int BM>
+constexpr int dg_stage_floats() {
+  return (BM + kDgBN) * kDgRow;
+}
+
+// Workgroup -> output tile, XCD-aware: workgroups are dealt to the 8 XCDs
+// round-robin, and each XCD takes a contiguous range of an order that walks 8
+// tile rows at a time column by column, so its resident workgroups share weight
+// and activation panels in its L2.
+__device__ __forceinline__ void dg_tile(int tiles_n, int64_t& tm, int64_t& tn) {
+  const int tiles = (int)gridDim.x;
+  const int tiles_m = tiles / tiles_n;
+  const int xcd = (int)blockIdx.x % kDgXcds, local = (int)blockIdx.x / kDgXcds;
+  const int per = tiles / kDgXcds, extra = tiles % kDgXcds;
+  const int id = xcd * per + (xcd < extra ? xcd : extra) + local;
+  const int gsz = 8 * tiles_n;
+  const int first = (id / gsz) * 8;
+  const int rows_g = tiles_m - first < 8 ? tiles_m - first : 8;
+  const int in_g = id % gsz;
+  tm = first + in_g % rows_g;
+  tn = in_g / rows_g;
+}
+
+// The 4-element form of an 8-element weight source, for the ragged-k staging.
+template <typename S>
+struct Narrow;
+template <typename T>
+struct Narrow<Table<8, T>> {
+  using type = Table<4, T>;
+  __device__ static type make(const Table<8, T>& s) { return type{s.table}; }
+};
+template <int L>
+struct Narrow<Q4K<8, L>> {
+  using type = Q4K<4, L>;
+  __device__ static type make(const Q4K<8, L>& s) { return type{s.wq}; }
+};
+template <>
+struct Narrow<Q5K<8>> {
+  using type = Q5K<4>;
+  __device__ static type make(const Q5K<8>& s) { return type{s.wq}; }
+};
+template <>
+struct Narrow<Q6K<8>> {
+  using type = Q6K<4>;
+  __device__ static type make(const Q6K<8>& s) { return type{s.wq}; }
+};
+
+// Element e of a weight source: K-quants decode the aligned 4-run that holds it
+// (inside e's 256-element superblock); plain rows read the element alone, so
+// nothing past the table's end is touched.
+template <typename S4>
+__device__ __forceinline__ float element_at(const S4& s, int64_t e) {
+  float v[4];
+  s.decode(s.load(e & ~int64_t(3)), v);
+  return v[e & 3];
+}
+template <typename T>
+__device__ __forceinline__ float element_at(const Table<4, T>& s, int64_t e) {
+  return to_f32(s.table[e]);
+}
+
+// The tile kernel over a problem policy P, which names the workgroup's tiles and
+// the element offsets of their rows and columns, and stores the results.  A
+// workgroup takes items blockIdx.x, blockIdx.x + gridDim.x, ... until tile() says
+// there are no more (a policy with more tiles than the grid has workgroups):
+//   bool tile(int64_t item, int tiles_n, Tile& t)  -- false: no such item
+//   static constexpr bool kLoop                    -- false: one item per workgroup
+//   int64_t a_row(const Tile&, int r)         -- element offset of tile row r in x, or -1
+//   int64_t b_row(const Tile&, int c)         -- element offset of tile column c's weight row, or -1
+//   void store(const Tile&, int r, int c, v)  -- result of tile row r, column c
+// PlainProb below is the plain GEMM; the MoE expert products supply their own.
+template <typename TX, typename Src, int BM, bool RAGGED, typename P>
+__global__ __launch_bounds__(kDgThreads) __attribute__((amdgpu_waves_per_eu(2))) void gemm_tile_kernel(
+    const TX* __restrict__ x, Src w, P prob, int64_t k, int tiles_n) {
+  constexpr int WN = BM == 128 ? 2 : 4;              // waves along n
+  constexpr int TM = BM == 128 ? 2 : 1;              // 32-row MFMA tiles per wave
+  constexpr int TN = BM == 128 ? 2 : 1;              // 32-column MFMA tiles per wave
+  constexpr int kStage = dg_stage_floats<BM>();
+  __shared__ float lds[2 * kStage];
+  for (int64_t item = blockIdx.x;; item += gridDim.x) {
+    typename P::Tile tile;
+    if (!prob.tile(item, tiles_n, tile)) break;  // uniform per workgroup
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave / WN, wn = wave % WN;
+
+    // staging roles: thread t moves 8 k-values (half t & 1 of the stage) of activation
+    // row t >> 1 (t < 2 BM) and of weight column t >> 1
+    const int sr = tid >> 1, sh = (tid & 1) * 8;
+    const bool a_role = sr < BM;
+    const int64_t a_off = a_role ? prob.a_row(tile, sr) : -1, b_off = prob.b_row(tile, sr);
+    const bool a_ok = a_off >= 0, b_ok = b_off >= 0;
+    const Table<8, TX> xs{x};
+    typename Table<8, TX>::Raw ar;
+    typename Src::Raw br;
+    const int64_t a_e0 = a_off + sh;  // element offsets at stage 0
+    const int64_t b_e0 = b_off + sh;
+    int staged = 0;  // RAGGED: the stage the next store writes
+    auto load = [&](int st) {
+      const int64_t kc = (int64_t)st * kDgKC;
+      if constexpr (RAGGED) {
+        staged = st;
+      } else {
+        if (a_ok) ar = xs.load(a_e0 + kc);
+        if (b_ok) br = w.load(b_e0 + kc);
+      }
+    };
+    auto store = [&](int buf) {
+      float* s = lds + buf * kStage;
+      float v[8];
+      if constexpr (RAGGED) {
+        const int64_t i0 = (int64_t)staged * kDgKC + sh;  // k index of v[0]
+        if (a_role) {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) v[i] = a_ok && i0 + i < k ? to_f32(x[a_e0 - sh + i0 + i]) : 0.0f;
+          float* d = s + sr * kDgRow + sh;
+          st16(d, Pack<float>::pack(v));
+          st16(d + 4, Pack<float>::pack(v + 4));
+        }
+        const auto w4 = Narrow<Src>::make(w);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = b_ok && i0 + i < k ? element_at(w4, b_e0 - sh + i0 + i) : 0.0f;
+        float* d = s + (BM + sr) * kDgRow + sh;
+        st16(d, Pack<float>::pack(v));
+        st16(d + 4, Pack<float>::pack(v + 4));
+        return;
+      }
+      if (a_role) {
+        if (a_ok) {
+          xs.decode(ar, v);
+        } else {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) v[i] = 0.0f;
+        }
+        float* d = s + sr * kDgRow + sh;
+        st16(d, Pack<float>::pack(v));
+        st16(d + 4, Pack<float>::pack(v + 4));
+      }
+      if (b_ok) {
+        w.decode(br, v);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = 0.0f;
+      }
+      float* d = s + (BM + sr) * kDgRow + sh;
+      st16(d, Pack<float>::pack(v));
+      st16(d + 4, Pack<float>::pack(v + 4));
+    };
+
+    f32x16 acc[TM][TN];
+#pragma unroll
+    for (int a = 0; a < TM; ++a)
+#pragma unroll
+      for (int b = 0; b < TN; ++b) acc[a][b] = f32x16{};
+    // fragment rows: MFMA tile a of this wave covers rows 32 (TM wm + a) + (lane & 31)
+    const int half = lane >> 5;
+    const int fa = (TM * 32 * wm + (lane & 31)) * kDgRow + 8 * half;
+    const int fb = (BM + TN * 32 * wn + (lane & 31)) * kDgRow + 8 * half;
+
+    const int nst = (int)((k + kDgKC - 1) / kDgKC);
+    load(0);
+    store(0);
+    __syncthreads();
+#pragma unroll 1
+    for (int st = 0; st < nst; ++st) {
+      const float* s = lds + (st & 1) * kStage;
+      if (st + 1 < nst) load(st + 1);  // in flight during this stage's MFMAs
+      f32x4 av[TM][2], bv[TN][2];
+#pragma unroll
+      for (int a = 0; a < TM; ++a) {
+        av[a][0] = __builtin_bit_cast(f32x4, ld16(s + fa + a * 32 * kDgRow));
+        av[a][1] = __builtin_bit_cast(f32x4, ld16(s + fa + a * 32 * kDgRow + 4));
+      }
+#pragma unroll
+      for (int b = 0; b < TN; ++b) {
+        bv[b][0] = __builtin_bit_cast(f32x4, ld16(s + fb + b * 32 * kDgRow));
+        bv[b][1] = __builtin_bit_cast(f32x4, ld16(s + fb + b * 32 * kDgRow + 4));
+      }
+#pragma unroll
+      for (int step = 0; step < 8; ++step)
+#pragma unroll
+        for (int a = 0; a < TM; ++a)
+#pragma unroll
+          for (int b = 0; b < TN; ++b)
+            acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[a][step >> 2][step & 3], bv[b][step >> 2][step & 3],
+                                                           acc[a][b], 0, 0, 0);
+      if (st + 1 < nst) {
+        store((st + 1) & 1);  // the other buffer: its last readers passed the previous barrier
+        __syncthreads();
+      }
+    }
+
+    // D layout of v_mfma_f32_32x32x2f32: lane l, value j -> column l % 32,
+    // row 8 (j / 4) + 4 (l / 32) + j % 4
+#pragma unroll
+    for (int a = 0; a < TM; ++a)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const int r = TM * 32 * wm + 32 * a + 8 * (j >> 2) + 4 * half + (j & 3);
+#pragma unroll
+        for (int b = 0; b < TN; ++b) prob.store(tile, r, TN * 32 * wn + 32 * b + (lane & 31), acc[a][b][j]);
+      }
+    if constexpr (!P::kLoop) break;  // one item per workgroup
+    __syncthreads();                 // LDS is reused by the next item
+  }
+}
+
+// The plain GEMM: out[m][n] (row-major, TO) = x[m][k] . W[n][k]^T, tiles in dg_tile's
+// XCD-aware order.
+template <int BM, typename TO>
+struct PlainProb {
+  static constexpr bool kLoop = false;
+  TO* out;
+  int64_t m, n, k;
+  struct Tile {
+    int64_t row0, col0;
+  };
+  __device__ bool tile(int64_t item, int tiles_n, Tile& t) const {
+    if (item != blockIdx.x) return false;  // one tile per workgroup
+    int64_t tm, tn;
+    dg_tile(tiles_n, tm, tn);
+    t.row0 = tm * BM;
+    t.col0 = tn * kDgBN;
+    return true;
+  }
+  __device__ int64_t a_row(const Tile& t, int r) const { return t.row0 + r < m ? (t.row0 + r) * k : -1; }
+  __device__ int64_t b_row(const Tile& t, int c) const { return t.col0 + c < n ? (t.col0 + c) * k : -1; }
+  __device__ void store(const Tile& t, int r, int c, float v) const {
+    const int64_t rr = t.row0 + r, cc = t.col0 + c;
+    if (rr < m && cc < n) out[rr * n + cc] = from_f32<TO>(v);
+  }
+};
+
+// ---------------------------------------------------------------------------
+// Decode-shaped product on v_mfma_f32_16x16x4_f32 (m <= 16 rows): lane l = 16 s + j
+// gives activation row j and weight column j at k slot s.  Lane l streams 16
+// (dense: two runs of 8) or 32 consecutive k at offset (16 or 32) s of column j of
+// each of C 16-column groups; value i of the lane's span is MFMA step i, with
+// k slot s <-> k = span s + i.  The matrix core sums the k slots; the 4 waves of a
+// workgroup split K and meet in LDS, summed in wave order.  The problem policy P
+// names the columns of work item `item` (items blockIdx.x, blockIdx.x + gridDim.x,
+// ... until it answers false) and the element offsets of its rows and columns:
+//   bool tile(int64_t item, int cols, Tile& t), a_row(t, j), b_row(t, c), store(t, r, c, v).
+constexpr int kGvWaves = 4;
+
+template <typename S>
+struct RunOf;  // elements one load of a source yields
+template <typename T>
+struct RunOf<Table<8, T>> {
+  static constexpr int value = 8;
+};
+
+template <typename TX, int R>
+__device__ __forceinline__ void load_x_run(const Table<8, TX>& xs, int64_t e0, typename Table<8, TX>::Raw* xr) {
+#pragma unroll
+  for (int u = 0; u < R / 8; ++u) xr[u] = xs.load(e0 + 8 * u);
+}
+template <typename TX, int R>
+__device__ __forceinline__ void decode_x_run(const Table<8, TX>& xs, const typename Table<8, TX>::Raw* xr, float* v) {
+#pragma unroll
+  for (int u = 0; u < R / 8; ++u) xs.decode(xr[u], v + 8 * u);
+}
+
+template <typename TX, typename Src, int C, typename P>
+__global__ __launch_bounds__(kGvWaves * 64) void gemv_mfma_kernel(const TX* __restrict__ x, Src w, P prob,
+                                                                  int64_t k) {
+  constexpr int R = RunOf<Src>::value, H = R == 8 ? 2 : 1, SPAN = H * R, KS = 4 * SPAN;
+  __shared__ float part[kGvWaves][C][16][17];  // [wave][group][row][column] (padded)
+  const int lane = threadIdx.x & 63, j = lane & 15, ks = lane >> 4;
+  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  for (int64_t item = blockIdx.x;; item += gridDim.x) {
+    typename P::Tile tile;
+    if (!prob.tile(item, 16 * C, tile)) break;  // uniform per workgroup
+    const int64_t nsteps = (k + KS - 1) / KS;
+    const int64_t s_begin = nsteps * wave / kGvWaves, s_end = nsteps * (wave + 1) / kGvWaves;
+    const Table<8, TX> xs{x};
+    const int64_t x_off = prob.a_row(tile, j);
+    const bool row_ok = x_off >= 0;
+    int64_t w_off[C];
+    bool col_ok[C];
+#pragma unroll
+    for (int q = 0; q < C; ++q) {
+      w_off[q] = prob.b_row(tile, 16 * q + j);
+      col_ok[q] = w_off[q] >= 0;
+    }
+    f32x4 acc[C];
+#pragma unroll
+    for (int q = 0; q < C; ++q) acc[q] = f32x4{};
+
+    for (int64_t s = s_begin; s < s_end; ++s) {
+      const int64_t kk = s * KS + (int64_t)SPAN * ks;
+      typename Src::Raw wr[C][H];
+      typename Table<8, TX>::Raw xr[H][R / 8];
+      bool h_ok[H];
+#pragma unroll
+      for (int h = 0; h < H; ++h) {
+        h_ok[h] = kk + R * h < k;
+#pragma unroll
+        for (int q = 0; q < C; ++q)
+          if (h_ok[h] && col_ok[q]) wr[q][h] = w.load(w_off[q] + kk + R * h);
+        if (h_ok[h] && row_ok) load_x_run<TX, R>(xs, x_off + kk + R * h, xr[h]);
+      }
+#pragma unroll
+      for (int h = 0; h < H; ++h) {
+        float xv[R];
+        if (h_ok[h] && row_ok) {
+          decode_x_run<TX, R>(xs, xr[h], xv);
+        } else {
+#pragma unroll
+          for (int i = 0; i < R; ++i) xv[i] = 0.0f;
+        }
+#pragma unroll
+        for (int q = 0; q < C; ++q) {
+          float wv[R];
+          if (h_ok[h] && col_ok[q]) {
+            w.decode(wr[q][h], wv);
+          } else {
+#pragma unroll
+            for (int i = 0; i < R; ++i) wv[i] = 0.0f;
+          }
+#pragma unroll
+          for (int i = 0; i < R; ++i) acc[q] = __builtin_amdgcn_mfma_f32_16x16x4f32(xv[i], wv[i], acc[q], 0, 0, 0);
+        }
+      }
+    }
+
+    // D of v_mfma_f32_16x16x4_f32: lane l, value r -> row 4 (l / 16) + r, column l % 16
+#pragma unroll
+    for (int q = 0; q < C; ++q)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) part[wave][q][4 * ks + r][j] = acc[q][r];
+    __syncthreads();
+    for (int t = (int)threadIdx.x; t < C * 256; t += kGvWaves * 64) {
+      const int jj = t & 15, row = (t >> 4) & 15, q = t >> 8;
+      float v = part[0][q][row][jj];
+#pragma unroll
+      for (int wv = 1; wv < kGvWaves; ++wv) v += part[wv][q][row][jj];
+      prob.store(tile, row, 16 * q + jj, v);
+    }
+    if constexpr (!P::kLoop) break;  // one item per workgroup
+    __syncthreads();                 // LDS is reused by the next item
+  }
+}
+
+// The plain decode product: out[m][n] = x[m][k] . W[n][k]^T, m <= 16, workgroup b
+// on columns [b 16 C, (b + 1) 16 C).
+template <typename TO>
+struct PlainGemvProb {
+  static constexpr bool kLoop = false;
+  TO* out;
+  int64_t m, n, k;
+  struct Tile {
+    int64_t col0;
+  };
+  __device__ bool tile(int64_t item, int cols, Tile& t) const {
+    if (item != blockIdx.x) return false;  // one column group per workgroup
+    t.col0 = item * cols;
+    return true;
+  }
+  __device__ int64_t a_row(const Tile&, int j) const { return j < m ? (int64_t)j * k : -1; }
+  __device__ int64_t b_row(const Tile& t, int c) const { return t.col0 + c < n ? (t.col0 + c) * k : -1; }
+  __device__ void store(const Tile& t, int r, int c, float v) const {
+    if (r < m && t.col0 + c < n) out[(int64_t)r * n + t.col0 + c] = from_f32<TO>(v);
+  }
+};
+
+
+}  // namespace nvf

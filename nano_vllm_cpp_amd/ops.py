@@ -41,6 +41,16 @@ SIGNATURES: dict[str, tuple] = {
     "hip_embedding_q8": (None, [_vp, _vp, _vp, _i32, _i32, _vp]),
     "hip_embedding_qk": (None, [_vp, _vp, _i32, _i32, _vp, _i32]),
     "hip_gather_rows": (None, [_vp, _vp, _i32, _i32, _i32, _vp]),
+    "hip_moe_route": (None, [_vp, _i32, _i32, _i32, C.c_bool, _vp, _vp]),
+    "hip_moe_ffn": (None, [_vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, C.c_bool, _vp]),
+    "hip_add_inplace": (None, [_vp, _vp, C.c_size_t]),
+    "hip_scale_rows_sigmoid": (None, [_vp, _vp, _i32, _i32]),
+    "nvf_moe_route": (_i32, [_vp, _i64, _i64, _i64, _i32, _vp, _vp, _vp]),
+    "nvf_moe_ffn_workspace_size": (_i64, [_i64, _i64, _i64, _i64, _i64]),
+    "nvf_moe_ffn_ws": (_i32, [_vp, _i32, _vp, _vp, _vp, _vp, _i32, _vp, _i64, _i64, _i64, _i64, _i64, _vp, _i32, _vp,
+                              _i64, _vp]),
+    "nvf_add_inplace": (_i32, [_vp, _vp, _i64, _vp]),
+    "nvf_scale_rows_sigmoid": (_i32, [_vp, _vp, _i64, _i64, _vp]),
     "hip_matmul": (None, [_vp, _vp, _i32, _i32, _i32, _vp]),
     "hip_matmul_u16": (None, [_vp, _vp, _i32, _i32, _i32, _vp, C.c_bool]),
     "hip_matmul_qk": (None, [_vp, _vp, _i32, _i32, _i32, _vp, _i32]),
@@ -548,4 +558,44 @@ def matmul(x: torch.Tensor, w: torch.Tensor, n: int, w_format: int, out_dtype=No
         raise ValueError("out must be [m, n] in out_dtype")
     _check(lib().nvf_matmul(_dev(x, "x"), _dt(x), _dev(w, "w"), w_format, qk_layout, m, n, k, _dev(out, "out"),
                             _DT[out_dtype], _stream()), "matmul")
+    return out
+
+
+# ---------------------------------------------------------------------------
+# mixture of experts
+# ---------------------------------------------------------------------------
+def moe_route(logits: torch.Tensor, k: int, norm: bool) -> tuple[torch.Tensor, torch.Tensor]:
+    """Top-k experts of each fp32 logits row [rows, E] (the reference's hip_moe_route):
+    (idx int32 [rows, k], score fp32 [rows, k])."""
+    if logits.dtype != torch.float32 or logits.dim() != 2:
+        raise ValueError("logits must be float32 [rows, E]")
+    rows, e = logits.shape
+    idx = torch.empty((rows, k), dtype=torch.int32, device=logits.device)
+    score = torch.empty((rows, k), dtype=torch.float32, device=logits.device)
+    _check(lib().nvf_moe_route(_dev(logits, "logits"), rows, e, k, 1 if norm else 0, _dev(idx, "idx"),
+                               _dev(score, "score"), _stream()), "moe_route")
+    return idx, score
+
+
+def moe_ffn(x: torch.Tensor, idx: torch.Tensor, score: torch.Tensor, gu: torch.Tensor, dn: torch.Tensor,
+            slot_of: torch.Tensor, inter: int, slots: int, out: torch.Tensor) -> torch.Tensor:
+    """out[t] += sum_k score[t,k] * down(silu(gate(x[t])) * up(x[t])) for expert slot
+    slot_of[idx[t,k]] (the reference's hip_moe_ffn): x [rows, H] and out [rows, H] fp32 /
+    fp16 / bf16, gu [slots, 2*inter, H] and dn [slots, H, inter] fp16 or bf16."""
+    rows, hidden = x.shape
+    k = idx.shape[1]
+    if idx.dtype != torch.int32 or score.dtype != torch.float32 or idx.shape != (rows, k) or score.shape != (rows, k):
+        raise ValueError("idx must be int32 and score float32, both [rows, K]")
+    if gu.dtype != dn.dtype or gu.dtype not in (torch.float16, torch.bfloat16):
+        raise ValueError("gu and dn must both be float16 or bfloat16")
+    if gu.numel() < slots * 2 * inter * hidden or dn.numel() < slots * hidden * inter:
+        raise ValueError("gu / dn hold fewer than `slots` experts")
+    if slot_of.dtype != torch.int32 or out.shape != (rows, hidden):
+        raise ValueError("slot_of must be int32 and out [rows, H]")
+    wb = lib().nvf_moe_ffn_workspace_size(rows, hidden, inter, k, slots)
+    work = torch.empty(max(wb, 16), dtype=torch.uint8, device=x.device)
+    _check(lib().nvf_moe_ffn_ws(_dev(x, "x"), _dt(x), _dev(idx, "idx"), _dev(score, "score"), _dev(gu, "gu"),
+                                _dev(dn, "dn"), 1 if gu.dtype == torch.bfloat16 else 0, _dev(slot_of, "slot_of"),
+                                rows, hidden, inter, k, slots, _dev(out, "out"), _dt(out), work.data_ptr(), wb,
+                                _stream()), "moe_ffn")
     return out

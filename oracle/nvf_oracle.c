@@ -654,3 +654,117 @@ void orc_embedding_rms_norm(const int64_t* ids, int format, const void* table, c
   free(x);
   free(emb);
 }
+
+/* src/hip_ops.hip:813-844 (moe_route_kernel), one row at a time as the reference's
+ * single thread does it. */
+void orc_moe_route(const float* logits, int64_t rows, int E, int K, int norm, int32_t* idx, float* score) {
+  double* pr = (double*)malloc(sizeof(double) * (size_t)E);
+  int* ix = (int*)malloc(sizeof(int) * (size_t)E);
+  for (int64_t t = 0; t < rows; ++t) {
+    const float* lg = logits + t * E;
+    double maxv = -1e300;
+    for (int i = 0; i < E; ++i) maxv = maxv > (double)lg[i] ? maxv : (double)lg[i];
+    double sum = 0.0;
+    for (int i = 0; i < E; ++i) {
+      pr[i] = exp((double)lg[i] - maxv);
+      sum += pr[i];
+    }
+    const double inv = 1.0 / sum;
+    for (int i = 0; i < E; ++i) {
+      pr[i] *= inv;
+      ix[i] = i;
+    }
+    for (int i = 0; i < K; ++i) {
+      int best = i;
+      for (int j = i + 1; j < E; ++j)
+        if (pr[j] > pr[best]) best = j;
+      const double tp = pr[i];
+      pr[i] = pr[best];
+      pr[best] = tp;
+      const int ti = ix[i];
+      ix[i] = ix[best];
+      ix[best] = ti;
+      idx[t * K + i] = ix[i];
+      score[t * K + i] = (float)pr[i];
+    }
+    if (norm) {
+      double s = 0.0;
+      for (int i = 0; i < K; ++i) s += pr[i];
+      const double sinv = 1.0 / s;
+      for (int i = 0; i < K; ++i) score[t * K + i] = (float)(pr[i] * sinv);
+    }
+  }
+  free(pr);
+  free(ix);
+}
+
+/* src/hip_ops.hip:861-893 (moe_ffn_kernel) in double, with a first-order fp32 bound. */
+void orc_moe_ffn(const void* x, int x_dtype, const int32_t* idx, const float* score, const uint16_t* gu,
+                 const uint16_t* dn, int w_bf16, const int32_t* slot_of, int64_t rows, int64_t H, int64_t I,
+                 int64_t K, int64_t slots, const double* out_in, double* out, double* err) {
+  const double u = 1.0 / 16777216.0; /* 2^-24 */
+  double* xv = (double*)malloc(sizeof(double) * (size_t)H);
+  double* y = (double*)malloc(sizeof(double) * (size_t)I);
+  double* ey = (double*)malloc(sizeof(double) * (size_t)I);
+  double* res = (double*)malloc(sizeof(double) * (size_t)H);
+  double* eres = (double*)malloc(sizeof(double) * (size_t)H);
+  double* wv = (double*)malloc(sizeof(double) * (size_t)H);
+#define ORC_W(p, i) ((double)(w_bf16 ? orc_bf16_to_f32((p)[i]) : orc_fp16_to_f32((p)[i])))
+  for (int64_t t = 0; t < rows; ++t) {
+    for (int64_t i = 0; i < H; ++i) {
+      xv[i] = (double)orc_load(x, t * H + i, x_dtype);
+      res[i] = 0.0;
+      eres[i] = 0.0;
+      wv[i] = 0.0;
+    }
+    for (int64_t k = 0; k < K; ++k) {
+      const double w = (double)score[t * K + k];
+      if (w == 0.0) continue;
+      const int32_t sl = slot_of[idx[t * K + k]];
+      if (sl < 0 || sl >= slots) continue;
+      const uint16_t* g = gu + (int64_t)sl * 2 * I * H;
+      const uint16_t* d = dn + (int64_t)sl * H * I;
+      for (int64_t j = 0; j < I; ++j) {
+        double gg = 0.0, uu = 0.0, ag = 0.0, au = 0.0;
+        for (int64_t i = 0; i < H; ++i) {
+          const double a = xv[i] * ORC_W(g, j * H + i), b = xv[i] * ORC_W(g, (I + j) * H + i);
+          gg += a;
+          uu += b;
+          ag += fabs(a);
+          au += fabs(b);
+        }
+        const double eg = (double)(H + 2) * u * ag, eu = (double)(H + 2) * u * au;
+        const double sg = 1.0 / (1.0 + exp(-gg));
+        const double silu = gg * sg;
+        const double dsilu = sg * (1.0 + gg * (1.0 - sg));
+        y[j] = silu * uu;
+        ey[j] = fabs(dsilu * uu) * eg + fabs(silu) * eu + 8.0 * u * fabs(y[j]);
+      }
+      for (int64_t o = 0; o < H; ++o) {
+        double v = 0.0, av = 0.0, prop = 0.0;
+        for (int64_t j = 0; j < I; ++j) {
+          const double dw = ORC_W(d, o * I + j);
+          v += y[j] * dw;
+          av += fabs(y[j] * dw);
+          prop += fabs(dw) * ey[j];
+        }
+        const double ev = (double)(I + 2) * u * av + prop;
+        res[o] += w * v;
+        eres[o] += fabs(w) * ev;
+        wv[o] += fabs(w * v);
+      }
+    }
+    for (int64_t o = 0; o < H; ++o) {
+      const double r = out_in[t * H + o] + res[o];
+      out[t * H + o] = r;
+      err[t * H + o] = eres[o] + (double)(K + 1) * u * wv[o] + u * (fabs(r) + fabs(res[o]));
+    }
+  }
+#undef ORC_W
+  free(xv);
+  free(y);
+  free(ey);
+  free(res);
+  free(eres);
+  free(wv);
+}

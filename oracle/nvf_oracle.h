@@ -125,14 +125,36 @@ void orc_q8_quantize(const void* x, const float* scale, int8_t* q, int64_t rows,
 /* Q8_0 GEMM, src/hip_ops.hip:639-686: out[r,c] = (sum_b ws[c,b] * I[r,c,b]) /
  * scale[r] with exact integer block dots I, in double, and err[r,c], the fp32
  * recursive-summation bound (k/32 + 4) * 2^-24 * sum_b |ws*I| / scale[r]. */
-void orc_matmul_w(const void* x, int x_dtype, const void* w, int w_format, int layout, int64_t m, int64_t n,
-                  int64_t k, double* out, double* err);
-void orc_gather_rows(const void* rows, const int32_t* indices, int64_t cols, int64_t out_rows, void* out,
-                     int dtype);
 void orc_matmul_q8_i8(const int8_t* xq, const float* scale, const uint8_t* w8, const uint16_t* ws, int64_t m,
                       int64_t n, int64_t k, double* out, double* err);
 void orc_matmul_q8(const void* x, int dtype, const uint8_t* w8, const uint16_t* ws, int64_t m, int64_t n, int64_t k,
                    double* out, double* err, float* scale_out, int8_t* xq_out);
+
+/* Dense / K-quant weight GEMM, src/hip_ops.hip:43-64 and :577-598 (qk_w :184-193):
+ * out[r,c] = sum_i x[r,i] * w(c,i), w decoded exactly (fp32 / fp16 / bf16 rows, Q4_K in
+ * `layout`, Q5_K, Q6_K), in double; err[r,c] = (k + 2) * 2^-24 * sum_i |x w|, which covers
+ * fp32 sums of the products in any order. */
+void orc_matmul_w(const void* x, int x_dtype, const void* w, int w_format, int layout, int64_t m, int64_t n,
+                  int64_t k, double* out, double* err);
+
+/* src/hip_ops.hip:611-619 (gather_rows_kernel): out[r,:] = rows[indices[r],:]. */
+void orc_gather_rows(const void* rows, const int32_t* indices, int64_t cols, int64_t out_rows, void* out,
+                     int dtype);
+
+/* src/hip_ops.hip:813-844 (moe_route_kernel): softmax of each logits row in double, the
+ * top K by the reference's selection sort (swaps included), scores rounded to fp32,
+ * renormalised over the K when `norm`. */
+void orc_moe_route(const float* logits, int64_t rows, int E, int K, int norm, int32_t* idx, float* score);
+
+/* src/hip_ops.hip:861-893 (moe_ffn_kernel): out[t,o] = out_in[t,o] + sum_k w_k v_k[o] with
+ * v = dn_e . (silu(gu_e[:I] . x) * (gu_e[I:] . x)), e = slot_of[idx[t,k]], for w != 0 and
+ * 0 <= e < slots; in double over the exact inputs.  err[t,o]: a first-order bound on an fp32
+ * evaluation in any summation order -- each product's (n + 2) 2^-24 sum |terms|, carried
+ * through SiLU(g) * u by its derivatives plus 8 2^-24 |y| for expf and the divide, through
+ * the down product, the k-sum (K 2^-24 sum |w v|) and the final add. */
+void orc_moe_ffn(const void* x, int x_dtype, const int32_t* idx, const float* score, const uint16_t* gu,
+                 const uint16_t* dn, int w_bf16, const int32_t* slot_of, int64_t rows, int64_t H, int64_t I,
+                 int64_t K, int64_t slots, const double* out_in, double* out, double* err);
 
 /* KV store (src/hip_ops.hip:452-466) and paged attention (:468-550): see the
  * definitions for the exact indexing; attention is computed in double and

@@ -71,6 +71,23 @@ void ref_hip_gather_rows(const float* rows, const int32_t* indices, int rows_cou
   hip_gather_rows(rows, indices, rows_count, cols, out_rows, out);
   HIP_CHECK(hipDeviceSynchronize());
 }
+void ref_hip_moe_route(const float* logits, int rows, int E, int K, bool norm, int32_t* idx, float* score) {
+  hip_moe_route(logits, rows, E, K, norm, idx, score);
+  HIP_CHECK(hipDeviceSynchronize());
+}
+void ref_hip_moe_ffn(const float* x, const int32_t* idx, const float* score, const uint16_t* gu, const uint16_t* dn,
+                     const int32_t* slot_of, int rows, int H, int I, int K, bool bf16, float* out) {
+  hip_moe_ffn(x, idx, score, gu, dn, slot_of, rows, H, I, K, bf16, out);
+  HIP_CHECK(hipDeviceSynchronize());
+}
+void ref_hip_add_inplace(float* dst, const float* src, size_t n) {
+  hip_add_inplace(dst, src, n);
+  HIP_CHECK(hipDeviceSynchronize());
+}
+void ref_hip_scale_rows_sigmoid(float* dst, const float* s, int rows, int cols) {
+  hip_scale_rows_sigmoid(dst, s, rows, cols);
+  HIP_CHECK(hipDeviceSynchronize());
+}
 void ref_hip_store_kv(const float* key, const float* value, float* k_cache, float* v_cache, const int32_t* slots,
                       int tokens, int kv_heads, int head_dim) {
   hip_store_kv(key, value, k_cache, v_cache, slots, tokens, kv_heads, head_dim);

@@ -55,6 +55,8 @@ _ORACLE_SIGS = {
     "orc_matmul_q8": (None, [_vp, _i32, _vp, _vp, _i64, _i64, _i64, _vp, _vp, _vp, _vp]),
     "orc_matmul_w": (None, [_vp, _i32, _vp, _i32, _i32, _i64, _i64, _i64, _vp, _vp]),
     "orc_gather_rows": (None, [_vp, _vp, _i64, _i64, _vp, _i32]),
+    "orc_moe_route": (None, [_vp, _i64, _i32, _i32, _i32, _vp, _vp]),
+    "orc_moe_ffn": (None, [_vp, _i32, _vp, _vp, _vp, _vp, _i32, _vp, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _vp]),
 }
 
 _cache: dict[str, C.CDLL] = {}
@@ -112,6 +114,10 @@ def ref_hip() -> C.CDLL | None:
     h.ref_hip_matmul_qk.argtypes = [_vp, _vp, _i32, _i32, _i32, _vp, _i32]
     h.ref_hip_matmul_any_async.argtypes = [_i32, _vp, _vp, _i32, _i32, _i32, _vp]
     h.ref_hip_gather_rows.argtypes = [_vp, _vp, _i32, _i32, _i32, _vp]
+    h.ref_hip_moe_route.argtypes = [_vp, _i32, _i32, _i32, C.c_bool, _vp, _vp]
+    h.ref_hip_moe_ffn.argtypes = [_vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, C.c_bool, _vp]
+    h.ref_hip_add_inplace.argtypes = [_vp, _vp, C.c_size_t]
+    h.ref_hip_scale_rows_sigmoid.argtypes = [_vp, _vp, _i32, _i32]
     return h
 
 

@@ -820,3 +820,132 @@ def test_gather_rows_is_indexing(o, dt):
     out = np.empty((5, 40), rows.dtype)
     o.orc_gather_rows(H.ptr(rows), H.ptr(idx), 40, 5, H.ptr(out), dt)
     assert np.array_equal(out, rows[idx])
+
+
+# ---------------------------------------------------------------------------
+# MoE routing (src/hip_ops.hip:813-844) and expert FFN (:861-893)
+# ---------------------------------------------------------------------------
+def _route(o, logits, k, norm):
+    rows, e = logits.shape
+    idx = np.empty((rows, k), np.int32)
+    sc = np.empty((rows, k), np.float32)
+    o.orc_moe_route(H.ptr(np.ascontiguousarray(logits, np.float32)), rows, e, k, int(norm), H.ptr(idx), H.ptr(sc))
+    return idx, sc
+
+
+@pytest.mark.parametrize("norm", [False, True])
+def test_moe_route_is_sorted_softmax(o, norm):
+    """Distinct logits: the experts are the K largest in descending order and the scores the
+    softmax probabilities (renormalised over the K with norm), from numpy's own routes."""
+    r = H.rng(60 + norm)
+    logits = (r.permutation(64 * 40).reshape(40, 64) * 0.01 - 12.0).astype(np.float32)  # distinct values
+    idx, sc = _route(o, logits, 6, norm)
+    l64 = logits.astype(np.float64)
+    p = np.exp(l64 - l64.max(1, keepdims=True))
+    p /= p.sum(1, keepdims=True)
+    want = np.argsort(-l64, axis=1, kind="stable")[:, :6]
+    assert np.array_equal(idx, want)
+    top = np.take_along_axis(p, want, 1)
+    if norm:
+        top = top / top.sum(1, keepdims=True)
+    assert np.allclose(sc, top.astype(np.float32), rtol=2 ** -23, atol=0)
+
+
+@pytest.mark.parametrize("logits,k,want", [
+    ([1.0, 1.0, 1.0, 1.0], 4, [0, 1, 2, 3]),
+    ([1.0, 3.0, 1.0, 1.0], 3, [1, 0, 2]),
+    # the first round swaps expert 0 to position 2, behind expert 1: ties follow positions, not ids
+    ([1.0, 1.0, 3.0, 1.0], 3, [2, 1, 0]),
+    # round 2 swaps expert 0 (value 2) forward past experts 1 and 2, which end up reversed
+    ([2.0, 1.0, 1.0, 5.0, 1.0], 4, [3, 0, 2, 1]),
+])
+def test_moe_route_tie_order_is_the_selection_sorts(o, logits, k, want):
+    """Hand-worked selection sorts: each round takes the first position holding the maximum
+    among positions >= i, then swaps it with position i."""
+    idx, sc = _route(o, np.array([logits], np.float32), k, False)
+    assert idx[0].tolist() == want
+    assert np.all(np.diff(sc[0]) <= 0)
+
+
+def _moe_case(r, rows, hid, inter, k, n_exp, slots, w_bf16):
+    x = r.standard_normal((rows, hid)).astype(np.float32)
+    gu = H.to_storage((r.standard_normal((slots, 2 * inter, hid)) * 0.05).astype(np.float32), H.BF16 if w_bf16 else H.F16)
+    dn = H.to_storage((r.standard_normal((slots, hid, inter)) * 0.05).astype(np.float32), H.BF16 if w_bf16 else H.F16)
+    idx = np.stack([r.permutation(n_exp)[:k] for _ in range(rows)]).astype(np.int32)
+    score = r.uniform(0.05, 0.5, (rows, k)).astype(np.float32)
+    slot_of = r.permutation(slots)[:n_exp].astype(np.int32)
+    return x, gu, dn, idx, score, slot_of
+
+
+def _moe_oracle(o, x, x_dt, gu, dn, w_bf16, idx, score, slot_of, slots, out_in):
+    rows, hid = out_in.shape
+    inter = dn.shape[-1]
+    k = idx.shape[1]
+    out = np.empty((rows, hid), np.float64)
+    err = np.empty((rows, hid), np.float64)
+    o.orc_moe_ffn(H.ptr(x), x_dt, H.ptr(idx), H.ptr(score), H.ptr(gu), H.ptr(dn), int(w_bf16), H.ptr(slot_of), rows,
+                  hid, inter, k, slots, H.ptr(np.ascontiguousarray(out_in, np.float64)), H.ptr(out), H.ptr(err))
+    return out, err
+
+
+def test_moe_ffn_equals_numpy(o):
+    """Against numpy's float64 matrix products of the same experts; a pair with score 0 and
+    a pair whose expert has no slot (-1) add nothing."""
+    r = H.rng(61)
+    rows, hid, inter, k, n_exp, slots = 5, 48, 40, 3, 6, 8
+    x, gu, dn, idx, score, slot_of = _moe_case(r, rows, hid, inter, k, n_exp, slots, False)
+    score[1, 2] = 0.0
+    slot_of[idx[3, 0]] = -1
+    out_in = r.standard_normal((rows, hid))
+    out, err = _moe_oracle(o, x, H.F32, gu, dn, False, idx, score, slot_of, slots, out_in)
+    G = H.from_storage(gu, H.F16)
+    D = H.from_storage(dn, H.F16)
+    want = out_in.copy()
+    for t in range(rows):
+        for j in range(k):
+            s = slot_of[idx[t, j]]
+            if score[t, j] == 0 or s < 0:
+                continue
+            g, u = G[s, :inter] @ x[t].astype(np.float64), G[s, inter:] @ x[t].astype(np.float64)
+            want[t] += float(score[t, j]) * (D[s] @ (g / (1 + np.exp(-g)) * u))
+    assert np.allclose(out, want, rtol=1e-12, atol=1e-12)
+    assert (err > 0).all()
+
+
+def _ref_block_dot(a, b):
+    """The reference's block_dot (src/hip_ops.hip:846-859) in fp32: 256 strided partial
+    sums (fused multiply-adds), then one thread sums the partials in order."""
+    n = a.shape[-1]
+    part = np.zeros(256, np.float32)
+    for i in range(n):
+        part[i % 256] = np.float32(np.float64(part[i % 256]) + np.float64(a[i]) * np.float64(b[i]))
+    s = np.float32(0)
+    for v in part:
+        s = np.float32(s + v)
+    return s
+
+
+def test_moe_ffn_bound_covers_the_references_fp32_order(o):
+    """The reference kernel's own fp32 evaluation order (block_dot, expf, res += w * v as a
+    fused multiply-add, out += res) lies within the oracle's bound."""
+    r = H.rng(62)
+    rows, hid, inter, k, n_exp, slots = 3, 300, 260, 2, 4, 4
+    x, gu, dn, idx, score, slot_of = _moe_case(r, rows, hid, inter, k, n_exp, slots, True)
+    out_in = r.standard_normal((rows, hid)).astype(np.float32)
+    out, err = _moe_oracle(o, x, H.F32, gu, dn, True, idx, score, slot_of, slots, out_in.astype(np.float64))
+    G = H.from_storage(gu, H.BF16).astype(np.float32)
+    D = H.from_storage(dn, H.BF16).astype(np.float32)
+    for t in range(rows):
+        res = np.zeros(hid, np.float32)
+        for j in range(k):
+            s = slot_of[idx[t, j]]
+            ys = np.empty(inter, np.float32)
+            for c in range(inter):
+                gg = _ref_block_dot(x[t], G[s, c])
+                uu = _ref_block_dot(x[t], G[s, inter + c])
+                ys[c] = np.float32(np.float32(gg / np.float32(np.float32(1) + np.exp(-gg))) * uu)
+            for c in range(hid):
+                v = _ref_block_dot(ys, D[s, c])
+                res[c] = np.float32(np.float64(res[c]) + np.float64(score[t, j]) * np.float64(v))
+        got = (out_in[t] + res).astype(np.float64)
+        assert (np.abs(got - out[t]) <= err[t]).all()
