@@ -119,7 +119,7 @@ def main() -> int:
     emb_fmt = args.emb or cfg.emb
     nbytes = op_bytes(cfg, e, emb_fmt)
     only = set(filter(None, args.only.split(","))) or {"emb", "rms", "rope", "silu", "copy", "copy12", "copy12_emb",
-                                                       "gemm", "gemv", "split", "lm_head", "lm_head_q4k",
+                                                       "gemm", "gemv", "split", "lm_head", "lm_head_q4k", "moe",
                                                        "attn", "attn_decode", "attn_f32", "attn_decode_f32", "attn_decode_small", "layer", "layer_decode", "layer_b1", "layer_b1_graph"}
 
     def nsets(b: int) -> int:
@@ -189,6 +189,19 @@ def main() -> int:
             else:
                 lm_w = (torch.randn(V, Hd, generator=g, device=dev) * 0.05).to(torch.bfloat16)
             lm_sets[n_] = (lm_w, wf_, randn((1, Hd)), torch.empty(1, V, dtype=torch.float32, device=dev))
+    moe_in = None
+    if "moe" in only:  # Qwen3-30B-A3B's experts (H 2048, expert intermediate 768, 128 experts, top 8), bf16,
+        # 256 rows (config 1's decode batch) routed from random logits; workspace allocated once
+        mH, mI, mE, mK, mrows = 2048, 768, 128, 8, 256
+        m_gu = (torch.randn(mE, 2 * mI, mH, generator=g, device=dev) * 0.05).to(torch.bfloat16)
+        m_dn = (torch.randn(mE, mH, mI, generator=g, device=dev) * 0.05).to(torch.bfloat16)
+        m_x = torch.randn(mrows, mH, generator=g, device=dev)
+        m_idx, m_sc = ops.moe_route(torch.randn(mrows, mE, generator=g, device=dev), mK, True)
+        m_slot = torch.arange(mE, dtype=torch.int32, device=dev)
+        m_wb = ops.lib().nvf_moe_ffn_workspace_size(mrows, mH, mI, mK, mE)
+        moe_in = dict(H=mH, I=mI, E=mE, K=mK, rows=mrows, gu=m_gu, dn=m_dn, x=m_x, idx=m_idx, sc=m_sc, slot=m_slot,
+                      out=torch.zeros(mrows, mH, device=dev), work=torch.empty(m_wb, dtype=torch.uint8, device=dev),
+                      wb=m_wb, experts=int(torch.unique(m_idx).numel()))
     if "split" in only:  # gate_up weights as GGUF blocks, rotated like the GEMV's
         nb_split = 2 * I * Hd // 32
         for _ in range(nsets(nbytes["split"])):
@@ -386,6 +399,13 @@ def main() -> int:
             ops.matmul(x_, w_, V, wf_, out_dtype=torch.float32, out=o_)
         return f
 
+    def run_moe(i):
+        m = moe_in
+        ops._check(ops.lib().nvf_moe_ffn_ws(m["x"].data_ptr(), ops._dt(m["x"]), m["idx"].data_ptr(), m["sc"].data_ptr(),
+                                            m["gu"].data_ptr(), m["dn"].data_ptr(), 1, m["slot"].data_ptr(), m["rows"],
+                                            m["H"], m["I"], m["K"], m["E"], m["out"].data_ptr(), ops._dt(m["out"]),
+                                            m["work"].data_ptr(), m["wb"], ops._stream()), "moe_ffn")
+
     def run_split(i):
         blk_, w8_, ws_ = split_sets[i % len(split_sets)]
         ops._check(ops.lib().nvf_q8_0_split_blocks(blk_.data_ptr(), nb_split, w8_.data_ptr(), ws_.data_ptr(),
@@ -488,7 +508,7 @@ def main() -> int:
              ("rms_q8", run_rms_q8), ("silu_q8", run_silu_q8), ("copy", run_copy),
              ("copy12", run_copy12), ("copy12_emb", run_copy12_emb), ("gemm", run_gemm),
              ("gemv", run_gemv), ("split", run_split), ("lm_head", run_lm("lm_head")),
-             ("lm_head_q4k", run_lm("lm_head_q4k")), ("attn", run_attn), ("attn_decode", run_attn_decode),
+             ("lm_head_q4k", run_lm("lm_head_q4k")), ("moe", run_moe), ("attn", run_attn), ("attn_decode", run_attn_decode),
              ("attn_f32", run_attn_f32), ("attn_decode_f32", run_attn_decode_f32), ("attn_decode_small", run_attn_decode_small),
              ("layer", run_layer), ("layer_decode", run_layer_decode), ("layer_b1", run_layer_b1),
              ("layer_b1_graph", run_layer_b1_graph)]
@@ -546,6 +566,15 @@ def main() -> int:
         if n == "gemv":
             entry.pop("tokens_per_s")
             entry["shape"] = f"m={GEMV_M} n={2 * I} k={Hd} (gate_up, decode)"
+        elif n == "moe":
+            m = moe_in
+            wbytes = m["experts"] * 3 * m["H"] * m["I"] * 2
+            flops = 2.0 * m["rows"] * m["K"] * 3 * m["H"] * m["I"]
+            entry.update({"shape": f"MoE FFN, {m['rows']} rows, top {m['K']} of {m['E']} experts, H {m['H']}, expert "
+                                   f"intermediate {m['I']}, bf16 experts, fp32 activations (Qwen3-30B-A3B's shape)",
+                          "expert_weight_GB_s": round(wbytes / (t_us * 1e-6) / 1e9, 1),
+                          "TFLOP_s": round(flops / (t_us * 1e-6) / 1e12, 1),
+                          "frac_of_fp32_peak": round(flops / (t_us * 1e-6) / FP32_PEAK_FLOPS, 4)})
         elif n in ("lm_head", "lm_head_q4k"):
             entry.pop("tokens_per_s")
             entry["shape"] = (f"m=1 n={V} k={Hd} (LM head at decode, {'Q4_K' if n == 'lm_head_q4k' else 'bf16'} "
@@ -659,6 +688,7 @@ def main() -> int:
         "q8_gemv": res_ops.get("gemv"),
         "q8_0_split": res_ops.get("split"),
         "weight_gemv": {k: res_ops[k] for k in ("lm_head", "lm_head_q4k") if k in res_ops} or None,
+        "moe_ffn": res_ops.get("moe"),
         "layer": res_ops.get("layer"),
         "layer_decode": res_ops.get("layer_decode"),
         "layer_b1": res_ops.get("layer_b1"),

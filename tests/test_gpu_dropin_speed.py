@@ -1,8 +1,11 @@
 """The fp32 drop-in entry points against the reference's own kernels
 (src/hip_ops.hip built for gfx950 into oracle/_ref), timed on the same inputs
-in the same process at BASELINE config 2's shapes (Q4_K at config 4's).
+in the same process at BASELINE config 2's shapes (Q4_K at config 4's), plus the decode
+products of the other weight formats (bf16 LM head, Q4_K gate_up) and the MoE ops at
+Qwen3-30B-A3B's expert shape.
 
-Each pair is timed with HIP events, median of 20 launches after 3 warm-ups,
+Each pair is timed with HIP events, median of 20 launches after 3 warm-ups (3 for the
+MoE FFN, whose reference kernel takes about 0.3 s a call),
 inputs resident in HBM.  The test asserts only that the drop-in is faster (the
 measured margins are 1.4x and up) and prints the table; run it with -s to see
 it.  Skipped when oracle/_ref was not built."""
@@ -43,9 +46,9 @@ def median_us(f, it: int = 20) -> float:
     return float(np.median(ts))
 
 
-def compare(name: str, nbytes: float, ours, theirs) -> None:
+def compare(name: str, nbytes: float, ours, theirs, it: int = 20) -> None:
     print(f"[case] drop-in speed: {name}", flush=True)
-    to, tr = median_us(ours), median_us(theirs)
+    to, tr = median_us(ours, it), median_us(theirs, it)
     print(f"| {name} | {to:.1f} | {nbytes / to / 1e3:.0f} | {tr:.1f} | {nbytes / tr / 1e3:.0f} | {tr / to:.1f}x |",
           flush=True)
     assert to < tr, f"{name}: drop-in {to:.1f} us, reference {tr:.1f} us"
@@ -111,3 +114,38 @@ def test_dropins_faster_than_reference_kernels(gpu, ref):
     compare("Q4_K embedding gather [32768 x 3584], config 4", t4 * HID * 144 / 256 + 8.0 * t4 + t4 * HID * 4,
             lambda: lib.hip_embedding_qk(p(ids4), p(wq), t4, HID, p(eo4), 12),
             lambda: ref.ref_hip_embedding_qk(p(ids4), p(wq), t4, HID, p(eo4), 12))
+    del ids4, wq, eo4
+
+    # the other weight formats at decode: the LM head in bf16, gate_up in Q4_K (m = 1, fp32 logits)
+    xl = torch.randn(1, HID, device=gpu, generator=g)
+    wl = (torch.randn(VOCAB, HID, device=gpu, generator=g) * 0.05).to(torch.bfloat16)
+    ol = torch.empty(1, VOCAB, device=gpu)
+    compare("bf16 LM head at decode, m = 1 [152064, 3584]", VOCAB * HID * 2 + HID * 4 + VOCAB * 4,
+            lambda: lib.hip_matmul_u16(p(xl), p(wl), 1, VOCAB, HID, p(ol), True),
+            lambda: ref.ref_hip_matmul_u16(p(xl), p(wl), 1, VOCAB, HID, p(ol), True))
+    del wl, ol
+    wg = torch.randint(0, 256, (2 * INTER * HID // 256, 144), device=gpu, dtype=torch.uint8, generator=g)
+    wg[:, 0:4] = torch.tensor([0x1E, 0x1C, 0x1E, 0x1C], dtype=torch.uint8, device=gpu)  # d, dmin ~ 4e-3
+    og = torch.empty(1, 2 * INTER, device=gpu)
+    compare("Q4_K gate_up at decode, m = 1 [37888, 3584]", 2 * INTER * HID // 256 * 144 + HID * 4 + 2 * INTER * 4,
+            lambda: lib.hip_matmul_qk(p(xl), p(wg), 1, 2 * INTER, HID, p(og), 12),
+            lambda: ref.ref_hip_matmul_qk(p(xl), p(wg), 1, 2 * INTER, HID, p(og), 12))
+    del wg, og
+
+    # MoE at Qwen3-30B-A3B's expert shape: routing 256 rows; the FFN for one decode token
+    mH, mI, mE, mK = 2048, 768, 128, 8
+    lg = torch.randn(256, mE, device=gpu, generator=g)
+    idx = torch.empty(256, mK, dtype=torch.int32, device=gpu)
+    sc = torch.empty(256, mK, device=gpu)
+    compare("MoE routing, 256 rows x 128 experts, top 8", 256 * mE * 4 + 256 * mK * 8,
+            lambda: lib.hip_moe_route(p(lg), 256, mE, mK, True, p(idx), p(sc)),
+            lambda: ref.ref_hip_moe_route(p(lg), 256, mE, mK, True, p(idx), p(sc)))
+    mgu = (torch.randn(mE, 2 * mI, mH, device=gpu, generator=g) * 0.05).to(torch.bfloat16)
+    mdn = (torch.randn(mE, mH, mI, device=gpu, generator=g) * 0.05).to(torch.bfloat16)
+    slot_of = torch.arange(mE, dtype=torch.int32, device=gpu)
+    mx = torch.randn(1, mH, device=gpu, generator=g)
+    mo = torch.zeros(1, mH, device=gpu)
+    compare("MoE expert FFN, 1 token, top 8 of 128 (bf16 experts)", mK * 3 * mH * mI * 2,
+            lambda: lib.hip_moe_ffn(p(mx), p(idx), p(sc), p(mgu), p(mdn), p(slot_of), 1, mH, mI, mK, True, p(mo)),
+            lambda: ref.ref_hip_moe_ffn(p(mx), p(idx), p(sc), p(mgu), p(mdn), p(slot_of), 1, mH, mI, mK, True, p(mo)),
+            it=3)
