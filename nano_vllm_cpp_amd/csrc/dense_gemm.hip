@@ -179,6 +179,10 @@ template <>
 struct RunOf<Q6KGroup> {
   static constexpr int value = 32;
 };
+template <>
+struct GemvPrefetch<Q6KGroup> {
+  static constexpr bool value = false;
+};
 
 // ---------------------------------------------------------------------------
 // Decode-shaped products (m <= 16 rows, k a multiple of the run below): bound by streaming the

@@ -282,6 +282,52 @@ struct RunOf<Table<8, T>> {
   static constexpr int value = 8;
 };
 
+
+// bf16 weight rows take the split product: each fp32 activation is the exact sum of
+// three bf16 pieces (RNE to 8 bits, then the remainder, twice: 24 = 3 x 8 significand
+// bits), so the three bf16 matrix-core products x_i . w are exact products summed in
+// fp32 -- 3k terms instead of k, at 16 / 3 times the fp32 matrix-core rate.
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+// Whether the decode product double-buffers a source's raw loads: measured per
+// source -- it pays for fp16 / bf16 rows and Q4_K / Q5_K groups, and costs more in
+// occupancy than it gains for fp32 rows and Q6_K groups (larger raw registers).
+template <typename S>
+struct GemvPrefetch {
+  static constexpr bool value = true;
+};
+template <>
+struct GemvPrefetch<Table<8, float>> {
+  static constexpr bool value = false;
+};
+
+template <typename S>
+struct SplitBf16 {
+  static constexpr bool value = false;
+};
+template <>
+struct SplitBf16<Table<8, __bf16>> {
+  static constexpr bool value = true;
+};
+__device__ __forceinline__ void split3(const float* v, bf16x8* p) {
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const __bf16 a = (__bf16)v[i];
+    const float r1 = v[i] - (float)a;  // exact: the bits below a's 8
+    const __bf16 b = (__bf16)r1;
+    const float r2 = r1 - (float)b;    // exact, and at most 8 significant bits
+    p[0][i] = a;
+    p[1][i] = b;
+    p[2][i] = (__bf16)r2;
+  }
+}
+__device__ __forceinline__ bf16x8 raw_bf16x8(const Table<8, __bf16>::Raw& r) {
+  return __builtin_bit_cast(bf16x8, u32x4{r.w[0], r.w[1], r.w[2], r.w[3]});
+}
+template <typename T>
+__device__ __forceinline__ bf16x8 raw_bf16x8(const T&) {  // never called: the split takes bf16 rows only
+  return bf16x8{};
+}
+
 template <typename TX, int R>
 __device__ __forceinline__ void load_x_run(const Table<8, TX>& xs, int64_t e0, typename Table<8, TX>::Raw* xr) {
 #pragma unroll
@@ -297,66 +343,122 @@ template <typename TX, typename Src, int C, typename P>
 __global__ __launch_bounds__(kGvWaves * 64) void gemv_mfma_kernel(const TX* __restrict__ x, Src w, P prob,
                                                                   int64_t k) {
   constexpr int R = RunOf<Src>::value, H = R == 8 ? 2 : 1, SPAN = H * R, KS = 4 * SPAN;
+  constexpr bool kSplit = SplitBf16<Src>::value;
   __shared__ float part[kGvWaves][C][16][17];  // [wave][group][row][column] (padded)
   const int lane = threadIdx.x & 63, j = lane & 15, ks = lane >> 4;
   const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const Table<8, TX> xs{x};
+  struct Buf {  // one step's raw loads
+    typename Src::Raw w[C][H];
+    typename Table<8, TX>::Raw x[H][R / 8];
+  };
   for (int64_t item = blockIdx.x;; item += gridDim.x) {
     typename P::Tile tile;
     if (!prob.tile(item, 16 * C, tile)) break;  // uniform per workgroup
-    const int64_t nsteps = (k + KS - 1) / KS;
+    const int64_t nsteps = (k + KS - 1) / KS, full = k / KS;  // steps; steps every lane's runs are inside
     const int64_t s_begin = nsteps * wave / kGvWaves, s_end = nsteps * (wave + 1) / kGvWaves;
-    const Table<8, TX> xs{x};
-    const int64_t x_off = prob.a_row(tile, j);
+    const int64_t f_end = s_end < full ? s_end : full;
+    // a row or column outside the problem reads row 0 of its operand instead (valid
+    // memory; its results are never stored), so the loop has no per-lane branches
+    int64_t x_off = prob.a_row(tile, j);
     const bool row_ok = x_off >= 0;
+    if (!row_ok) x_off = 0;
     int64_t w_off[C];
     bool col_ok[C];
 #pragma unroll
     for (int q = 0; q < C; ++q) {
       w_off[q] = prob.b_row(tile, 16 * q + j);
       col_ok[q] = w_off[q] >= 0;
+      if (!col_ok[q]) w_off[q] = 0;
     }
     f32x4 acc[C];
 #pragma unroll
     for (int q = 0; q < C; ++q) acc[q] = f32x4{};
 
-    for (int64_t s = s_begin; s < s_end; ++s) {
-      const int64_t kk = s * KS + (int64_t)SPAN * ks;
-      typename Src::Raw wr[C][H];
-      typename Table<8, TX>::Raw xr[H][R / 8];
-      bool h_ok[H];
+    // lane runs h of step st: k = st KS + SPAN ks + R h .. + R; `lim` masks the runs
+    // of a partial last step (every run is inside on a full step)
+    auto load = [&](Buf& f, int64_t st, bool partial) {
+      const int64_t kk = st * KS + (int64_t)SPAN * ks;
 #pragma unroll
       for (int h = 0; h < H; ++h) {
-        h_ok[h] = kk + R * h < k;
+        if (partial && kk + R * h >= k) continue;
 #pragma unroll
-        for (int q = 0; q < C; ++q)
-          if (h_ok[h] && col_ok[q]) wr[q][h] = w.load(w_off[q] + kk + R * h);
-        if (h_ok[h] && row_ok) load_x_run<TX, R>(xs, x_off + kk + R * h, xr[h]);
+        for (int q = 0; q < C; ++q) f.w[q][h] = w.load(w_off[q] + kk + R * h);
+        // without the prefetch every step waits for all its loads, so a row outside the
+        // problem may skip its load (its lanes' results are not stored)
+        if (GemvPrefetch<Src>::value || row_ok) load_x_run<TX, R>(xs, x_off + kk + R * h, f.x[h]);
       }
+    };
+    auto compute = [&](const Buf& f, int64_t st, bool partial) {
+      const int64_t kk = st * KS + (int64_t)SPAN * ks;
 #pragma unroll
       for (int h = 0; h < H; ++h) {
+        const bool in = !partial || kk + R * h < k;
         float xv[R];
-        if (h_ok[h] && row_ok) {
-          decode_x_run<TX, R>(xs, xr[h], xv);
+        if (in) {
+          decode_x_run<TX, R>(xs, f.x[h], xv);
         } else {
 #pragma unroll
           for (int i = 0; i < R; ++i) xv[i] = 0.0f;
         }
+        if constexpr (kSplit) {
+          // x = x1 + x2 + x3 exactly in bf16; each piece times a bf16 weight is exact in fp32
+          bf16x8 xp[3];
+          split3(xv, xp);
 #pragma unroll
-        for (int q = 0; q < C; ++q) {
-          float wv[R];
-          if (h_ok[h] && col_ok[q]) {
-            w.decode(wr[q][h], wv);
-          } else {
+          for (int q = 0; q < C; ++q) {
+            const bf16x8 wb = in ? raw_bf16x8(f.w[q][h]) : bf16x8{};
 #pragma unroll
-            for (int i = 0; i < R; ++i) wv[i] = 0.0f;
+            for (int pc = 2; pc >= 0; --pc)  // the smallest pieces first
+              acc[q] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xp[pc], wb, acc[q], 0, 0, 0);
           }
+        } else {
 #pragma unroll
-          for (int i = 0; i < R; ++i) acc[q] = __builtin_amdgcn_mfma_f32_16x16x4f32(xv[i], wv[i], acc[q], 0, 0, 0);
+          for (int q = 0; q < C; ++q) {
+            float wv[R];
+            if (in) {
+              w.decode(f.w[q][h], wv);
+            } else {
+#pragma unroll
+              for (int i = 0; i < R; ++i) wv[i] = 0.0f;
+            }
+#pragma unroll
+            for (int i = 0; i < R; ++i) acc[q] = __builtin_amdgcn_mfma_f32_16x16x4f32(xv[i], wv[i], acc[q], 0, 0, 0);
+          }
         }
       }
+    };
+    // full steps; with GemvPrefetch, two raw buffers in turn with the next step's loads
+    // in flight, the prefetch unconditional (the last step reloads itself), which keeps
+    // the memory-counter waits exact
+    Buf fa;
+    int64_t st = s_begin;
+    if constexpr (GemvPrefetch<Src>::value) {
+      Buf fb;
+      if (st < f_end) {
+        const int64_t last = f_end - 1;
+        load(fa, st, false);
+        while (true) {
+          load(fb, st + 1 < last ? st + 1 : last, false);
+          compute(fa, st, false);
+          if (++st >= f_end) break;
+          load(fa, st + 1 < last ? st + 1 : last, false);
+          compute(fb, st, false);
+          if (++st >= f_end) break;
+        }
+      }
+    } else {
+      for (; st < f_end; ++st) {
+        load(fa, st, false);
+        compute(fa, st, false);
+      }
+    }
+    if (f_end < s_end) {  // the partial last step
+      load(fa, f_end, true);
+      compute(fa, f_end, true);
     }
 
-    // D of v_mfma_f32_16x16x4_f32: lane l, value r -> row 4 (l / 16) + r, column l % 16
+    // D of v_mfma_f32_16x16x4_f32 and 16x16x32_bf16: lane l, value r -> row 4 (l / 16) + r, column l % 16
 #pragma unroll
     for (int q = 0; q < C; ++q)
 #pragma unroll

@@ -6,7 +6,9 @@ Bars:
 * GEMM outputs within the oracle's bound `err` = (k + 2) 2^-24 sum_i |x_i w_i|
   around the exact (float64) product of the exactly decoded weights, which covers
   fp32 sums in any order (tests/test_oracle.py pins it against three orders), plus
-  half an ulp of the output dtype for fp16/bf16 outputs;
+  half an ulp of the output dtype for fp16/bf16 outputs.  bf16 weights: three times
+  that bound -- the decode product splits each activation into three bf16 pieces whose
+  exact products it sums in fp32, 3k terms instead of k;
 * bit-exact where every fp32 partial sum is exact (small integer activations,
   weights that are small multiples of 1/8);
 * the reference's own kernels (oracle/_ref, where built) held to the same bound on
@@ -53,9 +55,10 @@ def oracle_matmul(x, x_dt, w, w_format, m, n, k, layout=H.GGML):
     return out, err
 
 
-def assert_within(got: np.ndarray, ideal: np.ndarray, err: np.ndarray, out_dt: int, what: str) -> None:
+def assert_within(got: np.ndarray, ideal: np.ndarray, err: np.ndarray, out_dt: int, what: str,
+                  w_format: int | None = None) -> None:
     g = H.from_storage(got, out_dt)
-    tol = err + (0.0 if out_dt == H.F32 else 0.5 * H.ulp(ideal, out_dt))
+    tol = (3.0 if w_format == H.BF16 else 1.0) * err + (0.0 if out_dt == H.F32 else 0.5 * H.ulp(ideal, out_dt))
     bad = ~(np.abs(g - ideal) <= tol)
     if bad.any():
         i = tuple(np.argwhere(bad)[0])
@@ -79,7 +82,7 @@ def test_matmul_within_bound(gpu, w_format, x_dt, m, n, k):
         case(f"nvf_matmul fmt={w_format} x={x_dt} out={out_dt} m={m} n={n} k={k}")
         got = ops.matmul(H.to_dev(x, gpu, x_dt), w_dev(w, w_format, gpu), n, w_format,
                          out_dtype=H.torch_dtype(out_dt))
-        assert_within(H.to_host(got), ideal, err, out_dt, f"fmt {w_format} x {x_dt} out {out_dt}")
+        assert_within(H.to_host(got), ideal, err, out_dt, f"fmt {w_format} x {x_dt} out {out_dt}", w_format)
 
 
 @pytest.mark.parametrize("w_format", FORMATS, ids=FMT_IDS)
@@ -92,7 +95,7 @@ def test_matmul_ragged_k(gpu, w_format, m, n, k):
     ideal, err = oracle_matmul(x, H.F32, w, w_format, m, n, k)
     case(f"nvf_matmul ragged fmt={w_format} m={m} n={n} k={k}")
     got = ops.matmul(H.to_dev(x, gpu), w_dev(w, w_format, gpu), n, w_format)
-    assert_within(H.to_host(got), ideal, err, H.F32, f"ragged fmt {w_format}")
+    assert_within(H.to_host(got), ideal, err, H.F32, f"ragged fmt {w_format}", w_format)
 
 
 @pytest.mark.parametrize("w_format", FORMATS, ids=FMT_IDS)
@@ -110,7 +113,7 @@ def test_matmul_decode_rows(gpu, w_format, m, n, k):
     ideal, err = oracle_matmul(x, H.BF16, w, w_format, m, n, k)
     case(f"nvf_matmul decode fmt={w_format} m={m} n={n} k={k}")
     got = ops.matmul(H.to_dev(x, gpu, H.BF16), w_dev(w, w_format, gpu), n, w_format, out_dtype=torch.float32)
-    assert_within(H.to_host(got), ideal, err, H.F32, f"decode fmt {w_format}")
+    assert_within(H.to_host(got), ideal, err, H.F32, f"decode fmt {w_format}", w_format)
 
 
 @pytest.mark.parametrize("w_format", [H.F32, H.BF16, 14], ids=["f32", "bf16", "q6k"])
@@ -136,7 +139,7 @@ def test_matmul_unaligned_operands(gpu, w_format, m):
         wv = wb[2:]
     case(f"nvf_matmul unaligned fmt={w_format} m={m}")
     got = ops.matmul(xv, wv, n, w_format)
-    assert_within(H.to_host(got), ideal, err, H.F32, f"unaligned fmt {w_format}")
+    assert_within(H.to_host(got), ideal, err, H.F32, f"unaligned fmt {w_format}", w_format)
 
 
 @pytest.mark.parametrize("w_format", [H.F32, H.F16, H.BF16], ids=DT_IDS)
@@ -201,7 +204,7 @@ def test_dropin_matmul_vs_oracle(gpu, w_format, m, n, k):
     case(f"drop-in matmul fmt={w_format} m={m} n={n} k={k}")
     dropin(ops.lib(), w_format, d_x, d_w, m, n, k, out)
     torch.cuda.synchronize()
-    assert_within(out.cpu().numpy(), ideal, err, H.F32, f"drop-in fmt {w_format}")
+    assert_within(out.cpu().numpy(), ideal, err, H.F32, f"drop-in fmt {w_format}", w_format)
 
 
 @pytest.mark.parametrize("w_format", FORMATS, ids=FMT_IDS)
@@ -241,7 +244,7 @@ def test_dropin_matmul_vs_reference_kernels(gpu, ref, w_format, m, n, k):
         if w_format == 12:
             ops._check(ops.lib().nvf_set_dropin_q4k_layout(H.GGML), "set layout")
     assert_within(theirs.cpu().numpy(), ideal, err, H.F32, f"reference kernel fmt {w_format}")
-    assert_within(mine.cpu().numpy(), ideal, err, H.F32, f"drop-in fmt {w_format}")
+    assert_within(mine.cpu().numpy(), ideal, err, H.F32, f"drop-in fmt {w_format}", w_format)
 
 
 @pytest.mark.parametrize("dt", DTYPES, ids=DT_IDS)
