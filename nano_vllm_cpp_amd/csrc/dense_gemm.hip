@@ -386,6 +386,12 @@ int launch_dense(const void* x, const Src& src, void* out, int64_t m, int64_t n,
   } else {
     const dim3 g((unsigned)(((m + 127) / 128) * tiles_n));
     const PlainProb<128, TO> prob{op, m, n, k};
+    if constexpr (SplitTile<Src>::value) {  // fp16 / bf16 weights: the split product on the bf16 matrix cores
+      if (!ragged) {
+        gemm_tile_split_kernel<TX><<<g, kDgThreads, 0, st>>>(xp, src, prob, k, tiles_n);
+        return launch_status("dense_gemm (split)");
+      }
+    }
     if (ragged)
       gemm_tile_kernel<TX, Src, 128, true><<<g, kDgThreads, 0, st>>>(xp, src, prob, k, tiles_n);
     else

@@ -24,6 +24,66 @@ namespace nvf {
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
+// bf16 weight rows take the split product: each fp32 activation is the exact sum of
+// three bf16 pieces (RNE to 8 bits, then the remainder, twice: 24 = 3 x 8 significand
+// bits), so the three bf16 matrix-core products x_i . w are exact products summed in
+// fp32 -- 3k terms instead of k, at 16 / 3 times the fp32 matrix-core rate.
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+// Whether the decode product double-buffers a source's raw loads: measured per
+// source -- it pays for fp16 / bf16 rows and Q4_K / Q5_K groups, and costs more in
+// occupancy than it gains for fp32 rows and Q6_K groups (larger raw registers).
+template <typename S>
+struct GemvPrefetch {
+  static constexpr bool value = true;
+};
+template <>
+struct GemvPrefetch<Table<8, float>> {
+  static constexpr bool value = false;
+};
+
+template <typename S>
+struct SplitBf16 {
+  static constexpr bool value = false;
+};
+template <>
+struct SplitBf16<Table<8, __bf16>> {
+  static constexpr bool value = true;
+};
+// the tile kernel splits fp16 weights too (two exact bf16 pieces each)
+template <typename S>
+struct SplitTile {
+  static constexpr bool value = false;
+};
+template <>
+struct SplitTile<Table<8, __bf16>> {
+  static constexpr bool value = true;
+};
+template <>
+struct SplitTile<Table<8, _Float16>> {
+  static constexpr bool value = true;
+};
+__device__ __forceinline__ void split3(const float* v, bf16x8* p) {
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const __bf16 a = (__bf16)v[i];
+    const float r1 = v[i] - (float)a;  // exact: the bits below a's 8
+    const __bf16 b = (__bf16)r1;
+    const float r2 = r1 - (float)b;    // exact, and at most 8 significant bits
+    p[0][i] = a;
+    p[1][i] = b;
+    p[2][i] = (__bf16)r2;
+  }
+}
+__device__ __forceinline__ bf16x8 raw_bf16x8(const Table<8, __bf16>::Raw& r) {
+  return __builtin_bit_cast(bf16x8, u32x4{r.w[0], r.w[1], r.w[2], r.w[3]});
+}
+template <typename T>
+__device__ __forceinline__ bf16x8 raw_bf16x8(const T&) {  // never called: the split takes bf16 rows only
+  return bf16x8{};
+}
+
+
 constexpr int kDgBN = 128;           // output columns per workgroup
 constexpr int kDgKC = 16;            // k elements per LDS stage
 constexpr int kDgRow = kDgKC + 4;    // LDS floats per staged row (padded)
@@ -237,6 +297,129 @@ __global__ __launch_bounds__(kDgThreads) __attribute__((amdgpu_waves_per_eu(2)))
   }
 }
 
+// fp16 / bf16 weight rows on the bf16 matrix cores (BM = 128, k % 16 == 0,
+// vector-aligned operands): the tile kernel's structure with each staged activation
+// split into three bf16 pieces (split3: exact) and each weight staged as it is (bf16)
+// or as two bf16 pieces (fp16: 11 significand bits = 8 + the exact remainder), so
+// 3 x WP v_mfma_f32_32x32x16_bf16 per 16-k stage and 32 x 32 tile sum exact products
+// in fp32 (3 WP k terms instead of k).  LDS per stage: three activation planes and WP
+// weight planes, rows of 16 bf16 padded to 48 bytes (the 16 rows of a ds_read_b128
+// phase hit distinct bank groups: 3 r mod 16).  Lane l reads 8 bf16 of row l % 32 at
+// k slot 8 (l / 32) for both operands, so the instruction contracts matching k.
+constexpr int kSpRow = 24;  // bf16 per staged row (16 + padding)
+template <typename TX, typename TW, typename P>
+__global__ __launch_bounds__(kDgThreads) __attribute__((amdgpu_waves_per_eu(2))) void gemm_tile_split_kernel(
+    const TX* __restrict__ x, Table<8, TW> w, P prob, int64_t k, int tiles_n) {
+  constexpr int BM = 128, WN = 2, TM = 2, TN = 2;
+  constexpr int WP = __is_same(TW, __bf16) ? 1 : 2;                 // weight pieces
+  constexpr int kPlane = BM * kSpRow, kStage = (3 + WP) * kPlane;  // activation planes + weight planes (bf16)
+  __shared__ __attribute__((aligned(16))) __bf16 lds[2 * kStage];
+  for (int64_t item = blockIdx.x;; item += gridDim.x) {
+    typename P::Tile tile;
+    if (!prob.tile(item, tiles_n, tile)) break;  // uniform per workgroup
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave / WN, wn = wave % WN;
+    // staging: thread t moves 8 k-values (half t & 1 of the stage) of activation row
+    // t >> 1 and of weight column t >> 1
+    const int sr = tid >> 1, sh = (tid & 1) * 8;
+    const int64_t a_off = prob.a_row(tile, sr), b_off = prob.b_row(tile, sr);
+    const bool a_ok = a_off >= 0, b_ok = b_off >= 0;
+    const Table<8, TX> xs{x};
+    typename Table<8, TX>::Raw ar;
+    typename Table<8, TW>::Raw br;
+    auto load = [&](int st) {
+      const int64_t kc = (int64_t)st * kDgKC + sh;
+      if (a_ok) ar = xs.load(a_off + kc);
+      if (b_ok) br = w.load(b_off + kc);
+    };
+    auto store = [&](int buf) {
+      __bf16* s = lds + buf * kStage;
+      float v[8];
+      if (a_ok) {
+        xs.decode(ar, v);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = 0.0f;
+      }
+      bf16x8 p[3];
+      split3(v, p);
+#pragma unroll
+      for (int pc = 0; pc < 3; ++pc) st16(s + pc * kPlane + sr * kSpRow + sh, __builtin_bit_cast(u32x4, p[pc]));
+      if constexpr (WP == 1) {
+        st16(s + 3 * kPlane + sr * kSpRow + sh, b_ok ? u32x4{br.w[0], br.w[1], br.w[2], br.w[3]} : u32x4{});
+      } else {
+        float wv[8];
+        if (b_ok) {
+          w.decode(br, wv);
+        } else {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) wv[i] = 0.0f;
+        }
+        bf16x8 q[3];
+        split3(wv, q);  // an fp16 value: q[2] is 0
+        st16(s + 3 * kPlane + sr * kSpRow + sh, __builtin_bit_cast(u32x4, q[0]));
+        st16(s + 4 * kPlane + sr * kSpRow + sh, __builtin_bit_cast(u32x4, q[1]));
+      }
+    };
+
+    f32x16 acc[TM][TN];
+#pragma unroll
+    for (int a = 0; a < TM; ++a)
+#pragma unroll
+      for (int b = 0; b < TN; ++b) acc[a][b] = f32x16{};
+    const int half = lane >> 5;
+    const int fa = (TM * 32 * wm + (lane & 31)) * kSpRow + 8 * half;
+    const int fb = (TN * 32 * wn + (lane & 31)) * kSpRow + 8 * half;
+
+    const int nst = (int)(k / kDgKC);
+    load(0);
+    store(0);
+    __syncthreads();
+#pragma unroll 1
+    for (int st = 0; st < nst; ++st) {
+      const __bf16* s = lds + (st & 1) * kStage;
+      if (st + 1 < nst) load(st + 1);  // in flight during this stage's MFMAs
+#pragma unroll
+      for (int wq = WP - 1; wq >= 0; --wq) {  // the smallest pieces first
+        bf16x8 bv[TN];
+#pragma unroll
+        for (int b = 0; b < TN; ++b)
+          bv[b] = __builtin_bit_cast(bf16x8, ld16(s + (3 + wq) * kPlane + fb + b * 32 * kSpRow));
+#pragma unroll
+        for (int pc = 2; pc >= 0; --pc) {
+          bf16x8 av[TM];
+#pragma unroll
+          for (int a = 0; a < TM; ++a)
+            av[a] = __builtin_bit_cast(bf16x8, ld16(s + pc * kPlane + fa + a * 32 * kSpRow));
+#pragma unroll
+          for (int a = 0; a < TM; ++a)
+#pragma unroll
+            for (int b = 0; b < TN; ++b)
+              acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[a], bv[b], acc[a][b], 0, 0, 0);
+        }
+      }
+      if (st + 1 < nst) {
+        store((st + 1) & 1);  // the other buffer: its last readers passed the previous barrier
+        __syncthreads();
+      }
+    }
+
+    // D layout of the 32 x 32 MFMAs: lane l, value j -> column l % 32,
+    // row 8 (j / 4) + 4 (l / 32) + j % 4
+#pragma unroll
+    for (int a = 0; a < TM; ++a)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const int r = TM * 32 * wm + 32 * a + 8 * (j >> 2) + 4 * half + (j & 3);
+#pragma unroll
+        for (int b = 0; b < TN; ++b) prob.store(tile, r, TN * 32 * wn + 32 * b + (lane & 31), acc[a][b][j]);
+      }
+    if constexpr (!P::kLoop) break;  // one item per workgroup
+    __syncthreads();                 // LDS is reused by the next item
+  }
+}
+
 // The plain GEMM: out[m][n] (row-major, TO) = x[m][k] . W[n][k]^T, tiles in dg_tile's
 // XCD-aware order.
 template <int BM, typename TO>
@@ -282,51 +465,6 @@ struct RunOf<Table<8, T>> {
   static constexpr int value = 8;
 };
 
-
-// bf16 weight rows take the split product: each fp32 activation is the exact sum of
-// three bf16 pieces (RNE to 8 bits, then the remainder, twice: 24 = 3 x 8 significand
-// bits), so the three bf16 matrix-core products x_i . w are exact products summed in
-// fp32 -- 3k terms instead of k, at 16 / 3 times the fp32 matrix-core rate.
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-// Whether the decode product double-buffers a source's raw loads: measured per
-// source -- it pays for fp16 / bf16 rows and Q4_K / Q5_K groups, and costs more in
-// occupancy than it gains for fp32 rows and Q6_K groups (larger raw registers).
-template <typename S>
-struct GemvPrefetch {
-  static constexpr bool value = true;
-};
-template <>
-struct GemvPrefetch<Table<8, float>> {
-  static constexpr bool value = false;
-};
-
-template <typename S>
-struct SplitBf16 {
-  static constexpr bool value = false;
-};
-template <>
-struct SplitBf16<Table<8, __bf16>> {
-  static constexpr bool value = true;
-};
-__device__ __forceinline__ void split3(const float* v, bf16x8* p) {
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const __bf16 a = (__bf16)v[i];
-    const float r1 = v[i] - (float)a;  // exact: the bits below a's 8
-    const __bf16 b = (__bf16)r1;
-    const float r2 = r1 - (float)b;    // exact, and at most 8 significant bits
-    p[0][i] = a;
-    p[1][i] = b;
-    p[2][i] = (__bf16)r2;
-  }
-}
-__device__ __forceinline__ bf16x8 raw_bf16x8(const Table<8, __bf16>::Raw& r) {
-  return __builtin_bit_cast(bf16x8, u32x4{r.w[0], r.w[1], r.w[2], r.w[3]});
-}
-template <typename T>
-__device__ __forceinline__ bf16x8 raw_bf16x8(const T&) {  // never called: the split takes bf16 rows only
-  return bf16x8{};
-}
 
 template <typename TX, int R>
 __device__ __forceinline__ void load_x_run(const Table<8, TX>& xs, int64_t e0, typename Table<8, TX>::Raw* xr) {

@@ -465,6 +465,12 @@ int moe_product(const TX* a, const TW* w, Prob prob, int64_t k, const MoePlan& p
     prob.cols = kDgBN;
     const int tiles_n = (int)((prob.n_cols + kDgBN - 1) / kDgBN);
     const dim3 g = moe_grid(max_tiles, tiles_n);
+    if constexpr (SplitTile<Table<8, TW>>::value) {  // the split product on the bf16 matrix cores
+      if (plan.bm == 128 && vec) {
+        gemm_tile_split_kernel<TX><<<g, kDgThreads, 0, st>>>(a, src, prob, k, tiles_n);
+        return launch_status("moe expert product (split)");
+      }
+    }
     if (plan.bm == 128)
       vec ? gemm_tile_kernel<TX, Table<8, TW>, 128, false><<<g, kDgThreads, 0, st>>>(a, src, prob, k, tiles_n)
           : gemm_tile_kernel<TX, Table<8, TW>, 128, true><<<g, kDgThreads, 0, st>>>(a, src, prob, k, tiles_n);

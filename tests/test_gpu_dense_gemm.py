@@ -7,8 +7,9 @@ Bars:
   around the exact (float64) product of the exactly decoded weights, which covers
   fp32 sums in any order (tests/test_oracle.py pins it against three orders), plus
   half an ulp of the output dtype for fp16/bf16 outputs.  bf16 weights: three times
-  that bound -- the decode product splits each activation into three bf16 pieces whose
-  exact products it sums in fp32, 3k terms instead of k;
+  that bound, fp16 weights six times -- the split products take each activation as three
+  exact bf16 pieces (and an fp16 weight as two) and sum the exact piece products in
+  fp32, 3k (6k) terms instead of k;
 * bit-exact where every fp32 partial sum is exact (small integer activations,
   weights that are small multiples of 1/8);
 * the reference's own kernels (oracle/_ref, where built) held to the same bound on
@@ -58,7 +59,7 @@ def oracle_matmul(x, x_dt, w, w_format, m, n, k, layout=H.GGML):
 def assert_within(got: np.ndarray, ideal: np.ndarray, err: np.ndarray, out_dt: int, what: str,
                   w_format: int | None = None) -> None:
     g = H.from_storage(got, out_dt)
-    tol = (3.0 if w_format == H.BF16 else 1.0) * err + (0.0 if out_dt == H.F32 else 0.5 * H.ulp(ideal, out_dt))
+    tol = {H.BF16: 3.0, H.F16: 6.0}.get(w_format, 1.0) * err + (0.0 if out_dt == H.F32 else 0.5 * H.ulp(ideal, out_dt))
     bad = ~(np.abs(g - ideal) <= tol)
     if bad.any():
         i = tuple(np.argwhere(bad)[0])

@@ -7,9 +7,9 @@ Bars:
   included); scores bit-exact against the reference's kernel (the same device exp), and
   within one fp32 ulp of the oracle (host libm exp);
 * FFN: every output within twice the oracle's first-order fp32 bound `err` (plus half an
-  ulp for 16-bit outputs) around its float64 value -- six times for bf16 experts, whose
-  decode products sum three exact bf16 piece products per term; the reference's own
-  kernel is held to the same bar on the same inputs;
+  ulp for 16-bit outputs) around its float64 value -- six times for bf16 experts and
+  twelve for fp16 ones, whose split products sum three (six) exact bf16 piece products
+  per term; the reference's own kernel is held to the same bar on the same inputs;
 * add_inplace bit-exact; scale_rows_sigmoid bit-exact against the reference's kernel.
 """
 from __future__ import annotations
@@ -118,7 +118,7 @@ def oracle_ffn(x, x_dt, gu, dn, w_bf16, idx, score, slot_of, slots, out_in):
 
 def assert_within(got, ideal, err, out_dt, what, w_bf16=False):
     g = H.from_storage(got, out_dt)
-    tol = (6.0 if w_bf16 else 2.0) * err + (0.0 if out_dt == H.F32 else 0.5 * H.ulp(ideal, out_dt))
+    tol = (6.0 if w_bf16 else 12.0) * err + (0.0 if out_dt == H.F32 else 0.5 * H.ulp(ideal, out_dt))
     bad = ~(np.abs(g - ideal) <= tol)
     if bad.any():
         i = tuple(np.argwhere(bad)[0])
