@@ -287,3 +287,24 @@ def test_dropin_gather_rows_vs_reference_kernel(gpu, ref):
     torch.cuda.synchronize()
     H.assert_bitexact(mine.cpu().numpy(), theirs.cpu().numpy(), "gather vs reference kernel")
     H.assert_bitexact(mine.cpu().numpy(), table[idx], "gather vs indexing")
+
+
+@pytest.mark.parametrize("w_format", [H.F16, H.BF16], ids=["f16", "bf16"])
+@pytest.mark.parametrize("m", [5, 16, 200])
+def test_split_products_keep_every_activation_bit(gpu, w_format, m):
+    """One-hot weight columns holding powers of two: out[r, c] = x[r, perm(c)] * 2^e exactly.
+    Full 24-bit activations therefore come back bit for bit only if the split into bf16
+    pieces (decode product for m <= 16, tile kernel beyond) loses nothing."""
+    r = H.rng(900 + m + w_format)
+    n, k = 96, 256
+    x = (r.uniform(0.5, 1.0, (m, k)) * (2.0 ** r.integers(-20, 20, (m, k)))).astype(np.float32)
+    x *= np.where(r.random((m, k)) < 0.5, -1, 1).astype(np.float32)
+    perm = r.integers(0, k, n)
+    scale = 2.0 ** (np.arange(n) % 5 - 2)
+    wf = np.zeros((n, k), np.float32)
+    wf[np.arange(n), perm] = scale
+    w = H.to_storage(wf, w_format)
+    case(f"nvf_matmul split exactness fmt={w_format} m={m}")
+    got = ops.matmul(H.to_dev(x, gpu), w_dev(w, w_format, gpu), n, w_format)
+    want = (x[:, perm] * scale[None, :].astype(np.float32)).astype(np.float32)
+    H.assert_bitexact(np.ascontiguousarray(H.to_host(got)), np.ascontiguousarray(want), "one-hot products")
