@@ -117,7 +117,8 @@ void hip_matmul_u16(const float* x, const uint16_t* w, int m, int n, int k, floa
 void hip_matmul_qk(const float* x, const uint8_t* wq, int m, int n, int k, float* out, int kind);
 
 /* hip_ops.hpp:34 -- out[r,:] = rows[indices[r],:] for r < out_rows (the last-token rows
- * ahead of the LM head, src/model.cpp:839); rows_count is unused, as in the reference. */
+ * ahead of the LM head, src/model.cpp:839).  rows_count > 0 bounds the indices: an index
+ * outside [0, rows_count) gives a NaN row (the reference ignores rows_count and reads it). */
 void hip_gather_rows(const float* rows, const int32_t* indices, int rows_count, int cols, int out_rows, float* out);
 
 /* hip_ops.hpp:37 -- top-K experts per row of fp32 router logits [rows, E]: softmax in

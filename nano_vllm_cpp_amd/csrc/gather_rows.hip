@@ -92,10 +92,11 @@ extern "C" int nvf_gather_rows(const void* rows, const int32_t* indices, int64_t
 }
 
 // Drop-in: include/nanovllm/hip_ops.hpp:34 / src/hip_ops.hip:788-795 (fp32, null
-// stream; rows_count is unused there too: indices are trusted).
+// stream).  The reference ignores rows_count and reads wherever an index points; here
+// a positive rows_count bounds the indices (an index outside gives a NaN row), which
+// changes nothing for valid indices.
 extern "C" void hip_gather_rows(const float* rows, const int32_t* indices, int rows_count, int cols, int out_rows,
                                 float* out) {
-  (void)rows_count;
   if (out_rows <= 0 || cols <= 0) return;
-  dropin_check(nvf_gather_rows(rows, indices, 0, cols, out_rows, out, NVF_F32, nullptr), "hip_gather_rows");
+  dropin_check(nvf_gather_rows(rows, indices, rows_count, cols, out_rows, out, NVF_F32, nullptr), "hip_gather_rows");
 }

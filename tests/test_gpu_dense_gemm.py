@@ -270,6 +270,15 @@ def test_gather_rows_bad_index_gives_nan_row(gpu):
     got = ops.gather_rows(torch.from_numpy(table).to(gpu), torch.from_numpy(idx).to(gpu)).cpu().numpy()
     assert np.array_equal(got[[0, 3]], table[[2, 9]])
     assert np.isnan(got[[1, 2, 4]]).all()
+    case("hip_gather_rows out-of-range indices")
+    d_t, d_i = torch.from_numpy(table).to(gpu), torch.from_numpy(idx).to(gpu)
+    out = torch.empty((5, 70), device=gpu)
+    torch.cuda.synchronize()
+    ops.lib().hip_gather_rows(dptr(d_t), dptr(d_i), 10, 70, 5, dptr(out))
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    assert np.array_equal(got[[0, 3]], table[[2, 9]])
+    assert np.isnan(got[[1, 2, 4]]).all()
 
 
 def test_dropin_gather_rows_vs_reference_kernel(gpu, ref):
