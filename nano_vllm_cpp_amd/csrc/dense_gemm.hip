@@ -195,115 +195,11 @@ struct GemvPrefetch<Q6KGroup> {
 // takes runs of R = 8 consecutive weights (dense rows) or R = 32 (one K-quant
 // group: header and scale decoded once per run).
 //
-// m <= 2 (dense_gemv_fma_kernel): LPC = 16 (dense) or 8 (K-quants) lanes per
-// column; lane l = CPS b + j (CPS = 64 / LPC columns per set) streams run b of
-// column j of each of its C column sets (LPC runs: 128 or 256 contiguous k of one
-// column per step) with the same k of each of the m rows, accumulating m x C fp32
-// sums; the LPC lanes of a column are summed at the end.
+// m <= 2: gemv_fma_kernel (gemm_tile.hpp, plain FMAs) with the plain problem policy.
 //
 // 2 < m <= 16: gemv_mfma_kernel (gemm_tile.hpp, v_mfma_f32_16x16x4_f32) with the
 // plain problem policy.
 constexpr int kGemvRows = 16;
-
-template <typename TX, typename Src, int MR, int C, int S, typename TO>
-__global__ __launch_bounds__(kGvWaves * 64) void dense_gemv_fma_kernel(const TX* __restrict__ x, Src w,
-                                                                       TO* __restrict__ out, int64_t m, int64_t n,
-                                                                       int64_t k) {
-  constexpr int R = RunOf<Src>::value, LPC = R == 8 ? 16 : 8, CPS = 64 / LPC, KS = LPC * R;
-  constexpr int G = kGvWaves / S;               // column groups per workgroup (S waves split K in each)
-  __shared__ float part[kGvWaves][MR][C][CPS];  // [wave][row][set][column]
-  const int lane = threadIdx.x & 63, j = lane % CPS, b = lane / CPS;
-  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
-  const int grp = wave / S, split = wave % S;
-  const int64_t c0 = ((int64_t)blockIdx.x * G + grp) * CPS * C;
-  const int64_t nsteps = (k + KS - 1) / KS, full = k / KS;  // steps; steps every lane's run is inside
-  const int64_t s_begin = nsteps * split / S, s_end = nsteps * (split + 1) / S;
-  const int64_t f_end = s_end < full ? s_end : full;
-  const Table<8, TX> xs{x};
-  // columns past n read column n - 1 (their sums are never stored): no per-lane
-  // branches in the loop
-  int64_t wrow[C];
-#pragma unroll
-  for (int q = 0; q < C; ++q) {
-    const int64_t c = c0 + CPS * q + j;
-    wrow[q] = (c < n ? c : n - 1) * k + (int64_t)R * b;
-  }
-  const int64_t xrow = (int64_t)R * b;
-  float acc[MR][C];
-#pragma unroll
-  for (int r = 0; r < MR; ++r)
-#pragma unroll
-    for (int q = 0; q < C; ++q) acc[r][q] = 0.0f;
-
-  struct Buf {
-    typename Src::Raw w[C];
-    typename Table<8, TX>::Raw x[MR][R / 8];
-  };
-  auto load = [&](Buf& f, int64_t st) {
-    const int64_t kk = st * KS;
-#pragma unroll
-    for (int q = 0; q < C; ++q) f.w[q] = w.load(wrow[q] + kk);
-#pragma unroll
-    for (int r = 0; r < MR; ++r) load_x_run<TX, R>(xs, (int64_t)r * k + xrow + kk, f.x[r]);
-  };
-  auto compute = [&](const Buf& f) {
-    float xv[MR][R];
-#pragma unroll
-    for (int r = 0; r < MR; ++r) decode_x_run<TX, R>(xs, f.x[r], xv[r]);
-#pragma unroll
-    for (int q = 0; q < C; ++q) {
-      float wv[R];
-      w.decode(f.w[q], wv);
-#pragma unroll
-      for (int i = 0; i < R; ++i)
-#pragma unroll
-        for (int r = 0; r < MR; ++r) acc[r][q] = __builtin_fmaf(xv[r][i], wv[i], acc[r][q]);
-    }
-  };
-  // full steps, two raw buffers in turn: the next step's loads are in flight
-  // while the current one is decoded.  The prefetch is unconditional (the last
-  // step reloads itself), so the memory counter waits stay exact: a load that
-  // may or may not have been issued makes the compiler wait for all of them.
-  Buf fa, fb;
-  int64_t st = s_begin;
-  if (st < f_end) {
-    const int64_t last = f_end - 1;
-    load(fa, st);
-    while (true) {
-      load(fb, st + 1 < last ? st + 1 : last);
-      compute(fa);
-      if (++st >= f_end) break;
-      load(fa, st + 1 < last ? st + 1 : last);
-      compute(fb);
-      if (++st >= f_end) break;
-    }
-  }
-  // the last, partial step (k not a multiple of the step): lanes past k add nothing
-  if (f_end < s_end && xrow + f_end * KS < k) {
-    load(fa, f_end);
-    compute(fa);
-  }
-
-#pragma unroll
-  for (int r = 0; r < MR; ++r)
-#pragma unroll
-    for (int q = 0; q < C; ++q) {
-      float v = acc[r][q];
-#pragma unroll
-      for (int d = CPS; d < 64; d *= 2) v += __shfl_xor(v, d, 64);
-      if (lane < CPS) part[wave][r][q][j] = v;
-    }
-  __syncthreads();
-  for (int t = (int)threadIdx.x; t < G * MR * C * CPS; t += kGvWaves * 64) {
-    const int jj = t % CPS, q = (t / CPS) % C, r = (t / (CPS * C)) % MR, g = t / (CPS * C * MR);
-    const int64_t col = ((int64_t)blockIdx.x * G + g) * CPS * C + CPS * q + jj;
-    if (r >= m || col >= n) continue;
-    float v = part[g * S][r][q][jj];
-#pragma unroll
-    for (int wv = 1; wv < S; ++wv) v += part[g * S + wv][r][q][jj];
-    out[(int64_t)r * n + col] = from_f32<TO>(v);
-  }
-}
 
 // Column sets / groups per wave: 4 (dense) or 2 (K-quants, larger runs) when that
 // leaves >= ~1000 workgroups, fewer for narrow outputs.
@@ -315,12 +211,13 @@ int launch_gemv_fma(const TX* x, const Src& src, TO* out, int64_t m, int64_t n, 
   auto grid = [&](int cols) { return dim3((unsigned)((n + cols - 1) / cols)); };
   // wide outputs: each wave walks the whole K of its own columns (S = 1); narrow
   // ones split K over the 4 waves to fill the GPU
+  const PlainGemvProb<TO> prob{out, m, n, k};
   if (n >= (int64_t)CPS * CMAX * kGvWaves * 1024)
-    dense_gemv_fma_kernel<TX, Src, MR, CMAX, 1, TO><<<grid(CPS * CMAX * kGvWaves), blk, 0, st>>>(x, src, out, m, n, k);
+    gemv_fma_kernel<TX, Src, MR, CMAX, 1><<<grid(CPS * CMAX * kGvWaves), blk, 0, st>>>(x, src, prob, k);
   else if (n >= (int64_t)CPS * CMAX * 1024)
-    dense_gemv_fma_kernel<TX, Src, MR, CMAX, 4, TO><<<grid(CPS * CMAX), blk, 0, st>>>(x, src, out, m, n, k);
+    gemv_fma_kernel<TX, Src, MR, CMAX, 4><<<grid(CPS * CMAX), blk, 0, st>>>(x, src, prob, k);
   else
-    dense_gemv_fma_kernel<TX, Src, MR, 1, 4, TO><<<grid(CPS), blk, 0, st>>>(x, src, out, m, n, k);
+    gemv_fma_kernel<TX, Src, MR, 1, 4><<<grid(CPS), blk, 0, st>>>(x, src, prob, k);
   return launch_status("dense_gemv_fma");
 }
 

@@ -614,6 +614,119 @@ __global__ __launch_bounds__(kGvWaves * 64) void gemv_mfma_kernel(const TX* __re
   }
 }
 
+// ---------------------------------------------------------------------------
+// Decode-shaped product with plain FMAs (m <= MR rows, MR = 1 or 2): LPC = 16 (dense
+// rows) or 8 (K-quant groups) lanes per column; lane l = CPS b + j (CPS = 64 / LPC
+// columns per set) streams run b of column j of each of its C column sets (LPC runs:
+// 128 or 256 contiguous k of one column per step) with the same k of each row,
+// accumulating MR x C fp32 sums; the LPC lanes of a column are summed at the end.  S
+// waves of the workgroup split K (S = 4), or each wave owns its own columns (S = 1,
+// wide outputs).  Full steps double-buffer the raw loads with an unconditional
+// prefetch (the last step reloads itself), which keeps the memory-counter waits
+// exact.  A row or column outside the problem reads row 0 (valid memory; its results
+// are never stored).  The policy names the workgroup's G C CPS columns per item.
+template <typename TX, typename Src, int MR, int C, int S, typename P>
+__global__ __launch_bounds__(kGvWaves * 64) void gemv_fma_kernel(const TX* __restrict__ x, Src w, P prob,
+                                                                 int64_t k) {
+  constexpr int R = RunOf<Src>::value, LPC = R == 8 ? 16 : 8, CPS = 64 / LPC, KS = LPC * R;
+  constexpr int G = kGvWaves / S;               // column groups per workgroup (S waves split K in each)
+  __shared__ float part[kGvWaves][MR][C][CPS];  // [wave][row][set][column]
+  const int lane = threadIdx.x & 63, j = lane % CPS, b = lane / CPS;
+  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int grp = wave / S, split = wave % S;
+  const Table<8, TX> xs{x};
+  struct Buf {
+    typename Src::Raw w[C];
+    typename Table<8, TX>::Raw x[MR][R / 8];
+  };
+  for (int64_t item = blockIdx.x;; item += gridDim.x) {
+    typename P::Tile tile;
+    if (!prob.tile(item, G * CPS * C, tile)) break;  // uniform per workgroup
+    const int64_t nsteps = (k + KS - 1) / KS, full = k / KS;  // steps; steps every lane's run is inside
+    const int64_t s_begin = nsteps * split / S, s_end = nsteps * (split + 1) / S;
+    const int64_t f_end = s_end < full ? s_end : full;
+    const int64_t kb = (int64_t)R * b;  // this lane's run inside a step
+    int64_t wrow[C];
+#pragma unroll
+    for (int q = 0; q < C; ++q) {
+      const int64_t o = prob.b_row(tile, grp * CPS * C + CPS * q + j);
+      wrow[q] = (o >= 0 ? o : 0) + kb;
+    }
+    int64_t xrow[MR];
+#pragma unroll
+    for (int r = 0; r < MR; ++r) {
+      const int64_t o = prob.a_row(tile, r);
+      xrow[r] = (o >= 0 ? o : 0) + kb;
+    }
+    float acc[MR][C];
+#pragma unroll
+    for (int r = 0; r < MR; ++r)
+#pragma unroll
+      for (int q = 0; q < C; ++q) acc[r][q] = 0.0f;
+
+    auto load = [&](Buf& f, int64_t st) {
+      const int64_t kk = st * KS;
+#pragma unroll
+      for (int q = 0; q < C; ++q) f.w[q] = w.load(wrow[q] + kk);
+#pragma unroll
+      for (int r = 0; r < MR; ++r) load_x_run<TX, R>(xs, xrow[r] + kk, f.x[r]);
+    };
+    auto compute = [&](const Buf& f) {
+      float xv[MR][R];
+#pragma unroll
+      for (int r = 0; r < MR; ++r) decode_x_run<TX, R>(xs, f.x[r], xv[r]);
+#pragma unroll
+      for (int q = 0; q < C; ++q) {
+        float wv[R];
+        w.decode(f.w[q], wv);
+#pragma unroll
+        for (int i = 0; i < R; ++i)
+#pragma unroll
+          for (int r = 0; r < MR; ++r) acc[r][q] = __builtin_fmaf(xv[r][i], wv[i], acc[r][q]);
+      }
+    };
+    Buf fa, fb;
+    int64_t st = s_begin;
+    if (st < f_end) {
+      const int64_t last = f_end - 1;
+      load(fa, st);
+      while (true) {
+        load(fb, st + 1 < last ? st + 1 : last);
+        compute(fa);
+        if (++st >= f_end) break;
+        load(fa, st + 1 < last ? st + 1 : last);
+        compute(fb);
+        if (++st >= f_end) break;
+      }
+    }
+    // the last, partial step (k not a multiple of the step): lanes past k add nothing
+    if (f_end < s_end && kb + f_end * KS < k) {
+      load(fa, f_end);
+      compute(fa);
+    }
+
+#pragma unroll
+    for (int r = 0; r < MR; ++r)
+#pragma unroll
+      for (int q = 0; q < C; ++q) {
+        float v = acc[r][q];
+#pragma unroll
+        for (int d = CPS; d < 64; d *= 2) v += __shfl_xor(v, d, 64);
+        if (lane < CPS) part[wave][r][q][j] = v;
+      }
+    __syncthreads();
+    for (int t = (int)threadIdx.x; t < G * MR * C * CPS; t += kGvWaves * 64) {
+      const int jj = t % CPS, q = (t / CPS) % C, r = (t / (CPS * C)) % MR, g = t / (CPS * C * MR);
+      float v = part[g * S][r][q][jj];
+#pragma unroll
+      for (int wv = 1; wv < S; ++wv) v += part[g * S + wv][r][q][jj];
+      prob.store(tile, r, g * CPS * C + CPS * q + jj, v);
+    }
+    if constexpr (!P::kLoop) break;  // one item per workgroup
+    __syncthreads();                 // LDS is reused by the next item
+  }
+}
+
 // The plain decode product: out[m][n] = x[m][k] . W[n][k]^T, m <= 16, workgroup b
 // on columns [b 16 C, (b + 1) 16 C).
 template <typename TO>

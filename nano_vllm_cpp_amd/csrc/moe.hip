@@ -610,7 +610,7 @@ int nvf_moe_route(const float* logits, int64_t rows, int64_t E, int64_t K, int n
 
 int64_t nvf_moe_ffn_workspace_size(int64_t rows, int64_t H, int64_t I, int64_t K, int64_t slots) {
   if (rows <= 0 || H <= 0 || I <= 0 || K <= 0 || slots <= 0) return 0;
-  return MoeLayout(rows * K, H, I, slots, 16).total;  // the most tiles any plan lists
+  return MoeLayout(rows * K, H, I, slots, 16).total;  // the most tiles any plan lists (16-row tiles)
 }
 
 int nvf_moe_ffn_ws(const void* x, int x_dtype, const int32_t* idx, const float* score, const void* gu,
