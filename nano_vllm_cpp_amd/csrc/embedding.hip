@@ -238,7 +238,9 @@ struct SlotBytes<F, decltype((void)F::kSlotBytes)> {
   static constexpr int value = F::kSlotBytes;
 };
 
-template <typename TO, typename Fmt, int L16>  // L16: 16-byte loads per lane to stage a row
+// PARTS waves per row: wave p of a row stages and decodes blocks [nblk p / PARTS,
+// nblk (p + 1) / PARTS) of it, so a row's blocks are spread over more waves.
+template <typename TO, typename Fmt, int L16, int PARTS>  // L16: 16-byte loads per lane to stage a part
 __global__ __launch_bounds__(kEmbThreads) void embed_rows_staged_kernel(const int64_t* __restrict__ ids,
                                                                         const uint8_t* __restrict__ table,
                                                                         TO* __restrict__ out, int64_t tokens,
@@ -247,11 +249,15 @@ __global__ __launch_bounds__(kEmbThreads) void embed_rows_staged_kernel(const in
   extern __shared__ __attribute__((aligned(16))) uint8_t stage[];  // kEmbWaves slices of stage_bytes
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x / kWave));
-  const int64_t t = (int64_t)blockIdx.x * kEmbWaves + wave;
+  const int64_t gw = (int64_t)blockIdx.x * kEmbWaves + wave;
+  const int64_t t = gw / PARTS;
+  const int part = (int)(gw % PARTS);
   if (t >= tokens) return;  // wave-uniform; the wave's LDS slice is its own (no workgroup barrier)
   const int64_t id = ids[t];
-  const int nch = hidden / N;
-  TO* dst = out + t * hidden;
+  const int nblk = hidden / Fmt::kBlockElems;
+  const int b0 = nblk * part / PARTS, b1 = nblk * (part + 1) / PARTS;
+  const int nch = (b1 - b0) * Fmt::kBlockElems / N;
+  TO* dst = out + t * hidden + (int64_t)b0 * Fmt::kBlockElems;
   if (bad_id(id, vocab)) {
     float nan[N];
 #pragma unroll
@@ -259,15 +265,14 @@ __global__ __launch_bounds__(kEmbThreads) void embed_rows_staged_kernel(const in
     for (int c = lane; c < nch; c += kWave) st16(dst + c * N, Pack<TO>::pack(nan));
     return;
   }
-  const int nblk = hidden / Fmt::kBlockElems;
-  const uint8_t* row = table + id * (int64_t)nblk * Fmt::kBlockBytes;
+  const uint8_t* row = table + (id * (int64_t)nblk + b0) * Fmt::kBlockBytes;
   constexpr int kSlot = SlotBytes<Fmt>::value;
   if constexpr (kSlot > 0) {
     // 16-byte loads k = 0 .. kPer - 1 of block b: from block byte Fmt::slot_src(k)
     // into slot bytes 16 k; none reads past the block, so none leaves the table
     constexpr int kPer = kSlot / 16;
     uint8_t* my = stage + wave * stage_bytes;
-    const int nld = nblk * kPer;
+    const int nld = (b1 - b0) * kPer;
     u32x4 r[L16];
 #pragma unroll
     for (int u = 0; u < L16; ++u) {
@@ -296,7 +301,7 @@ __global__ __launch_bounds__(kEmbThreads) void embed_rows_staged_kernel(const in
   }
   const uintptr_t a16 = reinterpret_cast<uintptr_t>(row) & ~uintptr_t(15);
   const int delta = (int)(reinterpret_cast<uintptr_t>(row) - a16);
-  const int n16 = (delta + nblk * Fmt::kBlockBytes + 15) >> 4;
+  const int n16 = (delta + (b1 - b0) * Fmt::kBlockBytes + 15) >> 4;
   uint8_t* my = stage + wave * stage_bytes;
   u32x4 r[L16];
 #pragma unroll
@@ -329,16 +334,34 @@ static bool launch_staged(const int64_t* ids, const uint8_t* table, TO* out, int
   // flat staging reads from the 16-byte boundary at or below the row: one chunk more
   const int64_t n16 = kSlot > 0 ? row_bytes / 16 : (15 + row_bytes + 15) / 16;
   if (hidden % Fmt::kBlockElems != 0 || n16 * 16 > kStageMaxBytesPerWave || hidden > INT32_MAX) return false;
-  const int stage_bytes = (int)(n16 * 16);
+  // two waves per row when the row has at least 8 blocks (measured at Qwen2.5-7B's
+  // shape: Q5_K 70.7 -> 74.3%, Q4_K 75.4 -> 76.7%, Q6_K 63.1 -> 64.3%, Q8_0 blocks
+  // 67.0 -> 67.8% of 8 TB/s; four waves per row was slower for every format)
+  const int parts = hidden / Fmt::kBlockElems >= 8 ? 2 : 1;
+  // 16-byte chunks of the larger part: ceil(nblk / 2) blocks (flat: plus the alignment lead)
+  const int64_t half_blocks = (hidden / Fmt::kBlockElems + parts - 1) / parts;
+  const int64_t part_n16 = parts == 1 ? n16
+                           : kSlot > 0 ? half_blocks * (kSlot / 16)
+                                       : (15 + half_blocks * Fmt::kBlockBytes + 15) / 16;
+  const int stage_bytes = (int)(part_n16 * 16);
   const size_t lds = (size_t)stage_bytes * kEmbWaves;
-  const dim3 grid((unsigned)((tokens + kEmbWaves - 1) / kEmbWaves));
+  const int64_t waves = tokens * parts;
+  const dim3 grid((unsigned)((waves + kEmbWaves - 1) / kEmbWaves));
   const int h = (int)hidden;
-  const int l16 = (int)((n16 + kWave - 1) / kWave);
-  switch (l16) {
-#define NVF_STAGE_CASE(L)                                                                                   \
-  case L:                                                                                                   \
-    embed_rows_staged_kernel<TO, Fmt, L><<<grid, kEmbThreads, lds, st>>>(ids, table, out, tokens, h, vocab, \
-                                                                          stage_bytes);                      \
+  const int l16 = (int)((part_n16 + kWave - 1) / kWave);
+  switch (l16 * 4 + (parts - 1)) {
+#define NVF_STAGE_CASE(L)                                                                                     \
+  case 4 * L:                                                                                                 \
+    embed_rows_staged_kernel<TO, Fmt, L, 1><<<grid, kEmbThreads, lds, st>>>(ids, table, out, tokens, h, vocab, \
+                                                                             stage_bytes);                      \
+    break;                                                                                                    \
+  case 4 * L + 1:                                                                                             \
+    embed_rows_staged_kernel<TO, Fmt, L, 2><<<grid, kEmbThreads, lds, st>>>(ids, table, out, tokens, h, vocab, \
+                                                                             stage_bytes);                      \
+    break;                                                                                                    \
+  case 4 * L + 3:                                                                                             \
+    embed_rows_staged_kernel<TO, Fmt, L, 4><<<grid, kEmbThreads, lds, st>>>(ids, table, out, tokens, h, vocab, \
+                                                                             stage_bytes);                      \
     break;
     NVF_STAGE_CASE(1) NVF_STAGE_CASE(2) NVF_STAGE_CASE(3) NVF_STAGE_CASE(4)
     NVF_STAGE_CASE(5) NVF_STAGE_CASE(6) NVF_STAGE_CASE(7) NVF_STAGE_CASE(8)
