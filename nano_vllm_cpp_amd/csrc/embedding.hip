@@ -349,18 +349,14 @@ static bool launch_staged(const int64_t* ids, const uint8_t* table, TO* out, int
   const dim3 grid((unsigned)((waves + kEmbWaves - 1) / kEmbWaves));
   const int h = (int)hidden;
   const int l16 = (int)((part_n16 + kWave - 1) / kWave);
-  switch (l16 * 4 + (parts - 1)) {
+  switch (l16 * 2 + (parts - 1)) {
 #define NVF_STAGE_CASE(L)                                                                                     \
-  case 4 * L:                                                                                                 \
+  case 2 * L:                                                                                                 \
     embed_rows_staged_kernel<TO, Fmt, L, 1><<<grid, kEmbThreads, lds, st>>>(ids, table, out, tokens, h, vocab, \
                                                                              stage_bytes);                      \
     break;                                                                                                    \
-  case 4 * L + 1:                                                                                             \
+  case 2 * L + 1:                                                                                             \
     embed_rows_staged_kernel<TO, Fmt, L, 2><<<grid, kEmbThreads, lds, st>>>(ids, table, out, tokens, h, vocab, \
-                                                                             stage_bytes);                      \
-    break;                                                                                                    \
-  case 4 * L + 3:                                                                                             \
-    embed_rows_staged_kernel<TO, Fmt, L, 4><<<grid, kEmbThreads, lds, st>>>(ids, table, out, tokens, h, vocab, \
                                                                              stage_bytes);                      \
     break;
     NVF_STAGE_CASE(1) NVF_STAGE_CASE(2) NVF_STAGE_CASE(3) NVF_STAGE_CASE(4)
