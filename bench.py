@@ -292,7 +292,7 @@ def main() -> int:
             assert ((lpos + 1) <= np.array(lnb)[lseq] * bs_kv).all(), "layer inputs: keys past the block tables"
             lslots = (ltab[lseq, lpos // bs_kv].astype(np.int64) * bs_kv + lpos % bs_kv).astype(np.int32)
             lrows = sum(lnb) * bs_kv
-            return dict(lw, T=n_, mql=mql, h=randn((n_, Hd)), r=randn((n_, Hd)),
+            return dict(lw, T=n_, mql=mql, h=randn((n_, Hd)), r=randn((n_, Hd)), r2=torch.empty(n_, Hd, dtype=tdt, device=dev),
                         pos=torch.from_numpy(lpos.astype(np.int64)).to(dev),
                         kc=torch.zeros(lrows, cfg.kv_heads, cfg.head_dim, dtype=tdt, device=dev),
                         vc=torch.zeros(lrows, cfg.kv_heads, cfg.head_dim, dtype=tdt, device=dev),
@@ -432,9 +432,17 @@ def main() -> int:
         # qkv, then in one launch the qkv bias (Qwen2.5) or the QK-norm (Qwen3), RoPE on the q and k
         # columns of the packed row and the KV store, paged attention, o (quantize + GEMM),
         # post-attention residual-add RMSNorm (int8 rows), gate_up, SwiGLU (int8 rows), down
+        # (decode GEMV, n <= 16 rows: the input norm runs in the qkv GEMV's prologue, its
+        # residual going to r2, and the o and down projections quantize their own rows; the
+        # post-attention norm stays a launch of its own: fused into gate_up's 592 workgroups it
+        # measured no faster)
         n_ = L_["T"]
-        _, sc, xq = ops.rms_norm_q8(L_["h"], L_["w_in"], cfg.eps, residual=L_["r"], want_out=False)
-        qkv = ops.matmul_q8_0(xq, sc, *L_["qkv"], qs + 2 * ks, tdt, out=L_["qkv_out"])
+        if n_ <= 16:
+            qkv = ops.matmul_q8_0_rms(L_["h"], L_["w_in"], cfg.eps, *L_["qkv"], qs + 2 * ks, residual=L_["r"],
+                                      residual_out=L_["r2"], out=L_["qkv_out"])
+        else:
+            _, sc, xq = ops.rms_norm_q8(L_["h"], L_["w_in"], cfg.eps, residual=L_["r"], want_out=False)
+            qkv = ops.matmul_q8_0(xq, sc, *L_["qkv"], qs + 2 * ks, tdt, out=L_["qkv_out"])
         ops.qk_norm_rope_store_kv(qkv[:, :qs], qkv[:, qs:qs + ks], qkv[:, qs + ks:], L_["pos"], L_["qn"], L_["kn"],
                                   inv, cfg.q_heads, cfg.kv_heads, cfg.head_dim, L_["kc"], L_["vc"], L_["slots"],
                                   cfg.eps, qkv_bias=L_["bias"])
@@ -442,12 +450,13 @@ def main() -> int:
                                   L_["qlen"], L_["tab"], bs_kv, cfg.head_dim ** -0.5, out=L_["attn_out"],
                                   max_query_len=L_["mql"], cu_seqlens=L_.get("cu"),
                                   noalloc=L_["mql"] == 1)  # decode: the split's partials in the static scratch
-        if n_ <= 16:  # decode GEMV: the o and down projections quantize their own input rows
+        if n_ <= 16:
             o = ops.matmul_q8_0_act(att.view(n_, qs), *L_["o"], Hd, out=L_["o_out"])
         else:
             sc2, xq2 = ops.q8_quantize_rows(att.view(n_, qs))
             o = ops.matmul_q8_0(xq2, sc2, *L_["o"], Hd, tdt, out=L_["o_out"])
-        _, sc3, xq3 = ops.rms_norm_q8(o, L_["w_post"], cfg.eps, residual=L_["r"], want_out=False)
+        _, sc3, xq3 = ops.rms_norm_q8(o, L_["w_post"], cfg.eps, residual=L_["r2"] if n_ <= 16 else L_["r"],
+                                      want_out=False)
         gu = ops.matmul_q8_0(xq3, sc3, *L_["gu"], 2 * I, tdt, out=L_["gu_out"])
         if n_ <= 16:  # SwiGLU + its quantizer inside the down GEMV
             ops.matmul_q8_0_act(gu, *L_["down"], Hd, swiglu=True, out=L_["down_out"])

@@ -360,6 +360,21 @@ int nvf_matmul_q8_0_ws(const int8_t* xq, const float* row_scale, const uint8_t* 
 int nvf_matmul_q8_0_act(const void* x, int64_t x_stride, int act, const uint8_t* w8, const uint16_t* ws, int64_t m,
                         int64_t n, int64_t k, void* out, int dtype, void* stream);
 
+/* Decode GEMV (m <= 16 rows) with residual-add + RMSNorm + quantizer in its prologue:
+ * out [m, n] = the Q8_0 product of the rows nvf_rms_norm_q8 would produce, bit for bit.
+ * With residual [m, k]: v = round(x + residual), written to residual_out [m, k]
+ * (which must not overlap x or residual: every workgroup reads them); without
+ * (both NULL): v = x.  Then round(v / rms(v) * norm_weight) quantized per row.  Each
+ * workgroup repeats the norm in its prologue, its sum of squares in nvf_rms_norm_q8's
+ * own order.  This fuses the reference's hip_rms_norm_add then the next Q8_0 matmul
+ * (src/model.cpp:762 then :764, :787 then :829; src/hip_ops.hip:395-417, :639-680) into
+ * one launch; the in-place residual becomes a second buffer (alternate two across the
+ * layer's two norms).  x rows x_stride elements apart; all pointers 16-byte aligned
+ * (ws 2); k % 32 == 0 and k * dtype bytes <= 64 KiB; else NVF_ERR_INVALID. */
+int nvf_matmul_q8_0_rms(const void* x, int64_t x_stride, const void* residual, void* residual_out,
+                        const void* norm_weight, float eps, const uint8_t* w8, const uint16_t* ws, int64_t m, int64_t n,
+                        int64_t k, void* out, int dtype, void* stream);
+
 int64_t nvf_matmul_q8_0_workspace_size(int64_t m, int64_t n, int64_t k);
 
 /* KV store (replaces hip_store_kv, hip_ops.hpp:22-23) with the cache in `dtype`;

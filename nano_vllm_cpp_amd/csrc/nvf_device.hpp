@@ -188,6 +188,14 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
 // Q8 activation quantizer of the reference's INT8 GEMM path: per-row scale
 // 127 / max|x| (0 for an all-~zero row) and q = (int8)clamp(x * scale, +-127)
 // with C truncation (src/hip_ops.hip:205-217, :244-245).
+// RMSNorm row layout (rms_norm.hip, and the decode GEMV's fused norm, which must sum
+// the squares in the same order to give a bit-identical 1/rms): a row of nvec
+// 16-byte vectors goes to rms_waves_per_row(nvec) waves; vector i of lane l in
+// sub-wave s is (i * wpr + s) * 64 + l; each lane sums its squares by fmaf in
+// (i, element) order, then wave_sum, then the sub-waves' sums in order s = 0, 1, ...
+__host__ __device__ constexpr int rms_waves_per_row(int64_t nvec) { return nvec >= 256 ? 4 : (nvec >= 128 ? 2 : 1); }
+constexpr int kRmsMaxVpl = 16;  // vectors per lane of the register-resident 4-wave row
+
 __device__ __forceinline__ float q8_row_scale(float max_abs) { return max_abs > 1e-8f ? 127.0f / max_abs : 0.0f; }
 __device__ __forceinline__ int q8_quantize(float v, float scale) {
   return (int)(int8_t)fminf(127.0f, fmaxf(-127.0f, v * scale));

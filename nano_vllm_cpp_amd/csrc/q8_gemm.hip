@@ -405,6 +405,11 @@ constexpr int gemv_cols() { return W / S * 16; }  // columns per workgroup of W 
 // nvf_q8_quantize_rows (XF = 1) or nvf_silu_and_mul_q8 over [gate | up] rows
 // (XF = 2) would: the row maximum is order-independent and each value is quantized
 // alone, so the int8 rows and scales are bit-identical to the separate pass's.
+// XF = 3: residual-add + RMSNorm over the rows first, exactly as nvf_rms_norm_q8
+// (xres, when given, is the residual: the rows become round(x + xres), which
+// workgroup 0 stores to xres_out; then round(v * inv_rms * xg)).  Bit-identity
+// needs the norm's own sum of squares: a first pass sums each row's squares in the
+// norm kernel's layout (rms_waves_per_row) and order, one (row, sub-wave) per wave.
 template <typename TO, int W, int S, bool XL, int XF = 0>
 __global__ __launch_bounds__(W * 64) void q8_gemv_kernel(const int8_t* __restrict__ xq,
                                                          const float* __restrict__ rscale,
@@ -412,7 +417,9 @@ __global__ __launch_bounds__(W * 64) void q8_gemv_kernel(const int8_t* __restric
                                                          const uint16_t* __restrict__ ws,
                                                          TO* __restrict__ out, int64_t m, int64_t n, int64_t k,
                                                          int sc_bytes, const TO* __restrict__ xf = nullptr,
-                                                         int64_t xf_ld = 0) {
+                                                         int64_t xf_ld = 0, const TO* __restrict__ xres = nullptr,
+                                                         TO* __restrict__ xres_out = nullptr,
+                                                         const TO* __restrict__ xg = nullptr, float eps = 0.0f) {
   static_assert(XF == 0 || XL, "the fused quantizer writes the staged LDS rows");
   constexpr int kCols = gemv_cols<W, S>();
   constexpr int kGvDmaLds = W * 2 * kGvWaveBuf;
@@ -432,6 +439,7 @@ __global__ __launch_bounds__(W * 64) void q8_gemv_kernel(const int8_t* __restric
   // only, so the kernel may take the whole 160 KiB)
   float* xf_max = reinterpret_cast<float*>(x_lds + ((m * (k + 16) + 15) & ~int64_t(15)));
   float* xf_scale = xf_max + W * kGemvMaxM;
+  float* xf_ss = xf_scale + kGemvMaxM;  // XF 3: [row][sub-wave] sums of squares
   const int64_t xrow = k + 16;  // LDS bytes per staged activation row
 
   const int64_t c0 = wg_c0 + (int64_t)grp * 16;  // this wave's first column
@@ -503,6 +511,49 @@ __global__ __launch_bounds__(W * 64) void q8_gemv_kernel(const int8_t* __restric
               (uint32_t)(r * k + kb), 0, 0, 0);
       }
     }
+    // XF: the fp rows' loads go out here too, so their latency overlaps weight stage 0
+    // (not after the wait below): a single row's values for the thread (hold), and for
+    // XF 3 each wave's rows in the norm's layout (npre)
+    constexpr int N = Pack<TO>::N;
+    const int64_t nv = k / N;
+    constexpr int kHold = XF == 3 ? 4 : 8;  // a single row of up to kHold vectors per thread stays in registers
+    constexpr int kNormPre = 4;             // norm-layout vectors per lane preloaded
+    const bool hold = XF != 0 && m == 1 && nv <= (int64_t)kHold * W * 64;
+    // (fp32 rows of XF 1 / 2 are loaded after the wait: preloaded they take ~230 VGPRs)
+    constexpr bool kPre = sizeof(TO) == 2 || XF == 3;
+    const int wpr = rms_waves_per_row(nv);
+    const int vpl = (int)((nv + (int64_t)wpr * 64 - 1) / ((int64_t)wpr * 64));
+    const bool npre = XF == 3 && m * wpr <= W && vpl <= kNormPre;
+    u32x4 ha[kHold], hb[kHold], hg[kHold];  // x; up (XF 2) or residual (XF 3); norm weight (XF 3)
+    u32x4 na[kNormPre], nb[kNormPre];
+    if constexpr (XF != 0) {
+      if (kPre && hold) {
+#pragma unroll
+        for (int i = 0; i < kHold; ++i) {
+          const int64_t c = threadIdx.x + (int64_t)i * W * 64;
+          if (c < nv) {
+            ha[i] = ld16(xf + c * N);
+            if constexpr (XF == 2) hb[i] = ld16(xf + k + c * N);
+            if constexpr (XF == 3) {
+              if (xres) hb[i] = ld16(xres + c * N);
+              hg[i] = ld16(xg + c * N);
+            }
+          }
+        }
+      }
+      if (npre && wave < m * wpr) {
+        const int64_t r = wave / wpr;
+        const int sub = wave % wpr;
+#pragma unroll
+        for (int i = 0; i < kNormPre; ++i) {
+          const int64_t c = ((int64_t)i * wpr + sub) * 64 + lane;
+          if (i < vpl && c < nv) {
+            na[i] = ld16(xf + r * xf_ld + c * N);
+            if (xres) nb[i] = ld16(xres + r * k + c * N);
+          }
+        }
+      }
+    }
     if (active) {
       if constexpr (!XL) load_x(0);
       if (nst > 1) issue(1);
@@ -518,28 +569,123 @@ __global__ __launch_bounds__(W * 64) void q8_gemv_kernel(const int8_t* __restric
       // the scale, then every value quantized into the staged row (the values are
       // computed twice rather than held: up to 16 rows of k).  Weight stage 1 stays
       // in flight meanwhile.
-      constexpr int N = Pack<TO>::N;
-      const int64_t nv = k / N;
-      auto act = [&](int64_t r, int64_t c, float* v) {
-        const TO* row = xf + r * xf_ld;
-        Pack<TO>::unpack(ld16(row + c * N), v);
-        if constexpr (XF == 2) {
-          float u[N];
-          Pack<TO>::unpack(ld16(row + k + c * N), u);
+      // XF 3: the row value round(x + residual) (or x), as the norm stores it
+      auto res_raw = [&](const u32x4& xv4, const u32x4& rv4, float* v) {
+        Pack<TO>::unpack(xv4, v);
+        if (xres) {
+          float a[N];
+          Pack<TO>::unpack(rv4, a);
 #pragma unroll
-          for (int e = 0; e < N; ++e) v[e] = to_f32(from_f32<TO>(silu_mul<TO>(v[e], u[e])));  // the stored value
+          for (int e = 0; e < N; ++e) v[e] += a[e];
+          Pack<TO>::unpack(Pack<TO>::pack(v), v);
         }
       };
-      constexpr int kHold = 8;  // a single row of up to kHold vectors per thread stays in registers
-      const bool hold = m == 1 && nv <= (int64_t)kHold * W * 64;
+      // the raw vectors of row r, vector c
+      auto load_raw = [&](int64_t r, int64_t c, u32x4& a, u32x4& b, u32x4& gg) {
+        a = ld16(xf + r * xf_ld + c * N);
+        if constexpr (XF == 2) b = ld16(xf + r * xf_ld + k + c * N);
+        if constexpr (XF == 3) {
+          if (xres) b = ld16(xres + r * k + c * N);
+          gg = ld16(xg + c * N);
+        }
+      };
+      if constexpr (XF == 3) {  // pass 0: the norm's sums of squares, in its layout and order
+        auto sum_row = [&](auto&& vec_at) {
+          float ss = 0.0f;
+          for (int i = 0; i < vpl; ++i) {
+            float v[N];
+            if (vec_at(i, v)) {
+#pragma unroll
+              for (int e = 0; e < N; ++e) ss = fmaf(v[e], v[e], ss);
+            }
+          }
+          return wave_sum(ss);
+        };
+        if (npre) {
+          if (wave < m * wpr) {
+            const int64_t r = wave / wpr;
+            const int sub = wave % wpr;
+            float ss = 0.0f;
+#pragma unroll
+            for (int i = 0; i < kNormPre; ++i) {
+              const int64_t c = ((int64_t)i * wpr + sub) * 64 + lane;
+              if (i < vpl && c < nv) {
+                float v[N];
+                res_raw(na[i], nb[i], v);
+#pragma unroll
+                for (int e = 0; e < N; ++e) ss = fmaf(v[e], v[e], ss);
+              }
+            }
+            ss = wave_sum(ss);
+            if (lane == 0) xf_ss[r * 4 + sub] = ss;
+          }
+        } else {
+          for (int64_t it = wave; it < m * wpr; it += W) {
+            const int64_t r = it / wpr;
+            const int sub = (int)(it % wpr);
+            const float ss = sum_row([&](int i, float* v) {
+              const int64_t c = ((int64_t)i * wpr + sub) * 64 + lane;
+              if (c >= nv) return false;
+              u32x4 a, b, gg;
+              load_raw(r, c, a, b, gg);
+              res_raw(a, b, v);
+              return true;
+            });
+            if (lane == 0) xf_ss[r * 4 + sub] = ss;
+          }
+        }
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      }
+      auto row_inv = [&](int64_t r) {  // the norm's 1/rms of row r
+        float ss = xf_ss[r * 4];
+        if (wpr > 1) {
+          ss = 0.0f;
+          for (int s4 = 0; s4 < wpr; ++s4) ss += xf_ss[r * 4 + s4];
+        }
+        return rsqrtf(ss / (float)k + eps);
+      };
+      // the quantizer's input values from the raw vectors; pass 1 stores the residual
+      // row (workgroup 0 only), pass 2 only recomputes
+      auto finish = [&](int64_t r, int64_t c, const u32x4& a, const u32x4& b, const u32x4& gg, float* v, float inv,
+                        bool store_res) {
+        if constexpr (XF == 3) {
+          float g[N], o[N];
+          res_raw(a, b, v);
+          if (store_res && xres && blockIdx.x == 0) st16(xres_out + r * k + c * N, Pack<TO>::pack(v));
+          Pack<TO>::unpack(gg, g);
+#pragma unroll
+          for (int e = 0; e < N; ++e) o[e] = v[e] * inv * g[e];
+          Pack<TO>::unpack(Pack<TO>::pack(o), v);  // the stored (rounded) normalised value
+        } else {
+          Pack<TO>::unpack(a, v);
+          if constexpr (XF == 2) {
+            float u[N];
+            Pack<TO>::unpack(b, u);
+#pragma unroll
+            for (int e = 0; e < N; ++e) v[e] = to_f32(from_f32<TO>(silu_mul<TO>(v[e], u[e])));  // the stored value
+          }
+        }
+      };
+      auto act = [&](int64_t r, int64_t c, float* v, float inv, bool store_res) {
+        u32x4 a, b, gg;
+        load_raw(r, c, a, b, gg);
+        finish(r, c, a, b, gg, v, inv, store_res);
+      };
       float hv[kHold][N];
       if (hold) {
         float mx = 0.0f;
+        const float inv0 = XF == 3 ? row_inv(0) : 0.0f;
 #pragma unroll
         for (int i = 0; i < kHold; ++i) {
           const int64_t c = threadIdx.x + (int64_t)i * W * 64;
           if (c < nv) {
-            act(0, c, hv[i]);
+            if constexpr (kPre)
+              finish(0, c, ha[i], hb[i], hg[i], hv[i], inv0, true);
+            else
+              act(0, c, hv[i], inv0, true);
 #pragma unroll
             for (int e = 0; e < N; ++e) mx = fmaxf(mx, fabsf(hv[i][e]));
           }
@@ -549,9 +695,10 @@ __global__ __launch_bounds__(W * 64) void q8_gemv_kernel(const int8_t* __restric
       }
       for (int64_t r = 0; r < (hold ? 0 : m); ++r) {
         float mx = 0.0f;
+        const float inv = XF == 3 ? row_inv(r) : 0.0f;
         for (int64_t c = threadIdx.x; c < nv; c += W * 64) {
           float v[N];
-          act(r, c, v);
+          act(r, c, v, inv, true);
 #pragma unroll
           for (int e = 0; e < N; ++e) mx = fmaxf(mx, fabsf(v[e]));
         }
@@ -593,9 +740,10 @@ __global__ __launch_bounds__(W * 64) void q8_gemv_kernel(const int8_t* __restric
         for (int w = 1; w < W; ++w) mx = fmaxf(mx, xf_max[w * kGemvMaxM + r]);
         const float sc = q8_row_scale(mx);
         if (threadIdx.x == 0) xf_scale[r] = sc;
+        const float inv = XF == 3 ? row_inv(r) : 0.0f;
         for (int64_t c = threadIdx.x; c < nv; c += W * 64) {
           float v[N];
-          act(r, c, v);
+          act(r, c, v, inv, false);
           quant_store(r, c, v, sc);
         }
       }
@@ -741,13 +889,23 @@ bool try_gemv(const int8_t* xq, const float* rscale, const int8_t* w8, const uin
 
 // The GEMV with the fused activation quantizer (XF 1 or 2): always the staged-row
 // form; false when the rows or the scales would not fit the workgroup's LDS.
+// The fused norm's operands (XF 3).
+template <typename TO>
+struct RmsOperands {
+  const TO* res = nullptr;
+  TO* res_out = nullptr;
+  const TO* g = nullptr;
+  float eps = 0.0f;
+};
+
 template <typename TO, int W, int S, int XF>
 bool try_gemv_act(const TO* xf, int64_t xf_ld, const int8_t* w8, const uint16_t* ws, TO* out, int64_t m, int64_t n,
-                  int64_t k, hipStream_t stream) {
+                  int64_t k, hipStream_t stream, const RmsOperands<TO>& rn) {
   constexpr int kDma = W * 2 * kGvWaveBuf;
   constexpr int kCols = gemv_cols<W, S>();
   const int64_t sc_bytes = (kCols * (k / 32) * 2 + 15) & ~15;
-  const int64_t x_bytes = ((m * (k + 16) + 15) & ~int64_t(15)) + (W + 1) * kGemvMaxM * 4;  // rows, maxima, scales
+  // rows, then maxima, scales and the norm's sums of squares
+  const int64_t x_bytes = ((m * (k + 16) + 15) & ~int64_t(15)) + (W + 1 + 4) * kGemvMaxM * 4;
   if (sc_bytes > kGemvScaleLds || x_bytes > kGemvXLdsMax || kDma + sc_bytes + x_bytes > kLdsPerCu) return false;
   static std::once_flag attr_once;
   std::call_once(attr_once, [] {
@@ -757,7 +915,8 @@ bool try_gemv_act(const TO* xf, int64_t xf_ld, const int8_t* w8, const uint16_t*
   });
   const int64_t wgs = (n + kCols - 1) / kCols;
   q8_gemv_kernel<TO, W, S, true, XF><<<dim3((unsigned)wgs), dim3(W * 64), (size_t)(kDma + sc_bytes + x_bytes),
-                                        stream>>>(nullptr, nullptr, w8, ws, out, m, n, k, (int)sc_bytes, xf, xf_ld);
+                                        stream>>>(nullptr, nullptr, w8, ws, out, m, n, k, (int)sc_bytes, xf, xf_ld,
+                                                  rn.res, rn.res_out, rn.g, rn.eps);
   return true;
 }
 
@@ -899,13 +1058,13 @@ int launch_gemm(const int8_t* xq, const float* rscale, const int8_t* w8, const u
 // choice as launch_gemm; NVF_ERR_INVALID when no GEMV form fits.
 template <typename TO, int XF>
 int launch_gemv_act(const TO* xf, int64_t xf_ld, const int8_t* w8, const uint16_t* ws, TO* out, int64_t m, int64_t n,
-                    int64_t k, hipStream_t stream) {
+                    int64_t k, hipStream_t stream, const RmsOperands<TO>& rn = {}) {
   const int64_t groups = (n + 15) / 16;
   bool ok = false;
-  if (groups >= 2048) ok = try_gemv_act<TO, 4, 1, XF>(xf, xf_ld, w8, ws, out, m, n, k, stream);
-  if (!ok && groups >= 1024) ok = try_gemv_act<TO, 4, 2, XF>(xf, xf_ld, w8, ws, out, m, n, k, stream);
-  if (!ok && groups >= 512) ok = try_gemv_act<TO, 4, 4, XF>(xf, xf_ld, w8, ws, out, m, n, k, stream);
-  if (!ok) ok = try_gemv_act<TO, 8, 8, XF>(xf, xf_ld, w8, ws, out, m, n, k, stream);
+  if (groups >= 2048) ok = try_gemv_act<TO, 4, 1, XF>(xf, xf_ld, w8, ws, out, m, n, k, stream, rn);
+  if (!ok && groups >= 1024) ok = try_gemv_act<TO, 4, 2, XF>(xf, xf_ld, w8, ws, out, m, n, k, stream, rn);
+  if (!ok && groups >= 512) ok = try_gemv_act<TO, 4, 4, XF>(xf, xf_ld, w8, ws, out, m, n, k, stream, rn);
+  if (!ok) ok = try_gemv_act<TO, 8, 8, XF>(xf, xf_ld, w8, ws, out, m, n, k, stream, rn);
   if (!ok)
     return fail(NVF_ERR_INVALID, "matmul_q8_0_act: m=%lld rows of k=%lld do not fit the GEMV's LDS (quantize "
                 "separately and use nvf_matmul_q8_0)", (long long)m, (long long)k);
@@ -996,6 +1155,51 @@ int nvf_matmul_q8_0_act(const void* x, int64_t x_stride, int act, const uint8_t*
   else
     NVF_DISPATCH_DTYPE(dtype, T, rc = (launch_gemv_act<T, 2>(static_cast<const T*>(x), x_stride, w, ws,
                                                             static_cast<T*>(out), m, n, k, as_stream(stream))));
+  return rc;
+}
+
+int nvf_matmul_q8_0_rms(const void* x, int64_t x_stride, const void* residual, void* residual_out,
+                        const void* norm_weight, float eps, const uint8_t* w8, const uint16_t* ws, int64_t m, int64_t n,
+                        int64_t k, void* out, int dtype, void* stream) {
+  static const char* who = "matmul_q8_0_rms";
+  if (m < 0 || n < 0 || k < 0) return fail(NVF_ERR_INVALID, "%s: negative size", who);
+  if (k % 32 != 0) return fail(NVF_ERR_INVALID, "%s: k=%lld is not a multiple of the Q8_0 block (32)", who, (long long)k);
+  if (!dtype_ok(dtype)) return fail(NVF_ERR_INVALID, "%s: bad dtype %d", who, dtype);
+  if (m > kGemvMaxM)
+    return fail(NVF_ERR_INVALID, "%s: m=%lld > %d rows (the decode GEMV's; use nvf_rms_norm_q8 and "
+                "nvf_matmul_q8_0)", who, (long long)m, kGemvMaxM);
+  const int64_t eb = dtype_bytes(dtype);
+  const int64_t nvec = k * eb / 16;
+  if (nvec > (int64_t)kRmsMaxVpl * 4 * 64)
+    return fail(NVF_ERR_INVALID, "%s: k=%lld exceeds the register-resident norm row (use nvf_rms_norm_q8 and "
+                "nvf_matmul_q8_0)", who, (long long)k);
+  if (x_stride < k) return fail(NVF_ERR_INVALID, "%s: x_stride=%lld too small", who, (long long)x_stride);
+  if ((residual == nullptr) != (residual_out == nullptr))
+    return fail(NVF_ERR_INVALID, "%s: residual and residual_out go together", who);
+  if (m == 0 || n == 0 || k == 0) return NVF_OK;
+  if (!x || !norm_weight || !w8 || !ws || !out) return fail(NVF_ERR_INVALID, "%s: null pointer", who);
+  if (!aligned16(x) || !aligned16(w8) || !aligned16(norm_weight) || (x_stride * eb) % 16 != 0 ||
+      (residual && (!aligned16(residual) || !aligned16(residual_out))))
+    return fail(NVF_ERR_INVALID, "%s: x (and its rows), residual, residual_out, norm_weight and w8 must be 16-byte "
+                "aligned", who);
+  if ((reinterpret_cast<uintptr_t>(ws) & 1u) != 0) return fail(NVF_ERR_INVALID, "%s: ws must be 2-byte aligned", who);
+  if (residual) {
+    // every workgroup reads x and residual while workgroup 0 writes residual_out
+    auto overlap = [](const void* a, int64_t an, const void* b, int64_t bn) {
+      const uintptr_t pa = reinterpret_cast<uintptr_t>(a), pb = reinterpret_cast<uintptr_t>(b);
+      return pa < pb + (uintptr_t)bn && pb < pa + (uintptr_t)an;
+    };
+    const int64_t rb = m * k * eb, xb = ((m - 1) * x_stride + k) * eb;
+    if (overlap(residual_out, rb, residual, rb) || overlap(residual_out, rb, x, xb))
+      return fail(NVF_ERR_INVALID, "%s: residual_out must not overlap residual or x", who);
+  }
+  const int8_t* w = reinterpret_cast<const int8_t*>(w8);
+  int rc = NVF_OK;
+  NVF_DISPATCH_DTYPE(dtype, T, (rc = launch_gemv_act<T, 3>(
+                                    static_cast<const T*>(x), x_stride, w, ws, static_cast<T*>(out), m, n, k,
+                                    as_stream(stream),
+                                    RmsOperands<T>{static_cast<const T*>(residual), static_cast<T*>(residual_out),
+                                                   static_cast<const T*>(norm_weight), eps})));
   return rc;
 }
 

@@ -28,7 +28,7 @@ namespace nvf {
 
 constexpr int kNormThreads = 256;
 constexpr int kNormWaves = kNormThreads / kWave;
-constexpr int kNormMaxVpl = 16;  // 16 x 4 waves x 64 lanes x 16 B = a 64 KiB row in registers
+constexpr int kNormMaxVpl = kRmsMaxVpl;  // 16 x 4 waves x 64 lanes x 16 B = a 64 KiB row in registers
 
 template <typename T, int VPL, int WPR, bool ADD, bool Q8>
 __global__ __launch_bounds__(kNormThreads) void rms_norm_vec_kernel(const T* x, T* residual, const T* __restrict__ w,
@@ -76,7 +76,7 @@ __global__ __launch_bounds__(kNormThreads) void rms_norm_vec_kernel(const T* x, 
         Pack<T>::unpack(stored, v[i]);  // the norm sees the stored (rounded) row
       }
 #pragma unroll
-      for (int j = 0; j < N; ++j) ss += v[i][j] * v[i][j];
+      for (int j = 0; j < N; ++j) ss = fmaf(v[i][j], v[i][j], ss);
     }
   }
   ss = wave_sum(ss);
@@ -192,7 +192,7 @@ static int launch_rms(const void* x, void* residual, const void* w, void* out, i
   constexpr int N = Pack<T>::N;
   const int64_t nvec = hidden / N;
   // waves per row: 4 once a row has >= 256 vectors, else fewer, so lanes stay busy
-  const int wpr = nvec >= 4 * kWave ? 4 : (nvec >= 2 * kWave ? 2 : 1);
+  const int wpr = rms_waves_per_row(nvec);
   const int vpl = (int)((nvec + (int64_t)wpr * kWave - 1) / ((int64_t)wpr * kWave));
   const bool vec_ok = hidden % N == 0 && vpl >= 1 && vpl <= (wpr == 4 ? kNormMaxVpl : 2) && aligned16(x) &&
                       aligned16(w) && (!out || aligned16(out)) && (!ADD || aligned16(residual)) &&

@@ -75,6 +75,8 @@ SIGNATURES: dict[str, tuple] = {
     "nvf_matmul_q8_0_ws": (_i32, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _i32, _vp, _i64, _vp]),
     "nvf_matmul_q8_0_workspace_size": (_i64, [_i64, _i64, _i64]),
     "nvf_matmul_q8_0_act": (_i32, [_vp, _i64, _i32, _vp, _vp, _i64, _i64, _i64, _vp, _i32, _vp]),
+    "nvf_matmul_q8_0_rms": (_i32, [_vp, _i64, _vp, _vp, _vp, C.c_float, _vp, _vp, _i64, _i64, _i64, _vp, _i32,
+                                   _vp]),
     "nvf_rms_norm_add": (_i32, [_vp, _vp, _vp, _vp, _i64, _i64, _f32, _i32, _vp]),
     "nvf_rms_norm": (_i32, [_vp, _vp, _vp, _i64, _i64, _f32, _i32, _vp]),
     "nvf_rms_norm_q8": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _f32, _i32, _vp]),
@@ -262,6 +264,31 @@ def matmul_q8_0_act(x: torch.Tensor, w8: torch.Tensor, ws: torch.Tensor, n: int,
         raise ValueError("out must be [m, n] in x's dtype")
     _check(lib().nvf_matmul_q8_0_act(_dev_rows(x, "x"), x.stride(0), 1 if swiglu else 0, _dev(w8, "w8"),
                                      _dev(ws, "ws"), m, n, k, _dev(out, "out"), _dt(x), _stream()), "matmul_q8_0_act")
+    return out
+
+
+def matmul_q8_0_rms(x: torch.Tensor, weight: torch.Tensor, eps: float, w8: torch.Tensor, ws: torch.Tensor, n: int,
+                    residual: torch.Tensor | None = None, residual_out: torch.Tensor | None = None,
+                    out: torch.Tensor | None = None) -> torch.Tensor:
+    """Decode GEMV (x.shape[0] <= 16 rows) with (residual-add +) RMSNorm and the quantizer
+    in its prologue: out [m, n] is bit-identical to rms_norm_q8 then matmul_q8_0.  With a
+    residual [m, k] the summed rows go to residual_out (a second [m, k] buffer; required
+    with residual, and it must not overlap x or residual)."""
+    m, k = x.shape
+    if weight.dtype != x.dtype or weight.numel() != k:
+        raise ValueError("weight must be [k] in x's dtype")
+    if (residual is None) != (residual_out is None):
+        raise ValueError("residual and residual_out go together")
+    for name, t in (("residual", residual), ("residual_out", residual_out)):
+        if t is not None and (t.dtype != x.dtype or t.shape != (m, k) or not t.is_contiguous()):
+            raise ValueError(f"{name} must be a contiguous [m, k] tensor in x's dtype")
+    out = torch.empty((m, n), dtype=x.dtype, device=x.device) if out is None else out
+    if out.dtype != x.dtype or out.shape != (m, n):
+        raise ValueError("out must be [m, n] in x's dtype")
+    _check(lib().nvf_matmul_q8_0_rms(
+        _dev_rows(x, "x"), x.stride(0), _dev(residual, "residual") if residual is not None else None,
+        _dev(residual_out, "residual_out") if residual_out is not None else None, _dev(weight, "weight"), eps,
+        _dev(w8, "w8"), _dev(ws, "ws"), m, n, k, _dev(out, "out"), _dt(x), _stream()), "matmul_q8_0_rms")
     return out
 
 

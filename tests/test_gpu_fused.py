@@ -235,6 +235,57 @@ def test_gemv_with_fused_quantizer_rejects(gpu):
 
 
 @pytest.mark.parametrize("dt", DTYPES, ids=DT_IDS)
+@pytest.mark.parametrize("m,k,n,add", [
+    (1, 3584, 4608, True),     # batch-1 qkv after the input norm (W8 S8 workgroups)
+    (1, 3584, 37888, True),    # batch-1 gate_up after the post-attention norm (W4 S1)
+    (1, 4096, 6144, False),    # first layer: no residual yet
+    (3, 3584, 4608, True),
+    (16, 2048, 1040, True),    # 16 rows, ragged column count
+    (2, 1024, 520, False),     # a 2-wave norm row for fp16/bf16 (128 vectors)
+    (1, 512, 256, True),       # a 1-wave norm row
+    (1, 8192, 1024, True),     # fp32: a norm row past the preloaded 4 vectors per lane
+])
+def test_gemv_with_fused_rms_norm(gpu, dt, m, k, n, add):
+    """nvf_matmul_q8_0_rms (residual-add + RMSNorm + quantizer in the decode GEMV's
+    prologue) is bit-identical to nvf_rms_norm_q8 followed by nvf_matmul_q8_0, the
+    residual it writes to the residual of the separate norm, and residual and x are
+    left unchanged."""
+    r = H.rng(m * 11 + k + n + dt + 5 * add)
+    w8, ws = H.gen_q8_0(r, n, k)
+    d_w8, d_ws = H.to_dev(w8, gpu), H.to_dev(ws, gpu)
+    x_full = H.to_dev(H.gen_act(r, (m, k + 64), dt), gpu, dt)
+    x = x_full[:, :k]  # strided rows
+    g = H.to_dev(H.gen_act(r, (k,), dt), gpu, dt)
+    res = H.to_dev(H.gen_act(r, (m, k), dt), gpu, dt) if add else None
+    res_before = res.clone() if add else None
+    x_before = x.clone()
+    res_out = torch.full_like(res, float("nan")) if add else None
+    case(f"gemv rms m={m} k={k} n={n} add={add} dt={dt}")
+    got = ops.matmul_q8_0_rms(x, g, 1e-6, d_w8, d_ws, n, residual=res, residual_out=res_out)
+    res_sep = res.clone() if add else None
+    _, sc, q = ops.rms_norm_q8(x.contiguous(), g, 1e-6, residual=res_sep, want_out=False)
+    want = ops.matmul_q8_0(q, sc, d_w8, d_ws, n, x.dtype)
+    torch.cuda.synchronize()
+    H.assert_bitexact(H.to_host(got), H.to_host(want), "fused norm vs separate norm + GEMV")
+    H.assert_bitexact(H.to_host(x), H.to_host(x_before), "x unchanged")
+    if add:
+        H.assert_bitexact(H.to_host(res_out), H.to_host(res_sep), "residual_out vs the norm's residual")
+        H.assert_bitexact(H.to_host(res), H.to_host(res_before), "residual unchanged")
+
+
+def test_gemv_with_fused_rms_norm_rejects(gpu):
+    x = torch.zeros(1, 1024, dtype=torch.float16, device=gpu)
+    g = torch.ones(1024, dtype=torch.float16, device=gpu)
+    w8 = torch.zeros(64 * 1024, dtype=torch.int8, device=gpu)
+    ws = torch.zeros(64 * 32, dtype=torch.int16, device=gpu)
+    res = torch.zeros_like(x)
+    with pytest.raises(RuntimeError, match="overlap"):
+        ops.matmul_q8_0_rms(x, g, 1e-6, w8, ws, 64, residual=res, residual_out=res)
+    with pytest.raises(RuntimeError, match="m=17"):
+        ops.matmul_q8_0_rms(torch.zeros(17, 1024, dtype=torch.float16, device=gpu), g, 1e-6, w8, ws, 64)
+
+
+@pytest.mark.parametrize("dt", DTYPES, ids=DT_IDS)
 @pytest.mark.parametrize("tokens,qh,kvh,hd,norm", [
     (37, 28, 4, 128, False),   # Qwen2.5-7B heads, packed [q | k | v] rows
     (5, 32, 8, 128, True),     # Qwen3-8B: QK-norm fused as well
