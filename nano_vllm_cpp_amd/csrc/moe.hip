@@ -601,6 +601,7 @@ int nvf_moe_route(const float* logits, int64_t rows, int64_t E, int64_t K, int n
   if (rows < 0 || E <= 0 || K <= 0 || K > E || E > kMoeMaxExperts)
     return fail(NVF_ERR_INVALID, "nvf_moe_route: bad sizes rows=%lld E=%lld K=%lld (E <= %d, K <= E)",
                 (long long)rows, (long long)E, (long long)K, kMoeMaxExperts);
+  if (rows > INT32_MAX) return fail(NVF_ERR_INVALID, "nvf_moe_route: rows=%lld exceed one launch", (long long)rows);
   if (rows == 0) return NVF_OK;
   if (!logits || !idx || !score) return fail(NVF_ERR_INVALID, "nvf_moe_route: NULL pointer");
   moe_route_kernel<<<(unsigned)rows, 64, (size_t)E * (sizeof(double) + sizeof(int)), as_stream(stream)>>>(
@@ -688,6 +689,8 @@ int nvf_add_inplace(float* dst, const float* src, int64_t n, void* stream) {
 
 int nvf_scale_rows_sigmoid(float* dst, const float* s, int64_t rows, int64_t cols, void* stream) {
   if (rows < 0 || cols < 0) return fail(NVF_ERR_INVALID, "nvf_scale_rows_sigmoid: negative size");
+  if (rows > INT32_MAX)
+    return fail(NVF_ERR_INVALID, "nvf_scale_rows_sigmoid: rows=%lld exceed one launch", (long long)rows);
   if (rows == 0 || cols == 0) return NVF_OK;
   if (!dst || !s) return fail(NVF_ERR_INVALID, "nvf_scale_rows_sigmoid: NULL pointer");
   scale_rows_sigmoid_kernel<<<(unsigned)rows, 256, 0, as_stream(stream)>>>(dst, s, cols);
