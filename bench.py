@@ -60,7 +60,7 @@ def parse() -> argparse.Namespace:
                    help="no benchmark: build profiles/traffic.json from rocprofv3 FETCH_SIZE / WRITE_SIZE runs under DIR")
     p.add_argument("--only", default="",
                    help="comma list of ops (default emb,rms,rope,silu,copy,gemm,gemv,split,attn,attn_decode,attn_f32,"
-                        "attn_decode_f32,attn_decode_small,layer,layer_decode,layer_b1,layer_b1_graph); "
+                        "attn_decode_ordered,attn_decode_f32,attn_decode_small,layer,layer_decode,layer_b1,layer_b1_graph); "
                         "also emb_rms, rms_q8, silu_q8 (fusions)")
     return p.parse_args()
 
@@ -120,7 +120,7 @@ def main() -> int:
     nbytes = op_bytes(cfg, e, emb_fmt)
     only = set(filter(None, args.only.split(","))) or {"emb", "rms", "rope", "silu", "copy", "copy12", "copy12_emb",
                                                        "gemm", "gemv", "split", "lm_head", "lm_head_q4k", "moe",
-                                                       "attn", "attn_decode", "attn_f32", "attn_decode_f32", "attn_decode_small", "layer", "layer_decode", "layer_b1", "layer_b1_graph"}
+                                                       "attn", "attn_decode", "attn_decode_ordered", "attn_f32", "attn_decode_f32", "attn_decode_small", "layer", "layer_decode", "layer_b1", "layer_b1_graph"}
 
     def nsets(b: int) -> int:
         return max(2, -(-POOL_BYTES // b))
@@ -233,7 +233,7 @@ def main() -> int:
         # host-side guard before any kernel runs: every key a query attends has a block
         aseq = np.repeat(np.arange(len(lens)), lens)
         assert ((apos + 1) <= np.array(nblk)[aseq] * bs_kv).all(), "attention inputs: keys past the block tables"
-    if {"attn_decode", "attn_decode_f32"} & only:  # one token per sequence, 256 sequences, context uniform in 1..4096
+    if {"attn_decode", "attn_decode_ordered", "attn_decode_f32"} & only:  # one token per sequence, 256 sequences, context uniform in 1..4096
         ctx = np.random.default_rng(cfg.seed + 11).integers(1, 4097, 256)
         nblk = [-(-int(n) // bs_kv) for n in ctx]
         tables = torch.full((256, max(nblk)), -1, dtype=torch.int32)
@@ -248,6 +248,8 @@ def main() -> int:
                     torch.from_numpy(ctx.astype(np.int32)).to(dev), tables.to(dev))
         dec_bytes = float(ctx.sum()) * cfg.kv_heads * cfg.head_dim * 2 * e + 2 * 256 * cfg.q_heads * cfg.head_dim * e
         dec_bytes32 = dec_bytes * 4 / e
+        # the schedule an engine computes from the key counts it holds on the host
+        dec_order = torch.from_numpy(ops.decode_token_order(ctx)).to(dev)
     attn_small = None
     if "attn_decode_small" in only:  # 4 sequences x 32768 keys of context: the split decode path
         sctx, sB = 32768, 4
@@ -320,6 +322,8 @@ def main() -> int:
         if "layer_decode" in only:  # a decode step: 256 sequences, one new token each, context U[1, 4096]
             dctx = np.random.default_rng(cfg.seed + 7).integers(1, 4097, 256)
             layer_dec = build_layer(dctx - 1, np.arange(256), dctx, 1, cfg.seed + 8)
+            # the decode kernel's schedule from the key counts the engine holds on the host
+            layer_dec["order"] = torch.from_numpy(ops.decode_token_order(dctx)).to(dev)
             dec_ops, dec_attn_flops = layer_flops(256, dctx - 1)
             dec_kv_bytes = float(dctx.sum()) * cfg.kv_heads * cfg.head_dim * 2 * e
         if {"layer_b1", "layer_b1_graph"} & only:  # latency: one sequence, one new token, 4096 keys of context
@@ -421,6 +425,11 @@ def main() -> int:
         q_, kc_, vc_, qs_, ql_, tb_ = attn_dec
         ops.paged_attention(q_, kc_, vc_, qs_, ql_, tb_, bs_kv, cfg.head_dim ** -0.5, out=dec_out, max_query_len=1)
 
+    def run_attn_decode_ordered(i):
+        q_, kc_, vc_, qs_, ql_, tb_ = attn_dec
+        ops.paged_attention(q_, kc_, vc_, qs_, ql_, tb_, bs_kv, cfg.head_dim ** -0.5, out=dec_out, max_query_len=1,
+                            token_order=dec_order)
+
     def run_attn_decode_small(i):
         q_, kc_, vc_, qs_, ql_, tb_ = attn_small
         ops.paged_attention(q_, kc_, vc_, qs_, ql_, tb_, bs_kv, cfg.head_dim ** -0.5, out=small_out, max_query_len=1)
@@ -448,8 +457,10 @@ def main() -> int:
                                   cfg.eps, qkv_bias=L_["bias"])
         att = ops.paged_attention(qkv[:, :qs].view(n_, cfg.q_heads, cfg.head_dim), L_["kc"], L_["vc"], L_["qseq"],
                                   L_["qlen"], L_["tab"], bs_kv, cfg.head_dim ** -0.5, out=L_["attn_out"],
-                                  max_query_len=L_["mql"], cu_seqlens=L_.get("cu"),
-                                  noalloc=L_["mql"] == 1)  # decode: the split's partials in the static scratch
+                                  max_query_len=L_["mql"], cu_seqlens=L_.get("cu"), token_order=L_.get("order"),
+                                  # decode: the split's partials in the static scratch (a scheduled
+                                  # 256-sequence step never splits)
+                                  noalloc=L_["mql"] == 1 and L_.get("order") is None)
         if n_ <= 16:
             o = ops.matmul_q8_0_act(att.view(n_, qs), *L_["o"], Hd, out=L_["o_out"])
         else:
@@ -518,6 +529,7 @@ def main() -> int:
              ("copy12", run_copy12), ("copy12_emb", run_copy12_emb), ("gemm", run_gemm),
              ("gemv", run_gemv), ("split", run_split), ("lm_head", run_lm("lm_head")),
              ("lm_head_q4k", run_lm("lm_head_q4k")), ("moe", run_moe), ("attn", run_attn), ("attn_decode", run_attn_decode),
+             ("attn_decode_ordered", run_attn_decode_ordered),
              ("attn_f32", run_attn_f32), ("attn_decode_f32", run_attn_decode_f32), ("attn_decode_small", run_attn_decode_small),
              ("layer", run_layer), ("layer_decode", run_layer_decode), ("layer_b1", run_layer_b1),
              ("layer_b1_graph", run_layer_b1_graph)]
@@ -603,10 +615,12 @@ def main() -> int:
             entry.update({"shape": f"as attn, fp32 cache and activations (the drop-in hip_paged_attention)",
                           "TFLOP_s": round(attn_flops / (t_us * 1e-6) / 1e12, 1),
                           "frac_of_fp32_peak": round(attn_flops / (t_us * 1e-6) / FP32_PEAK_FLOPS, 4)})
-        elif n in ("attn_decode", "attn_decode_f32"):
-            db = dec_bytes if n == "attn_decode" else dec_bytes32
+        elif n in ("attn_decode", "attn_decode_ordered", "attn_decode_f32"):
+            db = dec_bytes32 if n == "attn_decode_f32" else dec_bytes
             entry.update({"shape": f"decode 256 sequences, context uniform in 1..4096, {cfg.q_heads}/{cfg.kv_heads} "
-                                   f"heads x {cfg.head_dim}" + (", fp32 cache" if n != "attn_decode" else ""),
+                                   f"heads x {cfg.head_dim}" + (", fp32 cache" if n == "attn_decode_f32" else "") +
+                                   (", host-computed token order (nvf_decode_token_order)"
+                                    if n == "attn_decode_ordered" else ""),
                           "bytes": int(db), "GB_s": round(db / (t_us * 1e-6) / 1e9, 1),
                           "frac_of_peak": round(db / (t_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)})
         elif n == "attn_decode_small":
@@ -702,7 +716,8 @@ def main() -> int:
         "layer_decode": res_ops.get("layer_decode"),
         "layer_b1": res_ops.get("layer_b1"),
         "layer_b1_graph": res_ops.get("layer_b1_graph"),
-        "paged_attention": {k: res_ops[k] for k in ("attn", "attn_decode", "attn_f32", "attn_decode_f32",
+        "paged_attention": {k: res_ops[k] for k in ("attn", "attn_decode", "attn_decode_ordered", "attn_f32",
+                                                    "attn_decode_f32",
                                                     "attn_decode_small") if k in res_ops} or None,
         "cpu_baseline": cpu,
     }

@@ -427,6 +427,24 @@ int nvf_paged_attention_seqs_ws(const void* q, void* out, const void* k_cache, c
                                 int64_t q_stride, int64_t max_query_len, void* workspace, int64_t workspace_bytes,
                                 int dtype, void* stream);
 
+/* nvf_paged_attention_ws with the caller's schedule for the decode kernel (no
+ * counterpart in the reference): token_order (device int32 [tokens], a permutation of
+ * 0 .. tokens-1) names the token each decode workgroup computes.  Results equal
+ * nvf_paged_attention_ws's; only the time depends on it.  For a decode batch with
+ * ragged contexts, nvf_decode_token_order gives one that balances the GPU's 8 XCDs
+ * (workgroup id mod 8 is its XCD); the engine holds the key counts on the host
+ * (src/model_runner.cpp:122) and uploads the order with them.  16-bit caches; the
+ * fp32 decode kernel and prefill tiles ignore it. */
+int nvf_paged_attention_order_ws(const void* q, void* out, const void* k_cache, const void* v_cache,
+                                 const int32_t* query_seq, const int32_t* query_key_len, const int32_t* block_tables,
+                                 const int32_t* token_order, int64_t tokens, int q_heads, int kv_heads, int head_dim,
+                                 int block_size, int max_blocks, float scale, int64_t q_stride, int64_t max_query_len,
+                                 void* workspace, int64_t workspace_bytes, int dtype, void* stream);
+
+/* Host only: order_host [tokens] = the tokens sorted by key_len_host (descending, ties
+ * by index) and dealt over 8 XCDs in snake order, for nvf_paged_attention_order_ws. */
+int nvf_decode_token_order(const int32_t* key_len_host, int64_t tokens, int32_t* order_host);
+
 /* Bytes of workspace nvf_paged_attention_ws uses for this shape and max_query_len
  * hint (0: it would not split).  The context bound is block_size * max_blocks. */
 int64_t nvf_paged_attention_workspace_size(int64_t tokens, int q_heads, int kv_heads, int head_dim, int block_size,

@@ -22,7 +22,9 @@
 
 #include <math.h>
 
+#include <algorithm>
 #include <mutex>
+#include <vector>
 
 #include "nvf_device.hpp"
 #include "nvf_host.hpp"
@@ -667,13 +669,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
     const T* __restrict__ q, T* __restrict__ out, const T* __restrict__ kc, const T* __restrict__ vc,
     const int32_t* __restrict__ qseq, const int32_t* __restrict__ qlen, const int32_t* __restrict__ tables,
     int64_t tokens, int q_heads, int kv_heads, int bs, int max_blocks, float scale_log2, int64_t q_stride,
-    int split_keys, float* __restrict__ part) {
+    int split_keys, float* __restrict__ part, const int32_t* __restrict__ order) {
   using M = Mfma16x16<T>;
   using v8 = typename M::v8;
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
-  const int64_t t = blockIdx.x;
+  // order (not with SKIP): the caller's permutation of the tokens over the workgroups
+  // (which token each computes; the results do not depend on it)
+  const int64_t t = !SKIP && order ? (int64_t)order[blockIdx.x] : (int64_t)blockIdx.x;
   // workgroup-uniform: the whole workgroup leaves (fa_prefill_kernel's tile)
   if (SKIP && fa_tile_uniform(qseq, tokens, t / kFaBq)) return;
   // The tiles' second launch (SKIP) has one workgroup per token, so that its many
@@ -1187,7 +1191,7 @@ template <typename T>
 int attention_dispatch(const void* q, void* out, const void* kc, const void* vc, const int32_t* qseq,
                        const int32_t* qlen, const int32_t* tables, int64_t tokens, int q_heads, int kv_heads, int hd,
                        int bs, int max_blocks, float scale, int64_t q_stride, int64_t max_query_len, void* ws,
-                       int64_t ws_bytes, hipStream_t st, bool aligned = false) {
+                       int64_t ws_bytes, hipStream_t st, bool aligned = false, const int32_t* order = nullptr) {
   // aligned: every sequence starts at a multiple of kFaBq tokens (checked on the host
   // from the caller's cu_seqlens), so every tile is uniform and the tiles' second
   // launch, whose workgroups would all exit, is not made
@@ -1269,6 +1273,9 @@ int attention_dispatch(const void* q, void* out, const void* kc, const void* vc,
 #define NVF_DEC_LAUNCH(KERN, LDS)                                                                              \
   KERN<<<grid, 256, LDS, st>>>(qt, ot, kt, vt, qseq, qlen, tables, tokens, q_heads, kv_heads, bs, max_blocks, sl, \
                                q_stride, kk, pp)
+#define NVF_DEC_LAUNCH_ORD(KERN, LDS, ORD)                                                                     \
+  KERN<<<grid, 256, LDS, st>>>(qt, ot, kt, vt, qseq, qlen, tables, tokens, q_heads, kv_heads, bs, max_blocks, sl, \
+                               q_stride, kk, pp, ORD)
     if constexpr (sizeof(T) == 2) {
       static std::once_flag dec_once;
       std::call_once(dec_once, [] {
@@ -1278,10 +1285,10 @@ int attention_dispatch(const void* q, void* out, const void* kc, const void* vc,
                              reinterpret_cast<const void*>(&fa_decode_kernel<T, true, true>)};
         for (const void* k : ks) (void)hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, kFdLds);
       });
-      if (split && tiles) NVF_DEC_LAUNCH((fa_decode_kernel<T, true, true>), kFdLds);
-      else if (split) NVF_DEC_LAUNCH((fa_decode_kernel<T, true, false>), kFdLds);
-      else if (tiles) NVF_DEC_LAUNCH((fa_decode_kernel<T, false, true>), kFdLds);
-      else NVF_DEC_LAUNCH((fa_decode_kernel<T, false, false>), kFdLds);
+      if (split && tiles) NVF_DEC_LAUNCH_ORD((fa_decode_kernel<T, true, true>), kFdLds, nullptr);
+      else if (split) NVF_DEC_LAUNCH_ORD((fa_decode_kernel<T, true, false>), kFdLds, order);
+      else if (tiles) NVF_DEC_LAUNCH_ORD((fa_decode_kernel<T, false, true>), kFdLds, nullptr);
+      else NVF_DEC_LAUNCH_ORD((fa_decode_kernel<T, false, false>), kFdLds, order);
     } else {
       if (split && tiles) NVF_DEC_LAUNCH((fa_decode_f32_kernel<true, true>), 0);
       else if (split) NVF_DEC_LAUNCH((fa_decode_f32_kernel<true, false>), 0);
@@ -1289,6 +1296,7 @@ int attention_dispatch(const void* q, void* out, const void* kc, const void* vc,
       else NVF_DEC_LAUNCH((fa_decode_f32_kernel<false, false>), 0);
     }
 #undef NVF_DEC_LAUNCH
+#undef NVF_DEC_LAUNCH_ORD
     int rc = launch_status("paged_attention(decode)");
     if (rc != NVF_OK || !split) return rc;
     attn_split_combine_kernel<T><<<dim3((unsigned)tokens, (unsigned)q_heads), 256, 0, st>>>(part, ot, tokens,
@@ -1363,7 +1371,8 @@ static int paged_attention_entry(const void* q, void* out, const void* k_cache, 
                                  const int32_t* query_seq, const int32_t* query_key_len, const int32_t* block_tables,
                                  int64_t tokens, int q_heads, int kv_heads, int head_dim, int block_size,
                                  int max_blocks, float scale, int64_t q_stride, int64_t max_query_len, void* workspace,
-                                 int64_t workspace_bytes, int dtype, void* stream, bool aligned) {
+                                 int64_t workspace_bytes, int dtype, void* stream, bool aligned,
+                                 const int32_t* order = nullptr) {
   if (!dtype_ok(dtype)) return fail(NVF_ERR_INVALID, "nvf_paged_attention: bad dtype %d", dtype);
   if (tokens < 0 || q_heads <= 0 || kv_heads <= 0 || head_dim <= 0 || block_size <= 0 || max_blocks <= 0)
     return fail(NVF_ERR_INVALID, "nvf_paged_attention: bad shape");
@@ -1383,7 +1392,7 @@ static int paged_attention_entry(const void* q, void* out, const void* k_cache, 
   NVF_DISPATCH_DTYPE(dtype, T, rc = attention_dispatch<T>(q, out, k_cache, v_cache, query_seq, query_key_len,
                                                          block_tables, tokens, q_heads, kv_heads, head_dim, block_size,
                                                          max_blocks, scale, q_stride, max_query_len, workspace,
-                                                         workspace_bytes, as_stream(stream), aligned));
+                                                         workspace_bytes, as_stream(stream), aligned, order));
   return rc;
 }
 
@@ -1395,6 +1404,37 @@ int nvf_paged_attention_ws(const void* q, void* out, const void* k_cache, const 
   return paged_attention_entry(q, out, k_cache, v_cache, query_seq, query_key_len, block_tables, tokens, q_heads,
                                kv_heads, head_dim, block_size, max_blocks, scale, q_stride, max_query_len, workspace,
                                workspace_bytes, dtype, stream, false);
+}
+
+int nvf_decode_token_order(const int32_t* key_len_host, int64_t tokens, int32_t* order_host) {
+  if (tokens < 0 || tokens > INT32_MAX) return fail(NVF_ERR_INVALID, "nvf_decode_token_order: bad token count");
+  if (tokens == 0) return NVF_OK;
+  if (!key_len_host || !order_host) return fail(NVF_ERR_INVALID, "nvf_decode_token_order: NULL pointer");
+  // longest first (ties by token), dealt over the 8 XCDs in snake order: round r of 8
+  // workgroups r*8 .. r*8+7 (workgroup id mod 8 is its XCD) takes the next 8 tokens,
+  // reversed on odd rounds, so every XCD's sum of key counts is nearly equal; a last
+  // partial round stays in order so that every id is below tokens
+  std::vector<int32_t> idx((size_t)tokens);
+  for (int64_t i = 0; i < tokens; ++i) idx[(size_t)i] = (int32_t)i;
+  std::stable_sort(idx.begin(), idx.end(),
+                   [&](int32_t a, int32_t b) { return key_len_host[a] > key_len_host[b]; });
+  for (int64_t p = 0; p < tokens; ++p) {
+    const int64_t r = p / 8, x = p % 8;
+    const bool full = r * 8 + 8 <= tokens;
+    order_host[r * 8 + ((r & 1) && full ? 7 - x : x)] = idx[(size_t)p];
+  }
+  return NVF_OK;
+}
+
+int nvf_paged_attention_order_ws(const void* q, void* out, const void* k_cache, const void* v_cache,
+                                 const int32_t* query_seq, const int32_t* query_key_len, const int32_t* block_tables,
+                                 const int32_t* token_order, int64_t tokens, int q_heads, int kv_heads, int head_dim,
+                                 int block_size, int max_blocks, float scale, int64_t q_stride, int64_t max_query_len,
+                                 void* workspace, int64_t workspace_bytes, int dtype, void* stream) {
+  if (!token_order) return fail(NVF_ERR_INVALID, "nvf_paged_attention_order_ws: NULL token_order");
+  return paged_attention_entry(q, out, k_cache, v_cache, query_seq, query_key_len, block_tables, tokens, q_heads,
+                               kv_heads, head_dim, block_size, max_blocks, scale, q_stride, max_query_len, workspace,
+                               workspace_bytes, dtype, stream, false, token_order);
 }
 
 int nvf_paged_attention_seqs_ws(const void* q, void* out, const void* k_cache, const void* v_cache,

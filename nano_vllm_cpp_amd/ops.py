@@ -66,6 +66,9 @@ SIGNATURES: dict[str, tuple] = {
                                       _i64, _i64, _vp, _i64, _i32, _vp]),
     "nvf_paged_attention_seqs_ws": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i64, _i32, _i32, _i32,
                                            _i32, _i32, _f32, _i64, _i64, _vp, _i64, _i32, _vp]),
+    "nvf_paged_attention_order_ws": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i32, _i32, _i32, _i32,
+                                            _i32, _f32, _i64, _i64, _vp, _i64, _i32, _vp]),
+    "nvf_decode_token_order": (_i32, [_vp, _i64, _vp]),
     "nvf_paged_attention_noalloc": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i32, _i32, _i32, _i32, _i32,
                                            _f32, _i64, _i64, _i32, _vp]),
     "nvf_paged_attention_noalloc_max_bytes": (_i64, []),
@@ -324,10 +327,20 @@ def store_kv(key: torch.Tensor, value: torch.Tensor, k_cache: torch.Tensor, v_ca
                               key.stride(0), value.stride(0), _dt(key), _stream()), "store_kv")
 
 
+def decode_token_order(key_len) -> np.ndarray:
+    """Host-side schedule for a decode batch (nvf_decode_token_order): the tokens
+    longest-first, dealt over the GPU's 8 XCDs in snake order.  key_len: the tokens' key
+    counts on the host.  Returns int32 [tokens] to upload as paged_attention's token_order."""
+    kl = np.ascontiguousarray(np.asarray(key_len, dtype=np.int32))
+    order = np.empty(len(kl), dtype=np.int32)
+    _check(lib().nvf_decode_token_order(kl.ctypes.data, len(kl), order.ctypes.data), "decode_token_order")
+    return order
+
+
 def paged_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, query_seq: torch.Tensor,
                     query_key_len: torch.Tensor, block_tables: torch.Tensor, block_size: int, scale: float,
                     out: torch.Tensor | None = None, max_query_len: int = 0, split: bool = True,
-                    cu_seqlens=None, noalloc: bool = False) -> torch.Tensor:
+                    cu_seqlens=None, noalloc: bool = False, token_order: torch.Tensor | None = None) -> torch.Tensor:
     """q [tokens, q_heads, head_dim] (row stride from the tensor); caches
     [rows, kv_heads, head_dim]; block_tables [seqs, max_blocks] int32.
     max_query_len = 1 promises a decode batch (one query per sequence).  split:
@@ -337,15 +350,17 @@ def paged_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tenso
     (nvf_paged_attention_seqs_ws: no launch for mixed tiles when every sequence
     starts at a multiple of 128 tokens).  noalloc: nvf_paged_attention_noalloc (the
     split's partials in the library's static device scratch, no workspace
-    allocated).
+    allocated).  token_order: a device int32 [tokens] permutation of the tokens over the
+    decode kernel's workgroups (decode_token_order; nvf_paged_attention_order_ws), results
+    unchanged.
     Returns out [tokens, q_heads, head_dim] in q's dtype."""
     tokens, q_heads, head_dim = q.shape
     kv_heads = k_cache.shape[1]
     max_blocks = block_tables.shape[1]
     out = torch.empty((tokens, q_heads, head_dim), dtype=q.dtype, device=q.device) if out is None else out
     if noalloc:
-        if cu_seqlens is not None or not split:
-            raise ValueError("noalloc takes neither cu_seqlens nor split=False")
+        if cu_seqlens is not None or not split or token_order is not None:
+            raise ValueError("noalloc takes neither cu_seqlens, token_order nor split=False")
         _check(lib().nvf_paged_attention_noalloc(
             _dev_rows(q, "q"), _dev(out, "out"), _dev(k_cache, "k_cache"), _dev(v_cache, "v_cache"),
             _dev(query_seq, "query_seq"), _dev(query_key_len, "query_key_len"), _dev(block_tables, "block_tables"),
@@ -355,6 +370,18 @@ def paged_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tenso
     ws_bytes = lib().nvf_paged_attention_workspace_size(tokens, q_heads, kv_heads, head_dim, block_size,
                                                        max_blocks, max_query_len) if split else 0
     ws = torch.empty((ws_bytes + 15) // 16 * 4, dtype=torch.float32, device=q.device) if ws_bytes > 0 else None
+    if token_order is not None:
+        if cu_seqlens is not None:
+            raise ValueError("token_order takes no cu_seqlens")
+        if token_order.dtype != torch.int32 or token_order.shape != (tokens,):
+            raise ValueError("token_order must be int32 [tokens]")
+        _check(lib().nvf_paged_attention_order_ws(
+            _dev_rows(q, "q"), _dev(out, "out"), _dev(k_cache, "k_cache"), _dev(v_cache, "v_cache"),
+            _dev(query_seq, "query_seq"), _dev(query_key_len, "query_key_len"), _dev(block_tables, "block_tables"),
+            _dev(token_order, "token_order"), tokens, q_heads, kv_heads, head_dim, block_size, max_blocks, scale,
+            q.stride(0), max_query_len, ws.data_ptr() if ws is not None else None, ws_bytes, _dt(q), _stream()),
+            "paged_attention")
+        return out
     if cu_seqlens is not None:
         cu = np.ascontiguousarray(np.asarray(cu_seqlens, dtype=np.int32))
         _check(lib().nvf_paged_attention_seqs_ws(

@@ -148,3 +148,25 @@ def test_missing_library_fails_loudly(monkeypatch, tmp_path):
     monkeypatch.setattr(ops, "_lib", None)
     with pytest.raises(RuntimeError, match="no CPU fallback"):
         ops.lib()
+
+
+@pytest.mark.parametrize("n", [0, 1, 5, 8, 13, 200, 256, 1000])
+def test_decode_token_order(n):
+    """nvf_decode_token_order (host only): a permutation of the tokens with every id
+    below n, the 8 longest contexts first (one per XCD), and each XCD's (workgroup id
+    mod 8) sum of key counts within one maximal context of every other's."""
+    r = np.random.default_rng(n)
+    kl = r.integers(0, 4097, n).astype(np.int32)
+    if n == 0:
+        assert ops.lib().nvf_decode_token_order(None, 0, None) == 0
+        return
+    order = ops.decode_token_order(kl)
+    assert sorted(order.tolist()) == list(range(n))
+    k = min(n, 8)
+    assert sorted(kl[order[:k]].tolist(), reverse=True) == sorted(kl.tolist(), reverse=True)[:k]
+    if n >= 16:
+        full = n // 8 * 8
+        sums = [int(kl[order[x:full:8]].sum()) for x in range(8)]
+        assert max(sums) - min(sums) <= int(kl.max())
+    with pytest.raises(RuntimeError):
+        ops._check(ops.lib().nvf_decode_token_order(kl.ctypes.data, -1, order.ctypes.data), "decode_token_order")

@@ -482,3 +482,42 @@ def test_paged_attention_host_cu_seqlens(gpu, dt, lens, prefix):
     H.assert_bitexact(H.to_host(got), H.to_host(ref), "host cu_seqlens vs device-only metadata")
     with pytest.raises(RuntimeError):  # the last entry must be the token count
         ops.paged_attention(q, kc, vc, qs, ql, tab, bs, hd ** -0.5, cu_seqlens=cu[:-1])
+
+
+@pytest.mark.parametrize("dt", [H.F16, H.BF16, H.F32], ids=["f16", "bf16", "f32"])
+@pytest.mark.parametrize("n,ctx_max,order_kind", [(256, 4096, "schedule"),   # config 1's ragged decode batch
+                                                  (13, 2048, "schedule"),    # not a multiple of 8
+                                                  (200, 1024, "random"),     # any permutation
+                                                  (3, 20000, "schedule")])   # a small batch: the split path
+def test_paged_attention_token_order(gpu, dt, n, ctx_max, order_kind):
+    """nvf_paged_attention_order_ws (the caller's token order for the decode kernel's
+    workgroups) gives the bit-identical output of nvf_paged_attention_ws, for the
+    nvf_decode_token_order schedule and for any permutation; key_len 0 included."""
+    g = torch.Generator(device=gpu)
+    g.manual_seed(n + ctx_max + dt)
+    tdt = H.torch_dtype(dt)
+    qh, kvh, hd, bs = 28, 4, 128, 256
+    r = np.random.default_rng(n * 7 + dt)
+    ctx = r.integers(1, ctx_max + 1, n).astype(np.int32)
+    nbs = [-(-int(c) // bs) for c in ctx]
+    rows = sum(nbs) * bs
+    kc = torch.randn(rows, kvh, hd, device=gpu, generator=g).to(tdt)
+    vc = torch.randn(rows, kvh, hd, device=gpu, generator=g).to(tdt)
+    tab = np.full((n, max(nbs)), -1, np.int32)
+    perm = r.permutation(sum(nbs)).astype(np.int32)
+    o = 0
+    for s_, nb in enumerate(nbs):
+        tab[s_, :nb] = perm[o:o + nb]
+        o += nb
+    kl = ctx.copy()
+    kl[n // 2] = 0  # a query with no keys: a zero row
+    q = torch.randn(n, qh, hd, device=gpu, generator=g).to(tdt)
+    args = (q, kc, vc, torch.arange(n, dtype=torch.int32, device=gpu), torch.from_numpy(kl).to(gpu),
+            torch.from_numpy(tab).to(gpu), bs, hd ** -0.5)
+    order = ops.decode_token_order(kl) if order_kind == "schedule" else r.permutation(n).astype(np.int32)
+    case(f"paged_attention token order n={n} ctx_max={ctx_max} {order_kind} dt={dt}")
+    ref = ops.paged_attention(*args, max_query_len=1)
+    got = ops.paged_attention(*args, max_query_len=1, token_order=torch.from_numpy(order).to(gpu))
+    torch.cuda.synchronize()
+    H.assert_bitexact(H.to_host(got), H.to_host(ref), "token order vs none")
+    assert not got[n // 2].float().abs().sum().item()
