@@ -433,8 +433,8 @@ int nvf_paged_attention_seqs_ws(const void* q, void* out, const void* k_cache, c
  * nvf_paged_attention_ws's; only the time depends on it.  For a decode batch with
  * ragged contexts, nvf_decode_token_order gives one that balances the GPU's 8 XCDs
  * (workgroup id mod 8 is its XCD); the engine holds the key counts on the host
- * (src/model_runner.cpp:122) and uploads the order with them.  16-bit caches; the
- * fp32 decode kernel and prefill tiles ignore it. */
+ * (src/model_runner.cpp:122) and uploads the order with them.  The prefill tiles
+ * ignore it. */
 int nvf_paged_attention_order_ws(const void* q, void* out, const void* k_cache, const void* v_cache,
                                  const int32_t* query_seq, const int32_t* query_key_len, const int32_t* block_tables,
                                  const int32_t* token_order, int64_t tokens, int q_heads, int kv_heads, int head_dim,

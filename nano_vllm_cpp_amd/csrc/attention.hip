@@ -841,11 +841,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
     const float* __restrict__ q, float* __restrict__ out, const float* __restrict__ kc, const float* __restrict__ vc,
     const int32_t* __restrict__ qseq, const int32_t* __restrict__ qlen, const int32_t* __restrict__ tables,
     int64_t tokens, int q_heads, int kv_heads, int bs, int max_blocks, float scale_log2, int64_t q_stride,
-    int split_keys, float* __restrict__ part) {
+    int split_keys, float* __restrict__ part, const int32_t* __restrict__ order) {
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   __shared__ float merge[4][kDecMergeFloats];
-  const int64_t t = blockIdx.x;
+  const int64_t t = !SKIP && order ? (int64_t)order[blockIdx.x] : (int64_t)blockIdx.x;  // as fa_decode_kernel
   // workgroup-uniform: the whole workgroup leaves (fa_prefill_f32_kernel's tile)
   if (SKIP && fa_tile_uniform(qseq, tokens, t / kFaBq)) return;
   // as fa_decode_kernel: the tiles' second launch walks the kv heads per token
@@ -1270,9 +1270,6 @@ int attention_dispatch(const void* q, void* out, const void* kc, const void* vc,
     const dim3 grid((unsigned)tokens, tiles ? 1u : (unsigned)kv_heads, nz);
     const int kk = split ? skeys : 0;
     float* pp = split ? part : nullptr;
-#define NVF_DEC_LAUNCH(KERN, LDS)                                                                              \
-  KERN<<<grid, 256, LDS, st>>>(qt, ot, kt, vt, qseq, qlen, tables, tokens, q_heads, kv_heads, bs, max_blocks, sl, \
-                               q_stride, kk, pp)
 #define NVF_DEC_LAUNCH_ORD(KERN, LDS, ORD)                                                                     \
   KERN<<<grid, 256, LDS, st>>>(qt, ot, kt, vt, qseq, qlen, tables, tokens, q_heads, kv_heads, bs, max_blocks, sl, \
                                q_stride, kk, pp, ORD)
@@ -1290,12 +1287,11 @@ int attention_dispatch(const void* q, void* out, const void* kc, const void* vc,
       else if (tiles) NVF_DEC_LAUNCH_ORD((fa_decode_kernel<T, false, true>), kFdLds, nullptr);
       else NVF_DEC_LAUNCH_ORD((fa_decode_kernel<T, false, false>), kFdLds, order);
     } else {
-      if (split && tiles) NVF_DEC_LAUNCH((fa_decode_f32_kernel<true, true>), 0);
-      else if (split) NVF_DEC_LAUNCH((fa_decode_f32_kernel<true, false>), 0);
-      else if (tiles) NVF_DEC_LAUNCH((fa_decode_f32_kernel<false, true>), 0);
-      else NVF_DEC_LAUNCH((fa_decode_f32_kernel<false, false>), 0);
+      if (split && tiles) NVF_DEC_LAUNCH_ORD((fa_decode_f32_kernel<true, true>), 0, nullptr);
+      else if (split) NVF_DEC_LAUNCH_ORD((fa_decode_f32_kernel<true, false>), 0, order);
+      else if (tiles) NVF_DEC_LAUNCH_ORD((fa_decode_f32_kernel<false, true>), 0, nullptr);
+      else NVF_DEC_LAUNCH_ORD((fa_decode_f32_kernel<false, false>), 0, order);
     }
-#undef NVF_DEC_LAUNCH
 #undef NVF_DEC_LAUNCH_ORD
     int rc = launch_status("paged_attention(decode)");
     if (rc != NVF_OK || !split) return rc;
