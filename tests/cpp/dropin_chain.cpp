@@ -1,7 +1,9 @@
 // C++ caller of the drop-in entry points, in the order Qwen3Model::forward_logits
 // calls them (src/model.cpp:756-844), on one Qwen3-0.6B-like layer: two 32-token
 // prefill sequences over a paged KV cache, every projection a Q8_0 GEMM, then the
-// final norm and the tied lm_head on the last token.
+// final norm and the tied lm_head on the last token.  Beside it, on the same
+// activations: Qwen2.5's qkv bias and the mixture-of-experts branch (router, routing,
+// shared expert with its gate, routed experts).
 // It includes only include/nvf_ops.h (the C ABI) and hip_runtime, exactly as
 // model.cpp would after the switch, and checks each stage against the C oracle
 // (test infrastructure), each stage fed the GPU's own input to that stage.
@@ -112,6 +114,17 @@ static void oracle_gemm(const std::vector<float>& x, const uint8_t* w8, const ui
   ideal.assign((size_t)(m * n), 0.0);
   bound.assign((size_t)(m * n), 0.0);
   orc_matmul_q8(x.data(), ORC_F32, w8, ws, m, n, k, ideal.data(), bound.data(), nullptr, nullptr);
+}
+
+// The oracle's product with fp32 / fp16 / bf16 weights on the GPU's own input: ideal
+// values and bounds, the bound scaled by `factor` (3 for bf16 weights: the prefill
+// kernels sum exact bf16 piece products, three terms per product)
+static void oracle_matmul_w(const std::vector<float>& x, const void* w, int w_format, int64_t m, int64_t n, int64_t k,
+                            double factor, std::vector<double>& ideal, std::vector<double>& bound) {
+  ideal.assign((size_t)(m * n), 0.0);
+  bound.assign((size_t)(m * n), 0.0);
+  orc_matmul_w(x.data(), ORC_F32, w, w_format, ORC_QK_LAYOUT_GGML, m, n, k, ideal.data(), bound.data());
+  for (auto& b : bound) b *= factor;
 }
 
 int main() {
@@ -250,6 +263,99 @@ int main() {
   sync();
   oracle_gemm(mx, wdn.w8.data(), wdn.ws.data(), T, H, I, ideal, bound);
   expect_within("down projection", hidden.host(), ideal, bound);
+
+  // Qwen2.5's qkv bias (:768-772; this layer is Qwen3-like and takes QK-norm instead), on a
+  // copy of the projected q: bit-exact (one fp32 add)
+  {
+    std::vector<float> bias(q_size);
+    for (auto& b : bias) b = g01(rng) - 1.f;
+    Dev<float> qb(q), d_bias(bias);
+    hip_add_bias_inplace(qb.d, d_bias.d, T, q_size);
+    sync();
+    std::vector<float> r_qb = q;
+    orc_add_bias(r_qb.data(), bias.data(), T, q_size, q_size, ORC_F32);
+    expect("qkv bias (bit-exact)", qb.host(), r_qb, true);
+  }
+
+  // a mixture-of-experts FFN in the dense MLP's place (:789-826, Qwen2-MoE-like), on the same
+  // post-attention norm output: router (fp32 weights), top-K routing, the shared expert
+  // (bf16) with its sigmoid gate, then the routed bf16 experts added on top
+  {
+    const int E = 16, K = 4, Ie = 256, SI = 512;
+    std::normal_distribution<float> w05(0.f, 0.05f);
+    auto bf16_weights = [&](size_t count) {
+      std::vector<uint16_t> w(count);
+      for (auto& e : w) e = orc_f32_to_bf16(w05(rng));
+      return w;
+    };
+    std::vector<float> router((size_t)E * H);
+    for (auto& e : router) e = w05(rng);
+    const std::vector<uint16_t> sh_gu = bf16_weights((size_t)2 * SI * H), sh_dn = bf16_weights((size_t)H * SI),
+                                sh_gate = bf16_weights(H), ex_gu = bf16_weights((size_t)E * 2 * Ie * H),
+                                ex_dn = bf16_weights((size_t)E * H * Ie);
+    std::vector<int32_t> slot_of(E);
+    for (int e = 0; e < E; ++e) slot_of[e] = (e * 7) % E;  // experts placed in permuted slots (moe_place)
+    Dev<float> d_router(router), route((size_t)T * E), d_sc((size_t)T * K), sgate((size_t)T * 2 * SI),
+        smlp((size_t)T * SI), moe((size_t)T * H), shs((size_t)T);
+    Dev<uint16_t> d_shgu(sh_gu), d_shdn(sh_dn), d_shg(sh_gate), d_exgu(ex_gu), d_exdn(ex_dn);
+    Dev<int32_t> d_slot(slot_of), d_idx((size_t)T * K);
+    const std::vector<float> nx2 = norm.host();
+
+    hip_matmul(norm.d, d_router.d, T, E, H, route.d);  // :797
+    sync();
+    oracle_matmul_w(nx2, router.data(), NVF_W_F32, T, E, H, 1.0, ideal, bound);
+    expect_within("MoE router logits (fp32 weights)", route.host(), ideal, bound);
+    const std::vector<float> lg = route.host();
+    hip_moe_route(route.d, T, E, K, true, d_idx.d, d_sc.d);  // :798
+    sync();
+    std::vector<int32_t> r_idx((size_t)T * K);
+    std::vector<float> r_sc((size_t)T * K);
+    orc_moe_route(lg.data(), T, E, K, 1, r_idx.data(), r_sc.data());
+    const bool ids_ok = d_idx.host() == r_idx;
+    std::printf("%-40s %s\n", "MoE routing: expert ids (exact)", ids_ok ? "ok" : "FAIL");
+    if (!ids_ok) ++failures;
+    expect("MoE routing: scores (bit-exact)", d_sc.host(), r_sc, true);
+
+    hip_matmul_u16(norm.d, d_shgu.d, T, 2 * SI, H, sgate.d, true);  // shared expert, :802-804
+    sync();
+    oracle_matmul_w(nx2, sh_gu.data(), NVF_W_BF16, T, 2 * SI, H, 3.0, ideal, bound);
+    expect_within("shared expert gate_up (bf16 weights)", sgate.host(), ideal, bound);
+    const std::vector<float> sg = sgate.host();
+    std::vector<float> r_sm((size_t)T * SI);
+    hip_silu_and_mul(sgate.d, smlp.d, T, SI);
+    sync();
+    orc_silu_and_mul(sg.data(), r_sm.data(), T, SI, ORC_F32);
+    expect("shared expert silu_and_mul", smlp.host(), r_sm, false);
+    const std::vector<float> sm = smlp.host();
+    hip_matmul_u16(smlp.d, d_shdn.d, T, H, SI, moe.d, true);
+    sync();
+    oracle_matmul_w(sm, sh_dn.data(), NVF_W_BF16, T, H, SI, 3.0, ideal, bound);
+    expect_within("shared expert down", moe.host(), ideal, bound);
+    hip_matmul_u16(norm.d, d_shg.d, T, 1, H, shs.d, true);  // its gate, :805-809
+    sync();
+    oracle_matmul_w(nx2, sh_gate.data(), NVF_W_BF16, T, 1, H, 3.0, ideal, bound);
+    expect_within("shared expert gate logit", shs.host(), ideal, bound);
+    const std::vector<float> mo = moe.host(), sv = shs.host();
+    std::vector<float> r_gated(mo.size());
+    for (int t = 0; t < T; ++t)
+      for (int c = 0; c < H; ++c)
+        r_gated[(size_t)t * H + c] = mo[(size_t)t * H + c] * (1.0f / (1.0f + std::exp(-sv[t])));
+    hip_scale_rows_sigmoid(moe.d, shs.d, T, H);
+    sync();
+    expect("shared expert sigmoid gate", moe.host(), r_gated, false);
+
+    const std::vector<float> base = moe.host();  // the routed experts add to it (:817-825)
+    const std::vector<double> base_d(base.begin(), base.end());
+    const std::vector<int32_t> hidx = d_idx.host();
+    const std::vector<float> hsc = d_sc.host();
+    hip_moe_ffn(norm.d, d_idx.d, d_sc.d, d_exgu.d, d_exdn.d, d_slot.d, T, H, Ie, K, true, moe.d);
+    sync();
+    std::vector<double> m_ideal((size_t)T * H), m_err((size_t)T * H);
+    orc_moe_ffn(nx2.data(), ORC_F32, hidx.data(), hsc.data(), ex_gu.data(), ex_dn.data(), 1, slot_of.data(), T, H, Ie,
+                K, E, base_d.data(), m_ideal.data(), m_err.data());
+    for (auto& e : m_err) e *= 6.0;  // bf16 experts on the split products (as the MoE GPU tests)
+    expect_within("routed experts (hip_moe_ffn, added)", moe.host(), m_ideal, m_err);
+  }
 
   // final norm (:835) and the tied lm_head on the last token (:840-844; m = 1, the decode GEMV)
   norm_add("final norm", final_ln, d_final_ln);
