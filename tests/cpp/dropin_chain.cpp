@@ -1,9 +1,9 @@
 // C++ caller of the drop-in entry points, in the order Qwen3Model::forward_logits
 // calls them (src/model.cpp:756-844), on one Qwen3-0.6B-like layer: two 32-token
 // prefill sequences over a paged KV cache, every projection a Q8_0 GEMM, then the
-// final norm and the tied lm_head on the last token.  Beside it, on the same
-// activations: Qwen2.5's qkv bias and the mixture-of-experts branch (router, routing,
-// shared expert with its gate, routed experts).
+// final norm, the last rows gathered and the tied lm_head on them (Q8_0, Q4_K and bf16
+// tables and heads).  Beside it, on the same activations: Qwen2.5's qkv bias and the
+// mixture-of-experts branch (router, routing, shared expert with its gate, routed experts).
 // It includes only include/nvf_ops.h (the C ABI) and hip_runtime, exactly as
 // model.cpp would after the switch, and checks each stage against the C oracle
 // (test infrastructure), each stage fed the GPU's own input to that stage.
@@ -163,7 +163,7 @@ int main() {
   Dev<int32_t> d_qseq(qseq), d_qlen(qlen), d_slots(slots), d_tables(tables);
   Dev<float> hidden((size_t)T * H), residual((size_t)T * H), norm((size_t)T * H), d_q((size_t)T * q_size),
       d_k((size_t)T * kv_size), d_v((size_t)T * kv_size), attn((size_t)T * q_size), gate((size_t)T * 2 * I),
-      mlp((size_t)T * I), logits((size_t)V);
+      mlp((size_t)T * I);
   Dev<float> k_cache((size_t)num_blocks * bs * kv_size), v_cache((size_t)num_blocks * bs * kv_size);
   auto sync = [] { CHECK_HIP(hipDeviceSynchronize()); };
   std::vector<double> ideal, bound;
@@ -357,13 +357,63 @@ int main() {
     expect_within("routed experts (hip_moe_ffn, added)", moe.host(), m_ideal, m_err);
   }
 
-  // final norm (:835) and the tied lm_head on the last token (:840-844; m = 1, the decode GEMV)
+  // final norm (:835), each sequence's last row gathered (:837-839), the tied lm_head on
+  // them (:841-843; m = 2, the decode GEMV)
   norm_add("final norm", final_ln, d_final_ln);
-  std::vector<float> last(norm.host().begin() + (size_t)(T - 1) * H, norm.host().begin() + (size_t)T * H);
-  hip_matmul_q8(norm.d + (size_t)(T - 1) * H, d_emb8.d, d_embs.d, 1, V, H, logits.d);
+  const std::vector<int32_t> last_idx = {per - 1, T - 1};  // ctx.last_indices
+  Dev<int32_t> d_last(last_idx);
+  Dev<float> selected((size_t)2 * H), logits2((size_t)2 * V);
+  const std::vector<float> nf = norm.host();
+  hip_gather_rows(norm.d, d_last.d, T, H, 2, selected.d);
   sync();
-  oracle_gemm(last, emb.w8.data(), emb.ws.data(), 1, V, H, ideal, bound);
-  expect_within("lm_head logits (m = 1)", logits.host(), ideal, bound);
+  std::vector<float> r_sel((size_t)2 * H);
+  orc_gather_rows(nf.data(), last_idx.data(), H, 2, r_sel.data(), ORC_F32);
+  expect("last rows gathered (bit-exact)", selected.host(), r_sel, true);
+  hip_matmul_q8(selected.d, d_emb8.d, d_embs.d, 2, V, H, logits2.d);
+  sync();
+  oracle_gemm(r_sel, emb.w8.data(), emb.ws.data(), 2, V, H, ideal, bound);
+  expect_within("lm_head logits (Q8_0, m = 2)", logits2.host(), ideal, bound);
+
+  // the other table and head formats embedding_dispatch / matmul_dispatch take
+  // (:665-696): a Q4_K table (GGUF nibble order, the drop-in's default) and a bf16 one,
+  // each gathered for the prompt and used as the tied head on the gathered rows
+  {
+    std::vector<uint8_t> q4k((size_t)V * H / 256 * 144);
+    std::uniform_int_distribution<int> byte(0, 255);
+    std::uniform_real_distribution<float> us(1e-3f, 1e-2f);
+    for (size_t b = 0; b < q4k.size() / 144; ++b) {
+      uint8_t* blk = q4k.data() + b * 144;
+      const uint16_t d = orc_f32_to_fp16(us(rng)), dmin = orc_f32_to_fp16(us(rng));
+      std::memcpy(blk, &d, 2);
+      std::memcpy(blk + 2, &dmin, 2);
+      for (int i = 4; i < 144; ++i) blk[i] = (uint8_t)byte(rng);  // any 12 bytes are valid 6-bit scales / mins
+    }
+    std::normal_distribution<float> n01(0.f, 1.f);
+    std::vector<uint16_t> tbf((size_t)V * H);
+    for (auto& e : tbf) e = orc_f32_to_bf16(n01(rng) * 0.05f);
+    Dev<uint8_t> d_q4k(q4k);
+    Dev<uint16_t> d_tbf(tbf);
+    Dev<float> e_out((size_t)T * H);
+    std::vector<float> r_e((size_t)T * H);
+
+    hip_embedding_qk(d_ids.d, d_q4k.d, T, H, e_out.d, NVF_Q4_K);  // :691
+    sync();
+    orc_embedding_qk(ids.data(), q4k.data(), T, H, NVF_Q4_K, ORC_QK_LAYOUT_GGML, r_e.data(), ORC_F32);
+    expect("Q4_K embedding (bit-exact)", e_out.host(), r_e, true);
+    hip_embedding_u16(d_ids.d, d_tbf.d, T, H, e_out.d, true);  // :695
+    sync();
+    orc_embedding_u16(ids.data(), tbf.data(), T, H, 1, r_e.data(), ORC_F32);
+    expect("bf16 embedding (bit-exact)", e_out.host(), r_e, true);
+
+    hip_matmul_qk(selected.d, d_q4k.d, 2, V, H, logits2.d, NVF_Q4_K);  // :667
+    sync();
+    oracle_matmul_w(r_sel, q4k.data(), NVF_W_Q4_K, 2, V, H, 1.0, ideal, bound);
+    expect_within("lm_head logits (Q4_K, m = 2)", logits2.host(), ideal, bound);
+    hip_matmul_u16(selected.d, d_tbf.d, 2, V, H, logits2.d, true);  // :671
+    sync();
+    oracle_matmul_w(r_sel, tbf.data(), NVF_W_BF16, 2, V, H, 3.0, ideal, bound);
+    expect_within("lm_head logits (bf16, m = 2)", logits2.host(), ideal, bound);
+  }
 
   // a decode step over a longer cache (model_runner.cpp:100-128: one query per
   // sequence, key_len = its context) in 64-key blocks: few (token, kv head) pairs,
