@@ -133,6 +133,7 @@ def assert_within(got, ideal, err, out_dt, what, w_bf16=False):
     (37, 512, 320, 4, 16, 20),       # 32-row tiles, ragged 2I / H against the 128-column tile
     (600, 256, 96, 8, 32, 32),       # 4800 pairs: 128-row tiles
     (9, 200, 72, 3, 6, 6),           # H and I not multiples of 16
+    (300, 256, 128, 8, 16, 16),      # 2400 pairs, 150 per slot
     (5, 100, 44, 2, 4, 4),           # H not a multiple of 8: the tile kernel, element-wise staging
     (300, 64, 32, 1, 1, 1),          # every pair in one slot: one long run of tiles
 ])
