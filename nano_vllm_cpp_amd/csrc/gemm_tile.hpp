@@ -625,10 +625,12 @@ __global__ __launch_bounds__(kGvWaves * 64) void gemv_mfma_kernel(const TX* __re
 // prefetch (the last step reloads itself), which keeps the memory-counter waits
 // exact.  A row or column outside the problem reads row 0 (valid memory; its results
 // are never stored).  The policy names the workgroup's G C CPS columns per item.
-template <typename TX, typename Src, int MR, int C, int S, typename P>
+// LPCX (optional): lanes per column instead (64: a load instruction covers 1 KB of one
+// weight row).
+template <typename TX, typename Src, int MR, int C, int S, typename P, int LPCX = 0>
 __global__ __launch_bounds__(kGvWaves * 64) void gemv_fma_kernel(const TX* __restrict__ x, Src w, P prob,
                                                                  int64_t k) {
-  constexpr int R = RunOf<Src>::value, LPC = R == 8 ? 16 : 8, CPS = 64 / LPC, KS = LPC * R;
+  constexpr int R = RunOf<Src>::value, LPC = LPCX ? LPCX : (R == 8 ? 16 : 8), CPS = 64 / LPC, KS = LPC * R;
   constexpr int G = kGvWaves / S;               // column groups per workgroup (S waves split K in each)
   __shared__ float part[kGvWaves][MR][C][CPS];  // [wave][row][set][column]
   const int lane = threadIdx.x & 63, j = lane % CPS, b = lane / CPS;
