@@ -216,6 +216,8 @@ int launch_gemv_fma(const TX* x, const Src& src, TO* out, int64_t m, int64_t n, 
     gemv_fma_kernel<TX, Src, MR, 2, 1, PlainGemvProb<TO>, 64><<<grid(2 * kGvWaves), blk, 0, st>>>(x, src, prob, k);
   else if (n >= (int64_t)CPS * CMAX * kGvWaves * 1024)
     gemv_fma_kernel<TX, Src, MR, CMAX, 1><<<grid(CPS * CMAX * kGvWaves), blk, 0, st>>>(x, src, prob, k);
+  else if (RunOf<Src>::value == 8 && n >= (int64_t)CPS * CMAX * 1024)
+    gemv_fma_kernel<TX, Src, MR, 2, 4, PlainGemvProb<TO>, 64><<<grid(2), blk, 0, st>>>(x, src, prob, k);
   else if (n >= (int64_t)CPS * CMAX * 1024)
     gemv_fma_kernel<TX, Src, MR, CMAX, 4><<<grid(CPS * CMAX), blk, 0, st>>>(x, src, prob, k);
   else

@@ -102,10 +102,11 @@ def test_matmul_ragged_k(gpu, w_format, m, n, k):
 @pytest.mark.parametrize("w_format", FORMATS, ids=FMT_IDS)
 @pytest.mark.parametrize("m,n,k", [(1, 1000, 3584), (2, 37, 264), (4, 4100, 256), (5, 513, 1032), (8, 9000, 512),
                                    (12, 20000, 256), (16, 64, 8), (3, 256, 40), (2, 66000, 256),
-                                   (1, 65601, 512)])
+                                   (1, 65601, 512), (1, 20000, 1000), (2, 40001, 3584)])
 def test_matmul_decode_rows(gpu, w_format, m, n, k):
     """m <= 16 with k % 8 == 0: the weight-streaming decode product (every row-group
-    size, column-quad count, a k that is not a multiple of the 128-element step)."""
+    size, column-quad count, a k that is not a multiple of the 128- or 512-element step;
+    wide and mid-width dense outputs take 64 lanes per weight row)."""
     if w_format >= 12 and (n * k) % 256:
         pytest.skip("K-quant weights cover whole 256-element superblocks")
     r = H.rng(700 + w_format + m + k)
