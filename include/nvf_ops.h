@@ -430,7 +430,9 @@ int nvf_paged_attention_seqs_ws(const void* q, void* out, const void* k_cache, c
 /* nvf_paged_attention_ws with the caller's schedule for the decode kernel (no
  * counterpart in the reference): token_order (device int32 [tokens], a permutation of
  * 0 .. tokens-1) names the token each decode workgroup computes.  Results equal
- * nvf_paged_attention_ws's; only the time depends on it.  For a decode batch with
+ * nvf_paged_attention_ws's; only the time depends on it.  (Not a permutation: an entry
+ * outside 0 .. tokens-1 computes nothing and reads or writes no memory for it; the
+ * output of a token the order does not name is unspecified.)  For a decode batch with
  * ragged contexts, nvf_decode_token_order gives one that balances the GPU's 8 XCDs
  * (workgroup id mod 8 is its XCD); the engine holds the key counts on the host
  * (src/model_runner.cpp:122) and uploads the order with them.  The prefill tiles

@@ -678,6 +678,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
   // order (not with SKIP): the caller's permutation of the tokens over the workgroups
   // (which token each computes; the results do not depend on it)
   const int64_t t = !SKIP && order ? (int64_t)order[blockIdx.x] : (int64_t)blockIdx.x;
+  if (t < 0 || t >= tokens) return;  // an order entry outside the batch: nothing to compute (uniform)
   // workgroup-uniform: the whole workgroup leaves (fa_prefill_kernel's tile)
   if (SKIP && fa_tile_uniform(qseq, tokens, t / kFaBq)) return;
   // The tiles' second launch (SKIP) has one workgroup per token, so that its many
@@ -846,6 +847,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
   const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   __shared__ float merge[4][kDecMergeFloats];
   const int64_t t = !SKIP && order ? (int64_t)order[blockIdx.x] : (int64_t)blockIdx.x;  // as fa_decode_kernel
+  if (t < 0 || t >= tokens) return;
   // workgroup-uniform: the whole workgroup leaves (fa_prefill_f32_kernel's tile)
   if (SKIP && fa_tile_uniform(qseq, tokens, t / kFaBq)) return;
   // as fa_decode_kernel: the tiles' second launch walks the kv heads per token

@@ -521,3 +521,34 @@ def test_paged_attention_token_order(gpu, dt, n, ctx_max, order_kind):
     torch.cuda.synchronize()
     H.assert_bitexact(H.to_host(got), H.to_host(ref), "token order vs none")
     assert not got[n // 2].float().abs().sum().item()
+
+
+def test_paged_attention_token_order_out_of_range_entry(gpu):
+    """An order entry outside 0 .. tokens-1 computes nothing and touches no memory (the
+    call completes); every token the order names equals the unordered result (this batch
+    takes the split path, whose merge also covers the unnamed token: its row is
+    unspecified)."""
+    g = torch.Generator(device=gpu)
+    g.manual_seed(5)
+    n, qh, kvh, hd, bs = 24, 28, 4, 128, 256
+    ctx = np.random.default_rng(5).integers(1, 1500, n).astype(np.int32)
+    nbs = [-(-int(c) // bs) for c in ctx]
+    tab = np.full((n, max(nbs)), -1, np.int32)
+    o = 0
+    for s_, nb in enumerate(nbs):
+        tab[s_, :nb] = np.arange(o, o + nb)
+        o += nb
+    kc = torch.randn(o * bs, kvh, hd, device=gpu, generator=g).half()
+    vc = torch.randn(o * bs, kvh, hd, device=gpu, generator=g).half()
+    q = torch.randn(n, qh, hd, device=gpu, generator=g).half()
+    args = (q, kc, vc, torch.arange(n, dtype=torch.int32, device=gpu), torch.from_numpy(ctx).to(gpu),
+            torch.from_numpy(tab).to(gpu), bs, hd ** -0.5)
+    order = np.arange(n, dtype=np.int32)
+    order[3] = 10 ** 6  # token 3 is not named
+    case("paged_attention token order with an out-of-range entry")
+    ref = ops.paged_attention(*args, max_query_len=1)
+    out = torch.full_like(q, 7.0)
+    ops.paged_attention(*args, max_query_len=1, out=out, token_order=torch.from_numpy(order).to(gpu))
+    torch.cuda.synchronize()
+    keep = [i for i in range(n) if i != 3]
+    H.assert_bitexact(H.to_host(out[keep]), H.to_host(ref[keep]), "the named tokens")
