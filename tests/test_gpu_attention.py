@@ -485,19 +485,20 @@ def test_paged_attention_host_cu_seqlens(gpu, dt, lens, prefix):
 
 
 @pytest.mark.parametrize("dt", [H.F16, H.BF16, H.F32], ids=["f16", "bf16", "f32"])
-@pytest.mark.parametrize("n,ctx_max,order_kind", [(256, 4096, "schedule"),   # config 1's ragged decode batch
-                                                  (13, 2048, "schedule"),    # not a multiple of 8
-                                                  (200, 1024, "random"),     # any permutation
-                                                  (3, 20000, "schedule")])   # a small batch: the split path
-def test_paged_attention_token_order(gpu, dt, n, ctx_max, order_kind):
+@pytest.mark.parametrize("n,ctx_max,order_kind,heads", [(256, 4096, "schedule", (28, 4)),  # config 1's batch
+                                                        (256, 4096, "schedule", (32, 8)),  # Qwen3-8B's heads
+                                                        (13, 2048, "schedule", (28, 4)),   # not a multiple of 8
+                                                        (200, 1024, "random", (28, 4)),    # any permutation
+                                                        (3, 20000, "schedule", (28, 4))])  # the split path
+def test_paged_attention_token_order(gpu, dt, n, ctx_max, order_kind, heads):
     """nvf_paged_attention_order_ws (the caller's token order for the decode kernel's
     workgroups) gives the bit-identical output of nvf_paged_attention_ws, for the
     nvf_decode_token_order schedule and for any permutation; key_len 0 included."""
     g = torch.Generator(device=gpu)
     g.manual_seed(n + ctx_max + dt)
     tdt = H.torch_dtype(dt)
-    qh, kvh, hd, bs = 28, 4, 128, 256
-    r = np.random.default_rng(n * 7 + dt)
+    (qh, kvh), hd, bs = heads, 128, 256
+    r = np.random.default_rng(n * 7 + dt + qh)
     ctx = r.integers(1, ctx_max + 1, n).astype(np.int32)
     nbs = [-(-int(c) // bs) for c in ctx]
     rows = sum(nbs) * bs
@@ -515,7 +516,7 @@ def test_paged_attention_token_order(gpu, dt, n, ctx_max, order_kind):
     args = (q, kc, vc, torch.arange(n, dtype=torch.int32, device=gpu), torch.from_numpy(kl).to(gpu),
             torch.from_numpy(tab).to(gpu), bs, hd ** -0.5)
     order = ops.decode_token_order(kl) if order_kind == "schedule" else r.permutation(n).astype(np.int32)
-    case(f"paged_attention token order n={n} ctx_max={ctx_max} {order_kind} dt={dt}")
+    case(f"paged_attention token order n={n} ctx_max={ctx_max} {order_kind} heads={heads} dt={dt}")
     ref = ops.paged_attention(*args, max_query_len=1)
     got = ops.paged_attention(*args, max_query_len=1, token_order=torch.from_numpy(order).to(gpu))
     torch.cuda.synchronize()
