@@ -854,9 +854,9 @@ def test_moe_route_is_sorted_softmax(o, norm):
 @pytest.mark.parametrize("logits,k,want", [
     ([1.0, 1.0, 1.0, 1.0], 4, [0, 1, 2, 3]),
     ([1.0, 3.0, 1.0, 1.0], 3, [1, 0, 2]),
-    # the first round swaps expert 0 to position 2, behind expert 1: ties follow positions, not ids
+    # the first selection pass swaps expert 0 to position 2, behind expert 1: ties follow positions, not ids
     ([1.0, 1.0, 3.0, 1.0], 3, [2, 1, 0]),
-    # round 2 swaps expert 0 (value 2) forward past experts 1 and 2, which end up reversed
+    # the second selection pass swaps expert 0 (value 2) forward past experts 1 and 2, which end up reversed
     ([2.0, 1.0, 1.0, 5.0, 1.0], 4, [3, 0, 2, 1]),
 ])
 def test_moe_route_tie_order_is_the_selection_sorts(o, logits, k, want):
