@@ -54,10 +54,16 @@ def parse() -> argparse.Namespace:
     p.add_argument("--warmup", type=int, default=5)
     p.add_argument("--config", type=int, default=2, help="BASELINE config index (1-4)")
     p.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU-baseline budget (0 = skip)")
+    p.add_argument("--configs", default="0,1,3,4",
+                   help="after the headline config, the chain (gather, norm, RoPE, SwiGLU) of each of these BASELINE "
+                        "configs, GPU and CPU, under \"configs\" ('' = none; the headline config is skipped here)")
     p.add_argument("--emb", default="", choices=["", "q8_0", "q8_0_blocks", "q4_k", "q5_k", "q6_k", "f16"],
                    help="embedding table format (default: the config's)")
     p.add_argument("--write-traffic", default="", metavar="DIR",
                    help="no benchmark: build profiles/traffic.json from rocprofv3 FETCH_SIZE / WRITE_SIZE runs under DIR")
+    p.add_argument("--source-commit", default="",
+                   help="with --write-traffic: the commit the profiled tree was built from (run where .git is; "
+                        "the stamp then also records whether the kernel sources differ from it)")
     p.add_argument("--only", default="",
                    help="comma list of ops (default emb,rms,rope,silu,copy,gemm,gemv,split,attn,attn_decode,attn_f32,"
                         "attn_decode_ordered,attn_decode_f32,attn_decode_small,layer,layer_decode,layer_b1,layer_b1_graph); "
@@ -95,7 +101,8 @@ def op_bytes(cfg, e: int, emb_fmt: str) -> dict[str, int]:
 def main() -> int:
     args = parse()
     if args.write_traffic:
-        print(json.dumps(write_traffic(args.write_traffic, args.config)[f"c{args.config}"], indent=1))
+        print(json.dumps(write_traffic(args.write_traffic, args.config, args.source_commit)[f"c{args.config}"],
+                         indent=1))
         return 0
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print(json.dumps({"error": "this build measures one GPU only; run with --gpus 1",
@@ -721,8 +728,113 @@ def main() -> int:
                                                     "attn_decode_small") if k in res_ops} or None,
         "cpu_baseline": cpu,
     }
+    extra = [int(c_) for c_ in args.configs.split(",") if c_.strip() != "" and int(c_) != args.config]
+    if extra and chain_ops == ["emb", "rms", "rope", "silu"] and not args.emb:
+        # free the headline's sets first: config 4's SwiGLU alone holds ~7 GB
+        del emb_sets, rms_sets, rope_sets, silu_sets
+        torch.cuda.empty_cache()
+        line["configs"] = {f"c{c_}": bench_chain(c_, args, torch, ops, H, stream, cyc_per_us, group, n_launch)
+                           for c_ in extra}
     print(json.dumps(line), flush=True)
     return 0
+
+
+def bench_chain(ci: int, args, torch, ops, H, stream, cyc_per_us: float, group: int, n_launch: int) -> dict:
+    """The four chain ops of BASELINE config ci at its full size, inputs resident in HBM and
+    rotated over >= 1 GiB per op like the headline's, timed the same way (timed_launches);
+    then the chain back to back for `steps` steps, and the C oracle on this host
+    (cpu_baseline: config 0's whole 64-token chain, the others a bounded sample)."""
+    cfg = H.CONFIGS[ci]
+    dev = torch.device("cuda:0")
+    tdt = H.torch_dtype(cfg.dtype)
+    e = 2 if cfg.dtype != H.F32 else 4
+    T, Hd, I, V = cfg.tokens, cfg.hidden, cfg.inter, cfg.vocab
+    qs, ks = cfg.q_heads * cfg.head_dim, cfg.kv_heads * cfg.head_dim
+    g = torch.Generator(device=dev).manual_seed(cfg.seed)
+    nbytes = op_bytes(cfg, e, cfg.emb)
+
+    def nsets(b: int) -> int:
+        return max(2, -(-POOL_BYTES // b))
+
+    def randn(shape, mean=0.0, std=1.0):
+        return (torch.randn(shape, generator=g, device=dev) * std + mean).to(tdt)
+
+    if cfg.emb == "q8_0":
+        w8 = torch.randint(-127, 128, (V * Hd,), generator=g, device=dev, dtype=torch.int8)
+        ws = torch.empty(V * Hd // 32, device=dev).uniform_(1e-3, 1e-2, generator=g).half().view(torch.int16)
+    else:
+        blocks = torch.from_numpy(H.gen_q4_k(np.random.default_rng(cfg.seed), V * Hd // 256)).to(dev)
+    sets = {
+        "emb": [(torch.randint(0, V, (T,), generator=g, device=dev), torch.empty(T, Hd, dtype=tdt, device=dev))
+                for _ in range(nsets(nbytes["emb"]))],
+        "rms": [(randn((T, Hd)), randn((T, Hd)), torch.empty(T, Hd, dtype=tdt, device=dev))
+                for _ in range(nsets(nbytes["rms"]))],
+        "rope": [(randn((T, qs)), randn((T, ks))) for _ in range(nsets(nbytes["rope"]))],
+        "silu": [(randn((T, 2 * I)), torch.empty(T, I, dtype=tdt, device=dev)) for _ in range(nsets(nbytes["silu"]))],
+    }
+    gamma = randn((Hd,), 1.0, 0.1)
+    pos = torch.from_numpy(cfg.positions()).to(dev)
+    inv = ops.rope_inv_freq(cfg.theta, cfg.head_dim, dev)
+    qw = randn((cfg.head_dim,), 1.0, 0.1) if cfg.qk_norm else None
+    kw = randn((cfg.head_dim,), 1.0, 0.1) if cfg.qk_norm else None
+
+    def run_emb(i):
+        ids, out = sets["emb"][i % len(sets["emb"])]
+        if cfg.emb == "q8_0":
+            ops.embedding_q8_0(ids, w8, ws, Hd, V, out=out)
+        else:
+            ops.embedding_qk(ids, blocks, Hd, ops.Q4_K, V, out=out)
+
+    def run_rms(i):
+        x, r, out = sets["rms"][i % len(sets["rms"])]
+        ops.rms_norm_add(x, r, gamma, cfg.eps, out=out)
+
+    def run_rope(i):
+        q, k = sets["rope"][i % len(sets["rope"])]
+        ops.qk_norm_rope(q, k, pos, qw, kw, inv, cfg.q_heads, cfg.kv_heads, cfg.head_dim, cfg.eps)
+
+    def run_silu(i):
+        gu, out = sets["silu"][i % len(sets["silu"])]
+        ops.silu_and_mul(gu, out=out)
+
+    fns = {"emb": run_emb, "rms": run_rms, "rope": run_rope, "silu": run_silu}
+    for i in range(args.warmup):
+        for f in fns.values():
+            f(i)
+    torch.cuda.synchronize()
+    res = {}
+    for n, f in fns.items():
+        per, ahead = timed_launches(torch, stream, f, args.warmup, n_launch, cyc_per_us, group)
+        t_us, p50 = float(per.mean()), float(np.percentile(per, 50))
+        gbs = nbytes[n] / (t_us * 1e-6) / 1e9
+        res[n] = {"us": round(t_us, 2), "p50_us": round(p50, 2), "bytes": nbytes[n], "GB_s": round(gbs, 1),
+                  "frac_of_peak": round(gbs / HBM_PEAK_GBS, 4),
+                  "frac_of_peak_p50": round(nbytes[n] / (p50 * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                  "tokens_per_s": round(T / (t_us * 1e-6), 1), **({} if ahead else {"host_bound": True})}
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    a.record(stream)
+    for i in range(args.steps):
+        for f in fns.values():
+            f(args.warmup + i)
+    b.record(stream)
+    torch.cuda.synchronize()
+    step_us = a.elapsed_time(b) * 1e3 / args.steps
+    del sets
+    if cfg.emb == "q8_0":
+        del w8, ws
+    else:
+        del blocks
+    torch.cuda.empty_cache()
+    out = {"workload": f"BASELINE config {ci}: {cfg.name}; {cfg.emb} embedding gather + residual-add RMSNorm + "
+                       f"{'QK-norm + ' if cfg.qk_norm else ''}NeoX RoPE q/k + SwiGLU",
+           "tokens": T, "dtype": {H.F16: "f16", H.BF16: "bf16", H.F32: "f32"}[cfg.dtype],
+           "step_us": round(step_us, 2), "tokens_per_s": round(T / (step_us * 1e-6), 1), "ops": res}
+    if args.cpu_seconds > 0:
+        # config 0 is the CPU reference's own case: its whole chain (all 64 tokens, the full table)
+        out["cpu_baseline"] = cpu_baseline(cfg, 3.0 if ci == 0 else 2.0, H, full=ci == 0, all_cores=ci == 0)
+        out["gpu_over_cpu"] = round(out["tokens_per_s"] / out["cpu_baseline"]["value"], 1)
+    return out
 
 
 def sleep_rate(torch, stream) -> float:
@@ -804,7 +916,7 @@ def traffic_from_profiles(op: str, config: int):
     return e.get("hbm_bytes_per_launch")
 
 
-def write_traffic(prof_dir: str, config: int) -> dict:
+def write_traffic(prof_dir: str, config: int, source_commit: str = "") -> dict:
     """Builds profiles/traffic.json from two rocprofv3 passes over the chain and the copy,
     <prof_dir>/FETCH_SIZE/*counter_collection.csv and <prof_dir>/WRITE_SIZE/..., made by
       rocprofv3 --pmc FETCH_SIZE -f csv -d <prof_dir>/FETCH_SIZE -o FETCH_SIZE -- \
@@ -855,6 +967,15 @@ def write_traffic(prof_dir: str, config: int) -> dict:
                             "fetch_factor": round(ff, 4), "write_factor": round(wf, 4)},
            "_note": "hbm_bytes_per_launch = FETCH_SIZE[KiB]*1024*fetch_factor + WRITE_SIZE[KiB]*1024*write_factor"}
     entry = {}
+    if source_commit:  # the profiled tree's commit, given; its kernel sources compared with the working tree's
+        try:
+            head = subprocess.run(["git", "-C", str(ROOT), "rev-parse", source_commit], capture_output=True,
+                                  text=True, check=True).stdout.strip()
+            dirty = subprocess.run(["git", "-C", str(ROOT), "diff", "--quiet", head, "--", "nano_vllm_cpp_amd/csrc"],
+                                   capture_output=True).returncode != 0
+        except (OSError, subprocess.CalledProcessError):
+            head, dirty = source_commit, None
+        out["_source"].update({"commit": head, "kernel_sources_modified": dirty})
     for op, d in sorted(cfg_ops.items()):
         hbm = d["FETCH_SIZE"] * 1024 * ff + d["WRITE_SIZE"] * 1024 * wf
         entry[op] = {"kernel": d["kernel"], "grid": d["grid"], "fetch_kib_raw": round(d["FETCH_SIZE"], 1),
@@ -871,19 +992,24 @@ def write_traffic(prof_dir: str, config: int) -> dict:
     return whole
 
 
-def cpu_chain_sample(cfg, H, seed: int):
+def cpu_chain_sample(cfg, H, seed: int, full: bool = False, table=None):
     """Buffers for one S-token sample of the chain and a function running it once
-    through the C oracle; returns (run, S).  run() returns the four ops' seconds."""
+    through the C oracle; returns (run, S, table).  run() returns the four ops' seconds.
+    full: the config's own tokens (all of them) over its whole table.  table: the
+    embedding table of an earlier call to share (threads read it, none writes it)."""
     o = H.oracle()
     r = np.random.default_rng(seed)
-    S = 256  # sample tokens per chain call
+    S = cfg.tokens if full else min(256, cfg.tokens)  # sample tokens per chain call
     Hd, I, dt = cfg.hidden, cfg.inter, cfg.dtype
-    Vs = 4096  # gathered rows come from a 4096-row slice of the table: same per-row work
+    # gathered rows come from a 4096-row slice of the table (same per-row work), or the whole table
+    Vs = cfg.vocab if full else 4096
     ids = r.integers(0, Vs, S).astype(np.int64)
+    if table is None:
+        table = H.gen_q8_0(r, Vs, Hd) if cfg.emb == "q8_0" else H.gen_q4_k(r, Vs * Hd // 256)
     if cfg.emb == "q8_0":
-        w8, ws = H.gen_q8_0(r, Vs, Hd)
+        w8, ws = table
     else:
-        blocks = H.gen_q4_k(r, Vs * Hd // 256)
+        blocks = table
     emb = np.empty((S, Hd), H.NP_STORAGE[dt])
     x, res = H.gen_act(r, (S, Hd), dt), H.gen_act(r, (S, Hd), dt)
     w = H.gen_act(r, (Hd,), dt, 1.0, 0.1)
@@ -914,14 +1040,15 @@ def cpu_chain_sample(cfg, H, seed: int):
         t4 = time.perf_counter()
         return t1 - t, t2 - t1, t3 - t2, t4 - t3
 
-    return run, S
+    return run, S, table
 
 
-def cpu_baseline(cfg, budget_s: float, H) -> dict:
-    """The C oracle (scalar, 1 thread, -O2) on a bounded sample of the same chain,
-    then the same oracle on every host core the box gives this job (threads, each
-    on its own sample; ctypes releases the GIL), reported under "all_cores"."""
-    run, S = cpu_chain_sample(cfg, H, cfg.seed)
+def cpu_baseline(cfg, budget_s: float, H, full: bool = False, all_cores: bool = True) -> dict:
+    """The C oracle (scalar, 1 thread, -O2) on a bounded sample of the same chain (full:
+    the config's whole chain, repeated), then the same oracle on every host core the box
+    gives this job (threads, each on its own sample; ctypes releases the GIL), reported
+    under "all_cores"."""
+    run, S, table = cpu_chain_sample(cfg, H, cfg.seed, full)
     per = {"emb": 0.0, "rms": 0.0, "rope": 0.0, "silu": 0.0}
     calls = 0
     t_start = time.perf_counter()
@@ -934,7 +1061,7 @@ def cpu_baseline(cfg, budget_s: float, H) -> dict:
             break
     total = sum(per.values())
     e = 2 if cfg.dtype != H.F32 else 4
-    scale = {k_: v * S / cfg.tokens for k_, v in op_bytes(cfg, e, "q8_0").items()}  # bytes of one S-token call
+    scale = {k_: v * S / cfg.tokens for k_, v in op_bytes(cfg, e, cfg.emb).items()}  # bytes of one S-token call
     cpu_model = ""
     try:
         for ln in Path("/proc/cpuinfo").read_text().splitlines():
@@ -944,15 +1071,18 @@ def cpu_baseline(cfg, budget_s: float, H) -> dict:
     except OSError:
         pass
     result = {"value": round(calls * S / total, 1), "unit": "tokens/s", "cores": 1, "kind": "port",
-              "sample": f"{calls} x the {S}-token chain of the same config (table rows from a 4096-row slice), "
+              "sample": f"{calls} x the {S}-token chain of the same config ("
+                        f"{'the whole table' if full else 'table rows from a 4096-row slice'}), "
                         f"{total:.1f} s of single-thread C oracle (-O2) on {cpu_model or 'this host'}, "
                         f"nproc={os.cpu_count()}",
               "ops_GB_s": {k_: round(scale[k_] * calls / per[k_] / 1e9, 3) for k_ in per}}
 
+    if not all_cores:
+        return result
     # all cores: at most 16 threads (the box's CPU share per GPU), half the budget
     import concurrent.futures as cf
     n = max(1, min(16, os.cpu_count() or 1))
-    runs = [cpu_chain_sample(cfg, H, cfg.seed + 1 + i)[0] for i in range(n)]
+    runs = [cpu_chain_sample(cfg, H, cfg.seed + 1 + i, full, table)[0] for i in range(n)]
     all_budget = budget_s / 2
 
     def worker(fn):

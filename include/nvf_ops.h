@@ -356,7 +356,8 @@ int nvf_matmul_q8_0_ws(const int8_t* xq, const float* row_scale, const uint8_t* 
  * fuses what the reference does in one call, hip_matmul_q8's quantizer and GEMV
  * (src/hip_ops.hip:205-217, :317-364), and for act 1 also hip_silu_and_mul before it
  * (src/model.cpp:830).  x: 16-byte aligned rows, x_stride elements apart (>= k, or
- * 2k for act 1).  m > 16 or rows too long for the workgroup's LDS: NVF_ERR_INVALID. */
+ * 2k for act 1); out must not overlap x.  m > 16, overlapping out, or rows too long
+ * for the workgroup's LDS: NVF_ERR_INVALID. */
 int nvf_matmul_q8_0_act(const void* x, int64_t x_stride, int act, const uint8_t* w8, const uint16_t* ws, int64_t m,
                         int64_t n, int64_t k, void* out, int dtype, void* stream);
 
@@ -364,7 +365,7 @@ int nvf_matmul_q8_0_act(const void* x, int64_t x_stride, int act, const uint8_t*
  * out [m, n] = the Q8_0 product of the rows nvf_rms_norm_q8 would produce, bit for bit.
  * With residual [m, k]: v = round(x + residual), written to residual_out [m, k]
  * (which must not overlap x or residual: every workgroup reads them); without
- * (both NULL): v = x.  Then round(v / rms(v) * norm_weight) quantized per row.  Each
+ * (both NULL): v = x.  out must not overlap x, residual or residual_out.  Then round(v / rms(v) * norm_weight) quantized per row.  Each
  * workgroup repeats the norm in its prologue, its sum of squares in nvf_rms_norm_q8's
  * own order.  This fuses the reference's hip_rms_norm_add then the next Q8_0 matmul
  * (src/model.cpp:762 then :764, :787 then :829; src/hip_ops.hip:395-417, :639-680) into

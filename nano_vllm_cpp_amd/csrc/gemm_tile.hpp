@@ -66,8 +66,11 @@ struct SplitTile<Table<8, _Float16>> {
 __device__ __forceinline__ void split3(const float* v, bf16x8* p) {
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
-    const __bf16 a = (__bf16)v[i];
-    const float r1 = v[i] - (float)a;  // exact: the bits below a's 8
+    // the first piece truncates (the top 16 bits of v): exact, and it cannot round up
+    // past the largest bf16 to infinity the way round-to-nearest would near FLT_MAX;
+    // an infinite v keeps its infinity in the first piece alone
+    const __bf16 a = __builtin_bit_cast(__bf16, (uint16_t)(__builtin_bit_cast(uint32_t, v[i]) >> 16));
+    const float r1 = __builtin_isinf(v[i]) ? 0.0f : v[i] - (float)a;  // exact: the bits below a's 8
     const __bf16 b = (__bf16)r1;
     const float r2 = r1 - (float)b;    // exact, and at most 8 significant bits
     p[0][i] = a;

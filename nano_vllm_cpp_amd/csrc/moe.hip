@@ -74,10 +74,12 @@ __global__ __launch_bounds__(64) void moe_route_kernel(const float* __restrict__
   }
   __syncthreads();
   for (int i = 0; i < K; ++i) {
-    // largest value at positions >= i; a tie goes to the smaller position
-    double bv = -1.0;
-    int bp = E;
-    for (int j = i + lane; j < E; j += 64)
+    // largest value at positions >= i; a tie goes to the smaller position.  Every
+    // lane starts from position i itself, as the reference's scan does (best = i),
+    // so a NaN there keeps i (nothing compares greater) and NaNs elsewhere never win.
+    double bv = pr[i];
+    int bp = i;
+    for (int j = i + 1 + lane; j < E; j += 64)
       if (pr[j] > bv) {
         bv = pr[j];
         bp = j;

@@ -27,6 +27,12 @@ inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s);
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// True if the byte ranges [a, a + an) and [b, b + bn) share a byte.
+inline bool bytes_overlap(const void* a, int64_t an, const void* b, int64_t bn) {
+  const uintptr_t pa = reinterpret_cast<uintptr_t>(a), pb = reinterpret_cast<uintptr_t>(b);
+  return an > 0 && bn > 0 && pa < pb + (uintptr_t)bn && pb < pa + (uintptr_t)an;
+}
+
 inline int dtype_bytes(int dt) { return dt == NVF_F32 ? 4 : 2; }
 inline bool dtype_ok(int dt) { return dt == NVF_F32 || dt == NVF_F16 || dt == NVF_BF16; }
 

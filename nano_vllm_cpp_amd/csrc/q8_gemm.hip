@@ -116,6 +116,10 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, in
 }
 
 constexpr uint32_t kOob = 0x80000000u;  // a buffer offset past every tile: reads zero
+// Cache policy of a load read exactly once (the decode GEMV's weights and scales):
+// non-temporal.  An LDS DMA stream of 136 MB runs 10% faster with it (22.1 against
+// 24.6 us, the rate of plain register loads).
+constexpr int kNt = 2;
 
 // LDS rows hold kGemmKC bytes (kGemmCPR chunks of 16 B) with chunk c of row r at
 // position c ^ ((r / kGemmSwz) % kGemmCPR): rows kGemmKC bytes apart fall on
@@ -410,8 +414,16 @@ constexpr int gemv_cols() { return W / S * 16; }  // columns per workgroup of W 
 // workgroup 0 stores to xres_out; then round(v * inv_rms * xg)).  Bit-identity
 // needs the norm's own sum of squares: a first pass sums each row's squares in the
 // norm kernel's layout (rms_waves_per_row) and order, one (row, sub-wave) per wave.
-template <typename TO, int W, int S, bool XL, int XF = 0>
-__global__ __launch_bounds__(W * 64) void q8_gemv_kernel(const int8_t* __restrict__ xq,
+//
+// H8 (m <= 8): both blocks of a pair in one MFMA.  Lane (j, q) takes activation row
+// j % 8, and only for j < 8 with q < 2 (the pair's first block) or j >= 8 with q >= 2
+// (its second); other lanes hold zero (their loads fall outside the buffer).  D rows
+// 0-7 are then the first block's dots of rows 0-7 and D rows 8-15 the second block's,
+// so lane (j, q) applies one scale, block 2 p + q / 2 of column j, and the two halves
+// of a row meet in the final sum.  Half the MFMAs and half the applies of the
+// two-MFMA form, none of them on padding rows.
+template <typename TO, int W, int S, bool XL, int XF = 0, bool H8 = false>
+__global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(2))) void q8_gemv_kernel(const int8_t* __restrict__ xq,
                                                          const float* __restrict__ rscale,
                                                          const int8_t* __restrict__ w8,
                                                          const uint16_t* __restrict__ ws,
@@ -467,20 +479,34 @@ __global__ __launch_bounds__(W * 64) void q8_gemv_kernel(const int8_t* __restric
 #pragma unroll
     for (int i = 0; i < 4; ++i)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (__attribute__((address_space(3))) void*)(dst + i * 1024), 16,
-                                               dma_off[i], soff, 0, 0);
+                                               dma_off[i], soff, 0, kNt);
   };
-  const uint32_t x_off = (uint32_t)(j * k) + 16u * q;  // activation row j
-  i32x4 xv[4];
-  auto load_x = [&](int st) {  // register path: 16 bytes of each of the stage's 4 pairs (zero past k)
+  const int xr = H8 ? (j & 7) : j;                          // the activation row lane (j, q) holds
+  const bool x_half_ok = !H8 || ((j < 8) == (q < 2));       // H8: this lane's block of the pair
+  const uint32_t x_off = (uint32_t)(xr * k) + 16u * q;
+  // Register path (no XL): the activations of stage st + 1 are loaded at the top of
+  // stage st into the other half of a register double buffer.  These loads are
+  // invisible to the compiler (inline asm): its own vmcnt waits, which do not count
+  // the LDS DMA, would otherwise drain the next weight stage wherever the registers
+  // are read.  The stage-end vmcnt wait covers them; x_ready() then ties the
+  // registers to that wait, so no read of them can be scheduled before it.
+  const i32x4 x_desc = {(int)(uint32_t)reinterpret_cast<uintptr_t>(xq),
+                        (int)(uint32_t)((reinterpret_cast<uintptr_t>(xq) >> 32) & 0xffffu), (int)(m * k), 0x00020000};
+  i32x4 xa[4], xb[4];
+  auto load_x = [&](i32x4 (&xv)[4], int st) {  // 16 bytes of each of stage st's 4 pairs (zero past k)
     const int64_t pst = p_begin + 4 * st;
 #pragma unroll
     for (int pp = 0; pp < 4; ++pp) {
       const int64_t p = pst + pp;
-      const bool ok = p < p_end && 64 * p + 16 * q < k;
-      xv[pp] = __builtin_bit_cast(
-          i32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, ok ? x_off + (uint32_t)(64 * p) : kOob, 0, 0));
+      const bool ok = x_half_ok && p < p_end && 64 * p + 16 * q < k;
+      const uint32_t off = ok ? x_off + (uint32_t)(64 * p) : kOob;
+      asm volatile("buffer_load_dwordx4 %0, %1, %2, 0 offen" : "=v"(xv[pp]) : "v"(off), "s"(x_desc) : "memory");
     }
   };
+  auto x_ready = [&](i32x4 (&xv)[4]) {
+    asm volatile("" : "+v"(xv[0]), "+v"(xv[1]), "+v"(xv[2]), "+v"(xv[3]));
+  };
+  (void)rx;
   // Issue order: weight stage 0, the scales (and XL rows), stage 0's register
   // activations, weight stage 1.  vmcnt counts in issue order, so vmcnt(4) waits
   // for everything but stage 1, which stays in flight; the prologue's HBM
@@ -498,7 +524,7 @@ __global__ __launch_bounds__(W * 64) void q8_gemv_kernel(const int8_t* __restric
       const int64_t i = i0 + threadIdx.x;
       if (i < cnt / 2)
         __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            rs, (__attribute__((address_space(3))) void*)(dst + i0 + 64 * wave), 4, (uint32_t)(4 * i), 0, 0, 0);
+            rs, (__attribute__((address_space(3))) void*)(dst + i0 + 64 * wave), 4, (uint32_t)(4 * i), 0, 0, kNt);
     }
     if constexpr (XL && XF == 0) {  // m rows of k bytes (k % 32 == 0), 1 KB transfers spread over the waves
       const int per_row = (int)((k + 1023) / 1024);
@@ -555,13 +581,16 @@ __global__ __launch_bounds__(W * 64) void q8_gemv_kernel(const int8_t* __restric
       }
     }
     if (active) {
-      if constexpr (!XL) load_x(0);
+      if constexpr (!XL) load_x(xa, 0);
       if (nst > 1) issue(1);
     }
     if (active && nst > 1)
       __builtin_amdgcn_s_waitcnt(0x0F74);  // vmcnt(4): all but weight stage 1
     else
       __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+    if constexpr (!XL) {
+      if (active) x_ready(xa);
+    }
     if ((cnt & 1) && threadIdx.x == 0)
       sc_lds[cnt - 1] = (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(rs, (uint32_t)(2 * (cnt - 1)), 0, 0);
     if constexpr (XF != 0) {
@@ -759,16 +788,24 @@ __global__ __launch_bounds__(W * 64) void q8_gemv_kernel(const int8_t* __restric
 
   if (active) {
     const uint16_t* sc_col = sc_lds + ((int64_t)grp * 16 + j) * nblk;
-    // XL: lane (j, q) reads row j (rows past m hold zero: the address is clamped
-    // to row 0 and the value selected away)
-    const bool x_row_ok = j < m;
-    const uint8_t* x_src = x_lds + (x_row_ok ? j : 0) * xrow + 16 * q;
+    // XL: lane (j, q) reads row xr (rows past m, and under H8 the other block's
+    // lanes, hold zero: the address is clamped to row 0 and the value selected away)
+    const bool x_row_ok = xr < m && x_half_ok;
+    const uint8_t* x_src = x_lds + (x_row_ok ? xr : 0) * xrow + 16 * q;
+    // xa holds the stage's register activations, xb receives the next stage's and
+    // is copied into xa after the stage-end wait (a copy before it would read
+    // registers the loads have not yet written)
     for (int st = 0; st < nst; ++st) {
+      i32x4 (&xc)[4] = xa;
+      i32x4 (&xn)[4] = xb;
       // weight stage st (and its register activations) are here; stage st + 1 is in flight
+      if constexpr (!XL) {
+        if (st + 1 < nst) load_x(xn, st + 1);
+      }
       const int64_t pst = p_begin + 4 * st;
       const int npp = p_end - pst < 4 ? (int)(p_end - pst) : 4;
       const uint8_t* src = wbuf + (st & 1) * kGvWaveBuf + j * kGvKC;
-      // one block pair: operands from LDS (or registers), then its two MFMAs and applies
+      // one block pair: operands from LDS (or registers), then its MFMA(s) and applies
       struct Operands {
         i32x4 wv, x;
         float s_lo, s_hi;
@@ -779,26 +816,39 @@ __global__ __launch_bounds__(W * 64) void q8_gemv_kernel(const int8_t* __restric
         Operands o;
         o.wv = *reinterpret_cast<const i32x4*>(src + 16 * ((4 * pp + q) ^ j));
         if constexpr (XL) {
-          const i32x4 xr = *reinterpret_cast<const i32x4*>(x_src + 64 * p);
-          o.x = x_row_ok && 64 * p + 16 * q < k ? xr : i32x4{0, 0, 0, 0};
+          const i32x4 xl = *reinterpret_cast<const i32x4*>(x_src + 64 * p);
+          o.x = x_row_ok && 64 * p + 16 * q < k ? xl : i32x4{0, 0, 0, 0};
         } else {
-          o.x = xv[pp];
+          o.x = xc[pp];
         }
-        o.s_lo = fp16_bits_to_float(sc_col[b]);
-        const float s1 = fp16_bits_to_float(sc_col[b + 1 < nblk ? b + 1 : b]);  // read unconditionally
-        o.s_hi = b + 1 < nblk ? s1 : 0.0f;
+        if constexpr (H8) {  // this lane's block: b or b + 1 (scale 0 past the last block)
+          const int64_t bq = b + (q >> 1);
+          const float sv = fp16_bits_to_float(sc_col[bq < nblk ? bq : b]);  // read unconditionally
+          o.s_lo = bq < nblk ? sv : 0.0f;
+          o.s_hi = 0.0f;
+        } else {
+          o.s_lo = fp16_bits_to_float(sc_col[b]);
+          const float s1 = fp16_bits_to_float(sc_col[b + 1 < nblk ? b + 1 : b]);  // read unconditionally
+          o.s_hi = b + 1 < nblk ? s1 : 0.0f;
+        }
         return o;
       };
       auto apply = [&](const Operands& o) {
         const i32x4 z = {0, 0, 0, 0};
-        const i32x4 x_lo = q < 2 ? o.x : z;  // first block of the pair
-        const i32x4 x_hi = q < 2 ? z : o.x;  // second block
-        const i32x4 d_lo = __builtin_amdgcn_mfma_i32_16x16x64_i8(x_lo, o.wv, z, 0, 0, 0);
-        const i32x4 d_hi = __builtin_amdgcn_mfma_i32_16x16x64_i8(x_hi, o.wv, z, 0, 0, 0);
+        if constexpr (H8) {
+          const i32x4 d = __builtin_amdgcn_mfma_i32_16x16x64_i8(o.x, o.wv, z, 0, 0, 0);
 #pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          acc[v] = fmaf(o.s_lo, (float)d_lo[v], acc[v]);
-          acc[v] = fmaf(o.s_hi, (float)d_hi[v], acc[v]);
+          for (int v = 0; v < 4; ++v) acc[v] = fmaf(o.s_lo, (float)d[v], acc[v]);
+        } else {
+          const i32x4 x_lo = q < 2 ? o.x : z;  // first block of the pair
+          const i32x4 x_hi = q < 2 ? z : o.x;  // second block
+          const i32x4 d_lo = __builtin_amdgcn_mfma_i32_16x16x64_i8(x_lo, o.wv, z, 0, 0, 0);
+          const i32x4 d_hi = __builtin_amdgcn_mfma_i32_16x16x64_i8(x_hi, o.wv, z, 0, 0, 0);
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            acc[v] = fmaf(o.s_lo, (float)d_lo[v], acc[v]);
+            acc[v] = fmaf(o.s_hi, (float)d_hi[v], acc[v]);
+          }
         }
       };
       if (npp == 4) {  // uniform: a full stage reads all its operands first, then computes
@@ -808,18 +858,24 @@ __global__ __launch_bounds__(W * 64) void q8_gemv_kernel(const int8_t* __restric
 #pragma unroll
         for (int pp = 0; pp < 4; ++pp) apply(o[pp]);
       } else {
-        for (int pp = 0; pp < npp; ++pp) apply(fetch(pp));
+#pragma unroll
+        for (int pp = 0; pp < 4; ++pp)
+          if (pp < npp) apply(fetch(pp));
       }
       if (st + 1 < nst) {
-        // the next stage's register activations, then weight stage st + 2 into the
-        // buffer just read (its values are in registers); vmcnt(4) leaves that one
-        // in flight
-        if constexpr (!XL) load_x(st + 1);
+        // weight stage st + 2 into the buffer just read (its values are in
+        // registers); vmcnt(4) leaves that one in flight and completes stage st + 1
+        // and its register activations
         if (st + 2 < nst) {
           issue(st + 2);
           __builtin_amdgcn_s_waitcnt(0x0F74);
         } else {
           __builtin_amdgcn_s_waitcnt(0x0F70);
+        }
+        if constexpr (!XL) {
+          x_ready(xn);
+#pragma unroll
+          for (int pp = 0; pp < 4; ++pp) xc[pp] = xn[pp];
         }
       }
     }
@@ -840,7 +896,10 @@ __global__ __launch_bounds__(W * 64) void q8_gemv_kernel(const int8_t* __restric
     if (r < m && col < n) {
       float sum = 0.0f;
 #pragma unroll
-      for (int sp = 0; sp < S; ++sp) sum += part(g * S + sp, r, cj);
+      for (int sp = 0; sp < S; ++sp) {
+        sum += part(g * S + sp, r, cj);
+        if constexpr (H8) sum += part(g * S + sp, r + 8, cj);  // the pairs' second blocks
+      }
       const float sc = XF != 0 ? xf_scale[r] : rscale[r];
       const float inv = sc > 0.0f ? 1.0f / sc : 0.0f;  // the reference's adq (:358)
       gemm_store_out(out + r * n + col, sum * inv);
@@ -872,18 +931,31 @@ bool try_gemv(const int8_t* xq, const float* rscale, const int8_t* w8, const uin
                   std::min(resident(lds_x), need) >= std::min(resident(lds_r), need);
   static std::once_flag attr_once;
   std::call_once(attr_once, [] {
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&q8_gemv_kernel<TO, W, S, false>),
-                              hipFuncAttributeMaxDynamicSharedMemorySize, kDma + kGemvScaleLds);
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&q8_gemv_kernel<TO, W, S, true>),
-                              hipFuncAttributeMaxDynamicSharedMemorySize,
-                              (int)std::min<int64_t>(kLdsPerCu, kDma + kGemvScaleLds + kGemvXLdsMax));
+    const int lds_reg = kDma + kGemvScaleLds;
+    const int lds_xl = (int)std::min<int64_t>(kLdsPerCu, kDma + kGemvScaleLds + kGemvXLdsMax);
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&q8_gemv_kernel<TO, W, S, false, 0, false>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, lds_reg);
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&q8_gemv_kernel<TO, W, S, false, 0, true>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, lds_reg);
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&q8_gemv_kernel<TO, W, S, true, 0, false>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, lds_xl);
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&q8_gemv_kernel<TO, W, S, true, 0, true>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, lds_xl);
   });
-  if (xl)
-    q8_gemv_kernel<TO, W, S, true><<<dim3((unsigned)wgs), dim3(W * 64), (size_t)lds_x, stream>>>(
-        xq, rscale, w8, ws, out, m, n, k, (int)sc_bytes);
+  const dim3 grid((unsigned)wgs), block(W * 64);
+  const bool h8 = m <= 8;
+  if (xl && h8)
+    q8_gemv_kernel<TO, W, S, true, 0, true><<<grid, block, (size_t)lds_x, stream>>>(xq, rscale, w8, ws, out, m, n,
+                                                                                   k, (int)sc_bytes);
+  else if (xl)
+    q8_gemv_kernel<TO, W, S, true, 0, false><<<grid, block, (size_t)lds_x, stream>>>(xq, rscale, w8, ws, out, m, n,
+                                                                                    k, (int)sc_bytes);
+  else if (h8)
+    q8_gemv_kernel<TO, W, S, false, 0, true><<<grid, block, (size_t)lds_r, stream>>>(xq, rscale, w8, ws, out, m, n,
+                                                                                    k, (int)sc_bytes);
   else
-    q8_gemv_kernel<TO, W, S, false><<<dim3((unsigned)wgs), dim3(W * 64), (size_t)lds_r, stream>>>(
-        xq, rscale, w8, ws, out, m, n, k, (int)sc_bytes);
+    q8_gemv_kernel<TO, W, S, false, 0, false><<<grid, block, (size_t)lds_r, stream>>>(xq, rscale, w8, ws, out, m, n,
+                                                                                     k, (int)sc_bytes);
   return true;
 }
 
@@ -909,14 +981,21 @@ bool try_gemv_act(const TO* xf, int64_t xf_ld, const int8_t* w8, const uint16_t*
   if (sc_bytes > kGemvScaleLds || x_bytes > kGemvXLdsMax || kDma + sc_bytes + x_bytes > kLdsPerCu) return false;
   static std::once_flag attr_once;
   std::call_once(attr_once, [] {
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&q8_gemv_kernel<TO, W, S, true, XF>),
-                              hipFuncAttributeMaxDynamicSharedMemorySize,
-                              (int)std::min<int64_t>(kLdsPerCu, kDma + kGemvScaleLds + kGemvXLdsMax));
+    const int lds = (int)std::min<int64_t>(kLdsPerCu, kDma + kGemvScaleLds + kGemvXLdsMax);
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&q8_gemv_kernel<TO, W, S, true, XF, false>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&q8_gemv_kernel<TO, W, S, true, XF, true>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, lds);
   });
   const int64_t wgs = (n + kCols - 1) / kCols;
-  q8_gemv_kernel<TO, W, S, true, XF><<<dim3((unsigned)wgs), dim3(W * 64), (size_t)(kDma + sc_bytes + x_bytes),
-                                        stream>>>(nullptr, nullptr, w8, ws, out, m, n, k, (int)sc_bytes, xf, xf_ld,
-                                                  rn.res, rn.res_out, rn.g, rn.eps);
+  const dim3 grid((unsigned)wgs), block(W * 64);
+  const size_t lds = (size_t)(kDma + sc_bytes + x_bytes);
+  if (m <= 8)
+    q8_gemv_kernel<TO, W, S, true, XF, true><<<grid, block, lds, stream>>>(
+        nullptr, nullptr, w8, ws, out, m, n, k, (int)sc_bytes, xf, xf_ld, rn.res, rn.res_out, rn.g, rn.eps);
+  else
+    q8_gemv_kernel<TO, W, S, true, XF, false><<<grid, block, lds, stream>>>(
+        nullptr, nullptr, w8, ws, out, m, n, k, (int)sc_bytes, xf, xf_ld, rn.res, rn.res_out, rn.g, rn.eps);
   return true;
 }
 
@@ -1147,6 +1226,8 @@ int nvf_matmul_q8_0_act(const void* x, int64_t x_stride, int act, const uint8_t*
   if (!aligned16(x) || !aligned16(w8) || (x_stride * dtype_bytes(dtype)) % 16 != 0)
     return fail(NVF_ERR_INVALID, "%s: x (and its rows) and w8 must be 16-byte aligned", who);
   if ((reinterpret_cast<uintptr_t>(ws) & 1u) != 0) return fail(NVF_ERR_INVALID, "%s: ws must be 2-byte aligned", who);
+  if (bytes_overlap(out, m * n * dtype_bytes(dtype), x, ((m - 1) * x_stride + (act ? 2 : 1) * k) * dtype_bytes(dtype)))
+    return fail(NVF_ERR_INVALID, "%s: out must not overlap x (every workgroup reads x while others write out)", who);
   const int8_t* w = reinterpret_cast<const int8_t*>(w8);
   int rc = NVF_OK;
   if (act == 0)
@@ -1183,15 +1264,15 @@ int nvf_matmul_q8_0_rms(const void* x, int64_t x_stride, const void* residual, v
     return fail(NVF_ERR_INVALID, "%s: x (and its rows), residual, residual_out, norm_weight and w8 must be 16-byte "
                 "aligned", who);
   if ((reinterpret_cast<uintptr_t>(ws) & 1u) != 0) return fail(NVF_ERR_INVALID, "%s: ws must be 2-byte aligned", who);
-  if (residual) {
-    // every workgroup reads x and residual while workgroup 0 writes residual_out
-    auto overlap = [](const void* a, int64_t an, const void* b, int64_t bn) {
-      const uintptr_t pa = reinterpret_cast<uintptr_t>(a), pb = reinterpret_cast<uintptr_t>(b);
-      return pa < pb + (uintptr_t)bn && pb < pa + (uintptr_t)an;
-    };
-    const int64_t rb = m * k * eb, xb = ((m - 1) * x_stride + k) * eb;
-    if (overlap(residual_out, rb, residual, rb) || overlap(residual_out, rb, x, xb))
+  {
+    // every workgroup reads x and residual in its prologue while workgroup 0 writes
+    // residual_out and every workgroup writes its columns of out
+    const int64_t rb = m * k * eb, xb = ((m - 1) * x_stride + k) * eb, ob = m * n * eb;
+    if (residual && (bytes_overlap(residual_out, rb, residual, rb) || bytes_overlap(residual_out, rb, x, xb)))
       return fail(NVF_ERR_INVALID, "%s: residual_out must not overlap residual or x", who);
+    if (bytes_overlap(out, ob, x, xb) || (residual && (bytes_overlap(out, ob, residual, rb) ||
+                                                       bytes_overlap(out, ob, residual_out, rb))))
+      return fail(NVF_ERR_INVALID, "%s: out must not overlap x, residual or residual_out", who);
   }
   const int8_t* w = reinterpret_cast<const int8_t*>(w8);
   int rc = NVF_OK;

@@ -86,6 +86,25 @@ def test_matmul_within_bound(gpu, w_format, x_dt, m, n, k):
         assert_within(H.to_host(got), ideal, err, out_dt, f"fmt {w_format} x {x_dt} out {out_dt}", w_format)
 
 
+@pytest.mark.parametrize("w_format", [H.F16, H.BF16], ids=["f16", "bf16"])
+def test_matmul_tile_near_flt_max(gpu, w_format):
+    """fp32 activations above the largest bf16 (~3.39e38) on the 16-bit matrix-core tile
+    path (m > 16): the exact three-piece split must not turn them into inf - inf = NaN."""
+    r = H.rng(4242 + w_format)
+    m, n, k = 64, 128, 256
+    x = H.gen_act(r, (m, k), H.F32)
+    x[::2, 7] = np.float32(3.4e38)    # above the largest bf16, below FLT_MAX
+    x[1::2, 9] = np.float32(-3.39e38)
+    w = H.to_storage((r.standard_normal((n, k)) * 1e-3).astype(np.float32), w_format)
+    ideal, err = oracle_matmul(x, H.F32, w, w_format, m, n, k)
+    assert np.isfinite(ideal).all()
+    case(f"nvf_matmul near FLT_MAX fmt={w_format} m={m} n={n} k={k}")
+    got = ops.matmul(H.to_dev(x, gpu), w_dev(w, w_format, gpu), n, w_format)
+    g = H.to_host(got)
+    assert np.isfinite(g).all(), "non-finite output for finite inputs"
+    assert_within(g, ideal, err, H.F32, f"near FLT_MAX fmt {w_format}", w_format)
+
+
 @pytest.mark.parametrize("w_format", FORMATS, ids=FMT_IDS)
 @pytest.mark.parametrize("m,n,k", [(3, 256, 100), (70, 128, 200), (33, 512, 4)])
 def test_matmul_ragged_k(gpu, w_format, m, n, k):

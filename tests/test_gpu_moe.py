@@ -90,6 +90,33 @@ def test_moe_route_vs_reference_kernel(gpu, ref):
         H.assert_bitexact(sc2.cpu().numpy(), sc.cpu().numpy(), "scores vs reference kernel")
 
 
+@pytest.mark.parametrize("e,k", [(60, 4), (128, 8), (16, 16)])
+def test_moe_route_nan_rows(gpu, ref, e, k):
+    """A row with one NaN logit and an all-NaN row: every probability is NaN, and the
+    reference's scan (best = i, strict >) keeps ids 0..K-1 in order; no id leaves [0, E)."""
+    lg = H.rng(e + k).standard_normal((4, e)).astype(np.float32)
+    lg[1, e // 2] = np.nan
+    lg[2, :] = np.nan
+    want_idx, want_sc = oracle_route(lg, k, True)
+    d_lg = torch.from_numpy(lg).to(gpu)
+    case(f"nvf_moe_route NaN rows E={e} K={k}")
+    idx, sc = ops.moe_route(d_lg, k, True)
+    got_idx, got_sc = idx.cpu().numpy(), sc.cpu().numpy()
+    assert ((got_idx >= 0) & (got_idx < e)).all(), "expert id out of range"
+    H.assert_bitexact(got_idx, want_idx, "expert ids (NaN rows) vs oracle")
+    np.testing.assert_array_equal(np.isnan(got_sc), np.isnan(want_sc))
+    np.testing.assert_array_equal(got_idx[1:3], np.tile(np.arange(k, dtype=np.int32), (2, 1)))
+    ok = ~np.isnan(want_sc)
+    H.assert_bitexact(got_sc[ok], want_sc[ok], "finite scores (NaN rows) vs oracle")
+    ridx = torch.empty((4, k), dtype=torch.int32, device=gpu)
+    rsc = torch.empty((4, k), dtype=torch.float32, device=gpu)
+    torch.cuda.synchronize()
+    case(f"reference moe_route NaN rows E={e} K={k}")
+    ref.ref_hip_moe_route(dptr(d_lg), 4, e, k, True, dptr(ridx), dptr(rsc))
+    torch.cuda.synchronize()
+    H.assert_bitexact(got_idx, ridx.cpu().numpy(), "expert ids (NaN rows) vs reference kernel")
+
+
 def moe_case(r, rows, hid, inter, k, n_exp, slots, w_bf16, x_dt=H.F32):
     x = H.gen_act(r, (rows, hid), x_dt)
     wdt = H.BF16 if w_bf16 else H.F16
