@@ -642,10 +642,18 @@ constexpr int kDecMergeFloats = kFaHd * 16 + 32;  // one wave's state in the mer
 // chunks w, w + 4, ...) and merge their softmax states through LDS at the end, so
 // the longest contexts, which set a decode batch's tail, take a quarter of the
 // time, without a second launch.
-constexpr int kFdVRow = 64 * 2 + 8;              // V^T row: 64 keys, padded
+// V^T row (one dim): 64 keys in 16 units of 8 bytes, unit w of row r at position
+// w ^ ((r / 8) % 16), rows 144 bytes apart: both the transpose's 8-byte writes and
+// the operand reads take the minimum 2 LDS passes (a 8-byte pad alone: 4 and 3)
+constexpr int kFdVRow = 64 * 2 + 16;
 constexpr int kFdWaveLds = kFaHd * kFdVRow;      // per wave
 constexpr int kFdLds = 4 * kFdWaveLds;
 
+
+// A raw buffer over `bytes` bytes at p (32-bit dwords; offsets past the end read zero).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t attn_rsrc(const void* p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
+}
 
 template <typename T>
 struct Mfma16x16;
@@ -677,14 +685,24 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
   const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   // order (not with SKIP): the caller's permutation of the tokens over the workgroups
   // (which token each computes; the results do not depend on it)
-  const int64_t t = !SKIP && order ? (int64_t)order[blockIdx.x] : (int64_t)blockIdx.x;
+  // Without SKIP, workgroup x is one (token, kv head): with an order, token index
+  // x / kv_heads and kv head x % kv_heads -- one token's kv heads are dispatched
+  // together, so a longest-first order reaches every (token, kv head) pair longest
+  // first (measured at 256 sequences of U[1, 4096] keys: 186 against 200 us with
+  // the kv heads outermost); without one, token x % tokens, kv head x / tokens (a
+  // token's kv heads spread over the grid: 210 against 223 us for random lengths).
+  const bool tok_major = !SKIP && order;
+  const int64_t ti = SKIP ? (int64_t)blockIdx.x
+                     : tok_major ? (int64_t)blockIdx.x / kv_heads
+                                 : (int64_t)blockIdx.x % tokens;
+  const int64_t t = tok_major ? (int64_t)order[ti] : ti;
   if (t < 0 || t >= tokens) return;  // an order entry outside the batch: nothing to compute (uniform)
   // workgroup-uniform: the whole workgroup leaves (fa_prefill_kernel's tile)
   if (SKIP && fa_tile_uniform(qseq, tokens, t / kFaBq)) return;
   // The tiles' second launch (SKIP) has one workgroup per token, so that its many
-  // exiting workgroups stay few, and walks the kv heads; otherwise blockIdx.y is
-  // the kv head (one trip, known at compile time).
-  const int kvh0 = SKIP ? 0 : (int)blockIdx.y;
+  // exiting workgroups stay few, and walks the kv heads; otherwise the workgroup's
+  // kv head (one trip).
+  const int kvh0 = SKIP ? 0 : tok_major ? (int)(blockIdx.x % kv_heads) : (int)(blockIdx.x / tokens);
   const int kvh1 = SKIP ? kv_heads : kvh0 + 1;
   for (int kvh = kvh0; kvh < kvh1; ++kvh) {
     const int G = q_heads / kv_heads;
@@ -715,39 +733,52 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
       c1 = min(c1, c0 + split_keys / 64);
     }
     // chunk loads: K as MFMA A operands (key 16 kt + col, dims 32 s + 8 g);
-    // V rows for the transpose (key 4 i + g... : lane l covers dims 8 (l % 16) of
-    // keys 16 i + (l / 16) * 4 + {0..3} over i < 4, 16 loads)
+    // V rows for the transpose (lane l covers dims 8 (l % 16) of keys
+    // 16 i + (l / 16) * 4 + {0..3} over i < 4, 16 loads).  A chunk's 64 cache rows
+    // lie in one block, contiguous: buffer loads over that slab, the lane's part of
+    // each address in one VGPR (K and V), the rest in the scalar offset, so the 32
+    // loads take no address arithmetic.  V past L is zeroed when the chunk is
+    // transposed (only the sequence's last chunk has such keys).
+    const uint32_t k_lane = (uint32_t)(((int64_t)col * kv_stride + 8 * g) * sizeof(T));
+    const uint32_t v_lane = (uint32_t)(((int64_t)4 * g * kv_stride + 8 * col) * sizeof(T));
+    const uint32_t slab = (uint32_t)(64 * kv_stride * sizeof(T));
     u32x4 kr[4][4], vr[16];
     auto load_chunk = [&](int c) {
       const int k0 = c * 64;
       const int64_t row0 = (int64_t)tab[k0 / bs] * bs + k0 % bs;
-      const T* kb = kc + row0 * kv_stride + (int64_t)kvh * kFaHd;
+      const __amdgpu_buffer_rsrc_t rk = attn_rsrc(kc + row0 * kv_stride + (int64_t)kvh * kFaHd, slab);
+      const __amdgpu_buffer_rsrc_t rv = attn_rsrc(vc + row0 * kv_stride + (int64_t)kvh * kFaHd, slab);
   #pragma unroll
       for (int kt = 0; kt < 4; ++kt)
   #pragma unroll
-        for (int s = 0; s < 4; ++s) kr[kt][s] = ld16(kb + (int64_t)(16 * kt + col) * kv_stride + 32 * s + 8 * g);
-      const T* vb = vc + row0 * kv_stride + (int64_t)kvh * kFaHd + 8 * col;
+        for (int s = 0; s < 4; ++s)
+          kr[kt][s] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                    rk, k_lane, (uint32_t)((16 * kt * kv_stride + 32 * s) * sizeof(T)), 0));
   #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int key = 16 * (i >> 2) + 4 * g + (i & 3);
-        const u32x4 v = ld16(vb + (int64_t)key * kv_stride);  // inside the chunk's block: no branch
-        vr[i] = k0 + key < L ? v : u32x4{0, 0, 0, 0};           // past L: zero
-      }
+      for (int i = 0; i < 16; ++i)
+        vr[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                              rv, v_lane, (uint32_t)((16 * (i >> 2) + (i & 3)) * kv_stride * sizeof(T)), 0));
     };
     if (c0 + wave < c1) load_chunk(c0 + wave);
     for (int c = c0 + wave; c < c1; c += 4) {
-      // V^T into this wave's LDS: dim 8 col + e, keys 16 i4 + 4 g + {0..3}
+      if (c * 64 + 64 > L) {  // uniform: the last chunk, V of keys past L to zero
+  #pragma unroll
+        for (int i = 0; i < 16; ++i)
+          if (c * 64 + 16 * (i >> 2) + 4 * g + (i & 3) >= L) vr[i] = u32x4{0, 0, 0, 0};
+      }
+      const int gx = g ^ col;  // (4 i4 + g) ^ col = 4 i4 ^ (g ^ col): i4 only sets bits 2, 3
+      // V^T into this wave's LDS: dim 8 col + e, keys 16 i4 + 4 g + {0..3}; the
+      // 16-bit values of two keys go into one dword by a byte permute
   #pragma unroll
       for (int i4 = 0; i4 < 4; ++i4)
   #pragma unroll
         for (int e = 0; e < 8; ++e) {
-          const int sh = (e & 1) * 16;
-          const uint32_t lo =
-              ((vr[4 * i4][e >> 1] >> sh) & 0xffffu) | (((vr[4 * i4 + 1][e >> 1] >> sh) & 0xffffu) << 16);
-          const uint32_t hi =
-              ((vr[4 * i4 + 2][e >> 1] >> sh) & 0xffffu) | (((vr[4 * i4 + 3][e >> 1] >> sh) & 0xffffu) << 16);
+          const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;  // high or low halves of (b, a)
+          const uint32_t lo = __builtin_amdgcn_perm(vr[4 * i4 + 1][e >> 1], vr[4 * i4][e >> 1], sel);
+          const uint32_t hi = __builtin_amdgcn_perm(vr[4 * i4 + 3][e >> 1], vr[4 * i4 + 2][e >> 1], sel);
           typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-          *reinterpret_cast<u32x2*>(vt + (8 * col + e) * kFdVRow + (16 * i4 + 4 * g) * 2) = u32x2{lo, hi};
+          // row 8 col + e, unit 4 i4 + g (keys 16 i4 + 4 g + {0..3})
+          *reinterpret_cast<u32x2*>(vt + (8 * col + e) * kFdVRow + 8 * ((4 * i4) ^ gx)) = u32x2{lo, hi};
         }
       // S^T = K . Q^T, 4 tiles of 16 keys
       f32x4 st[4];
@@ -789,6 +820,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
       ls += __shfl_xor(ls, 32);
       l = l * alpha + ls;
       m = m_new;
+      const int gc3 = g ^ (col >> 3);
       // O^T += V^T . P^T: dims 16 d + col, key step u: keys 32 u + 4 g + {0..3}, 32 u + 16 + 4 g + {0..3}
   #pragma unroll
       for (int d = 0; d < kFaHd / 16; ++d) {
@@ -796,9 +828,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
   #pragma unroll
         for (int u = 0; u < 2; ++u) {
           typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-          const uint8_t* r = vt + (16 * d + col) * kFdVRow + (32 * u + 4 * g) * 2;
-          const u32x2 lo = *reinterpret_cast<const u32x2*>(r);
-          const u32x2 hi = *reinterpret_cast<const u32x2*>(r + 32);
+          // row 16 d + col: units 8 u + g and 8 u + g + 4 (keys 32 u + 4 g + {0..3}, + 16), swizzled
+          // by (2 d + col / 8); (8 u + g) ^ (2 d + col / 8) = (8 u ^ 2 d) ^ (g ^ col / 8)
+          const uint8_t* r = vt + (16 * d + col) * kFdVRow;
+          const u32x2 lo = *reinterpret_cast<const u32x2*>(r + 8 * ((8 * u ^ 2 * d) ^ gc3));
+          const u32x2 hi = *reinterpret_cast<const u32x2*>(r + 8 * (((8 * u + 4) ^ 2 * d) ^ gc3));
           o[d] = M::mma(__builtin_bit_cast(v8, u32x4{lo[0], lo[1], hi[0], hi[1]}), pb[u], o[d]);
         }
       }
@@ -846,12 +880,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   __shared__ float merge[4][kDecMergeFloats];
-  const int64_t t = !SKIP && order ? (int64_t)order[blockIdx.x] : (int64_t)blockIdx.x;  // as fa_decode_kernel
+  const bool tok_major = !SKIP && order;  // the workgroup's (token, kv head) as fa_decode_kernel's
+  const int64_t ti = SKIP ? (int64_t)blockIdx.x
+                     : tok_major ? (int64_t)blockIdx.x / kv_heads
+                                 : (int64_t)blockIdx.x % tokens;
+  const int64_t t = tok_major ? (int64_t)order[ti] : ti;
   if (t < 0 || t >= tokens) return;
   // workgroup-uniform: the whole workgroup leaves (fa_prefill_f32_kernel's tile)
   if (SKIP && fa_tile_uniform(qseq, tokens, t / kFaBq)) return;
   // as fa_decode_kernel: the tiles' second launch walks the kv heads per token
-  const int kvh0 = SKIP ? 0 : (int)blockIdx.y;
+  const int kvh0 = SKIP ? 0 : tok_major ? (int)(blockIdx.x % kv_heads) : (int)(blockIdx.x / tokens);
   const int kvh1 = SKIP ? kv_heads : kvh0 + 1;
   for (int kvh = kvh0; kvh < kvh1; ++kvh) {
     const int G = q_heads / kv_heads;
@@ -1198,7 +1236,7 @@ int attention_dispatch(const void* q, void* out, const void* kc, const void* vc,
   // from the caller's cu_seqlens), so every tile is uniform and the tiles' second
   // launch, whose workgroups would all exit, is not made
   constexpr int N = Pack<T>::N;
-  if (tokens > INT32_MAX) return fail(NVF_ERR_INVALID, "paged_attention: too many tokens");
+  if (tokens * kv_heads > INT32_MAX) return fail(NVF_ERR_INVALID, "paged_attention: too many tokens");
   const float sl = scale * 1.4426950408889634f;
   const int64_t ntiles = (tokens + kFaBq - 1) / kFaBq;
   if (ntiles * q_heads > INT32_MAX) return fail(NVF_ERR_INVALID, "paged_attention: too many tiles");
@@ -1269,7 +1307,7 @@ int attention_dispatch(const void* q, void* out, const void* kc, const void* vc,
   if (dec) {
     // one workgroup per (token, kv head); for the tiles' second launch (SKIP), one
     // per token walking the kv heads, since nearly all of its workgroups exit at once
-    const dim3 grid((unsigned)tokens, tiles ? 1u : (unsigned)kv_heads, nz);
+    const dim3 grid((unsigned)(tiles ? tokens : tokens * kv_heads), 1u, nz);
     const int kk = split ? skeys : 0;
     float* pp = split ? part : nullptr;
 #define NVF_DEC_LAUNCH_ORD(KERN, LDS, ORD)                                                                     \
