@@ -672,6 +672,10 @@ struct Mfma16x16<_Float16> {
   }
 };
 
+// Decode batches of at most this many tokens without a host order rank their
+// tokens in the kernel (each workgroup: tokens^2 / 256 comparisons).
+constexpr int64_t kDecSelfOrderMax = 512;
+
 template <typename T, bool SPLIT, bool SKIP>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void fa_decode_kernel(
     const T* __restrict__ q, T* __restrict__ out, const T* __restrict__ kc, const T* __restrict__ vc,
@@ -691,11 +695,42 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
   // first (measured at 256 sequences of U[1, 4096] keys: 186 against 200 us with
   // the kv heads outermost); without one, token x % tokens, kv head x / tokens (a
   // token's kv heads spread over the grid: 210 against 223 us for random lengths).
-  const bool tok_major = !SKIP && order;
+  const bool self_order = !SKIP && !SPLIT && !order && tokens <= kDecSelfOrderMax;
+  const bool tok_major = !SKIP && (order || self_order);
   const int64_t ti = SKIP ? (int64_t)blockIdx.x
                      : tok_major ? (int64_t)blockIdx.x / kv_heads
                                  : (int64_t)blockIdx.x % tokens;
-  const int64_t t = tok_major ? (int64_t)order[ti] : ti;
+  int64_t t;
+  if (self_order) {
+    // No order given and few tokens: the workgroup finds its token in longest-first
+    // order itself (key count descending, ties by token), dealt as
+    // nvf_decode_token_order deals it (slot ti holds rank r * 8 + x, x reversed on
+    // odd full rounds r of 8).  Every thread ranks its candidates against all
+    // counts, staged in LDS; the one whose rank is the slot's names it.
+    __shared__ int32_t sel;
+    int32_t* lens = reinterpret_cast<int32_t*>(lds);
+    const int n = (int)tokens;
+    for (int i = threadIdx.x; i < n; i += 256) lens[i] = qlen[i];
+    for (int i = n + threadIdx.x; i < ((n + 3) & ~3); i += 256) lens[i] = INT32_MIN;  // pads rank below all
+    __syncthreads();
+    const int64_t rr = ti / 8, rx = ti % 8;
+    const int64_t want = rr * 8 + ((rr & 1) && rr * 8 + 8 <= tokens ? 7 - rx : rx);
+    for (int i = threadIdx.x; i < n; i += 256) {
+      const int32_t li = lens[i];
+      int rank = 0;
+      for (int j4 = 0; j4 < n; j4 += 4) {
+        const int4 lj = *reinterpret_cast<const int4*>(lens + j4);
+        rank += (lj.x > li || (lj.x == li && j4 < i)) + (lj.y > li || (lj.y == li && j4 + 1 < i)) +
+                (lj.z > li || (lj.z == li && j4 + 2 < i)) + (lj.w > li || (lj.w == li && j4 + 3 < i));
+      }
+      if (rank == want) sel = i;
+    }
+    __syncthreads();
+    t = sel;
+    __syncthreads();  // the counts' LDS is the waves' buffers below
+  } else {
+    t = tok_major ? (int64_t)order[ti] : ti;
+  }
   if (t < 0 || t >= tokens) return;  // an order entry outside the batch: nothing to compute (uniform)
   // workgroup-uniform: the whole workgroup leaves (fa_prefill_kernel's tile)
   if (SKIP && fa_tile_uniform(qseq, tokens, t / kFaBq)) return;

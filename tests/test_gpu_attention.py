@@ -484,6 +484,44 @@ def test_paged_attention_host_cu_seqlens(gpu, dt, lens, prefix):
         ops.paged_attention(q, kc, vc, qs, ql, tab, bs, hd ** -0.5, cu_seqlens=cu[:-1])
 
 
+@pytest.mark.parametrize("n,lens", [(300, (64, 128)), (512, (5,)), (77, (1, 300, 300, 2048)), (513, (64, 700))],
+                         ids=["ties", "all-equal", "mixed", "past-self-order"])
+def test_paged_attention_decode_self_order(gpu, n, lens):
+    """Decode batches of at most 512 tokens without a token order rank their tokens
+    inside the kernel (longest first, ties by token): every token is computed exactly
+    once -- an output pre-filled with NaN keeps none -- and the result is bit-identical
+    to the host-ordered launch's; 513 tokens take the unranked path."""
+    g = torch.Generator(device=gpu)
+    g.manual_seed(n)
+    qh, kvh, hd, bs = 28, 4, 128, 256
+    r = np.random.default_rng(n + len(lens))
+    kl = np.array([lens[i % len(lens)] for i in range(n)], np.int32)
+    r.shuffle(kl)
+    kl[n // 3] = 0  # a query with no keys: a zero row
+    nbs = [max(1, -(-int(c) // bs)) for c in kl]
+    rows = sum(nbs) * bs
+    kc = torch.randn(rows, kvh, hd, device=gpu, generator=g).half()
+    vc = torch.randn(rows, kvh, hd, device=gpu, generator=g).half()
+    tab = np.full((n, max(nbs)), -1, np.int32)
+    perm = r.permutation(sum(nbs)).astype(np.int32)
+    o = 0
+    for s_, nb in enumerate(nbs):
+        tab[s_, :nb] = perm[o:o + nb]
+        o += nb
+    q = torch.randn(n, qh, hd, device=gpu, generator=g).half()
+    args = (q, kc, vc, torch.arange(n, dtype=torch.int32, device=gpu), torch.from_numpy(kl).to(gpu),
+            torch.from_numpy(tab).to(gpu), bs, hd ** -0.5)
+    case(f"paged_attention decode self-order n={n} lens={lens}")
+    out = torch.full((n, qh, hd), float("nan"), dtype=torch.float16, device=gpu)
+    ops.paged_attention(*args, max_query_len=1, split=False, out=out)
+    ref = ops.paged_attention(*args, max_query_len=1, split=False,
+                              token_order=torch.from_numpy(ops.decode_token_order(kl)).to(gpu))
+    torch.cuda.synchronize()
+    assert not torch.isnan(out).any().item(), "a token was not computed"
+    H.assert_bitexact(H.to_host(out), H.to_host(ref), "self-ordered vs host-ordered")
+    assert not out[n // 3].float().abs().sum().item()
+
+
 @pytest.mark.parametrize("dt", [H.F16, H.BF16, H.F32], ids=["f16", "bf16", "f32"])
 @pytest.mark.parametrize("n,ctx_max,order_kind,heads", [(256, 4096, "schedule", (28, 4)),  # config 1's batch
                                                         (256, 4096, "schedule", (32, 8)),  # Qwen3-8B's heads
