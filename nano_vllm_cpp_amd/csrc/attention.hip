@@ -214,9 +214,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
     uint8_t* vt = st + kFaKBytes + 8 * (ld_r ^ ((ld_c >> 1) & 7));
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      const int sh = (e & 1) * 16;
-      const uint32_t lo = ((vreg[0][e >> 1] >> sh) & 0xffffu) | (((vreg[1][e >> 1] >> sh) & 0xffffu) << 16);
-      const uint32_t hi = ((vreg[2][e >> 1] >> sh) & 0xffffu) | (((vreg[3][e >> 1] >> sh) & 0xffffu) << 16);
+      // the 16-bit values of two keys into one dword by a byte permute
+      const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;  // high or low halves of (b, a)
+      const uint32_t lo = __builtin_amdgcn_perm(vreg[1][e >> 1], vreg[0][e >> 1], sel);
+      const uint32_t hi = __builtin_amdgcn_perm(vreg[3][e >> 1], vreg[2][e >> 1], sel);
       typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
       *reinterpret_cast<u32x2*>(vt + (8 * ld_c + e) * kFaVRow) = u32x2{lo, hi};
     }
