@@ -207,23 +207,41 @@ struct StagedQ4K {
   }
 };
 
-// Staged flat: every other 34-byte block sits 2 bytes off dword alignment and its
-// reads take the unaligned path (17x the LDS issue stalls of Q5_K), but 48-byte
+// Staged flat: every other 34-byte block sits 2 bytes off dword alignment.  Its
+// quants are read as the aligned dwords that hold them (one more than their
+// count) and realigned with v_alignbyte: a 2-byte-aligned 8-byte LDS read takes
+// the hardware's unaligned path instead (17x the LDS issue stalls of Q5_K).  48-byte
 // aligned slots, at three 16-byte loads per block, measured slower (38.5 against
 // ~33 us at Qwen2.5-7B prefill shape): for 34-byte blocks the extra loads cost more.
+// The last dword read may reach 2 bytes past the row: the stage holds 16 spare bytes.
 template <int N>
 struct StagedQ8Blocks {
-  static constexpr int kBlockBytes = 34, kBlockElems = 32;
+  static constexpr int kBlockBytes = 34, kBlockElems = 32, kSpareBytes = 16;
   __device__ __forceinline__ static void decode(const uint8_t* blk, int i, float* v) {
     const float s = half_bits_to_f32(*reinterpret_cast<const uint16_t*>(blk));
+    const uint8_t* q8 = blk + 2 + i;
+    const uint32_t sh = (uint32_t)(reinterpret_cast<uintptr_t>(q8) & 3);  // 0 or 2
+    const uint32_t* d = reinterpret_cast<const uint32_t*>(q8 - sh);       // (pointer arithmetic: stays in LDS)
+    uint32_t dw[N / 4 + 1];
+#pragma unroll
+    for (int w = 0; w <= N / 4; ++w) dw[w] = d[w];
 #pragma unroll
     for (int w = 0; w < N / 4; ++w) {
-      uint32_t a;
-      __builtin_memcpy(&a, blk + 2 + i + 4 * w, 4);  // 2-byte aligned
+      const uint32_t q = __builtin_amdgcn_alignbyte(dw[w + 1], dw[w], sh);
 #pragma unroll
-      for (int k = 0; k < 4; ++k) v[4 * w + k] = s * sbyte(a, k);
+      for (int k = 0; k < 4; ++k) v[4 * w + k] = s * sbyte(q, k);
     }
   }
+};
+
+// kSpareBytes of a format: LDS bytes its decode may read past the staged row
+template <typename F, typename = void>
+struct SpareBytes {
+  static constexpr int value = 0;
+};
+template <typename F>
+struct SpareBytes<F, decltype((void)F::kSpareBytes)> {
+  static constexpr int value = F::kSpareBytes;
 };
 
 constexpr int kStageMaxBytesPerWave = 16384;  // LDS per wave: rows up to 16 KiB of blocks
@@ -307,7 +325,7 @@ __global__ __launch_bounds__(kEmbThreads) void embed_rows_staged_kernel(const in
 #pragma unroll
   for (int u = 0; u < L16; ++u) {
     const int c = u * kWave + lane;
-    if (c < n16) r[u] = ld16(reinterpret_cast<const uint8_t*>(a16) + c * 16);
+    if (c < n16) r[u] = ld16(row - delta + c * 16);  // (from row: a global load, not a flat one)
   }
 #pragma unroll
   for (int u = 0; u < L16; ++u) {
@@ -343,7 +361,7 @@ static bool launch_staged(const int64_t* ids, const uint8_t* table, TO* out, int
   const int64_t part_n16 = parts == 1 ? n16
                            : kSlot > 0 ? half_blocks * (kSlot / 16)
                                        : (15 + half_blocks * Fmt::kBlockBytes + 15) / 16;
-  const int stage_bytes = (int)(part_n16 * 16);
+  const int stage_bytes = (int)(part_n16 * 16) + SpareBytes<Fmt>::value;
   const size_t lds = (size_t)stage_bytes * kEmbWaves;
   const int64_t waves = tokens * parts;
   const dim3 grid((unsigned)((waves + kEmbWaves - 1) / kEmbWaves));
