@@ -65,7 +65,7 @@ def parse() -> argparse.Namespace:
                    help="with --write-traffic: the commit the profiled tree was built from (run where .git is; "
                         "the stamp then also records whether the kernel sources differ from it)")
     p.add_argument("--only", default="",
-                   help="comma list of ops (default emb,rms,rope,silu,copy,gemm,gemv,split,attn,attn_decode,attn_f32,"
+                   help="comma list of ops (default emb,rms,rope,silu,copy,gemm,gemv,gemv_down,gemv_qkv,gemv_o,split,attn,attn_decode,attn_f32,"
                         "attn_decode_ordered,attn_decode_f32,attn_decode_small,layer,layer_decode,layer_b1,layer_b1_graph); "
                         "also emb_rms, rms_q8, silu_q8 (fusions)")
     return p.parse_args()
@@ -91,11 +91,21 @@ def op_bytes(cfg, e: int, emb_fmt: str) -> dict[str, int]:
             "silu_q8": 2 * T * I * e + T * I + 4 * T,
             # decode GEMV (m = GEMV_M) at the gate_up shape: the weights once, plus activations and output
             "gemv": int(2 * I * Hd * 34 / 32) + GEMV_M * Hd + 4 * GEMV_M + GEMV_M * 2 * I * e,
+            # the layer's other decode GEMVs (m = GEMV_M): down [H, I], qkv [q + 2 kv, H], o [H, q]
+            **{k_: n_ * k2 // 32 * 34 + GEMV_M * k2 + 4 * GEMV_M + GEMV_M * n_ * e
+               for k_, (n_, k2, _) in gemv_shapes(cfg).items() if k_ != "gemv"},
             # on-device Q8_0 block split of the gate_up weights: 34 bytes in and 34 out per block
             "split": 2 * I * Hd // 32 * 68,
             # LM head at decode (m = 1): the [vocab, hidden] weights once (bf16 or Q4_K superblocks), x, fp32 logits
             "lm_head": cfg.vocab * Hd * 2 + Hd * e + 4 * cfg.vocab,
             "lm_head_q4k": cfg.vocab * Hd // 256 * 144 + Hd * e + 4 * cfg.vocab}
+
+
+def gemv_shapes(cfg) -> dict[str, tuple[int, int, str]]:
+    """Decode Q8_0 GEMV lines: name -> (n, k, projection)."""
+    qs, ks = cfg.q_heads * cfg.head_dim, cfg.kv_heads * cfg.head_dim
+    return {"gemv": (2 * cfg.inter, cfg.hidden, "gate_up"), "gemv_down": (cfg.hidden, cfg.inter, "down"),
+            "gemv_qkv": (qs + 2 * ks, cfg.hidden, "qkv"), "gemv_o": (cfg.hidden, qs, "o")}
 
 
 def main() -> int:
@@ -126,7 +136,7 @@ def main() -> int:
     emb_fmt = args.emb or cfg.emb
     nbytes = op_bytes(cfg, e, emb_fmt)
     only = set(filter(None, args.only.split(","))) or {"emb", "rms", "rope", "silu", "copy", "copy12", "copy12_emb",
-                                                       "gemm", "gemv", "split", "lm_head", "lm_head_q4k", "moe",
+                                                       "gemm", "gemv", "gemv_down", "gemv_qkv", "gemv_o", "split", "lm_head", "lm_head_q4k", "moe",
                                                        "attn", "attn_decode", "attn_decode_ordered", "attn_f32", "attn_decode_f32", "attn_decode_small", "layer", "layer_decode", "layer_b1", "layer_b1_graph"}
 
     def nsets(b: int) -> int:
@@ -177,14 +187,14 @@ def main() -> int:
     sq_sets = [(randn((T, 2 * I)), torch.empty(T, dtype=torch.float32, device=dev),
                 torch.empty(T, I, dtype=torch.int8, device=dev)) for _ in range(nsets(nbytes["silu_q8"]))] \
         if "silu_q8" in only else []
-    gemv_sets = []
-    if "gemv" in only:  # weights rotated over >= 1 GiB so every launch streams them from HBM
-        gsc1, gxq1 = ops.q8_quantize_rows(randn((GEMV_M, Hd)))
-        for _ in range(nsets(nbytes["gemv"])):
-            gemv_sets.append((torch.randint(-127, 128, (2 * I * Hd,), generator=g, device=dev, dtype=torch.int8),
-                              torch.empty(2 * I * Hd // 32, device=dev).uniform_(1e-3, 1e-2, generator=g).half()
-                              .view(torch.int16)))
-        gemv_out = torch.empty(GEMV_M, 2 * I, dtype=tdt, device=dev)
+    gemv_in = {}
+    for gn_, (gnn, gk, _) in gemv_shapes(cfg).items():
+        if gn_ in only:  # weights rotated over >= 1 GiB so every launch streams them from HBM
+            gsc1, gxq1 = ops.q8_quantize_rows(randn((GEMV_M, gk)))
+            gsets = [(torch.randint(-127, 128, (gnn * gk,), generator=g, device=dev, dtype=torch.int8),
+                      torch.empty(gnn * gk // 32, device=dev).uniform_(1e-3, 1e-2, generator=g).half().view(torch.int16))
+                     for _ in range(nsets(nbytes[gn_]))]
+            gemv_in[gn_] = (gxq1, gsc1, gsets, gnn, torch.empty(GEMV_M, gnn, dtype=tdt, device=dev))
     split_sets = []
     lm_sets = {}
     for n_, wf_ in (("lm_head", ops.W_BF16), ("lm_head_q4k", 12)):
@@ -400,9 +410,13 @@ def main() -> int:
         ops._check(ops.lib().nvf_silu_and_mul_q8(gu.data_ptr(), None, sc.data_ptr(), q.data_ptr(), T, I, ops._dt(gu),
                                                  ops._stream()), "silu_and_mul_q8")
 
-    def run_gemv(i):
-        w8_, ws_ = gemv_sets[i % len(gemv_sets)]
-        ops.matmul_q8_0(gxq1, gsc1, w8_, ws_, 2 * I, out=gemv_out)
+    def run_gemv_shape(name):
+        def f(i):
+            xq_, sc_, sets_, n_, o_ = gemv_in[name]
+            w8_, ws_ = sets_[i % len(sets_)]
+            ops.matmul_q8_0(xq_, sc_, w8_, ws_, n_, out=o_)
+        return f
+    run_gemv = run_gemv_shape("gemv")
 
     def run_lm(name):
         def f(i):
@@ -534,7 +548,8 @@ def main() -> int:
     table = [("emb", run_emb), ("rms", run_rms), ("rope", run_rope), ("silu", run_silu), ("emb_rms", run_emb_rms),
              ("rms_q8", run_rms_q8), ("silu_q8", run_silu_q8), ("copy", run_copy),
              ("copy12", run_copy12), ("copy12_emb", run_copy12_emb), ("gemm", run_gemm),
-             ("gemv", run_gemv), ("split", run_split), ("lm_head", run_lm("lm_head")),
+             ("gemv", run_gemv), ("gemv_down", run_gemv_shape("gemv_down")), ("gemv_qkv", run_gemv_shape("gemv_qkv")),
+             ("gemv_o", run_gemv_shape("gemv_o")), ("split", run_split), ("lm_head", run_lm("lm_head")),
              ("lm_head_q4k", run_lm("lm_head_q4k")), ("moe", run_moe), ("attn", run_attn), ("attn_decode", run_attn_decode),
              ("attn_decode_ordered", run_attn_decode_ordered),
              ("attn_f32", run_attn_f32), ("attn_decode_f32", run_attn_decode_f32), ("attn_decode_small", run_attn_decode_small),
@@ -591,9 +606,10 @@ def main() -> int:
             entry.update({"bytes": nbytes[n], "GB_s": round(gbs, 1), "frac_of_peak": round(gbs / HBM_PEAK_GBS, 4),
                           "frac_of_peak_p50": round(nbytes[n] / (entry["p50_us"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
                           "tokens_per_s": round(T / (t_us * 1e-6), 1)})
-        if n == "gemv":
+        if n in gemv_in:
             entry.pop("tokens_per_s")
-            entry["shape"] = f"m={GEMV_M} n={2 * I} k={Hd} (gate_up, decode)"
+            gnn, gk, gproj = gemv_shapes(cfg)[n]
+            entry["shape"] = f"m={GEMV_M} n={gnn} k={gk} ({gproj}, decode)"
         elif n == "moe":
             m = moe_in
             wbytes = m["experts"] * 3 * m["H"] * m["I"] * 2
@@ -716,6 +732,7 @@ def main() -> int:
         "roofline": roofline,
         "q8_gemm": res_ops.get("gemm"),
         "q8_gemv": res_ops.get("gemv"),
+        "q8_gemv_shapes": {k: res_ops[k] for k in ("gemv_down", "gemv_qkv", "gemv_o") if k in res_ops} or None,
         "q8_0_split": res_ops.get("split"),
         "weight_gemv": {k: res_ops[k] for k in ("lm_head", "lm_head_q4k") if k in res_ops} or None,
         "moe_ffn": res_ops.get("moe"),
