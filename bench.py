@@ -978,7 +978,7 @@ def write_traffic(prof_dir: str, config: int, source_commit: str = "") -> dict:
     out = {"_source": {"commit": head, "kernel_sources_modified": dirty,
                        "command": "rocprofv3 --pmc <FETCH_SIZE|WRITE_SIZE> -f csv -d <dir>/<counter> -o <counter> -- "
                                   f"python3 bench.py --config {config} --only emb,rms,rope,silu,copy --steps 10 "
-                                  "--warmup 2 --cpu-seconds 0"},
+                                  "--warmup 2 --cpu-seconds 0 --configs ''"},
            "_calibration": {"reference": "nvf_stream_copy of 1 GiB (16 B non-temporal loads/stores)",
                             "copy_fetch_kib": round(cal["FETCH_SIZE"], 1), "copy_write_kib": round(cal["WRITE_SIZE"], 1),
                             "fetch_factor": round(ff, 4), "write_factor": round(wf, 4)},
