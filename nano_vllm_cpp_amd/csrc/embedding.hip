@@ -126,34 +126,38 @@ static int launch_rows(const int64_t* ids, const Src& src, TO* out, int64_t toke
 // A format supplies
 //   kBlockBytes, kBlockElems, decode(const uint8_t* blk, int i, float* v)
 // reading the block from LDS (elements i .. i+N-1 of the block), and may supply
-//   kSlotBytes, slot_src(k)
-// to be staged block by block into aligned slots of kSlotBytes (16-byte chunk k
-// of a slot taken from block byte slot_src(k)) instead of as the flat row.
+// kSpareBytes, the bytes its decode may read past the staged row.
 // ---------------------------------------------------------------------------
 // Q6_K superblocks are 210 bytes, so flat staging leaves every other one 2 bytes
-// off dword alignment, and 8-byte LDS reads there take the hardware's unaligned
-// path (measured: 47x the LDS issue stalls of Q5_K).  The staged kernel gives
-// each one a 224-byte slot instead (kSlotBytes): bytes 0..207 at 0..207, and
-// bytes 194..209 at 208..223 (so d sits at 222), every read aligned.
+// off dword alignment.  As for the 34-byte Q8_0 blocks, the quants are read as the
+// aligned dwords that hold them (one more than their count) and realigned with
+// v_alignbyte: a 2-byte-aligned dword LDS read would take the hardware's
+// unaligned path.  The row is staged by aligned 16-byte global loads.  Every read
+// stays inside its block (the quants end at byte 192 of 210).
 template <int N>
 struct StagedQ6K {
-  static constexpr int kBlockBytes = 210, kBlockElems = 256, kSlotBytes = 224;
-  // block byte that slot chunk k starts at
-  __device__ __forceinline__ static int slot_src(int k) { return k < kSlotBytes / 16 - 1 ? 16 * k : 194; }
+  static constexpr int kBlockBytes = 210, kBlockElems = 256;
   __device__ __forceinline__ static void decode(const uint8_t* blk, int i, float* v) {
     const int h = i >> 7, t = i & 127, l0 = t & 31, slot = t >> 5;
     const int lsh = (slot >> 1) * 4, hsh = 2 * slot;
-    const float ds = half_bits_to_f32(*reinterpret_cast<const uint16_t*>(blk + 222)) *
+    const float ds = half_bits_to_f32(*reinterpret_cast<const uint16_t*>(blk + 208)) *
                      (float)(int8_t)blk[192 + 8 * h + (l0 >> 4) + 2 * slot];
-    const uint8_t* ql = blk + 64 * h + 32 * (slot & 1) + l0;
-    const uint8_t* qh = blk + 128 + 32 * h + l0;
+    const uint32_t sh = (uint32_t)(reinterpret_cast<uintptr_t>(blk) & 3);  // 0 or 2 (l0 % 4 == 0)
+    const uint32_t* ql = reinterpret_cast<const uint32_t*>(blk - sh + 64 * h + 32 * (slot & 1) + l0);
+    const uint32_t* qh = reinterpret_cast<const uint32_t*>(blk - sh + 128 + 32 * h + l0);
+    uint32_t da[N / 4 + 1], db[N / 4 + 1];
+#pragma unroll
+    for (int w = 0; w <= N / 4; ++w) {
+      da[w] = ql[w];
+      db[w] = qh[w];
+    }
     // four 6-bit values per dword at once (low nibbles | high 2 bits << 4), then per
     // byte an exact byte-to-float, an exact - 32 and the product, as the reference
     // (an fma with -32 ds folded in would give +0 where the reference gives -0)
 #pragma unroll
     for (int w = 0; w < N / 4; ++w) {
-      const uint32_t a = *reinterpret_cast<const uint32_t*>(ql + 4 * w);  // dword-aligned in the slot
-      const uint32_t b = *reinterpret_cast<const uint32_t*>(qh + 4 * w);
+      const uint32_t a = __builtin_amdgcn_alignbyte(da[w + 1], da[w], sh);
+      const uint32_t b = __builtin_amdgcn_alignbyte(db[w + 1], db[w], sh);
       const uint32_t q4 = ((a >> lsh) & 0x0f0f0f0fu) | (((b >> hsh) & 0x03030303u) << 4);
 #pragma unroll
       for (int k = 0; k < 4; ++k) v[4 * w + k] = ((float)byte_of(q4, k) - 32.0f) * ds;
@@ -246,16 +250,6 @@ struct SpareBytes<F, decltype((void)F::kSpareBytes)> {
 
 constexpr int kStageMaxBytesPerWave = 16384;  // LDS per wave: rows up to 16 KiB of blocks
 
-// kSlotBytes of a format (0: flat staging of the row's bytes)
-template <typename F, typename = void>
-struct SlotBytes {
-  static constexpr int value = 0;
-};
-template <typename F>
-struct SlotBytes<F, decltype((void)F::kSlotBytes)> {
-  static constexpr int value = F::kSlotBytes;
-};
-
 // PARTS waves per row: wave p of a row stages and decodes blocks [nblk p / PARTS,
 // nblk (p + 1) / PARTS) of it, so a row's blocks are spread over more waves.
 template <typename TO, typename Fmt, int L16, int PARTS>  // L16: 16-byte loads per lane to stage a part
@@ -284,39 +278,6 @@ __global__ __launch_bounds__(kEmbThreads) void embed_rows_staged_kernel(const in
     return;
   }
   const uint8_t* row = table + (id * (int64_t)nblk + b0) * Fmt::kBlockBytes;
-  constexpr int kSlot = SlotBytes<Fmt>::value;
-  if constexpr (kSlot > 0) {
-    // 16-byte loads k = 0 .. kPer - 1 of block b: from block byte Fmt::slot_src(k)
-    // into slot bytes 16 k; none reads past the block, so none leaves the table
-    constexpr int kPer = kSlot / 16;
-    uint8_t* my = stage + wave * stage_bytes;
-    const int nld = (b1 - b0) * kPer;
-    u32x4 r[L16];
-#pragma unroll
-    for (int u = 0; u < L16; ++u) {
-      const int c = u * kWave + lane;
-      if (c < nld) {
-        const int b = c / kPer, k = c - kPer * b;
-        const int off = Fmt::kBlockBytes * b + Fmt::slot_src(k);
-        __builtin_memcpy(&r[u], row + off, 16);  // 2-byte aligned: an unaligned 16-byte load
-      }
-    }
-#pragma unroll
-    for (int u = 0; u < L16; ++u) {
-      const int c = u * kWave + lane;
-      if (c < nld) *reinterpret_cast<u32x4*>(my + 16 * c) = r[u];  // slot b, chunk k: byte 16 (kPer b + k)
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    for (int c = lane; c < nch; c += kWave) {
-      const int e = c * N;
-      float v[N];
-      Fmt::decode(my + (e / Fmt::kBlockElems) * kSlot, e % Fmt::kBlockElems, v);
-      st16_nt(dst + (int64_t)c * N, Pack<TO>::pack(v));
-    }
-    return;
-  }
   const uintptr_t a16 = reinterpret_cast<uintptr_t>(row) & ~uintptr_t(15);
   const int delta = (int)(reinterpret_cast<uintptr_t>(row) - a16);
   const int n16 = (delta + (b1 - b0) * Fmt::kBlockBytes + 15) >> 4;
@@ -347,20 +308,17 @@ __global__ __launch_bounds__(kEmbThreads) void embed_rows_staged_kernel(const in
 template <typename TO, typename Fmt>
 static bool launch_staged(const int64_t* ids, const uint8_t* table, TO* out, int64_t tokens, int64_t hidden,
                           int64_t vocab, hipStream_t st) {
-  constexpr int kSlot = SlotBytes<Fmt>::value;
-  const int64_t row_bytes = hidden / Fmt::kBlockElems * (kSlot > 0 ? kSlot : Fmt::kBlockBytes);
-  // flat staging reads from the 16-byte boundary at or below the row: one chunk more
-  const int64_t n16 = kSlot > 0 ? row_bytes / 16 : (15 + row_bytes + 15) / 16;
+  const int64_t row_bytes = hidden / Fmt::kBlockElems * Fmt::kBlockBytes;
+  // the stage starts at the 16-byte boundary at or below the row: one chunk more
+  const int64_t n16 = (15 + row_bytes + 15) / 16;
   if (hidden % Fmt::kBlockElems != 0 || n16 * 16 > kStageMaxBytesPerWave || hidden > INT32_MAX) return false;
   // two waves per row when the row has at least 8 blocks (measured at Qwen2.5-7B's
   // shape: Q5_K 70.7 -> 74.3%, Q4_K 75.4 -> 76.7%, Q6_K 63.1 -> 64.3%, Q8_0 blocks
   // 67.0 -> 67.8% of 8 TB/s; four waves per row was slower for every format)
   const int parts = hidden / Fmt::kBlockElems >= 8 ? 2 : 1;
-  // 16-byte chunks of the larger part: ceil(nblk / 2) blocks (flat: plus the alignment lead)
+  // 16-byte chunks of the larger part: ceil(nblk / 2) blocks plus the alignment lead
   const int64_t half_blocks = (hidden / Fmt::kBlockElems + parts - 1) / parts;
-  const int64_t part_n16 = parts == 1 ? n16
-                           : kSlot > 0 ? half_blocks * (kSlot / 16)
-                                       : (15 + half_blocks * Fmt::kBlockBytes + 15) / 16;
+  const int64_t part_n16 = parts == 1 ? n16 : (15 + half_blocks * Fmt::kBlockBytes + 15) / 16;
   const int stage_bytes = (int)(part_n16 * 16) + SpareBytes<Fmt>::value;
   const size_t lds = (size_t)stage_bytes * kEmbWaves;
   const int64_t waves = tokens * parts;
