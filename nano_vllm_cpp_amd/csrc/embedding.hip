@@ -26,6 +26,7 @@
 //   * A hidden that is not a multiple of the block takes a per-element kernel
 //     (correct, not tuned).
 #include <atomic>
+#include <type_traits>
 
 #include "nvf_device.hpp"
 #include "nvf_host.hpp"
@@ -430,7 +431,14 @@ static bool launch_embed_rms(const int64_t* ids, const Src& src, const T* w, T* 
                              int64_t hidden, int64_t vocab, float eps, hipStream_t st) {
   constexpr int N = Pack<T>::N;
   const int64_t nch = hidden / N;
-  const int wpr = nch >= 4 * kWave ? 4 : 1;
+  // Long rows over 4 waves; 8-bit tables over 2 when there are at least 16384 rows
+  // (measured, fp16 / bf16 out: 16384 x 3584 Q8_0 52.5 against 54.5 us at 4 waves;
+  // 8192 x 4096 Q8_0 31.1 against 29.8 us, and 32768 x 3584 Q4_K 81-83 against
+  // 79-81 us, so those keep 4; a 4-workgroup residency cap was slower everywhere)
+  constexpr bool k8 = std::is_same<Src, Q8Split<N>>::value || std::is_same<Src, Q8Blocks<N>>::value;
+  const int wpr = nch < 4 * kWave ? 1
+                  : k8 && tokens >= 16384 && nch <= 2 * 16 * kWave ? 2
+                                                                   : 4;
   const int64_t per_lane = (nch + wpr * kWave - 1) / (wpr * kWave);
   if (per_lane < 1 || per_lane > 16) return false;
   const dim3 grid((unsigned)((tokens + kEmbWaves / wpr - 1) / (kEmbWaves / wpr)));
@@ -444,6 +452,14 @@ static bool launch_embed_rms(const int64_t* ids, const Src& src, const T* w, T* 
 #undef NVF_ER_CASE
       default: return false;
     }
+  } else if (wpr == 2) {
+    switch (per_lane) {
+#define NVF_ER_CASE(UU) case UU: NVF_ER_LAUNCH(UU, 2); break;
+      NVF_ER_CASE(1) NVF_ER_CASE(2) NVF_ER_CASE(3) NVF_ER_CASE(4) NVF_ER_CASE(5) NVF_ER_CASE(6) NVF_ER_CASE(7)
+      NVF_ER_CASE(8) NVF_ER_CASE(9) NVF_ER_CASE(10) NVF_ER_CASE(11) NVF_ER_CASE(12) NVF_ER_CASE(13) NVF_ER_CASE(14)
+      NVF_ER_CASE(15) NVF_ER_CASE(16)
+#undef NVF_ER_CASE
+    }
   } else {
     switch (per_lane) {
 #define NVF_ER_CASE(UU) case UU: NVF_ER_LAUNCH(UU, 4); break;
@@ -451,6 +467,7 @@ static bool launch_embed_rms(const int64_t* ids, const Src& src, const T* w, T* 
       NVF_ER_CASE(8) NVF_ER_CASE(9) NVF_ER_CASE(10) NVF_ER_CASE(11) NVF_ER_CASE(12) NVF_ER_CASE(13) NVF_ER_CASE(14)
       NVF_ER_CASE(15) NVF_ER_CASE(16)
 #undef NVF_ER_CASE
+      default: return false;
     }
   }
 #undef NVF_ER_LAUNCH

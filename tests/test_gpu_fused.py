@@ -86,7 +86,8 @@ def _emb_reference(o, fmt, ids, table, scales, T, Hd, dt):
 @pytest.mark.parametrize("dt", DTYPES, ids=DT_IDS)
 @pytest.mark.parametrize("fmt", [ops.EMB_Q8_0, ops.EMB_Q8_0_BLOCKS, ops.EMB_Q4_K, ops.EMB_Q5_K, ops.EMB_Q6_K],
                          ids=["q8_0", "q8_0_blocks", "q4_k", "q5_k", "q6_k"])
-@pytest.mark.parametrize("hidden", [3584, 1024])
+# (row splits at these 70 rows: 256 one wave per row, the others four)
+@pytest.mark.parametrize("hidden", [3584, 1024, 256, 12288])
 def test_embedding_rms_norm(gpu, dt, fmt, hidden):
     o = H.oracle()
     r = H.rng(hidden + fmt * 3 + dt)
@@ -106,6 +107,28 @@ def test_embedding_rms_norm(gpu, dt, fmt, hidden):
     ref_out = np.empty_like(emb)
     o.orc_rms_norm_add(H.ptr(emb), H.ptr(ref_res), H.ptr(w), H.ptr(ref_out), T, hidden, 1e-6, dt)
     case(f"embedding_rms_norm fmt={fmt} hidden={hidden} dt={dt}")
+    res, out = ops.embedding_rms_norm(H.to_dev(ids, gpu), fmt, H.to_dev(table, gpu),
+                                      H.to_dev(scales, gpu) if scales is not None else None, hidden,
+                                      H.to_dev(w, gpu, dt), 1e-6, V)
+    H.assert_bitexact(H.to_host(res), ref_res, "fused residual")
+    H.assert_close(H.to_host(out), ref_out, dt, what="fused norm")
+
+
+@pytest.mark.parametrize("fmt", [ops.EMB_Q8_0, ops.EMB_Q8_0_BLOCKS], ids=["q8_0", "q8_0_blocks"])
+def test_embedding_rms_norm_many_rows(gpu, fmt):
+    """16384 rows: the 8-bit tables' two-waves-per-row split."""
+    o = H.oracle()
+    dt, hidden, V, T = H.F16, 3584, 300, 16384
+    r = H.rng(fmt + 4242)
+    w8, ws = H.gen_q8_0(r, V, hidden)
+    table, scales = (w8, ws) if fmt == ops.EMB_Q8_0 else (H.q8_split_to_blocks(w8, ws), None)
+    ids = r.integers(0, V, T).astype(np.int64)
+    w = H.gen_act(r, (hidden,), dt, 1.0, 0.1)
+    emb = _emb_reference(o, fmt, ids, table, scales, T, hidden, dt)
+    ref_res = H.to_storage(np.zeros((T, hidden), np.float32), dt)
+    ref_out = np.empty_like(emb)
+    o.orc_rms_norm_add(H.ptr(emb), H.ptr(ref_res), H.ptr(w), H.ptr(ref_out), T, hidden, 1e-6, dt)
+    case(f"embedding_rms_norm fmt={fmt} rows={T}")
     res, out = ops.embedding_rms_norm(H.to_dev(ids, gpu), fmt, H.to_dev(table, gpu),
                                       H.to_dev(scales, gpu) if scales is not None else None, hidden,
                                       H.to_dev(w, gpu, dt), 1e-6, V)
