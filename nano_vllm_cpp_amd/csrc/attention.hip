@@ -634,7 +634,8 @@ constexpr int kDecMergeFloats = kFaHd * 16 + 32;  // one wave's state in the mer
 // block sizes a multiple of 64, at most 16 query heads per kv head): a wave
 // streams its share of one (token, kv head)'s keys in 64-key chunks.  The query
 // heads of the group are the 16 columns of v_mfma_f32_16x16x32 tiles:
-//   S^T = K . Q^T    (A = 16 keys x 32 dims straight from the cache, B = q)
+//   S^T = K . Q^T    (A = 16 keys x 32 dims, K rows loaded whole and passed
+//                     through the wave's LDS buffer to that layout, B = q)
 //   O^T += V^T . P^T (A = V^T from a wave-private LDS transpose of the chunk,
 //                     B = P^T, again S^T's own registers: a lane holds keys
 //                     32 u + 4 g + {0..3} and 32 u + 16 + 4 g + {0..3}, g = lane/16)
@@ -647,8 +648,12 @@ constexpr int kDecMergeFloats = kFaHd * 16 + 32;  // one wave's state in the mer
 // w ^ ((r / 8) % 16), rows 144 bytes apart: both the transpose's 8-byte writes and
 // the operand reads take the minimum 2 LDS passes (a 8-byte pad alone: 4 and 3)
 constexpr int kFdVRow = 64 * 2 + 16;
+// K rows staged row-major in the same buffer first: a 16-byte pad puts the 8 rows
+// of a read phase on distinct banks
+constexpr int kFdKRow = kFaHd * 2 + 16;
 constexpr int kFdWaveLds = kFaHd * kFdVRow;      // per wave
 constexpr int kFdLds = 4 * kFdWaveLds;
+static_assert(64 * kFdKRow <= kFdWaveLds, "a chunk's K rows fit the wave's V^T buffer");
 
 
 // A raw buffer over `bytes` bytes at p (32-bit dwords; offsets past the end read zero).
@@ -768,14 +773,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
       c0 = (int)blockIdx.z * (split_keys / 64);
       c1 = min(c1, c0 + split_keys / 64);
     }
-    // chunk loads: K as MFMA A operands (key 16 kt + col, dims 32 s + 8 g);
-    // V rows for the transpose (lane l covers dims 8 (l % 16) of keys
-    // 16 i + (l / 16) * 4 + {0..3} over i < 4, 16 loads).  A chunk's 64 cache rows
-    // lie in one block, contiguous: buffer loads over that slab, the lane's part of
-    // each address in one VGPR (K and V), the rest in the scalar offset, so the 32
-    // loads take no address arithmetic.  V past L is zeroed when the chunk is
-    // transposed (only the sequence's last chunk has such keys).
-    const uint32_t k_lane = (uint32_t)(((int64_t)col * kv_stride + 8 * g) * sizeof(T));
+    // chunk loads, K and V alike: lane l covers dims 8 (l % 16) of keys
+    // 16 i + (l / 16) * 4 + {0..3} over i < 4, 16 loads each, so every load
+    // instruction reads 4 whole 256-byte head rows.  (K read straight in the MFMA
+    // A layout, key 16 kt + col and dims 32 s + 8 g, reads 64-byte pieces of 16 rows
+    // per instruction: at 256 sequences of 1..4096 keys 187 against 184 us with the
+    // K rows passed through LDS to that layout.)  A chunk's 64 cache rows lie in one
+    // block, contiguous: buffer loads over that slab, the lane's part of each
+    // address in one VGPR, the rest in the scalar offset, so the 32 loads take no
+    // address arithmetic.  V past L is zeroed when the chunk is transposed (only the
+    // sequence's last chunk has such keys).
     const uint32_t v_lane = (uint32_t)(((int64_t)4 * g * kv_stride + 8 * col) * sizeof(T));
     const uint32_t slab = (uint32_t)(64 * kv_stride * sizeof(T));
     u32x4 kr[4][4], vr[16];
@@ -785,11 +792,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
       const __amdgpu_buffer_rsrc_t rk = attn_rsrc(kc + row0 * kv_stride + (int64_t)kvh * kFaHd, slab);
       const __amdgpu_buffer_rsrc_t rv = attn_rsrc(vc + row0 * kv_stride + (int64_t)kvh * kFaHd, slab);
   #pragma unroll
-      for (int kt = 0; kt < 4; ++kt)
-  #pragma unroll
-        for (int s = 0; s < 4; ++s)
-          kr[kt][s] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                    rk, k_lane, (uint32_t)((16 * kt * kv_stride + 32 * s) * sizeof(T)), 0));
+      for (int i = 0; i < 16; ++i)
+        kr[i >> 2][i & 3] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                        rk, v_lane, (uint32_t)((16 * (i >> 2) + (i & 3)) * kv_stride * sizeof(T)), 0));
   #pragma unroll
       for (int i = 0; i < 16; ++i)
         vr[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
@@ -797,6 +802,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
     };
     if (c0 + wave < c1) load_chunk(c0 + wave);
     for (int c = c0 + wave; c < c1; c += 4) {
+      // K rows into the wave's buffer, then back in the MFMA A layout (key 16 kt + col,
+      // dims 32 s + 8 g); the V^T transpose below reuses the buffer after these reads
+      // (a wave's LDS operations complete in order)
+  #pragma unroll
+      for (int i = 0; i < 16; ++i)
+        *reinterpret_cast<u32x4*>(vt + (16 * (i >> 2) + 4 * g + (i & 3)) * kFdKRow + 16 * col) = kr[i >> 2][i & 3];
+      __builtin_amdgcn_wave_barrier();
+  #pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+  #pragma unroll
+        for (int s = 0; s < 4; ++s)
+          kr[kt][s] = *reinterpret_cast<const u32x4*>(vt + (16 * kt + col) * kFdKRow + 16 * (4 * s + g));
+      __builtin_amdgcn_wave_barrier();
       if (c * 64 + 64 > L) {  // uniform: the last chunk, V of keys past L to zero
   #pragma unroll
         for (int i = 0; i < 16; ++i)
