@@ -917,12 +917,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
 // merge in LDS (as fa_decode_kernel), the group's query heads the 16 columns, 16-key
 // chunks straight from the cache into registers (the next chunk's loads in
 // flight during the current chunk's math; no LDS).
-//   S^T = K . Q^T   32 MFMAs; MFMA 4 i + e contracts dim 32 (lane / 16) + 4 i + e,
-//                   so a lane's operands are 16-byte runs of its key's K row / q.
+//   S^T = K . Q^T   32 MFMAs; MFMA 4 i + e contracts dim 16 i + 4 (lane / 16) + e,
+//                   so a lane's operands are 16-byte runs of its key's K row / q,
+//                   and one load instruction takes 64 bytes of each of 16 K rows.
 //   O^T += V^T . P^T  MFMA u contracts key 4 (lane / 16) + u, the key S^T's
 //                   register u of this lane holds (P^T = those registers); row r
-//                   of O^T tile dt is dim 8 r + dt, so one key's A operands for
-//                   the 8 tiles are 32 consecutive bytes of its V row.
+//                   of O^T tile dt is dim 64 (dt / 4) + 4 r + dt % 4, so one
+//                   load instruction takes 4 whole 256-byte halves of V rows.
 constexpr int kFd32Bk = 16;  // keys per chunk
 
 template <bool SPLIT, bool SKIP>
@@ -955,10 +956,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
     const int64_t kv_stride = (int64_t)kv_heads * kFaHd;
     const int32_t* tab = tables + seq * max_blocks;
 
-    f32x4 qf[8];  // B operand: head col, dims 32 g + 4 i + e
+    f32x4 qf[8];  // B operand: head col, dims 16 i + 4 g + e
   #pragma unroll
     for (int i = 0; i < 8; ++i)
-      qf[i] = head_ok ? __builtin_bit_cast(f32x4, ld16(q + t * q_stride + (int64_t)h * kFaHd + 32 * g + 4 * i))
+      qf[i] = head_ok ? __builtin_bit_cast(f32x4, ld16(q + t * q_stride + (int64_t)h * kFaHd + 16 * i + 4 * g))
                       : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     f32x4 o[8];
   #pragma unroll
@@ -971,21 +972,21 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
       c1 = min(c1, c0 + split_keys / kFd32Bk);
     }
 
-    // chunk c: K row of key 16 c + col, dims 32 g + 4 i (A operands of S^T); V row
-    // of key 16 c + 4 g + u, dims 8 col .. 8 col + 7 (A operands of O^T, zero past L)
+    // chunk c: K row of key 16 c + col, dims 16 i + 4 g (A operands of S^T); V row
+    // of key 16 c + 4 g + u, dims 4 col and 64 + 4 col (A operands of O^T, zero past L)
     auto load = [&](int c, u32x4* kr, u32x4* vr) {
       const int k0 = c * kFd32Bk;
       const int64_t row0 = (int64_t)tab[k0 / bs] * bs + k0 % bs;
-      const float* kb = kc + (row0 + col) * kv_stride + (int64_t)kvh * kFaHd + 32 * g;
+      const float* kb = kc + (row0 + col) * kv_stride + (int64_t)kvh * kFaHd + 4 * g;
   #pragma unroll
-      for (int i = 0; i < 8; ++i) kr[i] = ld16(kb + 4 * i);
-      const float* vb = vc + row0 * kv_stride + (int64_t)kvh * kFaHd + 8 * col;
+      for (int i = 0; i < 8; ++i) kr[i] = ld16(kb + 16 * i);
+      const float* vb = vc + row0 * kv_stride + (int64_t)kvh * kFaHd + 4 * col;
   #pragma unroll
       for (int u = 0; u < 4; ++u) {
         const int key = 4 * g + u;
         const bool ok = k0 + key < L;
         // (the rows lie inside the chunk's block: unconditional loads, selected values)
-        const u32x4 v0 = ld16(vb + (int64_t)key * kv_stride), v1 = ld16(vb + (int64_t)key * kv_stride + 4);
+        const u32x4 v0 = ld16(vb + (int64_t)key * kv_stride), v1 = ld16(vb + (int64_t)key * kv_stride + 64);
         vr[2 * u] = ok ? v0 : u32x4{0, 0, 0, 0};
         vr[2 * u + 1] = ok ? v1 : u32x4{0, 0, 0, 0};
       }
@@ -1024,9 +1025,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
       }
       const float m_use = m == -INFINITY ? 0.0f : m;
       float ls = 0.0f;
+      // (the product rounded as in the max, not fused into the difference: the key
+      // that set m weighs exactly 1, so a single key returns its V row exactly)
   #pragma unroll
       for (int v = 0; v < 4; ++v) {
-        st[v] = __builtin_amdgcn_exp2f(fmaf(st[v], scale_log2, -m_use));
+  #pragma clang fp contract(off)
+        st[v] = __builtin_amdgcn_exp2f(st[v] * scale_log2 - m_use);
         ls += st[v];
       }
       ls += __shfl_xor(ls, 16);
@@ -1054,12 +1058,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
         compute(c + 4, kb_, vb_);
       }
     }
-    // O^T: register v of tile d is dim 8 (4 g + v) + d of head col
+    // O^T: register v of tile d is dim 64 (d / 4) + 4 (4 g + v) + d % 4 of head col
     float* pw = merge[wave];
   #pragma unroll
     for (int d = 0; d < 8; ++d)
   #pragma unroll
-      for (int v = 0; v < 4; ++v) pw[(8 * (4 * g + v) + d) * 16 + col] = o[d][v];
+      for (int v = 0; v < 4; ++v) pw[(64 * (d >> 2) + 4 * (4 * g + v) + (d & 3)) * 16 + col] = o[d][v];
     if (g == 0) {
       pw[kFaHd * 16 + col] = m;
       pw[kFaHd * 16 + 16 + col] = l;
