@@ -90,7 +90,9 @@ constexpr int kFaHd = 128;
 constexpr int kFaBq = 128;                       // query tokens per workgroup
 constexpr int kFaBk = 64;                        // keys per chunk
 constexpr float kFaLazy = 8.0f;                  // exp2 units the running max may lag behind (16-bit tiles)
-constexpr int kFaKRow = kFaHd * 2 + 16;          // K row in LDS, padded (conflict-free 16 B reads)
+// K row in LDS, written by DMA: unpadded, its 16-byte units swizzled by row
+// (conflict-free 16 B reads)
+constexpr int kFaKRow = kFaHd * 2;
 constexpr int kFaVRow = kFaBk * 2 + 8;           // V^T row in LDS, padded
 constexpr int kFaKBytes = kFaBk * kFaKRow;
 constexpr int kFaStage = kFaKBytes + kFaHd * kFaVRow;
@@ -178,20 +180,37 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
     qf[s] = __builtin_bit_cast(v8, v);
   }
 
-  // chunk loads: K row key = tid/16 + 16 i, dims 8 (tid%16); V keys 4 (tid/16) + e, dims 8 (tid%16)
+  // chunk loads: V keys 4 (tid/16) + e, dims 8 (tid%16) into registers (transposed on
+  // the way to LDS); K by DMA (below)
   const int tid = threadIdx.x;
   const int ld_c = tid & 15, ld_r = tid >> 4;
-  u32x4 kreg[4], vreg[4];
+  u32x4 vreg[4];
   int vlive = 0;  // keys 4 ld_r .. 4 ld_r + 3 of the loaded chunk that lie inside the tile's range
   bool vlast = false;
-  auto load_chunk = [&](int c) {
+  // K by LDS DMA: transfer i of wave w takes rows 16 w + 4 i + lane / 16 whole, lane l
+  // fetching 16-byte unit (l % 16) ^ (row % 16) into position l % 16.  (Through
+  // registers and padded LDS rows, the prefill ran 614 against 594 us at config 2.)
+  uint32_t k_off[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int row = 16 * wave + 4 * i + (lane >> 4);
+    k_off[i] = (uint32_t)((int64_t)row * kv_stride * sizeof(T)) + 16u * (uint32_t)((lane & 15) ^ (row & 15));
+  }
+  auto load_chunk = [&](int c, uint8_t* stage) {
     const int k0 = c * kFaBk;
     const int64_t row0 = (int64_t)tab[k0 / bs] * bs + k0 % bs;
-    const T* kb = kc + row0 * kv_stride + (int64_t)kvh * kFaHd + ld_c * 8;
     const T* vb = vc + row0 * kv_stride + (int64_t)kvh * kFaHd + ld_c * 8;
+    {
+      const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
+          const_cast<T*>(kc + row0 * kv_stride + (int64_t)kvh * kFaHd), (short)0,
+          (int)(kFaBk * kv_stride * sizeof(T)), 0x00020000);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            rk, (__attribute__((address_space(3))) void*)(stage + (16 * wave + 4 * i) * kFaKRow), 16, k_off[i], 0, 0, 0);
+    }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      kreg[i] = ld16(kb + (int64_t)(ld_r + 16 * i) * kv_stride);
       // The row lies inside the chunk's block, so the load is unconditional.
       vreg[i] = ld16(vb + (int64_t)(4 * ld_r + i) * kv_stride);
     }
@@ -207,8 +226,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
       for (int i = 0; i < 4; ++i)
         if (i >= vlive) vreg[i] = u32x4{0, 0, 0, 0};
     }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) st16(st + (ld_r + 16 * i) * kFaKRow + ld_c * 16, kreg[i]);
     // V^T: dim 8 ld_c + e, keys 4 ld_r .. 4 ld_r + 3 -> 8 bytes, at key group
     // ld_r ^ ((row >> 4) & 7) of row 8 ld_c + e (the swizzle below)
     uint8_t* vt = st + kFaKBytes + 8 * (ld_r ^ ((ld_c >> 1) & 7));
@@ -242,9 +259,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
     c1 = min(c1, c0 + split_keys / kFaBk);
   }
   if (c0 < c1) {
-    load_chunk(c0);
+    load_chunk(c0, lds);
     store_chunk(lds);
   }
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the K transfers are in LDS
   __syncthreads();
   for (int c = c0; c < c1; ++c) {
     const uint8_t* buf = lds + ((c - c0) & 1) * kFaStage;
@@ -255,10 +273,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
     for (int s = 0; s < kFaHd / 16; ++s)
 #pragma unroll
       for (int kt = 0; kt < 2; ++kt) {
-        const v8 a = __builtin_bit_cast(v8, ld16(buf + (32 * kt + (lane & 31)) * kFaKRow + (16 * s + 8 * half) * 2));
+        const int kr = 32 * kt + (lane & 31), ku = 2 * s + half;  // K row, 16-byte unit
+        const v8 a = __builtin_bit_cast(v8, ld16(buf + kr * kFaKRow + 16 * (ku ^ (kr & 15))));
         st[kt] = M::mma(a, qf[s], st[kt]);
       }
-    if (c + 1 < c1) load_chunk(c + 1);  // in flight during the softmax and O^T += V^T . P^T
+    if (c + 1 < c1) load_chunk(c + 1, lds + ((c + 1 - c0) & 1) * kFaStage);  // in flight during the softmax and PV
     // online softmax for this lane's query; element j of tile kt is key
     // c*64 + 32 kt + 8 (j/4) + 4 half + j%4.  The running max m is kept in
     // exp2 units (score * scale_log2); since scale_log2 > 0 and rounding is
@@ -342,6 +361,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
           }
         }
     if (c + 1 < c1) store_chunk(lds + ((c + 1 - c0) & 1) * kFaStage);
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the K transfers are in LDS
     __syncthreads();
   }
 
