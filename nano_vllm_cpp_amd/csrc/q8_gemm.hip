@@ -368,9 +368,10 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(3)
 // Decode-shaped product (m <= kGemvMaxM rows): bound by streaming the weights
 // once from HBM, so the layout serves the loads.
 //
-// A wave owns 16 weight columns and a contiguous range of K; S waves of a
-// workgroup share a column group (splitting K) and meet in LDS at the end,
-// summed in split order; a workgroup holds 4 / S column groups.  The weights go
+// A wave owns 16 weight columns (or 32: CG = 2 groups of 16 sharing each
+// activation fragment) and a contiguous range of K; S waves of a workgroup
+// share a column group (splitting K) and meet in LDS at the end, summed in split
+// order; a workgroup holds W / S column groups.  The weights go
 // HBM -> LDS by DMA in 256-byte runs per column (one 1 KB transfer = 4 columns x
 // 256 B, the K offset in the scalar offset, so a stage costs no VALU), into a
 // wave-private double buffer: the next stage is in flight while the current one
@@ -400,8 +401,8 @@ constexpr int kGemvScaleLds = 32768;              // bytes of LDS for the staged
 constexpr int kGemvXLdsMax = 65536;               // bytes of LDS for staged activation rows
 constexpr int64_t kLdsPerCu = 160 * 1024;
 
-template <int W, int S>
-constexpr int gemv_cols() { return W / S * 16; }  // columns per workgroup of W waves
+template <int W, int S, int CG = 1>
+constexpr int gemv_cols() { return W / S * 16 * CG; }  // columns per workgroup of W waves
 
 // XF (fused activation quantizer, needs XL): the m rows arrive as 16-bit or fp32
 // activations in TO (xf, row stride xf_ld elements) instead of int8 rows + scales;
@@ -422,7 +423,19 @@ constexpr int gemv_cols() { return W / S * 16; }  // columns per workgroup of W 
 // so lane (j, q) applies one scale, block 2 p + q / 2 of column j, and the two halves
 // of a row meet in the final sum.  Half the MFMAs and half the applies of the
 // two-MFMA form, none of them on padding rows.
-template <typename TO, int W, int S, bool XL, int XF = 0, bool H8 = false>
+// vmcnt(4 CG): every load but the last weight stage's 4 CG transfers
+template <int CG>
+__device__ __forceinline__ void gemv_wait_but_stage() {
+  static_assert(CG == 1 || CG == 2, "one or two column groups per wave");
+  if constexpr (CG == 2)
+    __builtin_amdgcn_s_waitcnt(0x0F78);
+  else
+    __builtin_amdgcn_s_waitcnt(0x0F74);
+}
+
+// CG: 16-column groups per wave (2: each activation fragment feeds two MFMAs, half
+// the activation loads per weight byte).
+template <typename TO, int W, int S, bool XL, int XF = 0, bool H8 = false, int CG = 1>
 __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(2))) void q8_gemv_kernel(const int8_t* __restrict__ xq,
                                                          const float* __restrict__ rscale,
                                                          const int8_t* __restrict__ w8,
@@ -433,8 +446,9 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(2))) voi
                                                          TO* __restrict__ xres_out = nullptr,
                                                          const TO* __restrict__ xg = nullptr, float eps = 0.0f) {
   static_assert(XF == 0 || XL, "the fused quantizer writes the staged LDS rows");
-  constexpr int kCols = gemv_cols<W, S>();
-  constexpr int kGvDmaLds = W * 2 * kGvWaveBuf;
+  constexpr int kCols = gemv_cols<W, S, CG>();
+  constexpr int kWaveBuf = CG * kGvWaveBuf;  // one stage of one wave's columns
+  constexpr int kGvDmaLds = W * 2 * kWaveBuf;
   // [DMA buffers][scales][activation rows (XL)]; after the loop each wave's partial
   // sums reuse its own DMA buffers
   extern __shared__ __attribute__((aligned(16))) uint8_t dyn[];
@@ -454,31 +468,34 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(2))) voi
   float* xf_ss = xf_scale + kGemvMaxM;  // XF 3: [row][sub-wave] sums of squares
   const int64_t xrow = k + 16;  // LDS bytes per staged activation row
 
-  const int64_t c0 = wg_c0 + (int64_t)grp * 16;  // this wave's first column
-  const int64_t cols = n - c0 < 16 ? n - c0 : 16;
+  const int64_t c0 = wg_c0 + (int64_t)grp * 16 * CG;  // this wave's first column
+  const int64_t cols = n - c0 < 16 * CG ? n - c0 : 16 * CG;
   const int64_t p_begin = npairs * split / S, p_end = npairs * (split + 1) / S;
   const bool active = cols > 0 && p_end > p_begin;  // uniform per wave
-  float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  float acc[CG][4] = {};
 
   // rows past m / columns past n fall outside these resources and read zero
   const __amdgpu_buffer_rsrc_t rw = make_rsrc(w8 + (active ? c0 * k : 0), active ? cols * k : 0);
   const __amdgpu_buffer_rsrc_t rx = make_rsrc(xq, m * k);
-  uint8_t* wbuf = dyn + wave * 2 * kGvWaveBuf;
+  uint8_t* wbuf = dyn + wave * 2 * kWaveBuf;
   // DMA lane l of transfer i: column 4 i + l / 16, LDS position l % 16, fetching chunk (l % 16) ^ column
-  uint32_t dma_off[4];
+  // (loop bounds that do not depend on CG: the host compilation pass otherwise
+  // drops the kernel's instantiation, and its launch stub, without a diagnostic)
+  uint32_t dma_off[8];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+  for (int i = 0; i < 8; ++i) {
     const int col = 4 * i + (lane >> 4);
-    dma_off[i] = (uint32_t)(col * k) + 16u * (uint32_t)((lane & 15) ^ col);
+    dma_off[i] = (uint32_t)(col * k) + 16u * (uint32_t)((lane & 15) ^ (col & 15));
   }
   const int64_t kb0 = 64 * p_begin;
   const int nst = (int)((p_end - p_begin + 3) / 4);
   auto issue = [&](int st) {
-    uint8_t* dst = wbuf + (st & 1) * kGvWaveBuf;
+    uint8_t* dst = wbuf + (st & 1) * kWaveBuf;
     const uint32_t soff = (uint32_t)(kb0 + (int64_t)st * kGvKC);
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (__attribute__((address_space(3))) void*)(dst + i * 1024), 16,
+    for (int i = 0; i < 8; ++i)
+      if (i < 4 * CG)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (__attribute__((address_space(3))) void*)(dst + i * 1024), 16,
                                                dma_off[i], soff, 0, kNt);
   };
   const int xr = H8 ? (j & 7) : j;                          // the activation row lane (j, q) holds
@@ -585,7 +602,7 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(2))) voi
       if (nst > 1) issue(1);
     }
     if (active && nst > 1)
-      __builtin_amdgcn_s_waitcnt(0x0F74);  // vmcnt(4): all but weight stage 1
+      gemv_wait_but_stage<CG>();  // all but weight stage 1
     else
       __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
     if constexpr (!XL) {
@@ -787,7 +804,7 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(2))) voi
   }
 
   if (active) {
-    const uint16_t* sc_col = sc_lds + ((int64_t)grp * 16 + j) * nblk;
+    const uint16_t* sc_col = sc_lds + ((int64_t)grp * 16 * CG + j) * nblk;  // (+ 16 nblk per group)
     // XL: lane (j, q) reads row xr (rows past m, and under H8 the other block's
     // lanes, hold zero: the address is clamped to row 0 and the value selected away)
     const bool x_row_ok = xr < m && x_half_ok;
@@ -804,50 +821,59 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(2))) voi
       }
       const int64_t pst = p_begin + 4 * st;
       const int npp = p_end - pst < 4 ? (int)(p_end - pst) : 4;
-      const uint8_t* src = wbuf + (st & 1) * kGvWaveBuf + j * kGvKC;
+      const uint8_t* src = wbuf + (st & 1) * kWaveBuf + j * kGvKC;
       // one block pair: operands from LDS (or registers), then its MFMA(s) and applies
       struct Operands {
-        i32x4 wv, x;
-        float s_lo, s_hi;
+        i32x4 wv[CG], x;
+        float s_lo[CG], s_hi[CG];
       };
       auto fetch = [&](int pp) {
         const int64_t p = pst + pp;
         const int64_t b = 2 * p;
         Operands o;
-        o.wv = *reinterpret_cast<const i32x4*>(src + 16 * ((4 * pp + q) ^ j));
+#pragma unroll
+        for (int g = 0; g < CG; ++g)
+          o.wv[g] = *reinterpret_cast<const i32x4*>(src + g * 16 * kGvKC + 16 * ((4 * pp + q) ^ j));
         if constexpr (XL) {
           const i32x4 xl = *reinterpret_cast<const i32x4*>(x_src + 64 * p);
           o.x = x_row_ok && 64 * p + 16 * q < k ? xl : i32x4{0, 0, 0, 0};
         } else {
           o.x = xc[pp];
         }
-        if constexpr (H8) {  // this lane's block: b or b + 1 (scale 0 past the last block)
-          const int64_t bq = b + (q >> 1);
-          const float sv = fp16_bits_to_float(sc_col[bq < nblk ? bq : b]);  // read unconditionally
-          o.s_lo = bq < nblk ? sv : 0.0f;
-          o.s_hi = 0.0f;
-        } else {
-          o.s_lo = fp16_bits_to_float(sc_col[b]);
-          const float s1 = fp16_bits_to_float(sc_col[b + 1 < nblk ? b + 1 : b]);  // read unconditionally
-          o.s_hi = b + 1 < nblk ? s1 : 0.0f;
+#pragma unroll
+        for (int g = 0; g < CG; ++g) {
+          const uint16_t* scg = sc_col + g * 16 * nblk;
+          if constexpr (H8) {  // this lane's block: b or b + 1 (scale 0 past the last block)
+            const int64_t bq = b + (q >> 1);
+            const float sv = fp16_bits_to_float(scg[bq < nblk ? bq : b]);  // read unconditionally
+            o.s_lo[g] = bq < nblk ? sv : 0.0f;
+            o.s_hi[g] = 0.0f;
+          } else {
+            o.s_lo[g] = fp16_bits_to_float(scg[b]);
+            const float s1 = fp16_bits_to_float(scg[b + 1 < nblk ? b + 1 : b]);  // read unconditionally
+            o.s_hi[g] = b + 1 < nblk ? s1 : 0.0f;
+          }
         }
         return o;
       };
       auto apply = [&](const Operands& o) {
         const i32x4 z = {0, 0, 0, 0};
-        if constexpr (H8) {
-          const i32x4 d = __builtin_amdgcn_mfma_i32_16x16x64_i8(o.x, o.wv, z, 0, 0, 0);
 #pragma unroll
-          for (int v = 0; v < 4; ++v) acc[v] = fmaf(o.s_lo, (float)d[v], acc[v]);
-        } else {
-          const i32x4 x_lo = q < 2 ? o.x : z;  // first block of the pair
-          const i32x4 x_hi = q < 2 ? z : o.x;  // second block
-          const i32x4 d_lo = __builtin_amdgcn_mfma_i32_16x16x64_i8(x_lo, o.wv, z, 0, 0, 0);
-          const i32x4 d_hi = __builtin_amdgcn_mfma_i32_16x16x64_i8(x_hi, o.wv, z, 0, 0, 0);
+        for (int g = 0; g < CG; ++g) {
+          if constexpr (H8) {
+            const i32x4 d = __builtin_amdgcn_mfma_i32_16x16x64_i8(o.x, o.wv[g], z, 0, 0, 0);
 #pragma unroll
-          for (int v = 0; v < 4; ++v) {
-            acc[v] = fmaf(o.s_lo, (float)d_lo[v], acc[v]);
-            acc[v] = fmaf(o.s_hi, (float)d_hi[v], acc[v]);
+            for (int v = 0; v < 4; ++v) acc[g][v] = fmaf(o.s_lo[g], (float)d[v], acc[g][v]);
+          } else {
+            const i32x4 x_lo = q < 2 ? o.x : z;  // first block of the pair
+            const i32x4 x_hi = q < 2 ? z : o.x;  // second block
+            const i32x4 d_lo = __builtin_amdgcn_mfma_i32_16x16x64_i8(x_lo, o.wv[g], z, 0, 0, 0);
+            const i32x4 d_hi = __builtin_amdgcn_mfma_i32_16x16x64_i8(x_hi, o.wv[g], z, 0, 0, 0);
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+              acc[g][v] = fmaf(o.s_lo[g], (float)d_lo[v], acc[g][v]);
+              acc[g][v] = fmaf(o.s_hi[g], (float)d_hi[v], acc[g][v]);
+            }
           }
         }
       };
@@ -868,7 +894,7 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(2))) voi
         // and its register activations
         if (st + 2 < nst) {
           issue(st + 2);
-          __builtin_amdgcn_s_waitcnt(0x0F74);
+          gemv_wait_but_stage<CG>();
         } else {
           __builtin_amdgcn_s_waitcnt(0x0F70);
         }
@@ -881,24 +907,26 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(2))) voi
     }
   }
   // D layout of v_mfma_*_16x16: lane l, value v -> column l % 16, row 4 * (l / 16) + v.
-  // Partial sums [wave][16 rows][17] in the wave's own DMA buffers (all its
-  // transfers completed at its last vmcnt wait).
-  auto part = [&](int w, int r, int c) -> float& {
-    return reinterpret_cast<float*>(dyn + w * 2 * kGvWaveBuf)[r * 17 + c];
+  // Partial sums [wave][column group][16 rows][17] in the wave's own DMA buffers
+  // (all its transfers completed at its last vmcnt wait).
+  auto part = [&](int w, int cg, int r, int c) -> float& {
+    return reinterpret_cast<float*>(dyn + w * 2 * kWaveBuf)[(cg * 16 + r) * 17 + c];
   };
 #pragma unroll
-  for (int v = 0; v < 4; ++v) part(wave, 4 * q + v, j) = acc[v];
+  for (int g = 0; g < CG; ++g)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) part(wave, g, 4 * q + v, j) = acc[g][v];
   __syncthreads();
   for (int o = threadIdx.x; o < kCols * 16; o += W * 64) {
     const int c = o % kCols, r = o / kCols;  // consecutive threads -> consecutive columns
-    const int g = c / 16, cj = c % 16;
+    const int g = c / (16 * CG), cg = (c / 16) % CG, cj = c % 16;
     const int64_t col = wg_c0 + c;
     if (r < m && col < n) {
       float sum = 0.0f;
 #pragma unroll
       for (int sp = 0; sp < S; ++sp) {
-        sum += part(g * S + sp, r, cj);
-        if constexpr (H8) sum += part(g * S + sp, r + 8, cj);  // the pairs' second blocks
+        sum += part(g * S + sp, cg, r, cj);
+        if constexpr (H8) sum += part(g * S + sp, cg, r + 8, cj);  // the pairs' second blocks
       }
       const float sc = XF != 0 ? xf_scale[r] : rscale[r];
       const float inv = sc > 0.0f ? 1.0f / sc : 0.0f;  // the reference's adq (:358)
@@ -910,11 +938,11 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(2))) voi
 // Launches the GEMV with W waves per workgroup and K split S; false if the
 // staged scales would not fit.  The activation rows go to LDS (XL) when they fit
 // and cost no resident workgroups the launch can use.
-template <typename TO, int W, int S>
+template <typename TO, int W, int S, int CG = 1>
 bool try_gemv(const int8_t* xq, const float* rscale, const int8_t* w8, const uint16_t* ws, TO* out, int64_t m,
               int64_t n, int64_t k, hipStream_t stream) {
-  constexpr int kCols = gemv_cols<W, S>();
-  constexpr int kDma = W * 2 * kGvWaveBuf;
+  constexpr int kCols = gemv_cols<W, S, CG>();
+  constexpr int kDma = W * 2 * kGvWaveBuf * CG;
   const int64_t sc_bytes = (kCols * (k / 32) * 2 + 15) & ~15;
   if (sc_bytes > kGemvScaleLds) return false;
   const int64_t x_bytes = m * (k + 16);
@@ -933,28 +961,28 @@ bool try_gemv(const int8_t* xq, const float* rscale, const int8_t* w8, const uin
   std::call_once(attr_once, [] {
     const int lds_reg = kDma + kGemvScaleLds;
     const int lds_xl = (int)std::min<int64_t>(kLdsPerCu, kDma + kGemvScaleLds + kGemvXLdsMax);
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&q8_gemv_kernel<TO, W, S, false, 0, false>),
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&q8_gemv_kernel<TO, W, S, false, 0, false, CG>),
                               hipFuncAttributeMaxDynamicSharedMemorySize, lds_reg);
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&q8_gemv_kernel<TO, W, S, false, 0, true>),
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&q8_gemv_kernel<TO, W, S, false, 0, true, CG>),
                               hipFuncAttributeMaxDynamicSharedMemorySize, lds_reg);
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&q8_gemv_kernel<TO, W, S, true, 0, false>),
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&q8_gemv_kernel<TO, W, S, true, 0, false, CG>),
                               hipFuncAttributeMaxDynamicSharedMemorySize, lds_xl);
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&q8_gemv_kernel<TO, W, S, true, 0, true>),
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&q8_gemv_kernel<TO, W, S, true, 0, true, CG>),
                               hipFuncAttributeMaxDynamicSharedMemorySize, lds_xl);
   });
   const dim3 grid((unsigned)wgs), block(W * 64);
   const bool h8 = m <= 8;
   if (xl && h8)
-    q8_gemv_kernel<TO, W, S, true, 0, true><<<grid, block, (size_t)lds_x, stream>>>(xq, rscale, w8, ws, out, m, n,
+    q8_gemv_kernel<TO, W, S, true, 0, true, CG><<<grid, block, (size_t)lds_x, stream>>>(xq, rscale, w8, ws, out, m, n,
                                                                                    k, (int)sc_bytes);
   else if (xl)
-    q8_gemv_kernel<TO, W, S, true, 0, false><<<grid, block, (size_t)lds_x, stream>>>(xq, rscale, w8, ws, out, m, n,
+    q8_gemv_kernel<TO, W, S, true, 0, false, CG><<<grid, block, (size_t)lds_x, stream>>>(xq, rscale, w8, ws, out, m, n,
                                                                                     k, (int)sc_bytes);
   else if (h8)
-    q8_gemv_kernel<TO, W, S, false, 0, true><<<grid, block, (size_t)lds_r, stream>>>(xq, rscale, w8, ws, out, m, n,
+    q8_gemv_kernel<TO, W, S, false, 0, true, CG><<<grid, block, (size_t)lds_r, stream>>>(xq, rscale, w8, ws, out, m, n,
                                                                                     k, (int)sc_bytes);
   else
-    q8_gemv_kernel<TO, W, S, false, 0, false><<<grid, block, (size_t)lds_r, stream>>>(xq, rscale, w8, ws, out, m, n,
+    q8_gemv_kernel<TO, W, S, false, 0, false, CG><<<grid, block, (size_t)lds_r, stream>>>(xq, rscale, w8, ws, out, m, n,
                                                                                      k, (int)sc_bytes);
   return true;
 }
@@ -1090,7 +1118,10 @@ int launch_gemm(const int8_t* xq, const float* rscale, const int8_t* w8, const u
     // when the staged scales of a wider column set would not fit
     const int64_t groups = (n + 15) / 16;
     bool ok = false;
-    if (groups >= 2048) ok = try_gemv<TO, 4, 1>(xq, rscale, w8, ws, out, m, n, k, stream);
+    // (wide outputs: 2 waves of 32 columns each, so one activation fragment feeds two
+    // MFMAs; measured at the gate_up shape, m = 8: 28.5 against 30.8 us for 4 waves of
+    // 16 columns and 30.3 us for 1 wave of 64)
+    if (groups >= 2048) ok = try_gemv<TO, 2, 1, 2>(xq, rscale, w8, ws, out, m, n, k, stream);
     if (!ok && groups >= 1024) ok = try_gemv<TO, 4, 2>(xq, rscale, w8, ws, out, m, n, k, stream);
     if (!ok && groups >= 512) ok = try_gemv<TO, 4, 4>(xq, rscale, w8, ws, out, m, n, k, stream);
     if (!ok) ok = try_gemv<TO, 8, 8>(xq, rscale, w8, ws, out, m, n, k, stream);

@@ -83,8 +83,11 @@ def test_quantize_rows_bitexact(gpu, dt, m, k):
                                    # decode GEMV: batch-1 qkv (activation rows staged in LDS) and a wide output
                                    # whose staged rows would cost resident workgroups (register activations)
                                    (1, 4608, 3584), (8, 20000, 3584),
-                                   # fewer column groups than CUs, long K: 16 waves per column group
-                                   (12, 1000, 9216)])
+                                   # fewer column groups than CUs, long K
+                                   (12, 1000, 9216),
+                                   # at least 2048 column groups: waves of two 16-column groups
+                                   # (the last one partial)
+                                   (3, 33000, 512), (12, 32784, 256)])
 def test_matmul_q8_0_vs_oracle(gpu, out_dt, m, n, k):
     x, w8, ws = make(m + 3 * n + k + out_dt, m, n, k, H.F32)
     zero_row = 2 if m > 2 else None
