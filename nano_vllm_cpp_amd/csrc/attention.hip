@@ -732,22 +732,23 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
     // order itself (key count descending, ties by token), dealt as
     // nvf_decode_token_order deals it (slot ti holds rank r * 8 + x, x reversed on
     // odd full rounds r of 8).  Every thread ranks its candidates against all
-    // counts, staged in LDS; the one whose rank is the slot's names it.
+    // counts, staged in LDS as one distinct 64-bit key per token (the count above
+    // the complemented index: a larger key ranks first, ties by token), so a
+    // comparison is one compare; the one whose rank is the slot's names it.
     __shared__ int32_t sel;
-    int32_t* lens = reinterpret_cast<int32_t*>(lds);
+    int64_t* keys = reinterpret_cast<int64_t*>(lds);
     const int n = (int)tokens;
-    for (int i = threadIdx.x; i < n; i += 256) lens[i] = qlen[i];
-    for (int i = n + threadIdx.x; i < ((n + 3) & ~3); i += 256) lens[i] = INT32_MIN;  // pads rank below all
+    for (int i = threadIdx.x; i < n; i += 256) keys[i] = (int64_t)qlen[i] * 4294967296LL + (int64_t)(uint32_t)~i;
+    for (int i = n + threadIdx.x; i < ((n + 1) & ~1); i += 256) keys[i] = INT64_MIN;  // pads rank below all
     __syncthreads();
     const int64_t rr = ti / 8, rx = ti % 8;
     const int64_t want = rr * 8 + ((rr & 1) && rr * 8 + 8 <= tokens ? 7 - rx : rx);
     for (int i = threadIdx.x; i < n; i += 256) {
-      const int32_t li = lens[i];
+      const int64_t ki = keys[i];
       int rank = 0;
-      for (int j4 = 0; j4 < n; j4 += 4) {
-        const int4 lj = *reinterpret_cast<const int4*>(lens + j4);
-        rank += (lj.x > li || (lj.x == li && j4 < i)) + (lj.y > li || (lj.y == li && j4 + 1 < i)) +
-                (lj.z > li || (lj.z == li && j4 + 2 < i)) + (lj.w > li || (lj.w == li && j4 + 3 < i));
+      for (int j2 = 0; j2 < n; j2 += 2) {
+        const longlong2 kj = *reinterpret_cast<const longlong2*>(keys + j2);
+        rank += (kj.x > ki) + (kj.y > ki);
       }
       if (rank == want) sel = i;
     }
