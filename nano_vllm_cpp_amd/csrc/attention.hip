@@ -79,7 +79,7 @@ __global__ __launch_bounds__(256) void store_kv_generic_kernel(const T* __restri
 //   online softmax per query -- a query is a lane column of S^T, so its max,
 //                    sum and the O rescale are lane-local plus one swap with the
 //                    other lane half
-//   O^T += V^T . P^T (dims x queries: A = V^T from LDS, stored transposed; B = P^T,
+//   O^T += V^T . P^T (dims x queries: A = V^T by transpose reads of V's LDS rows; B = P^T,
 //                    which is S^T's own register layout: the 8 values a lane
 //                    holds for keys 16u + 4h + {0..3, 8..11} are its B operand
 //                    for key step u once both operands index keys that way)
@@ -93,9 +93,10 @@ constexpr float kFaLazy = 8.0f;                  // exp2 units the running max m
 // K row in LDS, written by DMA: unpadded, its 16-byte units swizzled by row
 // (conflict-free 16 B reads)
 constexpr int kFaKRow = kFaHd * 2;
-constexpr int kFaVRow = kFaBk * 2 + 8;           // V^T row in LDS, padded
 constexpr int kFaKBytes = kFaBk * kFaKRow;
-constexpr int kFaStage = kFaKBytes + kFaHd * kFaVRow;
+// V rows in LDS, written by DMA as K's: unpadded, 16-byte unit u of key row r at
+// position u ^ 4 (r % 4), read transposed (ds_read_b64_tr_b16) into the MFMA operand
+constexpr int kFaStage = 2 * kFaKBytes;
 constexpr int kFaLds = 2 * kFaStage;
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
@@ -180,72 +181,60 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
     qf[s] = __builtin_bit_cast(v8, v);
   }
 
-  // chunk loads: V keys 4 (tid/16) + e, dims 8 (tid%16) into registers (transposed on
-  // the way to LDS); K by DMA (below)
-  const int tid = threadIdx.x;
-  const int ld_c = tid & 15, ld_r = tid >> 4;
-  u32x4 vreg[4];
-  int vlive = 0;  // keys 4 ld_r .. 4 ld_r + 3 of the loaded chunk that lie inside the tile's range
-  bool vlast = false;
-  // K by LDS DMA: transfer i of wave w takes rows 16 w + 4 i + lane / 16 whole, lane l
-  // fetching 16-byte unit (l % 16) ^ (row % 16) into position l % 16.  (Through
-  // registers and padded LDS rows, the prefill ran 614 against 594 us at config 2.)
-  uint32_t k_off[4];
+  // K and V by LDS DMA: transfer i of wave w takes key rows 16 w + 4 i + lane / 16
+  // whole, lane l fetching the 16-byte unit that belongs at position l % 16: for K
+  // unit (l % 16) ^ (row % 16), for V unit (l % 16) ^ 4 (row % 4).  (Through
+  // registers and padded LDS rows, K ran 614 against 594 us at config 2.)  Keys
+  // past the tile's range may hold anything: V's resource ends at the range, so
+  // those rows arrive as zeros (their p is 0, and 0 * NaN would not be); K's are
+  // masked in the scores.
+  uint32_t k_off[4], v_off[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int row = 16 * wave + 4 * i + (lane >> 4);
-    k_off[i] = (uint32_t)((int64_t)row * kv_stride * sizeof(T)) + 16u * (uint32_t)((lane & 15) ^ (row & 15));
+    const uint32_t rb = (uint32_t)((int64_t)row * kv_stride * sizeof(T));
+    k_off[i] = rb + 16u * (uint32_t)((lane & 15) ^ (row & 15));
+    v_off[i] = rb + 16u * (uint32_t)((lane & 15) ^ (4 * (row & 3)));
   }
   auto load_chunk = [&](int c, uint8_t* stage) {
     const int k0 = c * kFaBk;
     const int64_t row0 = (int64_t)tab[k0 / bs] * bs + k0 % bs;
-    const T* vb = vc + row0 * kv_stride + (int64_t)kvh * kFaHd + ld_c * 8;
-    {
-      const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
-          const_cast<T*>(kc + row0 * kv_stride + (int64_t)kvh * kFaHd), (short)0,
-          (int)(kFaBk * kv_stride * sizeof(T)), 0x00020000);
+    const int64_t head = row0 * kv_stride + (int64_t)kvh * kFaHd;
+    const int vrows = Lmax - k0 < kFaBk ? Lmax - k0 : kFaBk;
+    const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<T*>(kc + head), (short)0, (int)(kFaBk * kv_stride * sizeof(T)), 0x00020000);
+    const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<T*>(vc + head), (short)0, (int)(vrows * kv_stride * sizeof(T)), 0x00020000);
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            rk, (__attribute__((address_space(3))) void*)(stage + (16 * wave + 4 * i) * kFaKRow), 16, k_off[i], 0, 0, 0);
-    }
+    for (int i = 0; i < 4; ++i)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rk, (__attribute__((address_space(3))) void*)(stage + (16 * wave + 4 * i) * kFaKRow), 16, k_off[i], 0, 0, 0);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      // The row lies inside the chunk's block, so the load is unconditional.
-      vreg[i] = ld16(vb + (int64_t)(4 * ld_r + i) * kv_stride);
-    }
-    vlive = Lmax - k0 - 4 * ld_r;
-    vlast = k0 + kFaBk > Lmax;
-  };
-  auto store_chunk = [&](uint8_t* st) {
-    // keys past the tile's range may hold anything: zero their V (their p is 0).  The
-    // select happens here, when the chunk goes to LDS, and not after the loads: a use
-    // of the loaded registers right after issuing them would wait for the loads there.
-    if (vlast) {  // wave-uniform: only the tile's last chunk can reach past its range
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        if (i >= vlive) vreg[i] = u32x4{0, 0, 0, 0};
-    }
-    // V^T: dim 8 ld_c + e, keys 4 ld_r .. 4 ld_r + 3 -> 8 bytes, at key group
-    // ld_r ^ ((row >> 4) & 7) of row 8 ld_c + e (the swizzle below)
-    uint8_t* vt = st + kFaKBytes + 8 * (ld_r ^ ((ld_c >> 1) & 7));
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      // the 16-bit values of two keys into one dword by a byte permute
-      const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;  // high or low halves of (b, a)
-      const uint32_t lo = __builtin_amdgcn_perm(vreg[1][e >> 1], vreg[0][e >> 1], sel);
-      const uint32_t hi = __builtin_amdgcn_perm(vreg[3][e >> 1], vreg[2][e >> 1], sel);
-      typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-      *reinterpret_cast<u32x2*>(vt + (8 * ld_c + e) * kFaVRow) = u32x2{lo, hi};
-    }
+    for (int i = 0; i < 4; ++i)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rv, (__attribute__((address_space(3))) void*)(stage + kFaKBytes + (16 * wave + 4 * i) * kFaKRow), 16,
+          v_off[i], 0, 0, 0);
   };
 
-  // V^T in LDS: row r (a dimension) holds 16 groups of 4 keys, group g stored at
-  // position g ^ ((r >> 4) & 7).  The 16 lanes of a write phase (rows 8 apart)
-  // and of a read phase (16 consecutive rows) then each cover all 32 banks.  For
-  // a read of row 32 d + (lane & 31), group g0 + half (g0 even), the position is
-  // (g0 ^ 2d) + (half ^ ((lane >> 4) & 1)): a constant plus this lane offset.
-  const int vt_lane = 8 * (half ^ ((lane >> 4) & 1));
+  // The PV operand by transpose reads.  ds_read_b64_tr_b16 over a 16-lane group:
+  // lane i receives, as its element e, 16-bit element i % 4 of the 8 bytes that
+  // lane 4 e + i / 4 addresses.  So when lane s of the group addresses key row
+  // key0 + s / 4, dims dim0 + 4 (s % 4) .. + 3, lane i receives dim dim0 + i of
+  // keys key0 .. key0 + 3: the A operand (row = dim, k = key) of the 32x32x16 MFMA.
+  // Lane l: dims 32 d + 16 ((l >> 4) & 1) + 4 (s % 4), keys 4 half + s / 4 (+ 8 for
+  // the operand's second half) past the key step's first, s = l % 16.  Its 16-byte
+  // unit 4 d + 2 ((l >> 4) & 1) + (s % 4) / 2 sits at that ^ 4 (key % 4) = ^ 4 (s / 4):
+  // a lane base per d; the key step and the half are row offsets.  Each 32-lane half
+  // of a read covers 4 keys x 4 units, at 16 distinct positions of one 256-byte row
+  // span: no bank conflicts.
+  uint32_t v_lane[kFaHd / 32];
+  {
+    const int s16 = lane & 15, g16 = (lane >> 4) & 1;
+#pragma unroll
+    for (int d = 0; d < kFaHd / 32; ++d)
+      v_lane[d] = (uint32_t)((4 * half + s16 / 4) * kFaKRow + 16 * ((4 * d + 2 * g16 + (s16 & 3) / 2) ^ (4 * (s16 / 4))) +
+                             8 * (s16 & 1));
+  }
 
   f32x16 o[kFaHd / 32];
 #pragma unroll
@@ -258,10 +247,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
     c0 = (int)blockIdx.z * (split_keys / kFaBk);
     c1 = min(c1, c0 + split_keys / kFaBk);
   }
-  if (c0 < c1) {
-    load_chunk(c0, lds);
-    store_chunk(lds);
-  }
+  if (c0 < c1) load_chunk(c0, lds);
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the K transfers are in LDS
   __syncthreads();
   for (int c = c0; c < c1; ++c) {
@@ -332,16 +318,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
     ls += __shfl_xor(ls, 32);
     l += ls;
     // O^T += V^T . P^T, key step u of tile kt: keys 32 kt + 16 u + 4 half + {0..3, 8..11},
-    // key groups g0 + half and g0 + 2 + half (g0 = 8 kt + 4 u) of row 32 d + (lane & 31)
-    // For odd d the swizzle puts the +8 key group at the lower address; those MFMAs take
-    // the groups in address order, (+8, +0), with P's halves swapped to match (the same
-    // contraction with its k order permuted), so the paired LDS read lands in operand order.
-    v8 pbx[2][2];
-#pragma unroll
-    for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-      for (int u = 0; u < 2; ++u) pbx[kt][u] = __builtin_shufflevector(pb[kt][u], pb[kt][u], 4, 5, 6, 7, 0, 1, 2, 3);
-    const uint8_t* vt = buf + kFaKBytes + vt_lane;
+    // P^T's keys, and V^T's by two transpose reads (+0 and +8 key rows)
+    const uint8_t* vt = buf + kFaKBytes;
     // (the four dim tiles' MFMA chains interleaved)
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt)
@@ -349,18 +327,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
       for (int u = 0; u < 2; ++u)
 #pragma unroll
         for (int d = 0; d < kFaHd / 32; ++d) {
-          typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-          const int g0 = 8 * kt + 4 * u;
-          const uint8_t* r = vt + (32 * d + (lane & 31)) * kFaVRow;
-          const u32x2 lo = *reinterpret_cast<const u32x2*>(r + 8 * (g0 ^ (2 * d)));
-          const u32x2 hi = *reinterpret_cast<const u32x2*>(r + 8 * ((g0 + 2) ^ (2 * d)));
-          if (d & 1) {
-            o[d] = M::mma(__builtin_bit_cast(v8, u32x4{hi[0], hi[1], lo[0], lo[1]}), pbx[kt][u], o[d]);
-          } else {
-            o[d] = M::mma(__builtin_bit_cast(v8, u32x4{lo[0], lo[1], hi[0], hi[1]}), pb[kt][u], o[d]);
-          }
+          typedef short s16x4 __attribute__((ext_vector_type(4)));
+          const uint8_t* r = vt + v_lane[d] + (32 * kt + 16 * u) * kFaKRow;
+          const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (__attribute__((address_space(3))) s16x4*)(r));
+          const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (__attribute__((address_space(3))) s16x4*)(r + 8 * kFaKRow));
+          o[d] = M::mma(__builtin_bit_cast(v8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7)), pb[kt][u],
+                        o[d]);
         }
-    if (c + 1 < c1) store_chunk(lds + ((c + 1 - c0) & 1) * kFaStage);
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the K transfers are in LDS
     __syncthreads();
   }
