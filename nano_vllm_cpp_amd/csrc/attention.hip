@@ -70,8 +70,10 @@ __global__ __launch_bounds__(256) void store_kv_generic_kernel(const T* __restri
 // sizes a multiple of 64 (the reference's are multiples of 256,
 // include/nanovllm/config.hpp:254).  A workgroup owns kFaBq = 128 consecutive
 // query tokens of one sequence and one query head (32 per wave) and walks the
-// keys in 64-key chunks staged in LDS (double-buffered, the next chunk's loads
-// in flight during the current chunk's math).
+// keys in 64-key chunks staged in LDS by DMA: K double-buffered (the next chunk's
+// K in flight during the softmax and PV), V single-buffered (the next chunk's V
+// in flight during S and the softmax; a second barrier per chunk guards it).  48
+// KiB of LDS and at most 168 VGPRs per wave: three workgroups per CU.
 //
 // Per wave and chunk, with 32x32x16 MFMAs:
 //   S^T = K . Q^T   (keys x queries: A = K rows from LDS, B = the wave's q rows,
@@ -96,8 +98,8 @@ constexpr int kFaKRow = kFaHd * 2;
 constexpr int kFaKBytes = kFaBk * kFaKRow;
 // V rows in LDS, written by DMA as K's: unpadded, 16-byte unit u of key row r at
 // position u ^ 4 (r % 4), read transposed (ds_read_b64_tr_b16) into the MFMA operand
-constexpr int kFaStage = 2 * kFaKBytes;
-constexpr int kFaLds = 2 * kFaStage;
+// [K chunk buffer 0][K chunk buffer 1][V chunk]: 48 KiB, three workgroups per CU
+constexpr int kFaLds = 3 * kFaKBytes;
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -135,7 +137,7 @@ __device__ __forceinline__ bool fa_tile_uniform(const int32_t* __restrict__ qseq
 }
 
 template <typename T, bool SPLIT>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void fa_prefill_kernel(
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void fa_prefill_kernel(
     const T* __restrict__ q, T* __restrict__ out, const T* __restrict__ kc, const T* __restrict__ vc,
     const int32_t* __restrict__ qseq, const int32_t* __restrict__ qlen, const int32_t* __restrict__ tables,
     int64_t tokens, int q_heads, int kv_heads, int bs, int max_blocks, float scale_log2, int64_t q_stride,
@@ -196,24 +198,28 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
     k_off[i] = rb + 16u * (uint32_t)((lane & 15) ^ (row & 15));
     v_off[i] = rb + 16u * (uint32_t)((lane & 15) ^ (4 * (row & 3)));
   }
-  auto load_chunk = [&](int c, uint8_t* stage) {
+  auto chunk_head = [&](int c) {
     const int k0 = c * kFaBk;
     const int64_t row0 = (int64_t)tab[k0 / bs] * bs + k0 % bs;
-    const int64_t head = row0 * kv_stride + (int64_t)kvh * kFaHd;
-    const int vrows = Lmax - k0 < kFaBk ? Lmax - k0 : kFaBk;
+    return row0 * kv_stride + (int64_t)kvh * kFaHd;
+  };
+  auto load_k = [&](int c, uint8_t* dst) {
     const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<T*>(kc + head), (short)0, (int)(kFaBk * kv_stride * sizeof(T)), 0x00020000);
+        const_cast<T*>(kc + chunk_head(c)), (short)0, (int)(kFaBk * kv_stride * sizeof(T)), 0x00020000);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rk, (__attribute__((address_space(3))) void*)(dst + (16 * wave + 4 * i) * kFaKRow), 16, k_off[i], 0, 0, 0);
+  };
+  auto load_v = [&](int c, uint8_t* dst) {
+    const int k0 = c * kFaBk;
+    const int vrows = Lmax - k0 < kFaBk ? Lmax - k0 : kFaBk;
     const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<T*>(vc + head), (short)0, (int)(vrows * kv_stride * sizeof(T)), 0x00020000);
+        const_cast<T*>(vc + chunk_head(c)), (short)0, (int)(vrows * kv_stride * sizeof(T)), 0x00020000);
 #pragma unroll
     for (int i = 0; i < 4; ++i)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          rk, (__attribute__((address_space(3))) void*)(stage + (16 * wave + 4 * i) * kFaKRow), 16, k_off[i], 0, 0, 0);
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          rv, (__attribute__((address_space(3))) void*)(stage + kFaKBytes + (16 * wave + 4 * i) * kFaKRow), 16,
-          v_off[i], 0, 0, 0);
+          rv, (__attribute__((address_space(3))) void*)(dst + (16 * wave + 4 * i) * kFaKRow), 16, v_off[i], 0, 0, 0);
   };
 
   // The PV operand by transpose reads.  ds_read_b64_tr_b16 over a 16-lane group:
@@ -247,11 +253,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
     c0 = (int)blockIdx.z * (split_keys / kFaBk);
     c1 = min(c1, c0 + split_keys / kFaBk);
   }
-  if (c0 < c1) load_chunk(c0, lds);
+  uint8_t* const vbuf = lds + 2 * kFaKBytes;
+  if (c0 < c1) {
+    load_k(c0, lds);
+    load_v(c0, vbuf);
+  }
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the K transfers are in LDS
   __syncthreads();
   for (int c = c0; c < c1; ++c) {
-    const uint8_t* buf = lds + ((c - c0) & 1) * kFaStage;
+    const uint8_t* buf = lds + ((c - c0) & 1) * kFaKBytes;
     // S^T = K . Q^T for keys [32 kt, 32 kt + 32)
     // (the two key tiles' MFMA chains interleaved: neither waits on its own accumulator)
     f32x16 st[2] = {f32x16{}, f32x16{}};
@@ -263,7 +273,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
         const v8 a = __builtin_bit_cast(v8, ld16(buf + kr * kFaKRow + 16 * (ku ^ (kr & 15))));
         st[kt] = M::mma(a, qf[s], st[kt]);
       }
-    if (c + 1 < c1) load_chunk(c + 1, lds + ((c + 1 - c0) & 1) * kFaStage);  // in flight during the softmax and PV
+    if (c + 1 < c1) load_k(c + 1, lds + ((c + 1 - c0) & 1) * kFaKBytes);  // in flight during the softmax and PV
     // online softmax for this lane's query; element j of tile kt is key
     // c*64 + 32 kt + 8 (j/4) + 4 half + j%4.  The running max m is kept in
     // exp2 units (score * scale_log2); since scale_log2 > 0 and rounding is
@@ -319,7 +329,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
     l += ls;
     // O^T += V^T . P^T, key step u of tile kt: keys 32 kt + 16 u + 4 half + {0..3, 8..11},
     // P^T's keys, and V^T's by two transpose reads (+0 and +8 key rows)
-    const uint8_t* vt = buf + kFaKBytes;
+    // V(c): issued after the previous chunk's second barrier, before K(c + 1).  (Bare
+    // barriers: a workgroup fence would add a vmcnt(0) and drain K(c + 1); the
+    // wavefront fences keep the compiler's LDS accesses on their side.)
+    if (c > c0) {
+      if (c + 1 < c1)
+        __builtin_amdgcn_s_waitcnt(0x0F74);  // vmcnt(4): all but K(c + 1)
+      else
+        __builtin_amdgcn_s_waitcnt(0x0F70);
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_s_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+    const uint8_t* vt = vbuf;
     // (the four dim tiles' MFMA chains interleaved)
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt)
@@ -336,8 +358,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
           o[d] = M::mma(__builtin_bit_cast(v8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7)), pb[kt][u],
                         o[d]);
         }
-    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the K transfers are in LDS
-    __syncthreads();
+    if (c + 1 < c1) {
+      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): K(c + 1) is in LDS
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_s_barrier();  // and every wave is done with V(c)
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      load_v(c + 1, vbuf);
+    }
   }
 
   // O^T layout: lane column = query, dims 32 d + 8 (j/4) + 4 half + j%4
