@@ -26,6 +26,7 @@
 //   * A hidden that is not a multiple of the block takes a per-element kernel
 //     (correct, not tuned).
 #include <atomic>
+#include <algorithm>
 #include <type_traits>
 
 #include "nvf_device.hpp"
@@ -115,15 +116,17 @@ static int launch_rows(const int64_t* ids, const Src& src, TO* out, int64_t toke
 
 // ---------------------------------------------------------------------------
 // LDS-staged row gather for block formats.  A wave copies its row's blocks
-// into LDS with coalesced 16-byte loads (from the 16-byte-aligned address at
-// or below the row's first block), then every lane decodes its own chunks of
-// N outputs out of LDS and stores them as before.  This turns the many small
-// per-chunk loads of the K-quant formats (header, nibbles, high bits, scales)
-// into a few full-width loads per lane (measured at Qwen2.5-7B shape: Q5_K
-// 57% -> 69%, Q6_K 50% -> 60%, Q8_0 blocks 65% -> 68%, Q4_K 74% -> 75% of the
-// 8 TB/s peak).  The stage starts at the 16-byte-aligned address at or below
-// the row and ends with the 16-byte granule holding the row's last byte, so
-// the few extra bytes read never leave those granules (no fault is possible).
+// into LDS by buffer loads straight to LDS, 16 bytes per lane (from the
+// 16-byte-aligned address at or below the row's first block), then every lane
+// decodes its own chunks of N outputs out of LDS and stores them as before.
+// This turns the many small per-chunk loads of the K-quant formats (header,
+// nibbles, high bits, scales) into a few full-width loads per lane (measured at
+// Qwen2.5-7B shape: Q5_K 57% -> 69%, Q6_K 50% -> 60%, Q8_0 blocks 65% -> 68%,
+// Q4_K 74% -> 75% of the 8 TB/s peak, staged through registers; the direct LDS
+// loads then took Q5_K 70-74% -> 77%).  The stage starts at the 16-byte-aligned
+// address at or below the row and ends with the 16-byte granule holding the
+// row's last byte; the buffer resource ends there too, so lanes past it read
+// zeros (into their own slice of the stage) and no fault is possible.
 // A format supplies
 //   kBlockBytes, kBlockElems, decode(const uint8_t* blk, int i, float* v)
 // reading the block from LDS (elements i .. i+N-1 of the block), and may supply
@@ -295,16 +298,14 @@ __global__ __launch_bounds__(kEmbThreads) void embed_rows_staged_kernel(const in
   const int delta = (int)(reinterpret_cast<uintptr_t>(row) - a16);
   const int n16 = (delta + (b1 - b0) * Fmt::kBlockBytes + 15) >> 4;
   uint8_t* my = stage + wave * stage_bytes;
-  u32x4 r[L16];
+  {  // LDS DMA over the stage's 16-byte chunks (lanes past them read zeros, inside the slice)
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(row - delta), (short)0, n16 * 16, 0x00020000);
 #pragma unroll
-  for (int u = 0; u < L16; ++u) {
-    const int c = u * kWave + lane;
-    if (c < n16) r[u] = ld16(row - delta + c * 16);  // (from row: a global load, not a flat one)
-  }
-#pragma unroll
-  for (int u = 0; u < L16; ++u) {
-    const int c = u * kWave + lane;
-    if (c < n16) *reinterpret_cast<u32x4*>(my + c * 16) = r[u];
+    for (int u = 0; u < L16; ++u)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)(my + u * kWave * 16), 16,
+                                               (uint32_t)(16 * lane), (uint32_t)(u * kWave * 16), 0, 0);
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
   }
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
@@ -345,12 +346,13 @@ static bool launch_staged(const int64_t* ids, const uint8_t* table, TO* out, int
   // 16-byte chunks of the larger part: ceil(nblk / 2) blocks plus the alignment lead
   const int64_t half_blocks = (hidden / Fmt::kBlockElems + parts - 1) / parts;
   const int64_t part_n16 = parts == 1 ? n16 : (15 + half_blocks * Fmt::kBlockBytes + 15) / 16;
-  const int stage_bytes = (int)(part_n16 * 16) + SpareBytes<Fmt>::value;
+  const int l16 = (int)((part_n16 + kWave - 1) / kWave);
+  int stage_bytes = (int)(part_n16 * 16) + SpareBytes<Fmt>::value;
+  stage_bytes = std::max(stage_bytes, l16 * kWave * 16);  // every DMA lane writes its 16 bytes
   const size_t lds = (size_t)stage_bytes * kEmbWaves;
   const int64_t waves = tokens * parts;
   const dim3 grid((unsigned)((waves + kEmbWaves - 1) / kEmbWaves));
   const int h = (int)hidden;
-  const int l16 = (int)((part_n16 + kWave - 1) / kWave);
   switch (l16 * 2 + (parts - 1)) {
 #define NVF_STAGE_CASE(L)                                                                                     \
   case 2 * L:                                                                                                 \
