@@ -1118,10 +1118,12 @@ int launch_gemm(const int8_t* xq, const float* rscale, const int8_t* w8, const u
     // when the staged scales of a wider column set would not fit
     const int64_t groups = (n + 15) / 16;
     bool ok = false;
-    // (wide outputs: 2 waves of 32 columns each, so one activation fragment feeds two
-    // MFMAs; measured at the gate_up shape, m = 8: 28.5 against 30.8 us for 4 waves of
-    // 16 columns and 30.3 us for 1 wave of 64)
-    if (groups >= 2048) ok = try_gemv<TO, 2, 1, 2>(xq, rscale, w8, ws, out, m, n, k, stream);
+    // (wide outputs: one-wave workgroups of 32 columns, so one activation fragment feeds
+    // two MFMAs and the many small workgroups spread evenly over the CUs, 4 or 5 each;
+    // measured at the gate_up shape, m = 8: 25.7-26.0 us against 28.1-28.4 for 2 waves
+    // of 32 columns (2 or 3 workgroups per CU), 30.8 for 4 waves of 16 columns and 30.3
+    // for 1 wave of 64; capping residency at 5 one-wave workgroups per CU: 36.4)
+    if (groups >= 2048) ok = try_gemv<TO, 1, 1, 2>(xq, rscale, w8, ws, out, m, n, k, stream);
     if (!ok && groups >= 1024) ok = try_gemv<TO, 4, 2>(xq, rscale, w8, ws, out, m, n, k, stream);
     if (!ok && groups >= 512) ok = try_gemv<TO, 4, 4>(xq, rscale, w8, ws, out, m, n, k, stream);
     if (!ok) ok = try_gemv<TO, 8, 8>(xq, rscale, w8, ws, out, m, n, k, stream);
