@@ -312,6 +312,7 @@ def test_gemv_with_fused_rms_norm_rejects(gpu):
 @pytest.mark.parametrize("tokens,qh,kvh,hd,norm", [
     (37, 28, 4, 128, False),   # Qwen2.5-7B heads, packed [q | k | v] rows
     (5, 32, 8, 128, True),     # Qwen3-8B: QK-norm fused as well
+    (7, 40, 8, 128, True),     # 40 + 8 heads (Qwen3-14B): a token's heads in two passes
     (9, 14, 2, 64, False),     # Qwen2.5-0.5B heads
     (3, 4, 1, 256, True),
     (6, 4, 2, 80, False),      # head_dim 80: the two-launch fallback
@@ -360,6 +361,7 @@ def test_qk_norm_rope_store_kv(gpu, dt, tokens, qh, kvh, hd, norm):
 @pytest.mark.parametrize("tokens,qh,kvh,hd,norm", [
     (37, 28, 4, 128, False),   # Qwen2.5-7B heads, packed [q | k | v] rows: the bias is Qwen2.5's
     (5, 32, 8, 128, True),     # Qwen3-8B heads with QK-norm (bias and norm together)
+    (7, 40, 8, 128, True),     # 40 + 8 heads (Qwen3-14B): a token's heads in two passes
     (9, 14, 2, 64, False),     # Qwen2.5-0.5B heads
     (3, 4, 1, 256, True),
     (6, 4, 2, 80, False),      # head_dim 80: the separate-op fallback (add bias, RoPE, store)

@@ -273,7 +273,7 @@ def _rope_case(gpu, dt, T, hq, hk, hd, norm, packed, seed, positions=None):
 
 @pytest.mark.parametrize("dt", DTYPES, ids=DT_IDS)
 @pytest.mark.parametrize("norm", [False, True], ids=["rope", "qknorm_rope"])
-@pytest.mark.parametrize("hq,hk,hd", [(14, 2, 64), (28, 4, 128), (32, 8, 128), (4, 1, 256), (3, 1, 80)])
+@pytest.mark.parametrize("hq,hk,hd", [(14, 2, 64), (28, 4, 128), (32, 8, 128), (40, 8, 128), (64, 8, 128), (4, 1, 256), (3, 1, 80)])
 def test_qk_norm_rope(gpu, dt, norm, hq, hk, hd):
     _rope_case(gpu, dt, 61, hq, hk, hd, norm, False, seed=hq * hd + dt + norm)
 
