@@ -265,6 +265,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void f
     // S^T = K . Q^T for keys [32 kt, 32 kt + 32)
     // (the two key tiles' MFMA chains interleaved: neither waits on its own accumulator)
     f32x16 st[2] = {f32x16{}, f32x16{}};
+    // Wave priority 1 over the MFMA blocks (S here, PV below), 0 over the softmax: a
+    // SIMD's three waves then hand its issue slots to the one with matrix work first, and
+    // the others' softmax fills the MFMAs' shadow (545 -> 536 us at config 2; raising
+    // the softmax instead: 539).
+    __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int s = 0; s < kFaHd / 16; ++s)
 #pragma unroll
@@ -273,6 +278,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void f
         const v8 a = __builtin_bit_cast(v8, ld16(buf + kr * kFaKRow + 16 * (ku ^ (kr & 15))));
         st[kt] = M::mma(a, qf[s], st[kt]);
       }
+    __builtin_amdgcn_s_setprio(0);
     if (c + 1 < c1) load_k(c + 1, lds + ((c + 1 - c0) & 1) * kFaKBytes);  // in flight during the softmax and PV
     // online softmax for this lane's query; element j of tile kt is key
     // c*64 + 32 kt + 8 (j/4) + 4 half + j%4.  The running max m is kept in
@@ -342,6 +348,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void f
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     }
     const uint8_t* vt = vbuf;
+    __builtin_amdgcn_s_setprio(1);
     // (the four dim tiles' MFMA chains interleaved)
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt)
@@ -359,6 +366,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void f
                         o[d]);
         }
     if (c + 1 < c1) {
+      __builtin_amdgcn_s_setprio(0);
       __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): K(c + 1) is in LDS
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_s_barrier();  // and every wave is done with V(c)
