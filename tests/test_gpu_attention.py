@@ -96,6 +96,8 @@ CASES = [
     ([256], [256], 4, 1, 128, 128),                       # exact tiles
     ([33, 64, 1], [2, 1, 1], 32, 1, 128, 64),             # 32 heads per kv head: beyond the 16-column tiles
     ([150, 70], [150, 70], 21, 3, 128, 64),               # 3 kv heads; a tile spans the sequence switch
+    ([385, 200], [385, 200], 32, 2, 128, 64),             # 16 query heads per kv head; tails ending mid-chunk
+    ([1100], [1100], 8, 1, 128, 512),                     # 512-key blocks: chunks of a block's interior
 ]
 
 
