@@ -157,6 +157,15 @@ def test_embedding_out_of_range_ids_give_nan_rows(gpu):
     got = ops.embedding_qk(H.to_dev(ids, gpu), H.to_dev(blocks, gpu), hidden, ops.Q4_K, V,
                            out_dtype=torch.bfloat16).float().cpu().numpy()
     assert np.isnan(got[[1, 2, 4]]).all() and np.isfinite(got[[0, 3]]).all()
+    # the staged gathers with two waves per row (8 blocks of 256), Q6_K's four-slot decode among them
+    wide = 2048
+    for kind in (ops.Q5_K, ops.Q6_K):
+        bb, offs = H.KQ_BLOCK[kind]
+        blocks = H.gen_raw_blocks(r, V * wide // 256, bb, offs)
+        case(f"embedding out-of-range ids kind={kind}")
+        got = ops.embedding_qk(H.to_dev(ids, gpu), H.to_dev(blocks, gpu), wide, kind, V,
+                               out_dtype=torch.float16).float().cpu().numpy()
+        assert np.isnan(got[[1, 2, 4]]).all() and np.isfinite(got[[0, 3]]).all()
 
 
 # ---------------------------------------------------------------------------
