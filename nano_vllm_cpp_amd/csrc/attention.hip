@@ -265,11 +265,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void f
     // S^T = K . Q^T for keys [32 kt, 32 kt + 32)
     // (the two key tiles' MFMA chains interleaved: neither waits on its own accumulator)
     f32x16 st[2] = {f32x16{}, f32x16{}};
-    // Wave priority 1 over the MFMA blocks (S here, PV below), 0 over the softmax: a
+    // Wave priority over the MFMA blocks (S 2 here, PV 1 below), 0 over the softmax: a
     // SIMD's three waves then hand its issue slots to the one with matrix work first, and
-    // the others' softmax fills the MFMAs' shadow (545 -> 536 us at config 2; raising
-    // the softmax instead: 539).
-    __builtin_amdgcn_s_setprio(1);
+    // the others' softmax fills the MFMAs' shadow (config 2: 545 -> 536 us with 1 for
+    // both, 555 -> 545 with S above PV on another box; raising the softmax instead: 539).
+    __builtin_amdgcn_s_setprio(2);
 #pragma unroll
     for (int s = 0; s < kFaHd / 16; ++s)
 #pragma unroll
