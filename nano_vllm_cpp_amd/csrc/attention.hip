@@ -518,6 +518,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
     if (c + 1 < c1) load_chunk(c + 1);  // in flight during this chunk
     // S^T: lane row (key) lane & 31 of the chunk, dims 64 half + ...
     f32x16 st = f32x16{};
+    // wave priority as in fa_prefill_kernel: S 2, PV 1, the softmax 0 (3957-3968 ->
+    // 3900-3908 us at config 2)
+    __builtin_amdgcn_s_setprio(2);
     const uint8_t* krow = buf + (lane & 31) * kF32KRow + 256 * half;
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
@@ -525,6 +528,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
 #pragma unroll
       for (int e = 0; e < 4; ++e) st = __builtin_amdgcn_mfma_f32_32x32x2f32(a[e], qf[i][e], st, 0, 0, 0);
     }
+    __builtin_amdgcn_s_setprio(0);
     // online softmax for this lane's query over its keys c*32 + 8 (j/4) + 4 half + j%4
     // (the running max in exp2 units, as in fa_prefill_kernel)
     float mx = -INFINITY;
@@ -562,6 +566,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
     // O^T += V^T . P^T: MFMA s takes key 8 (s/4) + 4 half + s%4 (P^T = st[s]); lane
     // row r = lane & 31 of tile d is dim 4 r + d
     const uint8_t* vrow = buf + kF32KBytes + 16 * (lane & 31);
+    __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int s = 0; s < 16; ++s) {
       const int key = 8 * (s >> 2) + 4 * half + (s & 3);
@@ -569,6 +574,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void f
 #pragma unroll
       for (int d = 0; d < 4; ++d) o[d] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[d], st[s], o[d], 0, 0, 0);
     }
+    __builtin_amdgcn_s_setprio(0);
     if (c + 1 < c1) store_chunk(lds + ((c + 1 - c0) & 1) * kF32Stage);
     __syncthreads();
   }
